@@ -1,0 +1,98 @@
+"""Build libcuca_hip.so: the gfx950 code object plus the C-ABI host runtime.
+
+    python -m cuca_amd.build
+
+1. hipcc compiles csrc/kernels/cuca_kernels.hip for gfx950 only into a raw
+   ELF code object (_build/cuca_kernels.co), with -ffp-contract=off (RoPE
+   and the dequant are bit-exact only without FMA contraction) and packed
+   FP32 instructions disabled.
+2. The kernel names in csrc/kernel_list.inc are checked against the code
+   object's symbols.
+3. g++ compiles csrc/runtime.cpp (host code only) with the code object
+   embedded (.incbin) into libcuca_hip.so, linked to libamdhip64.
+
+Both outputs are written in-tree (cuca_amd/), so the .so travels with the
+repository snapshot to the GPU box; nothing is JIT-compiled at run time.
+"""
+
+import os
+import re
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+BUILD = os.path.join(HERE, "_build")
+LIB = os.path.join(HERE, "libcuca_hip.so")
+CODE_OBJECT = os.path.join(BUILD, "cuca_kernels.co")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+
+HIPCC_FLAGS = [
+    "--offload-arch=gfx950", "--offload-device-only", "--no-gpu-bundle-output",
+    "-O3", "-std=c++17", "-ffp-contract=off",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Werror=return-type",
+]
+
+
+def _run(cmd, verbose):
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass does not know the packed-fp32 feature; that warning is noise
+    noise = re.compile(r"packed-fp32-ops|^\d+ warnings? generated")
+    err = "\n".join(l for l in res.stderr.splitlines() if not noise.search(l))
+    if res.returncode != 0:
+        raise RuntimeError(f"build step failed ({res.returncode}): {' '.join(cmd)}\n{err}")
+    if verbose and err.strip():
+        print(err, file=sys.stderr)
+
+
+def kernel_names():
+    names = []
+    with open(os.path.join(CSRC, "kernel_list.inc")) as f:
+        for line in f:
+            m = re.match(r"\s*K\((\w+)\)", line)
+            if m:
+                names.append(m.group(1))
+    return names
+
+
+def code_object_kernels(path):
+    out = subprocess.run([os.path.join(ROCM, "llvm/bin/llvm-readelf"), "--symbols", path],
+                         capture_output=True, text=True, check=True).stdout
+    syms = set()
+    for line in out.splitlines():
+        parts = line.split()
+        if parts and parts[-1].endswith(".kd"):  # one kernel descriptor per kernel
+            syms.add(parts[-1][:-3])
+    return syms
+
+
+def build(verbose: bool = False) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    co_tmp = CODE_OBJECT + ".tmp"
+    _run([os.path.join(ROCM, "bin/hipcc"), *HIPCC_FLAGS,
+          os.path.join(CSRC, "kernels", "cuca_kernels.hip"), "-o", co_tmp], verbose)
+    os.replace(co_tmp, CODE_OBJECT)
+    listed = kernel_names()
+    present = code_object_kernels(CODE_OBJECT)
+    missing = [k for k in listed if k not in present]
+    unlisted = sorted(present - set(listed))
+    if missing or unlisted:
+        raise RuntimeError(f"kernel_list.inc and the code object disagree: missing {missing}, "
+                           f"unlisted {unlisted}")
+    lib_tmp = LIB + ".tmp"
+    _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra",
+          "-D__HIP_PLATFORM_AMD__", f"-DCUCA_CODE_OBJECT=\"{CODE_OBJECT}\"",
+          f"-I{os.path.join(ROOT, 'include')}", f"-I{CSRC}", f"-I{ROCM}/include",
+          os.path.join(CSRC, "runtime.cpp"), "-o", lib_tmp,
+          f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib",
+          "-Wl,--no-undefined"], verbose)
+    os.replace(lib_tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-q" not in sys.argv))

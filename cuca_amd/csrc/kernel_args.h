@@ -1,0 +1,85 @@
+/*
+ * kernel_args.h -- by-value argument blocks of the gfx950 kernels.
+ *
+ * Shared by the host runtime (runtime.cpp, which packs one block per
+ * hipModuleLaunchKernel call) and the device code (the kernels/ sources, where each
+ * kernel takes its block as its only parameter).  Plain C layout only.
+ */
+#ifndef CUCA_KERNEL_ARGS_H
+#define CUCA_KERNEL_ARGS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Device status words, one per kind of bad input the kernels can meet.
+ * Each holds (row << 32 | value) of the smallest bad row seen, or all
+ * ones.  The host resets them after reading (cuca_hip_check_device). */
+enum { CUCA_STATUS_EMBED_ID = 0, CUCA_STATUS_ROPE_POS = 1, CUCA_STATUS_WORDS = 4 };
+
+typedef struct {
+    const uint8_t *table;   /* [vocab, row_bytes]                          */
+    const uint32_t *ids;    /* [n]                                         */
+    void *out;              /* [n, hidden] f32 or f16                      */
+    unsigned long long *status;
+    int64_t vocab;
+    int64_t row_bytes;
+    int32_t hidden;
+    int32_t n;
+    float scale;
+    int32_t pad_;
+} EmbedArgs;
+
+typedef struct {
+    const void *x;          /* [rows, hidden]                              */
+    const void *branch;     /* [rows, hidden] or NULL                      */
+    const float *w;         /* [hidden] or NULL                            */
+    const float *w_post;    /* [hidden] or NULL                            */
+    void *x_out;            /* [rows, hidden] or NULL                      */
+    void *h_out;            /* [rows, hidden]                              */
+    int64_t rows;
+    int32_t hidden;
+    float eps;
+    float post_eps;
+    float rs;               /* residual scale                              */
+} NormArgs;
+
+typedef struct {
+    const void *gate;
+    const void *up;
+    void *out;
+    const int32_t *offsets; /* ragged: device [n_experts + 1] or NULL      */
+    int64_t rows;           /* dense: rows; ragged: max_rows               */
+    int64_t gate_ld, up_ld, out_ld; /* row strides in elements             */
+    int32_t ff;
+    int32_t blocks_per_row;
+    int32_t n_experts;
+    float clamp;            /* > 0: clamp gate from above, up to +-clamp   */
+} GluArgs;
+
+typedef struct {
+    void *q;                /* [rows, nq, d] with row stride q_ld           */
+    void *k;                /* [rows, nk, d] with row stride k_ld           */
+    const float *cos_t;     /* [table_rows, n_dims / 2]                     */
+    const float *sin_t;
+    const int32_t *pos;     /* [rows]                                       */
+    const float *q_norm_w;  /* [d] or NULL                                  */
+    const float *k_norm_w;  /* [d] or NULL                                  */
+    unsigned long long *status;
+    int64_t q_ld, k_ld;
+    int64_t table_rows;
+    int32_t rows;
+    int32_t nq, nk;
+    int32_t head_dim;
+    int32_t n_dims;
+    int32_t tph_log2;       /* log2(threads per head), vector kernels       */
+    float eps;
+    int32_t kind;           /* generic kernel: 0 NORM, 2 NEOX               */
+} RopeArgs;
+
+#ifdef __cplusplus
+}
+#endif
+#endif

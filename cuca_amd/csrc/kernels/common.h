@@ -1,0 +1,97 @@
+// common.h -- shared device helpers of the gfx950 per-layer kernels.
+//
+// Every kernel is wave64 and bandwidth-bound: activations move in 16-byte
+// chunks (4 f32 or 8 f16 per lane, one global_load/store_dwordx4), all
+// arithmetic is f32, and f16 results are rounded once (v_cvt_f16_f32,
+// round-to-nearest-even).  The whole code object is built with
+// -ffp-contract=off, so a*c - b*s is two rounded products and a rounded
+// difference, as in the reference's scalar f32 code; fmaf() is written out
+// where a fused multiply-add is wanted.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../kernel_args.h"
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+#define CUCA_WAVE 64
+#define CUCA_BLOCK 256
+
+// A 16-byte chunk of activations of type T, widened to f32 in registers.
+template <typename T> struct Chunk;
+
+template <> struct Chunk<float> {
+    static constexpr int N = 4;
+    __device__ static inline void load(const void *base, int64_t chunk, float (&v)[4]) {
+        f32x4 t = reinterpret_cast<const f32x4 *>(base)[chunk];
+        v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+    }
+    __device__ static inline void store(void *base, int64_t chunk, const float (&v)[4]) {
+        f32x4 t = {v[0], v[1], v[2], v[3]};
+        reinterpret_cast<f32x4 *>(base)[chunk] = t;
+    }
+    // The value the activation type holds for v (identity for f32).
+    __device__ static inline float as_stored(float v) { return v; }
+};
+
+template <> struct Chunk<_Float16> {
+    static constexpr int N = 8;
+    __device__ static inline void load(const void *base, int64_t chunk, float (&v)[8]) {
+        f16x8 t = reinterpret_cast<const f16x8 *>(base)[chunk];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = (float)t[i];
+    }
+    __device__ static inline void store(void *base, int64_t chunk, const float (&v)[8]) {
+        f16x8 t;
+#pragma unroll
+        for (int i = 0; i < 8; i++) t[i] = (_Float16)v[i];
+        reinterpret_cast<f16x8 *>(base)[chunk] = t;
+    }
+    __device__ static inline float as_stored(float v) { return (float)(_Float16)v; }
+};
+
+// Scalar element access for the shape-generic fallback kernels.
+template <typename T> __device__ static inline float load1(const void *p, int64_t i) {
+    return (float)reinterpret_cast<const T *>(p)[i];
+}
+template <typename T> __device__ static inline void store1(void *p, int64_t i, float v) {
+    reinterpret_cast<T *>(p)[i] = (T)v;
+}
+
+// Sum over aligned groups of G lanes (G a power of two <= 64).  A butterfly:
+// at every step lane i adds lane i^off, and float addition is commutative,
+// so every lane of a group ends with the same bits; the order is fixed by
+// the lane layout alone, so a row's result never depends on its neighbours.
+template <int G> __device__ static inline float group_sum(float v) {
+#pragma unroll
+    for (int off = G / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, CUCA_WAVE);
+    return v;
+}
+
+__device__ static inline float group_sum_rt(float v, int g) {
+    for (int off = g / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, CUCA_WAVE);
+    return v;
+}
+
+// Sum over the whole block (blockDim.x a multiple of 64, <= 1024); every
+// thread receives the same value.  `red` holds 16 floats of LDS.
+__device__ static inline float block_sum(float v, float *red) {
+    v = group_sum<CUCA_WAVE>(v);
+    const int wave = threadIdx.x / CUCA_WAVE, nw = blockDim.x / CUCA_WAVE;
+    __syncthreads(); // `red` may still be read by a previous call
+    if ((threadIdx.x & (CUCA_WAVE - 1)) == 0) red[wave] = v;
+    __syncthreads();
+    float s = 0.0f;
+    for (int i = 0; i < nw; i++) s += red[i];
+    return s;
+}
+
+// Record (row, value) of a bad input in a status word, keeping the
+// smallest row (global atomic, vector memory path).
+__device__ static inline void record_bad(unsigned long long *word, uint32_t row, uint32_t value) {
+    atomicMin(word, ((unsigned long long)row << 32) | value);
+}

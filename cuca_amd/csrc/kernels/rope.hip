@@ -1,0 +1,203 @@
+// rope.hip -- rotary embedding on Q and K in place, with the optional fused
+// per-head QK-norm, on gfx950.
+//
+// Replaces apply_rope / rotate_calls (cpu.rs:2996-3026, 3672-3688; candle's
+// rope and rope_i) and the GPU rope (gpu.rs:5922-5964: narrow / cat / mul,
+// several launches and copies), plus the QK-norm in front of it
+// (cpu.rs:2840-2864, 3040-3055).  One launch covers the Q and the K heads
+// of every row, in the projection's own [rows, heads, head_dim] layout
+// (row stride q_ld / k_ld, so Q and K may sit inside a fused QKV buffer).
+//
+// Vector kernel: a head is handled by TPH = head_dim / (2 * VP) lanes, VP
+// values per 16-byte chunk (4 f32, 8 f16); every lane owns 2 * VP values:
+//   NEOX: values i .. i+VP and their partners i+n/2 .. i+n/2+VP,
+//   NORM: 2 * VP adjacent values = VP (2i, 2i+1) pairs,
+// plus pass-through chunks past n_dims.  The cos/sin row of the position
+// (n_dims / 2 f32) is shared by all heads of the row and stays in cache.
+// The QK-norm sum is a butterfly over the head's TPH lanes.
+//
+// a' = a*c - b*s, b' = a*s + b*c with separately rounded products
+// (-ffp-contract=off, and the pragma below): without the norm the result is
+// bit-identical to the reference's f32 rotation, in f16 too (exact widening,
+// one rounding).
+//
+// Generic kernel (any head_dim / n_dims / alignment): one wave per head.
+
+#include "common.h"
+
+#pragma clang fp contract(off)
+
+template <int VP>
+__device__ static inline void load_tab(const float *t, int64_t first, float (&v)[VP]) {
+    const f32x4 *p = reinterpret_cast<const f32x4 *>(t + first);
+#pragma unroll
+    for (int j = 0; j < VP / 4; j++) {
+        f32x4 x = p[j];
+        v[4 * j] = x.x; v[4 * j + 1] = x.y; v[4 * j + 2] = x.z; v[4 * j + 3] = x.w;
+    }
+}
+
+template <typename T, int KIND, bool NORM>
+__device__ static inline void rope_body(const RopeArgs &a) {
+    constexpr int VP = Chunk<T>::N;
+    const int tl = a.tph_log2;
+    const int tph = 1 << tl;
+    const uint32_t gh = blockIdx.x * (uint32_t)(CUCA_BLOCK >> tl) + (threadIdx.x >> tl);
+    const int u = threadIdx.x & (tph - 1);
+    const uint32_t heads = (uint32_t)(a.nq + a.nk);
+    bool live = gh < (uint32_t)a.rows * heads;
+    const uint32_t row = live ? gh / heads : 0;
+    const int h = live ? (int)(gh - row * heads) : 0;
+    const int32_t pos = live ? a.pos[row] : 0;
+    if (live && (pos < 0 || (int64_t)pos >= a.table_rows)) {
+        if (u == 0 && h == 0) record_bad(a.status + CUCA_STATUS_ROPE_POS, row, (uint32_t)pos);
+        live = false;
+    }
+    const bool isq = h < a.nq;
+    const int D = a.head_dim;
+    T *base = isq ? reinterpret_cast<T *>(a.q) + (int64_t)row * a.q_ld + (int64_t)h * D
+                  : reinterpret_cast<T *>(a.k) + (int64_t)row * a.k_ld + (int64_t)(h - a.nq) * D;
+    const float *nw = isq ? a.q_norm_w : a.k_norm_w;
+    const int half = a.n_dims >> 1;
+
+    // This lane's two chunks (element offsets ia and ib within the head).
+    int ia, ib;
+    bool rot;
+    if (KIND == 2) {
+        const int nr = half / VP;
+        if (u < nr) {
+            ia = u * VP; ib = ia + half; rot = true;
+        } else {
+            ia = a.n_dims + (u - nr) * 2 * VP; ib = ia + VP; rot = false;
+        }
+    } else {
+        ia = u * 2 * VP; ib = ia + VP; rot = ia < a.n_dims;
+    }
+    float va[VP], vb[VP];
+    if (live) {
+        Chunk<T>::load(base, ia / VP, va);
+        Chunk<T>::load(base, ib / VP, vb);
+    } else {
+#pragma unroll
+        for (int i = 0; i < VP; i++) va[i] = vb[i] = 0.0f;
+    }
+    if (NORM) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < VP; i++) ss += va[i] * va[i];
+#pragma unroll
+        for (int i = 0; i < VP; i++) ss += vb[i] * vb[i];
+        ss = group_sum_rt(ss, tph);
+        if (nw) {
+            const float m = sqrtf(ss / (float)D + a.eps);
+            float wa[VP], wb[VP];
+            load_tab<VP>(nw, ia, wa);
+            load_tab<VP>(nw, ib, wb);
+#pragma unroll
+            for (int i = 0; i < VP; i++) {
+                va[i] = va[i] / m * wa[i];
+                vb[i] = vb[i] / m * wb[i];
+            }
+        }
+    }
+    if (!live) return;
+    if (rot) {
+        float c[VP], s[VP];
+        const int64_t trow = (int64_t)pos * half;
+        if (KIND == 2) {
+            load_tab<VP>(a.cos_t, trow + ia, c);
+            load_tab<VP>(a.sin_t, trow + ia, s);
+#pragma unroll
+            for (int i = 0; i < VP; i++) {
+                const float x0 = va[i], x1 = vb[i];
+                va[i] = x0 * c[i] - x1 * s[i];
+                vb[i] = x0 * s[i] + x1 * c[i];
+            }
+        } else {
+            load_tab<VP>(a.cos_t, trow + (ia >> 1), c);
+            load_tab<VP>(a.sin_t, trow + (ia >> 1), s);
+            float w[2 * VP];
+#pragma unroll
+            for (int i = 0; i < VP; i++) { w[i] = va[i]; w[VP + i] = vb[i]; }
+#pragma unroll
+            for (int j = 0; j < VP; j++) {
+                const float x0 = w[2 * j], x1 = w[2 * j + 1];
+                w[2 * j] = x0 * c[j] - x1 * s[j];
+                w[2 * j + 1] = x0 * s[j] + x1 * c[j];
+            }
+#pragma unroll
+            for (int i = 0; i < VP; i++) { va[i] = w[i]; vb[i] = w[VP + i]; }
+        }
+    } else if (!NORM || !nw) {
+        return; // pass-through values are left untouched
+    }
+    Chunk<T>::store(base, ia / VP, va);
+    Chunk<T>::store(base, ib / VP, vb);
+}
+
+template <typename T>
+__device__ static inline void rope_generic_body(const RopeArgs &a) {
+    const int lane = threadIdx.x & (CUCA_WAVE - 1);
+    const uint32_t gh = blockIdx.x * (uint32_t)(CUCA_BLOCK / CUCA_WAVE) + threadIdx.x / CUCA_WAVE;
+    const uint32_t heads = (uint32_t)(a.nq + a.nk);
+    if (gh >= (uint32_t)a.rows * heads) return; // whole wave
+    const uint32_t row = gh / heads;
+    const int h = (int)(gh - row * heads);
+    const int32_t pos = a.pos[row];
+    if (pos < 0 || (int64_t)pos >= a.table_rows) {
+        if (lane == 0 && h == 0) record_bad(a.status + CUCA_STATUS_ROPE_POS, row, (uint32_t)pos);
+        return;
+    }
+    const bool isq = h < a.nq;
+    const int D = a.head_dim;
+    T *base = isq ? reinterpret_cast<T *>(a.q) + (int64_t)row * a.q_ld + (int64_t)h * D
+                  : reinterpret_cast<T *>(a.k) + (int64_t)row * a.k_ld + (int64_t)(h - a.nq) * D;
+    const float *nw = isq ? a.q_norm_w : a.k_norm_w;
+    float m = 1.0f;
+    if (nw) {
+        float ss = 0.0f;
+        for (int e = lane; e < D; e += CUCA_WAVE) {
+            const float v = load1<T>(base, e);
+            ss += v * v;
+        }
+        ss = group_sum<CUCA_WAVE>(ss);
+        m = sqrtf(ss / (float)D + a.eps);
+    }
+    const int half = a.n_dims >> 1;
+    const float *cs = a.cos_t + (int64_t)pos * half;
+    const float *sn = a.sin_t + (int64_t)pos * half;
+    // every lane reads its elements before any lane of the wave writes
+    // (the norm pass above read all of them); pairs are disjoint per lane
+    for (int i = lane; i < half; i += CUCA_WAVE) {
+        const int ea = a.kind == 2 ? i : 2 * i;
+        const int eb = a.kind == 2 ? i + half : 2 * i + 1;
+        float x0 = load1<T>(base, ea), x1 = load1<T>(base, eb);
+        if (nw) {
+            x0 = x0 / m * nw[ea];
+            x1 = x1 / m * nw[eb];
+        }
+        store1<T>(base, ea, x0 * cs[i] - x1 * sn[i]);
+        store1<T>(base, eb, x0 * sn[i] + x1 * cs[i]);
+    }
+    if (nw) {
+        for (int e = a.n_dims + lane; e < D; e += CUCA_WAVE)
+            store1<T>(base, e, load1<T>(base, e) / m * nw[e]);
+    }
+}
+
+#define CUCA_ROPE(NAME, T, KIND, NORM)                                                     \
+    extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void NAME(RopeArgs a) {            \
+        rope_body<T, KIND, NORM>(a);                                                       \
+    }
+#define CUCA_ROPE_SET(TN, T)                                                               \
+    CUCA_ROPE(cuca_rope_##TN##_norm, T, 0, false)                                          \
+    CUCA_ROPE(cuca_rope_##TN##_neox, T, 2, false)                                          \
+    CUCA_ROPE(cuca_rope_##TN##_norm_qkn, T, 0, true)                                       \
+    CUCA_ROPE(cuca_rope_##TN##_neox_qkn, T, 2, true)                                       \
+    extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void cuca_rope_##TN##_generic(     \
+        RopeArgs a) {                                                                      \
+        rope_generic_body<T>(a);                                                           \
+    }
+
+CUCA_ROPE_SET(f32, float)
+CUCA_ROPE_SET(f16, _Float16)

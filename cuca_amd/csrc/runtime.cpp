@@ -1,0 +1,658 @@
+// runtime.cpp -- implementation of the C ABI in include/cuca_hip.h.
+//
+// The kernels are one gfx950 code object (kernels/cuca_kernels.hip) that
+// the build embeds into this library (CUCA_CODE_OBJECT, .incbin below).  A
+// context loads it with hipModuleLoadData, resolves every kernel once with
+// hipModuleGetFunction and launches with hipModuleLaunchKernel, each kernel
+// taking one by-value argument block (kernel_args.h).  Host code only: no
+// device code is compiled into this file.
+#include "cuca_hip.h"
+#include "kernel_args.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#ifndef CUCA_CODE_OBJECT
+#error "CUCA_CODE_OBJECT must name the gfx950 code object to embed"
+#endif
+
+extern "C" const unsigned char cuca_code_object_start[];
+extern "C" const unsigned char cuca_code_object_end[];
+__asm__(".section .rodata\n"
+        ".global cuca_code_object_start\n"
+        ".balign 4096\n"
+        "cuca_code_object_start:\n"
+        ".incbin \"" CUCA_CODE_OBJECT "\"\n"
+        ".global cuca_code_object_end\n"
+        "cuca_code_object_end:\n"
+        ".previous\n");
+
+namespace {
+
+// Every kernel of the code object, resolved at context creation.
+enum Kernel {
+#define K(name) name,
+#include "kernel_list.inc"
+#undef K
+    KERNEL_COUNT
+};
+const char *const kKernelNames[] = {
+#define K(name) #name,
+#include "kernel_list.inc"
+#undef K
+};
+
+thread_local std::string g_thread_error;
+
+}  // namespace
+
+struct cuca_hip_ctx {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    hipModule_t module = nullptr;
+    hipFunction_t fn[KERNEL_COUNT] = {};
+    unsigned long long *status = nullptr;  // CUCA_STATUS_WORDS device words
+    hipEvent_t t0 = nullptr, t1 = nullptr;
+    bool capturing = false;
+    int64_t last_vocab = 0;       // for the out-of-range message
+    int64_t last_table_rows = 0;
+    std::string error;
+};
+
+struct cuca_hip_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+namespace {
+
+cuca_status fail(cuca_hip_ctx *ctx, cuca_status st, const char *fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (ctx) ctx->error = buf;
+    else g_thread_error = buf;
+    return st;
+}
+
+cuca_status hip_fail(cuca_hip_ctx *ctx, hipError_t e, const char *what) {
+    return fail(ctx, CUCA_HIP_ERROR, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+#define HIP_TRY(ctx, call)                                    \
+    do {                                                      \
+        hipError_t e_ = (call);                               \
+        if (e_ != hipSuccess) return hip_fail(ctx, e_, #call); \
+    } while (0)
+
+// Make the context's device current for the calling thread.
+cuca_status use(cuca_hip_ctx *ctx) {
+    if (!ctx) return fail(nullptr, CUCA_INVALID_ARG, "null context");
+    int cur = -1;
+    HIP_TRY(ctx, hipGetDevice(&cur));
+    if (cur != ctx->device) HIP_TRY(ctx, hipSetDevice(ctx->device));
+    return CUCA_OK;
+}
+
+template <typename Args>
+cuca_status launch(cuca_hip_ctx *ctx, Kernel k, unsigned grid, unsigned block, unsigned lds,
+                   Args &args) {
+    if (grid == 0) return CUCA_OK;
+    void *params[] = {&args};
+    hipError_t e = hipModuleLaunchKernel(ctx->fn[k], grid, 1, 1, block, 1, 1, lds, ctx->stream,
+                                         params, nullptr);
+    if (e != hipSuccess) return fail(ctx, CUCA_HIP_ERROR, "launching %s: %s", kKernelNames[k],
+                                     hipGetErrorString(e));
+    return CUCA_OK;
+}
+
+inline bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline size_t esize(cuca_dtype t) { return t == CUCA_F16 ? 2 : 4; }
+inline bool dtype_ok(cuca_dtype t) { return t == CUCA_F32 || t == CUCA_F16; }
+inline int chunk_elems(cuca_dtype t) { return t == CUCA_F16 ? 8 : 4; }
+inline unsigned div_up(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
+
+}  // namespace
+
+extern "C" {
+
+const char *cuca_hip_last_error(const cuca_hip_ctx *ctx) {
+    return ctx ? ctx->error.c_str() : g_thread_error.c_str();
+}
+
+cuca_status cuca_hip_ctx_create(int device, cuca_hip_ctx **out) {
+    if (!out) return fail(nullptr, CUCA_INVALID_ARG, "null output pointer");
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0)
+        return fail(nullptr, CUCA_HIP_ERROR, "no HIP device (%s)", hipGetErrorString(e));
+    if (device < 0 || device >= n)
+        return fail(nullptr, CUCA_INVALID_ARG, "device %d outside 0..%d", device, n - 1);
+    hipDeviceProp_t prop;
+    e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) return fail(nullptr, CUCA_HIP_ERROR, "hipGetDeviceProperties: %s",
+                                     hipGetErrorString(e));
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return fail(nullptr, CUCA_NOT_GFX950, "device %d is %s; this library is built for gfx950 only",
+                    device, prop.gcnArchName);
+    cuca_hip_ctx *ctx = new cuca_hip_ctx();
+    ctx->device = device;
+    cuca_status st = CUCA_OK;
+    do {
+        if ((e = hipSetDevice(device)) != hipSuccess) { st = hip_fail(ctx, e, "hipSetDevice"); break; }
+        // default priority: streams of other priorities are not used anywhere
+        if ((e = hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking)) != hipSuccess) {
+            st = hip_fail(ctx, e, "hipStreamCreateWithFlags"); break;
+        }
+        ctx->stream = ctx->own_stream;
+        if ((e = hipModuleLoadData(&ctx->module, cuca_code_object_start)) != hipSuccess) {
+            st = hip_fail(ctx, e, "hipModuleLoadData(gfx950 code object)"); break;
+        }
+        for (int k = 0; k < KERNEL_COUNT; k++) {
+            if ((e = hipModuleGetFunction(&ctx->fn[k], ctx->module, kKernelNames[k])) != hipSuccess) {
+                st = fail(ctx, CUCA_HIP_ERROR, "kernel %s: %s", kKernelNames[k], hipGetErrorString(e));
+                break;
+            }
+        }
+        if (st != CUCA_OK) break;
+        if ((e = hipMalloc(&ctx->status, CUCA_STATUS_WORDS * sizeof(unsigned long long))) != hipSuccess) {
+            st = hip_fail(ctx, e, "hipMalloc(status)"); break;
+        }
+        unsigned long long ones[CUCA_STATUS_WORDS];
+        std::memset(ones, 0xff, sizeof ones);
+        if ((e = hipMemcpy(ctx->status, ones, sizeof ones, hipMemcpyHostToDevice)) != hipSuccess) {
+            st = hip_fail(ctx, e, "hipMemcpy(status)"); break;
+        }
+        if ((e = hipEventCreate(&ctx->t0)) != hipSuccess || (e = hipEventCreate(&ctx->t1)) != hipSuccess) {
+            st = hip_fail(ctx, e, "hipEventCreate"); break;
+        }
+    } while (0);
+    if (st != CUCA_OK) {
+        g_thread_error = ctx->error;
+        cuca_hip_ctx_destroy(ctx);
+        return st;
+    }
+    *out = ctx;
+    return CUCA_OK;
+}
+
+void cuca_hip_ctx_destroy(cuca_hip_ctx *ctx) {
+    if (!ctx) return;
+    int cur = -1;
+    if (hipGetDevice(&cur) == hipSuccess && cur != ctx->device) (void)hipSetDevice(ctx->device);
+    if (ctx->own_stream) (void)hipStreamSynchronize(ctx->own_stream);
+    if (ctx->stream && ctx->stream != ctx->own_stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->t0) (void)hipEventDestroy(ctx->t0);
+    if (ctx->t1) (void)hipEventDestroy(ctx->t1);
+    if (ctx->status) (void)hipFree(ctx->status);
+    if (ctx->module) (void)hipModuleUnload(ctx->module);
+    if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
+    delete ctx;
+}
+
+cuca_status cuca_hip_set_stream(cuca_hip_ctx *ctx, void *stream) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    if (ctx->capturing) return fail(ctx, CUCA_INVALID_ARG, "cannot change the stream during a capture");
+    ctx->stream = stream ? static_cast<hipStream_t>(stream) : ctx->own_stream;
+    return CUCA_OK;
+}
+
+void *cuca_hip_get_stream(const cuca_hip_ctx *ctx) { return ctx ? ctx->stream : nullptr; }
+
+int cuca_hip_device(const cuca_hip_ctx *ctx) { return ctx ? ctx->device : -1; }
+
+cuca_status cuca_hip_malloc(cuca_hip_ctx *ctx, size_t bytes, void **out) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    if (!out) return fail(ctx, CUCA_INVALID_ARG, "null output pointer");
+    *out = nullptr;
+    if (bytes == 0) return CUCA_OK;
+    HIP_TRY(ctx, hipMalloc(out, bytes));
+    return CUCA_OK;
+}
+
+cuca_status cuca_hip_free(cuca_hip_ctx *ctx, void *ptr) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    if (ptr) HIP_TRY(ctx, hipFree(ptr));
+    return CUCA_OK;
+}
+
+static cuca_status copy_async(cuca_hip_ctx *ctx, void *dst, const void *src, size_t bytes,
+                              hipMemcpyKind kind) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    if (bytes == 0) return CUCA_OK;
+    if (!dst || !src) return fail(ctx, CUCA_INVALID_ARG, "null copy pointer");
+    HIP_TRY(ctx, hipMemcpyAsync(dst, src, bytes, kind, ctx->stream));
+    return CUCA_OK;
+}
+
+cuca_status cuca_hip_memcpy_h2d_async(cuca_hip_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    return copy_async(ctx, dst, src, bytes, hipMemcpyHostToDevice);
+}
+cuca_status cuca_hip_memcpy_d2h_async(cuca_hip_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    return copy_async(ctx, dst, src, bytes, hipMemcpyDeviceToHost);
+}
+cuca_status cuca_hip_memcpy_d2d_async(cuca_hip_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    return copy_async(ctx, dst, src, bytes, hipMemcpyDeviceToDevice);
+}
+
+cuca_status cuca_hip_stream_sync(cuca_hip_ctx *ctx) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    return CUCA_OK;
+}
+
+cuca_status cuca_hip_check_device(cuca_hip_ctx *ctx) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    if (ctx->capturing) return fail(ctx, CUCA_INVALID_ARG, "cannot check the device during a capture");
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    unsigned long long w[CUCA_STATUS_WORDS];
+    HIP_TRY(ctx, hipMemcpy(w, ctx->status, sizeof w, hipMemcpyDeviceToHost));
+    const unsigned long long none = ~0ull;
+    bool bad = false;
+    for (int i = 0; i < CUCA_STATUS_WORDS; i++) bad |= w[i] != none;
+    if (!bad) return CUCA_OK;
+    unsigned long long ones[CUCA_STATUS_WORDS];
+    std::memset(ones, 0xff, sizeof ones);
+    HIP_TRY(ctx, hipMemcpy(ctx->status, ones, sizeof ones, hipMemcpyHostToDevice));
+    if (w[CUCA_STATUS_EMBED_ID] != none) {
+        unsigned long long v = w[CUCA_STATUS_EMBED_ID];
+        return fail(ctx, CUCA_OUT_OF_RANGE, "token id %u outside the embedding table of %lld rows (row %u)",
+                    (unsigned)(v & 0xffffffffu), (long long)ctx->last_vocab, (unsigned)(v >> 32));
+    }
+    unsigned long long v = w[CUCA_STATUS_ROPE_POS];
+    return fail(ctx, CUCA_OUT_OF_RANGE, "position %d outside the rope table of %lld rows (row %u)",
+                (int)(v & 0xffffffffu), (long long)ctx->last_table_rows, (unsigned)(v >> 32));
+}
+
+// ---------------------------------------------------------------------
+// embedding
+// ---------------------------------------------------------------------
+
+cuca_status cuca_hip_embed_gguf(cuca_hip_ctx *ctx, const void *table, uint32_t ggml_type,
+                                int64_t vocab, int64_t hidden, const uint32_t *ids, int64_t n,
+                                float scale, void *out, cuca_dtype out_dtype) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    if (ggml_type != CUCA_GGML_Q4_0 && ggml_type != CUCA_GGML_Q8_0)
+        return fail(ctx, CUCA_UNSUPPORTED, "ggml type %u: only Q4_0 (2) and Q8_0 (8) are supported", ggml_type);
+    if (!dtype_ok(out_dtype)) return fail(ctx, CUCA_INVALID_ARG, "bad output dtype %d", (int)out_dtype);
+    if (hidden <= 0 || hidden % 32 != 0)
+        return fail(ctx, CUCA_INVALID_ARG,
+                    "token embedding: row length %lld is not a whole number of %s blocks",
+                    (long long)hidden, ggml_type == CUCA_GGML_Q4_0 ? "Q4_0" : "Q8_0");
+    if (vocab <= 0 || vocab > 0xffffffffll) return fail(ctx, CUCA_INVALID_ARG, "bad vocab %lld", (long long)vocab);
+    if (n < 0 || n > 0x7fffffffll) return fail(ctx, CUCA_INVALID_ARG, "bad token count %lld", (long long)n);
+    if (n == 0) return CUCA_OK;
+    if (!table || !ids || !out) return fail(ctx, CUCA_INVALID_ARG, "null pointer");
+    if (!al16(out)) return fail(ctx, CUCA_INVALID_ARG, "output must be 16-byte aligned");
+    const int64_t row_bytes = hidden / 32 * (ggml_type == CUCA_GGML_Q4_0 ? 18 : 34);
+    if (row_bytes > 65536 || hidden > 0x7fffffffll)
+        return fail(ctx, CUCA_UNSUPPORTED, "rows of %lld bytes exceed the 64 KiB LDS staging", (long long)row_bytes);
+    const bool a16 = al16(table) && row_bytes % 16 == 0;
+    if (!a16 && (reinterpret_cast<uintptr_t>(table) & 1u))
+        return fail(ctx, CUCA_INVALID_ARG, "table must be 2-byte aligned");
+    Kernel k;
+    const bool f16 = out_dtype == CUCA_F16;
+    if (ggml_type == CUCA_GGML_Q4_0)
+        k = f16 ? (a16 ? cuca_embed_q4_0_f16_a16 : cuca_embed_q4_0_f16_a2)
+                : (a16 ? cuca_embed_q4_0_f32_a16 : cuca_embed_q4_0_f32_a2);
+    else
+        k = f16 ? (a16 ? cuca_embed_q8_0_f16_a16 : cuca_embed_q8_0_f16_a2)
+                : (a16 ? cuca_embed_q8_0_f32_a16 : cuca_embed_q8_0_f32_a2);
+    EmbedArgs a{};
+    a.table = static_cast<const uint8_t *>(table);
+    a.ids = ids;
+    a.out = out;
+    a.status = ctx->status;
+    a.vocab = vocab;
+    a.row_bytes = row_bytes;
+    a.hidden = (int32_t)hidden;
+    a.n = (int32_t)n;
+    a.scale = scale;
+    ctx->last_vocab = vocab;
+    const int64_t nch = hidden / chunk_elems(out_dtype);
+    int64_t threads = (nch + 63) / 64 * 64;
+    if (threads > 256) threads = 256;
+    const unsigned lds = (unsigned)((row_bytes + 15) / 16 * 16);
+    return launch(ctx, k, (unsigned)n, (unsigned)threads, lds, a);
+}
+
+// ---------------------------------------------------------------------
+// residual add + RMSNorm
+// ---------------------------------------------------------------------
+
+cuca_status cuca_hip_add_rmsnorm(cuca_hip_ctx *ctx, const void *x, const void *branch,
+                                 const float *w, const float *w_post, float eps, float post_eps,
+                                 float residual_scale, int64_t rows, int64_t hidden, void *x_out,
+                                 void *h_out, cuca_dtype dtype) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    if (!dtype_ok(dtype)) return fail(ctx, CUCA_INVALID_ARG, "bad dtype %d", (int)dtype);
+    if (hidden <= 0 || hidden > (1 << 30)) return fail(ctx, CUCA_INVALID_ARG, "bad hidden size %lld", (long long)hidden);
+    if (rows < 0) return fail(ctx, CUCA_INVALID_ARG, "bad row count %lld", (long long)rows);
+    if (rows == 0) return CUCA_OK;
+    if (!x || !h_out) return fail(ctx, CUCA_INVALID_ARG, "null x or h_out");
+    if (w_post && !branch) return fail(ctx, CUCA_INVALID_ARG, "w_post needs a branch");
+    if (!(eps >= 0.0f) || !(post_eps >= 0.0f)) return fail(ctx, CUCA_INVALID_ARG, "eps must be >= 0");
+    const size_t es = esize(dtype);
+    NormArgs a{};
+    a.x = x;
+    a.branch = branch;
+    a.w = w;
+    a.w_post = w_post;
+    a.x_out = x_out;
+    a.h_out = h_out;
+    a.rows = rows;
+    a.hidden = (int32_t)hidden;
+    a.eps = eps;
+    a.post_eps = post_eps;
+    a.rs = residual_scale;
+    const int N = chunk_elems(dtype);
+    const bool vec = hidden % N == 0 && al16(x) && al16(h_out) && (!branch || al16(branch)) &&
+                     (!x_out || al16(x_out)) && (!w || al16(w)) && (!w_post || al16(w_post)) &&
+                     ((size_t)hidden * es) % 16 == 0;
+    const int64_t nch = hidden / N;
+    const bool f16 = dtype == CUCA_F16;
+    static const Kernel narrow32[] = {cuca_norm_f32_l1_c1, cuca_norm_f32_l2_c1, cuca_norm_f32_l4_c1,
+                                      cuca_norm_f32_l8_c1, cuca_norm_f32_l16_c1, cuca_norm_f32_l32_c1,
+                                      cuca_norm_f32_l64_c1};
+    static const Kernel narrow16[] = {cuca_norm_f16_l1_c1, cuca_norm_f16_l2_c1, cuca_norm_f16_l4_c1,
+                                      cuca_norm_f16_l8_c1, cuca_norm_f16_l16_c1, cuca_norm_f16_l32_c1,
+                                      cuca_norm_f16_l64_c1};
+    static const Kernel wide32[] = {cuca_norm_f32_l64_c1, cuca_norm_f32_l64_c2, cuca_norm_f32_l64_c4,
+                                    cuca_norm_f32_l64_c8, cuca_norm_f32_l64_c16, cuca_norm_f32_l64_c32};
+    static const Kernel wide16[] = {cuca_norm_f16_l64_c1, cuca_norm_f16_l64_c2, cuca_norm_f16_l64_c4,
+                                    cuca_norm_f16_l64_c8, cuca_norm_f16_l64_c16};
+    const int64_t max_nch = f16 ? 16 * 64 : 32 * 64;
+    if (rows > 0x7fffffffll) return fail(ctx, CUCA_UNSUPPORTED, "too many rows (%lld)", (long long)rows);
+    if (!vec || nch > max_nch) {
+        return launch(ctx, f16 ? cuca_norm_f16_generic : cuca_norm_f32_generic, (unsigned)rows, 256, 0, a);
+    }
+    Kernel k;
+    int64_t rows_per_block;
+    if (nch <= 64) {
+        int lg = 0;
+        while ((1ll << lg) < nch) lg++;  // lanes per row = 2^lg >= nch
+        k = f16 ? narrow16[lg] : narrow32[lg];
+        rows_per_block = 4 * (64 >> lg);
+    } else {
+        int lg = 0;
+        while ((64ll << lg) < nch) lg++;  // chunks per lane = 2^lg
+        k = f16 ? wide16[lg] : wide32[lg];
+        rows_per_block = 4;
+    }
+    return launch(ctx, k, div_up(rows, rows_per_block), 256, 0, a);
+}
+
+// ---------------------------------------------------------------------
+// gated activation
+// ---------------------------------------------------------------------
+
+static cuca_status glu_common(cuca_hip_ctx *ctx, const void *gate, int64_t gate_ld, const void *up,
+                              int64_t up_ld, const int32_t *offsets, int32_t n_experts, int64_t rows,
+                              int64_t ff, cuca_act act, float clamp, void *out, int64_t out_ld,
+                              cuca_dtype dtype) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    if (!dtype_ok(dtype)) return fail(ctx, CUCA_INVALID_ARG, "bad dtype %d", (int)dtype);
+    if (act != CUCA_ACT_SILU && act != CUCA_ACT_GELU_TANH)
+        return fail(ctx, CUCA_INVALID_ARG, "bad activation %d", (int)act);
+    if (ff <= 0 || ff > (1 << 30)) return fail(ctx, CUCA_INVALID_ARG, "bad ff %lld", (long long)ff);
+    if (rows < 0) return fail(ctx, CUCA_INVALID_ARG, "bad row count %lld", (long long)rows);
+    if (gate_ld < ff || up_ld < ff || out_ld < ff)
+        return fail(ctx, CUCA_INVALID_ARG, "row strides (%lld, %lld, %lld) shorter than ff %lld",
+                    (long long)gate_ld, (long long)up_ld, (long long)out_ld, (long long)ff);
+    if (rows == 0) return CUCA_OK;
+    if (!gate || !up || !out) return fail(ctx, CUCA_INVALID_ARG, "null pointer");
+    if (!(clamp == clamp)) return fail(ctx, CUCA_INVALID_ARG, "clamp is NaN");
+    const bool ragged = offsets != nullptr;
+    const size_t es = esize(dtype);
+    const int N = chunk_elems(dtype);
+    const bool vec = ff % N == 0 && al16(gate) && al16(up) && al16(out) && (gate_ld * es) % 16 == 0 &&
+                     (up_ld * es) % 16 == 0 && (out_ld * es) % 16 == 0;
+    const bool f16 = dtype == CUCA_F16, gelu = act == CUCA_ACT_GELU_TANH;
+    Kernel k;
+    int64_t bpr;
+    if (vec) {
+        bpr = (ff / N + 255) / 256;
+        k = f16 ? (gelu ? (ragged ? cuca_glu_f16_gelu_ragged : cuca_glu_f16_gelu)
+                        : (ragged ? cuca_glu_f16_silu_ragged : cuca_glu_f16_silu))
+                : (gelu ? (ragged ? cuca_glu_f32_gelu_ragged : cuca_glu_f32_gelu)
+                        : (ragged ? cuca_glu_f32_silu_ragged : cuca_glu_f32_silu));
+    } else {
+        bpr = (ff + 255) / 256;
+        k = f16 ? (gelu ? (ragged ? cuca_glu_f16_gelu_ragged_generic : cuca_glu_f16_gelu_generic)
+                        : (ragged ? cuca_glu_f16_silu_ragged_generic : cuca_glu_f16_silu_generic))
+                : (gelu ? (ragged ? cuca_glu_f32_gelu_ragged_generic : cuca_glu_f32_gelu_generic)
+                        : (ragged ? cuca_glu_f32_silu_ragged_generic : cuca_glu_f32_silu_generic));
+    }
+    if (rows * bpr > 0x7fffffffll) return fail(ctx, CUCA_UNSUPPORTED, "grid too large (%lld rows)", (long long)rows);
+    GluArgs a{};
+    a.gate = gate;
+    a.up = up;
+    a.out = out;
+    a.offsets = offsets;
+    a.rows = rows;
+    a.gate_ld = gate_ld;
+    a.up_ld = up_ld;
+    a.out_ld = out_ld;
+    a.ff = (int32_t)ff;
+    a.blocks_per_row = (int32_t)bpr;
+    a.n_experts = n_experts;
+    a.clamp = clamp > 0.0f ? clamp : 0.0f;
+    return launch(ctx, k, (unsigned)(rows * bpr), 256, 0, a);
+}
+
+cuca_status cuca_hip_glu(cuca_hip_ctx *ctx, const void *gate, int64_t gate_ld, const void *up,
+                         int64_t up_ld, int64_t rows, int64_t ff, cuca_act act, float clamp,
+                         void *out, int64_t out_ld, cuca_dtype dtype) {
+    return glu_common(ctx, gate, gate_ld, up, up_ld, nullptr, 0, rows, ff, act, clamp, out, out_ld, dtype);
+}
+
+cuca_status cuca_hip_glu_ragged(cuca_hip_ctx *ctx, const void *gate, int64_t gate_ld, const void *up,
+                                int64_t up_ld, const int32_t *expert_offsets, int32_t n_experts,
+                                int64_t max_rows, int64_t ff, cuca_act act, float clamp, void *out,
+                                int64_t out_ld, cuca_dtype dtype) {
+    if (!expert_offsets) return fail(ctx, CUCA_INVALID_ARG, "null expert_offsets");
+    if (n_experts <= 0) return fail(ctx, CUCA_INVALID_ARG, "bad expert count %d", n_experts);
+    return glu_common(ctx, gate, gate_ld, up, up_ld, expert_offsets, n_experts, max_rows, ff, act, clamp,
+                      out, out_ld, dtype);
+}
+
+// ---------------------------------------------------------------------
+// RoPE
+// ---------------------------------------------------------------------
+
+cuca_status cuca_hip_rope(cuca_hip_ctx *ctx, void *q, int64_t q_ld, void *k, int64_t k_ld, int64_t rows,
+                          int32_t nq, int32_t nk, int32_t head_dim, int32_t n_dims, cuca_rope_kind kind,
+                          const float *cos, const float *sin, int64_t table_rows, const int32_t *positions,
+                          const float *q_norm_w, const float *k_norm_w, float eps, cuca_dtype dtype) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    if (!dtype_ok(dtype)) return fail(ctx, CUCA_INVALID_ARG, "bad dtype %d", (int)dtype);
+    if (kind != CUCA_ROPE_NORM && kind != CUCA_ROPE_NEOX)
+        return fail(ctx, CUCA_INVALID_ARG, "bad rope kind %d", (int)kind);
+    if (head_dim <= 0 || n_dims <= 0 || n_dims > head_dim || n_dims % 2 != 0)
+        return fail(ctx, CUCA_INVALID_ARG, "n_dims %d must be even and within head_dim %d", n_dims, head_dim);
+    if (nq < 0 || nk < 0 || rows < 0) return fail(ctx, CUCA_INVALID_ARG, "negative count");
+    if (nq > 0 && (!q || q_ld < (int64_t)nq * head_dim))
+        return fail(ctx, CUCA_INVALID_ARG, "q row stride %lld shorter than %d heads of %d", (long long)q_ld, nq, head_dim);
+    if (nk > 0 && (!k || k_ld < (int64_t)nk * head_dim))
+        return fail(ctx, CUCA_INVALID_ARG, "k row stride %lld shorter than %d heads of %d", (long long)k_ld, nk, head_dim);
+    if (rows == 0 || nq + nk == 0) return CUCA_OK;
+    if (!cos || !sin || !positions) return fail(ctx, CUCA_INVALID_ARG, "null table or positions");
+    if (table_rows <= 0) return fail(ctx, CUCA_INVALID_ARG, "empty rope table");
+    if (!(eps >= 0.0f)) return fail(ctx, CUCA_INVALID_ARG, "eps must be >= 0");
+    if (rows * (int64_t)(nq + nk) > 0x7fffffffll) return fail(ctx, CUCA_UNSUPPORTED, "too many heads");
+    const size_t es = esize(dtype);
+    const int VP = chunk_elems(dtype);
+    const bool norm = q_norm_w || k_norm_w;
+    RopeArgs a{};
+    a.q = q;
+    a.k = k;
+    a.cos_t = cos;
+    a.sin_t = sin;
+    a.pos = positions;
+    a.q_norm_w = q_norm_w;
+    a.k_norm_w = k_norm_w;
+    a.status = ctx->status;
+    a.q_ld = q_ld;
+    a.k_ld = k_ld;
+    a.table_rows = table_rows;
+    a.rows = (int32_t)rows;
+    a.nq = nq;
+    a.nk = nk;
+    a.head_dim = head_dim;
+    a.n_dims = n_dims;
+    a.eps = eps;
+    a.kind = (int32_t)kind;
+    ctx->last_table_rows = table_rows;
+    const int tph = head_dim / (2 * VP);
+    const bool pow2 = tph > 0 && (tph & (tph - 1)) == 0 && tph <= 64;
+    const bool vec = head_dim % (2 * VP) == 0 && n_dims % (2 * VP) == 0 && pow2 &&
+                     (nq == 0 || (al16(q) && (q_ld * es) % 16 == 0)) &&
+                     (nk == 0 || (al16(k) && (k_ld * es) % 16 == 0)) && al16(cos) && al16(sin) &&
+                     (!q_norm_w || al16(q_norm_w)) && (!k_norm_w || al16(k_norm_w));
+    const bool f16 = dtype == CUCA_F16, neox = kind == CUCA_ROPE_NEOX;
+    const int64_t heads = rows * (nq + nk);
+    if (!vec) {
+        Kernel kk = f16 ? cuca_rope_f16_generic : cuca_rope_f32_generic;
+        return launch(ctx, kk, div_up(heads, 4), 256, 0, a);
+    }
+    int lg = 0;
+    while ((1 << lg) < tph) lg++;
+    a.tph_log2 = lg;
+    Kernel kk = f16 ? (neox ? (norm ? cuca_rope_f16_neox_qkn : cuca_rope_f16_neox)
+                            : (norm ? cuca_rope_f16_norm_qkn : cuca_rope_f16_norm))
+                    : (neox ? (norm ? cuca_rope_f32_neox_qkn : cuca_rope_f32_neox)
+                            : (norm ? cuca_rope_f32_norm_qkn : cuca_rope_f32_norm));
+    return launch(ctx, kk, div_up(heads, 256 / tph), 256, 0, a);
+}
+
+// RopeSpec::tables (rope.rs:118-151): f64 angles with the platform libm,
+// `cos(theta) * mscale` rounded to f32.
+cuca_status cuca_hip_rope_tables(const cuca_rope_spec *spec, const float *factors, int64_t positions,
+                                 float *cos_out, float *sin_out) {
+    if (!spec || !cos_out || !sin_out) return fail(nullptr, CUCA_INVALID_ARG, "null pointer");
+    const int n_dims = spec->n_dims;
+    if (n_dims <= 0 || n_dims % 2 != 0) return fail(nullptr, CUCA_INVALID_ARG, "n_dims %d must be even", n_dims);
+    if (positions < 0) return fail(nullptr, CUCA_INVALID_ARG, "negative position count");
+    if (!(spec->base > 0.0) || !(spec->freq_scale > 0.0))
+        return fail(nullptr, CUCA_INVALID_ARG, "base and freq_scale must be positive");
+    const int half = n_dims / 2;
+    if (factors)
+        for (int i = 0; i < half; i++)
+            if (!(factors[i] > 0.0f) || !std::isfinite(factors[i]))
+                return fail(nullptr, CUCA_INVALID_ARG, "factors must be finite and positive");
+    const bool yarn = spec->yarn_ext_factor != 0.0;
+    double c0 = 0.0, c1 = 0.0;
+    if (yarn) {
+        // ggml rope_yarn_corr_dims (rope.rs:86-99)
+        auto corr = [&](double n_rot) {
+            return (double)n_dims * std::log((double)spec->yarn_n_ctx_orig / (n_rot * 2.0 * M_PI)) /
+                   (2.0 * std::log(spec->base));
+        };
+        c0 = std::fmax(0.0, std::floor(corr(spec->yarn_beta_fast)));
+        c1 = std::fmin((double)(n_dims - 1), std::ceil(corr(spec->yarn_beta_slow)));
+    }
+    for (int64_t pos = 0; pos < positions; pos++) {
+        for (int i = 0; i < half; i++) {
+            const double factor = factors ? (double)factors[i] : 1.0;
+            const int i0 = 2 * i;
+            const double extrap = (double)pos * std::pow(spec->base, -(double)i0 / (double)n_dims) / factor;
+            const double interp = spec->freq_scale * extrap;
+            double theta = interp, mscale = spec->attn_factor;
+            if (yarn) {
+                double r = ((double)(i0 / 2) - c0) / std::fmax(c1 - c0, 0.001);
+                r = r < 0.0 ? 0.0 : (r > 1.0 ? 1.0 : r);
+                const double mix = (1.0 - r) * spec->yarn_ext_factor;
+                mscale = spec->attn_factor * (1.0 + 0.1 * std::log(1.0 / spec->freq_scale));
+                theta = interp * (1.0 - mix) + extrap * mix;
+            }
+            cos_out[pos * half + i] = (float)(std::cos(theta) * mscale);
+            sin_out[pos * half + i] = (float)(std::sin(theta) * mscale);
+        }
+    }
+    return CUCA_OK;
+}
+
+// ---------------------------------------------------------------------
+// graphs and timing
+// ---------------------------------------------------------------------
+
+cuca_status cuca_hip_graph_begin(cuca_hip_ctx *ctx) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    if (ctx->capturing) return fail(ctx, CUCA_INVALID_ARG, "a capture is already open");
+    HIP_TRY(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    ctx->capturing = true;
+    return CUCA_OK;
+}
+
+cuca_status cuca_hip_graph_end(cuca_hip_ctx *ctx, cuca_hip_graph **out) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    if (!out) return fail(ctx, CUCA_INVALID_ARG, "null output pointer");
+    *out = nullptr;
+    if (!ctx->capturing) return fail(ctx, CUCA_INVALID_ARG, "no capture is open");
+    ctx->capturing = false;
+    hipGraph_t g = nullptr;
+    HIP_TRY(ctx, hipStreamEndCapture(ctx->stream, &g));
+    hipGraphExec_t exec = nullptr;
+    hipError_t e = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        return hip_fail(ctx, e, "hipGraphInstantiate");
+    }
+    *out = new cuca_hip_graph{g, exec};
+    return CUCA_OK;
+}
+
+cuca_status cuca_hip_graph_launch(cuca_hip_ctx *ctx, cuca_hip_graph *graph) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    if (!graph) return fail(ctx, CUCA_INVALID_ARG, "null graph");
+    HIP_TRY(ctx, hipGraphLaunch(graph->exec, ctx->stream));
+    return CUCA_OK;
+}
+
+void cuca_hip_graph_destroy(cuca_hip_graph *graph) {
+    if (!graph) return;
+    if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
+    if (graph->graph) (void)hipGraphDestroy(graph->graph);
+    delete graph;
+}
+
+cuca_status cuca_hip_timer_start(cuca_hip_ctx *ctx) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    HIP_TRY(ctx, hipEventRecord(ctx->t0, ctx->stream));
+    return CUCA_OK;
+}
+
+cuca_status cuca_hip_timer_stop(cuca_hip_ctx *ctx, float *ms) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    if (!ms) return fail(ctx, CUCA_INVALID_ARG, "null output pointer");
+    HIP_TRY(ctx, hipEventRecord(ctx->t1, ctx->stream));
+    HIP_TRY(ctx, hipEventSynchronize(ctx->t1));
+    HIP_TRY(ctx, hipEventElapsedTime(ms, ctx->t0, ctx->t1));
+    return CUCA_OK;
+}
+
+}  // extern "C"

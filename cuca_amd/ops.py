@@ -1,0 +1,206 @@
+"""The reference's per-layer op surface, over the C ABI.
+
+Names, argument meaning and errors follow provider-local's op sites (paths
+under src/provider/local/model/ of nassor/cuca 0.10.0), so that a caller
+(and the parity tests) read like the reference:
+
+    TokenEmbedding(dtype, data, rows, row_len).rows(tokens, scale)  quant.rs:352-411
+    rms(x, weight, eps)                                              cpu.rs:3652
+    add_rms(x, branch, weight, eps, ...)  (x + branch, rms of it)    cpu.rs:2650-2711
+    Glu(act, clamp).apply(gate, up)                                  cpu.rs:342-371
+    apply_rope(x, cos, sin, kind, n_dims, positions)                 cpu.rs:3672-3688
+    RopeSpec.plain(kind, n_dims, base).tables(factors, positions)    rope.rs:62-151
+
+Tensors are DeviceArrays (device memory through the C ABI); every op runs on
+the gfx950 kernels of libcuca_hip.so.  There is no host fallback.
+"""
+
+import numpy as np
+
+from . import hip
+from .hip import CucaError, DeviceArray
+
+_GGML_NAME = {hip.GGML_Q4_0: "Q4_0", hip.GGML_Q8_0: "Q8_0"}
+_BLOCK_BYTES = {hip.GGML_Q4_0: 18, hip.GGML_Q8_0: 34}
+
+
+def byte_len(ggml_type, n):
+    """GgufType::byte_len for Q4_0 / Q8_0 (gguf/dtype.rs:195-250): bytes of n
+    values, or None when n is not a whole number of 32-value blocks."""
+    if ggml_type not in _BLOCK_BYTES or n % 32 != 0:
+        return None
+    return n // 32 * _BLOCK_BYTES[ggml_type]
+
+
+class TokenEmbedding:
+    """The token-embedding table held in the file's type (quant.rs:352-411),
+    resident in HBM; a lookup dequantizes only the rows it reads, on the GPU."""
+
+    def __init__(self, ctx, dtype, data, rows, row_len):
+        if dtype not in _BLOCK_BYTES:
+            raise CucaError(hip.UNSUPPORTED, f"ggml type {dtype}: only Q4_0 and Q8_0 are supported")
+        name = _GGML_NAME[dtype]
+        row_bytes = byte_len(dtype, row_len)
+        if row_bytes is None:  # quant.rs:362-367
+            raise CucaError(hip.INVALID_ARG, f"token embedding: row length {row_len} is not a "
+                            f"whole number of {name} blocks")
+        data = np.ascontiguousarray(np.frombuffer(data, np.uint8) if isinstance(data, bytes)
+                                    else data, dtype=np.uint8).reshape(-1)
+        if rows * row_bytes != data.size:  # quant.rs:368-374
+            raise CucaError(hip.INVALID_ARG, f"token embedding: {data.size} bytes do not hold "
+                            f"{rows} rows of {row_len} {name} values")
+        self.ctx = ctx
+        self.dtype = dtype
+        self.rows_n = rows
+        self.row_len = row_len
+        self.row_bytes = row_bytes
+        self.table = ctx.array(data)
+
+    def rows(self, tokens, scale, out_dtype=np.float32):
+        """Embedding rows of `tokens`, concatenated and multiplied by `scale`
+        (quant.rs:391-411): a DeviceArray [len(tokens), row_len]."""
+        ids = np.asarray(tokens, dtype=np.int64).reshape(-1)
+        for i in ids:  # quant.rs:395-400, before anything runs
+            if i < 0 or i >= self.rows_n:
+                raise CucaError(hip.OUT_OF_RANGE, f"token id {int(i)} outside the embedding table "
+                                f"of {self.rows_n} rows")
+        dev_ids = self.ctx.array(ids.astype(np.uint32))
+        out = self.ctx.empty((ids.size, self.row_len), out_dtype)
+        self.rows_device(dev_ids, scale, out)
+        return out
+
+    def rows_device(self, ids, scale, out):
+        """The gather for ids already on the device (u32 DeviceArray); bad ids
+        are reported by ctx.check_device()."""
+        self.ctx.embed_gguf(self.table.ptr, self.dtype, self.rows_n, self.row_len, ids.ptr,
+                            ids.size, scale, out.ptr, hip.dtype_code(out.dtype))
+        return out
+
+
+def _w(ctx, w):
+    if w is None or isinstance(w, DeviceArray):
+        return w
+    return ctx.array(np.asarray(w, dtype=np.float32))
+
+
+def add_rms(x, branch, weight, eps, w_post=None, post_eps=None, residual_scale=1.0,
+            write_x=True, x_out=None, h_out=None):
+    """The fused residual add + RMSNorm of Transformer::block
+    (cpu.rs:2650-2711): returns (x', h) with x' = x + rs * [rms(branch,
+    w_post, post_eps)] and h = rms(x', weight, eps).  x_out may be x."""
+    ctx = x.ctx
+    rows, hidden = x.shape[0], int(np.prod(x.shape[1:]))
+    w = _w(ctx, weight)
+    wp = _w(ctx, w_post)
+    if write_x and x_out is None:
+        x_out = ctx.empty(x.shape, x.dtype)
+    if h_out is None:
+        h_out = ctx.empty(x.shape, x.dtype)
+    ctx.add_rmsnorm(x.ptr, None if branch is None else branch.ptr, None if w is None else w.ptr,
+                    None if wp is None else wp.ptr, eps, eps if post_eps is None else post_eps,
+                    residual_scale, rows, hidden, None if x_out is None else x_out.ptr,
+                    h_out.ptr, hip.dtype_code(x.dtype))
+    return (x_out if write_x else None), h_out
+
+
+def rms(x, weight, eps):
+    """RMSNorm with a learned weight, no `1 + w` (cpu.rs:3652); weight None
+    is the weightless norm (gpu.rs:5895).  The last dim is normalized."""
+    hidden = x.shape[-1]
+    rows = x.size // hidden
+    ctx = x.ctx
+    w = _w(ctx, weight)
+    out = ctx.empty(x.shape, x.dtype)
+    ctx.add_rmsnorm(x.ptr, None, None if w is None else w.ptr, None, eps, eps, 1.0, rows, hidden,
+                    None, out.ptr, hip.dtype_code(x.dtype))
+    return out
+
+
+class Glu:
+    """The gated activation `act(gate) * up` with the optional clamp
+    (cpu.rs:342-371)."""
+
+    def __init__(self, act, clamp=None):
+        self.act = act
+        self.clamp = clamp if (clamp is not None and clamp > 0.0) else None
+
+    @classmethod
+    def clamped(cls, act, limit):
+        return cls(act, limit if limit > 0.0 else None)
+
+    def apply(self, gate, up, out=None, rows=None, ff=None, gate_ld=None, up_ld=None):
+        ctx = gate.ctx
+        ff = gate.shape[-1] if ff is None else ff
+        rows = gate.size // gate.shape[-1] if rows is None else rows
+        if out is None:
+            out = ctx.empty((rows, ff), gate.dtype)
+        ctx.glu(gate.ptr, gate_ld or ff, up.ptr, up_ld or ff, rows, ff, self.act,
+                self.clamp or 0.0, out.ptr, ff, hip.dtype_code(gate.dtype))
+        return out
+
+    def apply_fused(self, y, ff):
+        """GateUp::Fused: y [rows, 2*ff] = [gate | up] (cpu.rs:3559-3562)."""
+        rows = y.shape[0]
+        return self.apply(y, y.view(ff, y.shape), rows=rows, ff=ff, gate_ld=2 * ff, up_ld=2 * ff)
+
+    def apply_ragged(self, gate, up, expert_offsets, n_experts, out=None):
+        """Rows grouped by expert (moe.rs:39-94); expert_offsets is a device
+        int32 [n_experts + 1] prefix sum read on the device."""
+        ctx = gate.ctx
+        rows, ff = gate.shape
+        if out is None:
+            out = ctx.empty((rows, ff), gate.dtype)
+        ctx.glu_ragged(gate.ptr, ff, up.ptr, ff, expert_offsets.ptr, n_experts, rows, ff,
+                       self.act, self.clamp or 0.0, out.ptr, ff, hip.dtype_code(gate.dtype))
+        return out
+
+
+def apply_rope(x, cos, sin, kind, n_dims, positions, norm_w=None, eps=1e-6):
+    """Rotate the first n_dims values of every head of x [rows, heads, d] in
+    place (apply_rope, cpu.rs:3672-3688); cos/sin are device [table_rows,
+    n_dims/2] tables and positions a device int32 [rows].  norm_w fuses the
+    per-head QK-norm in front (cpu.rs:2840-2864)."""
+    rows, heads, d = x.shape
+    ctx = x.ctx
+    nw = _w(ctx, norm_w)
+    ctx.rope(x.ptr, heads * d, None, 0, rows, heads, 0, d, n_dims, kind, cos.ptr, sin.ptr,
+             cos.shape[0], positions.ptr, None if nw is None else nw.ptr, None, eps,
+             hip.dtype_code(x.dtype))
+    return x
+
+
+def rope_qk(q, k, cos, sin, kind, n_dims, positions, q_norm_w=None, k_norm_w=None, eps=1e-6):
+    """Q and K of one attention call in one launch, with the optional QK-norm."""
+    rows, nq, d = q.shape
+    nk = 0 if k is None else k.shape[1]
+    ctx = q.ctx
+    qw, kw = _w(ctx, q_norm_w), _w(ctx, k_norm_w)
+    ctx.rope(q.ptr, nq * d, None if k is None else k.ptr, nk * d, rows, nq, nk, d, n_dims, kind,
+             cos.ptr, sin.ptr, cos.shape[0], positions.ptr, None if qw is None else qw.ptr,
+             None if kw is None else kw.ptr, eps, hip.dtype_code(q.dtype))
+    return q, k
+
+
+class RopeSpec:
+    """One rotary embedding (rope.rs:62-79)."""
+
+    def __init__(self, kind, n_dims, base, freq_scale=1.0, yarn=None, attn_factor=1.0):
+        self.kind = kind
+        self.n_dims = n_dims
+        self.base = base
+        self.freq_scale = freq_scale
+        self.yarn = yarn
+        self.attn_factor = attn_factor
+
+    @classmethod
+    def plain(cls, kind, n_dims, base):
+        return cls(kind, n_dims, base)
+
+    def tables(self, factors, positions):
+        """Host (cos, sin) f32 [positions, n_dims/2] (rope.rs:136-151)."""
+        return hip.rope_tables(self.kind, self.n_dims, self.base, positions, self.freq_scale,
+                               self.yarn, self.attn_factor, factors)
+
+    def device_tables(self, ctx, factors, positions):
+        cos, sin = self.tables(factors, positions)
+        return ctx.array(cos), ctx.array(sin)

@@ -1,0 +1,233 @@
+/*
+ * cuca_hip.h -- C ABI of the MI355X (gfx950) per-layer ops of the
+ * provider-local GGUF engine of nassor/cuca 0.10.0.
+ *
+ * This is the drop-in boundary.  Each op replaces one op site of the
+ * reference's layer loop (paths relative to src/provider/local/model/):
+ *
+ *   cuca_hip_embed_gguf    TokenEmbedding::rows           quant.rs:391-411
+ *                          (GPU engine: RowTable::rows +  quant.rs:477-501,
+ *                           upload in forward_stage)      gpu.rs:2976-2982, 4589-4598
+ *   cuca_hip_add_rmsnorm   rms / residual add in block    cpu.rs:2650-2711, 3652
+ *                          GPU rms, attn_tail, ffn_half,  gpu.rs:5420-5483, 5883-5896
+ *                          ffn_tail
+ *   cuca_hip_glu           activate(gate) * up, Glu::apply cpu.rs:342-371, 3554-3566, 3644
+ *                          GPU activate / gelu            gpu.rs:5899-5913
+ *   cuca_hip_glu_ragged    the same over expert-grouped   cpu.rs:3599-3642, moe.rs:39-94,
+ *                          rows (MoE up epilogue)         moe_kernel.rs:1265-1288
+ *   cuca_hip_rope          apply_rope / rotate_calls,     cpu.rs:2837-2871, 2996-3026,
+ *                          with the per-head QK-norm      3040-3055, 3672-3688
+ *                          GPU rope                       gpu.rs:5922-5964
+ *   cuca_hip_rope_tables   RopeSpec::tables (host)        rope.rs:118-151, mod.rs:460-472
+ *
+ * Conventions
+ * - A context owns one device, one HIP stream (or borrows the caller's),
+ *   the loaded gfx950 code object and a device status word.  A context is
+ *   not thread-safe: one per engine thread, as the reference runs every model
+ *   call on its single engine thread (local/mod.rs:2478).
+ * - Every buffer argument is a device pointer the caller owns (allocated
+ *   with cuca_hip_malloc or any other HIP allocator on the context's
+ *   device).  Ops never allocate, never synchronize and never retain a
+ *   pointer after they return, except inside a captured graph.
+ * - Ops are asynchronous on the context's stream; call cuca_hip_stream_sync
+ *   before reading results on the host.
+ * - Activations are f32 or f16 (cuca_dtype); arithmetic is always f32,
+ *   and f16 results are rounded once, to nearest-even.
+ * - Errors: every entry point returns a cuca_status; a message is kept for
+ *   cuca_hip_last_error.  Argument errors are caught on the host before any
+ *   launch.  Values only the device sees (token ids, positions) are checked
+ *   by the kernels, which skip the bad row and record it in the status word
+ *   that cuca_hip_check_device (a blocking call) reports.
+ */
+#ifndef CUCA_HIP_H
+#define CUCA_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CUCA_HIP_ABI_VERSION 1
+
+typedef struct cuca_hip_ctx cuca_hip_ctx;
+typedef struct cuca_hip_graph cuca_hip_graph;
+
+/* The reference maps its errors to CucaError::Provider(Local, msg)
+ * (model/mod.rs:222-228); a binding maps every non-OK status the same way,
+ * with cuca_hip_last_error as the message. */
+typedef enum {
+    CUCA_OK = 0,
+    CUCA_INVALID_ARG = 1,  /* shape, type, alignment or pointer error      */
+    CUCA_OUT_OF_RANGE = 2, /* token id >= vocab, position outside the table */
+    CUCA_HIP_ERROR = 3,    /* a HIP runtime call failed                     */
+    CUCA_NOT_GFX950 = 4,   /* the device is not an MI355X-class gfx950      */
+    CUCA_UNSUPPORTED = 5   /* a valid request this build has no kernel for  */
+} cuca_status;
+
+typedef enum { CUCA_F32 = 0, CUCA_F16 = 1 } cuca_dtype;
+
+/* ggml type ids (gguf/dtype.rs:195-250). */
+typedef enum { CUCA_GGML_Q4_0 = 2, CUCA_GGML_Q8_0 = 8 } cuca_ggml_type;
+
+/* Act (arch.rs:101-106). */
+typedef enum { CUCA_ACT_SILU = 0, CUCA_ACT_GELU_TANH = 1 } cuca_act;
+
+/* RopeKind (rope.rs:28-36), llama.cpp's rope type values. */
+typedef enum { CUCA_ROPE_NORM = 0, CUCA_ROPE_NEOX = 2 } cuca_rope_kind;
+
+/* ------------------------------------------------------------------ */
+/* Context, memory, stream                                              */
+/* ------------------------------------------------------------------ */
+
+/* Open `device`, check it is gfx950, create a stream of default priority
+ * and load the kernels.  Replaces the device open of GpuTransformer::load
+ * (gpu.rs:2597, adapter log gpu.rs:403-420). */
+cuca_status cuca_hip_ctx_create(int device, cuca_hip_ctx **out);
+void cuca_hip_ctx_destroy(cuca_hip_ctx *ctx);
+
+/* The last error message of `ctx`, or of the calling thread when ctx is
+ * NULL (context creation failures).  Never NULL; "" when there is none. */
+const char *cuca_hip_last_error(const cuca_hip_ctx *ctx);
+
+/* Run the context's work on `stream` (a hipStream_t of the same device,
+ * e.g. the caller's framework stream); NULL returns to the context's own. */
+cuca_status cuca_hip_set_stream(cuca_hip_ctx *ctx, void *stream);
+/* The hipStream_t ops are issued on. */
+void *cuca_hip_get_stream(const cuca_hip_ctx *ctx);
+int cuca_hip_device(const cuca_hip_ctx *ctx);
+
+cuca_status cuca_hip_malloc(cuca_hip_ctx *ctx, size_t bytes, void **out);
+cuca_status cuca_hip_free(cuca_hip_ctx *ctx, void *ptr);
+cuca_status cuca_hip_memcpy_h2d_async(cuca_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
+cuca_status cuca_hip_memcpy_d2h_async(cuca_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
+cuca_status cuca_hip_memcpy_d2d_async(cuca_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
+cuca_status cuca_hip_stream_sync(cuca_hip_ctx *ctx);
+
+/* Synchronize, then report (and clear) what the kernels recorded in the
+ * status word: CUCA_OUT_OF_RANGE with the first bad row in the message
+ * ("token id {id} outside the embedding table of {rows} rows", as
+ * quant.rs:395-400, or a RoPE position outside its table). */
+cuca_status cuca_hip_check_device(cuca_hip_ctx *ctx);
+
+/* ------------------------------------------------------------------ */
+/* Ops                                                                  */
+/* ------------------------------------------------------------------ */
+
+/* Token-embedding dequant-gather (TokenEmbedding::rows, quant.rs:391-411;
+ * dequant_ggml_row Q4_0/Q8_0, quant.rs:107-198).
+ *   table : [vocab, hidden/32 blocks] of ggml_type, resident on the device
+ *   ids   : device u32[n]
+ *   out   : device [n, hidden] of out_dtype
+ * out[t, :] = dequant_row(table row ids[t]) with `scale` folded into each
+ * block's f16 scale first (bit-exact with the reference; f16 output is the
+ * f32 value rounded to nearest-even).  hidden must be a multiple of 32.
+ * An id >= vocab writes a zero row and is reported by cuca_hip_check_device. */
+cuca_status cuca_hip_embed_gguf(cuca_hip_ctx *ctx, const void *table, uint32_t ggml_type,
+                                int64_t vocab, int64_t hidden, const uint32_t *ids,
+                                int64_t n, float scale, void *out, cuca_dtype out_dtype);
+
+/* Fused residual add + RMSNorm (Transformer::block, cpu.rs:2650-2711, with
+ * rms = candle_nn::ops::rms_norm, cpu.rs:3652; GPU attn_tail / ffn_half /
+ * ffn_tail, gpu.rs:5420-5483):
+ *   b  = w_post ? rms(branch, w_post, post_eps) : branch   (Gemma sandwich)
+ *   x' = branch ? x + residual_scale * b : x              -> x_out (nullable)
+ *   h  = rms(x' as stored, w, eps)                         -> h_out
+ * rms(v, w, eps) = v / sqrt(mean(v^2) + eps) * w; w == NULL is the
+ * weightless norm.  All of x, branch, x_out, h_out are [rows, hidden] of
+ * `dtype`; x_out may alias x; w and w_post are f32[hidden].  With branch ==
+ * NULL this is the plain `rms(x, w, eps)`. */
+cuca_status cuca_hip_add_rmsnorm(cuca_hip_ctx *ctx, const void *x, const void *branch,
+                                 const float *w, const float *w_post, float eps,
+                                 float post_eps, float residual_scale, int64_t rows,
+                                 int64_t hidden, void *x_out, void *h_out, cuca_dtype dtype);
+
+/* Gated activation (Glu::apply, cpu.rs:362-371; activate, cpu.rs:3644;
+ * FfnWeights::forward GateUp::{Split, Fused}, cpu.rs:319-330, 3554-3566):
+ *   g = clamp > 0 ? min(g, clamp) : g,  u = clamp > 0 ? clamp(u, -clamp, clamp) : u
+ *   out[r, j] = act(g[r, j]) * u[r, j]
+ * Row r of gate/up/out starts at r * gate_ld / up_ld / out_ld elements, so
+ * the fused [gate | up] projection is gate = y, up = y + ff, ld = 2 * ff.
+ * SiLU g / (1 + e^-g); GELU-tanh 0.5 g (1 + tanh(sqrt(2/pi) (g + 0.044715 g^3))). */
+cuca_status cuca_hip_glu(cuca_hip_ctx *ctx, const void *gate, int64_t gate_ld,
+                         const void *up, int64_t up_ld, int64_t rows, int64_t ff,
+                         cuca_act act, float clamp, void *out, int64_t out_ld,
+                         cuca_dtype dtype);
+
+/* The gated activation over MoE rows grouped by expert (route_with's
+ * per-expert grouping, moe.rs:39-94; expert_sum, cpu.rs:3599-3642; the
+ * reference fuses the same activation into up_kernel's epilogue,
+ * moe_kernel.rs:1265-1288).  expert_offsets is a DEVICE int32[n_experts + 1]
+ * prefix sum: expert e owns rows [offsets[e], offsets[e+1]).  The row count
+ * is read on the device (offsets[n_experts], capped at max_rows), so routing
+ * done on the device needs no host round trip and the call can be captured
+ * in a graph.  Rows past the count are not touched. */
+cuca_status cuca_hip_glu_ragged(cuca_hip_ctx *ctx, const void *gate, int64_t gate_ld,
+                                const void *up, int64_t up_ld,
+                                const int32_t *expert_offsets, int32_t n_experts,
+                                int64_t max_rows, int64_t ff, cuca_act act, float clamp,
+                                void *out, int64_t out_ld, cuca_dtype dtype);
+
+/* Rotary embedding on Q and K in place (apply_rope, cpu.rs:3672-3688 ->
+ * candle rope (NEOX) / rope_i (NORM); rotate_calls, cpu.rs:2996-3026; GPU
+ * rope, gpu.rs:5922-5964), with the optional per-head QK-norm fused in
+ * front (cpu.rs:2840-2864 for Q, 3040-3055 for K).
+ *   q : [rows, nq, head_dim] with row stride q_ld elements (>= nq*head_dim)
+ *   k : [rows, nk, head_dim] with row stride k_ld (k may be NULL when nk = 0)
+ *   cos, sin : f32 [table_rows, n_dims/2] (cuca_hip_rope_tables)
+ *   positions: device int32[rows], each < table_rows
+ * For every head: v = q_norm_w ? rms(head, q_norm_w[head_dim], eps) : head,
+ * then pair i of the first n_dims values (NORM: 2i, 2i+1; NEOX: i, i+n/2):
+ *   a' = a*c - b*s,  b' = a*s + b*c        (rope.rs:158-171)
+ * with each product rounded separately (no FMA): without QK-norm the result
+ * is bit-identical to the reference's f32 rotation.  Values past n_dims pass
+ * through (normalized when a norm weight is given).  k_norm_w applies to K. */
+cuca_status cuca_hip_rope(cuca_hip_ctx *ctx, void *q, int64_t q_ld, void *k, int64_t k_ld,
+                          int64_t rows, int32_t nq, int32_t nk, int32_t head_dim,
+                          int32_t n_dims, cuca_rope_kind kind, const float *cos,
+                          const float *sin, int64_t table_rows, const int32_t *positions,
+                          const float *q_norm_w, const float *k_norm_w, float eps,
+                          cuca_dtype dtype);
+
+/* RopeSpec (rope.rs:62-79). yarn_ext_factor == 0 disables YaRN. */
+typedef struct {
+    int32_t kind;         /* cuca_rope_kind (not used by the tables)   */
+    int32_t n_dims;       /* rotated leading dims, even                 */
+    double base;          /* frequency base (theta)                     */
+    double freq_scale;    /* 1 / scaling factor; 1.0 when unscaled      */
+    double yarn_ext_factor, yarn_beta_fast, yarn_beta_slow;
+    int64_t yarn_n_ctx_orig;
+    double attn_factor;   /* multiplier on cos and sin; 1.0 when plain  */
+} cuca_rope_spec;
+
+/* Host-side RopeSpec::tables (rope.rs:118-151): cos/sin [positions, n_dims/2]
+ * computed in f64 with the platform libm and rounded to f32, bit-identical
+ * to the reference's tables.  factors: NULL or n_dims/2 positive divisors
+ * (rope_factors, mod.rs:420-458).  Writes host memory; upload once. */
+cuca_status cuca_hip_rope_tables(const cuca_rope_spec *spec, const float *factors,
+                                 int64_t positions, float *cos_out, float *sin_out);
+
+/* ------------------------------------------------------------------ */
+/* Graphs (decode) and timing                                           */
+/* ------------------------------------------------------------------ */
+
+/* Capture every op issued on the context's stream between begin and end
+ * into an executable graph (the per-layer launches of a decode step).  The
+ * captured ops keep the pointers and scalars they were called with; replay
+ * with cuca_hip_graph_launch after refreshing the buffers' contents. */
+cuca_status cuca_hip_graph_begin(cuca_hip_ctx *ctx);
+cuca_status cuca_hip_graph_end(cuca_hip_ctx *ctx, cuca_hip_graph **out);
+cuca_status cuca_hip_graph_launch(cuca_hip_ctx *ctx, cuca_hip_graph *graph);
+void cuca_hip_graph_destroy(cuca_hip_graph *graph);
+
+/* Elapsed milliseconds of the work issued on the context's stream between
+ * cuca_hip_timer_start and cuca_hip_timer_stop (HIP events; blocks until
+ * the stop event completes). */
+cuca_status cuca_hip_timer_start(cuca_hip_ctx *ctx);
+cuca_status cuca_hip_timer_stop(cuca_hip_ctx *ctx, float *ms);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,411 @@
+/*
+ * cuca_oracle.c -- CPU restatement of the reference's per-layer ops.
+ *
+ * TEST INFRASTRUCTURE ONLY: the parity checker and the CPU-baseline timer.
+ * Nothing in the product (cuca_amd/, libcuca_hip.so) links or loads it.
+ * Build: oracle/build.py (gcc -O2 -ffp-contract=off -pthread).
+ *
+ * Each function names the reference file:line it follows; paths are under
+ * src/provider/local/model/ of nassor/cuca 0.10.0.  Where the reference
+ * calls candle 0.11.1 (not vendored in the reference), the restated
+ * formula is the one the reference's own tests and GPU mirror state
+ * (gpu.rs:5883-5913, moe_kernel.rs:2340-2352); the bit-level summation
+ * order of candle's kernels is not pinned (see the tests' tolerances).
+ */
+#include "cuca_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------ */
+/* binary16 conversions                                                */
+/* ------------------------------------------------------------------ */
+
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+float oracle_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu;
+    uint32_t m = h & 0x3ffu;
+    if (e == 0) {
+        if (m == 0) return u2f(sign);
+        /* subnormal: m * 2^-24, exact in f32 */
+        float v = (float)m * 5.9604644775390625e-8f;
+        return u2f(sign | f2u(v));
+    }
+    if (e == 31) return u2f(sign | 0x7f800000u | (m << 13));
+    return u2f(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+uint16_t oracle_f32_to_f16(float f) {
+    uint32_t x = f2u(f);
+    uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    uint32_t ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) { /* inf / nan (quiet the nan, keep top payload) */
+        if (ax == 0x7f800000u) return sign | 0x7c00u;
+        return sign | 0x7e00u | (uint16_t)((ax >> 13) & 0x3ffu);
+    }
+    uint32_t e = ax >> 23;
+    uint32_t m = ax & 0x7fffffu;
+    if (e < 113) { /* below 2^-14: f16 subnormal or zero */
+        if (e == 0) return sign; /* f32 subnormal is far below half of 2^-24 */
+        uint32_t M = m | 0x800000u;
+        uint32_t s = 126u - e; /* >= 14 */
+        if (s >= 25) return sign;
+        uint32_t r = M >> s;
+        uint32_t rem = M & ((1u << s) - 1u);
+        uint32_t half = 1u << (s - 1u);
+        if (rem > half || (rem == half && (r & 1u))) r++;
+        return sign | (uint16_t)r;
+    }
+    if (e > 142) return sign | 0x7c00u; /* >= 2^16: overflow */
+    uint32_t h = ((e - 112u) << 10) | (m >> 13);
+    uint32_t rem = m & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++; /* carries into e */
+    return sign | (uint16_t)h;
+}
+
+void oracle_f16_to_f32_n(const uint16_t *h, float *f, int64_t n) {
+    for (int64_t i = 0; i < n; i++) f[i] = oracle_f16_to_f32(h[i]);
+}
+
+void oracle_f32_to_f16_n(const float *f, uint16_t *h, int64_t n) {
+    for (int64_t i = 0; i < n; i++) h[i] = oracle_f32_to_f16(f[i]);
+}
+
+static inline float load_el(const void *p, int64_t i, int dtype) {
+    return dtype == OR_F16 ? oracle_f16_to_f32(((const uint16_t *)p)[i])
+                           : ((const float *)p)[i];
+}
+
+static inline void store_el(void *p, int64_t i, float v, int dtype) {
+    if (dtype == OR_F16) ((uint16_t *)p)[i] = oracle_f32_to_f16(v);
+    else ((float *)p)[i] = v;
+}
+
+/* ------------------------------------------------------------------ */
+/* a tiny row-parallel for (the CPU-baseline's threading)              */
+/* ------------------------------------------------------------------ */
+
+typedef void (*range_fn)(void *ctx, int64_t begin, int64_t end);
+
+typedef struct {
+    range_fn fn;
+    void *ctx;
+    int64_t begin, end;
+} range_job;
+
+static void *range_thread(void *arg) {
+    range_job *j = (range_job *)arg;
+    j->fn(j->ctx, j->begin, j->end);
+    return NULL;
+}
+
+static void parallel_rows(int nthreads, int64_t n, range_fn fn, void *ctx) {
+    if (nthreads <= 1 || n < 2) { fn(ctx, 0, n); return; }
+    if (nthreads > n) nthreads = (int)n;
+    if (nthreads > 256) nthreads = 256;
+    pthread_t th[256];
+    range_job jobs[256];
+    int64_t per = n / nthreads, extra = n % nthreads, at = 0;
+    for (int t = 0; t < nthreads; t++) {
+        int64_t len = per + (t < extra ? 1 : 0);
+        jobs[t] = (range_job){fn, ctx, at, at + len};
+        at += len;
+    }
+    int started = 0;
+    for (int t = 1; t < nthreads; t++) {
+        if (pthread_create(&th[t], NULL, range_thread, &jobs[t]) != 0) break;
+        started = t;
+    }
+    /* run job 0 here, and any job a thread could not be started for */
+    range_thread(&jobs[0]);
+    for (int t = started + 1; t < nthreads; t++) range_thread(&jobs[t]);
+    for (int t = 1; t <= started; t++) pthread_join(th[t], NULL);
+}
+
+/* ------------------------------------------------------------------ */
+/* a1-a3: Q4_0 / Q8_0 dequant and the embedding gather                 */
+/* ------------------------------------------------------------------ */
+
+int64_t oracle_row_bytes(uint32_t ggml_type, int64_t hidden) {
+    /* gguf/dtype.rs:195-250: Q4_0 = 18 B, Q8_0 = 34 B per 32 values */
+    int64_t bs = ggml_type == OR_Q4_0 ? 18 : ggml_type == OR_Q8_0 ? 34 : -1;
+    if (bs < 0 || hidden <= 0 || hidden % 32 != 0) return -1;
+    return hidden / 32 * bs;
+}
+
+/* quant.rs:107-198, the Q4_0 and Q8_0 arms of dequant_ggml_row.  The scale
+ * is folded into the block's f16 `d` first (quant.rs:121-123), then each
+ * quant is multiplied by it: two f32 roundings, in that order. */
+int oracle_dequant_row(uint32_t ggml_type, const uint8_t *bytes, int64_t nbytes,
+                       float scale, float *out, int64_t n) {
+    int64_t rb = oracle_row_bytes(ggml_type, n);
+    if (rb < 0 || rb != nbytes) return -1;
+    int64_t bs = ggml_type == OR_Q4_0 ? 18 : 34;
+    for (int64_t b = 0; b < n / 32; b++) {
+        const uint8_t *blk = bytes + b * bs;
+        float *o = out + b * 32;
+        uint16_t dbits = (uint16_t)(blk[0] | (blk[1] << 8));
+        float d = oracle_f16_to_f32(dbits) * scale;
+        if (ggml_type == OR_Q4_0) {
+            /* low nibbles are elements 0..16, high nibbles 16..32, minus 8 */
+            for (int j = 0; j < 16; j++) {
+                uint8_t q = blk[2 + j];
+                o[j] = (float)((int16_t)(q & 0x0f) - 8) * d;
+                o[j + 16] = (float)((int16_t)(q >> 4) - 8) * d;
+            }
+        } else {
+            for (int j = 0; j < 32; j++) o[j] = (float)(int8_t)blk[2 + j] * d;
+        }
+    }
+    return 0;
+}
+
+typedef struct {
+    const uint8_t *table;
+    uint32_t type;
+    int64_t hidden, row_bytes;
+    const uint32_t *ids;
+    float scale;
+    void *out;
+    int dtype;
+} embed_ctx;
+
+static void embed_range(void *c, int64_t begin, int64_t end) {
+    embed_ctx *e = (embed_ctx *)c;
+    float *row = (float *)malloc(sizeof(float) * (size_t)e->hidden);
+    for (int64_t t = begin; t < end; t++) {
+        const uint8_t *src = e->table + (int64_t)e->ids[t] * e->row_bytes;
+        oracle_dequant_row(e->type, src, e->row_bytes, e->scale, row, e->hidden);
+        if (e->dtype == OR_F16) {
+            oracle_f32_to_f16_n(row, (uint16_t *)e->out + t * e->hidden, e->hidden);
+        } else {
+            memcpy((float *)e->out + t * e->hidden, row, sizeof(float) * (size_t)e->hidden);
+        }
+    }
+    free(row);
+}
+
+/* TokenEmbedding::rows (quant.rs:391-411): bounds-check every id first
+ * (the reference returns before writing anything useful), then dequantize
+ * each row times `scale`. */
+int oracle_embed(const uint8_t *table, uint32_t ggml_type, int64_t vocab,
+                 int64_t hidden, const uint32_t *ids, int64_t n_tok, float scale,
+                 void *out, int out_dtype, int nthreads, int64_t *bad_index) {
+    int64_t rb = oracle_row_bytes(ggml_type, hidden);
+    if (rb < 0) return -1;
+    for (int64_t t = 0; t < n_tok; t++) {
+        if ((int64_t)ids[t] >= vocab) {
+            if (bad_index) *bad_index = t;
+            return -2;
+        }
+    }
+    embed_ctx c = {table, ggml_type, hidden, rb, ids, scale, out, out_dtype};
+    parallel_rows(nthreads, n_tok, embed_range, &c);
+    return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* a5-a6: residual add + RMSNorm                                        */
+/* ------------------------------------------------------------------ */
+
+/* candle_nn::ops::rms_norm on one f32 row (cpu.rs:3652 -> candle-nn 0.11.1):
+ * sum of squares in f32, index order; m = sqrt(sum/H + eps); y = v / m * w.
+ * The GPU mirror of the same formula is gpu.rs:5883-5896. */
+static void rms_row(const float *v, const float *w, float eps, int64_t H, float *y) {
+    float sum2 = 0.0f;
+    for (int64_t i = 0; i < H; i++) sum2 += v[i] * v[i];
+    float m = sqrtf(sum2 / (float)H + eps);
+    for (int64_t i = 0; i < H; i++) y[i] = w ? v[i] / m * w[i] : v[i] / m;
+}
+
+typedef struct {
+    const void *x, *branch;
+    const float *w, *w_post;
+    float eps, post_eps, rs;
+    int64_t H;
+    void *x_out, *h_out;
+    int dtype;
+} norm_ctx;
+
+static void norm_range(void *c, int64_t begin, int64_t end) {
+    norm_ctx *n = (norm_ctx *)c;
+    int64_t H = n->H;
+    float *xv = (float *)malloc(sizeof(float) * (size_t)H * 3);
+    float *bv = xv + H, *hv = bv + H;
+    for (int64_t r = begin; r < end; r++) {
+        for (int64_t i = 0; i < H; i++) xv[i] = load_el(n->x, r * H + i, n->dtype);
+        if (n->branch) {
+            for (int64_t i = 0; i < H; i++) bv[i] = load_el(n->branch, r * H + i, n->dtype);
+            /* Gemma sandwich: post_attn_norm / post_ffw_norm on the branch
+             * (cpu.rs:2675-2677, 2690-2692) */
+            if (n->w_post) rms_row(bv, n->w_post, n->post_eps, H, bv);
+            /* `scaled`: branch.affine(rs, 0) unless rs == 1 (cpu.rs:2661-2667) */
+            if (n->rs != 1.0f)
+                for (int64_t i = 0; i < H; i++) bv[i] = bv[i] * n->rs + 0.0f;
+            for (int64_t i = 0; i < H; i++) xv[i] = xv[i] + bv[i];
+        }
+        /* the residual stream is held in the activation type: the norm reads
+         * x' as stored */
+        for (int64_t i = 0; i < H; i++) {
+            if (n->dtype == OR_F16) xv[i] = oracle_f16_to_f32(oracle_f32_to_f16(xv[i]));
+            if (n->x_out) store_el(n->x_out, r * H + i, xv[i], n->dtype);
+        }
+        rms_row(xv, n->w, n->eps, H, hv);
+        for (int64_t i = 0; i < H; i++) store_el(n->h_out, r * H + i, hv[i], n->dtype);
+    }
+    free(xv);
+}
+
+void oracle_add_rmsnorm(const void *x, const void *branch, const float *w,
+                        const float *w_post, float eps, float post_eps,
+                        float residual_scale, int64_t rows, int64_t hidden,
+                        void *x_out, void *h_out, int dtype, int nthreads) {
+    norm_ctx c = {x, branch, w, w_post, eps, post_eps, residual_scale, hidden,
+                  x_out, h_out, dtype};
+    parallel_rows(nthreads, rows, norm_range, &c);
+}
+
+/* ------------------------------------------------------------------ */
+/* a7: gated activation                                                 */
+/* ------------------------------------------------------------------ */
+
+/* candle's Tensor::silu / Tensor::gelu (tanh) scalar f32 forms, as the
+ * reference restates them (gpu.rs:5899-5913, moe_kernel.rs:2340-2352). */
+static inline float act_f32(float v, int act) {
+    if (act == OR_SILU) return v / (1.0f + expf(-v));
+    const float k = sqrtf(2.0f / 3.14159265358979323846f);
+    return 0.5f * v * (1.0f + tanhf(k * v * (1.0f + 0.044715f * v * v)));
+}
+
+typedef struct {
+    const void *gate, *up;
+    int64_t gate_ld, up_ld, out_ld, ff;
+    int act;
+    float clamp;
+    void *out;
+    int dtype;
+} glu_ctx;
+
+static void glu_range(void *c, int64_t begin, int64_t end) {
+    glu_ctx *g = (glu_ctx *)c;
+    for (int64_t r = begin; r < end; r++) {
+        for (int64_t j = 0; j < g->ff; j++) {
+            float gv = load_el(g->gate, r * g->gate_ld + j, g->dtype);
+            float uv = load_el(g->up, r * g->up_ld + j, g->dtype);
+            if (g->clamp > 0.0f) { /* Glu::apply clamp (cpu.rs:364-368) */
+                gv = gv < g->clamp ? gv : g->clamp;
+                uv = uv > -g->clamp ? uv : -g->clamp;
+                uv = uv < g->clamp ? uv : g->clamp;
+            }
+            store_el(g->out, r * g->out_ld + j, act_f32(gv, g->act) * uv, g->dtype);
+        }
+    }
+}
+
+void oracle_glu(const void *gate, int64_t gate_ld, const void *up, int64_t up_ld,
+                int64_t rows, int64_t ff, int act, float clamp, void *out,
+                int64_t out_ld, int dtype, int nthreads) {
+    glu_ctx c = {gate, up, gate_ld, up_ld, out_ld, ff, act, clamp, out, dtype};
+    parallel_rows(nthreads, rows, glu_range, &c);
+}
+
+/* ------------------------------------------------------------------ */
+/* a8-a9: RoPE tables and rotation                                      */
+/* ------------------------------------------------------------------ */
+
+/* ggml rope_yarn_corr_dim (rope.rs:86-90) */
+static double corr_dim(int n_dims, int64_t n_ctx_orig, double n_rot, double base) {
+    return (double)n_dims * log((double)n_ctx_orig / (n_rot * 2.0 * M_PI)) / (2.0 * log(base));
+}
+
+void oracle_rope_tables(int n_dims, double base, double freq_scale,
+                        double yarn_ext_factor, double yarn_beta_fast,
+                        double yarn_beta_slow, int64_t yarn_n_ctx_orig,
+                        double attn_factor, const float *factors,
+                        int64_t positions, float *cos_out, float *sin_out) {
+    int half = n_dims / 2;
+    double c0 = 0.0, c1 = 0.0;
+    int yarn = yarn_ext_factor != 0.0;
+    if (yarn) { /* Yarn::corr_dims (rope.rs:93-99) */
+        double start = floor(corr_dim(n_dims, yarn_n_ctx_orig, yarn_beta_fast, base));
+        double end = ceil(corr_dim(n_dims, yarn_n_ctx_orig, yarn_beta_slow, base));
+        c0 = start > 0.0 ? start : 0.0;
+        c1 = end < (double)(n_dims - 1) ? end : (double)(n_dims - 1);
+    }
+    for (int64_t pos = 0; pos < positions; pos++) {
+        for (int i = 0; i < half; i++) {
+            /* RopeSpec::angle (rope.rs:117-132) */
+            double factor = factors ? (double)factors[i] : 1.0;
+            int i0 = 2 * i;
+            double extrap = (double)pos * pow(base, -(double)i0 / (double)n_dims) / factor;
+            double interp = freq_scale * extrap;
+            double theta, mscale;
+            if (yarn) {
+                double span = c1 - c0 > 0.001 ? c1 - c0 : 0.001;
+                double t = ((double)(i0 / 2) - c0) / span;
+                t = t < 0.0 ? 0.0 : (t > 1.0 ? 1.0 : t);
+                double mix = (1.0 - t) * yarn_ext_factor;
+                mscale = attn_factor * (1.0 + 0.1 * log(1.0 / freq_scale));
+                theta = interp * (1.0 - mix) + extrap * mix;
+            } else {
+                theta = interp;
+                mscale = attn_factor;
+            }
+            /* RopeSpec::tables (rope.rs:136-151): f64, then `as f32` */
+            cos_out[pos * half + i] = (float)(cos(theta) * mscale);
+            sin_out[pos * half + i] = (float)(sin(theta) * mscale);
+        }
+    }
+}
+
+typedef struct {
+    void *x;
+    int64_t ld;
+    int heads, d, n_dims, kind;
+    const float *cos_t, *sin_t;
+    const int32_t *pos;
+    const float *norm_w;
+    float eps;
+    int dtype;
+} rope_ctx;
+
+static void rope_range(void *c, int64_t begin, int64_t end) {
+    rope_ctx *p = (rope_ctx *)c;
+    int half = p->n_dims / 2;
+    float *v = (float *)malloc(sizeof(float) * (size_t)p->d * 2);
+    float *o = v + p->d;
+    for (int64_t r = begin; r < end; r++) {
+        const float *cs = p->cos_t + (int64_t)p->pos[r] * half;
+        const float *sn = p->sin_t + (int64_t)p->pos[r] * half;
+        for (int h = 0; h < p->heads; h++) {
+            int64_t at = r * p->ld + (int64_t)h * p->d;
+            for (int i = 0; i < p->d; i++) v[i] = load_el(p->x, at + i, p->dtype);
+            /* QK-norm per head: rms(q.reshape(1,t,nh,d), w[d]) (cpu.rs:2864) */
+            if (p->norm_w) rms_row(v, p->norm_w, p->eps, p->d, v);
+            memcpy(o, v, sizeof(float) * (size_t)p->d);
+            /* candle rope / rope_i = rotate_reference (rope.rs:158-171) */
+            for (int i = 0; i < half; i++) {
+                int a = p->kind == OR_ROPE_NEOX ? i : 2 * i;
+                int b = p->kind == OR_ROPE_NEOX ? i + half : 2 * i + 1;
+                o[a] = v[a] * cs[i] - v[b] * sn[i];
+                o[b] = v[a] * sn[i] + v[b] * cs[i];
+            }
+            for (int i = 0; i < p->d; i++) store_el(p->x, at + i, o[i], p->dtype);
+        }
+    }
+    free(v);
+}
+
+void oracle_rope(void *x, int64_t ld, int64_t rows, int heads, int head_dim,
+                 int n_dims, int kind, const float *cos_t, const float *sin_t,
+                 const int32_t *positions, const float *norm_w, float eps,
+                 int dtype, int nthreads) {
+    rope_ctx c = {x, ld, heads, head_dim, n_dims, kind, cos_t, sin_t,
+                  positions, norm_w, eps, dtype};
+    parallel_rows(nthreads, rows, rope_range, &c);
+}

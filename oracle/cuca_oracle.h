@@ -1,0 +1,104 @@
+/*
+ * cuca_oracle.h -- CPU restatement of the reference engine's per-layer
+ * non-matmul ops (nassor/cuca 0.10.0, provider-local).
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity checker and the
+ * CPU-baseline timer.  Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load it.  The product path (cuca_amd/, libcuca_hip.so)
+ * never links, loads or falls back to it.
+ *
+ * Every function cites the reference file:line it restates.  Paths are
+ * relative to the reference crate root (src/provider/local/model/...).
+ *
+ * Arithmetic contract: compiled with -ffp-contract=off so that every f32
+ * product and sum is rounded on its own, as Rust (which never contracts)
+ * and candle's scalar CPU kernels do.  f16 values are widened exactly and
+ * results are rounded once, to nearest-even, on output.
+ */
+#ifndef CUCA_ORACLE_H
+#define CUCA_ORACLE_H
+
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { OR_F32 = 0, OR_F16 = 1 };          /* element type of activations   */
+enum { OR_Q4_0 = 2, OR_Q8_0 = 8 };        /* ggml type ids (gguf/dtype.rs) */
+enum { OR_SILU = 0, OR_GELU_TANH = 1 };   /* arch.rs:101-106 Act          */
+enum { OR_ROPE_NORM = 0, OR_ROPE_NEOX = 2 }; /* rope.rs:28-36 RopeKind    */
+
+/* IEEE binary16 <-> binary32 (the `half` crate's to_f32 is exact;
+ * the f32 -> f16 direction rounds to nearest, ties to even). */
+float oracle_f16_to_f32(uint16_t h);
+uint16_t oracle_f32_to_f16(float f);
+void oracle_f16_to_f32_n(const uint16_t *h, float *f, int64_t n);
+void oracle_f32_to_f16_n(const float *f, uint16_t *h, int64_t n);
+
+/* Bytes per row of `hidden` values of a Q4_0 / Q8_0 tensor, or -1 when the
+ * row is not a whole number of 32-value blocks (quant.rs:110-118). */
+int64_t oracle_row_bytes(uint32_t ggml_type, int64_t hidden);
+
+/* dequant_row for Q4_0 / Q8_0 (quant.rs:107-198).  Returns 0, or -1 when
+ * `nbytes` is not exactly n/32 blocks. */
+int oracle_dequant_row(uint32_t ggml_type, const uint8_t *bytes, int64_t nbytes,
+                       float scale, float *out, int64_t n);
+
+/* TokenEmbedding::rows (quant.rs:391-411): out[n_tok, hidden] in `out_dtype`.
+ * Returns 0; -1 for a bad row geometry; -2 for an id >= vocab, whose index
+ * is stored in *bad_index (the reference's "token id {id} outside the
+ * embedding table" error, quant.rs:395-400).  Rows are split over
+ * `nthreads` threads (1 = the reference's scalar loop). */
+int oracle_embed(const uint8_t *table, uint32_t ggml_type, int64_t vocab,
+                 int64_t hidden, const uint32_t *ids, int64_t n_tok, float scale,
+                 void *out, int out_dtype, int nthreads, int64_t *bad_index);
+
+/* Fused residual add + RMSNorm, restating Transformer::block
+ * (cpu.rs:2650-2711) with candle's rms_norm (cpu.rs:3652):
+ *   b'  = w_post ? rms(branch, w_post, post_eps) : branch
+ *   b'' = residual_scale == 1 ? b' : b' * residual_scale + 0   (affine)
+ *   x'  = branch ? x + b'' : x           (stored in dtype -> x_out)
+ *   h   = rms(x' as stored, w, eps)      (w == NULL: weightless norm)
+ * rms(v, w, eps) = v / sqrt(sum(v*v)/H + eps) * w, sum in f32 in index
+ * order.  x_out may be NULL (then x' is not written) or alias x. */
+void oracle_add_rmsnorm(const void *x, const void *branch, const float *w,
+                        const float *w_post, float eps, float post_eps,
+                        float residual_scale, int64_t rows, int64_t hidden,
+                        void *x_out, void *h_out, int dtype, int nthreads);
+
+/* Glu::apply (cpu.rs:342-371) with activate (cpu.rs:3644-3649):
+ *   g = clamp > 0 ? min(g, clamp) : g;  u = clamp > 0 ? clamp(u, -c, c) : u
+ *   out = act(g) * u
+ * SiLU v/(1+exp(-v)); GELU-tanh 0.5*v*(1+tanh(sqrt(2/pi)*v*(1+0.044715*v*v))).
+ * Row r of gate/up/out starts at r*gate_ld / r*up_ld / r*out_ld elements. */
+void oracle_glu(const void *gate, int64_t gate_ld, const void *up, int64_t up_ld,
+                int64_t rows, int64_t ff, int act, float clamp, void *out,
+                int64_t out_ld, int dtype, int nthreads);
+
+/* RopeSpec::tables (rope.rs:118-151) in f64 with the platform libm, rounded
+ * to f32.  yarn_ext_factor == 0 disables YaRN.  factors: NULL or n_dims/2
+ * per-pair divisors.  cos/sin: [positions, n_dims/2]. */
+void oracle_rope_tables(int n_dims, double base, double freq_scale,
+                        double yarn_ext_factor, double yarn_beta_fast,
+                        double yarn_beta_slow, int64_t yarn_n_ctx_orig,
+                        double attn_factor, const float *factors,
+                        int64_t positions, float *cos_out, float *sin_out);
+
+/* apply_rope (cpu.rs:3672-3688, candle rope/rope_i) on x[rows, heads, d]
+ * in place, with an optional per-head RMSNorm first (QK-norm,
+ * cpu.rs:2840-2864, 3040-3055):
+ *   norm_w != NULL: v = rms(head, norm_w[head_dim], eps)
+ *   pair (a, b) of the first n_dims values (NORM: 2i,2i+1; NEOX: i,i+n/2):
+ *     a' = a*c - b*s;  b' = a*s + b*c     (rope.rs:158-171)
+ * c, s = cos/sin[positions[row], i].  Row r starts at r*ld elements. */
+void oracle_rope(void *x, int64_t ld, int64_t rows, int heads, int head_dim,
+                 int n_dims, int kind, const float *cos_t, const float *sin_t,
+                 const int32_t *positions, const float *norm_w, float eps,
+                 int dtype, int nthreads);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

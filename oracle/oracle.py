@@ -1,0 +1,177 @@
+"""numpy front end of the CPU oracle (liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, as the checker.  The product (cuca_amd) never
+imports it.
+
+Arrays are numpy: float32 for f32 activations, float16 for f16 ones (their
+bits are passed through unchanged), uint8 for quantized tables.
+"""
+
+import ctypes
+import os
+
+import numpy as np
+
+from . import build as _build
+
+_LIB = None
+
+F32, F16 = 0, 1
+Q4_0, Q8_0 = 2, 8
+SILU, GELU_TANH = 0, 1
+ROPE_NORM, ROPE_NEOX = 0, 2
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+_f64 = ctypes.c_double
+_int = ctypes.c_int
+
+
+def lib():
+    """Load liboracle.so, building it first when it is missing."""
+    global _LIB
+    if _LIB is None:
+        path = _build.LIB
+        if not os.path.exists(path):
+            _build.build()
+        L = ctypes.CDLL(path)
+        L.oracle_f16_to_f32.restype = _f32
+        L.oracle_f16_to_f32.argtypes = [ctypes.c_uint16]
+        L.oracle_f32_to_f16.restype = ctypes.c_uint16
+        L.oracle_f32_to_f16.argtypes = [_f32]
+        L.oracle_f16_to_f32_n.argtypes = [_p, _p, _i64]
+        L.oracle_f32_to_f16_n.argtypes = [_p, _p, _i64]
+        L.oracle_row_bytes.restype = _i64
+        L.oracle_row_bytes.argtypes = [ctypes.c_uint32, _i64]
+        L.oracle_dequant_row.restype = _int
+        L.oracle_dequant_row.argtypes = [ctypes.c_uint32, _p, _i64, _f32, _p, _i64]
+        L.oracle_embed.restype = _int
+        L.oracle_embed.argtypes = [_p, ctypes.c_uint32, _i64, _i64, _p, _i64, _f32,
+                                   _p, _int, _int, ctypes.POINTER(_i64)]
+        L.oracle_add_rmsnorm.argtypes = [_p, _p, _p, _p, _f32, _f32, _f32, _i64, _i64,
+                                         _p, _p, _int, _int]
+        L.oracle_glu.argtypes = [_p, _i64, _p, _i64, _i64, _i64, _int, _f32, _p, _i64,
+                                 _int, _int]
+        L.oracle_rope_tables.argtypes = [_int, _f64, _f64, _f64, _f64, _f64, _i64, _f64,
+                                         _p, _i64, _p, _p]
+        L.oracle_rope.argtypes = [_p, _i64, _i64, _int, _int, _int, _int, _p, _p, _p, _p,
+                                  _f32, _int, _int]
+        _LIB = L
+    return _LIB
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+def _dtype_code(a):
+    if a.dtype == np.float32:
+        return F32
+    if a.dtype == np.float16:
+        return F16
+    raise TypeError(f"activations must be float32 or float16, not {a.dtype}")
+
+
+def f16_to_f32(h):
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, np.float32)
+    lib().oracle_f16_to_f32_n(_ptr(h), _ptr(out), h.size)
+    return out
+
+
+def f32_to_f16(f):
+    f = np.ascontiguousarray(f, dtype=np.float32)
+    out = np.empty(f.shape, np.uint16)
+    lib().oracle_f32_to_f16_n(_ptr(f), _ptr(out), f.size)
+    return out
+
+
+def row_bytes(ggml_type, hidden):
+    return int(lib().oracle_row_bytes(ggml_type, hidden))
+
+
+def dequant_row(ggml_type, data, scale, n):
+    data = np.ascontiguousarray(data, dtype=np.uint8)
+    out = np.empty(n, np.float32)
+    rc = lib().oracle_dequant_row(ggml_type, _ptr(data), data.size, scale, _ptr(out), n)
+    if rc != 0:
+        raise ValueError(f"row of {data.size} bytes does not hold {n} elements")
+    return out
+
+
+class OracleError(ValueError):
+    pass
+
+
+def embed(table, ggml_type, vocab, hidden, ids, scale, out_dtype=np.float32, threads=1):
+    table = np.ascontiguousarray(table, dtype=np.uint8)
+    ids = np.ascontiguousarray(ids, dtype=np.uint32)
+    out = np.empty((ids.size, hidden), out_dtype)
+    bad = _i64(-1)
+    rc = lib().oracle_embed(_ptr(table), ggml_type, vocab, hidden, _ptr(ids), ids.size,
+                            scale, _ptr(out), _dtype_code(out), threads, ctypes.byref(bad))
+    if rc == -1:
+        raise OracleError(f"row length {hidden} is not a whole number of blocks")
+    if rc == -2:
+        raise OracleError(f"token id {int(ids[bad.value])} outside the embedding table "
+                          f"of {vocab} rows")
+    return out
+
+
+def add_rmsnorm(x, branch, w, eps, w_post=None, post_eps=None, residual_scale=1.0,
+                threads=1, write_x=True):
+    """Returns (x_out or None, h)."""
+    x = np.ascontiguousarray(x)
+    rows, hidden = x.shape
+    if branch is not None:
+        branch = np.ascontiguousarray(branch, dtype=x.dtype)
+    w = None if w is None else np.ascontiguousarray(w, dtype=np.float32)
+    w_post = None if w_post is None else np.ascontiguousarray(w_post, dtype=np.float32)
+    x_out = np.empty_like(x) if write_x else None
+    h = np.empty_like(x)
+    lib().oracle_add_rmsnorm(_ptr(x), _ptr(branch), _ptr(w), _ptr(w_post), eps,
+                             eps if post_eps is None else post_eps, residual_scale,
+                             rows, hidden, _ptr(x_out), _ptr(h), _dtype_code(x), threads)
+    return x_out, h
+
+
+def glu(gate, up, act, clamp=0.0, threads=1):
+    """act(gate) * up over [rows, ff] views (row strides taken from the arrays)."""
+    assert gate.shape == up.shape and gate.dtype == up.dtype
+    rows, ff = gate.shape
+    for a in (gate, up):
+        assert a.strides[1] == a.itemsize, "rows must be contiguous"
+    out = np.empty((rows, ff), gate.dtype)
+    lib().oracle_glu(_ptr(gate), gate.strides[0] // gate.itemsize, _ptr(up),
+                     up.strides[0] // up.itemsize, rows, ff, act, clamp, _ptr(out), ff,
+                     _dtype_code(gate), threads)
+    return out
+
+
+def rope_tables(n_dims, base, positions, freq_scale=1.0, yarn=None, attn_factor=1.0,
+                factors=None):
+    """yarn: None or (ext_factor, beta_fast, beta_slow, n_ctx_orig)."""
+    half = n_dims // 2
+    cos = np.empty((positions, half), np.float32)
+    sin = np.empty((positions, half), np.float32)
+    ext, bf, bs, nco = yarn if yarn is not None else (0.0, 32.0, 1.0, 0)
+    f = None if factors is None else np.ascontiguousarray(factors, dtype=np.float32)
+    lib().oracle_rope_tables(n_dims, base, freq_scale, ext, bf, bs, nco, attn_factor,
+                             _ptr(f), positions, _ptr(cos), _ptr(sin))
+    return cos, sin
+
+
+def rope(x, cos, sin, positions, kind, n_dims=None, norm_w=None, eps=1e-6, threads=1):
+    """Rotate a copy of x [rows, heads, d] (returned); optional fused QK-norm."""
+    x = np.array(x, copy=True, order="C")
+    rows, heads, d = x.shape
+    n_dims = d if n_dims is None else n_dims
+    cos = np.ascontiguousarray(cos, dtype=np.float32)
+    sin = np.ascontiguousarray(sin, dtype=np.float32)
+    pos = np.ascontiguousarray(positions, dtype=np.int32)
+    nw = None if norm_w is None else np.ascontiguousarray(norm_w, dtype=np.float32)
+    lib().oracle_rope(_ptr(x), heads * d, rows, heads, d, n_dims, kind, _ptr(cos),
+                      _ptr(sin), _ptr(pos), _ptr(nw), eps, _dtype_code(x), threads)
+    return x

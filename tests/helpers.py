@@ -1,0 +1,59 @@
+"""Tolerances and comparisons shared by the GPU parity tests.
+
+The bars: the embedding gather and RoPE without a norm
+are bit-exact; norm, activation and normed RoPE are within a maximum
+relative error of 1e-5 in f32 and 2 ulp in f16 (against the f16 rounding of
+the oracle), with these stated floors where the quantity is ill-conditioned:
+- GELU-tanh: + 2^-22 * |0.5 g u|, the rounding of candle's 1 + tanh(z) term,
+  which cancels for z << 0 (the GPU evaluates 2 sigma(2z), which does not);
+- QK-normed RoPE: relative to the magnitude of the rotated pair
+  sqrt(a'^2 + b'^2), the rotation's conditioning (a*c - b*s cancels);
+- everything: + 1e-37 absolute, below the f32 normal range.
+"""
+import numpy as np
+
+
+def _f64(a):
+    return np.asarray(a).astype(np.float64)
+
+
+def ulp16(v):
+    return np.spacing(np.abs(_f64(v)).astype(np.float16)).astype(np.float64)
+
+
+def assert_bits_equal(got, want, what=""):
+    got, want = np.asarray(got), np.asarray(want)
+    assert got.shape == want.shape, (got.shape, want.shape)
+    ib = np.uint16 if got.dtype == np.float16 else np.uint32
+    g, w = got.view(ib), want.view(ib)
+    bad = g != w
+    if bad.any():
+        idx = np.argwhere(bad)[:5]
+        raise AssertionError(f"{what}: {bad.sum()} of {bad.size} differ; first at {idx.tolist()}: "
+                             f"got {got[tuple(idx[0])]!r} want {want[tuple(idx[0])]!r}")
+
+
+def assert_close(got, want, floor=None, rel=1e-5, ulps=2, what=""):
+    """f32: |got - want| <= rel |want| + floor; f16: <= ulps * ulp16(want) +
+    floor.  `want` is the oracle's output in the same dtype."""
+    g, w = _f64(got), _f64(want)
+    assert g.shape == w.shape, (g.shape, w.shape)
+    if np.asarray(got).dtype == np.float16:
+        tol = ulps * ulp16(want)
+    else:
+        tol = rel * np.abs(w)
+    tol = tol + 1e-37
+    if floor is not None:
+        tol = tol + floor
+    same_nan = np.isnan(g) & np.isnan(w)
+    bad = (np.abs(g - w) > tol) & ~same_nan
+    if bad.any():
+        i = tuple(np.argwhere(bad)[0])
+        worst = np.max(np.abs(g - w)[bad] / np.maximum(tol[bad], 1e-300))
+        raise AssertionError(f"{what}: {bad.sum()} of {bad.size} outside tolerance "
+                             f"(worst {worst:.2f}x); first at {list(i)}: got {g[i]!r} want {w[i]!r}")
+
+
+def max_rel(got, want):
+    g, w = _f64(got), _f64(want)
+    return float(np.max(np.abs(g - w) / np.maximum(np.abs(w), 1e-30)))

@@ -1,0 +1,120 @@
+"""Embedding dequant-gather on the GPU against the oracle: bit-exact.
+
+Covers the reference's golden blocks, the table shapes of configs A/B/D/E
+(at a reduced vocab so the oracle runs in seconds), f32 and f16 output, the
+2-byte-aligned staging path, the scale fold, the host-side errors of
+TokenEmbedding::rows and the device-side guard for ids the host never saw.
+The full-size table (config C, 532 MiB Q8_0, 16384 ids) is checked on
+sampled rows.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from cuca_amd import hip, ops
+from cuca_amd import workloads as W
+from helpers import assert_bits_equal
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "quants_legacy.npz")
+
+
+@pytest.mark.parametrize("name,ty", [("q4_0", hip.GGML_Q4_0), ("q8_0", hip.GGML_Q8_0)])
+@pytest.mark.parametrize("hidden", [1024, 32])
+def test_golden_blocks(ctx, name, ty, hidden):
+    g = np.load(GOLDEN)
+    blocks, expected = g[name + "_blocks"], g[name + "_expected"]
+    rows = 1024 // hidden   # one row of 32 blocks, or 32 rows of one block (2-byte aligned rows)
+    emb = ops.TokenEmbedding(ctx, ty, blocks, rows, hidden)
+    ids = np.arange(rows)[::-1].copy()
+    got = emb.rows(ids, 1.0).numpy()
+    assert_bits_equal(got, expected.reshape(rows, hidden)[ids], f"{name} golden")
+    got16 = emb.rows(ids, 1.0, out_dtype=np.float16).numpy()
+    assert_bits_equal(got16, expected.reshape(rows, hidden)[ids].astype(np.float16))
+
+
+@pytest.mark.parametrize("cfg_name", ["A", "B", "D", "E"])
+@pytest.mark.parametrize("out", [np.float32, np.float16])
+def test_config_tables_bit_exact(ctx, cfg_name, out):
+    cfg = W.CONFIGS[cfg_name]
+    rng = np.random.default_rng(cfg["seed"])
+    vocab, hidden = 2048, cfg["hidden"]
+    table = W.quant_table(rng, vocab, hidden, cfg["qtype"], cfg["d_range"])
+    ty = W.GGML_ID[cfg["qtype"]]
+    ids = rng.integers(0, vocab, 96).astype(np.uint32)
+    ids[:3] = [0, vocab - 1, 0]
+    emb = ops.TokenEmbedding(ctx, ty, table, vocab, hidden)
+    got = emb.rows(ids, cfg["embd_scale"], out_dtype=out).numpy()
+    want = O.embed(table, ty, vocab, hidden, ids, cfg["embd_scale"], out_dtype=out, threads=8)
+    assert_bits_equal(got, want, f"config {cfg_name}")
+
+
+@pytest.mark.parametrize("hidden", [96, 160, 3584 + 32])
+def test_unaligned_rows_take_the_2_byte_path(ctx, hidden):
+    rng = np.random.default_rng(hidden)
+    for qtype in ("q4_0", "q8_0"):
+        table = W.quant_table(rng, 64, hidden, qtype, (0.001, 0.05))
+        ty = W.GGML_ID[qtype]
+        ids = rng.integers(0, 64, 40).astype(np.uint32)
+        emb = ops.TokenEmbedding(ctx, ty, table, 64, hidden)
+        got = emb.rows(ids, 1.37).numpy()
+        assert_bits_equal(got, O.embed(table, ty, 64, hidden, ids, 1.37), qtype)
+
+
+def test_empty_and_single_token(ctx):
+    rng = np.random.default_rng(1)
+    table = W.quant_table(rng, 8, 64, "q4_0", (0.001, 0.05))
+    emb = ops.TokenEmbedding(ctx, hip.GGML_Q4_0, table, 8, 64)
+    assert emb.rows([], 1.0).shape == (0, 64)
+    got = emb.rows([7], 2.0).numpy()
+    assert_bits_equal(got, O.embed(table, O.Q4_0, 8, 64, np.array([7], np.uint32), 2.0))
+
+
+def test_host_rejects_bad_ids_like_the_reference(ctx):
+    table = np.zeros(4 * 18, np.uint8)
+    emb = ops.TokenEmbedding(ctx, hip.GGML_Q4_0, table, 4, 32)
+    with pytest.raises(hip.CucaError, match="token id 4 outside the embedding table of 4 rows"):
+        emb.rows([1, 4], 1.0)
+
+
+def test_device_guard_reports_bad_ids_and_writes_zero_rows(ctx):
+    rng = np.random.default_rng(2)
+    table = W.quant_table(rng, 16, 128, "q8_0", (0.001, 0.02))
+    emb = ops.TokenEmbedding(ctx, hip.GGML_Q8_0, table, 16, 128)
+    ids = ctx.array(np.array([3, 16, 5, 99999], np.uint32))
+    out = ctx.empty((4, 128), np.float32)
+    emb.rows_device(ids, 1.0, out)
+    with pytest.raises(hip.CucaError, match="token id 16 outside the embedding table of 16 rows"):
+        ctx.check_device()
+    got = out.numpy()
+    assert np.all(got[1] == 0) and np.all(got[3] == 0)
+    want = O.embed(table, O.Q8_0, 16, 128, np.array([3, 5], np.uint32), 1.0)
+    assert_bits_equal(got[[0, 2]], want)
+    ctx.check_device()   # the status was cleared
+
+
+def test_full_size_config_c_sampled_rows(ctx):
+    torch = pytest.importorskip("torch")
+    cfg = W.CONFIGS["C"]
+    gen = torch.Generator(device="cuda").manual_seed(cfg["seed"])
+    vocab, hidden, n = cfg["vocab"], cfg["hidden"], 16384
+    table = W.quant_table_torch(gen, vocab, hidden, cfg["qtype"], cfg["d_range"])
+    ids = torch.randint(0, vocab, (n,), device="cuda", generator=gen, dtype=torch.int32)
+    out = torch.empty((n, hidden), dtype=torch.float16, device="cuda")
+    torch.cuda.synchronize()
+    ctx.embed_gguf(table.data_ptr(), hip.GGML_Q8_0, vocab, hidden, ids.data_ptr(), n, 1.0,
+                   out.data_ptr(), hip.F16)
+    ctx.sync()
+    ctx.check_device()
+    rb = W.row_bytes(cfg["qtype"], hidden)
+    sample = np.unique(np.concatenate([[0, n - 1], np.random.default_rng(0).integers(0, n, 254)]))
+    ids_h = ids.cpu().numpy().astype(np.uint32)
+    got = out[torch.from_numpy(sample).cuda()].cpu().numpy()
+    rows = table.view(vocab, rb)[torch.from_numpy(ids_h[sample].astype(np.int64)).cuda()]
+    sub_table = rows.cpu().numpy().reshape(-1)
+    want = O.embed(sub_table, O.Q8_0, sample.size, hidden, np.arange(sample.size, dtype=np.uint32),
+                   1.0, out_dtype=np.float16)
+    assert_bits_equal(got, want, "config C full-size sample")

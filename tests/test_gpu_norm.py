@@ -1,0 +1,123 @@
+"""Fused residual add + RMSNorm on the GPU against the oracle.
+
+Bars: x' (the residual sum) bit-exact; h within 1e-5 relative (f32) or
+2 f16 ulps of the oracle's f16 output.  Covers the hidden sizes of configs
+A-E (1024, 4096, 3584, 2048), the QK-norm row width 128, short rows
+(several rows per wave), the Gemma sandwich, the residual scale, the
+weightless norm, in-place x' = x, empty and ragged row counts, the generic
+kernel (hidden not a multiple of the chunk, rows wider than the register
+kernel, misaligned buffers) and the full config C size on sampled rows.
+"""
+import numpy as np
+import pytest
+
+from cuca_amd import ops
+from helpers import assert_bits_equal, assert_close
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+NP = {"f32": np.float32, "f16": np.float16}
+
+
+def run(ctx, x, b, w, eps, wp=None, post_eps=None, rs=1.0, in_place=False):
+    dx = ctx.array(x)
+    db = None if b is None else ctx.array(b)
+    xo = dx if in_place else None
+    x_out, h = ops.add_rms(dx, db, w, eps, w_post=wp, post_eps=post_eps, residual_scale=rs,
+                           x_out=xo)
+    return x_out.numpy(), h.numpy()
+
+
+def data(rows, hidden, dtype, seed, std=1.0):
+    rng = np.random.default_rng(seed)
+    x = (std * rng.standard_normal((rows, hidden))).astype(NP[dtype])
+    b = (std * rng.standard_normal((rows, hidden))).astype(NP[dtype])
+    w = (1 + 0.02 * rng.standard_normal(hidden)).astype(np.float32)
+    return x, b, w
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+@pytest.mark.parametrize("hidden,eps,rows", [(1024, 1e-6, 128), (4096, 1e-5, 32), (4096, 1e-5, 1),
+                                             (3584, 1e-6, 9), (2048, 1e-6, 64), (128, 1e-6, 77),
+                                             (64, 1e-5, 5), (8192, 1e-5, 3), (32, 1e-5, 33)])
+def test_add_rmsnorm_matches_oracle(ctx, dtype, hidden, eps, rows):
+    x, b, w = data(rows, hidden, dtype, hidden + rows)
+    xo, h = run(ctx, x, b, w, eps)
+    wx, wh = O.add_rmsnorm(x, b, w, eps)
+    assert_bits_equal(xo, wx, "x'")
+    assert_close(h, wh, what="h")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_gemma_sandwich_residual_scale_and_weightless(ctx, dtype):
+    x, b, w = data(8, 3584, dtype, 3, std=2.0)
+    wp = (1 + 0.02 * np.random.default_rng(4).standard_normal(3584)).astype(np.float32)
+    xo, h = run(ctx, x, b, w, 1e-6, wp=wp, post_eps=1e-5)
+    wx, wh = O.add_rmsnorm(x, b, w, 1e-6, w_post=wp, post_eps=1e-5)
+    # the branch's own norm sums in another order: x' is within tolerance, not exact
+    assert_close(xo, wx, floor=1e-6 * np.abs(b.astype(np.float64)), what="sandwich x'")
+    assert_close(h, wh, what="sandwich h")
+    xo, h = run(ctx, x, b, None, 1e-6, rs=0.22)
+    wx, wh = O.add_rmsnorm(x, b, None, 1e-6, residual_scale=0.22)
+    assert_bits_equal(xo, wx, "scaled x'")
+    assert_close(h, wh, what="weightless h")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_plain_rms_and_in_place(ctx, dtype):
+    x, b, w = data(17, 2048, dtype, 5)
+    got = ops.rms(ctx.array(x), w, 1e-6).numpy()
+    _, want = O.add_rmsnorm(x, None, w, 1e-6, write_x=False)
+    assert_close(got, want, what="rms")
+    xo, h = run(ctx, x, b, w, 1e-6, in_place=True)
+    wx, wh = O.add_rmsnorm(x, b, w, 1e-6)
+    assert_bits_equal(xo, wx, "in-place x'")
+    assert_close(h, wh, what="in-place h")
+
+
+def test_zero_rows_is_a_no_op(ctx):
+    x = ctx.empty((0, 1024), np.float32)
+    ops.add_rms(x, x, None, 1e-6)
+
+
+@pytest.mark.parametrize("dtype,hidden", [("f32", 1001), ("f16", 1004), ("f16", 20000),
+                                          ("f32", 9000), ("f32", 3)])
+def test_generic_kernel(ctx, dtype, hidden):
+    x, b, w = data(6, hidden, dtype, hidden)
+    wp = np.linspace(0.5, 1.5, hidden).astype(np.float32)
+    xo, h = run(ctx, x, b, w, 1e-5, wp=wp, post_eps=1e-6)
+    wx, wh = O.add_rmsnorm(x, b, w, 1e-5, w_post=wp, post_eps=1e-6)
+    assert_close(xo, wx, floor=1e-6 * np.abs(b.astype(np.float64)), what="generic x'")
+    assert_close(h, wh, what="generic h")
+
+
+def test_misaligned_buffers_take_the_generic_kernel(ctx):
+    x, b, w = data(5, 1024, "f32", 11)
+    buf = ctx.array(np.concatenate([np.zeros(1, np.float32), x.reshape(-1)]))
+    dx = buf.view(1, x.shape)   # 4 bytes past a 16-byte boundary
+    xo, h = ops.add_rms(dx, ctx.array(b), w, 1e-6)
+    wx, wh = O.add_rmsnorm(x, b, w, 1e-6)
+    assert_bits_equal(xo.numpy(), wx)
+    assert_close(h.numpy(), wh)
+
+
+def test_full_size_config_c_sampled_rows(ctx):
+    torch = pytest.importorskip("torch")
+    n, hidden = 16384, 4096
+    gen = torch.Generator(device="cuda").manual_seed(2)
+    x = torch.randn((n, hidden), device="cuda", generator=gen).to(torch.float16)
+    b = torch.randn((n, hidden), device="cuda", generator=gen).to(torch.float16)
+    w = (1 + 0.02 * torch.randn(hidden, device="cuda", generator=gen)).float()
+    xo = torch.empty_like(x)
+    h = torch.empty_like(x)
+    torch.cuda.synchronize()
+    ctx.add_rmsnorm(x.data_ptr(), b.data_ptr(), w.data_ptr(), None, 1e-5, 1e-5, 1.0, n, hidden,
+                    xo.data_ptr(), h.data_ptr(), 1)
+    ctx.sync()
+    sample = torch.from_numpy(np.unique(np.concatenate(
+        [[0, n - 1], np.random.default_rng(1).integers(0, n, 126)]))).cuda()
+    xs, bs = x[sample].cpu().numpy(), b[sample].cpu().numpy()
+    wx, wh = O.add_rmsnorm(xs, bs, w.cpu().numpy(), 1e-5)
+    assert_bits_equal(xo[sample].cpu().numpy(), wx)
+    assert_close(h[sample].cpu().numpy(), wh)
