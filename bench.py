@@ -89,6 +89,7 @@ class PrefillStep:
         self.w1 = (1 + 0.02 * torch.randn(H, device=dev, generator=gen)).float()
         self.w2 = (1 + 0.02 * torch.randn(H, device=dev, generator=gen)).float()
         self.q, self.k = act(n, nq, d), act(n, nk, d)
+        self.q0, self.k0 = self.q.clone(), self.k.clone()
         cos, sin = hip.rope_tables(hip.ROPE_NORM, d, cfg["theta"], n)
         self.cos, self.sin = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
         self.pos = torch.arange(n, device=dev, dtype=torch.int32)
@@ -121,6 +122,45 @@ class PrefillStep:
     def step(self):
         for name in STEP_OPS:
             self.launch(name)
+
+    def verify(self, torch, rows=24):
+        """Run the step once from fresh Q/K and compare sampled rows of every
+        output with the oracle (the timed kernels did the work they claim)."""
+        import numpy as np
+        from oracle import oracle as O
+        from cuca_amd import workloads as W
+        cfg, n = self.cfg, self.n
+        H, F, d = cfg["hidden"], cfg["ff"], cfg["head_dim"]
+        self.q.copy_(self.q0)
+        self.k.copy_(self.k0)
+        self.step()
+        torch.cuda.synchronize()
+        self.ctx.check_device()
+        s = np.unique(np.concatenate([[0, n - 1], np.random.default_rng(7).integers(0, n, rows)]))
+        st = torch.from_numpy(s).cuda()
+        host = lambda t: t[st].cpu().numpy()
+        rb = W.row_bytes(cfg["qtype"], H)
+        sub = self.table.view(cfg["vocab"], rb)[self.ids[st].long()].cpu().numpy().reshape(-1)
+        want = O.embed(sub, O.Q8_0, s.size, H, np.arange(s.size, dtype=np.uint32), 1.0,
+                       out_dtype=np.float16)
+        assert np.array_equal(host(self.emb).view(np.uint16), want.view(np.uint16)), "embed"
+        for x, b, w, xo, h in ((self.x1, self.b1, self.w1, self.xo1, self.h1),
+                               (self.x2, self.b2, self.w2, self.xo2, self.h2)):
+            wx, wh = O.add_rmsnorm(host(x), host(b), w.cpu().numpy(), cfg["eps"])
+            assert np.array_equal(host(xo).view(np.uint16), wx.view(np.uint16)), "x'"
+            g = host(h).astype(np.float64)
+            ulp = np.spacing(np.abs(wh).astype(np.float16)).astype(np.float64)
+            assert np.all(np.abs(g - wh.astype(np.float64)) <= 2 * ulp), "add_rmsnorm"
+        cos, sin = self.cos.cpu().numpy(), self.sin.cpu().numpy()
+        for t, t0 in ((self.q, self.q0), (self.k, self.k0)):
+            w = O.rope(host(t0), cos, sin, s.astype(np.int32), O.ROPE_NORM)
+            assert np.array_equal(host(t).view(np.uint16), w.view(np.uint16)), "rope"
+        gu = host(self.gu)
+        wa = O.glu(gu[:, :F], gu[:, F:], O.SILU)
+        g = host(self.out).astype(np.float64)
+        ulp = np.spacing(np.abs(wa).astype(np.float16)).astype(np.float64)
+        assert np.all(np.abs(g - wa.astype(np.float64)) <= 2 * ulp + 1e-37), "swiglu"
+        return int(s.size)
 
 
 def time_steps(torch, fn, steps, warmup):
@@ -281,8 +321,12 @@ def main():
         from cuca_amd import build
         build.build()
     log("context")
+    # one explicit stream (default priority) carries torch's data generation,
+    # the HIP events and every cuca launch
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
     ctx = hip.Context(0)
-    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    ctx.set_stream(stream.cuda_stream)
 
     log(f"prefill step buffers, {args.tokens} tokens")
     st = PrefillStep(ctx, torch, args.tokens)
@@ -299,6 +343,8 @@ def main():
                       frac=round(st.bytes[name] / (t / 1e3) / 1e9 / HBM_PEAK_GBS, 4))
            for name, t in ops_ms.items()}
     glu = ops["swiglu"]
+    log("verify sampled rows against the oracle")
+    checked_rows = st.verify(torch)
     del st
     torch.cuda.empty_cache()
 
@@ -335,6 +381,7 @@ def main():
                    "tokens": args.tokens, "hidden": 4096, "ff": 14336, "heads": "32q/8k x 128",
                    "activations": "f16 (decode: f32)", "bytes_per_step": step_bytes},
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+        "verified_rows": checked_rows,
         "ops": ops,
         "decode_us_per_layer": decode,
         "roofline": {"kernel": "swiglu (cuca_glu_f16_silu)", "bound": "hbm",

@@ -30,7 +30,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950", "--offload-device-only", "--no-gpu-bundle-output",
-    "-O3", "-std=c++17", "-ffp-contract=off",
+    "-O3", "-std=c++17", "-ffp-contract=off", "-mcode-object-version=5",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall", "-Werror=return-type",
 ]
