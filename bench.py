@@ -309,6 +309,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-large", action="store_true", help="skip the 16384-token step")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: these ops run on one GPU's share of the work and "
@@ -328,25 +329,36 @@ def main():
     ctx = hip.Context(0)
     ctx.set_stream(stream.cuda_stream)
 
-    log(f"prefill step buffers, {args.tokens} tokens")
-    st = PrefillStep(ctx, torch, args.tokens)
-    torch.cuda.synchronize()
-    step_bytes = sum(st.bytes.values())
-    log("timed steps")
-    ms = time_steps(torch, st.step, args.steps, args.warmup)
-    ctx.check_device()
-    log(f"{ms * 1000:.1f} us per step; per-op events")
-    ops_ms = per_op_ms(torch, st, args.steps)
+    def run_size(n, steps, warmup):
+        log(f"prefill step buffers, {n} tokens")
+        st = PrefillStep(ctx, torch, n)
+        torch.cuda.synchronize()
+        log("timed steps")
+        ms = time_steps(torch, st.step, steps, warmup)
+        ctx.check_device()
+        log(f"{ms * 1000:.1f} us per step; per-op events")
+        ops_ms = per_op_ms(torch, st, steps)
+        ops = {name: dict(us=round(t * 1000, 2), bytes=st.bytes[name],
+                          gbs=round(st.bytes[name] / (t / 1e3) / 1e9, 1),
+                          frac=round(st.bytes[name] / (t / 1e3) / 1e9 / HBM_PEAK_GBS, 4))
+               for name, t in ops_ms.items()}
+        log("verify sampled rows against the oracle")
+        rows = st.verify(torch)
+        step_bytes = sum(st.bytes.values())
+        del st
+        torch.cuda.empty_cache()
+        return ms, step_bytes, ops, rows
+
+    ms, step_bytes, ops, checked_rows = run_size(args.tokens, args.steps, args.warmup)
     value = step_bytes / (ms / 1e3) / 1e9
-    ops = {name: dict(us=round(t * 1000, 2), bytes=st.bytes[name],
-                      gbs=round(st.bytes[name] / (t / 1e3) / 1e9, 1),
-                      frac=round(st.bytes[name] / (t / 1e3) / 1e9 / HBM_PEAK_GBS, 4))
-           for name, t in ops_ms.items()}
     glu = ops["swiglu"]
-    log("verify sampled rows against the oracle")
-    checked_rows = st.verify(torch)
-    del st
-    torch.cuda.empty_cache()
+    big = None
+    if args.tokens != 16384 and not args.no_large:
+        ms_l, bytes_l, ops_l, rows_l = run_size(16384, max(5, args.steps // 4), 3)
+        checked_rows += rows_l
+        big = dict(tokens=16384, us_per_step=round(ms_l * 1000, 1),
+                   gbs=round(bytes_l / (ms_l / 1e3) / 1e9, 1),
+                   frac=round(bytes_l / (ms_l / 1e3) / 1e9 / HBM_PEAK_GBS, 4), ops=ops_l)
 
     decode = None
     if not args.no_decode:
@@ -383,8 +395,9 @@ def main():
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),
         "verified_rows": checked_rows,
         "ops": ops,
+        "prefill_16384": big,
         "decode_us_per_layer": decode,
-        "roofline": {"kernel": "swiglu (cuca_glu_f16_silu)", "bound": "hbm",
+        "roofline": {"kernel": "swiglu (cuca_glu_f16_silu, 4096 tokens)", "bound": "hbm",
                      "achieved": glu["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": glu["frac"], "traffic": traffic_from_profiles(),
                      "algorithmic_bytes_per_launch": glu["bytes"], "avg_launch_us": glu["us"]},

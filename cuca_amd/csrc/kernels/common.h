@@ -30,6 +30,12 @@ template <> struct Chunk<float> {
         f32x4 t = reinterpret_cast<const f32x4 *>(base)[chunk];
         v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
     }
+    // Streaming load (nontemporal hint): for inputs read once that are larger
+    // than the last-level cache, so they do not evict data that is reused.
+    __device__ static inline void load_nt(const void *base, int64_t chunk, float (&v)[4]) {
+        f32x4 t = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(base) + chunk);
+        v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+    }
     __device__ static inline void store(void *base, int64_t chunk, const float (&v)[4]) {
         f32x4 t = {v[0], v[1], v[2], v[3]};
         reinterpret_cast<f32x4 *>(base)[chunk] = t;
@@ -45,6 +51,11 @@ template <> struct Chunk<_Float16> {
 #pragma unroll
         for (int i = 0; i < 8; i++) v[i] = (float)t[i];
     }
+    __device__ static inline void load_nt(const void *base, int64_t chunk, float (&v)[8]) {
+        f16x8 t = __builtin_nontemporal_load(reinterpret_cast<const f16x8 *>(base) + chunk);
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = (float)t[i];
+    }
     __device__ static inline void store(void *base, int64_t chunk, const float (&v)[8]) {
         f16x8 t;
 #pragma unroll
@@ -53,6 +64,13 @@ template <> struct Chunk<_Float16> {
     }
     __device__ static inline float as_stored(float v) { return (float)(_Float16)v; }
 };
+
+// Load chunk `c` of `base`, streaming (NT) or cached.
+template <typename T, bool NT, int N>
+__device__ static inline void load_chunk(const void *base, int64_t c, float (&v)[N]) {
+    if (NT) Chunk<T>::load_nt(base, c, v);
+    else Chunk<T>::load(base, c, v);
+}
 
 // Scalar element access for the shape-generic fallback kernels.
 template <typename T> __device__ static inline float load1(const void *p, int64_t i) {

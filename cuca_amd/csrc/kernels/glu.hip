@@ -41,7 +41,7 @@ template <int ACT> __device__ static inline float act_fn(float g) {
     return ACT == 0 ? act_silu(g) : act_gelu_tanh(g);
 }
 
-template <typename T, int ACT, bool RAGGED>
+template <typename T, int ACT, bool RAGGED, bool NTL>
 __device__ static inline void glu_body(const GluArgs &a) {
     constexpr int N = Chunk<T>::N;
     const uint32_t bpr = (uint32_t)a.blocks_per_row;
@@ -57,8 +57,8 @@ __device__ static inline void glu_body(const GluArgs &a) {
     const int c = (int)cblk * CUCA_BLOCK + (int)threadIdx.x;
     if (c >= cpr) return;
     float g[N], u[N], o[N];
-    Chunk<T>::load(reinterpret_cast<const T *>(a.gate) + (int64_t)row * a.gate_ld, c, g);
-    Chunk<T>::load(reinterpret_cast<const T *>(a.up) + (int64_t)row * a.up_ld, c, u);
+    load_chunk<T, NTL>(reinterpret_cast<const T *>(a.gate) + (int64_t)row * a.gate_ld, c, g);
+    load_chunk<T, NTL>(reinterpret_cast<const T *>(a.up) + (int64_t)row * a.up_ld, c, u);
     if (a.clamp > 0.0f) { // Glu::apply's clamp (cpu.rs:364-368)
 #pragma unroll
         for (int i = 0; i < N; i++) {
@@ -92,15 +92,18 @@ __device__ static inline void glu_generic_body(const GluArgs &a) {
     store1<T>(a.out, (int64_t)row * a.out_ld + j, act_fn<ACT>(g) * u);
 }
 
-#define CUCA_GLU(NAME, BODY, T, ACT, RAGGED)                                               \
+#define CUCA_GLU(NAME, BODY, ...)                                                          \
     extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void NAME(GluArgs a) {             \
-        BODY<T, ACT, RAGGED>(a);                                                           \
+        BODY<__VA_ARGS__>(a);                                                              \
     }
+// "nt" variants stream gate and up (inputs larger than the last-level cache).
 #define CUCA_GLU_SET(TN, T)                                                                \
-    CUCA_GLU(cuca_glu_##TN##_silu, glu_body, T, 0, false)                                  \
-    CUCA_GLU(cuca_glu_##TN##_gelu, glu_body, T, 1, false)                                  \
-    CUCA_GLU(cuca_glu_##TN##_silu_ragged, glu_body, T, 0, true)                            \
-    CUCA_GLU(cuca_glu_##TN##_gelu_ragged, glu_body, T, 1, true)                            \
+    CUCA_GLU(cuca_glu_##TN##_silu, glu_body, T, 0, false, false)                           \
+    CUCA_GLU(cuca_glu_##TN##_gelu, glu_body, T, 1, false, false)                           \
+    CUCA_GLU(cuca_glu_##TN##_silu_nt, glu_body, T, 0, false, true)                         \
+    CUCA_GLU(cuca_glu_##TN##_gelu_nt, glu_body, T, 1, false, true)                         \
+    CUCA_GLU(cuca_glu_##TN##_silu_ragged, glu_body, T, 0, true, false)                     \
+    CUCA_GLU(cuca_glu_##TN##_gelu_ragged, glu_body, T, 1, true, false)                     \
     CUCA_GLU(cuca_glu_##TN##_silu_generic, glu_generic_body, T, 0, false)                  \
     CUCA_GLU(cuca_glu_##TN##_gelu_generic, glu_generic_body, T, 1, false)                  \
     CUCA_GLU(cuca_glu_##TN##_silu_ragged_generic, glu_generic_body, T, 0, true)            \

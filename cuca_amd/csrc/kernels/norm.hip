@@ -5,13 +5,16 @@
 // a chain of burn ops (gpu.rs:5883-5896).  One pass over HBM: read x and the
 // branch, write x' = x + rs * [rms(branch, w_post)] and h = rms(x', w).
 //
-// Vector kernel: LPR lanes per row (64 = one wave64 per row for hidden >=
-// 64 chunks; fewer lanes, several rows per wave, for short rows).  The row
-// lives in registers (NCH 16-byte chunks per lane), so x' is never re-read;
-// the sum of squares is a per-lane sum in index order followed by a
-// butterfly over the row's lanes.  m = sqrt(sum / H + eps) and
-// y = v / m * w use IEEE division and square root, the reference's formula;
-// only the summation order differs from candle's sequential sum.
+// Vector kernel: TPR threads per row, NCH 16-byte chunks per thread; the
+// row lives in registers, so x' is never re-read.  Short rows share a wave
+// (TPR < 64); long rows spread over up to 16 waves (TPR up to 1024, one row
+// per workgroup) so a few rows at decode still issue many loads at once and
+// a prefill wave holds only a few chunks.  The sum of squares is a
+// per-thread sum in index order, a butterfly inside the wave and, across
+// waves, an LDS sum in wave order: a fixed order, independent of the other
+// rows.  y = x * (1 / sqrt(sum / H + eps)) * w, the reciprocal form of the
+// reference's GPU rms (gpu.rs:5883-5896), with IEEE sqrt and reciprocal;
+// against candle's x / m it differs by the rounding of one product.
 //
 // Generic kernel (any hidden, any alignment): one workgroup per row, scalar
 // loads, block reduction through LDS, x' re-read from x_out (or recomputed).
@@ -28,14 +31,35 @@ __device__ static inline void load_w(const float *w, int64_t c, float (&v)[N]) {
     }
 }
 
-template <typename T, int LPR, int NCH>
+// TPR threads per row (a power of two up to 1024), NCH chunks per thread.
+// TPR <= 64: a block of 256 threads holds 256 / TPR rows.  TPR > 64: a block
+// is one row of TPR threads.
+// Rows wider than a wave reduce through LDS (one slot per wave), in a fixed
+// order, so every thread of the row gets the same bits.
+template <int TPR>
+__device__ static inline float row_sum(float v, float *red) {
+    if (TPR <= CUCA_WAVE) return group_sum<TPR>(v);
+    constexpr int W = TPR / CUCA_WAVE; // waves per row (one row per block)
+    v = group_sum<CUCA_WAVE>(v);
+    const int wave = threadIdx.x / CUCA_WAVE;
+    if ((threadIdx.x & (CUCA_WAVE - 1)) == 0) red[wave] = v;
+    __syncthreads();
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < W; i++) s += red[i];
+    return s;
+}
+
+template <typename T, int TPR, int NCH, bool NTL>
 __device__ static inline void norm_body(const NormArgs &a) {
     constexpr int N = Chunk<T>::N;
-    constexpr int RPW = CUCA_WAVE / LPR;
-    const int lane = threadIdx.x & (CUCA_WAVE - 1);
-    const int wave = threadIdx.x / CUCA_WAVE;
-    const int li = lane & (LPR - 1);
-    const int64_t row = ((int64_t)blockIdx.x * (CUCA_BLOCK / CUCA_WAVE) + wave) * RPW + lane / LPR;
+    constexpr int B = TPR > CUCA_WAVE ? TPR : CUCA_BLOCK;
+    __shared__ float red_post[TPR > CUCA_WAVE ? TPR / CUCA_WAVE : 1];
+    __shared__ float red_main[TPR > CUCA_WAVE ? TPR / CUCA_WAVE : 1];
+    const int li = threadIdx.x & (TPR - 1);
+    const int64_t row = (int64_t)blockIdx.x * (B / TPR) + threadIdx.x / TPR;
+    // TPR > 64: the whole block is one row, so `live` is uniform and every
+    // thread reaches the barriers of row_sum
     const bool live = row < a.rows;
     const int H = a.hidden;
     const int nch = H / N;
@@ -44,9 +68,9 @@ __device__ static inline void norm_body(const NormArgs &a) {
     float v[NCH][N];
 #pragma unroll
     for (int k = 0; k < NCH; k++) {
-        const int c = li + k * LPR;
+        const int c = li + k * TPR;
         if (live && c < nch) {
-            Chunk<T>::load(a.x, cb + c, v[k]);
+            load_chunk<T, NTL>(a.x, cb + c, v[k]);
         } else {
 #pragma unroll
             for (int i = 0; i < N; i++) v[k][i] = 0.0f;
@@ -56,9 +80,9 @@ __device__ static inline void norm_body(const NormArgs &a) {
         float b[NCH][N];
 #pragma unroll
         for (int k = 0; k < NCH; k++) {
-            const int c = li + k * LPR;
+            const int c = li + k * TPR;
             if (live && c < nch) {
-                Chunk<T>::load(a.branch, cb + c, b[k]);
+                load_chunk<T, NTL>(a.branch, cb + c, b[k]);
             } else {
 #pragma unroll
                 for (int i = 0; i < N; i++) b[k][i] = 0.0f;
@@ -70,16 +94,16 @@ __device__ static inline void norm_body(const NormArgs &a) {
             for (int k = 0; k < NCH; k++)
 #pragma unroll
                 for (int i = 0; i < N; i++) ss += b[k][i] * b[k][i];
-            ss = group_sum<LPR>(ss);
-            const float m = sqrtf(ss / (float)H + a.post_eps);
+            ss = row_sum<TPR>(ss, red_post);
+            const float inv = 1.0f / sqrtf(ss / (float)H + a.post_eps);
 #pragma unroll
             for (int k = 0; k < NCH; k++) {
-                const int c = li + k * LPR;
+                const int c = li + k * TPR;
                 if (c < nch) {
                     float w[N];
                     load_w<N>(a.w_post, c, w);
 #pragma unroll
-                    for (int i = 0; i < N; i++) b[k][i] = b[k][i] / m * w[i];
+                    for (int i = 0; i < N; i++) b[k][i] = b[k][i] * inv * w[i];
                 }
             }
         }
@@ -93,17 +117,11 @@ __device__ static inline void norm_body(const NormArgs &a) {
         for (int k = 0; k < NCH; k++)
 #pragma unroll
             for (int i = 0; i < N; i++) v[k][i] = Chunk<T>::as_stored(v[k][i] + b[k][i]);
-        if (a.x_out && live) {
-#pragma unroll
-            for (int k = 0; k < NCH; k++) {
-                const int c = li + k * LPR;
-                if (c < nch) Chunk<T>::store(a.x_out, cb + c, v[k]);
-            }
-        }
-    } else if (a.x_out && live) {
+    }
+    if (a.x_out && live) {
 #pragma unroll
         for (int k = 0; k < NCH; k++) {
-            const int c = li + k * LPR;
+            const int c = li + k * TPR;
             if (c < nch) Chunk<T>::store(a.x_out, cb + c, v[k]);
         }
     }
@@ -112,22 +130,23 @@ __device__ static inline void norm_body(const NormArgs &a) {
     for (int k = 0; k < NCH; k++)
 #pragma unroll
         for (int i = 0; i < N; i++) ss += v[k][i] * v[k][i];
-    ss = group_sum<LPR>(ss);
-    const float m = sqrtf(ss / (float)H + a.eps);
+    ss = row_sum<TPR>(ss, red_main);
+    // y = x * (1 / sqrt(mean + eps)) * w, the GPU mirror's form (gpu.rs:5883-5896)
+    const float inv = 1.0f / sqrtf(ss / (float)H + a.eps);
     if (!live) return;
 #pragma unroll
     for (int k = 0; k < NCH; k++) {
-        const int c = li + k * LPR;
+        const int c = li + k * TPR;
         if (c < nch) {
             float h[N];
             if (a.w) {
                 float w[N];
                 load_w<N>(a.w, c, w);
 #pragma unroll
-                for (int i = 0; i < N; i++) h[i] = v[k][i] / m * w[i];
+                for (int i = 0; i < N; i++) h[i] = v[k][i] * inv * w[i];
             } else {
 #pragma unroll
-                for (int i = 0; i < N; i++) h[i] = v[k][i] / m;
+                for (int i = 0; i < N; i++) h[i] = v[k][i] * inv;
             }
             Chunk<T>::store(a.h_out, cb + c, h);
         }
@@ -148,14 +167,14 @@ __device__ static inline void norm_generic_body(const NormArgs &a) {
             ss += b * b;
         }
         ss = block_sum(ss, red);
-        mb = sqrtf(ss / (float)H + a.post_eps);
+        mb = 1.0f / sqrtf(ss / (float)H + a.post_eps);
     }
     float ss = 0.0f;
     for (int i = threadIdx.x; i < H; i += blockDim.x) {
         float v = load1<T>(a.x, base + i);
         if (a.branch) {
             float b = load1<T>(a.branch, base + i);
-            if (a.w_post) b = b / mb * a.w_post[i];
+            if (a.w_post) b = b * mb * a.w_post[i];
             if (a.rs != 1.0f) b = b * a.rs + 0.0f;
             v = Chunk<T>::as_stored(v + b);
         }
@@ -163,7 +182,7 @@ __device__ static inline void norm_generic_body(const NormArgs &a) {
         ss += v * v;
     }
     ss = block_sum(ss, red);
-    const float m = sqrtf(ss / (float)H + a.eps);
+    const float inv = 1.0f / sqrtf(ss / (float)H + a.eps);
     for (int i = threadIdx.x; i < H; i += blockDim.x) {
         float v;
         if (a.x_out) { // this thread wrote element i above
@@ -172,32 +191,43 @@ __device__ static inline void norm_generic_body(const NormArgs &a) {
             v = load1<T>(a.x, base + i);
             if (a.branch) {
                 float b = load1<T>(a.branch, base + i);
-                if (a.w_post) b = b / mb * a.w_post[i];
+                if (a.w_post) b = b * mb * a.w_post[i];
                 if (a.rs != 1.0f) b = b * a.rs + 0.0f;
                 v = Chunk<T>::as_stored(v + b);
             }
         }
-        const float h = a.w ? v / m * a.w[i] : v / m;
+        const float h = a.w ? v * inv * a.w[i] : v * inv;
         store1<T>(a.h_out, base + i, h);
     }
 }
 
-#define CUCA_NORM(NAME, T, LPR, NCH)                                                       \
-    extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void NAME(NormArgs a) {            \
-        norm_body<T, LPR, NCH>(a);                                                         \
+#define CUCA_NORM(NAME, T, TPR, NCH, NTL)                                                  \
+    extern "C" __global__ __launch_bounds__(TPR > CUCA_WAVE ? TPR : CUCA_BLOCK) void NAME(    \
+        NormArgs a) {                                                                      \
+        norm_body<T, TPR, NCH, NTL>(a);                                                    \
     }
+// Shapes: TPR = 2^k threads per row with one chunk each up to 1024 (every
+// hidden size up to 1024 chunks: 4096 f32, 8192 f16), then 1024 threads with
+// 2 or 4 chunks (8 for f32); "nt" variants stream x and the branch.
 #define CUCA_NORM_SET(TN, T)                                                               \
-    CUCA_NORM(cuca_norm_##TN##_l64_c1, T, 64, 1)                                           \
-    CUCA_NORM(cuca_norm_##TN##_l64_c2, T, 64, 2)                                           \
-    CUCA_NORM(cuca_norm_##TN##_l64_c4, T, 64, 4)                                           \
-    CUCA_NORM(cuca_norm_##TN##_l64_c8, T, 64, 8)                                           \
-    CUCA_NORM(cuca_norm_##TN##_l64_c16, T, 64, 16)                                         \
-    CUCA_NORM(cuca_norm_##TN##_l32_c1, T, 32, 1)                                           \
-    CUCA_NORM(cuca_norm_##TN##_l16_c1, T, 16, 1)                                           \
-    CUCA_NORM(cuca_norm_##TN##_l8_c1, T, 8, 1)                                             \
-    CUCA_NORM(cuca_norm_##TN##_l4_c1, T, 4, 1)                                             \
-    CUCA_NORM(cuca_norm_##TN##_l2_c1, T, 2, 1)                                             \
-    CUCA_NORM(cuca_norm_##TN##_l1_c1, T, 1, 1)                                             \
+    CUCA_NORM(cuca_norm_##TN##_t1, T, 1, 1, false)                                         \
+    CUCA_NORM(cuca_norm_##TN##_t2, T, 2, 1, false)                                         \
+    CUCA_NORM(cuca_norm_##TN##_t4, T, 4, 1, false)                                         \
+    CUCA_NORM(cuca_norm_##TN##_t8, T, 8, 1, false)                                         \
+    CUCA_NORM(cuca_norm_##TN##_t16, T, 16, 1, false)                                       \
+    CUCA_NORM(cuca_norm_##TN##_t32, T, 32, 1, false)                                       \
+    CUCA_NORM(cuca_norm_##TN##_t64, T, 64, 1, false)                                       \
+    CUCA_NORM(cuca_norm_##TN##_t128, T, 128, 1, false)                                     \
+    CUCA_NORM(cuca_norm_##TN##_t256, T, 256, 1, false)                                     \
+    CUCA_NORM(cuca_norm_##TN##_t512, T, 512, 1, false)                                     \
+    CUCA_NORM(cuca_norm_##TN##_t1024, T, 1024, 1, false)                                   \
+    CUCA_NORM(cuca_norm_##TN##_t1024_c2, T, 1024, 2, false)                                \
+    CUCA_NORM(cuca_norm_##TN##_t1024_c4, T, 1024, 4, false)                                \
+    CUCA_NORM(cuca_norm_##TN##_t128_nt, T, 128, 1, true)                                   \
+    CUCA_NORM(cuca_norm_##TN##_t256_nt, T, 256, 1, true)                                   \
+    CUCA_NORM(cuca_norm_##TN##_t512_nt, T, 512, 1, true)                                   \
+    CUCA_NORM(cuca_norm_##TN##_t1024_nt, T, 1024, 1, true)                                 \
+    CUCA_NORM(cuca_norm_##TN##_t1024_c2_nt, T, 1024, 2, true)                              \
     extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void cuca_norm_##TN##_generic(     \
         NormArgs a) {                                                                      \
         norm_generic_body<T>(a);                                                           \
@@ -205,6 +235,6 @@ __device__ static inline void norm_generic_body(const NormArgs &a) {
 
 CUCA_NORM_SET(f32, float)
 CUCA_NORM_SET(f16, _Float16)
-// 8192-wide f32 rows (32 chunks per lane) still fit in registers; f16 rows
-// of 32 chunks would spill and take the generic kernel instead.
-CUCA_NORM(cuca_norm_f32_l64_c32, float, 64, 32)
+// 8 chunks per thread: f32 rows of up to 32768 values fit in registers; f16
+// rows that wide would spill and take the generic kernel.
+CUCA_NORM(cuca_norm_f32_t1024_c8, float, 1024, 8, false)
