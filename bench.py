@@ -11,8 +11,9 @@ of the hot path over one batch of 4096 prefill tokens with f16 activations
 (configs[2] at its smaller size): the Q8_0 embedding gather of the batch,
 the attention-side residual add + RMSNorm, RoPE on Q 32x128 / K 8x128, the
 SwiGLU over F 14336, and the FFN-side residual add + RMSNorm.  `value` is
-the algorithmic bytes of a step divided by its time, with every input
-resident in HBM (synthetic data generated on the device).  The decode figure
+the algorithmic bytes of a step divided by its time (K steps between two HIP
+events, synchronized on both sides), with every input resident in HBM
+(synthetic data generated on the device).  The decode figure
 is the same layer's non-matmul sequence (two fused norms, RoPE, SwiGLU) at
 batch 1 and 32 in f32, 32 layers captured in one hipGraph and
 replayed, in microseconds per layer.
@@ -25,8 +26,10 @@ Algorithmic bytes per unit (s = bytes per activation, H 4096, F 14336):
 Per-call constants (gamma, norm weights) are counted once.
 
 roofline: the dominant kernel (SwiGLU) -- its algorithmic bytes per launch
-divided by its average launch duration from HIP events recorded on the
-stream the kernels run on, against the 8 TB/s HBM peak.
+divided by its average launch duration over the timed steps, from the start
+and stop events the C ABI's profile attaches to every kernel
+(hipExtModuleLaunchKernel on the ops' stream; the same durations rocprofv3
+reports), against the 8 TB/s HBM peak.
 
 cpu_baseline: the oracle's C restatement of the reference's candle CPU path
 (oracle/), on the host's cores, over a bounded sample of the same step.
@@ -176,19 +179,29 @@ def time_steps(torch, fn, steps, warmup):
     return t0.elapsed_time(t1) / steps
 
 
-def per_op_ms(torch, step, steps):
-    """Average duration of every op of the step, from HIP events recorded
-    around each launch on the stream the kernels run on."""
-    evs = {name: [] for name in STEP_OPS}
-    for _ in range(steps):
-        for name in STEP_OPS:
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            step.launch(name)
-            b.record()
-            evs[name].append((a, b))
+def profiled_steps(torch, ctx, step, steps, warmup):
+    """Time `steps` steps between two HIP events on the ops' stream, with
+    every kernel also carrying start/stop events of its own (the C ABI's
+    profile, hipExtModuleLaunchKernel): returns (ms per step, {op: (kernel,
+    average kernel ms)})."""
+    for _ in range(warmup):
+        step.step()
     torch.cuda.synchronize()
-    return {name: sum(a.elapsed_time(b) for a, b in v) / len(v) for name, v in evs.items()}
+    ctx.profile_start(len(STEP_OPS) * steps)
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        step.step()
+    t1.record()
+    recs = ctx.profile_stop()
+    torch.cuda.synchronize()
+    assert len(recs) == len(STEP_OPS) * steps, len(recs)
+    per = {}
+    for i, (kernel, kms) in enumerate(recs):
+        name = STEP_OPS[i % len(STEP_OPS)]
+        k, tot = per.get(name, (kernel, 0.0))
+        per[name] = (kernel, tot + kms)
+    return t0.elapsed_time(t1) / steps, {n: (k, t / steps) for n, (k, t) in per.items()}
 
 
 class DecodeLayers:
@@ -333,28 +346,29 @@ def main():
         log(f"prefill step buffers, {n} tokens")
         st = PrefillStep(ctx, torch, n)
         torch.cuda.synchronize()
-        log("timed steps")
-        ms = time_steps(torch, st.step, steps, warmup)
+        log("timed steps (unprofiled)")
+        ms_plain = time_steps(torch, st.step, steps, warmup)
+        log("timed steps (kernel timestamps)")
+        ms, per = profiled_steps(torch, ctx, st, steps, warmup)
         ctx.check_device()
-        log(f"{ms * 1000:.1f} us per step; per-op events")
-        ops_ms = per_op_ms(torch, st, steps)
-        ops = {name: dict(us=round(t * 1000, 2), bytes=st.bytes[name],
+        log(f"{ms * 1000:.1f} us per step ({ms_plain * 1000:.1f} unprofiled)")
+        ops = {name: dict(kernel=k, us=round(t * 1000, 2), bytes=st.bytes[name],
                           gbs=round(st.bytes[name] / (t / 1e3) / 1e9, 1),
                           frac=round(st.bytes[name] / (t / 1e3) / 1e9 / HBM_PEAK_GBS, 4))
-               for name, t in ops_ms.items()}
+               for name, (k, t) in per.items()}
         log("verify sampled rows against the oracle")
         rows = st.verify(torch)
         step_bytes = sum(st.bytes.values())
         del st
         torch.cuda.empty_cache()
-        return ms, step_bytes, ops, rows
+        return ms, step_bytes, ops, rows, ms_plain
 
-    ms, step_bytes, ops, checked_rows = run_size(args.tokens, args.steps, args.warmup)
+    ms_prof, step_bytes, ops, checked_rows, ms = run_size(args.tokens, args.steps, args.warmup)
     value = step_bytes / (ms / 1e3) / 1e9
     glu = ops["swiglu"]
     big = None
     if args.tokens != 16384 and not args.no_large:
-        ms_l, bytes_l, ops_l, rows_l = run_size(16384, max(5, args.steps // 4), 3)
+        _, bytes_l, ops_l, rows_l, ms_l = run_size(16384, max(5, args.steps // 4), 3)
         checked_rows += rows_l
         big = dict(tokens=16384, us_per_step=round(ms_l * 1000, 1),
                    gbs=round(bytes_l / (ms_l / 1e3) / 1e9, 1),
@@ -383,6 +397,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 5),
+        "ms_per_step_profiled": round(ms_prof, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -397,7 +412,7 @@ def main():
         "ops": ops,
         "prefill_16384": big,
         "decode_us_per_layer": decode,
-        "roofline": {"kernel": "swiglu (cuca_glu_f16_silu, 4096 tokens)", "bound": "hbm",
+        "roofline": {"kernel": glu["kernel"], "bound": "hbm",
                      "achieved": glu["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": glu["frac"], "traffic": traffic_from_profiles(),
                      "algorithmic_bytes_per_launch": glu["bytes"], "avg_launch_us": glu["us"]},

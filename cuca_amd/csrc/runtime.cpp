@@ -16,6 +16,18 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <vector>
+
+// hipExtModuleLaunchKernel (libamdhip64): the module launch whose events
+// stamp the kernel's own start and end.  Declared here because hip_ext.h
+// also carries device-side templates a host-only C++ compiler cannot parse.
+extern "C" hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t globalWorkSizeX,
+                                               uint32_t globalWorkSizeY, uint32_t globalWorkSizeZ,
+                                               uint32_t localWorkSizeX, uint32_t localWorkSizeY,
+                                               uint32_t localWorkSizeZ, size_t sharedMemBytes,
+                                               hipStream_t hStream, void **kernelParams,
+                                               void **extra, hipEvent_t startEvent,
+                                               hipEvent_t stopEvent, uint32_t flags);
 
 #ifndef CUCA_CODE_OBJECT
 #error "CUCA_CODE_OBJECT must name the gfx950 code object to embed"
@@ -63,6 +75,12 @@ struct cuca_hip_ctx {
     int64_t last_vocab = 0;       // for the out-of-range message
     int64_t last_table_rows = 0;
     std::string error;
+    // per-kernel timing (cuca_hip_profile_start/stop)
+    struct ProfRec { int kernel; hipEvent_t start, stop; };
+    std::vector<ProfRec> prof;    // event pairs, created once and reused
+    size_t prof_used = 0;
+    size_t prof_limit = 0;
+    bool profiling = false;
 };
 
 struct cuca_hip_graph {
@@ -107,8 +125,17 @@ cuca_status launch(cuca_hip_ctx *ctx, Kernel k, unsigned grid, unsigned block, u
                    Args &args) {
     if (grid == 0) return CUCA_OK;
     void *params[] = {&args};
-    hipError_t e = hipModuleLaunchKernel(ctx->fn[k], grid, 1, 1, block, 1, 1, lds, ctx->stream,
-                                         params, nullptr);
+    hipError_t e;
+    if (ctx->profiling && !ctx->capturing && ctx->prof_used < ctx->prof_limit) {
+        cuca_hip_ctx::ProfRec &r = ctx->prof[ctx->prof_used++];
+        r.kernel = k;
+        // work sizes in work-items; the events stamp the kernel's own start and end
+        e = hipExtModuleLaunchKernel(ctx->fn[k], grid * block, 1, 1, block, 1, 1, lds, ctx->stream,
+                                     params, nullptr, r.start, r.stop, 0);
+    } else {
+        e = hipModuleLaunchKernel(ctx->fn[k], grid, 1, 1, block, 1, 1, lds, ctx->stream, params,
+                                  nullptr);
+    }
     if (e != hipSuccess) return fail(ctx, CUCA_HIP_ERROR, "launching %s: %s", kKernelNames[k],
                                      hipGetErrorString(e));
     return CUCA_OK;
@@ -193,6 +220,10 @@ void cuca_hip_ctx_destroy(cuca_hip_ctx *ctx) {
     if (ctx->stream && ctx->stream != ctx->own_stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->t0) (void)hipEventDestroy(ctx->t0);
     if (ctx->t1) (void)hipEventDestroy(ctx->t1);
+    for (auto &r : ctx->prof) {
+        (void)hipEventDestroy(r.start);
+        (void)hipEventDestroy(r.stop);
+    }
     if (ctx->status) (void)hipFree(ctx->status);
     if (ctx->module) (void)hipModuleUnload(ctx->module);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
@@ -691,6 +722,46 @@ cuca_status cuca_hip_timer_stop(cuca_hip_ctx *ctx, float *ms) {
     HIP_TRY(ctx, hipEventRecord(ctx->t1, ctx->stream));
     HIP_TRY(ctx, hipEventSynchronize(ctx->t1));
     HIP_TRY(ctx, hipEventElapsedTime(ms, ctx->t0, ctx->t1));
+    return CUCA_OK;
+}
+
+cuca_status cuca_hip_profile_start(cuca_hip_ctx *ctx, int32_t max_launches) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    if (ctx->capturing) return fail(ctx, CUCA_INVALID_ARG, "cannot profile during a capture");
+    if (max_launches < 0 || max_launches > (1 << 20))
+        return fail(ctx, CUCA_INVALID_ARG, "bad launch count %d", max_launches);
+    while (ctx->prof.size() < (size_t)max_launches) {
+        cuca_hip_ctx::ProfRec r{0, nullptr, nullptr};
+        HIP_TRY(ctx, hipEventCreate(&r.start));
+        hipError_t e = hipEventCreate(&r.stop);
+        if (e != hipSuccess) {
+            (void)hipEventDestroy(r.start);
+            return hip_fail(ctx, e, "hipEventCreate");
+        }
+        ctx->prof.push_back(r);
+    }
+    ctx->prof_used = 0;
+    ctx->prof_limit = (size_t)max_launches;
+    ctx->profiling = true;
+    return CUCA_OK;
+}
+
+cuca_status cuca_hip_profile_stop(cuca_hip_ctx *ctx, cuca_hip_kernel_time *out, int32_t max,
+                                  int32_t *count) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    if (!count || (max > 0 && !out)) return fail(ctx, CUCA_INVALID_ARG, "null output pointer");
+    if (!ctx->profiling) return fail(ctx, CUCA_INVALID_ARG, "profiling was not started");
+    ctx->profiling = false;
+    HIP_TRY(ctx, hipStreamSynchronize(ctx->stream));
+    const int32_t n = (int32_t)ctx->prof_used < max ? (int32_t)ctx->prof_used : max;
+    for (int32_t i = 0; i < n; i++) {
+        const cuca_hip_ctx::ProfRec &r = ctx->prof[i];
+        out[i].kernel = kKernelNames[r.kernel];
+        HIP_TRY(ctx, hipEventElapsedTime(&out[i].ms, r.start, r.stop));
+    }
+    *count = n;
     return CUCA_OK;
 }
 

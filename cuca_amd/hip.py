@@ -38,6 +38,11 @@ class RopeSpecC(ctypes.Structure):
                 ("yarn_n_ctx_orig", _i64), ("attn_factor", ctypes.c_double)]
 
 
+class KernelTime(ctypes.Structure):
+    """cuca_hip_kernel_time."""
+    _fields_ = [("kernel", ctypes.c_char_p), ("ms", _f32)]
+
+
 SIGNATURES = {
     "cuca_hip_ctx_create": (_st, [ctypes.c_int, _pp]),
     "cuca_hip_ctx_destroy": (None, [_p]),
@@ -66,6 +71,9 @@ SIGNATURES = {
     "cuca_hip_graph_destroy": (None, [_p]),
     "cuca_hip_timer_start": (_st, [_p]),
     "cuca_hip_timer_stop": (_st, [_p, ctypes.POINTER(_f32)]),
+    "cuca_hip_profile_start": (_st, [_p, _i32]),
+    "cuca_hip_profile_stop": (_st, [_p, ctypes.POINTER(KernelTime), _i32,
+                                    ctypes.POINTER(_i32)]),
 }
 
 _LIB = None
@@ -237,6 +245,18 @@ class Context:
         ms = ctypes.c_float()
         self.check(self.L.cuca_hip_timer_stop(self.ptr, ctypes.byref(ms)))
         return ms.value
+
+    def profile_start(self, max_launches):
+        self.check(self.L.cuca_hip_profile_start(self.ptr, max_launches))
+        self._prof_max = max_launches
+
+    def profile_stop(self):
+        """[(kernel name, ms)] of the launches since profile_start, in order."""
+        n = max(getattr(self, "_prof_max", 0), 1)
+        buf = (KernelTime * n)()
+        count = _i32()
+        self.check(self.L.cuca_hip_profile_stop(self.ptr, buf, n, ctypes.byref(count)))
+        return [(buf[i].kernel.decode(), buf[i].ms) for i in range(count.value)]
 
     def graph_begin(self):
         self.check(self.L.cuca_hip_graph_begin(self.ptr))

@@ -227,6 +227,22 @@ void cuca_hip_graph_destroy(cuca_hip_graph *graph);
 cuca_status cuca_hip_timer_start(cuca_hip_ctx *ctx);
 cuca_status cuca_hip_timer_stop(cuca_hip_ctx *ctx, float *ms);
 
+/* Per-kernel timing, the device-side counterpart of the engine's
+ * ServingCounters (engine/mod.rs:566-612, per-forward step_ns): between
+ * profile_start and profile_stop the first `max_launches` kernels the ops
+ * launch carry start/stop events on the kernel itself
+ * (hipExtModuleLaunchKernel), so their durations exclude dispatch gaps.
+ * profile_stop synchronizes and writes up to `max` records, in launch order.
+ * Not available during a graph capture. */
+typedef struct {
+    const char *kernel; /* the kernel's symbol in the code object (static) */
+    float ms;
+} cuca_hip_kernel_time;
+
+cuca_status cuca_hip_profile_start(cuca_hip_ctx *ctx, int32_t max_launches);
+cuca_status cuca_hip_profile_stop(cuca_hip_ctx *ctx, cuca_hip_kernel_time *out, int32_t max,
+                                  int32_t *count);
+
 #ifdef __cplusplus
 }
 #endif

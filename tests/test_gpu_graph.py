@@ -81,3 +81,23 @@ def test_graph_replays_match_eager(ctx, n):
         layer.issue()
         ctx.sync()
     graph.destroy()
+
+
+def test_profile_records_every_launch_in_order(ctx):
+    cfg = W.CONFIGS["B"]
+    rng = np.random.default_rng(3)
+    layer = Layer(ctx, rng, 4, cfg)
+    ctx.profile_start(8)
+    layer.issue()
+    recs = ctx.profile_stop()
+    names = [k for k, _ in recs]
+    assert len(recs) == 4
+    assert names[0].startswith("cuca_norm_f32") and names[1].startswith("cuca_rope_f32")
+    assert names[2].startswith("cuca_glu_f32") and names[3].startswith("cuca_norm_f32")
+    assert all(0.0 < ms < 100.0 for _, ms in recs)
+    # past the limit, launches still run, unrecorded
+    ctx.profile_start(2)
+    layer.issue()
+    assert len(ctx.profile_stop()) == 2
+    with pytest.raises(hip.CucaError, match="not started"):
+        ctx.profile_stop()
