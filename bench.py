@@ -22,8 +22,13 @@ Algorithmic bytes per unit (s = bytes per activation, H 4096, F 14336):
   embed       34 H/32 + 4 + s H        per token (block bytes, id, output)
   add_rmsnorm 4 s H                    per row   (x, branch in; x', h out)
   rope        2 s (nq + nk) D + 4 D    per row   (Q, K in and out; cos+sin)
-  swiglu      3 s F                    per row   (gate, up in; out)
+  glu         3 s F                    per row   (gate, up in; out)
 Per-call constants (gamma, norm weights) are counted once.
+
+`configs` repeats the step for the other workload configs (A Qwen3-0.6B,
+B Llama-3-8B decode batch, D Gemma-2-9B with the sandwich norms, GeGLU and
+interleaved RoPE, E Qwen3-30B-A3B with QK-norm RoPE and the ragged
+expert-grouped SwiGLU), each op's kernel GB/s from its timestamps.
 
 roofline: the dominant kernel (SwiGLU) -- its algorithmic bytes per launch
 divided by its average launch duration over the timed steps, from the start
@@ -50,120 +55,180 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def op_bytes(op, n, s, H=4096, F=14336, nq=32, nk=8, D=128, qbytes=34):
-    if op == "embed":
-        return n * (qbytes * H // 32 + 4 + s * H)
-    if op == "add_rmsnorm":
-        return n * 4 * s * H + 4 * H
-    if op == "rope":
-        return n * (2 * s * (nq + nk) * D + 4 * D)
-    if op == "swiglu":
-        return n * 3 * s * F
-    raise KeyError(op)
+STEP_OPS = ("embed", "add_rmsnorm_attn", "rope", "glu", "add_rmsnorm_ffn")
 
 
-STEP_OPS = ("embed", "add_rmsnorm_attn", "rope", "swiglu", "add_rmsnorm_ffn")
+class LayerStep:
+    """Device buffers of one pass of the hot path for a workload config
+    (cuca_amd.workloads.CONFIGS) at n tokens in `dtype`, and its launches:
+    the embedding gather of the batch, the attention-side residual add +
+    RMSNorm (Gemma: with the post-norm sandwich), RoPE on Q and K (Qwen3-MoE:
+    with the QK-norm), the gated activation (SwiGLU / GeGLU-tanh; Qwen3-MoE:
+    over the expert-grouped rows of top-k routing), and the FFN-side
+    residual add + RMSNorm.  Inputs are generated on the device."""
 
-
-def op_kind(name):
-    return "add_rmsnorm" if name.startswith("add_rmsnorm") else name
-
-
-class PrefillStep:
-    """Device buffers of one prefill step (config C shapes) and its launches."""
-
-    def __init__(self, ctx, torch, n, seed=2):
+    def __init__(self, ctx, torch, name, n, dtype):
         from cuca_amd import hip
         from cuca_amd import workloads as W
-        cfg = W.CONFIGS["C"]
-        self.hip, self.ctx, self.n, self.cfg = hip, ctx, n, cfg
+        import numpy as np
+        cfg = W.CONFIGS[name]
+        self.hip, self.ctx, self.torch, self.name, self.n, self.cfg = hip, ctx, torch, name, n, cfg
+        self.dt = hip.F16 if dtype == "f16" else hip.F32
+        tdt = torch.float16 if dtype == "f16" else torch.float32
+        s = 2 if dtype == "f16" else 4
         H, F, d, nq, nk = cfg["hidden"], cfg["ff"], cfg["head_dim"], cfg["nq"], cfg["nk"]
         dev = "cuda"
-        gen = torch.Generator(device=dev).manual_seed(seed)
-        f16 = torch.float16
-        self.table = W.quant_table_torch(gen, cfg["vocab"], H, cfg["qtype"], cfg["d_range"])
-        self.ids = torch.randint(0, cfg["vocab"], (n,), device=dev, generator=gen, dtype=torch.int32)
-        self.emb = torch.empty((n, H), device=dev, dtype=f16)
+        gen = torch.Generator(device=dev).manual_seed(cfg["seed"] * 1000 + n)
+        std = cfg["std"]
 
         def act(*shape):
-            return torch.randn(shape, device=dev, generator=gen).to(f16)
-        self.x1, self.b1, self.xo1, self.h1 = act(n, H), act(n, H), act(n, H), act(n, H)
-        self.x2, self.b2, self.xo2, self.h2 = act(n, H), act(n, H), act(n, H), act(n, H)
-        self.w1 = (1 + 0.02 * torch.randn(H, device=dev, generator=gen)).float()
-        self.w2 = (1 + 0.02 * torch.randn(H, device=dev, generator=gen)).float()
+            return (std * torch.randn(shape, device=dev, generator=gen)).to(tdt)
+
+        def gamma(k):
+            return (1 + 0.02 * torch.randn(k, device=dev, generator=gen)).float()
+        self.qtype = W.GGML_ID[cfg["qtype"]]
+        self.table = W.quant_table_torch(gen, cfg["vocab"], H, cfg["qtype"], cfg["d_range"])
+        self.ids = torch.randint(0, cfg["vocab"], (n,), device=dev, generator=gen, dtype=torch.int32)
+        self.emb = torch.empty((n, H), device=dev, dtype=tdt)
+        self.norm = []
+        for _ in range(2):
+            self.norm.append(dict(x=act(n, H), b=act(n, H), xo=torch.empty((n, H), device=dev, dtype=tdt),
+                                  h=torch.empty((n, H), device=dev, dtype=tdt), w=gamma(H),
+                                  wp=gamma(H) if cfg.get("sandwich") else None))
         self.q, self.k = act(n, nq, d), act(n, nk, d)
         self.q0, self.k0 = self.q.clone(), self.k.clone()
-        cos, sin = hip.rope_tables(hip.ROPE_NORM, d, cfg["theta"], n)
+        self.kind = hip.ROPE_NEOX if cfg["rope"] == "neox" else hip.ROPE_NORM
+        trows = W.table_rows_needed(cfg, n)
+        cos, sin = hip.rope_tables(self.kind, d, cfg["theta"], trows)
+        self.trows = trows
         self.cos, self.sin = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
-        self.pos = torch.arange(n, device=dev, dtype=torch.int32)
-        self.gu = act(n, 2 * F)
-        self.out = torch.empty((n, F), device=dev, dtype=f16)
-        self.bytes = {name: op_bytes(op_kind(name), n, 2) for name in STEP_OPS}
+        pos = W.positions(cfg, n, np.random.default_rng(cfg["seed"]))
+        self.pos = torch.from_numpy(pos).to(dev)
+        self.qn = gamma(d) if cfg.get("qk_norm") else None
+        self.kn = gamma(d) if cfg.get("qk_norm") else None
+        self.act = hip.ACT_GELU_TANH if cfg["act"] == "gelu" else hip.ACT_SILU
+        if cfg.get("moe"):
+            n_exp, k = cfg["moe"]
+            offsets, _ = W.zipf_expert_rows(np.random.default_rng(cfg["seed"]), n, n_exp, k)
+            self.n_exp, self.rows_glu = n_exp, int(offsets[-1])
+            self.offsets = torch.from_numpy(offsets).to(dev)
+            self.gate, self.up = act(self.rows_glu, F), act(self.rows_glu, F)
+        else:
+            self.offsets = None
+            self.rows_glu = n
+            self.gu = act(n, 2 * F)
+        self.out = torch.empty((self.rows_glu, F), device=dev, dtype=tdt)
+        bb = 18 if cfg["qtype"] == "q4_0" else 34
+        nw = 2 if cfg.get("sandwich") else 1
+        self.bytes = {
+            "embed": n * (bb * H // 32 + 4 + s * H),
+            "add_rmsnorm_attn": n * 4 * s * H + nw * 4 * H,
+            "rope": n * (2 * s * (nq + nk) * d + 4 * d) + (8 * d if cfg.get("qk_norm") else 0),
+            "glu": self.rows_glu * 3 * s * F,
+            "add_rmsnorm_ffn": n * 4 * s * H + nw * 4 * H,
+        }
 
     def launch(self, name):
-        c, hip, cfg, n = self.ctx, self.hip, self.cfg, self.n
+        c, hip, cfg, n, dt = self.ctx, self.hip, self.cfg, self.n, self.dt
         H, F, d, nq, nk = cfg["hidden"], cfg["ff"], cfg["head_dim"], cfg["nq"], cfg["nk"]
+        es = 2 if dt == hip.F16 else 4
         if name == "embed":
-            c.embed_gguf(self.table.data_ptr(), hip.GGML_Q8_0, cfg["vocab"], H, self.ids.data_ptr(),
-                         n, 1.0, self.emb.data_ptr(), hip.F16)
-        elif name == "add_rmsnorm_attn":
-            c.add_rmsnorm(self.x1.data_ptr(), self.b1.data_ptr(), self.w1.data_ptr(), None,
-                          cfg["eps"], cfg["eps"], 1.0, n, H, self.xo1.data_ptr(),
-                          self.h1.data_ptr(), hip.F16)
+            c.embed_gguf(self.table.data_ptr(), self.qtype, cfg["vocab"], H, self.ids.data_ptr(), n,
+                         cfg["embd_scale"], self.emb.data_ptr(), dt)
+        elif name.startswith("add_rmsnorm"):
+            b = self.norm[0 if name.endswith("attn") else 1]
+            c.add_rmsnorm(b["x"].data_ptr(), b["b"].data_ptr(), b["w"].data_ptr(),
+                          None if b["wp"] is None else b["wp"].data_ptr(), cfg["eps"], cfg["eps"], 1.0,
+                          n, H, b["xo"].data_ptr(), b["h"].data_ptr(), dt)
         elif name == "rope":
-            c.rope(self.q.data_ptr(), nq * d, self.k.data_ptr(), nk * d, n, nq, nk, d, d,
-                   hip.ROPE_NORM, self.cos.data_ptr(), self.sin.data_ptr(), n, self.pos.data_ptr(),
-                   None, None, cfg["eps"], hip.F16)
-        elif name == "swiglu":
-            c.glu(self.gu.data_ptr(), 2 * F, self.gu.data_ptr() + 2 * F, 2 * F, n, F,
-                  hip.ACT_SILU, 0.0, self.out.data_ptr(), F, hip.F16)
-        elif name == "add_rmsnorm_ffn":
-            c.add_rmsnorm(self.x2.data_ptr(), self.b2.data_ptr(), self.w2.data_ptr(), None,
-                          cfg["eps"], cfg["eps"], 1.0, n, H, self.xo2.data_ptr(),
-                          self.h2.data_ptr(), hip.F16)
+            c.rope(self.q.data_ptr(), nq * d, self.k.data_ptr(), nk * d, n, nq, nk, d, d, self.kind,
+                   self.cos.data_ptr(), self.sin.data_ptr(), self.trows, self.pos.data_ptr(),
+                   None if self.qn is None else self.qn.data_ptr(),
+                   None if self.kn is None else self.kn.data_ptr(), cfg["eps"], dt)
+        elif name == "glu":
+            if self.offsets is not None:
+                c.glu_ragged(self.gate.data_ptr(), F, self.up.data_ptr(), F, self.offsets.data_ptr(),
+                             self.n_exp, self.rows_glu, F, self.act, 0.0, self.out.data_ptr(), F, dt)
+            else:
+                c.glu(self.gu.data_ptr(), 2 * F, self.gu.data_ptr() + es * F, 2 * F, n, F, self.act,
+                      0.0, self.out.data_ptr(), F, dt)
 
     def step(self):
         for name in STEP_OPS:
             self.launch(name)
 
-    def verify(self, torch, rows=24):
+    def verify(self, rows=16):
         """Run the step once from fresh Q/K and compare sampled rows of every
-        output with the oracle (the timed kernels did the work they claim)."""
+        output with the oracle (the timed kernels did the work they claim):
+        the gather and plain RoPE bit for bit, the rest to 1e-5 relative (f32)
+        or 2 f16 ulps, with the floors of the parity tests for the GELU
+        cancellation, the sandwich sum and the QK-normed rotation."""
         import numpy as np
         from oracle import oracle as O
-        from cuca_amd import workloads as W
-        cfg, n = self.cfg, self.n
+        torch, cfg, n = self.torch, self.cfg, self.n
         H, F, d = cfg["hidden"], cfg["ff"], cfg["head_dim"]
         self.q.copy_(self.q0)
         self.k.copy_(self.k0)
         self.step()
         torch.cuda.synchronize()
         self.ctx.check_device()
-        s = np.unique(np.concatenate([[0, n - 1], np.random.default_rng(7).integers(0, n, rows)]))
+        f16 = self.dt == self.hip.F16
+        npdt = np.float16 if f16 else np.float32
+        rng = np.random.default_rng(7)
+        s = np.unique(np.concatenate([[0, n - 1], rng.integers(0, n, rows)]))
         st = torch.from_numpy(s).cuda()
-        host = lambda t: t[st].cpu().numpy()
-        rb = W.row_bytes(cfg["qtype"], H)
+
+        def host(t, idx=st):
+            return t[idx].cpu().numpy()
+
+        def close(got, want, what, floor=0.0):
+            g, w = got.astype(np.float64), want.astype(np.float64)
+            tol = (2 * np.spacing(np.abs(w).astype(np.float16)).astype(np.float64) if f16
+                   else 1e-5 * np.abs(w)) + floor + 1e-37
+            bad = np.abs(g - w) > tol
+            assert not bad.any(), f"{self.name} n={n} {what}: {bad.sum()} values outside tolerance"
+
+        rb = (18 if cfg["qtype"] == "q4_0" else 34) * H // 32
         sub = self.table.view(cfg["vocab"], rb)[self.ids[st].long()].cpu().numpy().reshape(-1)
-        want = O.embed(sub, O.Q8_0, s.size, H, np.arange(s.size, dtype=np.uint32), 1.0,
-                       out_dtype=np.float16)
-        assert np.array_equal(host(self.emb).view(np.uint16), want.view(np.uint16)), "embed"
-        for x, b, w, xo, h in ((self.x1, self.b1, self.w1, self.xo1, self.h1),
-                               (self.x2, self.b2, self.w2, self.xo2, self.h2)):
-            wx, wh = O.add_rmsnorm(host(x), host(b), w.cpu().numpy(), cfg["eps"])
-            assert np.array_equal(host(xo).view(np.uint16), wx.view(np.uint16)), "x'"
-            g = host(h).astype(np.float64)
-            ulp = np.spacing(np.abs(wh).astype(np.float16)).astype(np.float64)
-            assert np.all(np.abs(g - wh.astype(np.float64)) <= 2 * ulp), "add_rmsnorm"
+        want = O.embed(sub, self.qtype, s.size, H, np.arange(s.size, dtype=np.uint32),
+                       cfg["embd_scale"], out_dtype=npdt)
+        assert np.array_equal(host(self.emb).view(np.uint8), want.view(np.uint8)), "embed"
+        for b in self.norm:
+            x, br = host(b["x"]), host(b["b"])
+            wp = None if b["wp"] is None else b["wp"].cpu().numpy()
+            wx, wh = O.add_rmsnorm(x, br, b["w"].cpu().numpy(), cfg["eps"], w_post=wp)
+            if wp is None:
+                assert np.array_equal(host(b["xo"]).view(np.uint8), wx.view(np.uint8)), "x'"
+                close(host(b["h"]), wh, "h")
+            else:
+                b64 = br.astype(np.float64)
+                fx = 1e-5 * np.abs(b64 / np.sqrt((b64 ** 2).mean(-1, keepdims=True) + cfg["eps"]) * wp)
+                m = np.sqrt((wx.astype(np.float64) ** 2).mean(-1, keepdims=True) + cfg["eps"])
+                close(host(b["xo"]), wx, "sandwich x'", fx)
+                close(host(b["h"]), wh, "sandwich h", fx / m * np.abs(b["w"].cpu().numpy()))
         cos, sin = self.cos.cpu().numpy(), self.sin.cpu().numpy()
-        for t, t0 in ((self.q, self.q0), (self.k, self.k0)):
-            w = O.rope(host(t0), cos, sin, s.astype(np.int32), O.ROPE_NORM)
-            assert np.array_equal(host(t).view(np.uint16), w.view(np.uint16)), "rope"
-        gu = host(self.gu)
-        wa = O.glu(gu[:, :F], gu[:, F:], O.SILU)
-        g = host(self.out).astype(np.float64)
-        ulp = np.spacing(np.abs(wa).astype(np.float16)).astype(np.float64)
-        assert np.all(np.abs(g - wa.astype(np.float64)) <= 2 * ulp + 1e-37), "swiglu"
-        return int(s.size)
+        pos = self.pos[st].cpu().numpy()
+        for t, t0, nw in ((self.q, self.q0, self.qn), (self.k, self.k0, self.kn)):
+            if nw is None:
+                w = O.rope(host(t0), cos, sin, pos, self.kind)
+                assert np.array_equal(host(t).view(np.uint8), w.view(np.uint8)), "rope"
+            else:
+                w = O.rope(host(t0), cos, sin, pos, self.kind, norm_w=nw.cpu().numpy(), eps=cfg["eps"])
+                mag = np.sqrt((w.astype(np.float64) ** 2).sum(-1, keepdims=True) / d)
+                close(host(t), w, "normed rope", 1e-5 * mag)
+        gs = np.unique(np.concatenate([[0, self.rows_glu - 1],
+                                       rng.integers(0, self.rows_glu, rows)]))
+        gst = torch.from_numpy(gs).cuda()
+        if self.offsets is not None:
+            g, u = host(self.gate, gst), host(self.up, gst)
+        else:
+            gu = host(self.gu, gst)
+            g, u = gu[:, :F], gu[:, F:]
+        wa = O.glu(np.ascontiguousarray(g), np.ascontiguousarray(u),
+                   O.GELU_TANH if self.act == self.hip.ACT_GELU_TANH else O.SILU)
+        fl = 2.0 ** -22 * np.abs(0.5 * g.astype(np.float64) * u.astype(np.float64))
+        close(host(self.out, gst), wa, "glu", fl if self.act == self.hip.ACT_GELU_TANH else 0.0)
+        return int(s.size + gs.size)
 
 
 def time_steps(torch, fn, steps, warmup):
@@ -278,7 +343,8 @@ def cpu_baseline(seconds=10.0, n=64):
     cos, sin = O.rope_tables(d, cfg["theta"], n)
     pos = np.arange(n, dtype=np.int32)
     gu = rng.standard_normal((n, 2 * F)).astype(f16)
-    step_bytes = sum(op_bytes(op_kind(name), n, 2) for name in STEP_OPS)
+    step_bytes = (n * (34 * H // 32 + 4 + 2 * H) + 2 * (n * 8 * H + 4 * H)
+                  + n * (4 * (nq + nk) * d + 4 * d) + n * 6 * F)
 
     def step():
         O.embed(table, O.Q8_0, vocab, H, ids, 1.0, out_dtype=f16, threads=threads)
@@ -323,6 +389,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-large", action="store_true", help="skip the 16384-token step")
+    ap.add_argument("--no-configs", action="store_true", help="skip the A/B/D/E config steps")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: these ops run on one GPU's share of the work and "
@@ -342,9 +409,19 @@ def main():
     ctx = hip.Context(0)
     ctx.set_stream(stream.cuda_stream)
 
-    def run_size(n, steps, warmup):
-        log(f"prefill step buffers, {n} tokens")
-        st = PrefillStep(ctx, torch, n)
+    # A plain streaming kernel of known size, for context and as the
+    # reference reading of the HBM counters (FETCH_SIZE / WRITE_SIZE): torch's
+    # elementwise negation of 256 MiB of f16 reads 256 MiB and writes 256 MiB.
+    cal_n = (256 << 20) // 2
+    cal_src = torch.ones(cal_n, device="cuda", dtype=torch.float16)
+    cal_dst = torch.empty_like(cal_src)
+    cal_ms = time_steps(torch, lambda: torch.neg(cal_src, out=cal_dst), 10, 3)
+    copy_gbs = 2 * cal_n * 2 / (cal_ms / 1e3) / 1e9
+    del cal_src, cal_dst
+
+    def run_size(n, steps, warmup, name="C", dtype="f16"):
+        log(f"config {name}: step buffers, {n} tokens, {dtype}")
+        st = LayerStep(ctx, torch, name, n, dtype)
         torch.cuda.synchronize()
         log("timed steps (unprofiled)")
         ms_plain = time_steps(torch, st.step, steps, warmup)
@@ -357,7 +434,7 @@ def main():
                           frac=round(st.bytes[name] / (t / 1e3) / 1e9 / HBM_PEAK_GBS, 4))
                for name, (k, t) in per.items()}
         log("verify sampled rows against the oracle")
-        rows = st.verify(torch)
+        rows = st.verify()
         step_bytes = sum(st.bytes.values())
         del st
         torch.cuda.empty_cache()
@@ -365,7 +442,7 @@ def main():
 
     ms_prof, step_bytes, ops, checked_rows, ms = run_size(args.tokens, args.steps, args.warmup)
     value = step_bytes / (ms / 1e3) / 1e9
-    glu = ops["swiglu"]
+    glu = ops["glu"]
     big = None
     if args.tokens != 16384 and not args.no_large:
         _, bytes_l, ops_l, rows_l, ms_l = run_size(16384, max(5, args.steps // 4), 3)
@@ -373,6 +450,19 @@ def main():
         big = dict(tokens=16384, us_per_step=round(ms_l * 1000, 1),
                    gbs=round(bytes_l / (ms_l / 1e3) / 1e9, 1),
                    frac=round(bytes_l / (ms_l / 1e3) / 1e9 / HBM_PEAK_GBS, 4), ops=ops_l)
+
+    configs = None
+    if not args.no_configs:
+        # every workload config's own step (per-op kernel GB/s); configs[1]
+        # and [2] are Llama-3-8B (B at batch 32 here, C above)
+        configs = {}
+        for name, n, dtype in (("A", 128, "f32"), ("B", 32, "f32"), ("D", 8, "f32"),
+                               ("D", 2048, "f16"), ("E", 64, "f32"), ("E", 8192, "f16")):
+            _, b_c, ops_c, rows_c, ms_c = run_size(n, 20, 5, name, dtype)
+            checked_rows += rows_c
+            configs[f"{name}_{n}_{dtype}"] = dict(
+                us_per_step=round(ms_c * 1000, 2), gbs=round(b_c / (ms_c / 1e3) / 1e9, 1),
+                frac=round(b_c / (ms_c / 1e3) / 1e9 / HBM_PEAK_GBS, 4), ops=ops_c)
 
     decode = None
     if not args.no_decode:
@@ -408,9 +498,11 @@ def main():
                    "tokens": args.tokens, "hidden": 4096, "ff": 14336, "heads": "32q/8k x 128",
                    "activations": "f16 (decode: f32)", "bytes_per_step": step_bytes},
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),
+        "copy_gbs": round(copy_gbs, 1),
         "verified_rows": checked_rows,
         "ops": ops,
         "prefill_16384": big,
+        "configs": configs,
         "decode_us_per_layer": decode,
         "roofline": {"kernel": glu["kernel"], "bound": "hbm",
                      "achieved": glu["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -108,6 +108,16 @@ __device__ static inline float block_sum(float v, float *red) {
     return s;
 }
 
+// MI355X places workgroup p on XCD p % 8, and each of the 8 XCDs has its own
+// L2.  Renumbering so that XCD x runs one contiguous range of logical
+// blocks keeps the data neighbouring blocks share (a RoPE table row read by
+// every head of a token) in one L2 instead of fetching it once per XCD.
+// A bijection on [0, gridDim.x) for any grid size.
+__device__ static inline uint32_t xcd_block() {
+    const uint32_t n = gridDim.x, p = blockIdx.x, x = p & 7u, q = n >> 3, r = n & 7u;
+    return x * q + (x < r ? x : r) + (p >> 3);
+}
+
 // Record (row, value) of a bad input in a status word, keeping the
 // smallest row (global atomic, vector memory path).
 __device__ static inline void record_bad(unsigned long long *word, uint32_t row, uint32_t value) {

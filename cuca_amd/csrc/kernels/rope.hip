@@ -8,13 +8,11 @@
 // of every row, in the projection's own [rows, heads, head_dim] layout
 // (row stride q_ld / k_ld, so Q and K may sit inside a fused QKV buffer).
 //
-// Vector kernel: a head is handled by TPH = head_dim / (2 * VP) lanes, VP
-// values per 16-byte chunk (4 f32, 8 f16); every lane owns 2 * VP values:
-//   NEOX: values i .. i+VP and their partners i+n/2 .. i+n/2+VP,
-//   NORM: 2 * VP adjacent values = VP (2i, 2i+1) pairs,
-// plus pass-through chunks past n_dims.  The cos/sin row of the position
-// (n_dims / 2 f32) is shared by all heads of the row and stays in cache.
-// The QK-norm sum is a butterfly over the head's TPH lanes.
+// Vector kernel: a head is handled by TPH lanes, each owning whole 16-byte
+// chunks (VP = 4 f32 or 8 f16 values; the layouts are described at
+// rope_body).  The cos/sin row of the position (n_dims / 2 f32) is shared by
+// all heads of the row and stays in cache.  The QK-norm sum is a butterfly
+// over the head's TPH lanes.
 //
 // a' = a*c - b*s, b' = a*s + b*c with separately rounded products
 // (-ffp-contract=off, and the pragma below): without the norm the result is
@@ -27,22 +25,40 @@
 
 #pragma clang fp contract(off)
 
-template <int VP>
-__device__ static inline void load_tab(const float *t, int64_t first, float (&v)[VP]) {
-    const f32x4 *p = reinterpret_cast<const f32x4 *>(t + first);
+// `n` consecutive f32 of a table (n = 2, 4 or 8; 8-byte aligned for 2,
+// 16-byte aligned otherwise).
+template <int n>
+__device__ static inline void load_tab(const float *t, int64_t first, float (&v)[n]) {
+    if constexpr (n == 2) {
+        const float2 x = *reinterpret_cast<const float2 *>(t + first);
+        v[0] = x.x; v[1] = x.y;
+    } else {
+        const f32x4 *p = reinterpret_cast<const f32x4 *>(t + first);
 #pragma unroll
-    for (int j = 0; j < VP / 4; j++) {
-        f32x4 x = p[j];
-        v[4 * j] = x.x; v[4 * j + 1] = x.y; v[4 * j + 2] = x.z; v[4 * j + 3] = x.w;
+        for (int j = 0; j < n / 4; j++) {
+            f32x4 x = p[j];
+            v[4 * j] = x.x; v[4 * j + 1] = x.y; v[4 * j + 2] = x.z; v[4 * j + 3] = x.w;
+        }
     }
 }
 
+// Lane layout (TPH lanes per head, VP values per 16-byte chunk):
+//   NEOX: TPH = head_dim / (2 VP); lane u owns chunk u of the first half and
+//         its partner chunk u + n/(2 VP) (values i and i + n/2), or two
+//         pass-through chunks past n_dims -- both of a wave's load
+//         instructions cover contiguous bytes;
+//   NORM: TPH = head_dim / VP; lane u owns chunk u, i.e. VP/2 whole (2i,
+//         2i+1) pairs (or a pass-through chunk) -- one contiguous chunk per
+//         lane.  (Two adjacent chunks per lane measured 74 % of peak at 16384
+//         f16 rows against 80 % for this layout: each load instruction then
+//         touched every other chunk.)
 template <typename T, int KIND, bool NORM>
 __device__ static inline void rope_body(const RopeArgs &a) {
     constexpr int VP = Chunk<T>::N;
+    constexpr int NC = KIND == 2 ? 2 : 1; // chunks per lane
     const int tl = a.tph_log2;
     const int tph = 1 << tl;
-    const uint32_t gh = blockIdx.x * (uint32_t)(CUCA_BLOCK >> tl) + (threadIdx.x >> tl);
+    const uint32_t gh = xcd_block() * (uint32_t)(CUCA_BLOCK >> tl) + (threadIdx.x >> tl);
     const int u = threadIdx.x & (tph - 1);
     const uint32_t heads = (uint32_t)(a.nq + a.nk);
     bool live = gh < (uint32_t)a.rows * heads;
@@ -60,85 +76,83 @@ __device__ static inline void rope_body(const RopeArgs &a) {
     const float *nw = isq ? a.q_norm_w : a.k_norm_w;
     const int half = a.n_dims >> 1;
 
-    // This lane's two chunks (element offsets ia and ib within the head).
-    int ia, ib;
+    // This lane's chunks: element offsets e[0] (and e[1] for NEOX).
+    int e[NC];
     bool rot;
     if (KIND == 2) {
         const int nr = half / VP;
         if (u < nr) {
-            ia = u * VP; ib = ia + half; rot = true;
+            e[0] = u * VP; e[NC - 1] = e[0] + half; rot = true;
         } else {
-            ia = a.n_dims + (u - nr) * 2 * VP; ib = ia + VP; rot = false;
+            e[0] = a.n_dims + (u - nr) * 2 * VP; e[NC - 1] = e[0] + VP; rot = false;
         }
     } else {
-        ia = u * 2 * VP; ib = ia + VP; rot = ia < a.n_dims;
+        e[0] = u * VP; rot = e[0] < a.n_dims;
     }
-    float va[VP], vb[VP];
-    if (live) {
-        Chunk<T>::load(base, ia / VP, va);
-        Chunk<T>::load(base, ib / VP, vb);
-    } else {
+    float v[NC][VP];
 #pragma unroll
-        for (int i = 0; i < VP; i++) va[i] = vb[i] = 0.0f;
+    for (int k = 0; k < NC; k++) {
+        if (live) {
+            Chunk<T>::load(base, e[k] / VP, v[k]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < VP; i++) v[k][i] = 0.0f;
+        }
     }
     if (NORM) {
         float ss = 0.0f;
 #pragma unroll
-        for (int i = 0; i < VP; i++) ss += va[i] * va[i];
+        for (int k = 0; k < NC; k++)
 #pragma unroll
-        for (int i = 0; i < VP; i++) ss += vb[i] * vb[i];
+            for (int i = 0; i < VP; i++) ss += v[k][i] * v[k][i];
         ss = group_sum_rt(ss, tph);
         if (nw) {
-            const float m = sqrtf(ss / (float)D + a.eps);
-            float wa[VP], wb[VP];
-            load_tab<VP>(nw, ia, wa);
-            load_tab<VP>(nw, ib, wb);
+            // the norm kernel's reciprocal form, x * (1 / sqrt(mean + eps)) * w
+            const float inv = 1.0f / sqrtf(ss / (float)D + a.eps);
 #pragma unroll
-            for (int i = 0; i < VP; i++) {
-                va[i] = va[i] / m * wa[i];
-                vb[i] = vb[i] / m * wb[i];
+            for (int k = 0; k < NC; k++) {
+                float w[VP];
+                load_tab<VP>(nw, e[k], w);
+#pragma unroll
+                for (int i = 0; i < VP; i++) v[k][i] = v[k][i] * inv * w[i];
             }
         }
     }
     if (!live) return;
     if (rot) {
-        float c[VP], s[VP];
         const int64_t trow = (int64_t)pos * half;
         if (KIND == 2) {
-            load_tab<VP>(a.cos_t, trow + ia, c);
-            load_tab<VP>(a.sin_t, trow + ia, s);
+            float c[VP], s[VP];
+            load_tab<VP>(a.cos_t, trow + e[0], c);
+            load_tab<VP>(a.sin_t, trow + e[0], s);
 #pragma unroll
             for (int i = 0; i < VP; i++) {
-                const float x0 = va[i], x1 = vb[i];
-                va[i] = x0 * c[i] - x1 * s[i];
-                vb[i] = x0 * s[i] + x1 * c[i];
+                const float x0 = v[0][i], x1 = v[NC - 1][i];
+                v[0][i] = x0 * c[i] - x1 * s[i];
+                v[NC - 1][i] = x0 * s[i] + x1 * c[i];
             }
         } else {
-            load_tab<VP>(a.cos_t, trow + (ia >> 1), c);
-            load_tab<VP>(a.sin_t, trow + (ia >> 1), s);
-            float w[2 * VP];
+            float c[VP / 2], s[VP / 2];
+            load_tab<VP / 2>(a.cos_t, trow + (e[0] >> 1), c);
+            load_tab<VP / 2>(a.sin_t, trow + (e[0] >> 1), s);
 #pragma unroll
-            for (int i = 0; i < VP; i++) { w[i] = va[i]; w[VP + i] = vb[i]; }
-#pragma unroll
-            for (int j = 0; j < VP; j++) {
-                const float x0 = w[2 * j], x1 = w[2 * j + 1];
-                w[2 * j] = x0 * c[j] - x1 * s[j];
-                w[2 * j + 1] = x0 * s[j] + x1 * c[j];
+            for (int j = 0; j < VP / 2; j++) {
+                const float x0 = v[0][2 * j], x1 = v[0][2 * j + 1];
+                v[0][2 * j] = x0 * c[j] - x1 * s[j];
+                v[0][2 * j + 1] = x0 * s[j] + x1 * c[j];
             }
-#pragma unroll
-            for (int i = 0; i < VP; i++) { va[i] = w[i]; vb[i] = w[VP + i]; }
         }
     } else if (!NORM || !nw) {
         return; // pass-through values are left untouched
     }
-    Chunk<T>::store(base, ia / VP, va);
-    Chunk<T>::store(base, ib / VP, vb);
+#pragma unroll
+    for (int k = 0; k < NC; k++) Chunk<T>::store(base, e[k] / VP, v[k]);
 }
 
 template <typename T>
 __device__ static inline void rope_generic_body(const RopeArgs &a) {
     const int lane = threadIdx.x & (CUCA_WAVE - 1);
-    const uint32_t gh = blockIdx.x * (uint32_t)(CUCA_BLOCK / CUCA_WAVE) + threadIdx.x / CUCA_WAVE;
+    const uint32_t gh = xcd_block() * (uint32_t)(CUCA_BLOCK / CUCA_WAVE) + threadIdx.x / CUCA_WAVE;
     const uint32_t heads = (uint32_t)(a.nq + a.nk);
     if (gh >= (uint32_t)a.rows * heads) return; // whole wave
     const uint32_t row = gh / heads;
@@ -153,7 +167,7 @@ __device__ static inline void rope_generic_body(const RopeArgs &a) {
     T *base = isq ? reinterpret_cast<T *>(a.q) + (int64_t)row * a.q_ld + (int64_t)h * D
                   : reinterpret_cast<T *>(a.k) + (int64_t)row * a.k_ld + (int64_t)(h - a.nq) * D;
     const float *nw = isq ? a.q_norm_w : a.k_norm_w;
-    float m = 1.0f;
+    float inv = 1.0f;
     if (nw) {
         float ss = 0.0f;
         for (int e = lane; e < D; e += CUCA_WAVE) {
@@ -161,7 +175,7 @@ __device__ static inline void rope_generic_body(const RopeArgs &a) {
             ss += v * v;
         }
         ss = group_sum<CUCA_WAVE>(ss);
-        m = sqrtf(ss / (float)D + a.eps);
+        inv = 1.0f / sqrtf(ss / (float)D + a.eps);
     }
     const int half = a.n_dims >> 1;
     const float *cs = a.cos_t + (int64_t)pos * half;
@@ -173,15 +187,15 @@ __device__ static inline void rope_generic_body(const RopeArgs &a) {
         const int eb = a.kind == 2 ? i + half : 2 * i + 1;
         float x0 = load1<T>(base, ea), x1 = load1<T>(base, eb);
         if (nw) {
-            x0 = x0 / m * nw[ea];
-            x1 = x1 / m * nw[eb];
+            x0 = x0 * inv * nw[ea];
+            x1 = x1 * inv * nw[eb];
         }
         store1<T>(base, ea, x0 * cs[i] - x1 * sn[i]);
         store1<T>(base, eb, x0 * sn[i] + x1 * cs[i]);
     }
     if (nw) {
         for (int e = a.n_dims + lane; e < D; e += CUCA_WAVE)
-            store1<T>(base, e, load1<T>(base, e) / m * nw[e]);
+            store1<T>(base, e, load1<T>(base, e) * inv * nw[e]);
     }
 }
 

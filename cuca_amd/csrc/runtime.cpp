@@ -592,9 +592,13 @@ cuca_status cuca_hip_rope(cuca_hip_ctx *ctx, void *q, int64_t q_ld, void *k, int
     a.eps = eps;
     a.kind = (int32_t)kind;
     ctx->last_table_rows = table_rows;
-    const int tph = head_dim / (2 * VP);
+    // lanes per head: NEOX pairs chunk u with chunk u + n/(2 VP) (two per
+    // lane); NORM gives each lane one chunk of whole (2i, 2i+1) pairs
+    const bool neox_k = kind == CUCA_ROPE_NEOX;
+    const int per_lane = neox_k ? 2 * VP : VP;
+    const int tph = head_dim / per_lane;
     const bool pow2 = tph > 0 && (tph & (tph - 1)) == 0 && tph <= 64;
-    const bool vec = head_dim % (2 * VP) == 0 && n_dims % (2 * VP) == 0 && pow2 &&
+    const bool vec = head_dim % per_lane == 0 && n_dims % (2 * VP) == 0 && pow2 &&
                      (nq == 0 || (al16(q) && (q_ld * es) % 16 == 0)) &&
                      (nk == 0 || (al16(k) && (k_ld * es) % 16 == 0)) && al16(cos) && al16(sin) &&
                      (!q_norm_w || al16(q_norm_w)) && (!k_norm_w || al16(k_norm_w));
