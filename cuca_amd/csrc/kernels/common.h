@@ -42,6 +42,16 @@ template <> struct Chunk<float> {
     }
     // The value the activation type holds for v (identity for f32).
     __device__ static inline float as_stored(float v) { return v; }
+    // The chunk's raw 16 bytes, and their values.
+    __device__ static inline u32x4 load_raw(const void *base, int64_t chunk) {
+        return reinterpret_cast<const u32x4 *>(base)[chunk];
+    }
+    // (The whole vector is cast: __builtin_bit_cast(float, r.y) of one
+    // element compiled to a read of element 0.)
+    __device__ static inline void widen(u32x4 r, float (&v)[4]) {
+        const f32x4 t = __builtin_bit_cast(f32x4, r);
+        v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+    }
 };
 
 template <> struct Chunk<_Float16> {
@@ -63,6 +73,14 @@ template <> struct Chunk<_Float16> {
         reinterpret_cast<f16x8 *>(base)[chunk] = t;
     }
     __device__ static inline float as_stored(float v) { return (float)(_Float16)v; }
+    __device__ static inline u32x4 load_raw(const void *base, int64_t chunk) {
+        return reinterpret_cast<const u32x4 *>(base)[chunk];
+    }
+    __device__ static inline void widen(u32x4 r, float (&v)[8]) {
+        const f16x8 t = __builtin_bit_cast(f16x8, r);
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = (float)t[i];
+    }
 };
 
 // Load chunk `c` of `base`, streaming (NT) or cached.
@@ -106,16 +124,6 @@ __device__ static inline float block_sum(float v, float *red) {
     float s = 0.0f;
     for (int i = 0; i < nw; i++) s += red[i];
     return s;
-}
-
-// MI355X places workgroup p on XCD p % 8, and each of the 8 XCDs has its own
-// L2.  Renumbering so that XCD x runs one contiguous range of logical
-// blocks keeps the data neighbouring blocks share (a RoPE table row read by
-// every head of a token) in one L2 instead of fetching it once per XCD.
-// A bijection on [0, gridDim.x) for any grid size.
-__device__ static inline uint32_t xcd_block() {
-    const uint32_t n = gridDim.x, p = blockIdx.x, x = p & 7u, q = n >> 3, r = n & 7u;
-    return x * q + (x < r ? x : r) + (p >> 3);
 }
 
 // Record (row, value) of a bad input in a status word, keeping the

@@ -27,6 +27,16 @@
 
 // `n` consecutive f32 of a table (n = 2, 4 or 8; 8-byte aligned for 2,
 // 16-byte aligned otherwise).
+// Empty asm on loaded registers: the loads must complete before this point
+// and cannot be sunk past it (emits no instruction, only a wait).
+template <int n>
+__device__ static inline void pin(float (&v)[n]) {
+#pragma unroll
+    for (int i = 0; i < n; i++) asm volatile("" : "+v"(v[i]));
+}
+
+__device__ static inline void pin(u32x4 &r) { asm volatile("" : "+v"(r)); }
+
 template <int n>
 __device__ static inline void load_tab(const float *t, int64_t first, float (&v)[n]) {
     if constexpr (n == 2) {
@@ -55,20 +65,16 @@ __device__ static inline void load_tab(const float *t, int64_t first, float (&v)
 template <typename T, int KIND, bool NORM>
 __device__ static inline void rope_body(const RopeArgs &a) {
     constexpr int VP = Chunk<T>::N;
-    constexpr int NC = KIND == 2 ? 2 : 1; // chunks per lane
+    constexpr int NC = KIND == 2 ? 2 : 1;       // chunks per lane
+    constexpr int NT = KIND == 2 ? VP : VP / 2; // cos/sin entries per lane
     const int tl = a.tph_log2;
     const int tph = 1 << tl;
-    const uint32_t gh = xcd_block() * (uint32_t)(CUCA_BLOCK >> tl) + (threadIdx.x >> tl);
+    const uint32_t gh = blockIdx.x * (uint32_t)(CUCA_BLOCK >> tl) + (threadIdx.x >> tl);
     const int u = threadIdx.x & (tph - 1);
     const uint32_t heads = (uint32_t)(a.nq + a.nk);
-    bool live = gh < (uint32_t)a.rows * heads;
+    const bool live = gh < (uint32_t)a.rows * heads;
     const uint32_t row = live ? gh / heads : 0;
     const int h = live ? (int)(gh - row * heads) : 0;
-    const int32_t pos = live ? a.pos[row] : 0;
-    if (live && (pos < 0 || (int64_t)pos >= a.table_rows)) {
-        if (u == 0 && h == 0) record_bad(a.status + CUCA_STATUS_ROPE_POS, row, (uint32_t)pos);
-        live = false;
-    }
     const bool isq = h < a.nq;
     const int D = a.head_dim;
     T *base = isq ? reinterpret_cast<T *>(a.q) + (int64_t)row * a.q_ld + (int64_t)h * D
@@ -89,70 +95,88 @@ __device__ static inline void rope_body(const RopeArgs &a) {
     } else {
         e[0] = u * VP; rot = e[0] < a.n_dims;
     }
+    // Every load is issued up front and unconditionally, from addresses that
+    // are always valid (a lane past the last head reads row 0, a position
+    // outside the table or a pass-through lane reads table entry 0, a head
+    // without norm weights reads the other projection's), and pinned there
+    // by an empty asm on the loaded registers: the position, the head's
+    // chunks, the cos/sin entries and the norm weights are all in flight
+    // together.  Left to itself the compiler sinks the table loads into the
+    // predicated store's branch, behind a wait for the chunks (56-63 us
+    // against 53.5 us per 16384 f16 rows of 40 heads).
+    const int32_t pos = a.pos[row];
+    u32x4 raw[NC];
+#pragma unroll
+    for (int k = 0; k < NC; k++) raw[k] = Chunk<T>::load_raw(base, e[k] / VP);
+    const bool pos_ok = pos >= 0 && (int64_t)pos < a.table_rows;
+    const int64_t t0 = (rot && pos_ok) ? (int64_t)pos * half + (KIND == 2 ? e[0] : (e[0] >> 1)) : 0;
+    float c[NT], s[NT];
+    load_tab<NT>(a.cos_t, t0, c);
+    load_tab<NT>(a.sin_t, t0, s);
+    float w[NC][VP];
+    if (NORM) {
+        // the launch picks a _qkn kernel only when one of the two is set
+        const float *wp = nw ? nw : (isq ? a.k_norm_w : a.q_norm_w);
+#pragma unroll
+        for (int k = 0; k < NC; k++) load_tab<VP>(wp, e[k], w[k]);
+    }
+    __builtin_amdgcn_sched_barrier(0); // every load above is issued first
+    pin(c);
+    pin(s);
     float v[NC][VP];
 #pragma unroll
     for (int k = 0; k < NC; k++) {
-        if (live) {
-            Chunk<T>::load(base, e[k] / VP, v[k]);
-        } else {
-#pragma unroll
-            for (int i = 0; i < VP; i++) v[k][i] = 0.0f;
-        }
+        pin(raw[k]);
+        Chunk<T>::widen(raw[k], v[k]);
     }
     if (NORM) {
+#pragma unroll
+        for (int k = 0; k < NC; k++) pin(w[k]);
         float ss = 0.0f;
 #pragma unroll
         for (int k = 0; k < NC; k++)
 #pragma unroll
             for (int i = 0; i < VP; i++) ss += v[k][i] * v[k][i];
         ss = group_sum_rt(ss, tph);
-        if (nw) {
-            // the norm kernel's reciprocal form, x * (1 / sqrt(mean + eps)) * w
-            const float inv = 1.0f / sqrtf(ss / (float)D + a.eps);
+        // the norm kernel's reciprocal form, x * (1 / sqrt(mean + eps)) * w
+        const float inv = 1.0f / sqrtf(ss / (float)D + a.eps);
 #pragma unroll
-            for (int k = 0; k < NC; k++) {
-                float w[VP];
-                load_tab<VP>(nw, e[k], w);
+        for (int k = 0; k < NC; k++)
 #pragma unroll
-                for (int i = 0; i < VP; i++) v[k][i] = v[k][i] * inv * w[i];
-            }
+            for (int i = 0; i < VP; i++) v[k][i] = nw ? v[k][i] * inv * w[k][i] : v[k][i];
+    }
+    // The rotation is computed on every lane and selected.
+    if (KIND == 2) {
+#pragma unroll
+        for (int i = 0; i < VP; i++) {
+            const float x0 = v[0][i], x1 = v[NC - 1][i];
+            const float r0 = x0 * c[i] - x1 * s[i];
+            const float r1 = x0 * s[i] + x1 * c[i];
+            v[0][i] = rot ? r0 : x0;
+            v[NC - 1][i] = rot ? r1 : x1;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < VP / 2; j++) {
+            const float x0 = v[0][2 * j], x1 = v[0][2 * j + 1];
+            const float r0 = x0 * c[j] - x1 * s[j];
+            const float r1 = x0 * s[j] + x1 * c[j];
+            v[0][2 * j] = rot ? r0 : x0;
+            v[0][2 * j + 1] = rot ? r1 : x1;
         }
     }
-    if (!live) return;
-    if (rot) {
-        const int64_t trow = (int64_t)pos * half;
-        if (KIND == 2) {
-            float c[VP], s[VP];
-            load_tab<VP>(a.cos_t, trow + e[0], c);
-            load_tab<VP>(a.sin_t, trow + e[0], s);
+    if (live && pos_ok && (rot || (NORM && nw))) {
 #pragma unroll
-            for (int i = 0; i < VP; i++) {
-                const float x0 = v[0][i], x1 = v[NC - 1][i];
-                v[0][i] = x0 * c[i] - x1 * s[i];
-                v[NC - 1][i] = x0 * s[i] + x1 * c[i];
-            }
-        } else {
-            float c[VP / 2], s[VP / 2];
-            load_tab<VP / 2>(a.cos_t, trow + (e[0] >> 1), c);
-            load_tab<VP / 2>(a.sin_t, trow + (e[0] >> 1), s);
-#pragma unroll
-            for (int j = 0; j < VP / 2; j++) {
-                const float x0 = v[0][2 * j], x1 = v[0][2 * j + 1];
-                v[0][2 * j] = x0 * c[j] - x1 * s[j];
-                v[0][2 * j + 1] = x0 * s[j] + x1 * c[j];
-            }
-        }
-    } else if (!NORM || !nw) {
-        return; // pass-through values are left untouched
+        for (int k = 0; k < NC; k++) Chunk<T>::store(base, e[k] / VP, v[k]);
     }
-#pragma unroll
-    for (int k = 0; k < NC; k++) Chunk<T>::store(base, e[k] / VP, v[k]);
+    if (live && !pos_ok && u == 0 && h == 0)
+        record_bad(a.status + CUCA_STATUS_ROPE_POS, row, (uint32_t)pos);
 }
 
 template <typename T>
 __device__ static inline void rope_generic_body(const RopeArgs &a) {
     const int lane = threadIdx.x & (CUCA_WAVE - 1);
-    const uint32_t gh = xcd_block() * (uint32_t)(CUCA_BLOCK / CUCA_WAVE) + threadIdx.x / CUCA_WAVE;
+    const uint32_t gh = blockIdx.x * (uint32_t)(CUCA_BLOCK / CUCA_WAVE) + threadIdx.x / CUCA_WAVE;
     const uint32_t heads = (uint32_t)(a.nq + a.nk);
     if (gh >= (uint32_t)a.rows * heads) return; // whole wave
     const uint32_t row = gh / heads;

@@ -611,6 +611,7 @@ cuca_status cuca_hip_rope(cuca_hip_ctx *ctx, void *q, int64_t q_ld, void *k, int
     int lg = 0;
     while ((1 << lg) < tph) lg++;
     a.tph_log2 = lg;
+
     Kernel kk = f16 ? (neox ? (norm ? cuca_rope_f16_neox_qkn : cuca_rope_f16_neox)
                             : (norm ? cuca_rope_f16_norm_qkn : cuca_rope_f16_norm))
                     : (neox ? (norm ? cuca_rope_f32_neox_qkn : cuca_rope_f32_neox)

@@ -87,12 +87,3 @@ def test_ops_validate_on_the_host_before_any_device_work():
     with pytest.raises(hip.CucaError, match="do not hold 2 rows"):
         ops.TokenEmbedding(None, hip.GGML_Q4_0, np.zeros(18, np.uint8), 2, 32)
 
-
-def test_xcd_block_renumbering_is_a_bijection():
-    # common.h xcd_block(): workgroup p runs logical block
-    # x*q + min(x, r) + p/8 with x = p % 8, q = n / 8, r = n % 8
-    src = open(os.path.join(ROOT, "cuca_amd", "csrc", "kernels", "common.h")).read()
-    assert "return x * q + (x < r ? x : r) + (p >> 3);" in src
-    for n in list(range(1, 80)) + [5120, 5121, 8191]:
-        got = sorted((p & 7) * (n >> 3) + min(p & 7, n & 7) + (p >> 3) for p in range(n))
-        assert got == list(range(n)), n
