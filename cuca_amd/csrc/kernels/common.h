@@ -40,6 +40,17 @@ template <> struct Chunk<float> {
         f32x4 t = {v[0], v[1], v[2], v[3]};
         reinterpret_cast<f32x4 *>(base)[chunk] = t;
     }
+    // Streaming store (nontemporal hint): the vector kernels write every
+    // output this way.  Their outputs are read by a different kernel (a
+    // GEMM, the next layer), not by the next instructions; kept in the
+    // caches they would be written back to HBM during that next kernel and
+    // slow it.  Measured on MI355X over the five-op prefill step of the
+    // Llama-3-8B shapes: 154 -> 147 us at 4096 tokens, 550 -> 513 us at
+    // 16384; decode-graph latency unchanged.
+    __device__ static inline void store_nt(void *base, int64_t chunk, const float (&v)[4]) {
+        f32x4 t = {v[0], v[1], v[2], v[3]};
+        __builtin_nontemporal_store(t, reinterpret_cast<f32x4 *>(base) + chunk);
+    }
     // The value the activation type holds for v (identity for f32).
     __device__ static inline float as_stored(float v) { return v; }
     // The chunk's raw 16 bytes, and their values.
@@ -71,6 +82,12 @@ template <> struct Chunk<_Float16> {
 #pragma unroll
         for (int i = 0; i < 8; i++) t[i] = (_Float16)v[i];
         reinterpret_cast<f16x8 *>(base)[chunk] = t;
+    }
+    __device__ static inline void store_nt(void *base, int64_t chunk, const float (&v)[8]) {
+        f16x8 t;
+#pragma unroll
+        for (int i = 0; i < 8; i++) t[i] = (_Float16)v[i];
+        __builtin_nontemporal_store(t, reinterpret_cast<f16x8 *>(base) + chunk);
     }
     __device__ static inline float as_stored(float v) { return (float)(_Float16)v; }
     __device__ static inline u32x4 load_raw(const void *base, int64_t chunk) {

@@ -68,7 +68,7 @@ __device__ static inline void glu_body(const GluArgs &a) {
     }
 #pragma unroll
     for (int i = 0; i < N; i++) o[i] = act_fn<ACT>(g[i]) * u[i];
-    Chunk<T>::store(reinterpret_cast<T *>(a.out) + (int64_t)row * a.out_ld, c, o);
+    Chunk<T>::store_nt(reinterpret_cast<T *>(a.out) + (int64_t)row * a.out_ld, c, o);
 }
 
 // Any shape or alignment: one element per thread.

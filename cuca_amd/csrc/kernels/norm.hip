@@ -122,7 +122,7 @@ __device__ static inline void norm_body(const NormArgs &a) {
 #pragma unroll
         for (int k = 0; k < NCH; k++) {
             const int c = li + k * TPR;
-            if (c < nch) Chunk<T>::store(a.x_out, cb + c, v[k]);
+            if (c < nch) Chunk<T>::store_nt(a.x_out, cb + c, v[k]);
         }
     }
     float ss = 0.0f;
@@ -148,7 +148,7 @@ __device__ static inline void norm_body(const NormArgs &a) {
 #pragma unroll
                 for (int i = 0; i < N; i++) h[i] = v[k][i] * inv;
             }
-            Chunk<T>::store(a.h_out, cb + c, h);
+            Chunk<T>::store_nt(a.h_out, cb + c, h);
         }
     }
 }

@@ -167,7 +167,7 @@ __device__ static inline void rope_body(const RopeArgs &a) {
     }
     if (live && pos_ok && (rot || (NORM && nw))) {
 #pragma unroll
-        for (int k = 0; k < NC; k++) Chunk<T>::store(base, e[k] / VP, v[k]);
+        for (int k = 0; k < NC; k++) Chunk<T>::store_nt(base, e[k] / VP, v[k]);
     }
     if (live && !pos_ok && u == 0 && h == 0)
         record_bad(a.status + CUCA_STATUS_ROPE_POS, row, (uint32_t)pos);

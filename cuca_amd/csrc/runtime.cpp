@@ -335,8 +335,15 @@ cuca_status cuca_hip_embed_gguf(cuca_hip_ctx *ctx, const void *table, uint32_t g
     if (hidden > (1 << 28)) return fail(ctx, CUCA_UNSUPPORTED, "hidden size %lld too large", (long long)hidden);
     if (reinterpret_cast<uintptr_t>(table) & 1u) return fail(ctx, CUCA_INVALID_ARG, "table must be 2-byte aligned");
     const bool f16 = out_dtype == CUCA_F16;
-    const Kernel k = ggml_type == CUCA_GGML_Q4_0 ? (f16 ? cuca_embed_q4_0_f16 : cuca_embed_q4_0_f32)
-                                                 : (f16 ? cuca_embed_q8_0_f16 : cuca_embed_q8_0_f32);
+    // a wave per token, lane units of 8 values, up to 8 units per lane per round
+    const int64_t per_lane = (hidden / 8 + 63) / 64;
+    const int ui = per_lane <= 1 ? 0 : per_lane <= 2 ? 1 : per_lane <= 4 ? 2 : 3;
+    static const Kernel table_k[2][2][4] = {
+        {{cuca_embed_q4_0_f32_u1, cuca_embed_q4_0_f32_u2, cuca_embed_q4_0_f32_u4, cuca_embed_q4_0_f32_u8},
+         {cuca_embed_q4_0_f16_u1, cuca_embed_q4_0_f16_u2, cuca_embed_q4_0_f16_u4, cuca_embed_q4_0_f16_u8}},
+        {{cuca_embed_q8_0_f32_u1, cuca_embed_q8_0_f32_u2, cuca_embed_q8_0_f32_u4, cuca_embed_q8_0_f32_u8},
+         {cuca_embed_q8_0_f16_u1, cuca_embed_q8_0_f16_u2, cuca_embed_q8_0_f16_u4, cuca_embed_q8_0_f16_u8}}};
+    const Kernel k = table_k[ggml_type == CUCA_GGML_Q8_0][f16][ui];
     EmbedArgs a{};
     a.table = static_cast<const uint8_t *>(table);
     a.ids = ids;
@@ -348,10 +355,7 @@ cuca_status cuca_hip_embed_gguf(cuca_hip_ctx *ctx, const void *table, uint32_t g
     a.n = (int32_t)n;
     a.scale = scale;
     ctx->last_vocab = vocab;
-    const int64_t nch = hidden / chunk_elems(out_dtype);
-    int64_t threads = (nch + 63) / 64 * 64;
-    if (threads > 256) threads = 256;
-    return launch(ctx, k, (unsigned)n, (unsigned)threads, 0, a);
+    return launch(ctx, k, div_up(n, 4), 256, 0, a); // 4 waves, one token each
 }
 
 // ---------------------------------------------------------------------

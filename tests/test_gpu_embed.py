@@ -52,16 +52,22 @@ def test_config_tables_bit_exact(ctx, cfg_name, out):
     assert_bits_equal(got, want, f"config {cfg_name}")
 
 
-@pytest.mark.parametrize("hidden", [96, 160, 3584 + 32])
-def test_unaligned_rows_take_the_2_byte_path(ctx, hidden):
+# Row lengths whose rows start on a 2-byte (not 4-byte) boundary, that leave
+# the last round of units part-filled, or that take several rounds (more than
+# 8 units of 8 values per lane: hidden > 4096).
+@pytest.mark.parametrize("hidden", [96, 160, 3584 + 32, 8192 + 96])
+def test_odd_row_lengths_and_multi_round_rows(ctx, hidden):
     rng = np.random.default_rng(hidden)
     for qtype in ("q4_0", "q8_0"):
         table = W.quant_table(rng, 64, hidden, qtype, (0.001, 0.05))
         ty = W.GGML_ID[qtype]
-        ids = rng.integers(0, 64, 40).astype(np.uint32)
+        ids = rng.integers(0, 64, 41).astype(np.uint32)
         emb = ops.TokenEmbedding(ctx, ty, table, 64, hidden)
         got = emb.rows(ids, 1.37).numpy()
         assert_bits_equal(got, O.embed(table, ty, 64, hidden, ids, 1.37), qtype)
+        got16 = emb.rows(ids, 1.37, out_dtype=np.float16).numpy()
+        want16 = O.embed(table, ty, 64, hidden, ids, 1.37, out_dtype=np.float16)
+        assert_bits_equal(got16, want16, qtype + " f16")
 
 
 def test_empty_and_single_token(ctx):
