@@ -269,6 +269,102 @@ def profiled_steps(torch, ctx, step, steps, warmup):
     return t0.elapsed_time(t1) / steps, {n: (k, t / steps) for n, (k, t) in per.items()}
 
 
+def kv_store_bench(ctx, torch, name, n, dtype, steps=20, warmup=5):
+    """QK-norm + RoPE + paged K/V store (cuca_hip_rope_store_kv) at n tokens of
+    config `name`: the fused kernel's time and GB/s over its algorithmic bytes
+    (Q in and out, K and V in, K and V into the pool, the cos/sin rows), next
+    to the unfused sequence it replaces -- this library's RoPE on Q and K in
+    place, then K and V scattered into the pool by torch (index_put) -- and
+    sampled rows checked against the oracle."""
+    import numpy as np
+    from cuca_amd import hip
+    from cuca_amd import workloads as W
+    from oracle import oracle as O
+    cfg = W.CONFIGS[name]
+    d, nq, nk, eps = cfg["head_dim"], cfg["nq"], cfg["nk"], cfg["eps"]
+    dt = hip.F16 if dtype == "f16" else hip.F32
+    tdt = torch.float16 if dtype == "f16" else torch.float32
+    s = 2 if dtype == "f16" else 4
+    kind = hip.ROPE_NEOX if cfg["rope"] == "neox" else hip.ROPE_NORM
+    gen = torch.Generator(device="cuda").manual_seed(cfg["seed"] * 7 + n)
+    q = (cfg["std"] * torch.randn((n, nq, d), device="cuda", generator=gen)).to(tdt)
+    k = (cfg["std"] * torch.randn((n, nk, d), device="cuda", generator=gen)).to(tdt)
+    v = (cfg["std"] * torch.randn((n, nk, d), device="cuda", generator=gen)).to(tdt)
+    q0 = q.clone()
+    n_blocks = n // hip.KV_BLOCK + 64
+    pk = torch.zeros((n_blocks, nk, hip.KV_BLOCK, d), device="cuda", dtype=tdt)
+    pv = torch.zeros_like(pk)
+    table = np.random.default_rng(cfg["seed"]).permutation(n_blocks)[:(n + 15) // 16]
+    slots = hip.kv_slots(table.astype(np.uint32), 0, n, n_blocks)
+    dslots = torch.from_numpy(slots).cuda()
+    sb, sr = dslots.long() // hip.KV_BLOCK, dslots.long() % hip.KV_BLOCK
+    cos, sin = hip.rope_tables(kind, d, cfg["theta"], n)
+    dcos, dsin = torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda()
+    pos = torch.arange(n, dtype=torch.int32, device="cuda")
+    qn = kn = None
+    if cfg.get("qk_norm"):
+        qn = (1 + 0.02 * torch.randn(d, device="cuda", generator=gen)).float()
+        kn = (1 + 0.02 * torch.randn(d, device="cuda", generator=gen)).float()
+    ptr = (lambda t: None if t is None else t.data_ptr())
+    v_norm = 1 if cfg.get("qk_norm") else 0
+
+    def fused():
+        ctx.rope_store_kv(q.data_ptr(), nq * d, k.data_ptr(), nk * d, v.data_ptr(), nk * d, n, nq,
+                          nk, d, d, kind, dcos.data_ptr(), dsin.data_ptr(), n, pos.data_ptr(),
+                          ptr(qn), ptr(kn), v_norm, eps, pk.data_ptr(), pv.data_ptr(), n_blocks,
+                          dslots.data_ptr(), dt)
+
+    kw = k.clone()
+
+    def unfused():
+        ctx.rope(q.data_ptr(), nq * d, kw.data_ptr(), nk * d, n, nq, nk, d, d, kind,
+                 dcos.data_ptr(), dsin.data_ptr(), n, pos.data_ptr(), ptr(qn), ptr(kn), eps, dt)
+        pk[sb, :, sr] = kw
+        pv[sb, :, sr] = v
+
+    for _ in range(warmup):
+        fused()
+    torch.cuda.synchronize()
+    ctx.profile_start(steps)
+    for _ in range(steps):
+        fused()
+    recs = ctx.profile_stop()
+    kernel = recs[0][0]
+    k_ms = sum(t for _, t in recs) / len(recs)
+    un_ms = time_steps(torch, unfused, steps, warmup)
+    # one clean pass for the check (q is rotated in place)
+    q.copy_(q0)
+    pk.zero_()
+    pv.zero_()
+    fused()
+    torch.cuda.synchronize()
+    ctx.check_device()
+    sm = np.unique(np.concatenate([[0, 15, 16, n - 1], np.random.default_rng(5).integers(0, n, 28)]))
+    st = torch.from_numpy(sm).cuda()
+    hq, hk, hv = (t[st].cpu().numpy() for t in (q0, k, v))
+    p32 = sm.astype(np.int32)
+    hqn, hkn = (None if t is None else t.cpu().numpy() for t in (qn, kn))
+    wq = O.rope(hq, cos, sin, p32, kind, norm_w=hqn, eps=eps)
+    wk = O.rope(hk, cos, sin, p32, kind, norm_w=hkn, eps=eps)
+    wv = hv
+    if v_norm:
+        _, h = O.add_rmsnorm(hv.reshape(-1, d), None, None, eps, write_x=False)
+        wv = h.reshape(hv.shape)
+    got = (q[st].cpu().numpy(), pk[sb[st], :, sr[st]].cpu().numpy(),
+           pv[sb[st], :, sr[st]].cpu().numpy())
+    for g, w, what in zip(got, (wq, wk, wv), ("q", "pool k", "pool v")):
+        if qn is None:
+            assert np.array_equal(g.view(np.uint16 if dtype == "f16" else np.uint32),
+                                  w.view(np.uint16 if dtype == "f16" else np.uint32)), what
+        else:
+            err = np.abs(g.astype(np.float64) - w) / (np.abs(w.astype(np.float64)).max(-1, keepdims=True))
+            assert err.max() <= (4e-3 if dtype == "f16" else 1e-5), (what, err.max())
+    b = n * (2 * s * (nq + 2 * nk) * d + 4 * d) + (8 * d if qn is not None else 0)
+    return dict(kernel=kernel, us=round(k_ms * 1000, 2), bytes=b,
+                gbs=round(b / (k_ms / 1e3) / 1e9, 1), frac=round(b / (k_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                unfused_us=round(un_ms * 1000, 2), verified_rows=int(sm.size))
+
+
 class DecodeLayers:
     """32 layers of the decode step's non-matmul ops (config B, f32)."""
 
@@ -390,6 +486,7 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-large", action="store_true", help="skip the 16384-token step")
     ap.add_argument("--no-configs", action="store_true", help="skip the A/B/D/E config steps")
+    ap.add_argument("--no-kv", action="store_true", help="skip the fused RoPE + paged K/V store")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: these ops run on one GPU's share of the work and "
@@ -464,6 +561,17 @@ def main():
                 us_per_step=round(ms_c * 1000, 2), gbs=round(b_c / (ms_c / 1e3) / 1e9, 1),
                 frac=round(b_c / (ms_c / 1e3) / 1e9 / HBM_PEAK_GBS, 4), ops=ops_c)
 
+    kv = None
+    if not args.no_kv:
+        log("rope + paged K/V store")
+        kv = {}
+        for name, n, dtype in (("C", args.tokens, "f16"), ("C", 16384, "f16"), ("E", 8192, "f16"),
+                               ("B", 32, "f32")):
+            r = kv_store_bench(ctx, torch, name, n, dtype)
+            checked_rows += r.pop("verified_rows")
+            kv[f"{name}_{n}_{dtype}"] = r
+        torch.cuda.empty_cache()
+
     decode = None
     if not args.no_decode:
         log("decode graphs")
@@ -503,6 +611,7 @@ def main():
         "ops": ops,
         "prefill_16384": big,
         "configs": configs,
+        "rope_store_kv": kv,
         "decode_us_per_layer": decode,
         "roofline": {"kernel": glu["kernel"], "bound": "hbm",
                      "achieved": glu["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -17,7 +17,7 @@ extern "C" {
 /* Device status words, one per kind of bad input the kernels can meet.
  * Each holds (row << 32 | value) of the smallest bad row seen, or all
  * ones.  The host resets them after reading (cuca_hip_check_device). */
-enum { CUCA_STATUS_EMBED_ID = 0, CUCA_STATUS_ROPE_POS = 1, CUCA_STATUS_WORDS = 4 };
+enum { CUCA_STATUS_EMBED_ID = 0, CUCA_STATUS_ROPE_POS = 1, CUCA_STATUS_KV_SLOT = 2, CUCA_STATUS_WORDS = 4 };
 
 typedef struct {
     const uint8_t *table;   /* [vocab, row_bytes]                          */
@@ -77,6 +77,18 @@ typedef struct {
     int32_t tph_log2;       /* log2(threads per head), vector kernels       */
     float eps;
     int32_t kind;           /* generic kernel: 0 NORM, 2 NEOX               */
+    /* paged K/V store (the _kv kernels; zero otherwise): K heads are
+     * written to pool_k and V heads to pool_v instead of in place, row r
+     * to pool row slots[r] = block * 16 + position % 16 of a
+     * [n_blocks, nk, 16, d] pool                                            */
+    const void *v;          /* [rows, nk, d] with row stride v_ld           */
+    void *pool_k;
+    void *pool_v;
+    const int32_t *slots;   /* [rows]                                       */
+    int64_t v_ld;
+    int64_t n_slots;        /* n_blocks * 16                                */
+    int32_t nv;             /* V heads: nk for the store, else 0            */
+    int32_t v_norm;         /* weightless RMSNorm of V before the store     */
 } RopeArgs;
 
 #ifdef __cplusplus

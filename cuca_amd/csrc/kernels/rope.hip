@@ -1,5 +1,5 @@
 // rope.hip -- rotary embedding on Q and K in place, with the optional fused
-// per-head QK-norm, on gfx950.
+// per-head QK-norm, on gfx950; and the same fused with the paged K/V store.
 //
 // Replaces apply_rope / rotate_calls (cpu.rs:2996-3026, 3672-3688; candle's
 // rope and rope_i) and the GPU rope (gpu.rs:5922-5964: narrow / cat / mul,
@@ -18,6 +18,14 @@
 // (-ffp-contract=off, and the pragma below): without the norm the result is
 // bit-identical to the reference's f32 rotation, in f16 too (exact widening,
 // one rounding).
+//
+// The _kv kernels replace store_kv (cpu.rs:3028-3097) and KvPool::write
+// (gpu.rs:1786-1806): K is normalised, rotated and written straight into
+// the layer's paged pool, V (optionally RMS-normalised without a weight,
+// gpu.rs:5277) copied into its pool, so K makes one trip through HBM
+// instead of two.  The pools are [n_blocks, n_kv_head, 16, head_dim]
+// (paged_attn.rs:1-38); row r goes to pool row slots[r] = block * 16 +
+// position % 16, which the host derives from the sequence's block table.
 //
 // Generic kernel (any head_dim / n_dims / alignment): one wave per head.
 
@@ -62,7 +70,12 @@ __device__ static inline void load_tab(const float *t, int64_t first, float (&v)
 //         lane.  (Two adjacent chunks per lane measured 74 % of peak at 16384
 //         f16 rows against 80 % for this layout: each load instruction then
 //         touched every other chunk.)
-template <typename T, int KIND, bool NORM>
+// A row's heads, in launch order: nq Q heads, nk K heads, then (STORE) nk
+// V heads.  Without STORE every head is rotated in place.  With STORE the K
+// heads are rotated and the V heads (optionally RMS-normalised without a
+// weight) copied into the paged pools, at pool row slots[row] of their KV
+// head; Q stays in place.
+template <typename T, int KIND, bool NORM, bool STORE>
 __device__ static inline void rope_body(const RopeArgs &a) {
     constexpr int VP = Chunk<T>::N;
     constexpr int NC = KIND == 2 ? 2 : 1;       // chunks per lane
@@ -71,15 +84,18 @@ __device__ static inline void rope_body(const RopeArgs &a) {
     const int tph = 1 << tl;
     const uint32_t gh = blockIdx.x * (uint32_t)(CUCA_BLOCK >> tl) + (threadIdx.x >> tl);
     const int u = threadIdx.x & (tph - 1);
-    const uint32_t heads = (uint32_t)(a.nq + a.nk);
+    const int nqk = a.nq + a.nk;
+    const uint32_t heads = (uint32_t)(nqk + (STORE ? a.nv : 0));
     const bool live = gh < (uint32_t)a.rows * heads;
     const uint32_t row = live ? gh / heads : 0;
     const int h = live ? (int)(gh - row * heads) : 0;
-    const bool isq = h < a.nq;
+    const int hk = h < a.nq ? 0 : (h < nqk ? 1 : 2); // Q, K or V head
     const int D = a.head_dim;
-    T *base = isq ? reinterpret_cast<T *>(a.q) + (int64_t)row * a.q_ld + (int64_t)h * D
-                  : reinterpret_cast<T *>(a.k) + (int64_t)row * a.k_ld + (int64_t)(h - a.nq) * D;
-    const float *nw = isq ? a.q_norm_w : a.k_norm_w;
+    const T *src = hk == 0 ? reinterpret_cast<const T *>(a.q) + (int64_t)row * a.q_ld + (int64_t)h * D
+                 : hk == 1 ? reinterpret_cast<const T *>(a.k) + (int64_t)row * a.k_ld + (int64_t)(h - a.nq) * D
+                           : reinterpret_cast<const T *>(a.v) + (int64_t)row * a.v_ld + (int64_t)(h - nqk) * D;
+    const float *nw = hk == 0 ? a.q_norm_w : (hk == 1 ? a.k_norm_w : nullptr);
+    const bool scale_h = hk == 2 ? a.v_norm != 0 : nw != nullptr; // this head is normalised
     const int half = a.n_dims >> 1;
 
     // This lane's chunks: element offsets e[0] (and e[1] for NEOX).
@@ -95,28 +111,32 @@ __device__ static inline void rope_body(const RopeArgs &a) {
     } else {
         e[0] = u * VP; rot = e[0] < a.n_dims;
     }
+    rot = rot && hk != 2;
     // Every load is issued up front and unconditionally, from addresses that
     // are always valid (a lane past the last head reads row 0, a position
     // outside the table or a pass-through lane reads table entry 0, a head
     // without norm weights reads the other projection's), and pinned there
-    // by an empty asm on the loaded registers: the position, the head's
-    // chunks, the cos/sin entries and the norm weights are all in flight
-    // together.  Left to itself the compiler sinks the table loads into the
-    // predicated store's branch, behind a wait for the chunks (56-63 us
-    // against 53.5 us per 16384 f16 rows of 40 heads).
+    // by an empty asm on the loaded registers: the position (and slot), the
+    // head's chunks, the cos/sin entries and the norm weights are all in
+    // flight together.  Left to itself the compiler sinks the table loads
+    // into the predicated store's branch, behind a wait for the chunks
+    // (56-63 us against 53.5 us per 16384 f16 rows of 40 heads).
     const int32_t pos = a.pos[row];
+    const int32_t slot = STORE ? a.slots[row] : 0;
     u32x4 raw[NC];
 #pragma unroll
-    for (int k = 0; k < NC; k++) raw[k] = Chunk<T>::load_raw(base, e[k] / VP);
+    for (int k = 0; k < NC; k++) raw[k] = Chunk<T>::load_raw(src, e[k] / VP);
     const bool pos_ok = pos >= 0 && (int64_t)pos < a.table_rows;
+    const bool slot_ok = !STORE || (slot >= 0 && (int64_t)slot < a.n_slots);
     const int64_t t0 = (rot && pos_ok) ? (int64_t)pos * half + (KIND == 2 ? e[0] : (e[0] >> 1)) : 0;
     float c[NT], s[NT];
     load_tab<NT>(a.cos_t, t0, c);
     load_tab<NT>(a.sin_t, t0, s);
     float w[NC][VP];
-    if (NORM) {
-        // the launch picks a _qkn kernel only when one of the two is set
-        const float *wp = nw ? nw : (isq ? a.k_norm_w : a.q_norm_w);
+    // a uniform condition: are there norm weights at all?
+    const float *any_w = a.q_norm_w ? a.q_norm_w : a.k_norm_w;
+    if (NORM && any_w) {
+        const float *wp = nw ? nw : any_w;
 #pragma unroll
         for (int k = 0; k < NC; k++) load_tab<VP>(wp, e[k], w[k]);
     }
@@ -130,20 +150,26 @@ __device__ static inline void rope_body(const RopeArgs &a) {
         Chunk<T>::widen(raw[k], v[k]);
     }
     if (NORM) {
+        if (any_w) {
 #pragma unroll
-        for (int k = 0; k < NC; k++) pin(w[k]);
+            for (int k = 0; k < NC; k++) pin(w[k]);
+        }
         float ss = 0.0f;
 #pragma unroll
         for (int k = 0; k < NC; k++)
 #pragma unroll
             for (int i = 0; i < VP; i++) ss += v[k][i] * v[k][i];
         ss = group_sum_rt(ss, tph);
-        // the norm kernel's reciprocal form, x * (1 / sqrt(mean + eps)) * w
+        // the norm kernel's reciprocal form, x * (1 / sqrt(mean + eps)) * w;
+        // a weightless norm multiplies by 1 (exact)
         const float inv = 1.0f / sqrtf(ss / (float)D + a.eps);
 #pragma unroll
         for (int k = 0; k < NC; k++)
 #pragma unroll
-            for (int i = 0; i < VP; i++) v[k][i] = nw ? v[k][i] * inv * w[k][i] : v[k][i];
+            for (int i = 0; i < VP; i++) {
+                const float wi = nw ? w[k][i] : 1.0f;
+                v[k][i] = scale_h ? v[k][i] * inv * wi : v[k][i];
+            }
     }
     // The rotation is computed on every lane and selected.
     if (KIND == 2) {
@@ -165,73 +191,104 @@ __device__ static inline void rope_body(const RopeArgs &a) {
             v[0][2 * j + 1] = rot ? r1 : x1;
         }
     }
-    if (live && pos_ok && (rot || (NORM && nw))) {
-#pragma unroll
-        for (int k = 0; k < NC; k++) Chunk<T>::store_nt(base, e[k] / VP, v[k]);
+    T *dst;
+    if (STORE && hk != 0) {
+        // pool [n_blocks, nk, 16, d]: block slot / 16, KV head, row slot % 16
+        const int kvh = hk == 1 ? h - a.nq : h - nqk;
+        const int64_t prow = ((int64_t)(slot >> 4) * a.nk + kvh) * 16 + (slot & 15);
+        dst = reinterpret_cast<T *>(hk == 1 ? a.pool_k : a.pool_v) + prow * D;
+    } else {
+        dst = const_cast<T *>(src);
     }
-    if (live && !pos_ok && u == 0 && h == 0)
-        record_bad(a.status + CUCA_STATUS_ROPE_POS, row, (uint32_t)pos);
+    if (live && pos_ok && slot_ok && (rot || scale_h || (STORE && hk != 0))) {
+#pragma unroll
+        for (int k = 0; k < NC; k++) Chunk<T>::store_nt(dst, e[k] / VP, v[k]);
+    }
+    if (live && u == 0 && h == 0) {
+        if (!pos_ok) record_bad(a.status + CUCA_STATUS_ROPE_POS, row, (uint32_t)pos);
+        if (!slot_ok) record_bad(a.status + CUCA_STATUS_KV_SLOT, row, (uint32_t)slot);
+    }
 }
 
 template <typename T>
 __device__ static inline void rope_generic_body(const RopeArgs &a) {
     const int lane = threadIdx.x & (CUCA_WAVE - 1);
     const uint32_t gh = blockIdx.x * (uint32_t)(CUCA_BLOCK / CUCA_WAVE) + threadIdx.x / CUCA_WAVE;
-    const uint32_t heads = (uint32_t)(a.nq + a.nk);
+    const int nqk = a.nq + a.nk;
+    const uint32_t heads = (uint32_t)(nqk + a.nv);
     if (gh >= (uint32_t)a.rows * heads) return; // whole wave
     const uint32_t row = gh / heads;
     const int h = (int)(gh - row * heads);
     const int32_t pos = a.pos[row];
-    if (pos < 0 || (int64_t)pos >= a.table_rows) {
-        if (lane == 0 && h == 0) record_bad(a.status + CUCA_STATUS_ROPE_POS, row, (uint32_t)pos);
+    const int32_t slot = a.slots ? a.slots[row] : 0;
+    const bool pos_ok = pos >= 0 && (int64_t)pos < a.table_rows;
+    const bool slot_ok = !a.slots || (slot >= 0 && (int64_t)slot < a.n_slots);
+    if (!pos_ok || !slot_ok) {
+        if (lane == 0 && h == 0) {
+            if (!pos_ok) record_bad(a.status + CUCA_STATUS_ROPE_POS, row, (uint32_t)pos);
+            if (!slot_ok) record_bad(a.status + CUCA_STATUS_KV_SLOT, row, (uint32_t)slot);
+        }
         return;
     }
-    const bool isq = h < a.nq;
+    const int hk = h < a.nq ? 0 : (h < nqk ? 1 : 2); // Q, K or V head
     const int D = a.head_dim;
-    T *base = isq ? reinterpret_cast<T *>(a.q) + (int64_t)row * a.q_ld + (int64_t)h * D
-                  : reinterpret_cast<T *>(a.k) + (int64_t)row * a.k_ld + (int64_t)(h - a.nq) * D;
-    const float *nw = isq ? a.q_norm_w : a.k_norm_w;
+    const T *src = hk == 0 ? reinterpret_cast<const T *>(a.q) + (int64_t)row * a.q_ld + (int64_t)h * D
+                 : hk == 1 ? reinterpret_cast<const T *>(a.k) + (int64_t)row * a.k_ld + (int64_t)(h - a.nq) * D
+                           : reinterpret_cast<const T *>(a.v) + (int64_t)row * a.v_ld + (int64_t)(h - nqk) * D;
+    T *dst = const_cast<T *>(src);
+    if (a.slots && hk != 0) {
+        const int kvh = hk == 1 ? h - a.nq : h - nqk;
+        const int64_t prow = ((int64_t)(slot >> 4) * a.nk + kvh) * 16 + (slot & 15);
+        dst = reinterpret_cast<T *>(hk == 1 ? a.pool_k : a.pool_v) + prow * D;
+    }
+    const float *nw = hk == 0 ? a.q_norm_w : (hk == 1 ? a.k_norm_w : nullptr);
+    const bool scale_h = hk == 2 ? a.v_norm != 0 : nw != nullptr;
     float inv = 1.0f;
-    if (nw) {
+    if (scale_h) {
         float ss = 0.0f;
         for (int e = lane; e < D; e += CUCA_WAVE) {
-            const float v = load1<T>(base, e);
+            const float v = load1<T>(src, e);
             ss += v * v;
         }
         ss = group_sum<CUCA_WAVE>(ss);
         inv = 1.0f / sqrtf(ss / (float)D + a.eps);
     }
+    auto scaled = [&](int e) {
+        const float x = load1<T>(src, e);
+        return scale_h ? x * inv * (nw ? nw[e] : 1.0f) : x;
+    };
     const int half = a.n_dims >> 1;
+    const int rot_end = hk == 2 ? 0 : half; // V heads are not rotated
     const float *cs = a.cos_t + (int64_t)pos * half;
     const float *sn = a.sin_t + (int64_t)pos * half;
     // every lane reads its elements before any lane of the wave writes
     // (the norm pass above read all of them); pairs are disjoint per lane
-    for (int i = lane; i < half; i += CUCA_WAVE) {
+    for (int i = lane; i < rot_end; i += CUCA_WAVE) {
         const int ea = a.kind == 2 ? i : 2 * i;
         const int eb = a.kind == 2 ? i + half : 2 * i + 1;
-        float x0 = load1<T>(base, ea), x1 = load1<T>(base, eb);
-        if (nw) {
-            x0 = x0 * inv * nw[ea];
-            x1 = x1 * inv * nw[eb];
-        }
-        store1<T>(base, ea, x0 * cs[i] - x1 * sn[i]);
-        store1<T>(base, eb, x0 * sn[i] + x1 * cs[i]);
+        const float x0 = scaled(ea), x1 = scaled(eb);
+        store1<T>(dst, ea, x0 * cs[i] - x1 * sn[i]);
+        store1<T>(dst, eb, x0 * sn[i] + x1 * cs[i]);
     }
-    if (nw) {
-        for (int e = a.n_dims + lane; e < D; e += CUCA_WAVE)
-            store1<T>(base, e, load1<T>(base, e) * inv * nw[e]);
+    // pass-through values (past n_dims; a V head's whole row)
+    if (scale_h || dst != src) {
+        for (int e = (hk == 2 ? 0 : a.n_dims) + lane; e < D; e += CUCA_WAVE) store1<T>(dst, e, scaled(e));
     }
 }
 
-#define CUCA_ROPE(NAME, T, KIND, NORM)                                                     \
+#define CUCA_ROPE(NAME, T, KIND, NORM, STORE)                                              \
     extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void NAME(RopeArgs a) {            \
-        rope_body<T, KIND, NORM>(a);                                                       \
+        rope_body<T, KIND, NORM, STORE>(a);                                                \
     }
 #define CUCA_ROPE_SET(TN, T)                                                               \
-    CUCA_ROPE(cuca_rope_##TN##_norm, T, 0, false)                                          \
-    CUCA_ROPE(cuca_rope_##TN##_neox, T, 2, false)                                          \
-    CUCA_ROPE(cuca_rope_##TN##_norm_qkn, T, 0, true)                                       \
-    CUCA_ROPE(cuca_rope_##TN##_neox_qkn, T, 2, true)                                       \
+    CUCA_ROPE(cuca_rope_##TN##_norm, T, 0, false, false)                                   \
+    CUCA_ROPE(cuca_rope_##TN##_neox, T, 2, false, false)                                   \
+    CUCA_ROPE(cuca_rope_##TN##_norm_qkn, T, 0, true, false)                                \
+    CUCA_ROPE(cuca_rope_##TN##_neox_qkn, T, 2, true, false)                                \
+    CUCA_ROPE(cuca_rope_##TN##_norm_kv, T, 0, false, true)                                 \
+    CUCA_ROPE(cuca_rope_##TN##_neox_kv, T, 2, false, true)                                 \
+    CUCA_ROPE(cuca_rope_##TN##_norm_qkn_kv, T, 0, true, true)                              \
+    CUCA_ROPE(cuca_rope_##TN##_neox_qkn_kv, T, 2, true, true)                              \
     extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void cuca_rope_##TN##_generic(     \
         RopeArgs a) {                                                                      \
         rope_generic_body<T>(a);                                                           \

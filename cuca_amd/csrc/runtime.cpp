@@ -73,6 +73,7 @@ struct cuca_hip_ctx {
     hipEvent_t t0 = nullptr, t1 = nullptr;
     bool capturing = false;
     int64_t last_vocab = 0;       // for the out-of-range message
+    int64_t last_kv_blocks = 0;   // the pool size of the last K/V store (for messages)
     int64_t last_table_rows = 0;
     std::string error;
     // per-kernel timing (cuca_hip_profile_start/stop)
@@ -305,9 +306,14 @@ cuca_status cuca_hip_check_device(cuca_hip_ctx *ctx) {
         return fail(ctx, CUCA_OUT_OF_RANGE, "token id %u outside the embedding table of %lld rows (row %u)",
                     (unsigned)(v & 0xffffffffu), (long long)ctx->last_vocab, (unsigned)(v >> 32));
     }
-    unsigned long long v = w[CUCA_STATUS_ROPE_POS];
-    return fail(ctx, CUCA_OUT_OF_RANGE, "position %d outside the rope table of %lld rows (row %u)",
-                (int)(v & 0xffffffffu), (long long)ctx->last_table_rows, (unsigned)(v >> 32));
+    if (w[CUCA_STATUS_ROPE_POS] != none) {
+        unsigned long long v = w[CUCA_STATUS_ROPE_POS];
+        return fail(ctx, CUCA_OUT_OF_RANGE, "position %d outside the rope table of %lld rows (row %u)",
+                    (int)(v & 0xffffffffu), (long long)ctx->last_table_rows, (unsigned)(v >> 32));
+    }
+    unsigned long long v = w[CUCA_STATUS_KV_SLOT];
+    return fail(ctx, CUCA_OUT_OF_RANGE, "K/V slot %d outside the pool of %lld blocks (row %u)",
+                (int)(v & 0xffffffffu), (long long)ctx->last_kv_blocks, (unsigned)(v >> 32));
 }
 
 // ---------------------------------------------------------------------
@@ -552,12 +558,17 @@ cuca_status cuca_hip_glu_ragged(cuca_hip_ctx *ctx, const void *gate, int64_t gat
 // RoPE
 // ---------------------------------------------------------------------
 
-cuca_status cuca_hip_rope(cuca_hip_ctx *ctx, void *q, int64_t q_ld, void *k, int64_t k_ld, int64_t rows,
-                          int32_t nq, int32_t nk, int32_t head_dim, int32_t n_dims, cuca_rope_kind kind,
-                          const float *cos, const float *sin, int64_t table_rows, const int32_t *positions,
-                          const float *q_norm_w, const float *k_norm_w, float eps, cuca_dtype dtype) {
+// The store (STORE kernels) is on when `slots` is given.
+static cuca_status rope_common(cuca_hip_ctx *ctx, void *q, int64_t q_ld, const void *k, int64_t k_ld,
+                               const void *v, int64_t v_ld, int64_t rows, int32_t nq, int32_t nk,
+                               int32_t head_dim, int32_t n_dims, cuca_rope_kind kind, const float *cos,
+                               const float *sin, int64_t table_rows, const int32_t *positions,
+                               const float *q_norm_w, const float *k_norm_w, int32_t v_norm, float eps,
+                               void *pool_k, void *pool_v, int64_t n_blocks, const int32_t *slots,
+                               cuca_dtype dtype) {
     cuca_status st = use(ctx);
     if (st != CUCA_OK) return st;
+    const bool store = slots != nullptr;
     if (!dtype_ok(dtype)) return fail(ctx, CUCA_INVALID_ARG, "bad dtype %d", (int)dtype);
     if (kind != CUCA_ROPE_NORM && kind != CUCA_ROPE_NEOX)
         return fail(ctx, CUCA_INVALID_ARG, "bad rope kind %d", (int)kind);
@@ -568,17 +579,26 @@ cuca_status cuca_hip_rope(cuca_hip_ctx *ctx, void *q, int64_t q_ld, void *k, int
         return fail(ctx, CUCA_INVALID_ARG, "q row stride %lld shorter than %d heads of %d", (long long)q_ld, nq, head_dim);
     if (nk > 0 && (!k || k_ld < (int64_t)nk * head_dim))
         return fail(ctx, CUCA_INVALID_ARG, "k row stride %lld shorter than %d heads of %d", (long long)k_ld, nk, head_dim);
+    if (store) {
+        if (nk > 0 && (!v || v_ld < (int64_t)nk * head_dim))
+            return fail(ctx, CUCA_INVALID_ARG, "v row stride %lld shorter than %d heads of %d", (long long)v_ld, nk, head_dim);
+        if (nk > 0 && (!pool_k || !pool_v)) return fail(ctx, CUCA_INVALID_ARG, "null K/V pool");
+        if (n_blocks <= 0 || n_blocks > 0x7fffffffll / CUCA_KV_BLOCK)
+            return fail(ctx, CUCA_INVALID_ARG, "bad pool size %lld blocks", (long long)n_blocks);
+        if (v_norm != 0 && v_norm != 1) return fail(ctx, CUCA_INVALID_ARG, "v_norm must be 0 or 1");
+    }
+    const int32_t nv = store ? nk : 0;
     if (rows == 0 || nq + nk == 0) return CUCA_OK;
     if (!cos || !sin || !positions) return fail(ctx, CUCA_INVALID_ARG, "null table or positions");
     if (table_rows <= 0) return fail(ctx, CUCA_INVALID_ARG, "empty rope table");
     if (!(eps >= 0.0f)) return fail(ctx, CUCA_INVALID_ARG, "eps must be >= 0");
-    if (rows * (int64_t)(nq + nk) > 0x7fffffffll) return fail(ctx, CUCA_UNSUPPORTED, "too many heads");
+    if (rows * (int64_t)(nq + nk + nv) > 0x7fffffffll) return fail(ctx, CUCA_UNSUPPORTED, "too many heads");
     const size_t es = esize(dtype);
     const int VP = chunk_elems(dtype);
-    const bool norm = q_norm_w || k_norm_w;
+    const bool norm = q_norm_w || k_norm_w || (store && v_norm);
     RopeArgs a{};
     a.q = q;
-    a.k = k;
+    a.k = const_cast<void *>(k);
     a.cos_t = cos;
     a.sin_t = sin;
     a.pos = positions;
@@ -595,6 +615,17 @@ cuca_status cuca_hip_rope(cuca_hip_ctx *ctx, void *q, int64_t q_ld, void *k, int
     a.n_dims = n_dims;
     a.eps = eps;
     a.kind = (int32_t)kind;
+    if (store) {
+        a.v = v;
+        a.v_ld = v_ld;
+        a.pool_k = pool_k;
+        a.pool_v = pool_v;
+        a.slots = slots;
+        a.n_slots = n_blocks * CUCA_KV_BLOCK;
+        a.nv = nv;
+        a.v_norm = v_norm;
+        ctx->last_kv_blocks = n_blocks;
+    }
     ctx->last_table_rows = table_rows;
     // lanes per head: NEOX pairs chunk u with chunk u + n/(2 VP) (two per
     // lane); NORM gives each lane one chunk of whole (2i, 2i+1) pairs
@@ -605,9 +636,11 @@ cuca_status cuca_hip_rope(cuca_hip_ctx *ctx, void *q, int64_t q_ld, void *k, int
     const bool vec = head_dim % per_lane == 0 && n_dims % (2 * VP) == 0 && pow2 &&
                      (nq == 0 || (al16(q) && (q_ld * es) % 16 == 0)) &&
                      (nk == 0 || (al16(k) && (k_ld * es) % 16 == 0)) && al16(cos) && al16(sin) &&
-                     (!q_norm_w || al16(q_norm_w)) && (!k_norm_w || al16(k_norm_w));
+                     (!q_norm_w || al16(q_norm_w)) && (!k_norm_w || al16(k_norm_w)) &&
+                     (!store || nk == 0 ||
+                      (al16(v) && (v_ld * es) % 16 == 0 && al16(pool_k) && al16(pool_v)));
     const bool f16 = dtype == CUCA_F16, neox = kind == CUCA_ROPE_NEOX;
-    const int64_t heads = rows * (nq + nk);
+    const int64_t heads = rows * (nq + nk + nv);
     if (!vec) {
         Kernel kk = f16 ? cuca_rope_f16_generic : cuca_rope_f32_generic;
         return launch(ctx, kk, div_up(heads, 4), 256, 0, a);
@@ -615,12 +648,58 @@ cuca_status cuca_hip_rope(cuca_hip_ctx *ctx, void *q, int64_t q_ld, void *k, int
     int lg = 0;
     while ((1 << lg) < tph) lg++;
     a.tph_log2 = lg;
-
-    Kernel kk = f16 ? (neox ? (norm ? cuca_rope_f16_neox_qkn : cuca_rope_f16_neox)
-                            : (norm ? cuca_rope_f16_norm_qkn : cuca_rope_f16_norm))
-                    : (neox ? (norm ? cuca_rope_f32_neox_qkn : cuca_rope_f32_neox)
-                            : (norm ? cuca_rope_f32_norm_qkn : cuca_rope_f32_norm));
+    // [dtype][kind][norm][store]
+    static const Kernel table_k[2][2][2][2] = {
+        {{{cuca_rope_f32_norm, cuca_rope_f32_norm_kv}, {cuca_rope_f32_norm_qkn, cuca_rope_f32_norm_qkn_kv}},
+         {{cuca_rope_f32_neox, cuca_rope_f32_neox_kv}, {cuca_rope_f32_neox_qkn, cuca_rope_f32_neox_qkn_kv}}},
+        {{{cuca_rope_f16_norm, cuca_rope_f16_norm_kv}, {cuca_rope_f16_norm_qkn, cuca_rope_f16_norm_qkn_kv}},
+         {{cuca_rope_f16_neox, cuca_rope_f16_neox_kv}, {cuca_rope_f16_neox_qkn, cuca_rope_f16_neox_qkn_kv}}}};
+    const Kernel kk = table_k[f16][neox][norm][store];
     return launch(ctx, kk, div_up(heads, 256 / tph), 256, 0, a);
+}
+
+cuca_status cuca_hip_rope(cuca_hip_ctx *ctx, void *q, int64_t q_ld, void *k, int64_t k_ld, int64_t rows,
+                          int32_t nq, int32_t nk, int32_t head_dim, int32_t n_dims, cuca_rope_kind kind,
+                          const float *cos, const float *sin, int64_t table_rows, const int32_t *positions,
+                          const float *q_norm_w, const float *k_norm_w, float eps, cuca_dtype dtype) {
+    return rope_common(ctx, q, q_ld, k, k_ld, nullptr, 0, rows, nq, nk, head_dim, n_dims, kind, cos, sin,
+                       table_rows, positions, q_norm_w, k_norm_w, 0, eps, nullptr, nullptr, 0, nullptr, dtype);
+}
+
+cuca_status cuca_hip_rope_store_kv(cuca_hip_ctx *ctx, void *q, int64_t q_ld, const void *k, int64_t k_ld,
+                                   const void *v, int64_t v_ld, int64_t rows, int32_t nq, int32_t nk,
+                                   int32_t head_dim, int32_t n_dims, cuca_rope_kind kind, const float *cos,
+                                   const float *sin, int64_t table_rows, const int32_t *positions,
+                                   const float *q_norm_w, const float *k_norm_w, int32_t v_norm, float eps,
+                                   void *pool_k, void *pool_v, int64_t n_blocks, const int32_t *slots,
+                                   cuca_dtype dtype) {
+    if (!slots) return fail(ctx, CUCA_INVALID_ARG, "null slots");
+    return rope_common(ctx, q, q_ld, k, k_ld, v, v_ld, rows, nq, nk, head_dim, n_dims, kind, cos, sin,
+                       table_rows, positions, q_norm_w, k_norm_w, v_norm, eps, pool_k, pool_v, n_blocks,
+                       slots, dtype);
+}
+
+// The pool rows of cache indices start..start+t (paged.rs:9-16): position p
+// is row p % 16 of block table[p / 16]; a missing, released or out-of-pool
+// block fails like check_range (cpu/paged_attn.rs:42-65).
+cuca_status cuca_hip_kv_slots(const uint32_t *table, int64_t table_len, int64_t start, int64_t t,
+                              int64_t n_blocks, int32_t *slots_out) {
+    if (start < 0 || t < 0 || table_len < 0) return fail(nullptr, CUCA_INVALID_ARG, "negative count");
+    if (t == 0) return CUCA_OK;
+    if (!slots_out || (!table && table_len > 0)) return fail(nullptr, CUCA_INVALID_ARG, "null pointer");
+    if (n_blocks <= 0 || n_blocks > 0x7fffffffll / CUCA_KV_BLOCK)
+        return fail(nullptr, CUCA_INVALID_ARG, "bad pool size %lld blocks", (long long)n_blocks);
+    for (int64_t i = 0; i < t; i++) {
+        const int64_t p = start + i;
+        const int64_t bi = p / CUCA_KV_BLOCK;
+        const uint32_t id = bi < table_len ? table[bi] : CUCA_NO_BLOCK;
+        if (id == CUCA_NO_BLOCK || (int64_t)id >= n_blocks)
+            return fail(nullptr, CUCA_OUT_OF_RANGE,
+                        "position %lld has no K/V block (it left the window or was never allocated)",
+                        (long long)(bi * CUCA_KV_BLOCK));
+        slots_out[i] = (int32_t)((int64_t)id * CUCA_KV_BLOCK + p % CUCA_KV_BLOCK);
+    }
+    return CUCA_OK;
 }
 
 // RopeSpec::tables (rope.rs:118-151): f64 angles with the platform libm,

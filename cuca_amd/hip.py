@@ -64,6 +64,10 @@ SIGNATURES = {
                                   _i64, _st]),
     "cuca_hip_rope": (_st, [_p, _p, _i64, _p, _i64, _i64, _i32, _i32, _i32, _i32, _st, _p, _p,
                             _i64, _p, _p, _p, _f32, _st]),
+    "cuca_hip_rope_store_kv": (_st, [_p, _p, _i64, _p, _i64, _p, _i64, _i64, _i32, _i32, _i32, _i32,
+                                     _st, _p, _p, _i64, _p, _p, _p, _i32, _f32, _p, _p, _i64, _p,
+                                     _st]),
+    "cuca_hip_kv_slots": (_st, [_p, _i64, _i64, _i64, _i64, _p]),
     "cuca_hip_rope_tables": (_st, [ctypes.POINTER(RopeSpecC), _p, _i64, _p, _p]),
     "cuca_hip_graph_begin": (_st, [_p]),
     "cuca_hip_graph_end": (_st, [_p, _pp]),
@@ -292,6 +296,14 @@ class Context:
                                         kind, cos, sin, table_rows, positions, q_norm_w, k_norm_w,
                                         eps, dtype))
 
+    def rope_store_kv(self, q, q_ld, k, k_ld, v, v_ld, rows, nq, nk, head_dim, n_dims, kind, cos,
+                      sin, table_rows, positions, q_norm_w, k_norm_w, v_norm, eps, pool_k, pool_v,
+                      n_blocks, slots, dtype):
+        self.check(self.L.cuca_hip_rope_store_kv(self.ptr, q, q_ld, k, k_ld, v, v_ld, rows, nq, nk,
+                                                 head_dim, n_dims, kind, cos, sin, table_rows,
+                                                 positions, q_norm_w, k_norm_w, int(v_norm), eps,
+                                                 pool_k, pool_v, n_blocks, slots, dtype))
+
 
 class Graph:
     def __init__(self, ctx, ptr):
@@ -311,6 +323,20 @@ class Graph:
             self.destroy()
         except Exception:
             pass
+
+
+KV_BLOCK = 16          # positions per paged K/V block (paged.rs:45)
+NO_BLOCK = 0xFFFFFFFF  # a released block's table entry (paged.rs:49)
+
+
+def kv_slots(table, start, t, n_blocks):
+    """Pool rows of cache indices start..start+t of a sequence with block
+    table `table` (cuca_hip_kv_slots, host): int32[t], block * 16 + p % 16."""
+    tab = np.ascontiguousarray(table, dtype=np.uint32)
+    out = np.empty(t, np.int32)
+    _check(lib().cuca_hip_kv_slots(tab.ctypes.data if tab.size else None, tab.size, start, t,
+                                   n_blocks, out.ctypes.data), None)
+    return out
 
 
 def rope_tables(kind, n_dims, base, positions, freq_scale=1.0, yarn=None, attn_factor=1.0,

@@ -181,6 +181,52 @@ def rope_qk(q, k, cos, sin, kind, n_dims, positions, q_norm_w=None, k_norm_w=Non
     return q, k
 
 
+class KvPool:
+    """One K/V-owning layer's paged cache on the device (KvPool, gpu.rs:1774-1781;
+    KvLayer, cpu.rs:689-714): keys and values [n_blocks, n_kv_head, 16,
+    head_dim] of the activation dtype, zero-filled.  Position p of a sequence
+    lives in block table[p // 16], row p % 16 (paged.rs:9-16)."""
+
+    def __init__(self, ctx, n_blocks, n_kv_head, head_dim, dtype=np.float32):
+        self.ctx = ctx
+        self.n_blocks, self.n_kv_head, self.head_dim = n_blocks, n_kv_head, head_dim
+        shape = (n_blocks, n_kv_head, hip.KV_BLOCK, head_dim)
+        self.k = ctx.array(np.zeros(shape, dtype))
+        self.v = ctx.array(np.zeros(shape, dtype))
+
+    def slots(self, table, start, t):
+        """Pool rows of cache indices start..start+t (host, int32[t])."""
+        return hip.kv_slots(table, start, t, self.n_blocks)
+
+    def store_kv(self, q, k, v, cos, sin, kind, n_dims, positions, slots, q_norm_w=None,
+                 k_norm_w=None, v_norm=False, eps=1e-6):
+        """Normalise and rotate q [rows, nq, d] in place, and k [rows, nk, d]
+        into the pool, with v (normalised without a weight when v_norm) beside
+        it (store_kv, cpu.rs:3028-3097), in one launch.  slots: device int32
+        [rows] from `slots`."""
+        rows, nq, d = q.shape
+        nk = k.shape[1]
+        if k.shape != (rows, nk, d) or v.shape != (rows, nk, d) or nk != self.n_kv_head \
+                or d != self.head_dim:
+            raise CucaError(hip.INVALID_ARG, "store_kv: row shape mismatch")
+        ctx = q.ctx
+        qw, kw = _w(ctx, q_norm_w), _w(ctx, k_norm_w)
+        ctx.rope_store_kv(q.ptr, nq * d, k.ptr, nk * d, v.ptr, nk * d, rows, nq, nk, d, n_dims, kind,
+                          cos.ptr, sin.ptr, cos.shape[0], positions.ptr,
+                          None if qw is None else qw.ptr, None if kw is None else kw.ptr, v_norm,
+                          eps, self.k.ptr, self.v.ptr, self.n_blocks, slots.ptr,
+                          hip.dtype_code(q.dtype))
+        return q
+
+    def read(self, slots):
+        """The rows `slots` name, the inverse of the store (KvPool::read,
+        gpu.rs:1808-1830): host (k, v) [len(slots), n_kv_head, head_dim]."""
+        slots = np.asarray(slots, np.int64)
+        b, r = slots // hip.KV_BLOCK, slots % hip.KV_BLOCK
+        kp, vp = self.k.numpy(), self.v.numpy()
+        return kp[b, :, r, :], vp[b, :, r, :]
+
+
 class RopeSpec:
     """One rotary embedding (rope.rs:62-79)."""
 

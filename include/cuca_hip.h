@@ -19,6 +19,11 @@
  *                          with the per-head QK-norm      3040-3055, 3672-3688
  *                          GPU rope                       gpu.rs:5922-5964
  *   cuca_hip_rope_tables   RopeSpec::tables (host)        rope.rs:118-151, mod.rs:460-472
+ *   cuca_hip_rope_store_kv QK-norm + RoPE + the paged     cpu.rs:3028-3097,
+ *                          K/V store of store_kv          cpu/paged_attn.rs:370-400
+ *                          GPU k/v branch, KvPool::write  gpu.rs:5266-5285, 1786-1806
+ *   cuca_hip_kv_slots      block-table positions -> pool  paged.rs:9-16, gpu.rs:1940-1975
+ *                          rows (host)
  *
  * Conventions
  * - A context owns one device, one HIP stream (or borrows the caller's),
@@ -108,7 +113,8 @@ cuca_status cuca_hip_stream_sync(cuca_hip_ctx *ctx);
 /* Synchronize, then report (and clear) what the kernels recorded in the
  * status word: CUCA_OUT_OF_RANGE with the first bad row in the message
  * ("token id {id} outside the embedding table of {rows} rows", as
- * quant.rs:395-400, or a RoPE position outside its table). */
+ * quant.rs:395-400, a RoPE position outside its table, or a K/V slot outside
+ * its pool). */
 cuca_status cuca_hip_check_device(cuca_hip_ctx *ctx);
 
 /* ------------------------------------------------------------------ */
@@ -189,6 +195,44 @@ cuca_status cuca_hip_rope(cuca_hip_ctx *ctx, void *q, int64_t q_ld, void *k, int
                           const float *sin, int64_t table_rows, const int32_t *positions,
                           const float *q_norm_w, const float *k_norm_w, float eps,
                           cuca_dtype dtype);
+
+/* Positions per paged K/V block (paged.rs:45, BLOCK_SIZE), and the block
+ * table entry of a released block (paged.rs:49, NO_BLOCK). */
+#define CUCA_KV_BLOCK 16
+#define CUCA_NO_BLOCK 0xffffffffu
+
+/* cuca_hip_rope fused with the paged K/V store of a K/V-owning layer
+ * (store_kv, cpu.rs:3028-3097 -> store_rows, cpu/paged_attn.rs:370-400;
+ * GPU: the k/v branch of gpu.rs:5266-5285 -> KvPool::write,
+ * gpu.rs:1786-1806).  One launch:
+ *   Q: QK-norm (q_norm_w) and rotation in place, as cuca_hip_rope;
+ *   K: QK-norm (k_norm_w) and rotation, written to pool_k only (the k
+ *      buffer is read, not written);
+ *   V: rms(v, no weight, eps) when v_norm (gpu.rs:5277), written to pool_v.
+ * The pools are [n_blocks, nk, CUCA_KV_BLOCK, head_dim] in the activation
+ * dtype (paged_attn.rs:1-38): row r of the call goes to pool row
+ *   slots[r] = block * CUCA_KV_BLOCK + position % CUCA_KV_BLOCK
+ * of each KV head, i.e. element ((block*nk + h)*16 + slot%16)*head_dim.
+ * slots: device int32[rows] (cuca_hip_kv_slots builds them from a block
+ * table).  A slot outside [0, n_blocks*16) or a position outside the table
+ * leaves the row untouched and is reported by cuca_hip_check_device. */
+cuca_status cuca_hip_rope_store_kv(cuca_hip_ctx *ctx, void *q, int64_t q_ld, const void *k,
+                                   int64_t k_ld, const void *v, int64_t v_ld, int64_t rows,
+                                   int32_t nq, int32_t nk, int32_t head_dim, int32_t n_dims,
+                                   cuca_rope_kind kind, const float *cos, const float *sin,
+                                   int64_t table_rows, const int32_t *positions,
+                                   const float *q_norm_w, const float *k_norm_w, int32_t v_norm,
+                                   float eps, void *pool_k, void *pool_v, int64_t n_blocks,
+                                   const int32_t *slots, cuca_dtype dtype);
+
+/* Host-side: the pool slots of cache indices start..start+t of a sequence
+ * whose block table is table[table_len] (position p -> block table[p/16],
+ * row p%16, paged.rs:9-16; the write runs of gpu.rs:1940-1975).  Fails with
+ * CUCA_OUT_OF_RANGE, as check_range does (paged_attn.rs:42-65), when a
+ * position has no block: past the table, a released block (0xffffffff,
+ * NO_BLOCK) or an id outside the pool of n_blocks. */
+cuca_status cuca_hip_kv_slots(const uint32_t *table, int64_t table_len, int64_t start, int64_t t,
+                              int64_t n_blocks, int32_t *slots_out);
 
 /* RopeSpec (rope.rs:62-79). yarn_ext_factor == 0 disables YaRN. */
 typedef struct {

@@ -8,6 +8,8 @@
 //   cuca::Glu{act, clamp}.apply(gate, up)                                  cpu.rs:342-371
 //   cuca::apply_rope(x, cos, sin, kind, n_dims, positions)                 cpu.rs:3672-3688
 //   cuca::RopeSpec::plain(kind, n_dims, base).tables(factors, positions)   rope.rs:62-151
+//   cuca::KvPool{n_blocks, n_kv_head, head_dim}.store_kv(q, k, v, ...)     cpu.rs:3028-3097,
+//                                                                          gpu.rs:1774-1806
 //
 // Tensors are cuca::Tensor: a device buffer owned through the context, with
 // a row-major shape and an element type (f32, or f16 held as uint16_t bits).
@@ -316,5 +318,55 @@ inline void apply_rope(Context &ctx, Tensor &x, const Tensor &cos, const Tensor 
                             norm_w ? static_cast<const float *>(norm_w->data()) : nullptr, nullptr, eps,
                             (cuca_dtype)x.dtype()));
 }
+
+// One K/V-owning layer's paged cache (KvPool, gpu.rs:1774-1781; KvLayer,
+// cpu.rs:689-714): keys and values [n_blocks, n_kv_head, 16, head_dim] of
+// the activation type, zero-filled.  Position p of a sequence is row p % 16
+// of block table[p / 16] (paged.rs:9-16).
+class KvPool {
+  public:
+    KvPool(Context &ctx, int64_t n_blocks, int64_t n_kv_head, int64_t head_dim, DType dtype)
+        : n_blocks_(n_blocks), k_(ctx, {n_blocks, n_kv_head, CUCA_KV_BLOCK, head_dim}, dtype),
+          v_(ctx, {n_blocks, n_kv_head, CUCA_KV_BLOCK, head_dim}, dtype) {
+        std::vector<uint8_t> zeros(k_.bytes(), 0);
+        k_.upload(zeros);
+        v_.upload(zeros);
+    }
+
+    // The pool rows of cache indices start..start+t (host).
+    std::vector<int32_t> slots(const std::vector<uint32_t> &table, int64_t start, int64_t t) const {
+        std::vector<int32_t> out((size_t)t);
+        check(nullptr, cuca_hip_kv_slots(table.data(), (int64_t)table.size(), start, t, n_blocks_,
+                                         out.data()));
+        return out;
+    }
+
+    // store_kv (cpu.rs:3028-3097): q [rows, nq, d] normalised and rotated in
+    // place; k normalised, rotated and stored; v (weightless-normalised when
+    // v_norm) stored; one launch.  slots: device int32 [rows] from slots().
+    void store_kv(Context &ctx, Tensor &q, const Tensor &k, const Tensor &v, const Tensor &cos,
+                  const Tensor &sin, RopeKind kind, int32_t n_dims, const Tensor &positions,
+                  const Tensor &slots, const Tensor *q_norm_w = nullptr,
+                  const Tensor *k_norm_w = nullptr, bool v_norm = false, float eps = 1e-6f) {
+        const int64_t rows = q.dim(0), nq = q.dim(1), d = q.dim(2), nk = k.dim(1);
+        if (k.shape() != std::vector<int64_t>{rows, nk, d} || v.shape() != k.shape() ||
+            nk != k_.dim(1) || d != k_.dim(3))
+            throw Error(CUCA_INVALID_ARG, "store_kv: row shape mismatch");
+        auto w = [](const Tensor *t) { return t ? static_cast<const float *>(t->data()) : nullptr; };
+        ctx.check(cuca_hip_rope_store_kv(
+            ctx.raw(), q.data(), nq * d, k.data(), nk * d, v.data(), nk * d, rows, (int32_t)nq,
+            (int32_t)nk, (int32_t)d, n_dims, (cuca_rope_kind)kind, static_cast<const float *>(cos.data()),
+            static_cast<const float *>(sin.data()), cos.dim(0), static_cast<const int32_t *>(positions.data()),
+            w(q_norm_w), w(k_norm_w), v_norm ? 1 : 0, eps, k_.data(), v_.data(), n_blocks_,
+            static_cast<const int32_t *>(slots.data()), (cuca_dtype)q.dtype()));
+    }
+
+    const Tensor &k() const { return k_; }
+    const Tensor &v() const { return v_; }
+
+  private:
+    int64_t n_blocks_;
+    Tensor k_, v_;
+};
 
 }  // namespace cuca

@@ -409,3 +409,66 @@ void oracle_rope(void *x, int64_t ld, int64_t rows, int heads, int head_dim,
                   positions, norm_w, eps, dtype};
     parallel_rows(nthreads, rows, rope_range, &c);
 }
+
+/* ---- paged K/V pools (cpu/paged_attn.rs) ---- */
+
+#define KV_BLOCK 16
+#define KV_NO_BLOCK 0xffffffffu
+
+/* check_range (paged_attn.rs:42-65) */
+static int kv_range_ok(const uint32_t *table, int64_t table_len, int64_t lo, int64_t hi,
+                       int64_t n_blocks) {
+    if (lo >= hi) return 0;
+    for (int64_t b = lo / KV_BLOCK; b <= (hi - 1) / KV_BLOCK; b++) {
+        if (b >= table_len) return 0;
+        uint32_t id = table[b];
+        if (id == KV_NO_BLOCK || (int64_t)id >= n_blocks) return 0;
+    }
+    return 1;
+}
+
+/* row_offset (paged_attn.rs:33-38), in elements */
+static int64_t kv_row_offset(const uint32_t *table, int64_t pos, int kvh, int n_kv, int d) {
+    int64_t block = table[pos / KV_BLOCK];
+    return ((block * n_kv + kvh) * KV_BLOCK + pos % KV_BLOCK) * (int64_t)d;
+}
+
+int oracle_store_rows(const uint32_t *table, int64_t table_len, int64_t start, int64_t rows,
+                      const void *src, void *pool, int64_t n_blocks, int n_kv, int d,
+                      int dtype) {
+    size_t es = dtype == 1 ? 2 : 4;
+    if (rows == 0) return 0;
+    if (!kv_range_ok(table, table_len, start, start + rows, n_blocks)) return -1;
+    for (int kvh = 0; kvh < n_kv; kvh++) {
+        int64_t pos = start;
+        while (pos < start + rows) {
+            int64_t blk_end = (pos / KV_BLOCK + 1) * KV_BLOCK;
+            int64_t end = start + rows < blk_end ? start + rows : blk_end;
+            int64_t at = kv_row_offset(table, pos, kvh, n_kv, d);
+            int64_t from = ((int64_t)kvh * rows + (pos - start)) * d;
+            memcpy((char *)pool + at * es, (const char *)src + from * es, (size_t)((end - pos) * d) * es);
+            pos = end;
+        }
+    }
+    return 0;
+}
+
+int oracle_gather(const uint32_t *table, int64_t table_len, int64_t lo, int64_t hi,
+                  const void *pool, void *out, int64_t n_blocks, int n_kv, int d, int dtype) {
+    size_t es = dtype == 1 ? 2 : 4;
+    if (!kv_range_ok(table, table_len, lo, hi, n_blocks)) return -1;
+    char *o = (char *)out;
+    for (int kvh = 0; kvh < n_kv; kvh++) {
+        int64_t pos = lo;
+        while (pos < hi) {
+            int64_t blk_end = (pos / KV_BLOCK + 1) * KV_BLOCK;
+            int64_t end = hi < blk_end ? hi : blk_end;
+            int64_t at = kv_row_offset(table, pos, kvh, n_kv, d);
+            size_t n = (size_t)((end - pos) * d) * es;
+            memcpy(o, (const char *)pool + at * es, n);
+            o += n;
+            pos = end;
+        }
+    }
+    return 0;
+}

@@ -98,6 +98,22 @@ void oracle_rope(void *x, int64_t ld, int64_t rows, int heads, int head_dim,
                  const int32_t *positions, const float *norm_w, float eps,
                  int dtype, int nthreads);
 
+/* Paged K/V pools (cpu/paged_attn.rs:1-38): [n_blocks][n_kv][16][d]
+ * elements of `dtype` (1 = f16, else f32); position p of a sequence is row
+ * p % 16 of block table[p / 16] (paged.rs:9-16), KV head kvh of it starts at
+ * ((block * n_kv + kvh) * 16 + p % 16) * d (row_offset, :33-38).
+ *
+ * store_rows (:370-400): positions start..start+rows of src [n_kv][rows][d]
+ * into the pool.  gather (:340-362): positions lo..hi of the pool into
+ * out [n_kv][hi-lo][d].  Both check the range first as check_range does
+ * (:42-65) and return -1, writing nothing, when a position has no block
+ * (past the table, 0xffffffff, or an id >= n_blocks); 0 otherwise. */
+int oracle_store_rows(const uint32_t *table, int64_t table_len, int64_t start, int64_t rows,
+                      const void *src, void *pool, int64_t n_blocks, int n_kv, int d,
+                      int dtype);
+int oracle_gather(const uint32_t *table, int64_t table_len, int64_t lo, int64_t hi,
+                  const void *pool, void *out, int64_t n_blocks, int n_kv, int d, int dtype);
+
 #ifdef __cplusplus
 }
 #endif

@@ -58,6 +58,10 @@ def lib():
                                          _p, _i64, _p, _p]
         L.oracle_rope.argtypes = [_p, _i64, _i64, _int, _int, _int, _int, _p, _p, _p, _p,
                                   _f32, _int, _int]
+        L.oracle_store_rows.restype = _int
+        L.oracle_store_rows.argtypes = [_p, _i64, _i64, _i64, _p, _p, _i64, _int, _int, _int]
+        L.oracle_gather.restype = _int
+        L.oracle_gather.argtypes = [_p, _i64, _i64, _i64, _p, _p, _i64, _int, _int, _int]
         _LIB = L
     return _LIB
 
@@ -175,3 +179,65 @@ def rope(x, cos, sin, positions, kind, n_dims=None, norm_w=None, eps=1e-6, threa
     lib().oracle_rope(_ptr(x), heads * d, rows, heads, d, n_dims, kind, _ptr(cos),
                       _ptr(sin), _ptr(pos), _ptr(nw), eps, _dtype_code(x), threads)
     return x
+
+
+KV_BLOCK = 16
+NO_BLOCK = 0xFFFFFFFF
+
+
+class KvError(ValueError):
+    """A position without a K/V block (check_range, cpu/paged_attn.rs:42-65)."""
+
+
+def store_rows(table, start, src, pool):
+    """store_rows (cpu/paged_attn.rs:370-400): src [n_kv, rows, d] into the
+    positions start.. of `pool` [n_blocks, n_kv, 16, d] (modified in place)."""
+    n_blocks, n_kv, bs, d = pool.shape
+    assert bs == KV_BLOCK and pool.flags.c_contiguous and src.dtype == pool.dtype
+    src = np.ascontiguousarray(src)
+    assert src.shape[0] == n_kv and src.shape[2] == d
+    tab = np.ascontiguousarray(table, dtype=np.uint32)
+    rc = lib().oracle_store_rows(_ptr(tab), tab.size, start, src.shape[1], _ptr(src), _ptr(pool),
+                                 n_blocks, n_kv, d, _dtype_code(pool))
+    if rc != 0:
+        raise KvError(f"position range {start}..{start + src.shape[1]} has no K/V block")
+    return pool
+
+
+def gather(table, lo, hi, pool):
+    """gather (cpu/paged_attn.rs:340-362): positions lo..hi of `pool` as
+    [n_kv, hi - lo, d]."""
+    n_blocks, n_kv, bs, d = pool.shape
+    pool = np.ascontiguousarray(pool)
+    tab = np.ascontiguousarray(table, dtype=np.uint32)
+    out = np.empty((n_kv, hi - lo, d), pool.dtype)
+    rc = lib().oracle_gather(_ptr(tab), tab.size, lo, hi, _ptr(pool), _ptr(out), n_blocks, n_kv,
+                             d, _dtype_code(pool))
+    if rc != 0:
+        raise KvError(f"position range {lo}..{hi} has no K/V block")
+    return out
+
+
+def store_kv(q, k, v, cos, sin, kind, n_dims, calls, pool_k, pool_v, q_norm_w=None,
+             k_norm_w=None, v_norm=False, eps=1e-6, threads=1):
+    """store_kv (cpu.rs:3028-3097) for the rows of several calls: q, k, v
+    [rows, heads, d]; calls = [(offset, start, rope_start, t, table)], the
+    call's rows offset.. at cache indices start.. and RoPE positions
+    rope_start.. (AttnCall, cpu.rs:1314-1325).  Q and K are normalised
+    (per head) and rotated, V normalised without a weight when v_norm
+    (gpu.rs:5277), K and V stored into the pools (modified in place).
+    Returns the rotated Q."""
+    rows, nk, d = k.shape
+    pos = np.zeros(rows, np.int32)
+    for off, start, rope_start, t, table in calls:
+        pos[off:off + t] = np.arange(rope_start, rope_start + t)
+    qr = rope(q, cos, sin, pos, kind, n_dims, norm_w=q_norm_w, eps=eps, threads=threads)
+    kr = rope(k, cos, sin, pos, kind, n_dims, norm_w=k_norm_w, eps=eps, threads=threads)
+    vv = np.ascontiguousarray(v)
+    if v_norm:
+        _, h = add_rmsnorm(vv.reshape(rows * nk, d), None, None, eps, threads=threads, write_x=False)
+        vv = h.reshape(rows, nk, d)
+    for off, start, rope_start, t, table in calls:
+        store_rows(table, start, kr[off:off + t].transpose(1, 0, 2), pool_k)
+        store_rows(table, start, vv[off:off + t].transpose(1, 0, 2), pool_v)
+    return qr

@@ -123,6 +123,56 @@ int main() {
         ctx.check_device();
         std::printf("ok RopeSpec::tables / apply_rope\n");
     }
+    {  // KvPool::slots + store_kv (NEOX, f32), bit-exact against rope + store_rows
+        const int64_t rows = 21, nq = 4, nk = 2, d = 64, n_blocks = 6, start = 9;
+        const std::vector<uint32_t> table = {5, 1, 3};
+        cuca::KvPool pool(ctx, n_blocks, nk, d, cuca::DType::F32);
+        const auto slots = pool.slots(table, start, rows);
+        auto spec = cuca::RopeSpec::plain(cuca::RopeKind::Neox, (int32_t)d, 1e4);
+        auto t = spec.tables(nullptr, 64);
+        auto q = normal(g, rows * nq * d), k = normal(g, rows * nk * d), v = normal(g, rows * nk * d);
+        std::vector<int32_t> pos(rows);
+        for (int64_t i = 0; i < rows; i++) pos[i] = (int32_t)(start + i);
+        auto dq = ctx.tensor(q, {rows, nq, d}, cuca::DType::F32);
+        auto dk = ctx.tensor(k, {rows, nk, d}, cuca::DType::F32);
+        auto dv = ctx.tensor(v, {rows, nk, d}, cuca::DType::F32);
+        auto dc = ctx.tensor(t.cos, {64, d / 2}, cuca::DType::F32);
+        auto ds = ctx.tensor(t.sin, {64, d / 2}, cuca::DType::F32);
+        auto dp = ctx.tensor(pos, {rows}, cuca::DType::I32);
+        auto dsl = ctx.tensor(slots, {rows}, cuca::DType::I32);
+        pool.store_kv(ctx, dq, dk, dv, dc, ds, cuca::RopeKind::Neox, (int32_t)d, dp, dsl);
+        ctx.check_device();
+        std::vector<float> wq = q, wk = k;
+        oracle_rope(wq.data(), nq * d, rows, (int)nq, (int)d, (int)d, OR_ROPE_NEOX, t.cos.data(), t.sin.data(),
+                    pos.data(), nullptr, 1e-6f, OR_F32, 1);
+        oracle_rope(wk.data(), nk * d, rows, (int)nk, (int)d, (int)d, OR_ROPE_NEOX, t.cos.data(), t.sin.data(),
+                    pos.data(), nullptr, 1e-6f, OR_F32, 1);
+        // store_rows takes [n_kv][rows][d]
+        std::vector<float> sk(wk.size()), sv(v.size());
+        for (int64_t r = 0; r < rows; r++)
+            for (int64_t h = 0; h < nk; h++)
+                for (int64_t e = 0; e < d; e++) {
+                    sk[(h * rows + r) * d + e] = wk[(r * nk + h) * d + e];
+                    sv[(h * rows + r) * d + e] = v[(r * nk + h) * d + e];
+                }
+        std::vector<float> pk((size_t)(n_blocks * nk * 16 * d), 0.0f), pv = pk;
+        EXPECT(oracle_store_rows(table.data(), (int64_t)table.size(), start, rows, sk.data(), pk.data(), n_blocks,
+                                 (int)nk, (int)d, OR_F32) == 0, "oracle store k");
+        EXPECT(oracle_store_rows(table.data(), (int64_t)table.size(), start, rows, sv.data(), pv.data(), n_blocks,
+                                 (int)nk, (int)d, OR_F32) == 0, "oracle store v");
+        EXPECT(std::memcmp(dq.download<float>().data(), wq.data(), wq.size() * 4) == 0, "q not bit-exact");
+        EXPECT(std::memcmp(pool.k().download<float>().data(), pk.data(), pk.size() * 4) == 0, "pool k");
+        EXPECT(std::memcmp(pool.v().download<float>().data(), pv.data(), pv.size() * 4) == 0, "pool v");
+        bool threw = false;
+        try {
+            (void)pool.slots({5, CUCA_NO_BLOCK}, 0, 20);
+        } catch (const cuca::Error &e) {
+            threw = e.status == CUCA_OUT_OF_RANGE &&
+                    std::string(e.what()).find("position 16 has no K/V block") != std::string::npos;
+        }
+        EXPECT(threw, "a released block must be rejected");
+        std::printf("ok KvPool::slots / store_kv\n");
+    }
     {  // errors carry the library's message
         bool threw = false;
         try {

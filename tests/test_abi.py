@@ -87,3 +87,25 @@ def test_ops_validate_on_the_host_before_any_device_work():
     with pytest.raises(hip.CucaError, match="do not hold 2 rows"):
         ops.TokenEmbedding(None, hip.GGML_Q4_0, np.zeros(18, np.uint8), 2, 32)
 
+
+
+def test_kv_slots_place_rows_where_store_rows_does():
+    rng = np.random.default_rng(5)
+    n_kv, d = 3, 4
+    for table, start, t in [([5, 0, 9, 2], 0, 64), ([5, 0, 9, 2], 13, 40), ([7], 3, 1),
+                            ([1, 2], 15, 2)]:
+        slots = hip.kv_slots(table, start, t, 10)
+        src = rng.standard_normal((n_kv, t, d)).astype(np.float32)
+        want = np.zeros((10, n_kv, 16, d), np.float32)
+        O.store_rows(table, start, src, want)
+        got = np.zeros_like(want)
+        got[slots // 16, :, slots % 16, :] = src.transpose(1, 0, 2)
+        assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("table,start,t,where", [
+    ([3, hip.NO_BLOCK], 0, 20, 16), ([3], 10, 10, 16), ([3, 10], 0, 20, 16)])
+def test_kv_slots_reject_positions_without_a_block(table, start, t, where):
+    with pytest.raises(hip.CucaError, match=f"position {where} has no K/V block "
+                       r"\(it left the window or was never allocated\)"):
+        hip.kv_slots(table, start, t, 10)
