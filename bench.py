@@ -365,6 +365,70 @@ def kv_store_bench(ctx, torch, name, n, dtype, steps=20, warmup=5):
                 unfused_us=round(un_ms * 1000, 2), verified_rows=int(sm.size))
 
 
+def attn_bench(ctx, torch, name, rows, ctx_len, dtype, steps=20, warmup=5):
+    """Paged decode attention (cuca_hip_paged_decode): `rows` sequences of
+    config `name`, each with one query row over ctx_len keys in scrambled
+    blocks of a shared pool.  Algorithmic bytes: the keys and values of the
+    ranges (2 ctx_len n_kv d s per row) plus q and out.  Reports the split
+    and merge kernels and the total, and checks two rows against the oracle."""
+    import numpy as np
+    from cuca_amd import hip
+    from cuca_amd import workloads as W
+    from oracle import oracle as O
+    cfg = W.CONFIGS[name]
+    d, nq, nk = cfg["head_dim"], cfg["nq"], cfg["nk"]
+    dt = hip.F16 if dtype == "f16" else hip.F32
+    tdt = torch.float16 if dtype == "f16" else torch.float32
+    s = 2 if dtype == "f16" else 4
+    nb_row = ctx_len // hip.KV_BLOCK
+    n_blocks = rows * nb_row + 16
+    gen = torch.Generator(device="cuda").manual_seed(cfg["seed"] * 11 + rows)
+    pk = torch.randn((n_blocks, nk, hip.KV_BLOCK, d), device="cuda", generator=gen).to(tdt)
+    pv = torch.randn((n_blocks, nk, hip.KV_BLOCK, d), device="cuda", generator=gen).to(tdt)
+    q = torch.randn((rows, nq, d), device="cuda", generator=gen).to(tdt)
+    out = torch.empty_like(q)
+    tables = np.random.default_rng(rows).permutation(n_blocks)[:rows * nb_row].reshape(rows, nb_row)
+    dtab = torch.from_numpy(tables.astype(np.int32)).cuda()
+    ranges = np.tile(np.array([0, ctx_len], np.int32), (rows, 1))
+    drng = torch.from_numpy(ranges).cuda()
+    wsb = hip.paged_decode_workspace(rows, nq, d, nb_row)
+    ws = torch.empty(max(wsb, 16), dtype=torch.uint8, device="cuda")
+    scale = 1.0 / float(np.sqrt(d))
+
+    def call():
+        ctx.paged_decode(q.data_ptr(), pk.data_ptr(), pv.data_ptr(), n_blocks, dtab.data_ptr(),
+                         nb_row, drng.data_ptr(), rows, nq, nk, d, scale, ws.data_ptr(), wsb,
+                         out.data_ptr(), dt)
+    for _ in range(warmup):
+        call()
+    torch.cuda.synchronize()
+    ctx.profile_start(2 * steps)
+    for _ in range(steps):
+        call()
+    recs = ctx.profile_stop()
+    ctx.check_device()
+    split_ms = sum(t for k, t in recs[0::2]) / steps
+    merge_ms = sum(t for k, t in recs[1::2]) / steps
+    total_ms = time_steps(torch, call, steps, warmup)
+    call()
+    torch.cuda.synchronize()
+    chk = [0, rows - 1]
+    got = out[chk].cpu().numpy()
+    want = O.paged_attention(q[chk].cpu().numpy(), tables[chk].astype(np.uint32), ranges[chk],
+                             pk.cpu().numpy(), pv.cpu().numpy(), scale, threads=8)
+    err = np.max(np.abs(got.astype(np.float64) - want) / (1e-5 + np.abs(want.astype(np.float64))))
+    vmax = float(pv.abs().max().item())
+    assert np.max(np.abs(got.astype(np.float64) - want)) <= (
+        2 * np.spacing(np.abs(want).astype(np.float16)).astype(np.float64).max() if dtype == "f16" else 0
+    ) + 1e-5 * (np.abs(want).max() + vmax), err
+    b = rows * (2 * ctx_len * nk * d * s + 2 * nq * d * s)
+    return dict(kernels=[recs[0][0], recs[1][0]], split_us=round(split_ms * 1000, 2),
+                merge_us=round(merge_ms * 1000, 2), us=round(total_ms * 1000, 2), bytes=b,
+                gbs=round(b / (total_ms / 1e3) / 1e9, 1),
+                frac=round(b / (total_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4),
+                split_frac=round(b / (split_ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4))
+
+
 class DecodeLayers:
     """32 layers of the decode step's non-matmul ops (config B, f32)."""
 
@@ -487,6 +551,7 @@ def main():
     ap.add_argument("--no-large", action="store_true", help="skip the 16384-token step")
     ap.add_argument("--no-configs", action="store_true", help="skip the A/B/D/E config steps")
     ap.add_argument("--no-kv", action="store_true", help="skip the fused RoPE + paged K/V store")
+    ap.add_argument("--no-attn", action="store_true", help="skip the paged decode attention")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: these ops run on one GPU's share of the work and "
@@ -572,6 +637,17 @@ def main():
             kv[f"{name}_{n}_{dtype}"] = r
         torch.cuda.empty_cache()
 
+    attn = None
+    if not args.no_attn:
+        log("paged decode attention")
+        attn = {}
+        for name, rows, clen, dtype in (("B", 1, 8192, "f16"), ("B", 32, 8192, "f16"),
+                                        ("B", 64, 8192, "f16"), ("B", 32, 8192, "f32"),
+                                        ("B", 8, 32768, "f16"), ("E", 32, 8192, "f16")):
+            attn[f"{name}_b{rows}_{clen}_{dtype}"] = attn_bench(ctx, torch, name, rows, clen, dtype)
+            checked_rows += 2
+        torch.cuda.empty_cache()
+
     decode = None
     if not args.no_decode:
         log("decode graphs")
@@ -612,6 +688,7 @@ def main():
         "prefill_16384": big,
         "configs": configs,
         "rope_store_kv": kv,
+        "paged_decode": attn,
         "decode_us_per_layer": decode,
         "roofline": {"kernel": glu["kernel"], "bound": "hbm",
                      "achieved": glu["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",

@@ -17,7 +17,13 @@ extern "C" {
 /* Device status words, one per kind of bad input the kernels can meet.
  * Each holds (row << 32 | value) of the smallest bad row seen, or all
  * ones.  The host resets them after reading (cuca_hip_check_device). */
-enum { CUCA_STATUS_EMBED_ID = 0, CUCA_STATUS_ROPE_POS = 1, CUCA_STATUS_KV_SLOT = 2, CUCA_STATUS_WORDS = 4 };
+enum {
+    CUCA_STATUS_EMBED_ID = 0,
+    CUCA_STATUS_ROPE_POS = 1,
+    CUCA_STATUS_KV_SLOT = 2,
+    CUCA_STATUS_KV_RANGE = 3, /* attention: a key position without a block, or a bad range */
+    CUCA_STATUS_WORDS = 4
+};
 
 typedef struct {
     const uint8_t *table;   /* [vocab, row_bytes]                          */
@@ -90,6 +96,28 @@ typedef struct {
     int32_t nv;             /* V heads: nk for the store, else 0            */
     int32_t v_norm;         /* weightless RMSNorm of V before the store     */
 } RopeArgs;
+
+/* Paged decode attention: split pass (partials over `part_positions` key
+ * positions each) and merge pass (one wave per row and query head).
+ * part: [rows, n_head, max_parts, head_dim + 2] f32 partials (value
+ * accumulator, maximum, sum).  CUCA_ATTN_MIN_PART bounds part_positions
+ * from below (it sizes the workspace). */
+#define CUCA_ATTN_MIN_PART 64
+typedef struct {
+    const void *q;          /* [rows, n_head, d]                            */
+    const void *pool_k;     /* [n_blocks, n_kv, 16, d]                      */
+    const void *pool_v;
+    const uint32_t *tables; /* [rows, max_blocks]                           */
+    const int32_t *ranges;  /* [rows, 2]: lo, hi relative to the table      */
+    float *part;
+    void *out;              /* [rows, n_head, d]                            */
+    unsigned long long *status;
+    int64_t n_blocks;
+    int32_t rows, n_head, n_kv, head_dim;
+    int32_t max_blocks, max_parts;
+    int32_t part_positions; /* key positions per partial                    */
+    float scale;
+} AttnArgs;
 
 #ifdef __cplusplus
 }

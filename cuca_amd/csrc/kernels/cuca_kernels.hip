@@ -9,3 +9,4 @@
 #include "norm.hip"
 #include "glu.hip"
 #include "rope.hip"
+#include "attn.hip"

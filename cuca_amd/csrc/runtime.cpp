@@ -311,9 +311,18 @@ cuca_status cuca_hip_check_device(cuca_hip_ctx *ctx) {
         return fail(ctx, CUCA_OUT_OF_RANGE, "position %d outside the rope table of %lld rows (row %u)",
                     (int)(v & 0xffffffffu), (long long)ctx->last_table_rows, (unsigned)(v >> 32));
     }
-    unsigned long long v = w[CUCA_STATUS_KV_SLOT];
-    return fail(ctx, CUCA_OUT_OF_RANGE, "K/V slot %d outside the pool of %lld blocks (row %u)",
-                (int)(v & 0xffffffffu), (long long)ctx->last_kv_blocks, (unsigned)(v >> 32));
+    if (w[CUCA_STATUS_KV_SLOT] != none) {
+        unsigned long long v = w[CUCA_STATUS_KV_SLOT];
+        return fail(ctx, CUCA_OUT_OF_RANGE, "K/V slot %d outside the pool of %lld blocks (row %u)",
+                    (int)(v & 0xffffffffu), (long long)ctx->last_kv_blocks, (unsigned)(v >> 32));
+    }
+    unsigned long long v = w[CUCA_STATUS_KV_RANGE];
+    if ((v & 0xffffffffu) == 0xffffffffu)
+        return fail(ctx, CUCA_OUT_OF_RANGE, "attention row %u: empty key range, or one past its block table",
+                    (unsigned)(v >> 32));
+    return fail(ctx, CUCA_OUT_OF_RANGE,
+                "attention row %u: position %u has no K/V block (it left the window or was never allocated)",
+                (unsigned)(v >> 32), (unsigned)(v & 0xffffffffu));
 }
 
 // ---------------------------------------------------------------------
@@ -700,6 +709,117 @@ cuca_status cuca_hip_kv_slots(const uint32_t *table, int64_t table_len, int64_t 
         slots_out[i] = (int32_t)((int64_t)id * CUCA_KV_BLOCK + p % CUCA_KV_BLOCK);
     }
     return CUCA_OK;
+}
+
+// ---------------------------------------------------------------------
+// paged decode attention
+// ---------------------------------------------------------------------
+
+// Partials a row of max_blocks blocks can need: parts are never shorter
+// than CUCA_ATTN_MIN_PART positions.
+static int64_t attn_max_parts(int64_t max_blocks, int64_t part_positions) {
+    return (max_blocks * CUCA_KV_BLOCK + part_positions - 1) / part_positions;
+}
+
+cuca_status cuca_hip_paged_decode_workspace(int64_t rows, int32_t n_head, int32_t head_dim,
+                                            int64_t max_blocks, size_t *bytes) {
+    if (!bytes) return fail(nullptr, CUCA_INVALID_ARG, "null output pointer");
+    if (rows < 0 || n_head <= 0 || head_dim <= 0 || max_blocks <= 0)
+        return fail(nullptr, CUCA_INVALID_ARG, "bad attention shape");
+    *bytes = (size_t)rows * (size_t)n_head * (size_t)attn_max_parts(max_blocks, CUCA_ATTN_MIN_PART) *
+             (size_t)(head_dim + 2) * sizeof(float);
+    return CUCA_OK;
+}
+
+cuca_status cuca_hip_paged_decode(cuca_hip_ctx *ctx, const void *q, const void *pool_k, const void *pool_v,
+                                  int64_t n_blocks, const uint32_t *tables, int64_t max_blocks,
+                                  const int32_t *ranges, int64_t rows, int32_t n_head, int32_t n_kv,
+                                  int32_t head_dim, float scale, void *workspace, size_t workspace_bytes,
+                                  void *out, cuca_dtype dtype) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    if (!dtype_ok(dtype)) return fail(ctx, CUCA_INVALID_ARG, "bad dtype %d", (int)dtype);
+    if (rows < 0) return fail(ctx, CUCA_INVALID_ARG, "negative count");
+    if (n_head <= 0 || n_kv <= 0 || n_head % n_kv != 0)
+        return fail(ctx, CUCA_INVALID_ARG, "attention: query shape mismatch (%d heads over %d KV heads)",
+                    n_head, n_kv);
+    if (head_dim <= 0 || head_dim > 512) return fail(ctx, CUCA_UNSUPPORTED, "head_dim %d above 512", head_dim);
+    if (max_blocks <= 0 || max_blocks > (1 << 22))
+        return fail(ctx, CUCA_INVALID_ARG, "bad block table width %lld", (long long)max_blocks);
+    if (n_blocks <= 0) return fail(ctx, CUCA_INVALID_ARG, "bad pool size %lld blocks", (long long)n_blocks);
+    if (rows == 0) return CUCA_OK;
+    if (!q || !pool_k || !pool_v || !tables || !ranges || !out || !workspace)
+        return fail(ctx, CUCA_INVALID_ARG, "null pointer");
+    size_t need = 0;
+    cuca_hip_paged_decode_workspace(rows, n_head, head_dim, max_blocks, &need);
+    if (workspace_bytes < need)
+        return fail(ctx, CUCA_INVALID_ARG, "workspace of %zu bytes, %zu needed", workspace_bytes, need);
+    if (!al16(workspace)) return fail(ctx, CUCA_INVALID_ARG, "workspace must be 16-byte aligned");
+    const bool f16 = dtype == CUCA_F16;
+    const size_t es = esize(dtype);
+    const int G = n_head / n_kv;
+    const int di = head_dim == 64 ? 0 : head_dim == 128 ? 1 : head_dim == 256 ? 2 : -1;
+    const int gi = G == 1 ? 0 : G == 2 ? 1 : G == 4 ? 2 : G == 8 ? 3 : -1;
+    const bool vec = di >= 0 && gi >= 0 && !(di == 2 && gi == 3) && al16(pool_k) && al16(pool_v) &&
+                     ((size_t)head_dim * es) % 16 == 0;
+    // vector kernel: a part = 4 waves x CP positions, CP = 64 / LPP with
+    // LPP = max(1, row bytes / 256), and at least 2 for a group of 8;
+    // generic: a part = 64 positions
+    int64_t part_positions = CUCA_ATTN_MIN_PART;
+    if (vec) {
+        const int64_t rowb = (int64_t)head_dim * (int64_t)es;
+        int64_t lpp = rowb > 256 ? rowb / 256 : 1;
+        if (G >= 8 && lpp < 2) lpp = 2;
+        part_positions = 4 * (64 / lpp);
+    }
+    const int64_t parts = attn_max_parts(max_blocks, part_positions);
+    if (rows * n_head * parts > 0x7fffffffll) return fail(ctx, CUCA_UNSUPPORTED, "too many attention parts");
+    AttnArgs a{};
+    a.q = q;
+    a.pool_k = pool_k;
+    a.pool_v = pool_v;
+    a.tables = tables;
+    a.ranges = ranges;
+    a.part = static_cast<float *>(workspace);
+    a.out = out;
+    a.status = ctx->status;
+    a.n_blocks = n_blocks;
+    a.rows = (int32_t)rows;
+    a.n_head = n_head;
+    a.n_kv = n_kv;
+    a.head_dim = head_dim;
+    a.max_blocks = (int32_t)max_blocks;
+    a.max_parts = (int32_t)parts;
+    a.part_positions = (int32_t)part_positions;
+    a.scale = scale;
+    Kernel split;
+    unsigned grid;
+    if (vec) {
+        // [dtype][head_dim 64/128/256][group 1/2/4/8]; no d256 x 8 kernel
+        static const Kernel ks[2][3][4] = {
+            {{cuca_attn_split_f32_d64_g1, cuca_attn_split_f32_d64_g2, cuca_attn_split_f32_d64_g4,
+              cuca_attn_split_f32_d64_g8},
+             {cuca_attn_split_f32_d128_g1, cuca_attn_split_f32_d128_g2, cuca_attn_split_f32_d128_g4,
+              cuca_attn_split_f32_d128_g8},
+             {cuca_attn_split_f32_d256_g1, cuca_attn_split_f32_d256_g2, cuca_attn_split_f32_d256_g4, KERNEL_COUNT}},
+            {{cuca_attn_split_f16_d64_g1, cuca_attn_split_f16_d64_g2, cuca_attn_split_f16_d64_g4,
+              cuca_attn_split_f16_d64_g8},
+             {cuca_attn_split_f16_d128_g1, cuca_attn_split_f16_d128_g2, cuca_attn_split_f16_d128_g4,
+              cuca_attn_split_f16_d128_g8},
+             {cuca_attn_split_f16_d256_g1, cuca_attn_split_f16_d256_g2, cuca_attn_split_f16_d256_g4, KERNEL_COUNT}}};
+        split = ks[f16][di][gi];
+        grid = (unsigned)(rows * n_kv * parts); // a workgroup per (row, KV head, part)
+    } else {
+        split = f16 ? cuca_attn_split_f16_generic : cuca_attn_split_f32_generic;
+        grid = div_up(rows * n_head * parts, 4); // a wave per (row, head, part)
+    }
+    if ((st = launch(ctx, split, grid, 256, 0, a)) != CUCA_OK) return st;
+    static const Kernel km[2][4] = {
+        {cuca_attn_merge_f32_c1, cuca_attn_merge_f32_c2, cuca_attn_merge_f32_c4, cuca_attn_merge_f32_c8},
+        {cuca_attn_merge_f16_c1, cuca_attn_merge_f16_c2, cuca_attn_merge_f16_c4, cuca_attn_merge_f16_c8}};
+    const int cpl = (head_dim + 63) / 64;
+    const int ci = cpl <= 1 ? 0 : cpl <= 2 ? 1 : cpl <= 4 ? 2 : 3;
+    return launch(ctx, km[f16][ci], div_up(rows * n_head, 4), 256, 0, a);
 }
 
 // RopeSpec::tables (rope.rs:118-151): f64 angles with the platform libm,

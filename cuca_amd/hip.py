@@ -68,6 +68,9 @@ SIGNATURES = {
                                      _st, _p, _p, _i64, _p, _p, _p, _i32, _f32, _p, _p, _i64, _p,
                                      _st]),
     "cuca_hip_kv_slots": (_st, [_p, _i64, _i64, _i64, _i64, _p]),
+    "cuca_hip_paged_decode_workspace": (_st, [_i64, _i32, _i32, _i64, ctypes.POINTER(_sz)]),
+    "cuca_hip_paged_decode": (_st, [_p, _p, _p, _p, _i64, _p, _i64, _p, _i64, _i32, _i32, _i32,
+                                    _f32, _p, _sz, _p, _st]),
     "cuca_hip_rope_tables": (_st, [ctypes.POINTER(RopeSpecC), _p, _i64, _p, _p]),
     "cuca_hip_graph_begin": (_st, [_p]),
     "cuca_hip_graph_end": (_st, [_p, _pp]),
@@ -296,6 +299,12 @@ class Context:
                                         kind, cos, sin, table_rows, positions, q_norm_w, k_norm_w,
                                         eps, dtype))
 
+    def paged_decode(self, q, pool_k, pool_v, n_blocks, tables, max_blocks, ranges, rows, n_head,
+                     n_kv, head_dim, scale, workspace, workspace_bytes, out, dtype):
+        self.check(self.L.cuca_hip_paged_decode(self.ptr, q, pool_k, pool_v, n_blocks, tables,
+                                                max_blocks, ranges, rows, n_head, n_kv, head_dim,
+                                                scale, workspace, workspace_bytes, out, dtype))
+
     def rope_store_kv(self, q, q_ld, k, k_ld, v, v_ld, rows, nq, nk, head_dim, n_dims, kind, cos,
                       sin, table_rows, positions, q_norm_w, k_norm_w, v_norm, eps, pool_k, pool_v,
                       n_blocks, slots, dtype):
@@ -327,6 +336,14 @@ class Graph:
 
 KV_BLOCK = 16          # positions per paged K/V block (paged.rs:45)
 NO_BLOCK = 0xFFFFFFFF  # a released block's table entry (paged.rs:49)
+
+
+def paged_decode_workspace(rows, n_head, head_dim, max_blocks):
+    """Bytes of workspace cuca_hip_paged_decode needs (host)."""
+    out = _sz(0)
+    _check(lib().cuca_hip_paged_decode_workspace(rows, n_head, head_dim, max_blocks,
+                                                 ctypes.byref(out)), None)
+    return out.value
 
 
 def kv_slots(table, start, t, n_blocks):

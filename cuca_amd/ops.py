@@ -218,6 +218,25 @@ class KvPool:
                           hip.dtype_code(q.dtype))
         return q
 
+    def decode(self, q, tables, ranges, n_head, scale, workspace=None):
+        """Paged decode attention of q [rows, n_head, d] (one query row per
+        sequence) over this pool (paged_kernel.rs decode, gpu.rs:6002-6011):
+        tables device u32 [rows, max_blocks], ranges device int32 [rows, 2]
+        (lo, hi).  Returns a DeviceArray [rows, n_head, d].  `workspace`: a
+        DeviceArray of at least paged_decode_workspace bytes, or one is made."""
+        rows, nh, d = q.shape
+        if nh != n_head or d != self.head_dim:
+            raise CucaError(hip.INVALID_ARG, "attention: query shape mismatch")
+        max_blocks = tables.shape[1]
+        need = hip.paged_decode_workspace(rows, n_head, d, max_blocks)
+        if workspace is None:
+            workspace = self.ctx.empty((max(need, 16),), np.uint8)
+        out = self.ctx.empty((rows, n_head, d), q.dtype)
+        self.ctx.paged_decode(q.ptr, self.k.ptr, self.v.ptr, self.n_blocks, tables.ptr, max_blocks,
+                              ranges.ptr, rows, n_head, self.n_kv_head, d, scale, workspace.ptr,
+                              workspace.nbytes, out.ptr, hip.dtype_code(q.dtype))
+        return out
+
     def read(self, slots):
         """The rows `slots` name, the inverse of the store (KvPool::read,
         gpu.rs:1808-1830): host (k, v) [len(slots), n_kv_head, head_dim]."""

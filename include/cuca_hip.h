@@ -24,6 +24,8 @@
  *                          GPU k/v branch, KvPool::write  gpu.rs:5266-5285, 1786-1806
  *   cuca_hip_kv_slots      block-table positions -> pool  paged.rs:9-16, gpu.rs:1940-1975
  *                          rows (host)
+ *   cuca_hip_paged_decode  paged decode attention         paged_kernel.rs:92-282,
+ *                          (+ _workspace, host)           cpu/paged_attn.rs:105-290
  *
  * Conventions
  * - A context owns one device, one HIP stream (or borrows the caller's),
@@ -233,6 +235,34 @@ cuca_status cuca_hip_rope_store_kv(cuca_hip_ctx *ctx, void *q, int64_t q_ld, con
  * NO_BLOCK) or an id outside the pool of n_blocks. */
 cuca_status cuca_hip_kv_slots(const uint32_t *table, int64_t table_len, int64_t start, int64_t t,
                               int64_t n_blocks, int32_t *slots_out);
+
+/* Paged decode attention: one query row per sequence over its keys, read in
+ * place from the pools cuca_hip_rope_store_kv fills (the GPU engine's
+ * paged_attention_decode, paged_kernel.rs:92-282, on a step's stacked
+ * rows, gpu.rs:6002-6011; the CPU's attend_paged_rows for one row,
+ * cpu/paged_attn.rs:105-290).
+ *   q      : [rows, n_head, head_dim] of dtype
+ *   pools  : [n_blocks, n_kv, 16, head_dim] of dtype
+ *   tables : device u32 [rows, max_blocks] block ids; ranges: device int32
+ *            [rows, 2] = (lo, hi) key positions relative to the table (the
+ *            reference's BlockRead::Decode table and range)
+ *   out    : [rows, n_head, head_dim] of dtype
+ * Query head h reads KV head h / (n_head / n_kv); out = softmax(q.k * scale)
+ * . v over positions lo..hi-1, f32 throughout.  The keys are split into
+ * fixed chunks of 64 positions, merged in chunk order, so a row's result
+ * does not depend on the other rows of the call.  workspace: device, 16-byte
+ * aligned, at least cuca_hip_paged_decode_workspace bytes (the ops never
+ * allocate).  An empty range, a range past the table or a position whose
+ * block id is >= n_blocks is reported by cuca_hip_check_device (the row's
+ * output is then unspecified; zeros for a bad range). */
+cuca_status cuca_hip_paged_decode_workspace(int64_t rows, int32_t n_head, int32_t head_dim,
+                                            int64_t max_blocks, size_t *bytes);
+cuca_status cuca_hip_paged_decode(cuca_hip_ctx *ctx, const void *q, const void *pool_k,
+                                  const void *pool_v, int64_t n_blocks, const uint32_t *tables,
+                                  int64_t max_blocks, const int32_t *ranges, int64_t rows,
+                                  int32_t n_head, int32_t n_kv, int32_t head_dim, float scale,
+                                  void *workspace, size_t workspace_bytes, void *out,
+                                  cuca_dtype dtype);
 
 /* RopeSpec (rope.rs:62-79). yarn_ext_factor == 0 disables YaRN. */
 typedef struct {

@@ -472,3 +472,102 @@ int oracle_gather(const uint32_t *table, int64_t table_len, int64_t lo, int64_t 
     }
     return 0;
 }
+
+/* ---- paged attention (cpu/paged_attn.rs) ---- */
+
+/* dot (paged_attn.rs:67-82): eight independent lanes, fixed order */
+static float attn_dot(const float *a, const float *b, int n) {
+    float lanes[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int n8 = n / 8 * 8;
+    for (int j = 0; j < n8; j += 8)
+        for (int i = 0; i < 8; i++) lanes[i] += a[j + i] * b[j + i];
+    float sum = ((lanes[0] + lanes[4]) + (lanes[1] + lanes[5])) + ((lanes[2] + lanes[6]) + (lanes[3] + lanes[7]));
+    for (int j = n8; j < n; j++) sum += a[j] * b[j];
+    return sum;
+}
+
+typedef struct {
+    const void *q;
+    int n_head, n_kv, d;
+    const uint32_t *tables;
+    int64_t max_blocks;
+    const int32_t *ranges;
+    const void *pool_k, *pool_v;
+    float scale;
+    void *out;
+    int dtype;
+} attn_ctx;
+
+static void attn_load(const void *src, int64_t at, int n, int dtype, float *dst) {
+    if (dtype == 1) {
+        const uint16_t *h = (const uint16_t *)src + at;
+        for (int i = 0; i < n; i++) dst[i] = oracle_f16_to_f32(h[i]);
+    } else {
+        memcpy(dst, (const float *)src + at, sizeof(float) * (size_t)n);
+    }
+}
+
+static void attn_range(void *c, int64_t begin, int64_t end) {
+    attn_ctx *p = (attn_ctx *)c;
+    int d = p->d, group = p->n_head / p->n_kv;
+    float *qv = (float *)malloc(sizeof(float) * (size_t)d * 3);
+    float *row = qv + d, *acc = qv + 2 * d;
+    float scores[KV_BLOCK];
+    for (int64_t job = begin; job < end; job++) {
+        int64_t r = job / p->n_head;
+        int head = (int)(job % p->n_head), kvh = head / group;
+        const uint32_t *table = p->tables + r * p->max_blocks;
+        int64_t lo = p->ranges[2 * r], hi = p->ranges[2 * r + 1];
+        attn_load(p->q, job * d, d, p->dtype, qv);
+        /* attend_head (paged_attn.rs:115-176) */
+        for (int i = 0; i < d; i++) acc[i] = 0.0f;
+        float mx = -INFINITY, sum = 0.0f;
+        for (int64_t pos = lo; pos < hi;) {
+            int64_t blk_end = (pos / KV_BLOCK + 1) * KV_BLOCK;
+            int64_t e = hi < blk_end ? hi : blk_end;
+            int n = (int)(e - pos);
+            int64_t first = kv_row_offset(table, pos, kvh, p->n_kv, d);
+            float block_max = -INFINITY;
+            for (int j = 0; j < n; j++) {
+                attn_load(p->pool_k, first + (int64_t)j * d, d, p->dtype, row);
+                float sc = attn_dot(qv, row, d) * p->scale;
+                scores[j] = sc;
+                if (sc > block_max) block_max = sc;
+            }
+            if (block_max > mx) {
+                float corr = expf(mx - block_max);
+                sum *= corr;
+                for (int i = 0; i < d; i++) acc[i] *= corr;
+                mx = block_max;
+            }
+            for (int j = 0; j < n; j++) {
+                float pr = expf(scores[j] - mx);
+                sum += pr;
+                attn_load(p->pool_v, first + (int64_t)j * d, d, p->dtype, row);
+                for (int i = 0; i < d; i++) acc[i] += pr * row[i];
+            }
+            pos = e;
+        }
+        if (p->dtype == 1) {
+            uint16_t *o = (uint16_t *)p->out + job * d;
+            for (int i = 0; i < d; i++) o[i] = oracle_f32_to_f16(acc[i] / sum);
+        } else {
+            float *o = (float *)p->out + job * d;
+            for (int i = 0; i < d; i++) o[i] = acc[i] / sum;
+        }
+    }
+    free(qv);
+}
+
+int oracle_paged_attention(const void *q, int64_t rows, int n_head, int n_kv, int d,
+                           const uint32_t *tables, int64_t max_blocks, const int32_t *ranges,
+                           const void *pool_k, const void *pool_v, int64_t n_blocks, float scale,
+                           void *out, int dtype, int nthreads) {
+    if (n_kv <= 0 || n_head % n_kv != 0) return -1;
+    for (int64_t r = 0; r < rows; r++) /* check_range, every row first */
+        if (!kv_range_ok(tables + r * max_blocks, max_blocks, ranges[2 * r], ranges[2 * r + 1], n_blocks))
+            return -1;
+    attn_ctx c = {q, n_head, n_kv, d, tables, max_blocks, ranges, pool_k, pool_v, scale, out, dtype};
+    parallel_rows(nthreads, rows * n_head, attn_range, &c);
+    return 0;
+}

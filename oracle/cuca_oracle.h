@@ -114,6 +114,22 @@ int oracle_store_rows(const uint32_t *table, int64_t table_len, int64_t start, i
 int oracle_gather(const uint32_t *table, int64_t table_len, int64_t lo, int64_t hi,
                   const void *pool, void *out, int64_t n_blocks, int n_kv, int d, int dtype);
 
+/* attend_paged_rows (cpu/paged_attn.rs:105-290, attend_head :115-176) for
+ * `rows` query rows, each with its own block table tables[row][max_blocks]
+ * and key range ranges[row] = (lo, hi):
+ *   q   : [rows][n_head][d], pools [n_blocks][n_kv][16][d], out [rows][n_head][d]
+ *         (dtype 1 = f16, else f32; f16 values are widened, out rounded once)
+ * Query head h reads KV head h / (n_head / n_kv).  Per block of the range:
+ * scores dot(q, k) * scale (dot: eight lanes, paged_attn.rs:67-82), the
+ * block maximum, the running sum and accumulator rescaled by
+ * exp(max - block_max) when it grows, then p = exp(s - max), sum += p,
+ * acc += p * v; out = acc / sum.  Returns -1, computing nothing, when a row's
+ * range is empty or a position in it has no block (check_range); else 0. */
+int oracle_paged_attention(const void *q, int64_t rows, int n_head, int n_kv, int d,
+                           const uint32_t *tables, int64_t max_blocks, const int32_t *ranges,
+                           const void *pool_k, const void *pool_v, int64_t n_blocks, float scale,
+                           void *out, int dtype, int nthreads);
+
 #ifdef __cplusplus
 }
 #endif

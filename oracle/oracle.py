@@ -60,6 +60,9 @@ def lib():
                                   _f32, _int, _int]
         L.oracle_store_rows.restype = _int
         L.oracle_store_rows.argtypes = [_p, _i64, _i64, _i64, _p, _p, _i64, _int, _int, _int]
+        L.oracle_paged_attention.restype = _int
+        L.oracle_paged_attention.argtypes = [_p, _i64, _int, _int, _int, _p, _i64, _p, _p, _p,
+                                             _i64, _f32, _p, _int, _int]
         L.oracle_gather.restype = _int
         L.oracle_gather.argtypes = [_p, _i64, _i64, _i64, _p, _p, _i64, _int, _int, _int]
         _LIB = L
@@ -241,3 +244,24 @@ def store_kv(q, k, v, cos, sin, kind, n_dims, calls, pool_k, pool_v, q_norm_w=No
         store_rows(table, start, kr[off:off + t].transpose(1, 0, 2), pool_k)
         store_rows(table, start, vv[off:off + t].transpose(1, 0, 2), pool_v)
     return qr
+
+
+def paged_attention(q, tables, ranges, pool_k, pool_v, scale, threads=1):
+    """attend_paged_rows per row: q [rows, n_head, d]; tables u32 [rows,
+    max_blocks]; ranges int32 [rows, 2]; pools [n_blocks, n_kv, 16, d] of q's
+    dtype.  Returns [rows, n_head, d]; raises KvError for a bad range."""
+    q = np.ascontiguousarray(q)
+    rows, n_head, d = q.shape
+    n_blocks, n_kv, bs, d2 = pool_k.shape
+    assert bs == KV_BLOCK and d2 == d and pool_v.shape == pool_k.shape
+    assert pool_k.dtype == q.dtype == pool_v.dtype
+    tab = np.ascontiguousarray(tables, dtype=np.uint32).reshape(rows, -1)
+    rng = np.ascontiguousarray(ranges, dtype=np.int32).reshape(rows, 2)
+    pk, pv = np.ascontiguousarray(pool_k), np.ascontiguousarray(pool_v)
+    out = np.empty_like(q)
+    rc = lib().oracle_paged_attention(_ptr(q), rows, n_head, n_kv, d, _ptr(tab), tab.shape[1],
+                                      _ptr(rng), _ptr(pk), _ptr(pv), n_blocks, scale, _ptr(out),
+                                      _dtype_code(q), threads)
+    if rc != 0:
+        raise KvError("attention over an empty key range or a position without a K/V block")
+    return out

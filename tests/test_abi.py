@@ -109,3 +109,15 @@ def test_kv_slots_reject_positions_without_a_block(table, start, t, where):
     with pytest.raises(hip.CucaError, match=f"position {where} has no K/V block "
                        r"\(it left the window or was never allocated\)"):
         hip.kv_slots(table, start, t, 10)
+
+
+def test_kernels_bit_cast_no_vector_element_lvalue():
+    # hipcc (ROCm 7.2) compiled __builtin_bit_cast(T, v.y) of an ext-vector
+    # element to a read of element 0; the kernels cast whole vectors or
+    # values passed through a scalar instead
+    kdir = os.path.join(ROOT, "cuca_amd", "csrc", "kernels")
+    pat = re.compile(r"__builtin_bit_cast\([^,()]+,\s*[\w\[\]]+\.[xyzw]\s*\)")
+    for f in os.listdir(kdir):
+        text = open(os.path.join(kdir, f)).read()
+        text = re.sub(r"//[^\n]*", "", text)
+        assert not pat.search(text), (f, pat.search(text).group(0))

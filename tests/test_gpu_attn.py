@@ -1,0 +1,165 @@
+"""Paged decode attention on the GPU against the oracle (attend_paged_rows
+restated, per row).
+
+Bar: |got - want| <= 1e-5 |want| + 1e-5 max|v| (f32), 2 f16 ulps + the same
+floor (f16), where max|v| is the largest value magnitude of the row's range
+in that KV head: the output is a convex combination of the values, and the
+two sides sum the scores and the softmax in different orders (the reference
+holds its own GPU kernel to 1e-4 absolute, gpu.rs:8289-8350).
+
+Covers the reference GPU test's cases (scrambled blocks [7, 2, 11, 0, 9,
+4], lengths around block boundaries, a window floor with released blocks
+before it, heads 4/2 d 16, 6/2 d 8, 2/2 d 32 -- the generic kernel), the
+configs' head layouts (GQA groups 2, 4, 8; head_dim 128 and 256; f32 and
+f16) over contexts of 1 to 1000 keys, a row's bits alone and in a batch,
+bad ranges and blocks, workspace checks and config C at 8192 keys.
+"""
+import numpy as np
+import pytest
+
+from cuca_amd import hip, ops
+from cuca_amd import workloads as W
+from helpers import assert_bits_equal, assert_close
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+NP = {"f32": np.float32, "f16": np.float16}
+
+
+def floor_of(tables, ranges, pool_v, n_head):
+    """1e-5 x max |v| over each row's range, per (row, head), broadcast to d."""
+    rows = len(ranges)
+    n_kv, d = pool_v.shape[1], pool_v.shape[3]
+    f = np.zeros((rows, n_head, d))
+    for r in range(rows):
+        lo, hi = ranges[r]
+        vals = O.gather(tables[r], lo, hi, pool_v).astype(np.float64)  # [n_kv, l, d]
+        vmax = np.abs(vals).max(axis=(1, 2))
+        f[r] = 1e-5 * np.repeat(vmax, n_head // n_kv)[:, None]
+    return f
+
+
+def run(ctx, q, pk, pv, tables, ranges, n_head, scale):
+    rows, _, d = q.shape
+    n_blocks, n_kv = pk.shape[0], pk.shape[1]
+    pool = ops.KvPool(ctx, n_blocks, n_kv, d, q.dtype)
+    pool.k.upload(pk)
+    pool.v.upload(pv)
+    out = pool.decode(ctx.array(q), ctx.array(tables.astype(np.uint32)),
+                      ctx.array(ranges.astype(np.int32)), n_head, scale)
+    ctx.check_device()
+    return out.numpy()
+
+
+def check(ctx, q, pk, pv, tables, ranges, n_head, scale):
+    got = run(ctx, q, pk, pv, tables, ranges, n_head, scale)
+    want = O.paged_attention(q, tables, ranges, pk, pv, scale, threads=8)
+    assert_close(got, want, floor=floor_of(tables, ranges, pv, n_head), what="attention")
+    return got
+
+
+def test_the_reference_gpu_test_cases(ctx):
+    rng = np.random.default_rng(7)
+    n_blocks = 12
+    scrambled = [7, 2, 11, 0, 9, 4]
+    for nh, nkv, d in [(4, 2, 16), (6, 2, 8), (2, 2, 32)]:
+        pk = rng.standard_normal((n_blocks, nkv, 16, d)).astype(np.float32)
+        pv = rng.standard_normal((n_blocks, nkv, 16, d)).astype(np.float32)
+        tables, ranges = [], []
+        for hi in [1, 2, 15, 16, 17, 31, 32, 33, 70]:
+            los = sorted({0, max(hi - 5, 0)} | ({16} if hi > 17 else set()))
+            for lo in los:
+                t = list(scrambled)
+                t[:lo // 16] = [O.NO_BLOCK] * (lo // 16)
+                tables.append(t)
+                ranges.append((lo, hi))
+        tables, ranges = np.array(tables, np.uint32), np.array(ranges, np.int32)
+        q = (4.0 * rng.standard_normal((len(ranges), nh, d))).astype(np.float32)
+        check(ctx, q, pk, pv, tables, ranges, nh, 1.0 / np.sqrt(d))
+
+
+def make_batch(rng, lengths, n_blocks, width):
+    """Rows with the given key counts, some with a window floor, over
+    scrambled blocks of a shared pool."""
+    tables = np.full((len(lengths), width), O.NO_BLOCK, np.uint32)
+    ranges = np.zeros((len(lengths), 2), np.int32)
+    for r, hi in enumerate(lengths):
+        nb = (hi + 15) // 16
+        tables[r, :nb] = rng.choice(n_blocks, nb, replace=False)
+        lo = 0 if r % 3 else max(0, hi - 100)   # every third row: a window of 100
+        tables[r, :lo // 16] = O.NO_BLOCK
+        ranges[r] = (lo, hi)
+    return tables, ranges
+
+
+@pytest.mark.parametrize("cfg_name,dtype", [("A", "f32"), ("B", "f32"), ("C", "f16"),
+                                            ("D", "f32"), ("D", "f16"), ("E", "f32"),
+                                            ("E", "f16")])
+def test_configs(ctx, cfg_name, dtype):
+    cfg = W.CONFIGS[cfg_name]
+    rng = np.random.default_rng(cfg["seed"])
+    nq, nk, d = cfg["nq"], cfg["nk"], cfg["head_dim"]
+    lengths = [1, 15, 16, 17, 63, 64, 65, 129, 300, 1000]
+    n_blocks = 256
+    tables, ranges = make_batch(rng, lengths, n_blocks, 64)
+    pk = rng.standard_normal((n_blocks, nk, 16, d)).astype(NP[dtype])
+    pv = rng.standard_normal((n_blocks, nk, 16, d)).astype(NP[dtype])
+    q = (2.0 * rng.standard_normal((len(lengths), nq, d))).astype(NP[dtype])
+    check(ctx, q, pk, pv, tables, ranges, nq, 1.0 / np.sqrt(d))
+
+
+def test_a_row_is_bit_identical_alone_and_in_a_batch(ctx):
+    rng = np.random.default_rng(8)
+    nq, nk, d, n_blocks = 32, 8, 128, 128
+    tables, ranges = make_batch(rng, [700, 5, 64, 333], n_blocks, 48)
+    pk = rng.standard_normal((n_blocks, nk, 16, d)).astype(np.float32)
+    pv = rng.standard_normal((n_blocks, nk, 16, d)).astype(np.float32)
+    q = rng.standard_normal((4, nq, d)).astype(np.float32)
+    all_rows = run(ctx, q, pk, pv, tables, ranges, nq, 0.1)
+    for r in range(4):
+        # alone, and with a narrower table (the chunking follows the range only)
+        one = run(ctx, q[r:r + 1], pk, pv, tables[r:r + 1, :44], ranges[r:r + 1], nq, 0.1)
+        assert_bits_equal(one[0], all_rows[r], f"row {r}")
+
+
+def test_bad_blocks_and_ranges_are_reported(ctx):
+    rng = np.random.default_rng(9)
+    pk = rng.standard_normal((4, 1, 16, 64)).astype(np.float32)
+    q = rng.standard_normal((2, 2, 64)).astype(np.float32)
+    tables = np.array([[0, 1], [2, 9]], np.uint32)     # block 9 is outside a pool of 4
+    with pytest.raises(hip.CucaError, match="attention row 1: position 16 has no K/V block"):
+        run(ctx, q, pk, pk, tables, np.array([[0, 20], [0, 20]], np.int32), 2, 0.1)
+    with pytest.raises(hip.CucaError, match="attention row 0: empty key range"):
+        run(ctx, q, pk, pk, tables, np.array([[5, 5], [0, 3]], np.int32), 2, 0.1)
+    with pytest.raises(hip.CucaError, match="attention row 1: empty key range, or one past"):
+        run(ctx, q, pk, pk, tables, np.array([[0, 3], [0, 33]], np.int32), 2, 0.1)
+
+
+def test_host_checks(ctx):
+    pool = ops.KvPool(ctx, 4, 2, 64, np.float32)
+    q = ctx.array(np.zeros((1, 4, 64), np.float32))
+    tab = ctx.array(np.zeros((1, 2), np.uint32))
+    rng = ctx.array(np.array([[0, 5]], np.int32))
+    need = hip.paged_decode_workspace(1, 4, 64, 2)
+    assert need == 1 * 4 * 1 * 66 * 4
+    small = ctx.empty((need - 4,), np.uint8)
+    with pytest.raises(hip.CucaError, match="workspace of"):
+        pool.decode(q, tab, rng, 4, 0.1, workspace=small)
+    with pytest.raises(hip.CucaError, match="query shape mismatch"):
+        ctx.paged_decode(q.ptr, pool.k.ptr, pool.v.ptr, 4, tab.ptr, 2, rng.ptr, 1, 3, 2, 64, 0.1,
+                         small.ptr, need, q.ptr, hip.F32)
+
+
+def test_config_c_at_8192_keys(ctx):
+    cfg = W.CONFIGS["C"]
+    rng = np.random.default_rng(10)
+    nq, nk, d = cfg["nq"], cfg["nk"], cfg["head_dim"]
+    rows, ctx_len = 4, 8192
+    n_blocks = rows * ctx_len // 16 + 16
+    tables = rng.permutation(n_blocks)[:rows * ctx_len // 16].reshape(rows, -1).astype(np.uint32)
+    ranges = np.array([[0, ctx_len], [0, ctx_len - 1], [4096, ctx_len], [0, 5000]], np.int32)
+    pk = rng.standard_normal((n_blocks, nk, 16, d)).astype(np.float16)
+    pv = rng.standard_normal((n_blocks, nk, 16, d)).astype(np.float16)
+    q = rng.standard_normal((rows, nq, d)).astype(np.float16)
+    check(ctx, q, pk, pv, tables, ranges, nq, 1.0 / np.sqrt(d))
