@@ -10,18 +10,28 @@
 //
 // Split pass: a workgroup of 4 waves per (row, KV head, part of 4 CP key
 // positions); wave w takes the part's CP positions w*CP.. (CP = 64 / LPP,
-// LPP lanes per position: a K row slice of at most 256 bytes per lane).
-// The group's query heads (the GQA group) are staged once in LDS as f32.
-// Every lane issues all of its loads at once -- its slice of its position's
-// K row and its d/64 value columns of all CP positions (about 64 VGPRs
-// each) -- so a wave's 16-32 KiB are in flight together.  Scores q . k (f32,
-// in column order within a lane, then across the LPP lanes) times `scale`;
-// the wave's maximum and sum are wave reductions; the weights exp(s - max)
-// are broadcast from their lanes with readlane while each lane accumulates
-// its value columns in position order.  The 4 waves' partials are combined
-// in LDS (in wave order) into the part's (values, max, sum).  Part sizes
-// depend on the dtype and head_dim only, so a row's result depends on its
-// own range, never on the batch it is computed in.
+// LPP lanes per position: a K row slice of at most 256 bytes per lane, 128
+// for a group of 8).  Chunks start at the range's first block (positions
+// before lo are masked), so a wave's positions are CP / 16 whole blocks and
+// every value row is one of CP / 16 scalar block bases plus a constant
+// offset.  The group's query heads (the GQA group) are staged once in LDS
+// (f16 pairs, or f32).  Every lane issues all of its loads at once -- its
+// slice of its position's K row and its d/64 value columns of all CP
+// positions (about 64 VGPRs each) -- so a wave's 16-32 KiB are in flight
+// together.  Scores: f16 dot2 (exact products) or f32 fma over the lane's
+// columns, then across its LPP lanes, times `scale`; the wave's maximum and
+// sum are wave reductions; the weights exp(s - max) go through LDS to every
+// lane, which accumulates its value columns in position order (fma).  The 4
+// waves' partials are combined in LDS, in wave order, into the part's
+// (values, max, sum).  Part sizes depend on the dtype, head_dim and group
+// only, so a row's result depends on its own range, never on the batch it
+// is computed in.
+//
+// Measured on MI355X (f16, 32/8 heads of 128, 8192 keys per row): 60 % of
+// 8 TB/s at 32-64 rows, against 72 % for a kernel that only issues the
+// same loads (the block-scattered 4 KiB K/V pieces cap it below a
+// streaming copy's 80 %).  16-byte value loads (4 rows per instruction)
+// measured slower (53 % loads-only).
 //
 // Merge pass: one wave per (row, query head) combines the row's parts in
 // part order -- the global maximum M, then sum_p acc_p e^(m_p - M) /
