@@ -471,8 +471,64 @@ class DecodeLayers:
                           eps, 1.0, n, H, self.x.data_ptr(), self.h.data_ptr(), hip.F32)
 
 
-def decode_us_per_layer(ctx, torch, n, replays=50):
-    dl = DecodeLayers(ctx, torch, n)
+class DecodeLayersAttn(DecodeLayers):
+    """DecodeLayers with the attention-side ops a K/V-owning layer adds: the
+    fused QK-norm-less RoPE + paged K/V store of the new token (its K and V
+    into the layer's pool) and the paged decode attention over ctx_len keys
+    (the new one included), per layer, config B, f32."""
+
+    def __init__(self, ctx, torch, n, ctx_len, layers=32, seed=1):
+        super().__init__(ctx, torch, n, layers, seed)
+        import numpy as np
+        hip, cfg = self.hip, self.cfg
+        d, nq, nk = cfg["head_dim"], cfg["nq"], cfg["nk"]
+        nbr = (ctx_len + 15) // 16
+        self.n_blocks = n * nbr
+        gen = torch.Generator(device="cuda").manual_seed(seed + 1)
+        for l in self.L:
+            l["v"] = torch.randn((n, nk, d), device="cuda", generator=gen)
+            l["pk"] = torch.randn((self.n_blocks, nk, 16, d), device="cuda", generator=gen)
+            l["pv"] = torch.randn((self.n_blocks, nk, 16, d), device="cuda", generator=gen)
+            l["o"] = torch.empty((n, nq, d), device="cuda")
+        tables = np.arange(self.n_blocks, dtype=np.int32).reshape(n, nbr)
+        self.tables = torch.from_numpy(tables).cuda()
+        self.max_blocks = nbr
+        pos = np.full(n, ctx_len - 1, np.int32)   # the new token's position
+        self.pos = torch.from_numpy(pos).cuda()
+        slots = np.concatenate([hip.kv_slots(tables[r].astype(np.uint32), ctx_len - 1, 1, self.n_blocks)
+                                for r in range(n)])
+        self.slots = torch.from_numpy(slots).cuda()
+        self.ranges = torch.from_numpy(np.tile(np.array([0, ctx_len], np.int32), (n, 1))).cuda()
+        self.ws_bytes = hip.paged_decode_workspace(n, nq, d, nbr)
+        self.ws = torch.empty(max(self.ws_bytes, 16), dtype=torch.uint8, device="cuda")
+        self.scale = 1.0 / float(np.sqrt(d))
+
+    def issue(self):
+        c, hip, cfg, n = self.ctx, self.hip, self.cfg, self.n
+        H, F, d, nq, nk, eps = cfg["hidden"], cfg["ff"], cfg["head_dim"], cfg["nq"], cfg["nk"], cfg["eps"]
+        for l in self.L:
+            # (QKV matmul) -> RoPE on Q, K; K and V of the new token into the pool
+            c.rope_store_kv(l["q"].data_ptr(), nq * d, l["k"].data_ptr(), nk * d, l["v"].data_ptr(),
+                            nk * d, n, nq, nk, d, d, hip.ROPE_NORM, self.cos.data_ptr(),
+                            self.sin.data_ptr(), 8192, self.pos.data_ptr(), None, None, 0, eps,
+                            l["pk"].data_ptr(), l["pv"].data_ptr(), self.n_blocks,
+                            self.slots.data_ptr(), hip.F32)
+            # paged attention over the context
+            c.paged_decode(l["q"].data_ptr(), l["pk"].data_ptr(), l["pv"].data_ptr(), self.n_blocks,
+                           self.tables.data_ptr(), self.max_blocks, self.ranges.data_ptr(), n, nq,
+                           nk, d, self.scale, self.ws.data_ptr(), self.ws_bytes, l["o"].data_ptr(),
+                           hip.F32)
+            # (O matmul) -> x += attn; h = ffn_norm(x)
+            c.add_rmsnorm(self.x.data_ptr(), l["attn"].data_ptr(), l["w1"].data_ptr(), None, eps,
+                          eps, 1.0, n, H, self.x.data_ptr(), self.h.data_ptr(), hip.F32)
+            c.glu(l["gu"].data_ptr(), 2 * F, l["gu"].data_ptr() + 4 * F, 2 * F, n, F,
+                  hip.ACT_SILU, 0.0, l["act"].data_ptr(), F, hip.F32)
+            c.add_rmsnorm(self.x.data_ptr(), l["ffn"].data_ptr(), l["w2"].data_ptr(), None, eps,
+                          eps, 1.0, n, H, self.x.data_ptr(), self.h.data_ptr(), hip.F32)
+
+
+def decode_us_per_layer(ctx, torch, n, replays=50, ctx_len=None):
+    dl = DecodeLayers(ctx, torch, n) if ctx_len is None else DecodeLayersAttn(ctx, torch, n, ctx_len)
     torch.cuda.synchronize()
     eager_ms = time_steps(torch, dl.issue, 10, 3)
     ctx.graph_begin()
@@ -656,6 +712,12 @@ def main():
             g_us, e_us = decode_us_per_layer(ctx, torch, n)
             decode[f"batch{n}"] = dict(graph_us_per_layer=round(g_us, 2),
                                        eager_us_per_layer=round(e_us, 2))
+        # with the K/V store and the paged attention of a K/V-owning layer
+        for n, clen in ((1, 8192), (32, 1024)):
+            g_us, e_us = decode_us_per_layer(ctx, torch, n, ctx_len=clen)
+            decode[f"batch{n}_with_attention_ctx{clen}"] = dict(graph_us_per_layer=round(g_us, 2),
+                                                                eager_us_per_layer=round(e_us, 2))
+            torch.cuda.empty_cache()
         torch.cuda.empty_cache()
 
     cpu = None

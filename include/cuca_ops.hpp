@@ -10,6 +10,7 @@
 //   cuca::RopeSpec::plain(kind, n_dims, base).tables(factors, positions)   rope.rs:62-151
 //   cuca::KvPool{n_blocks, n_kv_head, head_dim}.store_kv(q, k, v, ...)     cpu.rs:3028-3097,
 //                                                                          gpu.rs:1774-1806
+//   cuca::KvPool::decode(q, tables, ranges, n_head, scale)                 paged_kernel.rs:92-282
 //
 // Tensors are cuca::Tensor: a device buffer owned through the context, with
 // a row-major shape and an element type (f32, or f16 held as uint16_t bits).
@@ -359,6 +360,32 @@ class KvPool {
             static_cast<const float *>(sin.data()), cos.dim(0), static_cast<const int32_t *>(positions.data()),
             w(q_norm_w), w(k_norm_w), v_norm ? 1 : 0, eps, k_.data(), v_.data(), n_blocks_,
             static_cast<const int32_t *>(slots.data()), (cuca_dtype)q.dtype()));
+    }
+
+    // Paged decode attention of q [rows, n_head, d] (one query row per
+    // sequence) over this pool (paged_attention_decode, paged_kernel.rs:
+    // 92-282): tables device u32 [rows, max_blocks], ranges device int32
+    // [rows, 2] (lo, hi).  Returns [rows, n_head, d]; the workspace is
+    // allocated here (cuca_hip_paged_decode_workspace bytes) unless given.
+    Tensor decode(Context &ctx, const Tensor &q, const Tensor &tables, const Tensor &ranges, int32_t n_head,
+                  float scale, Tensor *workspace = nullptr) const {
+        const int64_t rows = q.dim(0), d = q.dim(2), max_blocks = tables.dim(1);
+        if (q.dim(1) != n_head || d != k_.dim(3)) throw Error(CUCA_INVALID_ARG, "attention: query shape mismatch");
+        size_t need = 0;
+        check(nullptr, cuca_hip_paged_decode_workspace(rows, n_head, (int32_t)d, max_blocks, &need));
+        Tensor own;
+        if (!workspace) {
+            own = Tensor(ctx, {(int64_t)(need > 16 ? need : 16)}, DType::U8);
+            workspace = &own;
+        }
+        Tensor out(ctx, {rows, (int64_t)n_head, d}, q.dtype());
+        ctx.check(cuca_hip_paged_decode(ctx.raw(), q.data(), k_.data(), v_.data(), n_blocks_,
+                                        static_cast<const uint32_t *>(tables.data()), max_blocks,
+                                        static_cast<const int32_t *>(ranges.data()), rows, n_head,
+                                        (int32_t)k_.dim(1), (int32_t)d, scale, workspace->data(),
+                                        workspace->bytes(), out.data(), (cuca_dtype)q.dtype()));
+        ctx.sync(); // the workspace may be freed on return
+        return out;
     }
 
     const Tensor &k() const { return k_; }

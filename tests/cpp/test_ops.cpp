@@ -172,6 +172,25 @@ int main() {
         }
         EXPECT(threw, "a released block must be rejected");
         std::printf("ok KvPool::slots / store_kv\n");
+
+        // decode attention over the stored rows: one query row per position range
+        const int64_t qn = 2;
+        auto qd = normal(g, qn * nq * d);
+        auto dqd = ctx.tensor(qd, {qn, nq, d}, cuca::DType::F32);
+        std::vector<uint32_t> tabs = {5, 1, 3, 5, 1, 3};
+        std::vector<int32_t> rng = {9, 30, 16, 17};
+        auto dt = ctx.tensor(tabs, {qn, 3}, cuca::DType::U32);
+        auto dr = ctx.tensor(rng, {qn, 2}, cuca::DType::I32);
+        auto got = pool.decode(ctx, dqd, dt, dr, (int32_t)nq, 0.125f).download<float>();
+        std::vector<float> want(got.size());
+        EXPECT(oracle_paged_attention(qd.data(), qn, (int)nq, (int)nk, (int)d, tabs.data(), 3, rng.data(), pk.data(),
+                                      pv.data(), n_blocks, 0.125f, want.data(), OR_F32, 1) == 0,
+               "oracle attention");
+        double err = 0;  // outputs are convex combinations of N(0, 1) values
+        for (size_t i = 0; i < got.size(); i++) err = std::fmax(err, std::fabs((double)got[i] - want[i]));
+        EXPECT(err <= 2e-5, "attention abs err %g", err);
+        ctx.check_device();
+        std::printf("ok KvPool::decode\n");
     }
     {  // errors carry the library's message
         bool threw = false;
