@@ -119,6 +119,33 @@ typedef struct {
     float scale;
 } AttnArgs;
 
+/* Quantized matmul (qmm.hip): packed weights [n][ng][GB] (see there),
+ * activations x [m][ldx], out [m][out_ld] in the activation type.  The
+ * grid is nrb8 * ntile workgroups (nrb8 = nrb rounded up to a multiple of
+ * 8); workgroup id -> (row block, activation tile) is XCD-aware. */
+typedef struct {
+    const uint8_t *w;       /* packed weight (gate for the GLU kernels)     */
+    const uint8_t *w_up;    /* packed up weight (GLU kernels) or NULL       */
+    const void *x;          /* [m][ldx]                                      */
+    void *out;              /* [m][out_ld]                                   */
+    int64_t ldx, out_ld;    /* row strides in elements                       */
+    int64_t row_bytes;      /* packed bytes per weight row (ng * GB)         */
+    int32_t rows;           /* weight rows computed (<= n)                   */
+    int32_t m;              /* activation rows                               */
+    int32_t nb;             /* blocks per row (k / 32)                       */
+    int32_t ng;             /* groups per row                                */
+    int32_t nrb;            /* row blocks of 16 rows                         */
+    int32_t ntile;          /* activation tiles                              */
+    float clamp;            /* GLU: > 0 clamps gate from above, up to +-clamp */
+    int32_t pad_;
+} QmmArgs;
+
+typedef struct {
+    const uint8_t *src;     /* GGUF rows [n][nb * block bytes]               */
+    uint8_t *dst;           /* packed [n][ng][GB]                            */
+    int32_t n, nb, ng, pad_;
+} QPackArgs;
+
 #ifdef __cplusplus
 }
 #endif

@@ -10,3 +10,4 @@
 #include "glu.hip"
 #include "rope.hip"
 #include "attn.hip"
+#include "qmm.hip"

@@ -147,6 +147,7 @@ inline size_t esize(cuca_dtype t) { return t == CUCA_F16 ? 2 : 4; }
 inline bool dtype_ok(cuca_dtype t) { return t == CUCA_F32 || t == CUCA_F16; }
 inline int chunk_elems(cuca_dtype t) { return t == CUCA_F16 ? 8 : 4; }
 inline unsigned div_up(int64_t a, int64_t b) { return (unsigned)((a + b - 1) / b); }
+constexpr unsigned CUCA_BLOCK_THREADS = 256; // every kernel's workgroup size but the norm's
 
 }  // namespace
 
@@ -820,6 +821,141 @@ cuca_status cuca_hip_paged_decode(cuca_hip_ctx *ctx, const void *q, const void *
     const int cpl = (head_dim + 63) / 64;
     const int ci = cpl <= 1 ? 0 : cpl <= 2 ? 1 : cpl <= 4 ? 2 : 3;
     return launch(ctx, km[f16][ci], div_up(rows * n_head, 4), 256, 0, a);
+}
+
+// ---------------------------------------------------------------------
+// quantized matmul (QmmWeight, qmm.rs)
+// ---------------------------------------------------------------------
+
+// Packed layout of qmm.hip: groups of G blocks of GB bytes per row.
+static bool qfmt(uint32_t t, int *g, int *gb) {
+    if (t == CUCA_GGML_Q4_0) { *g = 16; *gb = 288; return true; }
+    if (t == CUCA_GGML_Q8_0) { *g = 8; *gb = 272; return true; }
+    return false;
+}
+
+// from_raw's checks (qmm.rs:1769-1782): a served type, whole blocks, n > 0.
+static cuca_status qweight_shape(cuca_hip_ctx *ctx, uint32_t t, int64_t n, int64_t k, int *g,
+                                 int *gb) {
+    if (!qfmt(t, g, gb))
+        return fail(ctx, CUCA_UNSUPPORTED, "ggml type %u: the quantized matmul serves Q4_0 (2) and Q8_0 (8)", t);
+    if (n <= 0 || n > 0x7fffffffll) return fail(ctx, CUCA_INVALID_ARG, "qmm: bad weight row count %lld", (long long)n);
+    if (k <= 0 || k % 32 != 0 || k / 32 > 0x7fffffffll)
+        return fail(ctx, CUCA_INVALID_ARG, "qmm: row length %lld is not a whole number of blocks", (long long)k);
+    return CUCA_OK;
+}
+
+cuca_status cuca_hip_qweight_bytes(uint32_t ggml_type, int64_t n, int64_t k, size_t *bytes) {
+    if (!bytes) return fail(nullptr, CUCA_INVALID_ARG, "null output pointer");
+    int g = 0, gb = 0;
+    cuca_status st = qweight_shape(nullptr, ggml_type, n, k, &g, &gb);
+    if (st != CUCA_OK) return st;
+    const int64_t ng = (k / 32 + g - 1) / g;
+    *bytes = (size_t)n * (size_t)ng * (size_t)gb;
+    return CUCA_OK;
+}
+
+cuca_status cuca_hip_qweight_pack(cuca_hip_ctx *ctx, const void *gguf, uint32_t ggml_type, int64_t n,
+                                  int64_t k, void *packed) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    int g = 0, gb = 0;
+    if ((st = qweight_shape(ctx, ggml_type, n, k, &g, &gb)) != CUCA_OK) return st;
+    if (!gguf || !packed) return fail(ctx, CUCA_INVALID_ARG, "null pointer");
+    if (!al16(packed)) return fail(ctx, CUCA_INVALID_ARG, "packed weight must be 16-byte aligned");
+    const int64_t nb = k / 32, ng = (nb + g - 1) / g;
+    const int64_t pieces = n * ng * (gb / 16);
+    if (pieces / CUCA_BLOCK_THREADS + 1 > 0x7fffffffll) return fail(ctx, CUCA_UNSUPPORTED, "weight too large");
+    QPackArgs a{};
+    a.src = static_cast<const uint8_t *>(gguf);
+    a.dst = static_cast<uint8_t *>(packed);
+    a.n = (int32_t)n;
+    a.nb = (int32_t)nb;
+    a.ng = (int32_t)ng;
+    return launch(ctx, ggml_type == CUCA_GGML_Q4_0 ? cuca_qpack_q4_0 : cuca_qpack_q8_0,
+                  div_up(pieces, CUCA_BLOCK_THREADS), CUCA_BLOCK_THREADS, 0, a);
+}
+
+// glu: 0 plain, 1 SiLU, 2 GELU-tanh
+static cuca_status qmm_common(cuca_hip_ctx *ctx, const void *w, const void *w_up, uint32_t ggml_type,
+                              int64_t n, int64_t k, const void *x, int64_t ldx, int64_t m, int64_t rows,
+                              int glu, float clamp, void *out, int64_t out_ld, cuca_dtype dtype) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    int g = 0, gb = 0;
+    if ((st = qweight_shape(ctx, ggml_type, n, k, &g, &gb)) != CUCA_OK) return st;
+    if (!dtype_ok(dtype)) return fail(ctx, CUCA_INVALID_ARG, "bad dtype %d", (int)dtype);
+    // forward_rows (qmm.rs:1823-1825)
+    if (rows <= 0 || rows > n)
+        return fail(ctx, CUCA_INVALID_ARG, "qmm: %lld weight rows of %lld", (long long)rows, (long long)n);
+    if (m < 0 || m > 0x7fffffffll) return fail(ctx, CUCA_INVALID_ARG, "qmm: bad activation row count %lld", (long long)m);
+    if (ldx < k)
+        return fail(ctx, CUCA_INVALID_ARG, "qmm: activation row stride %lld shorter than %lld", (long long)ldx,
+                    (long long)k);
+    if (out_ld < rows)
+        return fail(ctx, CUCA_INVALID_ARG, "qmm: output row stride %lld shorter than %lld", (long long)out_ld,
+                    (long long)rows);
+    if (!(clamp == clamp)) return fail(ctx, CUCA_INVALID_ARG, "clamp is NaN");
+    if (m == 0) return CUCA_OK;
+    if (!w || !x || !out || (glu && !w_up)) return fail(ctx, CUCA_INVALID_ARG, "null pointer");
+    const size_t es = esize(dtype);
+    if (!al16(w) || (w_up && !al16(w_up)))
+        return fail(ctx, CUCA_INVALID_ARG, "packed weights must be 16-byte aligned");
+    if (!al16(x) || ((size_t)ldx * es) % 16 != 0)
+        return fail(ctx, CUCA_INVALID_ARG, "qmm: activation rows must start 16-byte aligned");
+    const int64_t nb = k / 32, ng = (nb + g - 1) / g;
+    const int mt = m == 1 ? 1 : m == 2 ? 2 : 4;
+    const int mi = mt == 1 ? 0 : mt == 2 ? 1 : 2;
+    const int64_t ntile = (m + mt - 1) / mt;
+    const int64_t nrb = (rows + 15) / 16;
+    const int64_t nrb8 = (nrb + 7) / 8 * 8;
+    if (nrb8 * ntile > 0x7fffffffll) return fail(ctx, CUCA_UNSUPPORTED, "qmm: grid too large");
+    // [dtype][format][plain, silu, gelu][tile rows 1, 2, 4]
+    static const Kernel table_k[2][2][3][3] = {
+        {{{cuca_qmm_f32_q4_0_m1, cuca_qmm_f32_q4_0_m2, cuca_qmm_f32_q4_0_m4},
+          {cuca_qmm_glu_f32_q4_0_silu_m1, cuca_qmm_glu_f32_q4_0_silu_m2, cuca_qmm_glu_f32_q4_0_silu_m4},
+          {cuca_qmm_glu_f32_q4_0_gelu_m1, cuca_qmm_glu_f32_q4_0_gelu_m2, cuca_qmm_glu_f32_q4_0_gelu_m4}},
+         {{cuca_qmm_f32_q8_0_m1, cuca_qmm_f32_q8_0_m2, cuca_qmm_f32_q8_0_m4},
+          {cuca_qmm_glu_f32_q8_0_silu_m1, cuca_qmm_glu_f32_q8_0_silu_m2, cuca_qmm_glu_f32_q8_0_silu_m4},
+          {cuca_qmm_glu_f32_q8_0_gelu_m1, cuca_qmm_glu_f32_q8_0_gelu_m2, cuca_qmm_glu_f32_q8_0_gelu_m4}}},
+        {{{cuca_qmm_f16_q4_0_m1, cuca_qmm_f16_q4_0_m2, cuca_qmm_f16_q4_0_m4},
+          {cuca_qmm_glu_f16_q4_0_silu_m1, cuca_qmm_glu_f16_q4_0_silu_m2, cuca_qmm_glu_f16_q4_0_silu_m4},
+          {cuca_qmm_glu_f16_q4_0_gelu_m1, cuca_qmm_glu_f16_q4_0_gelu_m2, cuca_qmm_glu_f16_q4_0_gelu_m4}},
+         {{cuca_qmm_f16_q8_0_m1, cuca_qmm_f16_q8_0_m2, cuca_qmm_f16_q8_0_m4},
+          {cuca_qmm_glu_f16_q8_0_silu_m1, cuca_qmm_glu_f16_q8_0_silu_m2, cuca_qmm_glu_f16_q8_0_silu_m4},
+          {cuca_qmm_glu_f16_q8_0_gelu_m1, cuca_qmm_glu_f16_q8_0_gelu_m2, cuca_qmm_glu_f16_q8_0_gelu_m4}}}};
+    const Kernel kk = table_k[dtype == CUCA_F16][ggml_type == CUCA_GGML_Q8_0][glu][mi];
+    QmmArgs a{};
+    a.w = static_cast<const uint8_t *>(w);
+    a.w_up = static_cast<const uint8_t *>(w_up);
+    a.x = x;
+    a.out = out;
+    a.ldx = ldx;
+    a.out_ld = out_ld;
+    a.row_bytes = ng * gb;
+    a.rows = (int32_t)rows;
+    a.m = (int32_t)m;
+    a.nb = (int32_t)nb;
+    a.ng = (int32_t)ng;
+    a.nrb = (int32_t)nrb;
+    a.ntile = (int32_t)ntile;
+    a.clamp = clamp > 0.0f ? clamp : 0.0f;
+    return launch(ctx, kk, (unsigned)(nrb8 * ntile), CUCA_BLOCK_THREADS, 0, a);
+}
+
+cuca_status cuca_hip_qmm(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type, int64_t n, int64_t k,
+                         const void *x, int64_t ldx, int64_t m, int64_t rows, void *out, int64_t out_ld,
+                         cuca_dtype dtype) {
+    return qmm_common(ctx, w, nullptr, ggml_type, n, k, x, ldx, m, rows, 0, 0.0f, out, out_ld, dtype);
+}
+
+cuca_status cuca_hip_qmm_glu(cuca_hip_ctx *ctx, const void *gate, const void *up, uint32_t ggml_type,
+                             int64_t ff, int64_t k, const void *x, int64_t ldx, int64_t m, cuca_act act,
+                             float clamp, void *out, int64_t out_ld, cuca_dtype dtype) {
+    if (act != CUCA_ACT_SILU && act != CUCA_ACT_GELU_TANH)
+        return fail(ctx, CUCA_INVALID_ARG, "bad activation %d", (int)act);
+    return qmm_common(ctx, gate, up, ggml_type, ff, k, x, ldx, m, ff, act == CUCA_ACT_SILU ? 1 : 2, clamp,
+                      out, out_ld, dtype);
 }
 
 // RopeSpec::tables (rope.rs:118-151): f64 angles with the platform libm,

@@ -72,6 +72,11 @@ SIGNATURES = {
     "cuca_hip_paged_decode": (_st, [_p, _p, _p, _p, _i64, _p, _i64, _p, _i64, _i32, _i32, _i32,
                                     _f32, _p, _sz, _p, _st]),
     "cuca_hip_rope_tables": (_st, [ctypes.POINTER(RopeSpecC), _p, _i64, _p, _p]),
+    "cuca_hip_qweight_bytes": (_st, [_u32, _i64, _i64, ctypes.POINTER(_sz)]),
+    "cuca_hip_qweight_pack": (_st, [_p, _p, _u32, _i64, _i64, _p]),
+    "cuca_hip_qmm": (_st, [_p, _p, _u32, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _st]),
+    "cuca_hip_qmm_glu": (_st, [_p, _p, _p, _u32, _i64, _i64, _p, _i64, _i64, _st, _f32, _p, _i64,
+                               _st]),
     "cuca_hip_graph_begin": (_st, [_p]),
     "cuca_hip_graph_end": (_st, [_p, _pp]),
     "cuca_hip_graph_launch": (_st, [_p, _p]),
@@ -314,6 +319,18 @@ class Context:
                                                  pool_k, pool_v, n_blocks, slots, dtype))
 
 
+    def qweight_pack(self, gguf, ggml_type, n, k, packed):
+        self.check(self.L.cuca_hip_qweight_pack(self.ptr, gguf, ggml_type, n, k, packed))
+
+    def qmm(self, w, ggml_type, n, k, x, ldx, m, rows, out, out_ld, dtype):
+        self.check(self.L.cuca_hip_qmm(self.ptr, w, ggml_type, n, k, x, ldx, m, rows, out, out_ld,
+                                       dtype))
+
+    def qmm_glu(self, gate, up, ggml_type, ff, k, x, ldx, m, act, clamp, out, out_ld, dtype):
+        self.check(self.L.cuca_hip_qmm_glu(self.ptr, gate, up, ggml_type, ff, k, x, ldx, m, act,
+                                           clamp, out, out_ld, dtype))
+
+
 class Graph:
     def __init__(self, ctx, ptr):
         self.ctx = ctx
@@ -343,6 +360,13 @@ def paged_decode_workspace(rows, n_head, head_dim, max_blocks):
     out = _sz(0)
     _check(lib().cuca_hip_paged_decode_workspace(rows, n_head, head_dim, max_blocks,
                                                  ctypes.byref(out)), None)
+    return out.value
+
+
+def qweight_bytes(ggml_type, n, k):
+    """Bytes of the packed layout of an [n, k] Q4_0 / Q8_0 weight (host)."""
+    out = _sz(0)
+    _check(lib().cuca_hip_qweight_bytes(ggml_type, n, k, ctypes.byref(out)), None)
     return out.value
 
 

@@ -10,6 +10,8 @@ under src/provider/local/model/ of nassor/cuca 0.10.0), so that a caller
     Glu(act, clamp).apply(gate, up)                                  cpu.rs:342-371
     apply_rope(x, cos, sin, kind, n_dims, positions)                 cpu.rs:3672-3688
     RopeSpec.plain(kind, n_dims, base).tables(factors, positions)    rope.rs:62-151
+    QmmWeight.from_raw(dtype, data, n, k).forward_rows(x, m, rows)    qmm.rs:1744-1838
+    QmmWeight.glu(gate, up, x, glu)  (act(gate x) * up x, fused)     cpu.rs:342-371, 3554-3566
 
 Tensors are DeviceArrays (device memory through the C ABI); every op runs on
 the gfx950 kernels of libcuca_hip.so.  There is no host fallback.
@@ -269,3 +271,69 @@ class RopeSpec:
     def device_tables(self, ctx, factors, positions):
         cos, sin = self.tables(factors, positions)
         return ctx.array(cos), ctx.array(sin)
+
+
+class QmmWeight:
+    """A quantized [n, k] weight (y = x w^T) on the row-batched kernel
+    (QmmWeight, qmm.rs:1744-1838), Q4_0 or Q8_0, resident in HBM in the
+    kernels' packed layout (the file's bytes, reordered once on the device).
+    Products are the reference CPU engine's bits, row by row."""
+
+    def __init__(self, ctx, dtype, packed, n, k):
+        self.ctx, self.dtype, self.packed, self.n_, self.k_ = ctx, dtype, packed, n, k
+
+    @classmethod
+    def from_raw(cls, ctx, dtype, data, n, k):
+        """The weight of GGUF type `dtype` over its file bytes, or None for a
+        type the kernel does not serve, a row that is not whole blocks or a
+        wrong byte count (qmm.rs:1763-1783)."""
+        row = byte_len(dtype, k)
+        data = np.ascontiguousarray(np.frombuffer(data, np.uint8) if isinstance(data, bytes)
+                                    else data, dtype=np.uint8).reshape(-1)
+        if row is None or n <= 0 or row * n != data.size:
+            return None
+        raw = ctx.array(data)
+        packed = ctx.empty((hip.qweight_bytes(dtype, n, k),), np.uint8)
+        ctx.qweight_pack(raw.ptr, dtype, n, k, packed.ptr)
+        ctx.sync()
+        raw.free()
+        return cls(ctx, dtype, packed, n, k)
+
+    def n(self):
+        """Output width (weight rows)."""
+        return self.n_
+
+    def k(self):
+        """Input width (weight columns)."""
+        return self.k_
+
+    def forward(self, x, out=None):
+        return self.forward_rows(x, self.n_, out=out)
+
+    def forward_rows(self, x, rows, out=None):
+        """x [m, k] (DeviceArray, f32 or f16) times the first `rows` weight
+        rows: [m, rows] in x's dtype.  Row j depends on x[j] only, bit for bit."""
+        m, width = x.shape
+        if width != self.k_:  # qmm.rs:1815-1821
+            raise CucaError(hip.INVALID_ARG, f"qmm: activations hold {x.size} floats, expected "
+                            f"{m} rows of {self.k_}")
+        if out is None:
+            out = self.ctx.empty((m, rows), x.dtype)
+        self.ctx.qmm(self.packed.ptr, self.dtype, self.n_, self.k_, x.ptr, self.k_, m, rows,
+                     out.ptr, out.shape[1], hip.dtype_code(x.dtype))
+        return out
+
+    @staticmethod
+    def glu(gate, up, x, glu, out=None):
+        """act(gate x) * up x (FfnWeights::forward, GateUp::Split, with
+        Glu::apply, cpu.rs:3554-3566, 342-371) in one launch."""
+        ctx = gate.ctx
+        m, width = x.shape
+        if gate.dtype != up.dtype or gate.n_ != up.n_ or gate.k_ != up.k_ or width != gate.k_:
+            raise CucaError(hip.INVALID_ARG, "qmm glu: gate and up differ in type or shape")
+        if out is None:
+            out = ctx.empty((m, gate.n_), x.dtype)
+        ctx.qmm_glu(gate.packed.ptr, up.packed.ptr, gate.dtype, gate.n_, gate.k_, x.ptr, gate.k_, m,
+                    glu.act, glu.clamp if glu.clamp is not None else 0.0, out.ptr, out.shape[1],
+                    hip.dtype_code(x.dtype))
+        return out

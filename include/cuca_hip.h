@@ -26,6 +26,9 @@
  *                          rows (host)
  *   cuca_hip_paged_decode  paged decode attention         paged_kernel.rs:92-282,
  *                          (+ _workspace, host)           cpu/paged_attn.rs:105-290
+ *   cuca_hip_qmm           QmmWeight::forward_rows        qmm.rs:1810-1838
+ *   cuca_hip_qmm_glu       gate/up qmm + Glu::apply       cpu.rs:342-371, 3554-3566
+ *   cuca_hip_qweight_pack  (the weight upload)            qmm.rs:1763-1783
  *
  * Conventions
  * - A context owns one device, one HIP stream (or borrows the caller's),
@@ -263,6 +266,49 @@ cuca_status cuca_hip_paged_decode(cuca_hip_ctx *ctx, const void *q, const void *
                                   int32_t n_head, int32_t n_kv, int32_t head_dim, float scale,
                                   void *workspace, size_t workspace_bytes, void *out,
                                   cuca_dtype dtype);
+
+/* ------------------------------------------------------------------ */
+/* Quantized matmul (the CPU engine's QmmWeight, qmm.rs)               */
+/* ------------------------------------------------------------------ */
+
+/* A quantized [n, k] weight (y = x w^T) as the GGUF file stores it, Q4_0 or
+ * Q8_0, is repacked once on the device into the kernels' layout (groups of
+ * 16 (Q4_0) or 8 (Q8_0) blocks: the group's f16 scales, then one 16-byte
+ * chunk per lane holding that lane's quants of every block of the group;
+ * the same bytes as the file, reordered).  The reference reads the file
+ * bytes in place (QmmWeight::from_raw, qmm.rs:1763-1783); its GPU engine
+ * repacks into its own word order too (moe_kernel.rs DenseLayout).
+ * cuca_hip_qweight_bytes: the packed size.  cuca_hip_qweight_pack: gguf
+ * (device, [n][k/32 blocks]) -> packed (device, 16-byte aligned). */
+cuca_status cuca_hip_qweight_bytes(uint32_t ggml_type, int64_t n, int64_t k, size_t *bytes);
+cuca_status cuca_hip_qweight_pack(cuca_hip_ctx *ctx, const void *gguf, uint32_t ggml_type, int64_t n,
+                                  int64_t k, void *packed);
+
+/* QmmWeight::forward_rows (qmm.rs:1810-1838), bit for bit: out[j][r] =
+ * x[j] . w[r] for the first `rows` weight rows, with the reference CPU
+ * engine's arithmetic (qmm.rs:14-45): x quantised to Q8_0 per 32 values,
+ * sixteen f32 lanes each summing (f32)(exact integer pair dot) * (dw * dx)
+ * over the blocks in order, reduced by the fixed tree of hsum.  A row's
+ * result does not depend on m or on the other rows.
+ *   w   : packed weight (cuca_hip_qweight_pack) of n rows of k values
+ *   x   : [m][ldx] of dtype (f16 is widened exactly); 16-byte aligned rows
+ *   out : [m][out_ld] of dtype (f32: the reference's bits; f16: rounded once)
+ * rows outside 1..n is an error ("qmm: {rows} weight rows of {n}"). */
+cuca_status cuca_hip_qmm(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type, int64_t n, int64_t k,
+                         const void *x, int64_t ldx, int64_t m, int64_t rows, void *out, int64_t out_ld,
+                         cuca_dtype dtype);
+
+/* The dense FFN's gate and up projections with the gated activation fused in
+ * (FfnWeights::forward GateUp::Split + Glu::apply, cpu.rs:342-371,
+ * 3554-3566; the reference GPU engine fuses the same act * up into its
+ * up_kernel, moe_kernel.rs:1163-1288):
+ *   out[j][f] = act(min(g, clamp)) * clamp(u, -clamp, clamp)   (clamp > 0)
+ *             = act(g) * u                                     (clamp <= 0)
+ * g = qmm(gate)[j][f], u = qmm(up)[j][f] with cuca_hip_qmm's bits; the
+ * activation as cuca_hip_glu.  gate, up: packed [ff][k]; out [m][out_ld]. */
+cuca_status cuca_hip_qmm_glu(cuca_hip_ctx *ctx, const void *gate, const void *up, uint32_t ggml_type,
+                             int64_t ff, int64_t k, const void *x, int64_t ldx, int64_t m, cuca_act act,
+                             float clamp, void *out, int64_t out_ld, cuca_dtype dtype);
 
 /* RopeSpec (rope.rs:62-79). yarn_ext_factor == 0 disables YaRN. */
 typedef struct {

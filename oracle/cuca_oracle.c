@@ -571,3 +571,111 @@ int oracle_paged_attention(const void *q, int64_t rows, int n_head, int n_kv, in
     parallel_rows(nthreads, rows * n_head, attn_range, &c);
     return 0;
 }
+
+/* ------------------------------------------------------------------ */
+/* next, rank 3: the CPU engine's quantized matmul (QmmWeight)          */
+/* ------------------------------------------------------------------ */
+
+/* f32::round (ties away from zero), restating round_away (qmm.rs:1194-1201);
+ * C's roundf has the same definition. */
+static inline float qmm_round_away(float t) { return roundf(t); }
+
+/* Rust's `f as i8`: saturating, NaN -> 0. */
+static inline int8_t qmm_sat_i8(float t) {
+    if (t != t) return 0;
+    if (t >= 127.0f) return 127;
+    if (t <= -128.0f) return -128;
+    return (int8_t)t;
+}
+
+/* quantise_block (qmm.rs:1217-1240) for MIN_NONE. */
+static float qmm_quantise_block(const float *src, int8_t *q) {
+    float amax = 0.0f;
+    for (int e = 0; e < 32; e++) amax = fmaxf(amax, fabsf(src[e])); /* max ignores NaN */
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    for (int e = 0; e < 32; e++) q[e] = qmm_sat_i8(qmm_round_away(src[e] * id));
+    return oracle_f16_to_f32(oracle_f32_to_f16(d));
+}
+
+void oracle_q8_acts(const void *x, int64_t ld, int64_t m, int64_t k, int dtype,
+                    int8_t *q, float *scales) {
+    const int64_t nb = k / 32;
+    float src[32];
+    for (int64_t j = 0; j < m; j++)
+        for (int64_t b = 0; b < nb; b++) {
+            for (int e = 0; e < 32; e++) src[e] = load_el(x, j * ld + b * 32 + e, dtype);
+            scales[j * nb + b] = qmm_quantise_block(src, q + j * k + b * 32);
+        }
+}
+
+/* The block's f16 scale and its 32 quants as i16 in element order
+ * (Legacy::scale / Legacy::halves: Q4_0 qmm.rs:240-263, Q8_0 qmm.rs:404-426). */
+static float qmm_weight_block(uint32_t type, const uint8_t *blk, int16_t *w) {
+    const float dw = oracle_f16_to_f32((uint16_t)(blk[0] | (blk[1] << 8)));
+    if (type == OR_Q4_0) {
+        for (int i = 0; i < 16; i++) {
+            w[i] = (int16_t)((blk[2 + i] & 0x0F) - 8);
+            w[i + 16] = (int16_t)((blk[2 + i] >> 4) - 8);
+        }
+    } else {
+        for (int i = 0; i < 32; i++) w[i] = (int16_t)(int8_t)blk[2 + i];
+    }
+    return dw;
+}
+
+/* hsum (qmm.rs:1345-1353): the fixed pairwise tree over the 16 lanes. */
+static float qmm_hsum(const float *a) {
+    float h[8];
+    for (int i = 0; i < 8; i++) h[i] = a[i] + a[i + 8];
+    return ((h[0] + h[4]) + (h[1] + h[5])) + ((h[2] + h[6]) + (h[3] + h[7]));
+}
+
+typedef struct {
+    const uint8_t *w;
+    uint32_t type;
+    int64_t k, nb, row_bytes, m, rows;
+    const int8_t *q;
+    const float *xs;
+    float *out;
+} qmm_ctx;
+
+/* Weight rows [begin, end) against every activation row: the scalar
+ * definition of qmm/tests.rs:151-191 for a format without minima. */
+static void qmm_range(void *c, int64_t begin, int64_t end) {
+    qmm_ctx *g = (qmm_ctx *)c;
+    const int bb = g->type == OR_Q4_0 ? 18 : 34;
+    int16_t w[32];
+    for (int64_t r = begin; r < end; r++) {
+        for (int64_t j = 0; j < g->m; j++) {
+            float lanes[16] = {0};
+            for (int64_t b = 0; b < g->nb; b++) {
+                const float dw = qmm_weight_block(g->type, g->w + r * g->row_bytes + b * bb, w);
+                const int8_t *xq = g->q + j * g->k + b * 32;
+                const float s = dw * g->xs[j * g->nb + b];
+                for (int l = 0; l < 16; l++) {
+                    const int32_t p = (int32_t)w[l] * xq[l] + (int32_t)w[l + 16] * xq[l + 16];
+                    lanes[l] += (float)p * s;
+                }
+            }
+            g->out[j * g->rows + r] = qmm_hsum(lanes);
+        }
+    }
+}
+
+int oracle_qmm(const uint8_t *w, uint32_t ggml_type, int64_t n, int64_t k,
+               const void *x, int64_t ld, int64_t m, int64_t rows, float *out,
+               int dtype, int nthreads) {
+    if (ggml_type != OR_Q4_0 && ggml_type != OR_Q8_0) return -1;
+    if (k <= 0 || k % 32 != 0 || rows <= 0 || rows > n || m < 0 || ld < k) return -1;
+    if (m == 0) return 0;
+    int8_t *q = (int8_t *)malloc((size_t)(m * k));
+    float *xs = (float *)malloc(sizeof(float) * (size_t)(m * (k / 32)));
+    if (!q || !xs) { free(q); free(xs); return -1; }
+    oracle_q8_acts(x, ld, m, k, dtype, q, xs);
+    qmm_ctx c = {w, ggml_type, k, k / 32, oracle_row_bytes(ggml_type, k), m, rows, q, xs, out};
+    parallel_rows(nthreads, rows, qmm_range, &c);
+    free(q);
+    free(xs);
+    return 0;
+}

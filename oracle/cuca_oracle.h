@@ -130,6 +130,35 @@ int oracle_paged_attention(const void *q, int64_t rows, int n_head, int n_kv, in
                            const void *pool_k, const void *pool_v, int64_t n_blocks, float scale,
                            void *out, int dtype, int nthreads);
 
+/* Quantized matmul of the CPU engine, QmmWeight (qmm.rs), for Q4_0 and Q8_0
+ * weights (formats without minima, one entry per block).
+ *
+ * oracle_q8_acts restates Acts::new / quantise_block (qmm.rs:1217-1343) for
+ * MIN_NONE: per 32-value block of each of the m rows of x (f32, or f16
+ * widened): amax = max |v| (NaN ignored), d = amax / 127, id = d != 0 ?
+ * 1 / d : 0, scale = f16(d) widened, q[e] = i8(round_away(v[e] * id))
+ * (saturating, NaN -> 0).  q: [m][k] int8 in element order; scales: [m][k/32].
+ *
+ * oracle_qmm restates QmmWeight::forward_rows (qmm.rs:1810-1838) through the
+ * definition the reference's own test states (qmm/tests.rs:151-191, module
+ * docs qmm.rs:29-45): out[j][r] for weight rows r < rows is sixteen f32
+ * lanes; lane l adds, block by block in row order,
+ *     (float)(w[l]*q[l] + w[l+16]*q[l+16]) * (dw * dx)
+ * (the exact integer pair sum, times the rounded product of the two f32
+ * scales, product and sum each rounded), and the lanes are reduced by hsum
+ * (qmm.rs:1345-1353): h[i] = a[i] + a[i+8], then
+ * ((h0+h4)+(h1+h5))+((h2+h6)+(h3+h7)).  Q4_0 weight quants are nibble-8
+ * (element i low nibble of byte i, element i+16 its high nibble,
+ * qmm.rs:240-263); Q8_0 quants are the signed bytes (qmm.rs:404-426); dw is
+ * the block's f16 scale.  w: GGUF bytes [n][k/32 blocks]; x: [m][ld] of
+ * dtype; out: [m][rows] f32.  Returns 0, or -1 for a bad shape (k not a
+ * multiple of 32, rows outside 1..n). */
+void oracle_q8_acts(const void *x, int64_t ld, int64_t m, int64_t k, int dtype,
+                    int8_t *q, float *scales);
+int oracle_qmm(const uint8_t *w, uint32_t ggml_type, int64_t n, int64_t k,
+               const void *x, int64_t ld, int64_t m, int64_t rows, float *out,
+               int dtype, int nthreads);
+
 #ifdef __cplusplus
 }
 #endif

@@ -65,6 +65,10 @@ def lib():
                                              _i64, _f32, _p, _int, _int]
         L.oracle_gather.restype = _int
         L.oracle_gather.argtypes = [_p, _i64, _i64, _i64, _p, _p, _i64, _int, _int, _int]
+        L.oracle_q8_acts.argtypes = [_p, _i64, _i64, _i64, _int, _p, _p]
+        L.oracle_qmm.restype = _int
+        L.oracle_qmm.argtypes = [_p, ctypes.c_uint32, _i64, _i64, _p, _i64, _i64, _i64, _p,
+                                 _int, _int]
         _LIB = L
     return _LIB
 
@@ -264,4 +268,37 @@ def paged_attention(q, tables, ranges, pool_k, pool_v, scale, threads=1):
                                       _dtype_code(q), threads)
     if rc != 0:
         raise KvError("attention over an empty key range or a position without a K/V block")
+    return out
+
+
+def q8_acts(x):
+    """Acts::new (qmm.rs:1272-1343) for a format without minima: x [m, k]
+    (float32, or float16 widened) -> (quants int8 [m, k], scales f32 [m, k/32])."""
+    x = np.ascontiguousarray(x)
+    m, k = x.shape
+    q = np.empty((m, k), np.int8)
+    s = np.empty((m, k // 32), np.float32)
+    lib().oracle_q8_acts(_ptr(x), k, m, k, _dtype_code(x), _ptr(q), _ptr(s))
+    return q, s
+
+
+def qmm(w, ggml_type, n, k, x, rows=None, threads=1):
+    """QmmWeight::forward_rows (qmm.rs:1810-1838) for Q4_0 / Q8_0: w the GGUF
+    bytes of an [n, k] weight, x [m, k] (float32 or float16); returns the
+    f32 [m, rows] product with the first `rows` weight rows (default n)."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x)
+    if x.ndim == 1:
+        x = x.reshape(1, -1)
+    m = x.shape[0]
+    rows = n if rows is None else rows
+    if x.shape[1] != k:
+        raise OracleError(f"qmm: activations hold {x.size} floats, expected {m} rows of {k}")
+    if w.size != n * row_bytes(ggml_type, k):
+        raise OracleError(f"qmm: weight holds {w.size} bytes, expected {n} rows")
+    out = np.empty((m, rows), np.float32)
+    rc = lib().oracle_qmm(_ptr(w), ggml_type, n, k, _ptr(x), k, m, rows, _ptr(out),
+                          _dtype_code(x), threads)
+    if rc != 0:
+        raise OracleError(f"qmm: {rows} weight rows of {n}")
     return out

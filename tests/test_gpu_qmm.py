@@ -1,0 +1,204 @@
+"""Quantized matmul (QmmWeight) on the GPU against the oracle, through the C ABI.
+
+Bars:
+- cuca_hip_qmm: bit-exact against the oracle's restatement of the reference
+  CPU engine (qmm.rs), f32 output; f16 output is the oracle's f32 rounded
+  once to nearest-even, bit-exact too;
+- cuca_hip_qmm_glu: the gate and up products are those bits; the activation
+  is held to cuca_hip_glu's bar (1e-5 relative in f32, 2 f16 ulps, plus for
+  GELU-tanh the floor 2^-22 |0.5 g u|).
+Covers Q4_0 and Q8_0, f32 and f16 activations, activation tiles of 1, 2 and
+4 rows and ragged tails, rows that are not a multiple of the workgroup's 16,
+blocks per row that are not a multiple of the packing group (24 blocks),
+weight-row prefixes (forward_rows), awkward activations (a zero block,
+outliers, ties, a doubled maximum, subnormal and huge values), the
+summation-order known answers of the oracle's tests, the 8B shapes at
+decode, and the host's argument errors.
+"""
+import numpy as np
+import pytest
+
+from cuca_amd import hip, ops
+from cuca_amd import workloads as W
+from helpers import assert_bits_equal, assert_close
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+QT = {"q4_0": hip.GGML_Q4_0, "q8_0": hip.GGML_Q8_0}
+NP = {"f32": np.float32, "f16": np.float16}
+
+
+def weight(ctx, rng, qtype, n, k, d_range=(0.004, 0.012)):
+    raw = W.quant_table(rng, n, k, qtype, d_range)
+    return raw, ops.QmmWeight.from_raw(ctx, QT[qtype], raw, n, k)
+
+
+def awkward(rng, m, k, scale=3.0, huge=1e30):
+    """qmm/tests.rs:199-208 plus a block of tiny values (their scale is an f32
+    subnormal) and a block of huge ones (`huge`, 1e4 where f16 must hold it)."""
+    x = (rng.uniform(-1.0, 1.0, (m, k)) * scale).astype(np.float32)
+    x[:, :32] = 0.0
+    if k >= 64:
+        x[:, 32 + 3] = 127.0
+        x[:, 32 + 4] = 0.5
+        x[:, 32 + 5] = -1.5
+    if k >= 96:
+        x[:, 64 + 10] = -9.0
+        x[:, 64 + 20] = 9.0
+    if k >= 160:
+        x[:, 96:128] *= np.float32(1e-38)   # subnormal products of the scale
+        x[:, 128:160] *= np.float32(huge)
+    return x
+
+
+def want_out(raw, qtype, n, k, x, rows, dtype):
+    w = O.qmm(raw, QT[qtype], n, k, x, rows=rows, threads=8)
+    return w.astype(np.float16) if dtype == "f16" else w
+
+
+@pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+@pytest.mark.parametrize("n,k,m", [(10, 512, 7), (3, 256, 1), (130, 512, 41), (9, 1024, 2),
+                                   (10, 64, 7), (3, 96, 1), (37, 128, 6), (40, 768, 3),
+                                   (17, 4096, 4), (33, 2048, 5), (16, 14336, 1)])
+def test_qmm_is_bit_exact(ctx, qtype, dtype, n, k, m):
+    rng = np.random.default_rng(n * 31 + k + m)
+    raw, w = weight(ctx, rng, qtype, n, k)
+    x = awkward(rng, m, k, huge=1e30 if dtype == "f32" else 1e4).astype(NP[dtype])
+    got = w.forward(ctx.array(x)).numpy()
+    assert_bits_equal(got, want_out(raw, qtype, n, k, x, n, dtype), f"{qtype} {dtype} {n}x{k} m={m}")
+
+
+@pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
+def test_weight_row_prefix(ctx, qtype):
+    rng = np.random.default_rng(17)
+    for n, k, m, rows in [(10, 512, 3, 7), (600, 256, 2, 450), (64, 768, 5, 1), (100, 128, 1, 99)]:
+        raw, w = weight(ctx, rng, qtype, n, k)
+        x = awkward(rng, m, k)
+        dx = ctx.array(x)
+        part = w.forward_rows(dx, rows).numpy()
+        assert_bits_equal(part, want_out(raw, qtype, n, k, x, rows, "f32"), f"rows {rows} of {n}")
+        assert_bits_equal(part, w.forward(dx).numpy()[:, :rows], "prefix of the whole product")
+
+
+@pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
+def test_a_row_is_bit_identical_alone_and_in_any_batch(ctx, qtype):
+    rng = np.random.default_rng(3)
+    n, k = 70, 512
+    raw, w = weight(ctx, rng, qtype, n, k)
+    x = awkward(rng, 17, k)
+    alone = [w.forward(ctx.array(x[j:j + 1])).numpy()[0] for j in range(17)]
+    for m in (2, 3, 4, 5, 8, 9, 17):
+        batch = w.forward(ctx.array(x[:m])).numpy()
+        for j in range(m):
+            assert_bits_equal(batch[j], alone[j], f"row {j} of a batch of {m}")
+
+
+def _ones_block_x(d, entries):
+    x = np.zeros(32, np.float32)
+    x[31] = 127.0 * d
+    for e, qv in entries.items():
+        x[e] = qv * d
+    return x
+
+
+def _q8_block(d, quants):
+    b = np.zeros(34, np.uint8)
+    b[:2] = np.array([d], np.float16).view(np.uint8)
+    b[2:] = np.asarray(quants, np.int8).view(np.uint8)
+    return b
+
+
+def test_summation_order_known_answers(ctx):
+    """The oracle tests' hand-built cases: the lanes sum sequentially over the
+    blocks and are reduced by the hsum tree (answers 1.0)."""
+    # lanes sequential over blocks, then the tree
+    x = np.concatenate([_ones_block_x(1024.0, {0: 64, 16: 64}), _ones_block_x(1.0, {8: 1}),
+                        _ones_block_x(1024.0, {0: 64, 16: 64})]).reshape(1, 96)
+    w0 = np.zeros(32, np.int8); w0[0] = 64; w0[16] = 64
+    w1 = np.zeros(32, np.int8); w1[8] = 1
+    w2 = np.zeros(32, np.int8); w2[0] = -64; w2[16] = -64
+    raw = np.concatenate([_q8_block(1024.0, w0), _q8_block(1.0, w1), _q8_block(1024.0, w2)])
+    w = ops.QmmWeight.from_raw(ctx, hip.GGML_Q8_0, raw, 1, 96)
+    assert w.forward(ctx.array(x)).numpy()[0, 0] == 1.0
+    # the tree: a[0] + a[8] first
+    x = np.concatenate([_ones_block_x(1024.0, {0: 64, 16: 64, 8: 64, 24: 64}),
+                        _ones_block_x(1.0, {1: 1})]).reshape(1, 64)
+    w0 = np.zeros(32, np.int8); w0[0] = 64; w0[16] = 64; w0[8] = -64; w0[24] = -64
+    w1 = np.zeros(32, np.int8); w1[1] = 1
+    raw = np.concatenate([_q8_block(1024.0, w0), _q8_block(1.0, w1)])
+    w = ops.QmmWeight.from_raw(ctx, hip.GGML_Q8_0, raw, 1, 64)
+    assert w.forward(ctx.array(x)).numpy()[0, 0] == 1.0
+
+
+def test_zero_activations_give_exact_zeros(ctx):
+    rng = np.random.default_rng(6)
+    for qtype in ("q4_0", "q8_0"):
+        _, w = weight(ctx, rng, qtype, 33, 512)
+        out = w.forward(ctx.array(np.zeros((4, 512), np.float32))).numpy()
+        assert np.all(out == 0.0) and not np.signbit(out).any()
+
+
+def glu_floor(g, u, act):
+    if act != hip.ACT_GELU_TANH:
+        return None
+    return 2.0 ** -22 * np.abs(0.5 * g.astype(np.float64) * u.astype(np.float64))
+
+
+@pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+@pytest.mark.parametrize("act", [hip.ACT_SILU, hip.ACT_GELU_TANH])
+@pytest.mark.parametrize("ff,k,m,clamp", [(96, 512, 1, 0.0), (200, 256, 3, 0.0), (48, 768, 5, 0.0),
+                                          (64, 1024, 2, 2.0), (1000, 2048, 1, 0.0)])
+def test_qmm_glu(ctx, qtype, dtype, act, ff, k, m, clamp):
+    rng = np.random.default_rng(ff + k + m + act)
+    graw, gw = weight(ctx, rng, qtype, ff, k, (0.01, 0.05))
+    uraw, uw = weight(ctx, rng, qtype, ff, k, (0.01, 0.05))
+    x = awkward(rng, m, k, 1.0, huge=100.0).astype(NP[dtype])
+    got = ops.QmmWeight.glu(gw, uw, ctx.array(x), ops.Glu(act, clamp)).numpy()
+    g = O.qmm(graw, QT[qtype], ff, k, x, threads=8)
+    u = O.qmm(uraw, QT[qtype], ff, k, x, threads=8)
+    want = O.glu(g, u, act, clamp=clamp)
+    gc = np.minimum(g, clamp) if clamp > 0 else g
+    uc = np.clip(u, -clamp, clamp) if clamp > 0 else u
+    if dtype == "f16":
+        # the kernel rounds act(g) * u once; the oracle's f16 is that of its f32
+        assert_close(got, want.astype(np.float16), floor=glu_floor(gc, uc, act),
+                     what=f"glu {qtype} f16")
+    else:
+        assert_close(got, want, floor=glu_floor(gc, uc, act), what=f"glu {qtype} f32")
+
+
+@pytest.mark.parametrize("qtype,name,n,k", [("q4_0", "ffn_gate", 14336, 4096),
+                                            ("q8_0", "ffn_down", 4096, 14336),
+                                            ("q4_0", "attn_q", 4096, 4096)])
+@pytest.mark.parametrize("m", [1, 4])
+def test_llama3_8b_shapes(ctx, qtype, name, n, k, m):
+    rng = np.random.default_rng(n + k + m)
+    raw, w = weight(ctx, rng, qtype, n, k, (0.001, 0.02))
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    got = w.forward(ctx.array(x)).numpy()
+    assert_bits_equal(got, want_out(raw, qtype, n, k, x, n, "f32"), f"{name} m={m}")
+
+
+def test_host_rejects_bad_arguments(ctx):
+    rng = np.random.default_rng(1)
+    raw, w = weight(ctx, rng, "q4_0", 8, 256)
+    x = ctx.array(rng.standard_normal((2, 256)).astype(np.float32))
+    out = ctx.empty((2, 8), np.float32)
+    for rows in (0, 9):
+        with pytest.raises(hip.CucaError, match="weight rows"):
+            ctx.qmm(w.packed.ptr, hip.GGML_Q4_0, 8, 256, x.ptr, 256, 2, rows, out.ptr, 8, hip.F32)
+    with pytest.raises(hip.CucaError, match="Q4_0"):
+        ctx.qmm(w.packed.ptr, 3, 8, 256, x.ptr, 256, 2, 8, out.ptr, 8, hip.F32)
+    with pytest.raises(hip.CucaError, match="whole number of blocks"):
+        ctx.qmm(w.packed.ptr, hip.GGML_Q4_0, 8, 250, x.ptr, 256, 2, 8, out.ptr, 8, hip.F32)
+    with pytest.raises(hip.CucaError, match="aligned"):
+        ctx.qmm(w.packed.ptr, hip.GGML_Q4_0, 8, 256, x.ptr + 4, 256, 2, 8, out.ptr, 8, hip.F32)
+    with pytest.raises(hip.CucaError, match="activations hold"):
+        w.forward(ctx.array(np.zeros((2, 128), np.float32)))
+    assert ops.QmmWeight.from_raw(ctx, hip.GGML_Q4_0, raw[:-1], 8, 256) is None
+    assert ops.QmmWeight.from_raw(ctx, hip.GGML_Q4_0, raw, 8, 250) is None
+    # m = 0 is a no-op
+    ctx.qmm(w.packed.ptr, hip.GGML_Q4_0, 8, 256, x.ptr, 256, 0, 8, out.ptr, 8, hip.F32)
