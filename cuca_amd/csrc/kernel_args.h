@@ -22,7 +22,8 @@ enum {
     CUCA_STATUS_ROPE_POS = 1,
     CUCA_STATUS_KV_SLOT = 2,
     CUCA_STATUS_KV_RANGE = 3, /* attention: a key position without a block, or a bad range */
-    CUCA_STATUS_WORDS = 4
+    CUCA_STATUS_MOE_PAIR = 4, /* MoE: a pair whose token is outside the activation rows */
+    CUCA_STATUS_WORDS = 5
 };
 
 typedef struct {
@@ -137,8 +138,29 @@ typedef struct {
     int32_t nrb;            /* row blocks of 16 rows                         */
     int32_t ntile;          /* activation tiles                              */
     float clamp;            /* GLU: > 0 clamps gate from above, up to +-clamp */
-    int32_t pad_;
+    int32_t n_tokens;       /* MoE up: rows of x (pair tokens are checked)   */
+    /* MoE (moe_up / moe_down kernels): pairs grouped by expert, expert e
+     * owning pairs [offsets[e], offsets[e+1]); an activation tile is MT
+     * pairs of one expert; the expert's packed matrices start at
+     * w + e * w_estride (and w_up + e * w_estride).                          */
+    const int32_t *offsets;     /* [n_experts + 1], on the device            */
+    const int32_t *pair_token;  /* moe_up: token (row of x) of each pair     */
+    const float *pair_weight;   /* moe_down: routing weight of each pair     */
+    unsigned long long *status;
+    int64_t w_estride;          /* bytes between experts' packed matrices    */
+    int32_t n_experts;
+    int32_t max_pairs;          /* capacity of the pair arrays               */
 } QmmArgs;
+
+/* MoE expert sum: out[t] = sum over i < n_used of scratch[pairs[t][i]]
+ * (pairs in ascending expert order, -1 = none), f32 in order from 0. */
+typedef struct {
+    const float *scratch;   /* [pairs][scratch_ld] f32                       */
+    const int32_t *pairs;   /* [n_tokens][n_used]                            */
+    void *out;              /* [n_tokens][out_ld]                            */
+    int64_t scratch_ld, out_ld;
+    int32_t n_tokens, n_used, n_embd, max_pairs;
+} MoeSumArgs;
 
 typedef struct {
     const uint8_t *src;     /* GGUF rows [n][nb * block bytes]               */

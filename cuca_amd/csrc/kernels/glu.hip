@@ -18,15 +18,27 @@
 // (the identity 1 + tanh(z) = 2 / (1 + e^-2z) removes the cancellation of
 // 1 + tanh(z) for z << 0).  v_exp_f32 and v_rcp_f32 are accurate to 1 ulp;
 // the relative error stays below 1e-5 for |g| < 88 (the argument's own
-// rounding, |arg| * 2^-24, dominates for large |g|).
+// rounding, |arg| * 2^-24, dominates for large |g|); below that the result
+// underflows through the denormals to -0, as the reference's does.
 
 #include "common.h"
 
 #define CUCA_LOG2E 1.4426950408889634f
 
+// g * rcp(t) for t >= 1.  v_rcp_f32 flushes a denormal result to zero, so
+// for t >= 2^64 (g < -44 in SiLU) the reciprocal is taken of t * 2^-64 and
+// the product rescaled: near the f32 maximum (g < -87) the result then
+// underflows gradually, as g / t does in the reference (candle's
+// v / (1 + exp(-v))).  Scaling by a power of two does not change the
+// reciprocal's significand.
+__device__ static inline float mul_rcp(float g, float t) {
+    return t < 0x1p64f ? g * __builtin_amdgcn_rcpf(t)
+                       : (g * __builtin_amdgcn_rcpf(t * 0x1p-64f)) * 0x1p-64f;
+}
+
 __device__ static inline float act_silu(float g) {
     const float e = __builtin_amdgcn_exp2f(g * -CUCA_LOG2E);
-    return g * __builtin_amdgcn_rcpf(1.0f + e);
+    return mul_rcp(g, 1.0f + e);
 }
 
 __device__ static inline float act_gelu_tanh(float g) {
@@ -34,7 +46,7 @@ __device__ static inline float act_gelu_tanh(float g) {
     const float k2 = -2.0f * 0.7978845608028654f * CUCA_LOG2E;
     const float p = fmaf(0.044715f, g * g, 1.0f);
     const float e = __builtin_amdgcn_exp2f((k2 * g) * p);
-    return g * __builtin_amdgcn_rcpf(1.0f + e);
+    return mul_rcp(g, 1.0f + e);
 }
 
 template <int ACT> __device__ static inline float act_fn(float g) {

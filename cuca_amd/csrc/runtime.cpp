@@ -75,6 +75,7 @@ struct cuca_hip_ctx {
     int64_t last_vocab = 0;       // for the out-of-range message
     int64_t last_kv_blocks = 0;   // the pool size of the last K/V store (for messages)
     int64_t last_table_rows = 0;
+    int64_t last_moe_tokens = 0;  // the activation rows of the last MoE up call
     std::string error;
     // per-kernel timing (cuca_hip_profile_start/stop)
     struct ProfRec { int kernel; hipEvent_t start, stop; };
@@ -316,6 +317,11 @@ cuca_status cuca_hip_check_device(cuca_hip_ctx *ctx) {
         unsigned long long v = w[CUCA_STATUS_KV_SLOT];
         return fail(ctx, CUCA_OUT_OF_RANGE, "K/V slot %d outside the pool of %lld blocks (row %u)",
                     (int)(v & 0xffffffffu), (long long)ctx->last_kv_blocks, (unsigned)(v >> 32));
+    }
+    if (w[CUCA_STATUS_MOE_PAIR] != none) {
+        unsigned long long v = w[CUCA_STATUS_MOE_PAIR];
+        return fail(ctx, CUCA_OUT_OF_RANGE, "a routed token (%d) outside the %lld rows (pair %u)",
+                    (int)(v & 0xffffffffu), (long long)ctx->last_moe_tokens, (unsigned)(v >> 32));
     }
     unsigned long long v = w[CUCA_STATUS_KV_RANGE];
     if ((v & 0xffffffffu) == 0xffffffffu)
@@ -956,6 +962,140 @@ cuca_status cuca_hip_qmm_glu(cuca_hip_ctx *ctx, const void *gate, const void *up
         return fail(ctx, CUCA_INVALID_ARG, "bad activation %d", (int)act);
     return qmm_common(ctx, gate, up, ggml_type, ff, k, x, ldx, m, ff, act == CUCA_ACT_SILU ? 1 : 2, clamp,
                       out, out_ld, dtype);
+}
+
+// MoE (expert_sum, cpu.rs:3599-3642; the reference GPU engine's moe_up /
+// moe_down / moe_sum, moe_kernel.rs:1163-1385).  Pairs are grouped by
+// expert: expert e owns pairs [offsets[e], offsets[e+1]) of the pair arrays,
+// which hold max_pairs entries; the counts are read on the device.
+// up: 1 SiLU, 2 GELU-tanh; 0 = down.
+static cuca_status moe_common(cuca_hip_ctx *ctx, const void *w, const void *w_up, int64_t estride,
+                              uint32_t ggml_type, int64_t n, int64_t k, int32_t n_experts, const void *x,
+                              int64_t ldx, int64_t n_tokens, const int32_t *offsets, const int32_t *pair_token,
+                              const float *pair_weight, int64_t max_pairs, int up, float clamp, void *out,
+                              int64_t out_ld, cuca_dtype dtype) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    int g = 0, gb = 0;
+    if ((st = qweight_shape(ctx, ggml_type, n, k, &g, &gb)) != CUCA_OK) return st;
+    if (!dtype_ok(dtype)) return fail(ctx, CUCA_INVALID_ARG, "bad dtype %d", (int)dtype);
+    if (n_experts <= 0) return fail(ctx, CUCA_INVALID_ARG, "moe: bad expert count %d", n_experts);
+    if (max_pairs < 0 || max_pairs > 0x7fffffffll)
+        return fail(ctx, CUCA_INVALID_ARG, "moe: bad pair capacity %lld", (long long)max_pairs);
+    if (ldx < k) return fail(ctx, CUCA_INVALID_ARG, "moe: activation row stride %lld shorter than %lld",
+                             (long long)ldx, (long long)k);
+    if (out_ld < n) return fail(ctx, CUCA_INVALID_ARG, "moe: output row stride %lld shorter than %lld",
+                                (long long)out_ld, (long long)n);
+    if (!(clamp == clamp)) return fail(ctx, CUCA_INVALID_ARG, "clamp is NaN");
+    if (max_pairs == 0) return CUCA_OK;
+    if (!w || !x || !out || !offsets || (up && (!w_up || !pair_token)) || (!up && !pair_weight))
+        return fail(ctx, CUCA_INVALID_ARG, "null pointer");
+    if (up && (n_tokens <= 0 || n_tokens > 0x7fffffffll))
+        return fail(ctx, CUCA_INVALID_ARG, "moe: bad token count %lld", (long long)n_tokens);
+    const int64_t nb = k / 32, ng = (nb + g - 1) / g;
+    const int64_t packed = n * ng * gb;
+    if (estride < packed || estride % 16 != 0)
+        return fail(ctx, CUCA_INVALID_ARG, "moe: expert stride %lld bytes, at least %lld (a multiple of 16) needed",
+                    (long long)estride, (long long)packed);
+    const size_t es = esize(dtype);
+    if (!al16(w) || (w_up && !al16(w_up))) return fail(ctx, CUCA_INVALID_ARG, "packed weights must be 16-byte aligned");
+    if (!al16(x) || ((size_t)ldx * es) % 16 != 0)
+        return fail(ctx, CUCA_INVALID_ARG, "moe: activation rows must start 16-byte aligned");
+    // tile rows from the mean pairs per expert
+    const double mean = (double)max_pairs / (double)n_experts;
+    const int mt = mean <= 1.5 ? 1 : mean <= 3.0 ? 2 : 4;
+    const int mi = mt == 1 ? 0 : mt == 2 ? 1 : 2;
+    const int64_t ntile = (max_pairs + mt - 1) / mt + n_experts; // >= sum over experts of ceil(n_e / mt)
+    const int64_t nrb = (n + 15) / 16, nrb8 = (nrb + 7) / 8 * 8;
+    if (nrb8 * ntile > 0x7fffffffll) return fail(ctx, CUCA_UNSUPPORTED, "moe: grid too large");
+    // [dtype][format][up silu, up gelu, down][tile rows 1, 2, 4]
+    static const Kernel table_k[2][2][3][3] = {
+        {{{cuca_moe_up_f32_q4_0_silu_m1, cuca_moe_up_f32_q4_0_silu_m2, cuca_moe_up_f32_q4_0_silu_m4},
+          {cuca_moe_up_f32_q4_0_gelu_m1, cuca_moe_up_f32_q4_0_gelu_m2, cuca_moe_up_f32_q4_0_gelu_m4},
+          {cuca_moe_down_f32_q4_0_m1, cuca_moe_down_f32_q4_0_m2, cuca_moe_down_f32_q4_0_m4}},
+         {{cuca_moe_up_f32_q8_0_silu_m1, cuca_moe_up_f32_q8_0_silu_m2, cuca_moe_up_f32_q8_0_silu_m4},
+          {cuca_moe_up_f32_q8_0_gelu_m1, cuca_moe_up_f32_q8_0_gelu_m2, cuca_moe_up_f32_q8_0_gelu_m4},
+          {cuca_moe_down_f32_q8_0_m1, cuca_moe_down_f32_q8_0_m2, cuca_moe_down_f32_q8_0_m4}}},
+        {{{cuca_moe_up_f16_q4_0_silu_m1, cuca_moe_up_f16_q4_0_silu_m2, cuca_moe_up_f16_q4_0_silu_m4},
+          {cuca_moe_up_f16_q4_0_gelu_m1, cuca_moe_up_f16_q4_0_gelu_m2, cuca_moe_up_f16_q4_0_gelu_m4},
+          {cuca_moe_down_f16_q4_0_m1, cuca_moe_down_f16_q4_0_m2, cuca_moe_down_f16_q4_0_m4}},
+         {{cuca_moe_up_f16_q8_0_silu_m1, cuca_moe_up_f16_q8_0_silu_m2, cuca_moe_up_f16_q8_0_silu_m4},
+          {cuca_moe_up_f16_q8_0_gelu_m1, cuca_moe_up_f16_q8_0_gelu_m2, cuca_moe_up_f16_q8_0_gelu_m4},
+          {cuca_moe_down_f16_q8_0_m1, cuca_moe_down_f16_q8_0_m2, cuca_moe_down_f16_q8_0_m4}}}};
+    const Kernel kk = table_k[dtype == CUCA_F16][ggml_type == CUCA_GGML_Q8_0][up ? up - 1 : 2][mi];
+    QmmArgs a{};
+    a.w = static_cast<const uint8_t *>(w);
+    a.w_up = static_cast<const uint8_t *>(w_up);
+    a.x = x;
+    a.out = out;
+    a.ldx = ldx;
+    a.out_ld = out_ld;
+    a.row_bytes = ng * gb;
+    a.rows = (int32_t)n;
+    a.m = (int32_t)max_pairs;
+    a.nb = (int32_t)nb;
+    a.ng = (int32_t)ng;
+    a.nrb = (int32_t)nrb;
+    a.ntile = (int32_t)ntile;
+    a.clamp = clamp > 0.0f ? clamp : 0.0f;
+    a.n_tokens = (int32_t)(up ? n_tokens : max_pairs);
+    a.offsets = offsets;
+    a.pair_token = pair_token;
+    a.pair_weight = pair_weight;
+    a.status = ctx->status;
+    a.w_estride = estride;
+    a.n_experts = n_experts;
+    a.max_pairs = (int32_t)max_pairs;
+    if (up) ctx->last_moe_tokens = n_tokens;
+    return launch(ctx, kk, (unsigned)(nrb8 * ntile), CUCA_BLOCK_THREADS, 0, a);
+}
+
+cuca_status cuca_hip_moe_up(cuca_hip_ctx *ctx, const void *gate, const void *up, int64_t expert_stride,
+                            uint32_t ggml_type, int64_t ff, int64_t n_embd, int32_t n_experts, const void *x,
+                            int64_t ldx, int64_t n_tokens, const int32_t *offsets, const int32_t *pair_token,
+                            int64_t max_pairs, cuca_act act, float clamp, void *hidden, int64_t hidden_ld,
+                            cuca_dtype dtype) {
+    if (act != CUCA_ACT_SILU && act != CUCA_ACT_GELU_TANH)
+        return fail(ctx, CUCA_INVALID_ARG, "bad activation %d", (int)act);
+    return moe_common(ctx, gate, up, expert_stride, ggml_type, ff, n_embd, n_experts, x, ldx, n_tokens, offsets,
+                      pair_token, nullptr, max_pairs, act == CUCA_ACT_SILU ? 1 : 2, clamp, hidden, hidden_ld,
+                      dtype);
+}
+
+cuca_status cuca_hip_moe_down(cuca_hip_ctx *ctx, const void *down, int64_t expert_stride, uint32_t ggml_type,
+                              int64_t n_embd, int64_t ff, int32_t n_experts, const void *hidden,
+                              int64_t hidden_ld, const int32_t *offsets, const float *pair_weight,
+                              int64_t max_pairs, float *scratch, int64_t scratch_ld, cuca_dtype dtype) {
+    return moe_common(ctx, down, nullptr, expert_stride, ggml_type, n_embd, ff, n_experts, hidden, hidden_ld, 0,
+                      offsets, nullptr, pair_weight, max_pairs, 0, 0.0f, scratch, scratch_ld, dtype);
+}
+
+cuca_status cuca_hip_moe_sum(cuca_hip_ctx *ctx, const float *scratch, int64_t scratch_ld, int64_t max_pairs,
+                             const int32_t *token_pairs, int32_t n_used, int64_t n_tokens, int64_t n_embd,
+                             void *out, int64_t out_ld, cuca_dtype dtype) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    if (!dtype_ok(dtype)) return fail(ctx, CUCA_INVALID_ARG, "bad dtype %d", (int)dtype);
+    if (n_tokens < 0 || n_tokens > 0x7fffffffll || n_embd <= 0 || n_embd > 0x7fffffffll || n_used <= 0 ||
+        max_pairs < 0 || max_pairs > 0x7fffffffll)
+        return fail(ctx, CUCA_INVALID_ARG, "moe sum: bad shape");
+    if (scratch_ld < n_embd || out_ld < n_embd) return fail(ctx, CUCA_INVALID_ARG, "moe sum: row strides shorter than n_embd");
+    if (n_tokens == 0) return CUCA_OK;
+    if (!scratch || !token_pairs || !out) return fail(ctx, CUCA_INVALID_ARG, "null pointer");
+    const int64_t nq = (n_embd + 3) / 4;
+    if (n_tokens * nq / CUCA_BLOCK_THREADS + 1 > 0x7fffffffll) return fail(ctx, CUCA_UNSUPPORTED, "moe sum: grid too large");
+    MoeSumArgs a{};
+    a.scratch = scratch;
+    a.pairs = token_pairs;
+    a.out = out;
+    a.scratch_ld = scratch_ld;
+    a.out_ld = out_ld;
+    a.n_tokens = (int32_t)n_tokens;
+    a.n_used = n_used;
+    a.n_embd = (int32_t)n_embd;
+    a.max_pairs = (int32_t)max_pairs;
+    return launch(ctx, dtype == CUCA_F16 ? cuca_moe_sum_f16 : cuca_moe_sum_f32, div_up(n_tokens * nq, CUCA_BLOCK_THREADS),
+                  CUCA_BLOCK_THREADS, 0, a);
 }
 
 // RopeSpec::tables (rope.rs:118-151): f64 angles with the platform libm,

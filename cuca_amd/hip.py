@@ -77,6 +77,11 @@ SIGNATURES = {
     "cuca_hip_qmm": (_st, [_p, _p, _u32, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _st]),
     "cuca_hip_qmm_glu": (_st, [_p, _p, _p, _u32, _i64, _i64, _p, _i64, _i64, _st, _f32, _p, _i64,
                                _st]),
+    "cuca_hip_moe_up": (_st, [_p, _p, _p, _i64, _u32, _i64, _i64, _i32, _p, _i64, _i64, _p, _p, _i64,
+                              _st, _f32, _p, _i64, _st]),
+    "cuca_hip_moe_down": (_st, [_p, _p, _i64, _u32, _i64, _i64, _i32, _p, _i64, _p, _p, _i64, _p,
+                                _i64, _st]),
+    "cuca_hip_moe_sum": (_st, [_p, _p, _i64, _i64, _p, _i32, _i64, _i64, _p, _i64, _st]),
     "cuca_hip_graph_begin": (_st, [_p]),
     "cuca_hip_graph_end": (_st, [_p, _pp]),
     "cuca_hip_graph_launch": (_st, [_p, _p]),
@@ -329,6 +334,24 @@ class Context:
     def qmm_glu(self, gate, up, ggml_type, ff, k, x, ldx, m, act, clamp, out, out_ld, dtype):
         self.check(self.L.cuca_hip_qmm_glu(self.ptr, gate, up, ggml_type, ff, k, x, ldx, m, act,
                                            clamp, out, out_ld, dtype))
+
+
+    def moe_up(self, gate, up, estride, ggml_type, ff, n_embd, n_experts, x, ldx, n_tokens, offsets,
+               pair_token, max_pairs, act, clamp, hidden, hidden_ld, dtype):
+        self.check(self.L.cuca_hip_moe_up(self.ptr, gate, up, estride, ggml_type, ff, n_embd, n_experts,
+                                          x, ldx, n_tokens, offsets, pair_token, max_pairs, act, clamp,
+                                          hidden, hidden_ld, dtype))
+
+    def moe_down(self, down, estride, ggml_type, n_embd, ff, n_experts, hidden, hidden_ld, offsets,
+                 pair_weight, max_pairs, scratch, scratch_ld, dtype):
+        self.check(self.L.cuca_hip_moe_down(self.ptr, down, estride, ggml_type, n_embd, ff, n_experts,
+                                            hidden, hidden_ld, offsets, pair_weight, max_pairs, scratch,
+                                            scratch_ld, dtype))
+
+    def moe_sum(self, scratch, scratch_ld, max_pairs, token_pairs, n_used, n_tokens, n_embd, out,
+                out_ld, dtype):
+        self.check(self.L.cuca_hip_moe_sum(self.ptr, scratch, scratch_ld, max_pairs, token_pairs,
+                                           n_used, n_tokens, n_embd, out, out_ld, dtype))
 
 
 class Graph:

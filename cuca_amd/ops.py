@@ -12,6 +12,7 @@ under src/provider/local/model/ of nassor/cuca 0.10.0), so that a caller
     RopeSpec.plain(kind, n_dims, base).tables(factors, positions)    rope.rs:62-151
     QmmWeight.from_raw(dtype, data, n, k).forward_rows(x, m, rows)    qmm.rs:1744-1838
     QmmWeight.glu(gate, up, x, glu)  (act(gate x) * up x, fused)     cpu.rs:342-371, 3554-3566
+    ExpertBank.from_raw(...).expert_sum(x, per_expert, glu)           cpu.rs:373-419, 3599-3642
 
 Tensors are DeviceArrays (device memory through the C ABI); every op runs on
 the gfx950 kernels of libcuca_hip.so.  There is no host fallback.
@@ -337,3 +338,82 @@ class QmmWeight:
                     glu.act, glu.clamp if glu.clamp is not None else 0.0, out.ptr, out.shape[1],
                     hip.dtype_code(x.dtype))
         return out
+
+
+class ExpertBank:
+    """The routed experts of one MoE layer, resident in HBM: per expert the
+    gate, up and down matrices (GGUF Q4_0 / Q8_0) packed into three pools, one
+    expert every `stride` bytes (the reference GPU engine's expert slots,
+    moe_kernel.rs)."""
+
+    def __init__(self, ctx, dtype, n_embd, ff, n_experts, pools, stride_gu, stride_d):
+        self.ctx, self.dtype, self.n_embd, self.ff, self.n_experts = ctx, dtype, n_embd, ff, n_experts
+        self.gate, self.up, self.down = pools
+        self.stride_gu, self.stride_d = stride_gu, stride_d
+
+    @classmethod
+    def from_raw(cls, ctx, dtype, experts, n_embd, ff):
+        """experts[e] = (gate, up, down) GGUF bytes of [ff, n_embd],
+        [ff, n_embd], [n_embd, ff]."""
+        def pool(mats, n, k):
+            one = hip.qweight_bytes(dtype, n, k)
+            stride = (one + 15) // 16 * 16
+            dst = ctx.empty((stride * len(mats),), np.uint8)
+            for e, raw in enumerate(mats):
+                src = ctx.array(np.ascontiguousarray(raw, dtype=np.uint8).reshape(-1))
+                ctx.qweight_pack(src.ptr, dtype, n, k, dst.ptr + e * stride)
+                ctx.sync()
+                src.free()
+            return dst, stride
+        g, sgu = pool([m[0] for m in experts], ff, n_embd)
+        u, _ = pool([m[1] for m in experts], ff, n_embd)
+        d, sd = pool([m[2] for m in experts], n_embd, ff)
+        return cls(ctx, dtype, n_embd, ff, len(experts), (g, u, d), sgu, sd)
+
+    @staticmethod
+    def grouped(per_expert, n_tokens, n_used):
+        """Routing (moe.rs:15-21) as device-ready arrays: offsets
+        [n_experts + 1], pair_token and pair_weight in expert order, and per
+        token its pairs in ascending expert order ([n_tokens, n_used], -1
+        where a token has fewer)."""
+        offsets = np.zeros(len(per_expert) + 1, np.int32)
+        tok, wt = [], []
+        token_pairs = np.full((n_tokens, n_used), -1, np.int32)
+        fill = np.zeros(n_tokens, np.int64)
+        for e, picks in enumerate(per_expert):
+            for t, w in picks:
+                token_pairs[t, fill[t]] = len(tok)
+                fill[t] += 1
+                tok.append(t)
+                wt.append(w)
+            offsets[e + 1] = len(tok)
+        return (offsets, np.asarray(tok, np.int32), np.asarray(wt, np.float32), token_pairs)
+
+    def expert_sum(self, x, per_expert, glu, n_used):
+        """The routed experts' output over the rows x ([t, n_embd] DeviceArray)
+        for `per_expert` = [(token, weight)] per expert: moe_up, moe_down,
+        moe_sum.  The per-pair hidden activations are held in x's dtype (f32
+        keeps the reference CPU engine's values).  Returns (out [t, n_embd] in
+        x's dtype, hidden, scratch)."""
+        hidden_dtype = x.dtype
+        ctx = self.ctx
+        t = x.shape[0]
+        offsets, tok, wt, token_pairs = self.grouped(per_expert, t, n_used)
+        pairs = max(len(tok), 1)
+        d_off, d_tok = ctx.array(offsets), ctx.array(tok if len(tok) else np.zeros(1, np.int32))
+        d_wt = ctx.array(wt if len(wt) else np.zeros(1, np.float32))
+        d_tp = ctx.array(token_pairs)
+        hidden = ctx.empty((pairs, self.ff), hidden_dtype)
+        scratch = ctx.empty((pairs, self.n_embd), np.float32)
+        out = ctx.empty((t, self.n_embd), x.dtype)
+        ctx.moe_up(self.gate.ptr, self.up.ptr, self.stride_gu, self.dtype, self.ff, self.n_embd,
+                   self.n_experts, x.ptr, self.n_embd, t, d_off.ptr, d_tok.ptr, len(tok), glu.act,
+                   glu.clamp or 0.0, hidden.ptr, self.ff, hip.dtype_code(hidden_dtype))
+        ctx.moe_down(self.down.ptr, self.stride_d, self.dtype, self.n_embd, self.ff, self.n_experts,
+                     hidden.ptr, self.ff, d_off.ptr, d_wt.ptr, len(tok), scratch.ptr, self.n_embd,
+                     hip.dtype_code(hidden_dtype))
+        ctx.moe_sum(scratch.ptr, self.n_embd, len(tok), d_tp.ptr, n_used, t, self.n_embd, out.ptr,
+                    self.n_embd, hip.dtype_code(x.dtype))
+        # the routing arrays live as long as the output the queued kernels write
+        out.keep = (d_off, d_tok, d_wt, d_tp)
+        return out, hidden, scratch

@@ -29,6 +29,8 @@
  *   cuca_hip_qmm           QmmWeight::forward_rows        qmm.rs:1810-1838
  *   cuca_hip_qmm_glu       gate/up qmm + Glu::apply       cpu.rs:342-371, 3554-3566
  *   cuca_hip_qweight_pack  (the weight upload)            qmm.rs:1763-1783
+ *   cuca_hip_moe_up/down/  expert_sum, CpuExpert          cpu.rs:373-419, 3599-3642
+ *            _sum          (GPU moe_up/moe_down/moe_sum)  moe_kernel.rs:1163-1385
  *
  * Conventions
  * - A context owns one device, one HIP stream (or borrows the caller's),
@@ -309,6 +311,38 @@ cuca_status cuca_hip_qmm(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type, i
 cuca_status cuca_hip_qmm_glu(cuca_hip_ctx *ctx, const void *gate, const void *up, uint32_t ggml_type,
                              int64_t ff, int64_t k, const void *x, int64_t ldx, int64_t m, cuca_act act,
                              float clamp, void *out, int64_t out_ld, cuca_dtype dtype);
+
+/* Routed experts (MoE), the CPU engine's expert_sum (cpu.rs:3599-3642)
+ * with CpuExpert::forward / add_picks (cpu.rs:373-419), split as the
+ * reference GPU engine splits it (MoeKernels::moe_up / moe_down / moe_sum,
+ * moe_kernel.rs:1163-1385).  Routing (moe.rs:39-94) is the caller's: the
+ * (token, expert) pairs are grouped by expert, expert e owning pairs
+ * [offsets[e], offsets[e+1]) in token order (device int32[n_experts + 1],
+ * read on the device; the pair arrays hold max_pairs entries).  The
+ * experts' packed matrices (cuca_hip_qweight_pack) lie expert_stride bytes
+ * apart (a pool, as the reference GPU engine's expert slots).
+ *
+ * moe_up: hidden[p] = act(gate_e . x[pair_token[p]]) * (up_e . x[...]), the
+ *   products bit-exact with cuca_hip_qmm, the activation and clamp as
+ *   cuca_hip_glu.  hidden: [max_pairs][hidden_ld] of dtype.  A pair token
+ *   outside [0, n_tokens) is skipped and reported by cuca_hip_check_device.
+ * moe_down: scratch[p] = (down_e . hidden[p]) * pair_weight[p] (f32; the
+ *   product of add_picks, cpu.rs:400-417).
+ * moe_sum: out[t] = sum over i < n_used of scratch[token_pairs[t][i]], in
+ *   f32 from 0, in the given order (ascending expert order, as expert_sum
+ *   adds); entries < 0 are skipped. */
+cuca_status cuca_hip_moe_up(cuca_hip_ctx *ctx, const void *gate, const void *up, int64_t expert_stride,
+                            uint32_t ggml_type, int64_t ff, int64_t n_embd, int32_t n_experts, const void *x,
+                            int64_t ldx, int64_t n_tokens, const int32_t *offsets, const int32_t *pair_token,
+                            int64_t max_pairs, cuca_act act, float clamp, void *hidden, int64_t hidden_ld,
+                            cuca_dtype dtype);
+cuca_status cuca_hip_moe_down(cuca_hip_ctx *ctx, const void *down, int64_t expert_stride, uint32_t ggml_type,
+                              int64_t n_embd, int64_t ff, int32_t n_experts, const void *hidden,
+                              int64_t hidden_ld, const int32_t *offsets, const float *pair_weight,
+                              int64_t max_pairs, float *scratch, int64_t scratch_ld, cuca_dtype dtype);
+cuca_status cuca_hip_moe_sum(cuca_hip_ctx *ctx, const float *scratch, int64_t scratch_ld, int64_t max_pairs,
+                             const int32_t *token_pairs, int32_t n_used, int64_t n_tokens, int64_t n_embd,
+                             void *out, int64_t out_ld, cuca_dtype dtype);
 
 /* RopeSpec (rope.rs:62-79). yarn_ext_factor == 0 disables YaRN. */
 typedef struct {

@@ -302,3 +302,32 @@ def qmm(w, ggml_type, n, k, x, rows=None, threads=1):
     if rc != 0:
         raise OracleError(f"qmm: {rows} weight rows of {n}")
     return out
+
+
+def expert_sum(x, experts, qtype, per_expert, act, clamp=0.0, threads=1):
+    """expert_sum (cpu.rs:3599-3642) with CpuExpert::forward / add_picks
+    (cpu.rs:373-419): x [t, n_embd] (f32 or f16, widened); experts[e] =
+    (gate, up, down) GGUF bytes of [ff, n_embd], [ff, n_embd], [n_embd, ff];
+    per_expert[e] = [(token, weight)] in token order.  Every non-empty expert
+    runs once over its picked rows, in ascending expert order, and
+    out[token] += y * weight (f32, each product and sum rounded) from zeros.
+    Returns (out f32 [t, n_embd], hidden {(e, i): f32 [ff]}) -- hidden is the
+    activation each pick's down projection read."""
+    x = np.ascontiguousarray(x)
+    t, n_embd = x.shape
+    out = np.zeros((t, n_embd), np.float32)
+    hidden = {}
+    for e, picks in enumerate(per_expert):
+        if not picks:
+            continue
+        gate, up, down = experts[e]
+        ff = gate.size // row_bytes(qtype, n_embd)
+        rows = x[[tok for tok, _ in picks]].astype(np.float32)
+        g = qmm(gate, qtype, ff, n_embd, rows, threads=threads)
+        u = qmm(up, qtype, ff, n_embd, rows, threads=threads)
+        h = glu(g, u, act, clamp=clamp, threads=threads)
+        y = qmm(down, qtype, n_embd, ff, h, threads=threads)
+        for i, (tok, w) in enumerate(picks):
+            hidden[(e, i)] = h[i]
+            out[tok] = (out[tok] + (y[i] * np.float32(w)).astype(np.float32)).astype(np.float32)
+    return out, hidden

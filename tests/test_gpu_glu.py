@@ -109,3 +109,17 @@ def test_full_size_config_c_sampled_rows(ctx):
         [[0, n - 1], np.random.default_rng(2).integers(0, n, 30)]))).cuda()
     ys = y[sample].cpu().numpy()
     check(out[sample].cpu().numpy(), ys[:, :ff], ys[:, ff:], hip.ACT_SILU, what="C full size")
+
+
+@pytest.mark.parametrize("act", [hip.ACT_SILU, hip.ACT_GELU_TANH])
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+def test_tails_underflow_like_the_reference(ctx, act, dtype):
+    """Gate values out to +-100 and beyond: for g < -87 the reference's
+    g / (1 + exp(-g)) passes through the f32 denormals to -0, and for large
+    positive g it is g itself (no overflow in the kernel's rescaling)."""
+    g = np.concatenate([np.linspace(-100.0, 100.0, 4093), [-1e30, 1e30, 3e38]]).astype(np.float32)
+    g = g.reshape(4, -1).astype(NP[dtype]) if dtype == "f32" else \
+        np.clip(g, -6e4, 6e4).reshape(4, -1).astype(np.float16)
+    u = np.full(g.shape, 0.75, NP[dtype])
+    got = ops.Glu(act).apply(ctx.array(g), ctx.array(u)).numpy()
+    check(got, g, u, act, what=f"tails act {act} {dtype}")
