@@ -150,7 +150,28 @@ typedef struct {
     int64_t w_estride;          /* bytes between experts' packed matrices    */
     int32_t n_experts;
     int32_t max_pairs;          /* capacity of the pair arrays               */
+    /* LM head epilogue (plain kernels; cap_flags 0 = none): bit 1 scales
+     * by mul1 = f32(1 / logit_scale), bit 2 by mul2 = logit_mult, bit 4
+     * soft-caps: tanh(v * softcap_inv) * softcap; each step adds +0 as
+     * candle's affine does (cpu.rs:2603-2617).                              */
+    int32_t cap_flags;
+    float mul1, mul2, softcap_inv, softcap;
+    int32_t pad2_;
 } QmmArgs;
+
+/* Greedy argmax and top-k over logits rows (sampler.rs greedy and
+ * select_top_k).  top-k: keys are logit / temperature; the k best finite
+ * ones in (logit desc, id asc) order go to out_logits / out_ids, their
+ * count to out_count. */
+typedef struct {
+    const void *logits;     /* [rows][ld] f32 or f16                          */
+    float *out_logits;      /* [rows][k]                                      */
+    uint32_t *out_ids;      /* [rows][k] (argmax: [rows])                     */
+    int32_t *out_count;     /* [rows]                                         */
+    int64_t ld;
+    int32_t rows, vocab, k;
+    float temperature;
+} PickArgs;
 
 /* MoE expert sum: out[t] = sum over i < n_used of scratch[pairs[t][i]]
  * (pairs in ascending expert order, -1 = none), f32 in order from 0. */

@@ -11,3 +11,4 @@
 #include "rope.hip"
 #include "attn.hip"
 #include "qmm.hip"
+#include "pick.hip"

@@ -538,6 +538,11 @@ __device__ static inline void qmm_body(const QmmArgs &a) {
             }
             o = (ACT == 0 ? act_silu(g) : act_gelu_tanh(g)) * u;
         }
+        if (MODE == 0 && !GLU && a.cap_flags) { // cap_logits (cpu.rs:2603-2617)
+            if (a.cap_flags & 1) o = o * a.mul1 + 0.0f;
+            if (a.cap_flags & 2) o = o * a.mul2 + 0.0f;
+            if (a.cap_flags & 4) o = tanhf(o * a.softcap_inv + 0.0f) * a.softcap + 0.0f;
+        }
         if (lane == 0 && row < a.rows && tl.xrow[j] >= 0) {
             if (MODE == 2) // CpuExpert::add_picks: y * weight (cpu.rs:400-417)
                 reinterpret_cast<float *>(a.out)[tl.orow[j] + row] = o * tl.weight[j];

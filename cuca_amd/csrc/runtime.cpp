@@ -882,10 +882,16 @@ cuca_status cuca_hip_qweight_pack(cuca_hip_ctx *ctx, const void *gguf, uint32_t 
                   div_up(pieces, CUCA_BLOCK_THREADS), CUCA_BLOCK_THREADS, 0, a);
 }
 
+// The LM head epilogue of cap_logits (cpu.rs:2603-2617); all 1 / 0 = none.
+struct LogitCap {
+    float logit_scale = 1.0f, logit_mult = 1.0f, softcap = 0.0f;
+};
+
 // glu: 0 plain, 1 SiLU, 2 GELU-tanh
 static cuca_status qmm_common(cuca_hip_ctx *ctx, const void *w, const void *w_up, uint32_t ggml_type,
                               int64_t n, int64_t k, const void *x, int64_t ldx, int64_t m, int64_t rows,
-                              int glu, float clamp, void *out, int64_t out_ld, cuca_dtype dtype) {
+                              int glu, float clamp, void *out, int64_t out_ld, cuca_dtype dtype,
+                              const LogitCap &cap = LogitCap()) {
     cuca_status st = use(ctx);
     if (st != CUCA_OK) return st;
     int g = 0, gb = 0;
@@ -946,7 +952,133 @@ static cuca_status qmm_common(cuca_hip_ctx *ctx, const void *w, const void *w_up
     a.nrb = (int32_t)nrb;
     a.ntile = (int32_t)ntile;
     a.clamp = clamp > 0.0f ? clamp : 0.0f;
+    // candle's affine takes its factor as f64 and converts it to f32
+    if (cap.logit_scale != 1.0f) { a.cap_flags |= 1; a.mul1 = (float)(1.0 / (double)cap.logit_scale); }
+    if (cap.logit_mult != 1.0f) { a.cap_flags |= 2; a.mul2 = cap.logit_mult; }
+    if (cap.softcap > 0.0f) {
+        a.cap_flags |= 4;
+        a.softcap_inv = (float)(1.0 / (double)cap.softcap);
+        a.softcap = cap.softcap;
+    }
     return launch(ctx, kk, (unsigned)(nrb8 * ntile), CUCA_BLOCK_THREADS, 0, a);
+}
+
+cuca_status cuca_hip_lm_head(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type, int64_t vocab, int64_t n_embd,
+                             const void *x, int64_t ldx, int64_t m, int64_t rows, float logit_scale,
+                             float logit_mult, float softcap, void *logits, int64_t logits_ld, cuca_dtype dtype) {
+    if (!(logit_scale > 0.0f) || !std::isfinite(logit_scale) || !std::isfinite(logit_mult) ||
+        !(softcap >= 0.0f) || !std::isfinite(softcap))
+        return fail(ctx, CUCA_INVALID_ARG, "lm head: bad logit scale, multiplier or soft-cap");
+    LogitCap cap;
+    cap.logit_scale = logit_scale;
+    cap.logit_mult = logit_mult;
+    cap.softcap = softcap;
+    return qmm_common(ctx, w, nullptr, ggml_type, vocab, n_embd, x, ldx, m, rows, 0, 0.0f, logits, logits_ld,
+                      dtype, cap);
+}
+
+static cuca_status pick_check(cuca_hip_ctx *ctx, const void *logits, int64_t ld, int64_t rows, int64_t vocab,
+                              cuca_dtype dtype) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    if (!dtype_ok(dtype)) return fail(ctx, CUCA_INVALID_ARG, "bad dtype %d", (int)dtype);
+    if (rows < 0 || rows > 0x7fffffffll || vocab <= 0 || vocab > 0x7fffffffll || ld < vocab)
+        return fail(ctx, CUCA_INVALID_ARG, "bad logits shape (%lld rows of %lld, stride %lld)", (long long)rows,
+                    (long long)vocab, (long long)ld);
+    if (rows > 0 && !logits) return fail(ctx, CUCA_INVALID_ARG, "null logits");
+    return CUCA_OK;
+}
+
+cuca_status cuca_hip_argmax(cuca_hip_ctx *ctx, const void *logits, int64_t ld, int64_t rows, int64_t vocab,
+                            cuca_dtype dtype, uint32_t *ids) {
+    cuca_status st = pick_check(ctx, logits, ld, rows, vocab, dtype);
+    if (st != CUCA_OK || rows == 0) return st;
+    if (!ids) return fail(ctx, CUCA_INVALID_ARG, "null output");
+    PickArgs a{};
+    a.logits = logits;
+    a.out_ids = ids;
+    a.ld = ld;
+    a.rows = (int32_t)rows;
+    a.vocab = (int32_t)vocab;
+    return launch(ctx, dtype == CUCA_F16 ? cuca_argmax_f16 : cuca_argmax_f32, (unsigned)rows, CUCA_BLOCK_THREADS, 0, a);
+}
+
+cuca_status cuca_hip_top_k(cuca_hip_ctx *ctx, const void *logits, int64_t ld, int64_t rows, int64_t vocab,
+                           cuca_dtype dtype, int32_t k, float temperature, float *out_logits, uint32_t *out_ids,
+                           int32_t *out_count) {
+    cuca_status st = pick_check(ctx, logits, ld, rows, vocab, dtype);
+    if (st != CUCA_OK || rows == 0) return st;
+    if (k <= 0 || k > CUCA_TOP_K_MAX)
+        return fail(ctx, CUCA_UNSUPPORTED, "top-k of %d: 1..%d candidates are selected on the device", k,
+                    CUCA_TOP_K_MAX);
+    if (!(temperature > 0.0f) || !std::isfinite(temperature))
+        return fail(ctx, CUCA_INVALID_ARG, "temperature must be positive (greedy is cuca_hip_argmax)");
+    if (!out_logits || !out_ids || !out_count) return fail(ctx, CUCA_INVALID_ARG, "null output");
+    PickArgs a{};
+    a.logits = logits;
+    a.out_logits = out_logits;
+    a.out_ids = out_ids;
+    a.out_count = out_count;
+    a.ld = ld;
+    a.rows = (int32_t)rows;
+    a.vocab = (int32_t)vocab;
+    a.k = k;
+    a.temperature = temperature;
+    return launch(ctx, dtype == CUCA_F16 ? cuca_topk_f16 : cuca_topk_f32, (unsigned)rows, 1024, 0, a);
+}
+
+// The rest of sample() after select_top_k (sampler.rs:166-185 and
+// :308-334), on the host: softmax of the candidates from the first (the
+// largest), probabilities of zero dropped, cut_top_p, one SplitMix64 draw.
+// With no candidate the draw still happens, over the greedy fallback.
+cuca_status cuca_hip_sample_candidates(const float *logits, const uint32_t *ids, int32_t count, float top_p,
+                                       uint32_t fallback, uint64_t *rng_state, uint32_t *out_id) {
+    if (!rng_state || !out_id || (count > 0 && (!logits || !ids)))
+        return fail(nullptr, CUCA_INVALID_ARG, "null pointer");
+    if (count < 0) return fail(nullptr, CUCA_INVALID_ARG, "negative candidate count");
+    std::vector<float> p;
+    std::vector<uint32_t> id;
+    p.reserve((size_t)count);
+    id.reserve((size_t)count);
+    if (count > 0) {
+        const float max = logits[0];
+        float sum = 0.0f;
+        std::vector<float> e((size_t)count);
+        for (int32_t i = 0; i < count; i++) {
+            e[(size_t)i] = std::exp(logits[i] - max); // the platform's expf, as Rust's f32::exp
+            sum += e[(size_t)i];
+        }
+        for (int32_t i = 0; i < count; i++) {
+            const float v = e[(size_t)i] / sum;
+            if (v > 0.0f) { p.push_back(v); id.push_back(ids[i]); }
+        }
+    }
+    if (p.empty()) {
+        p.push_back(1.0f);
+        id.push_back(fallback);
+    } else {
+        // cut_top_p (sampler.rs:288-300)
+        float cumulative = 0.0f;
+        for (size_t i = 0; i < p.size(); i++) {
+            cumulative += p[i];
+            if (cumulative >= top_p) { p.resize(i + 1); id.resize(i + 1); break; }
+        }
+    }
+    float total = 0.0f;
+    for (float v : p) total += v;
+    // SplitMix64::next_f32 (sampler.rs:21-35)
+    uint64_t z = (*rng_state += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    z ^= z >> 31;
+    const float target = (float)(z >> 40) / 16777216.0f * total;
+    float acc = 0.0f;
+    *out_id = id.back();
+    for (size_t i = 0; i < p.size(); i++) {
+        acc += p[i];
+        if (target < acc) { *out_id = id[i]; break; }
+    }
+    return CUCA_OK;
 }
 
 cuca_status cuca_hip_qmm(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type, int64_t n, int64_t k,

@@ -82,6 +82,12 @@ SIGNATURES = {
     "cuca_hip_moe_down": (_st, [_p, _p, _i64, _u32, _i64, _i64, _i32, _p, _i64, _p, _p, _i64, _p,
                                 _i64, _st]),
     "cuca_hip_moe_sum": (_st, [_p, _p, _i64, _i64, _p, _i32, _i64, _i64, _p, _i64, _st]),
+    "cuca_hip_lm_head": (_st, [_p, _p, _u32, _i64, _i64, _p, _i64, _i64, _i64, _f32, _f32, _f32, _p,
+                               _i64, _st]),
+    "cuca_hip_argmax": (_st, [_p, _p, _i64, _i64, _i64, _st, _p]),
+    "cuca_hip_top_k": (_st, [_p, _p, _i64, _i64, _i64, _st, _i32, _f32, _p, _p, _p]),
+    "cuca_hip_sample_candidates": (_st, [_p, _p, _i32, _f32, _u32, ctypes.POINTER(ctypes.c_uint64),
+                                         ctypes.POINTER(_u32)]),
     "cuca_hip_graph_begin": (_st, [_p]),
     "cuca_hip_graph_end": (_st, [_p, _pp]),
     "cuca_hip_graph_launch": (_st, [_p, _p]),
@@ -354,6 +360,19 @@ class Context:
                                            n_used, n_tokens, n_embd, out, out_ld, dtype))
 
 
+    def lm_head(self, w, ggml_type, vocab, n_embd, x, ldx, m, rows, logit_scale, logit_mult, softcap,
+                logits, logits_ld, dtype):
+        self.check(self.L.cuca_hip_lm_head(self.ptr, w, ggml_type, vocab, n_embd, x, ldx, m, rows,
+                                           logit_scale, logit_mult, softcap, logits, logits_ld, dtype))
+
+    def argmax(self, logits, ld, rows, vocab, dtype, ids):
+        self.check(self.L.cuca_hip_argmax(self.ptr, logits, ld, rows, vocab, dtype, ids))
+
+    def top_k(self, logits, ld, rows, vocab, dtype, k, temperature, out_logits, out_ids, out_count):
+        self.check(self.L.cuca_hip_top_k(self.ptr, logits, ld, rows, vocab, dtype, k, temperature,
+                                         out_logits, out_ids, out_count))
+
+
 class Graph:
     def __init__(self, ctx, ptr):
         self.ctx = ctx
@@ -390,6 +409,18 @@ def qweight_bytes(ggml_type, n, k):
     """Bytes of the packed layout of an [n, k] Q4_0 / Q8_0 weight (host)."""
     out = _sz(0)
     _check(lib().cuca_hip_qweight_bytes(ggml_type, n, k, ctypes.byref(out)), None)
+    return out.value
+
+
+def sample_candidates(logits, ids, top_p, fallback, rng_state):
+    """cuca_hip_sample_candidates (host): one row's top-k candidates (best
+    first) -> the drawn id; rng_state (a ctypes.c_uint64) advances."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    ii = np.ascontiguousarray(ids, dtype=np.uint32)
+    out = _u32(0)
+    _check(lib().cuca_hip_sample_candidates(lg.ctypes.data if lg.size else None,
+                                            ii.ctypes.data if ii.size else None, lg.size, top_p,
+                                            fallback, ctypes.byref(rng_state), ctypes.byref(out)), None)
     return out.value
 
 

@@ -31,6 +31,9 @@
  *   cuca_hip_qweight_pack  (the weight upload)            qmm.rs:1763-1783
  *   cuca_hip_moe_up/down/  expert_sum, CpuExpert          cpu.rs:373-419, 3599-3642
  *            _sum          (GPU moe_up/moe_down/moe_sum)  moe_kernel.rs:1163-1385
+ *   cuca_hip_lm_head       head + cap_logits              cpu.rs:2588-2617
+ *   cuca_hip_argmax        greedy                         sampler.rs:44-56
+ *   cuca_hip_top_k         select_top_k                   sampler.rs:254-286
  *
  * Conventions
  * - A context owns one device, one HIP stream (or borrows the caller's),
@@ -311,6 +314,46 @@ cuca_status cuca_hip_qmm(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type, i
 cuca_status cuca_hip_qmm_glu(cuca_hip_ctx *ctx, const void *gate, const void *up, uint32_t ggml_type,
                              int64_t ff, int64_t k, const void *x, int64_t ldx, int64_t m, cuca_act act,
                              float clamp, void *out, int64_t out_ld, cuca_dtype dtype);
+
+/* The end of a step (Transformer::finish / head / cap_logits,
+ * cpu.rs:2495-2617; the final norm is cuca_hip_add_rmsnorm).
+ * cuca_hip_lm_head: the LM head's quantized matmul (cuca_hip_qmm's bits)
+ * with cap_logits fused into its epilogue, in candle's affine form:
+ *   v = v * f32(1 / logit_scale) + 0   (logit_scale != 1)
+ *   v = v * logit_mult + 0             (logit_mult != 1)
+ *   v = tanh(v * f32(1 / softcap) + 0) * softcap + 0   (softcap > 0)
+ * Without a soft-cap the logits are the reference's bits; tanh is the
+ * device's (within 2 ulp).  rows: the first `rows` vocabulary entries
+ * (head_rows, cpu.rs:2597-2601). */
+cuca_status cuca_hip_lm_head(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type, int64_t vocab, int64_t n_embd,
+                             const void *x, int64_t ldx, int64_t m, int64_t rows, float logit_scale,
+                             float logit_mult, float softcap, void *logits, int64_t logits_ld, cuca_dtype dtype);
+
+/* Sampling's scans over the vocabulary on the device (sampler.rs), so a
+ * step reads back an id or k candidates per row instead of the logits.
+ * cuca_hip_argmax: greedy (sampler.rs:44-56) per row: the first maximum
+ *   (NaN never wins; a row without a value above -inf gives 0).
+ * cuca_hip_top_k: select_top_k (sampler.rs:254-286) per row: after
+ *   l / temperature, the k best finite logits, best first by
+ *   (f32 total order desc, id asc) -- those of a full sort -- into
+ *   out_logits / out_ids ([rows][k]; the scaled logits), their count
+ *   (min(k, finite logits)) into out_count[rows].  The host continues
+ *   warp_candidates / sample (softmax, top-p, the SplitMix64 draw) on them.
+ *   k is at most CUCA_TOP_K_MAX. */
+#define CUCA_TOP_K_MAX 1024
+
+/* Host-side: the rest of sample() after select_top_k (sampler.rs:166-185,
+ * 308-334) over one row's candidates from cuca_hip_top_k (best first):
+ * p = exp(l - l[0]) / sum, zeros dropped (none left: `fallback`, the row's
+ * greedy id), cut_top_p, then one SplitMix64 draw (*rng_state advances) --
+ * the reference's bits with the platform libm's expf.  No GPU is used. */
+cuca_status cuca_hip_sample_candidates(const float *logits, const uint32_t *ids, int32_t count, float top_p,
+                                       uint32_t fallback, uint64_t *rng_state, uint32_t *out_id);
+cuca_status cuca_hip_argmax(cuca_hip_ctx *ctx, const void *logits, int64_t ld, int64_t rows, int64_t vocab,
+                            cuca_dtype dtype, uint32_t *ids);
+cuca_status cuca_hip_top_k(cuca_hip_ctx *ctx, const void *logits, int64_t ld, int64_t rows, int64_t vocab,
+                           cuca_dtype dtype, int32_t k, float temperature, float *out_logits, uint32_t *out_ids,
+                           int32_t *out_count);
 
 /* Routed experts (MoE), the CPU engine's expert_sum (cpu.rs:3599-3642)
  * with CpuExpert::forward / add_picks (cpu.rs:373-419), split as the

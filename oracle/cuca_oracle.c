@@ -679,3 +679,186 @@ int oracle_qmm(const uint8_t *w, uint32_t ggml_type, int64_t n, int64_t k,
     free(xs);
     return 0;
 }
+
+/* ------------------------------------------------------------------ */
+/* next, rank 4: cap_logits and the sampler                            */
+/* ------------------------------------------------------------------ */
+
+void oracle_cap_logits(float *v, int64_t n, float logit_scale, float logit_mult, float softcap) {
+    /* candle affine: mul and add are f64 converted to the element type */
+    const float m1 = (float)(1.0 / (double)logit_scale);
+    const float m2 = logit_mult;
+    const float ci = softcap > 0.0f ? (float)(1.0 / (double)softcap) : 0.0f;
+    for (int64_t i = 0; i < n; i++) {
+        float x = v[i];
+        if (logit_scale != 1.0f) x = x * m1 + 0.0f;
+        if (logit_mult != 1.0f) x = x * m2 + 0.0f;
+        if (softcap > 0.0f) x = tanhf(x * ci + 0.0f) * softcap + 0.0f;
+        v[i] = x;
+    }
+}
+
+uint32_t oracle_greedy(const float *logits, int64_t n) {
+    int64_t best = 0;
+    float bv = -INFINITY;
+    for (int64_t i = 0; i < n; i++)
+        if (logits[i] > bv) { best = i; bv = logits[i]; }
+    return (uint32_t)best;
+}
+
+uint64_t oracle_splitmix64(uint64_t *state) {
+    *state += 0x9E3779B97F4A7C15ull;
+    uint64_t z = *state;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+float oracle_next_f32(uint64_t *state) {
+    return (float)(oracle_splitmix64(state) >> 40) / 16777216.0f;
+}
+
+typedef struct { float v; uint32_t id; } cand_t;
+
+/* f32::total_cmp as a signed 32-bit key (sampler.rs by_logit_desc). */
+static int32_t total_key(float v) {
+    int32_t b;
+    memcpy(&b, &v, 4);
+    return b ^ (int32_t)(((uint32_t)(b >> 31)) >> 1);
+}
+
+/* by_logit_desc: descending total order, equal logits by ascending id. */
+static int by_logit_desc(const void *pa, const void *pb) {
+    const cand_t *a = (const cand_t *)pa, *b = (const cand_t *)pb;
+    const int32_t ka = total_key(a->v), kb = total_key(b->v);
+    if (ka != kb) return ka > kb ? -1 : 1;
+    return a->id < b->id ? -1 : (a->id > b->id ? 1 : 0);
+}
+
+int64_t oracle_select_top_k(const float *logits, int64_t n, float temperature, int64_t k,
+                            float *out_logits, uint32_t *out_ids) {
+    cand_t *c = (cand_t *)malloc(sizeof(cand_t) * (size_t)(n > 0 ? n : 1));
+    int64_t m = 0;
+    for (int64_t i = 0; i < n; i++) {
+        const float l = logits[i] / temperature;
+        if (isfinite(l)) c[m++] = (cand_t){l, (uint32_t)i};
+    }
+    qsort(c, (size_t)m, sizeof(cand_t), by_logit_desc);
+    const int64_t keep = m < k ? m : k;
+    for (int64_t i = 0; i < keep; i++) {
+        out_logits[i] = c[i].v;
+        out_ids[i] = c[i].id;
+    }
+    free(c);
+    return keep;
+}
+
+/* cut_top_p (sampler.rs:288-300) */
+static int64_t cut_top_p(const cand_t *c, int64_t n, float top_p) {
+    float cumulative = 0.0f;
+    for (int64_t i = 0; i < n; i++) {
+        cumulative += c[i].v;
+        if (cumulative >= top_p) return i + 1;
+    }
+    return n;
+}
+
+/* softmax of candidates (logit -> exp(l - max)), then / sum, dropping zeros */
+static int64_t softmax_retain(cand_t *c, int64_t n, float max) {
+    float sum = 0.0f;
+    for (int64_t i = 0; i < n; i++) {
+        c[i].v = expf(c[i].v - max);
+        sum += c[i].v;
+    }
+    int64_t m = 0;
+    for (int64_t i = 0; i < n; i++) {
+        const float p = c[i].v / sum;
+        if (p > 0.0f) c[m++] = (cand_t){p, c[i].id};
+    }
+    return m;
+}
+
+uint32_t oracle_sample(float *logits, int64_t n, float temperature, int64_t top_k, float top_p,
+                       uint64_t *rng) {
+    if (temperature <= 0.0f || n <= 1) return oracle_greedy(logits, n);
+    cand_t *c = (cand_t *)malloc(sizeof(cand_t) * (size_t)(n > 0 ? n : 1));
+    int64_t m = 0;
+    if (top_k > 0 && top_k < n) {
+        /* select_top_k: scale in place, the k best finite of a full sort */
+        for (int64_t i = 0; i < n; i++) logits[i] /= temperature;
+        for (int64_t i = 0; i < n; i++)
+            if (isfinite(logits[i])) c[m++] = (cand_t){logits[i], (uint32_t)i};
+        qsort(c, (size_t)m, sizeof(cand_t), by_logit_desc);
+        if (m > top_k) m = top_k;
+        if (m == 0) {
+            c[0] = (cand_t){1.0f, oracle_greedy(logits, n)};
+            m = 1;
+        } else {
+            const float max = c[0].v;
+            m = softmax_retain(c, m, max);
+            if (m == 0) {
+                c[0] = (cand_t){1.0f, oracle_greedy(logits, n)};
+                m = 1;
+            } else {
+                m = cut_top_p(c, m, top_p);
+            }
+        }
+    } else {
+        /* the whole vocabulary (sampler.rs:191-252) */
+        float max = -INFINITY;
+        for (int64_t i = 0; i < n; i++) {
+            logits[i] /= temperature;
+            if (isfinite(logits[i])) {
+                max = fmaxf(max, logits[i]);
+                c[m++] = (cand_t){logits[i], (uint32_t)i};
+            }
+        }
+        if (m == 0) {
+            c[0] = (cand_t){1.0f, oracle_greedy(logits, n)};
+            m = 1;
+        } else if (top_p >= 1.0f) {
+            m = softmax_retain(c, m, max);
+            if (m == 0) {
+                c[0] = (cand_t){1.0f, oracle_greedy(logits, n)};
+                m = 1;
+            }
+        } else {
+            /* sum over every candidate in vocabulary order; the nucleus is
+             * the shortest sorted prefix, widened from 256 fourfold while its
+             * mass is below top_p (NUCLEUS_FIRST, :154) */
+            float sum = 0.0f;
+            for (int64_t i = 0; i < m; i++) sum += expf(c[i].v - max);
+            qsort(c, (size_t)m, sizeof(cand_t), by_logit_desc);
+            int64_t w = m < 256 ? m : 256;
+            for (;;) {
+                float mass = 0.0f;
+                for (int64_t i = 0; i < w; i++) mass += expf(c[i].v - max);
+                mass /= sum;
+                if (mass >= top_p || w >= m) break;
+                w = w * 4 < m ? w * 4 : m;
+            }
+            int64_t k2 = 0;
+            for (int64_t i = 0; i < w; i++) {
+                const float p = expf(c[i].v - max) / sum;
+                if (p > 0.0f) c[k2++] = (cand_t){p, c[i].id};
+            }
+            if (k2 == 0) {
+                c[0] = (cand_t){1.0f, oracle_greedy(logits, n)};
+                m = 1;
+            } else {
+                m = cut_top_p(c, k2, top_p);
+            }
+        }
+    }
+    float total = 0.0f;
+    for (int64_t i = 0; i < m; i++) total += c[i].v;
+    const float target = oracle_next_f32(rng) * total;
+    float acc = 0.0f;
+    uint32_t out = c[m - 1].id;
+    for (int64_t i = 0; i < m; i++) {
+        acc += c[i].v;
+        if (target < acc) { out = c[i].id; break; }
+    }
+    free(c);
+    return out;
+}

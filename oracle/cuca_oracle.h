@@ -159,6 +159,25 @@ int oracle_qmm(const uint8_t *w, uint32_t ggml_type, int64_t n, int64_t k,
                const void *x, int64_t ld, int64_t m, int64_t rows, float *out,
                int dtype, int nthreads);
 
+/* The end of a step: cap_logits and the sampler.
+ * oracle_cap_logits restates cap_logits (cpu.rs:2603-2617) with candle's
+ * affine (v * f32(mul) + f32(add)) and tanhf, in place.
+ * oracle_greedy restates greedy (sampler.rs:44-56).
+ * oracle_splitmix64 / oracle_next_f32 restate SplitMix64 (sampler.rs:18-35).
+ * oracle_select_top_k: select_top_k (sampler.rs:254-286) by its definition,
+ * the k best finite logits / temperature of a full sort by by_logit_desc
+ * (sampler.rs:58-60, its test sampler.rs:578-596); returns the count.
+ * oracle_sample restates sample (sampler.rs:308-334) with warp_candidates
+ * (:159-252) and cut_top_p (:288-300); logits are scaled in place. */
+void oracle_cap_logits(float *v, int64_t n, float logit_scale, float logit_mult, float softcap);
+uint32_t oracle_greedy(const float *logits, int64_t n);
+uint64_t oracle_splitmix64(uint64_t *state);
+float oracle_next_f32(uint64_t *state);
+int64_t oracle_select_top_k(const float *logits, int64_t n, float temperature, int64_t k,
+                            float *out_logits, uint32_t *out_ids);
+uint32_t oracle_sample(float *logits, int64_t n, float temperature, int64_t top_k, float top_p,
+                       uint64_t *rng);
+
 #ifdef __cplusplus
 }
 #endif

@@ -66,6 +66,17 @@ def lib():
         L.oracle_gather.restype = _int
         L.oracle_gather.argtypes = [_p, _i64, _i64, _i64, _p, _p, _i64, _int, _int, _int]
         L.oracle_q8_acts.argtypes = [_p, _i64, _i64, _i64, _int, _p, _p]
+        L.oracle_cap_logits.argtypes = [_p, _i64, _f32, _f32, _f32]
+        L.oracle_greedy.restype = ctypes.c_uint32
+        L.oracle_greedy.argtypes = [_p, _i64]
+        L.oracle_splitmix64.restype = ctypes.c_uint64
+        L.oracle_splitmix64.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+        L.oracle_next_f32.restype = _f32
+        L.oracle_next_f32.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
+        L.oracle_select_top_k.restype = _i64
+        L.oracle_select_top_k.argtypes = [_p, _i64, _f32, _i64, _p, _p]
+        L.oracle_sample.restype = ctypes.c_uint32
+        L.oracle_sample.argtypes = [_p, _i64, _f32, _i64, _f32, ctypes.POINTER(ctypes.c_uint64)]
         L.oracle_qmm.restype = _int
         L.oracle_qmm.argtypes = [_p, ctypes.c_uint32, _i64, _i64, _p, _i64, _i64, _i64, _p,
                                  _int, _int]
@@ -331,3 +342,44 @@ def expert_sum(x, experts, qtype, per_expert, act, clamp=0.0, threads=1):
             hidden[(e, i)] = h[i]
             out[tok] = (out[tok] + (y[i] * np.float32(w)).astype(np.float32)).astype(np.float32)
     return out, hidden
+
+
+def cap_logits(v, logit_scale=1.0, logit_mult=1.0, softcap=0.0):
+    """cap_logits (cpu.rs:2603-2617) on a copy of f32 logits."""
+    v = np.array(v, dtype=np.float32, copy=True, order="C")
+    lib().oracle_cap_logits(_ptr(v), v.size, logit_scale, logit_mult, softcap)
+    return v
+
+
+def greedy(logits):
+    """greedy (sampler.rs:44-56): the first maximum."""
+    v = np.ascontiguousarray(logits, dtype=np.float32)
+    return int(lib().oracle_greedy(_ptr(v), v.size))
+
+
+class SplitMix64:
+    """SplitMix64 (sampler.rs:18-35) over the oracle's C implementation."""
+
+    def __init__(self, seed):
+        self.state = ctypes.c_uint64(seed)
+
+    def next_u64(self):
+        return int(lib().oracle_splitmix64(ctypes.byref(self.state)))
+
+    def next_f32(self):
+        return float(lib().oracle_next_f32(ctypes.byref(self.state)))
+
+
+def select_top_k(logits, temperature, k):
+    """select_top_k (sampler.rs:254-286): ((logit / temperature) f32[c], ids u32[c])."""
+    v = np.ascontiguousarray(logits, dtype=np.float32)
+    out_l = np.empty(max(k, 1), np.float32)
+    out_i = np.empty(max(k, 1), np.uint32)
+    c = lib().oracle_select_top_k(_ptr(v), v.size, temperature, k, _ptr(out_l), _ptr(out_i))
+    return out_l[:c], out_i[:c]
+
+
+def sample(logits, temperature, top_k, top_p, rng):
+    """sample (sampler.rs:308-334) on a copy of the logits with a SplitMix64."""
+    v = np.array(logits, dtype=np.float32, copy=True, order="C")
+    return int(lib().oracle_sample(_ptr(v), v.size, temperature, top_k, top_p, ctypes.byref(rng.state)))

@@ -1,0 +1,149 @@
+"""The end of a step on the GPU (cuca_hip_lm_head, cuca_hip_argmax,
+cuca_hip_top_k) against the oracle, through the C ABI.
+
+Bars:
+- lm_head without a soft-cap: bit-exact (the qmm bits, then candle's affine
+  multiplies); with a soft-cap: |got - want| <= 2^-22 * cap + 1e-6 |want|
+  (tanh is the device's, within 2 ulp of the reference's libm tanhf);
+- argmax: the same id as greedy (first maximum), rows with ties, NaN and
+  -inf included;
+- top_k: the same candidates, bit for bit (the scaled logits) and id for
+  id, in the same order as select_top_k, for k from 1 to 1024, temperatures
+  other than 1, many equal logits, masked entries and rows with fewer finite
+  logits than k;
+- device top-k + the library's host finish draw the same ids as the
+  reference's sample on the whole row, for 64 seeds.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+from cuca_amd import hip, ops
+from cuca_amd import workloads as W
+from helpers import assert_bits_equal
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("scale,mult,cap", [(1.0, 1.0, 0.0), (3.0, 1.0, 0.0), (1.0, 0.25, 0.0),
+                                            (1.0, 1.0, 30.0), (2.0, 0.5, 15.0)])
+def test_lm_head(ctx, qtype, scale, mult, cap):
+    rng = np.random.default_rng(int(scale * 10 + mult * 100 + cap))
+    vocab, k, m = 1000, 512, 3
+    raw = W.quant_table(rng, vocab, k, qtype, (0.01, 0.05))
+    w = ops.QmmWeight.from_raw(ctx, W.GGML_ID[qtype], raw, vocab, k)
+    x = (rng.standard_normal((m, k)) * 4).astype(np.float32)
+    dx = ctx.array(x)
+    out = ctx.empty((m, vocab), np.float32)
+    ctx.lm_head(w.packed.ptr, W.GGML_ID[qtype], vocab, k, dx.ptr, k, m, vocab, scale, mult, cap,
+                out.ptr, vocab, hip.F32)
+    got = out.numpy()
+    want = O.cap_logits(O.qmm(raw, W.GGML_ID[qtype], vocab, k, x), scale, mult, cap)
+    if cap == 0.0:
+        assert_bits_equal(got, want, "lm head")
+    else:
+        assert np.all(np.abs(got - want) <= 2.0 ** -22 * cap + 1e-6 * np.abs(want))
+        assert np.all(np.abs(got) <= cap)
+
+
+def test_lm_head_rows_prefix_and_errors(ctx):
+    rng = np.random.default_rng(1)
+    raw = W.quant_table(rng, 300, 256, "q8_0", (0.01, 0.05))
+    w = ops.QmmWeight.from_raw(ctx, hip.GGML_Q8_0, raw, 300, 256)
+    x = rng.standard_normal((2, 256)).astype(np.float32)
+    dx = ctx.array(x)
+    out = ctx.empty((2, 100), np.float32)
+    ctx.lm_head(w.packed.ptr, hip.GGML_Q8_0, 300, 256, dx.ptr, 256, 2, 100, 1.0, 1.0, 0.0, out.ptr, 100,
+                hip.F32)
+    assert_bits_equal(out.numpy(), O.qmm(raw, hip.GGML_Q8_0, 300, 256, x, rows=100), "head_rows")
+    with pytest.raises(hip.CucaError, match="soft-cap"):
+        ctx.lm_head(w.packed.ptr, hip.GGML_Q8_0, 300, 256, dx.ptr, 256, 2, 100, 0.0, 1.0, 0.0, out.ptr,
+                    100, hip.F32)
+
+
+def logits_rows(rng, rows, vocab, kind):
+    if kind == "normal":
+        x = (rng.standard_normal((rows, vocab)) * 3).astype(np.float32)
+    elif kind == "ties":
+        x = np.floor(rng.uniform(0, 16, (rows, vocab))).astype(np.float32)
+    else:  # masked: mostly -inf, a few values, NaNs
+        x = np.full((rows, vocab), -np.inf, np.float32)
+        for r in range(rows):
+            idx = rng.choice(vocab, min(vocab - 3, 20 + r), replace=False)
+            x[r, idx] = rng.standard_normal(idx.size).astype(np.float32)
+            x[r, rng.choice(vocab, 3, replace=False)] = np.nan
+    return x
+
+
+@pytest.mark.parametrize("vocab", [7, 1000, 128256, 151936, 256000])
+@pytest.mark.parametrize("kind", ["normal", "ties", "masked"])
+def test_argmax(ctx, vocab, kind):
+    rng = np.random.default_rng(vocab + len(kind))
+    rows = 4
+    x = logits_rows(rng, rows, vocab, kind)
+    if kind == "normal":
+        x[1, :] = -np.inf            # no value above -inf: id 0
+        x[2, vocab // 2:] = x[2].max() + 1.0   # ties at the maximum: the first
+    ids = ctx.empty((rows,), np.uint32)
+    dx = ctx.array(x)
+    ctx.argmax(dx.ptr, vocab, rows, vocab, hip.F32, ids.ptr)
+    assert ids.numpy().tolist() == [O.greedy(x[r]) for r in range(rows)]
+    x16 = x.astype(np.float16)
+    dx16 = ctx.array(x16)
+    ctx.argmax(dx16.ptr, vocab, rows, vocab, hip.F16, ids.ptr)
+    assert ids.numpy().tolist() == [O.greedy(x16[r].astype(np.float32)) for r in range(rows)]
+
+
+@pytest.mark.parametrize("vocab,k", [(1000, 1), (1000, 2), (1000, 40), (128256, 40), (151936, 333),
+                                     (256000, 1024), (5000, 1024), (100, 1000)])
+@pytest.mark.parametrize("kind", ["normal", "ties", "masked"])
+@pytest.mark.parametrize("temperature", [1.0, 0.7])
+def test_top_k(ctx, vocab, k, kind, temperature):
+    rng = np.random.default_rng(vocab + k + len(kind))
+    rows = 3
+    x = logits_rows(rng, rows, vocab, kind)
+    dx = ctx.array(x)
+    ol, oi, oc = ctx.empty((rows, k), np.float32), ctx.empty((rows, k), np.uint32), ctx.empty((rows,), np.int32)
+    ctx.top_k(dx.ptr, vocab, rows, vocab, hip.F32, k, temperature, ol.ptr, oi.ptr, oc.ptr)
+    gl, gi, gc = ol.numpy(), oi.numpy(), oc.numpy()
+    for r in range(rows):
+        wl, wi = O.select_top_k(x[r], temperature, k)
+        assert gc[r] == wl.size, (r, gc[r], wl.size)
+        assert gi[r, :gc[r]].tolist() == wi.tolist()
+        assert_bits_equal(gl[r, :gc[r]], wl, f"top-k logits row {r}")
+
+
+def test_device_top_k_then_host_finish_is_the_reference_sample(ctx):
+    rng = np.random.default_rng(12)
+    vocab, rows = 128256, 2
+    x = (rng.standard_normal((rows, vocab)) * 2).astype(np.float32)
+    dx = ctx.array(x)
+    for temperature, top_k, top_p in [(0.8, 40, 0.95), (1.0, 5, 1.0), (1.2, 100, 0.5)]:
+        ol, oi, oc = ctx.empty((rows, top_k), np.float32), ctx.empty((rows, top_k), np.uint32), \
+            ctx.empty((rows,), np.int32)
+        ctx.top_k(dx.ptr, vocab, rows, vocab, hip.F32, top_k, temperature, ol.ptr, oi.ptr, oc.ptr)
+        ids = ctx.empty((rows,), np.uint32)
+        ctx.argmax(dx.ptr, vocab, rows, vocab, hip.F32, ids.ptr)
+        gl, gi, gc, fb = ol.numpy(), oi.numpy(), oc.numpy(), ids.numpy()
+        for r in range(rows):
+            for seed in range(64):
+                want = O.sample(x[r], temperature, top_k, top_p, O.SplitMix64(seed))
+                got = hip.sample_candidates(gl[r, :gc[r]], gi[r, :gc[r]], top_p, int(fb[r]),
+                                            ctypes.c_uint64(seed))
+                assert got == want, (temperature, top_k, top_p, r, seed)
+
+
+def test_pick_errors(ctx):
+    x = ctx.array(np.zeros((1, 10), np.float32))
+    o = ctx.empty((1, 2000), np.float32)
+    i = ctx.empty((1, 2000), np.uint32)
+    c = ctx.empty((1,), np.int32)
+    with pytest.raises(hip.CucaError, match="1..1024"):
+        ctx.top_k(x.ptr, 10, 1, 10, hip.F32, 2000, 1.0, o.ptr, i.ptr, c.ptr)
+    with pytest.raises(hip.CucaError, match="temperature"):
+        ctx.top_k(x.ptr, 10, 1, 10, hip.F32, 5, 0.0, o.ptr, i.ptr, c.ptr)
+    with pytest.raises(hip.CucaError, match="logits shape"):
+        ctx.argmax(x.ptr, 5, 1, 10, hip.F32, i.ptr)
