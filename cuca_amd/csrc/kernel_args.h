@@ -159,6 +159,31 @@ typedef struct {
     int32_t pad2_;
 } QmmArgs;
 
+/* Activation quantisation for the decode GEMV (Acts::new, qmm.rs:1272-1343):
+ * x [m][ldx] -> quants [m][q_ld] int8 (element order) and scales [m][nb]. */
+typedef struct {
+    const void *x;
+    int8_t *quants;
+    float *scales;
+    int64_t ldx, q_ld;
+    int32_t m, nb;
+} Q8ActsArgs;
+
+/* The decode GEMV (qmv.hip) on quantised activations, tiles of MT <= 2
+ * activation rows held in LDS for the whole row length; tasks of 4 weight
+ * rows per wave.  Epilogue as QmmArgs (GLU, cap). */
+typedef struct {
+    const uint8_t *w, *w_up;    /* packed weights (gate/up for GLU)          */
+    const int8_t *quants;       /* [m][q_ld]                                 */
+    const float *scales;        /* [m][nb]                                   */
+    void *out;                  /* [m][out_ld]                               */
+    int64_t q_ld, out_ld, row_bytes;
+    int32_t rows, m, nb, ng, nbp, ntask;
+    float clamp;
+    int32_t cap_flags;
+    float mul1, mul2, softcap_inv, softcap;
+} QmvArgs;
+
 /* Greedy argmax and top-k over logits rows (sampler.rs greedy and
  * select_top_k).  top-k: keys are logit / temperature; the k best finite
  * ones in (logit desc, id asc) order go to out_logits / out_ids, their

@@ -12,3 +12,4 @@
 #include "attn.hip"
 #include "qmm.hip"
 #include "pick.hip"
+#include "qmv.hip"

@@ -61,6 +61,10 @@ const char *const kKernelNames[] = {
 
 thread_local std::string g_thread_error;
 
+// The context's scratch for quantised activations: two rows of up to
+// 16384 values (quants, then f32 block scales), rounded up.
+constexpr size_t kQScratchBytes = 64 << 10;
+
 }  // namespace
 
 struct cuca_hip_ctx {
@@ -76,6 +80,11 @@ struct cuca_hip_ctx {
     int64_t last_kv_blocks = 0;   // the pool size of the last K/V store (for messages)
     int64_t last_table_rows = 0;
     int64_t last_moe_tokens = 0;  // the activation rows of the last MoE up call
+    // device scratch for the quantised activations of a decode GEMV that
+    // cuca_hip_qmm / _qmm_glu / _lm_head route through cuca_q8_acts + qmv
+    // (allocated with the context: ops never allocate)
+    void *qscratch = nullptr;
+    int cu_count = 256;
     std::string error;
     // per-kernel timing (cuca_hip_profile_start/stop)
     struct ProfRec { int kernel; hipEvent_t start, stop; };
@@ -194,6 +203,10 @@ cuca_status cuca_hip_ctx_create(int device, cuca_hip_ctx **out) {
             }
         }
         if (st != CUCA_OK) break;
+        ctx->cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+        if ((e = hipMalloc(&ctx->qscratch, kQScratchBytes)) != hipSuccess) {
+            st = hip_fail(ctx, e, "hipMalloc(activation scratch)"); break;
+        }
         if ((e = hipMalloc(&ctx->status, CUCA_STATUS_WORDS * sizeof(unsigned long long))) != hipSuccess) {
             st = hip_fail(ctx, e, "hipMalloc(status)"); break;
         }
@@ -228,6 +241,7 @@ void cuca_hip_ctx_destroy(cuca_hip_ctx *ctx) {
         (void)hipEventDestroy(r.stop);
     }
     if (ctx->status) (void)hipFree(ctx->status);
+    if (ctx->qscratch) (void)hipFree(ctx->qscratch);
     if (ctx->module) (void)hipModuleUnload(ctx->module);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
@@ -887,6 +901,44 @@ struct LogitCap {
     float logit_scale = 1.0f, logit_mult = 1.0f, softcap = 0.0f;
 };
 
+// LDS of a qmv workgroup (qmv.hip QMV_LDS_BYTES) for MT rows, nbp padded
+// blocks of groups of G; the kernel is used when it fits in 64 KiB.
+static size_t qmv_lds(int64_t mt, int64_t nbp, int g) {
+    return (size_t)(mt * 16 * (nbp + 2) * 8 + mt * nbp * 4 + 4 * mt * 2 * 4 * g * 4);
+}
+static bool qmv_fits(int64_t m, int64_t nbp, int g) {
+    return m >= 1 && m <= 2 && qmv_lds(m, nbp, g) <= (64u << 10);
+}
+// qmm routes one or two rows to the decode GEMV only where its persistent
+// waves (four workgroups of four per CU) each get at least two four-row
+// tasks, so the per-workgroup expansion of the quants is shared: the LM
+// head.  Below that the one-pass kernel is faster (it has no separate
+// quantisation launch and fills the chip with more, shorter waves).
+static bool qmv_wins(const cuca_hip_ctx *ctx, int64_t rows) {
+    return (rows + 3) / 4 >= 2 * 16 * (int64_t)ctx->cu_count;
+}
+
+static cuca_status q8_acts_launch(cuca_hip_ctx *ctx, const void *x, int64_t ldx, int64_t m, int64_t k,
+                                  cuca_dtype dtype, int8_t *quants, int64_t q_ld, float *scales) {
+    Q8ActsArgs a{};
+    a.x = x;
+    a.quants = quants;
+    a.scales = scales;
+    a.ldx = ldx;
+    a.q_ld = q_ld;
+    a.m = (int32_t)m;
+    a.nb = (int32_t)(k / 32);
+    return launch(ctx, dtype == CUCA_F16 ? cuca_q8_acts_f16 : cuca_q8_acts_f32, div_up(m * (k / 32), CUCA_BLOCK_THREADS),
+                  CUCA_BLOCK_THREADS, 0, a);
+}
+
+// The decode GEMV on quantised activations (m <= 2, qmv_fits checked).
+// glu: 0 plain, 1 SiLU, 2 GELU-tanh.
+static cuca_status qmv_launch(cuca_hip_ctx *ctx, const void *w, const void *w_up, uint32_t ggml_type, int64_t n,
+                              int64_t k, const int8_t *quants, int64_t q_ld, const float *scales, int64_t m,
+                              int64_t rows, int glu, float clamp, void *out, int64_t out_ld, cuca_dtype dtype,
+                              const LogitCap &cap);
+
 // glu: 0 plain, 1 SiLU, 2 GELU-tanh
 static cuca_status qmm_common(cuca_hip_ctx *ctx, const void *w, const void *w_up, uint32_t ggml_type,
                               int64_t n, int64_t k, const void *x, int64_t ldx, int64_t m, int64_t rows,
@@ -916,6 +968,14 @@ static cuca_status qmm_common(cuca_hip_ctx *ctx, const void *w, const void *w_up
     if (!al16(x) || ((size_t)ldx * es) % 16 != 0)
         return fail(ctx, CUCA_INVALID_ARG, "qmm: activation rows must start 16-byte aligned");
     const int64_t nb = k / 32, ng = (nb + g - 1) / g;
+    // one or two rows of a tall matrix whose tile fits the LDS: quantise
+    // once into the context's scratch, then the decode GEMV
+    if (m <= 2 && qmv_wins(ctx, rows) && qmv_fits(m, ng * g, g) && (size_t)m * (size_t)k + (size_t)m * (size_t)nb * 4 + 16 <= kQScratchBytes) {
+        int8_t *q = static_cast<int8_t *>(ctx->qscratch);
+        float *sc = reinterpret_cast<float *>(q + ((size_t)m * (size_t)k + 15) / 16 * 16);
+        if ((st = q8_acts_launch(ctx, x, ldx, m, k, dtype, q, k, sc)) != CUCA_OK) return st;
+        return qmv_launch(ctx, w, w_up, ggml_type, n, k, q, k, sc, m, rows, glu, clamp, out, out_ld, dtype, cap);
+    }
     const int mt = m == 1 ? 1 : m == 2 ? 2 : 4;
     const int mi = mt == 1 ? 0 : mt == 2 ? 1 : 2;
     const int64_t ntile = (m + mt - 1) / mt;
@@ -1093,6 +1153,113 @@ cuca_status cuca_hip_qmm_glu(cuca_hip_ctx *ctx, const void *gate, const void *up
     if (act != CUCA_ACT_SILU && act != CUCA_ACT_GELU_TANH)
         return fail(ctx, CUCA_INVALID_ARG, "bad activation %d", (int)act);
     return qmm_common(ctx, gate, up, ggml_type, ff, k, x, ldx, m, ff, act == CUCA_ACT_SILU ? 1 : 2, clamp,
+                      out, out_ld, dtype);
+}
+
+static cuca_status qmv_launch(cuca_hip_ctx *ctx, const void *w, const void *w_up, uint32_t ggml_type, int64_t n,
+                              int64_t k, const int8_t *quants, int64_t q_ld, const float *scales, int64_t m,
+                              int64_t rows, int glu, float clamp, void *out, int64_t out_ld, cuca_dtype dtype,
+                              const LogitCap &cap) {
+    int g = 0, gb = 0;
+    qfmt(ggml_type, &g, &gb);
+    const int64_t nb = k / 32, ng = (nb + g - 1) / g, nbp = ng * g;
+    const int64_t ntask = (rows + 3) / 4;
+    int64_t grid = (ntask + 3) / 4;
+    const int64_t cap_wg = (int64_t)ctx->cu_count * 4; // persistent beyond four workgroups per CU
+    if (grid > cap_wg) grid = cap_wg;
+    // [dtype][format][plain, silu, gelu][rows 1, 2]
+    static const Kernel table_k[2][2][3][2] = {
+        {{{cuca_qmv_q4_0_m1_f32, cuca_qmv_q4_0_m2_f32},
+          {cuca_qmv_glu_q4_0_silu_m1_f32, cuca_qmv_glu_q4_0_silu_m2_f32},
+          {cuca_qmv_glu_q4_0_gelu_m1_f32, cuca_qmv_glu_q4_0_gelu_m2_f32}},
+         {{cuca_qmv_q8_0_m1_f32, cuca_qmv_q8_0_m2_f32},
+          {cuca_qmv_glu_q8_0_silu_m1_f32, cuca_qmv_glu_q8_0_silu_m2_f32},
+          {cuca_qmv_glu_q8_0_gelu_m1_f32, cuca_qmv_glu_q8_0_gelu_m2_f32}}},
+        {{{cuca_qmv_q4_0_m1_f16, cuca_qmv_q4_0_m2_f16},
+          {cuca_qmv_glu_q4_0_silu_m1_f16, cuca_qmv_glu_q4_0_silu_m2_f16},
+          {cuca_qmv_glu_q4_0_gelu_m1_f16, cuca_qmv_glu_q4_0_gelu_m2_f16}},
+         {{cuca_qmv_q8_0_m1_f16, cuca_qmv_q8_0_m2_f16},
+          {cuca_qmv_glu_q8_0_silu_m1_f16, cuca_qmv_glu_q8_0_silu_m2_f16},
+          {cuca_qmv_glu_q8_0_gelu_m1_f16, cuca_qmv_glu_q8_0_gelu_m2_f16}}}};
+    const Kernel kk = table_k[dtype == CUCA_F16][ggml_type == CUCA_GGML_Q8_0][glu][m == 2];
+    QmvArgs a{};
+    a.w = static_cast<const uint8_t *>(w);
+    a.w_up = static_cast<const uint8_t *>(w_up);
+    a.quants = quants;
+    a.scales = scales;
+    a.out = out;
+    a.q_ld = q_ld;
+    a.out_ld = out_ld;
+    a.row_bytes = ng * gb;
+    a.rows = (int32_t)rows;
+    a.m = (int32_t)m;
+    a.nb = (int32_t)nb;
+    a.ng = (int32_t)ng;
+    a.nbp = (int32_t)nbp;
+    a.ntask = (int32_t)ntask;
+    a.clamp = clamp > 0.0f ? clamp : 0.0f;
+    if (cap.logit_scale != 1.0f) { a.cap_flags |= 1; a.mul1 = (float)(1.0 / (double)cap.logit_scale); }
+    if (cap.logit_mult != 1.0f) { a.cap_flags |= 2; a.mul2 = cap.logit_mult; }
+    if (cap.softcap > 0.0f) {
+        a.cap_flags |= 4;
+        a.softcap_inv = (float)(1.0 / (double)cap.softcap);
+        a.softcap = cap.softcap;
+    }
+    return launch(ctx, kk, (unsigned)grid, CUCA_BLOCK_THREADS, (unsigned)qmv_lds(m, nbp, g), a);
+}
+
+cuca_status cuca_hip_q8_acts(cuca_hip_ctx *ctx, const void *x, int64_t ldx, int64_t m, int64_t k, cuca_dtype dtype,
+                             int8_t *quants, float *scales) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    if (!dtype_ok(dtype)) return fail(ctx, CUCA_INVALID_ARG, "bad dtype %d", (int)dtype);
+    if (k <= 0 || k % 32 != 0 || k / 32 > 0x7fffffffll)
+        return fail(ctx, CUCA_INVALID_ARG, "q8 acts: row length %lld is not a whole number of blocks", (long long)k);
+    if (m < 0 || m * (k / 32) > 0x7fffffffll) return fail(ctx, CUCA_INVALID_ARG, "q8 acts: bad row count %lld", (long long)m);
+    if (ldx < k) return fail(ctx, CUCA_INVALID_ARG, "q8 acts: row stride %lld shorter than %lld", (long long)ldx, (long long)k);
+    if (m == 0) return CUCA_OK;
+    if (!x || !quants || !scales) return fail(ctx, CUCA_INVALID_ARG, "null pointer");
+    if (!al16(x) || ((size_t)ldx * esize(dtype)) % 16 != 0 || !al16(quants) || k % 16 != 0)
+        return fail(ctx, CUCA_INVALID_ARG, "q8 acts: rows must start 16-byte aligned");
+    return q8_acts_launch(ctx, x, ldx, m, k, dtype, quants, k, scales);
+}
+
+static cuca_status qmv_common(cuca_hip_ctx *ctx, const void *w, const void *w_up, uint32_t ggml_type, int64_t n,
+                              int64_t k, const int8_t *quants, const float *scales, int64_t m, int64_t rows, int glu,
+                              float clamp, void *out, int64_t out_ld, cuca_dtype dtype) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    int g = 0, gb = 0;
+    if ((st = qweight_shape(ctx, ggml_type, n, k, &g, &gb)) != CUCA_OK) return st;
+    if (!dtype_ok(dtype)) return fail(ctx, CUCA_INVALID_ARG, "bad dtype %d", (int)dtype);
+    if (rows <= 0 || rows > n)
+        return fail(ctx, CUCA_INVALID_ARG, "qmm: %lld weight rows of %lld", (long long)rows, (long long)n);
+    if (out_ld < rows) return fail(ctx, CUCA_INVALID_ARG, "qmm: output row stride %lld shorter than %lld",
+                                   (long long)out_ld, (long long)rows);
+    if (!(clamp == clamp)) return fail(ctx, CUCA_INVALID_ARG, "clamp is NaN");
+    const int64_t ng = (k / 32 + g - 1) / g;
+    if (m == 0) return CUCA_OK;
+    if (!qmv_fits(m, ng * g, g))
+        return fail(ctx, CUCA_UNSUPPORTED, "qmv: %lld rows of %lld values do not fit the decode GEMV (1 or 2 rows; "
+                    "cuca_hip_qmm takes any)", (long long)m, (long long)k);
+    if (!w || !quants || !scales || !out || (glu && !w_up)) return fail(ctx, CUCA_INVALID_ARG, "null pointer");
+    if (!al16(w) || (w_up && !al16(w_up))) return fail(ctx, CUCA_INVALID_ARG, "packed weights must be 16-byte aligned");
+    return qmv_launch(ctx, w, w_up, ggml_type, n, k, quants, k, scales, m, rows, glu, clamp, out, out_ld, dtype,
+                      LogitCap());
+}
+
+cuca_status cuca_hip_qmv(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type, int64_t n, int64_t k,
+                         const int8_t *quants, const float *scales, int64_t m, int64_t rows, void *out, int64_t out_ld,
+                         cuca_dtype dtype) {
+    return qmv_common(ctx, w, nullptr, ggml_type, n, k, quants, scales, m, rows, 0, 0.0f, out, out_ld, dtype);
+}
+
+cuca_status cuca_hip_qmv_glu(cuca_hip_ctx *ctx, const void *gate, const void *up, uint32_t ggml_type, int64_t ff,
+                             int64_t k, const int8_t *quants, const float *scales, int64_t m, cuca_act act, float clamp,
+                             void *out, int64_t out_ld, cuca_dtype dtype) {
+    if (act != CUCA_ACT_SILU && act != CUCA_ACT_GELU_TANH)
+        return fail(ctx, CUCA_INVALID_ARG, "bad activation %d", (int)act);
+    return qmv_common(ctx, gate, up, ggml_type, ff, k, quants, scales, m, ff, act == CUCA_ACT_SILU ? 1 : 2, clamp,
                       out, out_ld, dtype);
 }
 

@@ -82,6 +82,9 @@ SIGNATURES = {
     "cuca_hip_moe_down": (_st, [_p, _p, _i64, _u32, _i64, _i64, _i32, _p, _i64, _p, _p, _i64, _p,
                                 _i64, _st]),
     "cuca_hip_moe_sum": (_st, [_p, _p, _i64, _i64, _p, _i32, _i64, _i64, _p, _i64, _st]),
+    "cuca_hip_q8_acts": (_st, [_p, _p, _i64, _i64, _i64, _st, _p, _p]),
+    "cuca_hip_qmv": (_st, [_p, _p, _u32, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _st]),
+    "cuca_hip_qmv_glu": (_st, [_p, _p, _p, _u32, _i64, _i64, _p, _p, _i64, _st, _f32, _p, _i64, _st]),
     "cuca_hip_lm_head": (_st, [_p, _p, _u32, _i64, _i64, _p, _i64, _i64, _i64, _f32, _f32, _f32, _p,
                                _i64, _st]),
     "cuca_hip_argmax": (_st, [_p, _p, _i64, _i64, _i64, _st, _p]),
@@ -359,6 +362,17 @@ class Context:
         self.check(self.L.cuca_hip_moe_sum(self.ptr, scratch, scratch_ld, max_pairs, token_pairs,
                                            n_used, n_tokens, n_embd, out, out_ld, dtype))
 
+
+    def q8_acts(self, x, ldx, m, k, dtype, quants, scales):
+        self.check(self.L.cuca_hip_q8_acts(self.ptr, x, ldx, m, k, dtype, quants, scales))
+
+    def qmv(self, w, ggml_type, n, k, quants, scales, m, rows, out, out_ld, dtype):
+        self.check(self.L.cuca_hip_qmv(self.ptr, w, ggml_type, n, k, quants, scales, m, rows, out, out_ld,
+                                       dtype))
+
+    def qmv_glu(self, gate, up, ggml_type, ff, k, quants, scales, m, act, clamp, out, out_ld, dtype):
+        self.check(self.L.cuca_hip_qmv_glu(self.ptr, gate, up, ggml_type, ff, k, quants, scales, m, act,
+                                           clamp, out, out_ld, dtype))
 
     def lm_head(self, w, ggml_type, vocab, n_embd, x, ldx, m, rows, logit_scale, logit_mult, softcap,
                 logits, logits_ld, dtype):

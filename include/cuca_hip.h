@@ -355,6 +355,25 @@ cuca_status cuca_hip_top_k(cuca_hip_ctx *ctx, const void *logits, int64_t ld, in
                            cuca_dtype dtype, int32_t k, float temperature, float *out_logits, uint32_t *out_ids,
                            int32_t *out_count);
 
+/* The decode GEMV in two steps, for callers that quantise an activation
+ * once for several matrices (Q, K and V of one row; gate and up):
+ * cuca_hip_q8_acts: Acts::new (qmm.rs:1272-1343) on the device: x [m][ldx]
+ *   -> quants int8 [m][k] (element order) and scales f32 [m][k/32] (the
+ *   f16-rounded block scales); quants 16-byte aligned, k a multiple of 32.
+ * cuca_hip_qmv / cuca_hip_qmv_glu: cuca_hip_qmm / _qmm_glu on those, the
+ *   same bits, for m = 1 or 2 rows whose row length fits the kernel (up to
+ *   about 15000 values for one row; CUCA_UNSUPPORTED otherwise).
+ * cuca_hip_qmm, _qmm_glu and _lm_head take this path by themselves for one
+ * or two rows, quantising into a small scratch the context owns. */
+cuca_status cuca_hip_q8_acts(cuca_hip_ctx *ctx, const void *x, int64_t ldx, int64_t m, int64_t k, cuca_dtype dtype,
+                             int8_t *quants, float *scales);
+cuca_status cuca_hip_qmv(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type, int64_t n, int64_t k,
+                         const int8_t *quants, const float *scales, int64_t m, int64_t rows, void *out, int64_t out_ld,
+                         cuca_dtype dtype);
+cuca_status cuca_hip_qmv_glu(cuca_hip_ctx *ctx, const void *gate, const void *up, uint32_t ggml_type, int64_t ff,
+                             int64_t k, const int8_t *quants, const float *scales, int64_t m, cuca_act act, float clamp,
+                             void *out, int64_t out_ld, cuca_dtype dtype);
+
 /* Routed experts (MoE), the CPU engine's expert_sum (cpu.rs:3599-3642)
  * with CpuExpert::forward / add_picks (cpu.rs:373-419), split as the
  * reference GPU engine splits it (MoeKernels::moe_up / moe_down / moe_sum,

@@ -202,3 +202,91 @@ def test_host_rejects_bad_arguments(ctx):
     assert ops.QmmWeight.from_raw(ctx, hip.GGML_Q4_0, raw, 8, 250) is None
     # m = 0 is a no-op
     ctx.qmm(w.packed.ptr, hip.GGML_Q4_0, 8, 256, x.ptr, 256, 0, 8, out.ptr, 8, hip.F32)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+@pytest.mark.parametrize("m,k", [(1, 32), (2, 4096), (5, 14336), (3, 96)])
+def test_q8_acts_is_the_reference_quantisation(ctx, dtype, m, k):
+    """cuca_hip_q8_acts = Acts::new (quants and f16-rounded scales, bit for bit)."""
+    rng = np.random.default_rng(m * k)
+    x = awkward(rng, m, k, huge=1e30 if dtype == "f32" else 1e4).astype(NP[dtype])
+    dx = ctx.array(x)
+    q, s = ctx.empty((m, k), np.int8), ctx.empty((m, k // 32), np.float32)
+    ctx.q8_acts(dx.ptr, k, m, k, hip.dtype_code(NP[dtype]), q.ptr, s.ptr)
+    wq, ws = O.q8_acts(x)
+    assert np.array_equal(q.numpy(), wq)
+    assert_bits_equal(s.numpy(), ws, "act scales")
+
+
+@pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("m", [1, 2])
+def test_qmv_two_steps(ctx, qtype, m):
+    """q8_acts once, then qmv (plain) and qmv_glu on the same quants."""
+    rng = np.random.default_rng(m + 7)
+    n, k = 300, 4096
+    graw, gw = weight(ctx, rng, qtype, n, k, (0.01, 0.05))
+    uraw, uw = weight(ctx, rng, qtype, n, k, (0.01, 0.05))
+    x = awkward(rng, m, k, 1.0, huge=100.0)
+    dx = ctx.array(x)
+    q, s = ctx.empty((m, k), np.int8), ctx.empty((m, k // 32), np.float32)
+    ctx.q8_acts(dx.ptr, k, m, k, hip.F32, q.ptr, s.ptr)
+    out = ctx.empty((m, n), np.float32)
+    ctx.qmv(gw.packed.ptr, QT[qtype], n, k, q.ptr, s.ptr, m, n, out.ptr, n, hip.F32)
+    g = O.qmm(graw, QT[qtype], n, k, x)
+    assert_bits_equal(out.numpy(), g, "qmv")
+    ctx.qmv_glu(gw.packed.ptr, uw.packed.ptr, QT[qtype], n, k, q.ptr, s.ptr, m, hip.ACT_SILU, 0.0, out.ptr, n,
+                hip.F32)
+    u = O.qmm(uraw, QT[qtype], n, k, x)
+    assert_close(out.numpy(), O.glu(g, u, hip.ACT_SILU), what="qmv glu")
+    with pytest.raises(hip.CucaError, match="decode GEMV"):
+        ctx.qmv(gw.packed.ptr, QT[qtype], n, k, q.ptr, s.ptr, 3, n, out.ptr, n, hip.F32)
+
+
+@pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("m", [1, 2])
+def test_rows_too_long_for_the_decode_gemv_take_the_chunked_kernel(ctx, qtype, m):
+    rng = np.random.default_rng(m + 11)
+    n, k = 40, 16384 if m == 1 else 14336
+    raw, w = weight(ctx, rng, qtype, n, k)
+    x = awkward(rng, m, k)
+    assert_bits_equal(w.forward(ctx.array(x)).numpy(), want_out(raw, qtype, n, k, x, n, "f32"), f"k={k} m={m}")
+
+
+@pytest.mark.parametrize("m", [1, 2])
+def test_lm_head_on_the_decode_gemv(ctx, m):
+    """A vocabulary tall enough (40000 rows) for qmm to route one or two rows
+    to the decode GEMV, each wave running several tasks."""
+    rng = np.random.default_rng(m)
+    vocab, k = 40000, 512
+    raw, w = weight(ctx, rng, "q8_0", vocab, k, (0.01, 0.05))
+    x = (rng.standard_normal((m, k)) * 4).astype(np.float32)
+    dx = ctx.array(x)
+    out = ctx.empty((m, vocab), np.float32)
+    for scale, mult, cap in [(1.0, 1.0, 0.0), (3.0, 0.5, 0.0), (1.0, 1.0, 30.0)]:
+        ctx.lm_head(w.packed.ptr, hip.GGML_Q8_0, vocab, k, dx.ptr, k, m, vocab, scale, mult, cap, out.ptr,
+                    vocab, hip.F32)
+        want = O.cap_logits(O.qmm(raw, hip.GGML_Q8_0, vocab, k, x, threads=8), scale, mult, cap)
+        if cap == 0.0:
+            assert_bits_equal(out.numpy(), want, "lm head")
+        else:
+            assert np.all(np.abs(out.numpy() - want) <= 2.0 ** -22 * cap + 1e-6 * np.abs(want))
+
+
+@pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("glu", [False, True])
+def test_decode_gemv_waves_that_run_several_tasks(ctx, qtype, glu):
+    """40000 rows: more four-row tasks than the persistent grid has waves, so
+    a wave runs several tasks one after the other (the LM head's case)."""
+    rng = np.random.default_rng(40000 + glu)
+    n, k = 40000, 256
+    raw, w = weight(ctx, rng, qtype, n, k)
+    x = awkward(rng, 1, k, 1.0, huge=100.0)
+    dx = ctx.array(x)
+    if glu:
+        uraw, uw = weight(ctx, rng, qtype, n, k)
+        got = ops.QmmWeight.glu(w, uw, dx, ops.Glu(hip.ACT_SILU)).numpy()
+        g = O.qmm(raw, QT[qtype], n, k, x, threads=8)
+        u = O.qmm(uraw, QT[qtype], n, k, x, threads=8)
+        assert_close(got, O.glu(g, u, hip.ACT_SILU), what="several tasks, glu")
+    else:
+        assert_bits_equal(w.forward(dx).numpy(), want_out(raw, qtype, n, k, x, n, "f32"), "several tasks")
