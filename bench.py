@@ -539,6 +539,198 @@ def decode_us_per_layer(ctx, torch, n, replays=50, ctx_len=None):
     return graph_ms * 1000.0 / dl.layers, eager_ms * 1000.0 / dl.layers
 
 
+def kernel_calls(ctx, call, reps, warmup=5):
+    """Run call(i) `reps` times with per-kernel timestamps: returns (median
+    of the per-call kernel-time sums in ms, [(kernel, median ms)] of one
+    call's launches)."""
+    import numpy as np
+    for i in range(warmup):
+        call(i)
+    ctx.sync()
+    ctx.profile_start(8 * reps)
+    for i in range(reps):
+        call(i)
+    recs = ctx.profile_stop()
+    ctx.check_device()
+    per = len(recs) // reps
+    calls = [recs[i * per:(i + 1) * per] for i in range(reps)]
+    parts = [(k, float(np.median([c[j][1] for c in calls]))) for j, (k, _) in enumerate(calls[0])]
+    return float(np.median([sum(t for _, t in c) for c in calls])), parts
+
+
+# Llama-3-8B's decode matmuls (n rows of weights, k inputs): the fused
+# gate/up GLU, down, q/o, k/v; then the LM head.
+QMM_SHAPES = (("gate_up", 14336, 4096, True), ("down", 4096, 14336, False),
+              ("q_o", 4096, 4096, False), ("k_v", 1024, 4096, False))
+
+
+def qmm_bench(ctx, torch, reps=30):
+    """The quantized matmul (cuca_hip_qmm, cuca_hip_qmm_glu) at the 8B
+    decode shapes, Q4_0 and Q8_0, f32 activations, 1 and 4 rows.  Weights
+    are rotated over copies totalling > 256 MiB so that no call finds its
+    weights in the last-level cache.  Algorithmic bytes per call: the weight
+    blocks (18 or 34 bytes per 32 values; both matrices for the GLU), the
+    activations in and the outputs, f32.  Each shape's first 64 output
+    columns are checked bit for bit against the oracle (the GLU's
+    activation to 1e-5 relative)."""
+    import numpy as np
+    from cuca_amd import hip, ops
+    from cuca_amd import workloads as W
+    from oracle import oracle as O
+    res = {}
+    for qtype in ("q4_0", "q8_0"):
+        gid = W.GGML_ID[qtype]
+        for name, n, k, glu in QMM_SHAPES:
+            rng = np.random.default_rng(n + k)
+            raws = [W.quant_table(rng, n, k, qtype, (0.001, 0.02)) for _ in range(2 if glu else 1)]
+            wbytes = sum(r.size for r in raws)
+            copies = max(2, int(np.ceil(320e6 / wbytes)))
+            ws = [[ops.QmmWeight.from_raw(ctx, gid, r, n, k) for r in raws] for _ in range(copies)]
+            for m in (1, 4):
+                x = rng.standard_normal((m, k)).astype(np.float32)
+                dx = ctx.array(x)
+                out = ctx.empty((m, n), np.float32)
+
+                def call(i, dx=dx, out=out):
+                    w = ws[i % copies]
+                    if glu:
+                        ops.QmmWeight.glu(w[0], w[1], dx, ops.Glu(hip.ACT_SILU), out=out)
+                    else:
+                        w[0].forward(dx, out=out)
+                ms, parts = kernel_calls(ctx, call, reps)
+                call(0)
+                got = out.numpy()[:, :64]
+                want = [O.qmm(r, gid, n, k, x, rows=64, threads=8) for r in raws]
+                if glu:
+                    want = O.glu(want[0], want[1], hip.ACT_SILU)
+                    assert np.all(np.abs(got - want) <= 1e-5 * np.abs(want) + 1e-30), f"qmm {name} {qtype}"
+                else:
+                    assert np.array_equal(got.view(np.uint32), want[0].view(np.uint32)), f"qmm {name} {qtype}"
+                b = wbytes + m * k * 4 + m * n * 4
+                res[f"{name}_{qtype}_m{m}"] = dict(
+                    kernels=[p for p, _ in parts], us=round(ms * 1000, 2), bytes=b,
+                    gbs=round(b / (ms / 1e3) / 1e9, 1), frac=round(b / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4))
+                dx.free()
+                out.free()
+            for w in ws:
+                for q in w:
+                    q.packed.free()
+    return res
+
+
+def moe_bench(ctx, torch, reps=30):
+    """Routed experts at config E (Qwen3-30B-A3B: 128 experts of ff 768 over
+    hidden 2048, Q4_0, top 8): moe_up (gate/up + SwiGLU), moe_down (times the
+    routing weight), moe_sum, f32, at decode batches of 1 and 32 tokens with
+    uniform routing.  Algorithmic bytes: the weights of the experts the
+    batch touches, the tokens' rows in, the hidden rows out and back in, the
+    output rows.  Checked against the oracle's expert_sum to 1e-4 of each
+    token's largest |output| (the bar of the layer test)."""
+    import numpy as np
+    from cuca_amd import hip, ops
+    from cuca_amd import workloads as W
+    from oracle import oracle as O
+    cfg = W.CONFIGS["E"]
+    H, F = cfg["hidden"], cfg["ff"]
+    n_exp, n_used = cfg["moe"]
+    qtype = cfg["qtype"]
+    rng = np.random.default_rng(5)
+    # eight distinct expert triples, each packed into every sixteenth slot:
+    # 128 separate experts in memory (340 MB), no two slots sharing bytes
+    base = [(W.quant_table(rng, F, H, qtype, (0.01, 0.05)), W.quant_table(rng, F, H, qtype, (0.01, 0.05)),
+             W.quant_table(rng, H, F, qtype, (0.004, 0.02))) for _ in range(8)]
+    experts = [base[e % 8] for e in range(n_exp)]
+    bank = ops.ExpertBank.from_raw(ctx, W.GGML_ID[qtype], experts, H, F)
+    per_matrix = [m.size for m in base[0]]
+    res = {}
+    for t in (1, 32):
+        x = rng.standard_normal((t, H)).astype(np.float32)
+        dx = ctx.array(x)
+        per = [[] for _ in range(n_exp)]
+        for tok in range(t):
+            for e, w in zip(sorted(rng.choice(n_exp, n_used, replace=False)),
+                            rng.uniform(0.05, 1.0, n_used).astype(np.float32)):
+                per[e].append((tok, float(w)))
+        touched = sum(1 for p in per if p)
+        keep = []
+
+        def call(i):
+            keep.append(bank.expert_sum(dx, per, ops.Glu(hip.ACT_SILU), n_used))
+            if len(keep) > 4:
+                keep.pop(0)
+        ms, parts = kernel_calls(ctx, call, reps)
+        out = keep[-1][0].numpy()
+        want, _ = O.expert_sum(x, experts, W.GGML_ID[qtype], per, hip.ACT_SILU, threads=8)
+        assert np.all(np.abs(out - want) <= 1e-4 * np.abs(want).max(-1, keepdims=True)), "moe"
+        pairs = t * n_used
+        b = touched * sum(per_matrix) + t * H * 4 + 2 * pairs * F * 4 + t * H * 4
+        res[f"E_decode_t{t}"] = dict(kernels=[p for p, _ in parts], us=round(ms * 1000, 2),
+                                     parts_us=[round(v * 1000, 2) for _, v in parts],
+                                     experts_touched=touched, bytes=b, gbs=round(b / (ms / 1e3) / 1e9, 1),
+                                     frac=round(b / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4))
+        keep.clear()
+        dx.free()
+    for p in (bank.gate, bank.up, bank.down):
+        p.free()
+    return res
+
+
+def head_bench(ctx, torch, reps=30):
+    """The end of a decode step for the 8B model at batch 1, f32: the LM head
+    (cuca_hip_lm_head, Q8_0 and Q4_0 128256 x 4096; the decode GEMV after the
+    activation quantisation) with the logits written once, then greedy
+    (cuca_hip_argmax) or top-k 40 at temperature 0.8 (cuca_hip_top_k).
+    Algorithmic bytes of the head: the weight blocks, the row in, the logits
+    out.  Checked: the first 64 logits bit for bit, the argmax and the top-k
+    against the oracle on the device's own logits."""
+    import numpy as np
+    from cuca_amd import hip, ops
+    from cuca_amd import workloads as W
+    from oracle import oracle as O
+    vocab, H = 128256, 4096
+    res = {}
+    for qtype in ("q8_0", "q4_0"):
+        gid = W.GGML_ID[qtype]
+        rng = np.random.default_rng(9)
+        raw = W.quant_table(rng, vocab, H, qtype, (0.001, 0.02))
+        ws = [ops.QmmWeight.from_raw(ctx, gid, raw, vocab, H) for _ in range(2)]
+        x = rng.standard_normal((1, H)).astype(np.float32)
+        dx = ctx.array(x)
+        logits = ctx.empty((1, vocab), np.float32)
+        ids = ctx.empty((1,), np.uint32)
+        tl, ti, tc = ctx.empty((1, 40), np.float32), ctx.empty((1, 40), np.uint32), ctx.empty((1,), np.int32)
+
+        def head(i):
+            w = ws[i % 2]
+            ctx.lm_head(w.packed.ptr, gid, vocab, H, dx.ptr, H, 1, vocab, 1.0, 1.0, 0.0, logits.ptr,
+                        vocab, hip.F32)
+        ms, parts = kernel_calls(ctx, head, reps)
+        b = raw.size + H * 4 + vocab * 4
+        r = dict(kernels=[p for p, _ in parts], us=round(ms * 1000, 2), bytes=b,
+                 gbs=round(b / (ms / 1e3) / 1e9, 1), frac=round(b / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4))
+        if qtype == "q8_0":
+            g_ms, _ = kernel_calls(ctx, lambda i: ctx.argmax(logits.ptr, vocab, 1, vocab, hip.F32, ids.ptr),
+                                   reps)
+            k_ms, _ = kernel_calls(ctx, lambda i: ctx.top_k(logits.ptr, vocab, 1, vocab, hip.F32, 40, 0.8,
+                                                              tl.ptr, ti.ptr, tc.ptr), reps)
+            r.update(argmax_us=round(g_ms * 1000, 2), top_k40_us=round(k_ms * 1000, 2))
+        head(0)
+        ctx.argmax(logits.ptr, vocab, 1, vocab, hip.F32, ids.ptr)
+        ctx.top_k(logits.ptr, vocab, 1, vocab, hip.F32, 40, 0.8, tl.ptr, ti.ptr, tc.ptr)
+        lg = logits.numpy()
+        want = O.qmm(raw, gid, vocab, H, x, rows=64, threads=8)
+        assert np.array_equal(lg[:, :64].view(np.uint32), want.view(np.uint32)), "lm head"
+        assert int(ids.numpy()[0]) == O.greedy(lg[0]), "argmax"
+        wl, wi = O.select_top_k(lg[0], 0.8, 40)
+        assert ti.numpy()[0, :tc.numpy()[0]].tolist() == wi.tolist(), "top-k"
+        res[f"lm_head_{qtype}_b1"] = r
+        for a in (dx, logits, ids, tl, ti, tc):
+            a.free()
+        for w in ws:
+            w.packed.free()
+    return res
+
+
 def cpu_baseline(seconds=10.0, n=64):
     """The oracle (candle-equivalent C restatement) over the same step's ops
     on n tokens, repeated for about `seconds`, on the host's cores."""
@@ -608,6 +800,8 @@ def main():
     ap.add_argument("--no-configs", action="store_true", help="skip the A/B/D/E config steps")
     ap.add_argument("--no-kv", action="store_true", help="skip the fused RoPE + paged K/V store")
     ap.add_argument("--no-attn", action="store_true", help="skip the paged decode attention")
+    ap.add_argument("--no-qmm", action="store_true",
+                    help="skip the quantized matmuls, routed experts and LM head")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: these ops run on one GPU's share of the work and "
@@ -704,6 +898,16 @@ def main():
             checked_rows += 2
         torch.cuda.empty_cache()
 
+    qmm = moe = head = None
+    if not args.no_qmm:
+        log("quantized matmuls (8B decode shapes)")
+        qmm = qmm_bench(ctx, torch)
+        log("routed experts (config E decode)")
+        moe = moe_bench(ctx, torch)
+        log("LM head + greedy / top-k")
+        head = head_bench(ctx, torch)
+        torch.cuda.empty_cache()
+
     decode = None
     if not args.no_decode:
         log("decode graphs")
@@ -751,6 +955,9 @@ def main():
         "configs": configs,
         "rope_store_kv": kv,
         "paged_decode": attn,
+        "qmm_decode": qmm,
+        "moe_decode": moe,
+        "end_of_step": head,
         "decode_us_per_layer": decode,
         "roofline": {"kernel": glu["kernel"], "bound": "hbm",
                      "achieved": glu["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",

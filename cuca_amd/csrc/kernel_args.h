@@ -187,15 +187,26 @@ typedef struct {
 /* Greedy argmax and top-k over logits rows (sampler.rs greedy and
  * select_top_k).  top-k: keys are logit / temperature; the k best finite
  * ones in (logit desc, id asc) order go to out_logits / out_ids, their
- * count to out_count. */
+ * count to out_count.  A row is split into `slices` of slice_len values;
+ * with more than one, the slices' results go to cand (argmax: one (value
+ * bits << 32 | id) per slice; top-k: up to k composites per slice, their
+ * count in cand_count) and a merge launch finishes the row. */
+#define CUCA_PICK_CAP 7680        /* top-k composites a workgroup holds in LDS */
+#define CUCA_PICK_MAX_SLICES 256  /* slices per row                           */
+
 typedef struct {
     const void *logits;     /* [rows][ld] f32 or f16                          */
     float *out_logits;      /* [rows][k]                                      */
     uint32_t *out_ids;      /* [rows][k] (argmax: [rows])                     */
     int32_t *out_count;     /* [rows]                                         */
+    unsigned long long *cand; /* [rows][slices][k] (argmax: [rows][slices])   */
+    int32_t *cand_count;    /* [rows][slices]                                 */
     int64_t ld;
     int32_t rows, vocab, k;
     float temperature;
+    int32_t slices, slice_len;
+    int32_t mode;           /* 0: whole rows, final; 1: slices to cand        */
+    int32_t pad_;
 } PickArgs;
 
 /* MoE expert sum: out[t] = sum over i < n_used of scratch[pairs[t][i]]

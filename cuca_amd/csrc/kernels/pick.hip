@@ -11,53 +11,107 @@
 //                sampler.rs:578-596).  The host then runs the rest of
 //                warp_candidates / sample on those k candidates.
 //
-// argmax: one workgroup per row; each thread scans a strided subsequence
-// with the strict comparison (its first maximum), and the workgroup keeps the
-// larger value, the smaller id on ties.
+// A decode step has one row per sequence, often a single one, so a row is
+// split into slices that separate workgroups take (the host picks the
+// slice count from the rows and the CU count), and a second launch combines
+// the slices' results; a row taken whole by one workgroup (many rows) needs
+// no second launch.
 //
-// top-k: one workgroup of 1024 threads per row.  A finite logit l becomes
-// the 32-bit key whose unsigned order is f32::total_cmp's (sign bit set:
-// ~bits, else bits | 2^31).  Four 8-bit radix passes (LDS histograms) find
-// the k-th largest key K; every key > K is kept, and the lowest ids with key
-// == K fill the rest (thread t scans a contiguous range, so a block scan of
-// the per-thread counts keeps id order).  The k candidates are sorted in
-// LDS by a bitonic sort of (key, ~id) and written best first.
+// argmax: a workgroup scans its slice, each thread a strided subsequence in
+// increasing index order with the strict comparison (its first maximum);
+// results combine as (larger value, or the smaller id on equal values), so
+// any split gives the first maximum of the row.
+//
+// top-k: a finite logit l becomes the 64-bit composite (key << 32) | ~id,
+// where the 32-bit key's unsigned order is f32::total_cmp's (sign bit set:
+// ~bits, else bits | 2^31).  Composites are distinct, and the k largest are
+// exactly the k best of (logit desc, id asc).  A workgroup holds up to
+// PICK_CAP composites in LDS; a radix select, 8 bits a pass from the top,
+// finds the k-th largest (stopping as soon as one bucket holds exactly the
+// entries still needed) and keeps the composites at or above it.  A slice
+// longer than the LDS is taken in rounds (the k kept ones plus the next
+// values).  The slices' candidates are a superset of the row's k best; the
+// combining workgroup selects among them the same way and writes the k in
+// order, each thread placing one candidate at its rank.
 #include "common.h"
 
 #define PICK_THREADS 1024
-#define PICK_MAX_K 1024
+#define PICK_CAP CUCA_PICK_CAP
+#define PICK_PER ((PICK_CAP + PICK_THREADS - 1) / PICK_THREADS)
+#define PICK_MAX_SLICES CUCA_PICK_MAX_SLICES
+#define ARGMAX_UNROLL 8
+
+typedef unsigned long long u64;
 
 template <typename T> __device__ static inline float pick_load(const void *p, int64_t i) {
     return (float)reinterpret_cast<const T *>(p)[i];
 }
 
-template <typename T> __device__ static inline void argmax_body(const PickArgs &a) {
-    const int row = blockIdx.x;
-    if (row >= a.rows) return;
-    const void *lg = reinterpret_cast<const T *>(a.logits) + (int64_t)row * a.ld;
-    float best = -__builtin_inff();
-    uint32_t bi = 0xffffffffu;
-    for (int i = threadIdx.x; i < a.vocab; i += CUCA_BLOCK) {
-        const float v = pick_load<T>(lg, i);
-        if (v > best) { best = v; bi = (uint32_t)i; }
-    }
-    // larger value; equal values: the smaller id (the earlier first maximum)
+// (value, id) pairs: the larger value wins, the smaller id on equal values;
+// id 0xffffffff is "none" (every value NaN or -inf so far).
+__device__ static inline void argmax_merge(float &best, uint32_t &bi, float ov, uint32_t oi) {
+    if (ov > best || (ov == best && oi < bi)) { best = ov; bi = oi; }
+}
+__device__ static inline u64 argmax_pack(float v, uint32_t id) {
+    return ((u64)__builtin_bit_cast(uint32_t, v) << 32) | id;
+}
+
+__device__ static inline void argmax_wave(float &best, uint32_t &bi) {
 #pragma unroll
     for (int off = CUCA_WAVE / 2; off >= 1; off >>= 1) {
         const float ov = __shfl_xor(best, off, CUCA_WAVE);
         const uint32_t oi = (uint32_t)__shfl_xor((int)bi, off, CUCA_WAVE);
-        if (ov > best || (ov == best && oi < bi)) { best = ov; bi = oi; }
+        argmax_merge(best, bi, ov, oi);
     }
+}
+
+// mode 0: the workgroup takes the whole row and writes the id; mode 1: it
+// takes slice blockIdx % slices and writes its (value, id) to cand.
+template <typename T> __device__ static inline void argmax_body(const PickArgs &a) {
+    const int row = blockIdx.x / a.slices, s = blockIdx.x - row * a.slices;
+    if (row >= a.rows) return;
+    const void *lg = reinterpret_cast<const T *>(a.logits) + (int64_t)row * a.ld;
+    const int lo = s * a.slice_len, hi = min(a.vocab, lo + a.slice_len);
+    float best = -__builtin_inff();
+    uint32_t bi = 0xffffffffu;
+    for (int i0 = lo + (int)threadIdx.x; i0 < hi; i0 += ARGMAX_UNROLL * CUCA_BLOCK) {
+        float v[ARGMAX_UNROLL];
+#pragma unroll
+        for (int u = 0; u < ARGMAX_UNROLL; u++) {
+            const int i = i0 + u * CUCA_BLOCK;
+            v[u] = i < hi ? pick_load<T>(lg, i) : -__builtin_inff();
+        }
+#pragma unroll
+        for (int u = 0; u < ARGMAX_UNROLL; u++)
+            if (v[u] > best) { best = v[u]; bi = (uint32_t)(i0 + u * CUCA_BLOCK); }
+    }
+    argmax_wave(best, bi);
     __shared__ float sv[CUCA_BLOCK / CUCA_WAVE];
     __shared__ uint32_t si[CUCA_BLOCK / CUCA_WAVE];
     const int wave = threadIdx.x / CUCA_WAVE;
     if ((threadIdx.x & (CUCA_WAVE - 1)) == 0) { sv[wave] = best; si[wave] = bi; }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < CUCA_BLOCK / CUCA_WAVE; w++)
-            if (sv[w] > best || (sv[w] == best && si[w] < bi)) { best = sv[w]; bi = si[w]; }
-        a.out_ids[row] = bi == 0xffffffffu ? 0u : bi;
+        for (int w = 1; w < CUCA_BLOCK / CUCA_WAVE; w++) argmax_merge(best, bi, sv[w], si[w]);
+        if (a.mode == 0) a.out_ids[row] = bi == 0xffffffffu ? 0u : bi;
+        else a.cand[(int64_t)row * a.slices + s] = argmax_pack(best, bi);
     }
+}
+
+// One wave per row over the row's slices, in any order (the merge is
+// order-free), CUCA_BLOCK / 64 rows per workgroup.
+__device__ static inline void argmax_merge_body(const PickArgs &a) {
+    const int row = blockIdx.x * (CUCA_BLOCK / CUCA_WAVE) + (int)threadIdx.x / CUCA_WAVE;
+    const int lane = threadIdx.x & (CUCA_WAVE - 1);
+    if (row >= a.rows) return;
+    float best = -__builtin_inff();
+    uint32_t bi = 0xffffffffu;
+    for (int s = lane; s < a.slices; s += CUCA_WAVE) {
+        const u64 p = a.cand[(int64_t)row * a.slices + s];
+        argmax_merge(best, bi, __builtin_bit_cast(float, (uint32_t)(p >> 32)), (uint32_t)p);
+    }
+    argmax_wave(best, bi);
+    if (lane == 0) a.out_ids[row] = bi == 0xffffffffu ? 0u : bi;
 }
 
 // f32::total_cmp order as an unsigned key.
@@ -69,145 +123,172 @@ __device__ static inline float pick_unkey(uint32_t k) {
     return __builtin_bit_cast(float, (k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
-// Exclusive block-wide prefix sum of v (PICK_THREADS threads); *total gets
-// the sum.  `red` holds PICK_THREADS / 64 ints.
-__device__ static inline int pick_scan(int v, int *red, int *total) {
-    const int lane = threadIdx.x & (CUCA_WAVE - 1), wave = threadIdx.x / CUCA_WAVE;
-    int incl = v;
+struct PickLds {
+    u64 c[PICK_CAP];
+    int hist[256];
+    int wsum[4];
+    int cnt[PICK_MAX_SLICES];
+    int count;
+    u64 prefix;
+    int need, exact;
+};
+
+// Number of nonzero entries of c[0, n) (block-uniform result).
+__device__ static inline int pick_nonzero(PickLds &L, const u64 (&e)[PICK_PER]) {
+    if (threadIdx.x == 0) L.count = 0;
+    __syncthreads();
+    int n = 0;
 #pragma unroll
-    for (int off = 1; off < CUCA_WAVE; off <<= 1) {
-        const int o = __shfl_up(incl, off, CUCA_WAVE);
-        if (lane >= off) incl += o;
-    }
+    for (int i = 0; i < PICK_PER; i++) n += e[i] != 0ull;
+#pragma unroll
+    for (int off = CUCA_WAVE / 2; off >= 1; off >>= 1) n += __shfl_xor(n, off, CUCA_WAVE);
+    if ((threadIdx.x & (CUCA_WAVE - 1)) == 0 && n) atomicAdd(&L.count, n);
     __syncthreads();
-    if (lane == CUCA_WAVE - 1) red[wave] = incl;
+    const int r = L.count;
     __syncthreads();
-    int before = 0, all = 0;
-    for (int w = 0; w < PICK_THREADS / CUCA_WAVE; w++) {
-        if (w < wave) before += red[w];
-        all += red[w];
-    }
-    *total = all;
-    return before + incl - v;
+    return r;
 }
 
-template <typename T> __device__ static inline void topk_body(const PickArgs &a) {
-    const int row = blockIdx.x;
-    if (row >= a.rows) return;
-    const void *lg = reinterpret_cast<const T *>(a.logits) + (int64_t)row * a.ld;
+// Keep the kk = min(k, nonzero) largest composites of c[0, n), moved to
+// c[0, kk) in any order; returns kk.
+__device__ static inline int pick_select(PickLds &L, int n, int k) {
     const int tid = threadIdx.x;
-    __shared__ int hist[256];
-    __shared__ int red[PICK_THREADS / CUCA_WAVE];
-    __shared__ uint32_t sh_prefix;
-    __shared__ int sh_need;
-    __shared__ unsigned long long cand[PICK_MAX_K];
-    // contiguous range of this thread (id order for the compaction)
-    const int per = (a.vocab + PICK_THREADS - 1) / PICK_THREADS;
-    const int lo = tid * per, hi = min(a.vocab, lo + per);
-    // the logit of element i as sample() sees it: l / temperature, finite only
-    auto key_at = [&](int i, bool *ok) -> uint32_t {
-        const float l = pick_load<T>(lg, i) / a.temperature;
-        *ok = __builtin_isfinite(l);
-        return pick_key(l);
-    };
-    // 1. radix select the k-th largest finite key, 8 bits at a time
-    uint32_t prefix = 0, mask = 0;
-    int need = a.k; // rank of the wanted key among those matching the prefix
-    int n_finite_total = 0;
-    for (int pass = 0; pass < 4; pass++) {
-        const int shift = 24 - 8 * pass;
-        for (int b = tid; b < 256; b += PICK_THREADS) hist[b] = 0;
-        __syncthreads();
-        int n_finite = 0;
-        for (int i = lo; i < hi; i++) {
-            bool ok;
-            const uint32_t key = key_at(i, &ok);
-            if (!ok) continue;
-            n_finite++;
-            if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1);
-        }
-        if (pass == 0) {
-            int tot;
-            (void)pick_scan(n_finite, red, &tot);
-            n_finite_total = tot;
-        }
-        __syncthreads();
-        if (tid == 0) {
-            int kk = need < n_finite_total ? need : n_finite_total;
-            if (kk <= 0) kk = 1;
-            int d = 255, acc = 0;
-            for (; d > 0; d--) {
-                if (acc + hist[d] >= kk) break;
-                acc += hist[d];
+    u64 e[PICK_PER];
+#pragma unroll
+    for (int i = 0; i < PICK_PER; i++) {
+        const int j = tid + i * PICK_THREADS;
+        e[i] = j < n ? L.c[j] : 0ull;
+    }
+    const int nnz = pick_nonzero(L, e);
+    const int kk = nnz < k ? nnz : k;
+    u64 thr = 1ull; // keep e >= thr (and nonzero)
+    if (nnz > k) {
+        u64 prefix = 0ull;
+        int need = kk;
+        for (int shift = 56; shift >= 0; shift -= 8) {
+            if (tid < 256) L.hist[tid] = 0;
+            __syncthreads();
+#pragma unroll
+            for (int i = 0; i < PICK_PER; i++) {
+                const bool match = e[i] != 0ull && (shift == 56 || (e[i] >> (shift + 8)) == (prefix >> (shift + 8)));
+                if (match) atomicAdd(&L.hist[(int)((e[i] >> shift) & 255ull)], 1);
             }
-            sh_prefix = prefix | ((uint32_t)d << shift);
-            sh_need = kk - acc;
-        }
-        __syncthreads();
-        prefix = sh_prefix;
-        need = sh_need;
-        mask |= 255u << shift;
-    }
-    const int kk = a.k < n_finite_total ? a.k : n_finite_total;
-    if (kk <= 0) {
-        if (tid == 0) a.out_count[row] = 0;
-        return;
-    }
-    // prefix is the k-th largest key K; `need` keys equal to K are kept
-    // 2. compaction: keys > K anywhere, then the first `need` keys == K in id order
-    int n_gt = 0, n_eq = 0;
-    for (int i = lo; i < hi; i++) {
-        bool ok;
-        const uint32_t key = key_at(i, &ok);
-        if (!ok) continue;
-        n_gt += key > prefix;
-        n_eq += key == prefix;
-    }
-    int tot_gt, tot_eq;
-    const int at_gt = pick_scan(n_gt, red, &tot_gt);
-    const int at_eq = pick_scan(n_eq, red, &tot_eq);
-    int wgt = at_gt, weq = tot_gt + at_eq;
-    for (int i = lo; i < hi; i++) {
-        bool ok;
-        const uint32_t key = key_at(i, &ok);
-        if (!ok) continue;
-        const unsigned long long c = ((unsigned long long)key << 32) | (0xffffffffu - (uint32_t)i);
-        if (key > prefix) {
-            if (wgt < PICK_MAX_K) cand[wgt] = c;
-            wgt++;
-        } else if (key == prefix) {
-            if (weq < tot_gt + need && weq < PICK_MAX_K) cand[weq] = c;
-            weq++;
-        }
-    }
-    // pad to a power of two for the bitonic sort
-    int n = 1;
-    while (n < kk) n <<= 1;
-    for (int i = kk + tid; i < n; i += PICK_THREADS) cand[i] = 0ull;
-    __syncthreads();
-    // 3. bitonic sort, descending
-    for (int size = 2; size <= n; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int i = tid; i < n; i += PICK_THREADS) {
-                const int j = i ^ stride;
-                if (j > i) {
-                    const bool desc = (i & size) == 0;
-                    const unsigned long long x = cand[i], y = cand[j];
-                    if ((x < y) == desc) { cand[i] = y; cand[j] = x; }
+            __syncthreads();
+            // buckets from the top (thread t holds bucket 255 - t): the one
+            // where the running count reaches `need`
+            const int lane = tid & (CUCA_WAVE - 1), w = tid / CUCA_WAVE;
+            int v = 0, incl = 0;
+            if (tid < 256) {
+                v = L.hist[255 - tid];
+                incl = v;
+#pragma unroll
+                for (int off = 1; off < CUCA_WAVE; off <<= 1) {
+                    const int o = __shfl_up(incl, off, CUCA_WAVE);
+                    if (lane >= off) incl += o;
+                }
+                if (lane == CUCA_WAVE - 1) L.wsum[w] = incl;
+            }
+            __syncthreads();
+            if (tid < 256) {
+                for (int q = 0; q < w; q++) incl += L.wsum[q];
+                const int excl = incl - v;
+                if (excl < need && need <= incl) {
+                    L.prefix = prefix | ((u64)(255 - tid) << shift);
+                    L.need = need - excl;
+                    L.exact = v == need - excl;
                 }
             }
             __syncthreads();
+            // L.prefix / need / exact are written again only after the next
+            // pass's barriers, and hist was last read above
+            prefix = L.prefix;
+            need = L.need;
+            if (L.exact) break;
         }
+        thr = prefix;
     }
-    for (int i = tid; i < kk; i += PICK_THREADS) {
-        const unsigned long long c = cand[i];
-        a.out_logits[(int64_t)row * a.k + i] = pick_unkey((uint32_t)(c >> 32));
-        a.out_ids[(int64_t)row * a.k + i] = 0xffffffffu - (uint32_t)c;
+    // compaction (order-free: composites are distinct)
+    if (tid == 0) L.count = 0;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < PICK_PER; i++)
+        if (e[i] != 0ull && e[i] >= thr) L.c[atomicAdd(&L.count, 1)] = e[i];
+    __syncthreads();
+    return kk;
+}
+
+// The composite of element i of a logits row.
+template <typename T>
+__device__ static inline u64 pick_composite(const void *lg, int i, float temperature) {
+    const float l = pick_load<T>(lg, i) / temperature;
+    if (!__builtin_isfinite(l)) return 0ull;
+    return ((u64)pick_key(l) << 32) | (uint32_t)~(uint32_t)i;
+}
+
+// Final: c[0, kk) sorted best first into the row's outputs.
+__device__ static inline void pick_write(PickLds &L, const PickArgs &a, int row, int kk) {
+    for (int t = threadIdx.x; t < kk; t += PICK_THREADS) {
+        const u64 mine = L.c[t];
+        int rank = 0;
+        for (int j = 0; j < kk; j++) rank += L.c[j] > mine;
+        a.out_logits[(int64_t)row * a.k + rank] = pick_unkey((uint32_t)(mine >> 32));
+        a.out_ids[(int64_t)row * a.k + rank] = ~(uint32_t)mine;
     }
-    if (tid == 0) a.out_count[row] = kk;
+    if (threadIdx.x == 0) a.out_count[row] = kk;
+}
+
+// SRC 0: the logits (mode 0 the whole row, final; mode 1 slice
+// blockIdx % slices, candidates to cand / cand_count); SRC 1: the row's
+// slices' candidates (final).
+template <typename T, int SRC> __device__ static inline void topk_body(const PickArgs &a) {
+    __shared__ PickLds L;
+    const int S = SRC == 1 ? 1 : a.slices;
+    const int row = blockIdx.x / S, s = blockIdx.x - row * S;
+    if (row >= a.rows) return;
+    const int tid = threadIdx.x;
+    const void *lg = reinterpret_cast<const T *>(a.logits) + (int64_t)row * a.ld;
+    int lo = 0, total = 0;
+    const u64 *cand = nullptr;
+    if (SRC == 0) {
+        lo = s * a.slice_len;
+        total = max(0, min(a.vocab, lo + a.slice_len) - lo);
+    } else {
+        for (int j = tid; j < a.slices; j += PICK_THREADS) L.cnt[j] = a.cand_count[(int64_t)row * a.slices + j];
+        cand = a.cand + (int64_t)row * a.slices * a.k;
+        total = a.slices * a.k; // slot (slice j, i) holds a candidate when i < cnt[j]
+        __syncthreads();
+    }
+    int held = 0, pos = 0;
+    for (;;) {
+        const int take = min(PICK_CAP - held, total - pos);
+        for (int j = tid; j < take; j += PICK_THREADS) {
+            const int q = pos + j;
+            u64 c;
+            if (SRC == 0) {
+                c = pick_composite<T>(lg, lo + q, a.temperature);
+            } else {
+                const int sl = q / a.k;
+                c = q - sl * a.k < L.cnt[sl] ? cand[q] : 0ull;
+            }
+            L.c[held + j] = c;
+        }
+        pos += take;
+        __syncthreads();
+        held = pick_select(L, held + take, a.k);
+        if (pos >= total) break;
+    }
+    if (SRC == 0 && a.mode == 1) {
+        u64 *dst = a.cand + ((int64_t)row * a.slices + s) * a.k;
+        for (int j = tid; j < held; j += PICK_THREADS) dst[j] = L.c[j];
+        if (tid == 0) a.cand_count[(int64_t)row * a.slices + s] = held;
+    } else {
+        pick_write(L, a, row, held);
+    }
 }
 
 extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void cuca_argmax_f32(PickArgs a) { argmax_body<float>(a); }
 extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void cuca_argmax_f16(PickArgs a) { argmax_body<_Float16>(a); }
-extern "C" __global__ __launch_bounds__(PICK_THREADS) void cuca_topk_f32(PickArgs a) { topk_body<float>(a); }
-extern "C" __global__ __launch_bounds__(PICK_THREADS) void cuca_topk_f16(PickArgs a) { topk_body<_Float16>(a); }
+extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void cuca_argmax_merge(PickArgs a) { argmax_merge_body(a); }
+extern "C" __global__ __launch_bounds__(PICK_THREADS) void cuca_topk_f32(PickArgs a) { topk_body<float, 0>(a); }
+extern "C" __global__ __launch_bounds__(PICK_THREADS) void cuca_topk_f16(PickArgs a) { topk_body<_Float16, 0>(a); }
+extern "C" __global__ __launch_bounds__(PICK_THREADS) void cuca_topk_merge(PickArgs a) { topk_body<float, 1>(a); }

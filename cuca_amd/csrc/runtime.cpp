@@ -64,6 +64,8 @@ thread_local std::string g_thread_error;
 // The context's scratch for quantised activations: two rows of up to
 // 16384 values (quants, then f32 block scales), rounded up.
 constexpr size_t kQScratchBytes = 64 << 10;
+// The context's scratch for the slices' results of argmax / top-k.
+constexpr size_t kPickScratchBytes = 4 << 20;
 
 }  // namespace
 
@@ -84,6 +86,8 @@ struct cuca_hip_ctx {
     // cuca_hip_qmm / _qmm_glu / _lm_head route through cuca_q8_acts + qmv
     // (allocated with the context: ops never allocate)
     void *qscratch = nullptr;
+    // device scratch for the per-slice results of cuca_hip_argmax / _top_k
+    void *pscratch = nullptr;
     int cu_count = 256;
     std::string error;
     // per-kernel timing (cuca_hip_profile_start/stop)
@@ -207,6 +211,9 @@ cuca_status cuca_hip_ctx_create(int device, cuca_hip_ctx **out) {
         if ((e = hipMalloc(&ctx->qscratch, kQScratchBytes)) != hipSuccess) {
             st = hip_fail(ctx, e, "hipMalloc(activation scratch)"); break;
         }
+        if ((e = hipMalloc(&ctx->pscratch, kPickScratchBytes)) != hipSuccess) {
+            st = hip_fail(ctx, e, "hipMalloc(selection scratch)"); break;
+        }
         if ((e = hipMalloc(&ctx->status, CUCA_STATUS_WORDS * sizeof(unsigned long long))) != hipSuccess) {
             st = hip_fail(ctx, e, "hipMalloc(status)"); break;
         }
@@ -242,6 +249,7 @@ void cuca_hip_ctx_destroy(cuca_hip_ctx *ctx) {
     }
     if (ctx->status) (void)hipFree(ctx->status);
     if (ctx->qscratch) (void)hipFree(ctx->qscratch);
+    if (ctx->pscratch) (void)hipFree(ctx->pscratch);
     if (ctx->module) (void)hipModuleUnload(ctx->module);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
@@ -1060,7 +1068,19 @@ cuca_status cuca_hip_argmax(cuca_hip_ctx *ctx, const void *logits, int64_t ld, i
     a.ld = ld;
     a.rows = (int32_t)rows;
     a.vocab = (int32_t)vocab;
-    return launch(ctx, dtype == CUCA_F16 ? cuca_argmax_f16 : cuca_argmax_f32, (unsigned)rows, CUCA_BLOCK_THREADS, 0, a);
+    // slices of at least 2048 values, enough of them to give the chip four
+    // workgroups per CU
+    int64_t slices = std::min<int64_t>((vocab + 2047) / 2048, std::max<int64_t>(1, 4 * ctx->cu_count / rows));
+    slices = std::min<int64_t>(slices, (int64_t)(kPickScratchBytes / 8) / rows);
+    if (slices < 2) slices = 1;
+    a.slices = (int32_t)slices;
+    a.slice_len = (int32_t)((vocab + slices - 1) / slices);
+    a.mode = slices > 1;
+    a.cand = static_cast<unsigned long long *>(ctx->pscratch);
+    if ((st = launch(ctx, dtype == CUCA_F16 ? cuca_argmax_f16 : cuca_argmax_f32, (unsigned)(rows * slices),
+                     CUCA_BLOCK_THREADS, 0, a)) != CUCA_OK || slices == 1)
+        return st;
+    return launch(ctx, cuca_argmax_merge, (unsigned)div_up(rows, CUCA_BLOCK_THREADS / 64), CUCA_BLOCK_THREADS, 0, a);
 }
 
 cuca_status cuca_hip_top_k(cuca_hip_ctx *ctx, const void *logits, int64_t ld, int64_t rows, int64_t vocab,
@@ -1084,7 +1104,23 @@ cuca_status cuca_hip_top_k(cuca_hip_ctx *ctx, const void *logits, int64_t ld, in
     a.vocab = (int32_t)vocab;
     a.k = k;
     a.temperature = temperature;
-    return launch(ctx, dtype == CUCA_F16 ? cuca_topk_f16 : cuca_topk_f32, (unsigned)rows, 1024, 0, a);
+    // slices of at least 2048 values, two workgroups per CU, at most
+    // CUCA_PICK_CAP candidates per row for the merge (one LDS round) and
+    // the candidates within the context's scratch
+    const int64_t per_slice = (int64_t)k * 8 + 4;
+    int64_t slices = std::min<int64_t>((vocab + 2047) / 2048, std::max<int64_t>(1, 2 * ctx->cu_count / rows));
+    slices = std::min<int64_t>(slices, std::min<int64_t>(CUCA_PICK_CAP / k, CUCA_PICK_MAX_SLICES));
+    slices = std::min<int64_t>(slices, (int64_t)kPickScratchBytes / (rows * per_slice));
+    if (slices < 2) slices = 1;
+    a.slices = (int32_t)slices;
+    a.slice_len = (int32_t)((vocab + slices - 1) / slices);
+    a.mode = slices > 1;
+    a.cand = static_cast<unsigned long long *>(ctx->pscratch);
+    a.cand_count = reinterpret_cast<int32_t *>(static_cast<char *>(ctx->pscratch) + rows * slices * k * 8);
+    if ((st = launch(ctx, dtype == CUCA_F16 ? cuca_topk_f16 : cuca_topk_f32, (unsigned)(rows * slices), 1024, 0,
+                     a)) != CUCA_OK || slices == 1)
+        return st;
+    return launch(ctx, cuca_topk_merge, (unsigned)rows, 1024, 0, a);
 }
 
 // The rest of sample() after select_top_k (sampler.rs:166-185 and

@@ -116,6 +116,30 @@ def test_top_k(ctx, vocab, k, kind, temperature):
         assert_bits_equal(gl[r, :gc[r]], wl, f"top-k logits row {r}")
 
 
+@pytest.mark.parametrize("kind", ["normal", "ties"])
+def test_many_rows_take_each_row_whole(ctx, kind):
+    """600 rows: one workgroup per row, no slices and no merge launch; a
+    32000-value row fills the workgroup's LDS several times over (rounds of
+    selection that carry the kept candidates forward)."""
+    rng = np.random.default_rng(600 + len(kind))
+    rows, vocab, k = 600, 32000, 50
+    x = logits_rows(rng, rows, vocab, kind)
+    x[7, :] = -np.inf
+    x[8, :200] = np.nan
+    dx = ctx.array(x)
+    ol, oi, oc = ctx.empty((rows, k), np.float32), ctx.empty((rows, k), np.uint32), ctx.empty((rows,), np.int32)
+    ctx.top_k(dx.ptr, vocab, rows, vocab, hip.F32, k, 0.9, ol.ptr, oi.ptr, oc.ptr)
+    ids = ctx.empty((rows,), np.uint32)
+    ctx.argmax(dx.ptr, vocab, rows, vocab, hip.F32, ids.ptr)
+    gl, gi, gc, ga = ol.numpy(), oi.numpy(), oc.numpy(), ids.numpy()
+    for r in range(rows):
+        wl, wi = O.select_top_k(x[r], 0.9, k)
+        assert gc[r] == wl.size, (r, gc[r], wl.size)
+        assert gi[r, :gc[r]].tolist() == wi.tolist(), r
+        assert_bits_equal(gl[r, :gc[r]], wl, f"top-k logits row {r}")
+        assert int(ga[r]) == O.greedy(x[r]), r
+
+
 def test_device_top_k_then_host_finish_is_the_reference_sample(ctx):
     rng = np.random.default_rng(12)
     vocab, rows = 128256, 2
