@@ -563,13 +563,28 @@ template <typename T> __device__ static inline void moe_sum_body(const MoeSumArg
     const int t = (int)(g / nq), q = (int)(g - (int64_t)t * nq);
     const int h0 = 4 * q;
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int i = 0; i < a.n_used; i++) {
-        const int p = a.pairs[(int64_t)t * a.n_used + i];
-        if (p < 0 || p >= a.max_pairs) continue;
-        const float *src = a.scratch + (int64_t)p * a.scratch_ld + h0;
+    // eight pairs at a time: their ids, then their rows, are all loaded
+    // before the sums (in the pairs' order) use them
+    for (int i0 = 0; i0 < a.n_used; i0 += 8) {
+        int p[8];
 #pragma unroll
-        for (int e = 0; e < 4; e++)
-            if (h0 + e < a.n_embd) acc[e] = acc[e] + src[e];
+        for (int j = 0; j < 8; j++) {
+            p[j] = i0 + j < a.n_used ? a.pairs[(int64_t)t * a.n_used + i0 + j] : -1;
+            if (p[j] >= a.max_pairs) p[j] = -1;
+        }
+        float v[8][4];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const float *src = a.scratch + (int64_t)(p[j] < 0 ? 0 : p[j]) * a.scratch_ld + h0;
+#pragma unroll
+            for (int e = 0; e < 4; e++) v[j][e] = (p[j] >= 0 && h0 + e < a.n_embd) ? src[e] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+            if (p[j] >= 0) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[e] = acc[e] + v[j][e];
+            }
     }
     T *dst = reinterpret_cast<T *>(a.out) + (int64_t)t * a.out_ld + h0;
 #pragma unroll

@@ -1340,7 +1340,10 @@ static cuca_status moe_common(cuca_hip_ctx *ctx, const void *w, const void *w_up
     const double mean = (double)max_pairs / (double)n_experts;
     const int mt = mean <= 1.5 ? 1 : mean <= 3.0 ? 2 : 4;
     const int mi = mt == 1 ? 0 : mt == 2 ? 1 : 2;
-    const int64_t ntile = (max_pairs + mt - 1) / mt + n_experts; // >= sum over experts of ceil(n_e / mt)
+    // an upper bound of the tiles, sum over experts of ceil(n_e / mt): at
+    // most min(n_experts, pairs) experts hold pairs, each adding at most
+    // (mt - 1) / mt of a tile to pairs / mt
+    const int64_t ntile = (max_pairs + (mt - 1) * std::min<int64_t>(n_experts, max_pairs)) / mt;
     const int64_t nrb = (n + 15) / 16, nrb8 = (nrb + 7) / 8 * 8;
     if (nrb8 * ntile > 0x7fffffffll) return fail(ctx, CUCA_UNSUPPORTED, "moe: grid too large");
     // [dtype][format][up silu, up gelu, down][tile rows 1, 2, 4]
