@@ -169,16 +169,25 @@ typedef struct {
     int32_t m, nb;
 } Q8ActsArgs;
 
-/* The decode GEMV (qmv.hip) on quantised activations, tiles of MT <= 2
- * activation rows held in LDS for the whole row length; tasks of 4 weight
- * rows per wave.  Epilogue as QmmArgs (GLU, cap). */
+/* The decode GEMV (qmv.hip): tiles of MT <= 4 activation rows held in LDS
+ * for the whole row length, either quantised already (quants / scales) or
+ * quantised by the workgroup from x; tasks of 4 weight rows per wave.
+ * Epilogue as QmmArgs (GLU, cap).  MoE (modes 1 / 2): workgroup (tile,
+ * split) takes tile `tile` of the expert order and row tasks
+ * [split * tps, (split + 1) * tps) of the expert's matrix. */
 typedef struct {
     const uint8_t *w, *w_up;    /* packed weights (gate/up for GLU)          */
-    const int8_t *quants;       /* [m][q_ld]                                 */
-    const float *scales;        /* [m][nb]                                   */
-    void *out;                  /* [m][out_ld]                               */
-    int64_t q_ld, out_ld, row_bytes;
+    const int8_t *quants;       /* mode 0: [m][q_ld]                         */
+    const float *scales;        /* mode 0: [m][nb]                           */
+    const void *x;              /* modes 1-3: activation rows [.][ldx]       */
+    void *out;                  /* [m or pairs][out_ld]                      */
+    const int32_t *offsets;     /* MoE: [n_experts + 1]                      */
+    const int32_t *pair_token;  /* MoE up: [max_pairs]                       */
+    const float *pair_weight;   /* MoE down: [max_pairs]                     */
+    unsigned long long *status;
+    int64_t q_ld, out_ld, row_bytes, ldx, w_estride;
     int32_t rows, m, nb, ng, nbp, ntask;
+    int32_t n_experts, max_pairs, n_tokens, splits, tps;
     float clamp;
     int32_t cap_flags;
     float mul1, mul2, softcap_inv, softcap;

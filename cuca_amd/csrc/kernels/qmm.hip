@@ -384,20 +384,21 @@ __device__ static inline float qmm_hsum(float v) {
 }
 
 // MoE: the expert and pair range of activation tile `tile`.  Expert e has
-// ceil(n_e / MT) tiles, in expert order; a workgroup finds its expert by a
-// prefix sum over the offsets.  Returns false (for the whole workgroup)
-// past the last tile.
+// ceil(n_e / MT) tiles, in expert order; a workgroup (CUCA_BLOCK threads)
+// finds its expert by a prefix sum over the offsets.  Returns false (for the
+// whole workgroup) past the last tile.
 template <int MT>
-__device__ static inline bool qmm_moe_tile(const QmmArgs &a, int tile, int *expert, int *p0, int *p1) {
+__device__ static inline bool moe_tile_lookup(const int32_t *offsets, int n_experts, int max_pairs, int tile,
+                                              int *expert, int *p0, int *p1) {
     __shared__ int sh[CUCA_BLOCK / CUCA_WAVE + 2];
     const int tid = threadIdx.x, wave = tid / CUCA_WAVE, lane = tid % CUCA_WAVE;
     if (tid == 0) { sh[CUCA_BLOCK / CUCA_WAVE] = -1; sh[CUCA_BLOCK / CUCA_WAVE + 1] = 0; }
     int base = 0;
-    for (int e0 = 0; e0 < a.n_experts; e0 += CUCA_BLOCK) {
+    for (int e0 = 0; e0 < n_experts; e0 += CUCA_BLOCK) {
         const int e = e0 + tid;
         int cnt = 0;
-        if (e < a.n_experts) {
-            const int lo = a.offsets[e], hi = a.offsets[e + 1];
+        if (e < n_experts) {
+            const int lo = offsets[e], hi = offsets[e + 1];
             cnt = hi > lo ? (hi - lo + MT - 1) / MT : 0;
         }
         // inclusive scan: within the wave, then over the waves
@@ -425,14 +426,19 @@ __device__ static inline bool qmm_moe_tile(const QmmArgs &a, int tile, int *expe
     const int e = sh[CUCA_BLOCK / CUCA_WAVE];
     if (e < 0) return false;
     const int local = sh[CUCA_BLOCK / CUCA_WAVE + 1];
-    int lo = a.offsets[e] + local * MT;
-    int hi = lo + MT < a.offsets[e + 1] ? lo + MT : a.offsets[e + 1];
-    if (hi > a.max_pairs) hi = a.max_pairs;
+    int lo = offsets[e] + local * MT;
+    int hi = lo + MT < offsets[e + 1] ? lo + MT : offsets[e + 1];
+    if (hi > max_pairs) hi = max_pairs;
     if (lo < 0) lo = 0;
     *expert = e;
     *p0 = lo;
     *p1 = hi;
     return true;
+}
+
+template <int MT>
+__device__ static inline bool qmm_moe_tile(const QmmArgs &a, int tile, int *expert, int *p0, int *p1) {
+    return moe_tile_lookup<MT>(a.offsets, a.n_experts, a.max_pairs, tile, expert, p0, p1);
 }
 
 // MODE 0: dense (x rows j0.., out rows j0..); 1: MoE up (act row of pair p =

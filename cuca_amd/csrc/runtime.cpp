@@ -61,9 +61,6 @@ const char *const kKernelNames[] = {
 
 thread_local std::string g_thread_error;
 
-// The context's scratch for quantised activations: two rows of up to
-// 16384 values (quants, then f32 block scales), rounded up.
-constexpr size_t kQScratchBytes = 64 << 10;
 // The context's scratch for the slices' results of argmax / top-k.
 constexpr size_t kPickScratchBytes = 4 << 20;
 
@@ -82,11 +79,8 @@ struct cuca_hip_ctx {
     int64_t last_kv_blocks = 0;   // the pool size of the last K/V store (for messages)
     int64_t last_table_rows = 0;
     int64_t last_moe_tokens = 0;  // the activation rows of the last MoE up call
-    // device scratch for the quantised activations of a decode GEMV that
-    // cuca_hip_qmm / _qmm_glu / _lm_head route through cuca_q8_acts + qmv
-    // (allocated with the context: ops never allocate)
-    void *qscratch = nullptr;
     // device scratch for the per-slice results of cuca_hip_argmax / _top_k
+    // (allocated with the context: ops never allocate)
     void *pscratch = nullptr;
     int cu_count = 256;
     std::string error;
@@ -208,9 +202,6 @@ cuca_status cuca_hip_ctx_create(int device, cuca_hip_ctx **out) {
         }
         if (st != CUCA_OK) break;
         ctx->cu_count = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
-        if ((e = hipMalloc(&ctx->qscratch, kQScratchBytes)) != hipSuccess) {
-            st = hip_fail(ctx, e, "hipMalloc(activation scratch)"); break;
-        }
         if ((e = hipMalloc(&ctx->pscratch, kPickScratchBytes)) != hipSuccess) {
             st = hip_fail(ctx, e, "hipMalloc(selection scratch)"); break;
         }
@@ -248,7 +239,6 @@ void cuca_hip_ctx_destroy(cuca_hip_ctx *ctx) {
         (void)hipEventDestroy(r.stop);
     }
     if (ctx->status) (void)hipFree(ctx->status);
-    if (ctx->qscratch) (void)hipFree(ctx->qscratch);
     if (ctx->pscratch) (void)hipFree(ctx->pscratch);
     if (ctx->module) (void)hipModuleUnload(ctx->module);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
@@ -912,7 +902,7 @@ struct LogitCap {
 // LDS of a qmv workgroup (qmv.hip QMV_LDS_BYTES) for MT rows, nbp padded
 // blocks of groups of G; the kernel is used when it fits in 64 KiB.
 static size_t qmv_lds(int64_t mt, int64_t nbp, int g) {
-    return (size_t)(mt * 16 * (nbp + 2) * 8 + mt * nbp * 4 + 4 * mt * 2 * 4 * g * 4);
+    return (size_t)(mt * 16 * (nbp + 2) * 8 + mt * nbp * 4 + 4 * mt * 2 * 4 * g * 4 + 4 * 32 * mt * 2 * 4 * 4);
 }
 static bool qmv_fits(int64_t m, int64_t nbp, int g) {
     return m >= 1 && m <= 2 && qmv_lds(m, nbp, g) <= (64u << 10);
@@ -940,12 +930,12 @@ static cuca_status q8_acts_launch(cuca_hip_ctx *ctx, const void *x, int64_t ldx,
                   CUCA_BLOCK_THREADS, 0, a);
 }
 
-// The decode GEMV on quantised activations (m <= 2, qmv_fits checked).
-// glu: 0 plain, 1 SiLU, 2 GELU-tanh.
-static cuca_status qmv_launch(cuca_hip_ctx *ctx, const void *w, const void *w_up, uint32_t ggml_type, int64_t n,
-                              int64_t k, const int8_t *quants, int64_t q_ld, const float *scales, int64_t m,
-                              int64_t rows, int glu, float clamp, void *out, int64_t out_ld, cuca_dtype dtype,
-                              const LogitCap &cap);
+// The decode GEMV (m <= 2, qmv_fits checked): mode 0 on quantised rows
+// (quants, scales), mode 3 on the rows of x.  glu: 0 plain, 1 SiLU, 2 GELU-tanh.
+static cuca_status qmv_launch(cuca_hip_ctx *ctx, int mode, const void *w, const void *w_up, uint32_t ggml_type,
+                              int64_t n, int64_t k, const int8_t *quants, int64_t q_ld, const float *scales,
+                              const void *x, int64_t ldx, int64_t m, int64_t rows, int glu, float clamp, void *out,
+                              int64_t out_ld, cuca_dtype dtype, const LogitCap &cap);
 
 // glu: 0 plain, 1 SiLU, 2 GELU-tanh
 static cuca_status qmm_common(cuca_hip_ctx *ctx, const void *w, const void *w_up, uint32_t ggml_type,
@@ -976,14 +966,11 @@ static cuca_status qmm_common(cuca_hip_ctx *ctx, const void *w, const void *w_up
     if (!al16(x) || ((size_t)ldx * es) % 16 != 0)
         return fail(ctx, CUCA_INVALID_ARG, "qmm: activation rows must start 16-byte aligned");
     const int64_t nb = k / 32, ng = (nb + g - 1) / g;
-    // one or two rows of a tall matrix whose tile fits the LDS: quantise
-    // once into the context's scratch, then the decode GEMV
-    if (m <= 2 && qmv_wins(ctx, rows) && qmv_fits(m, ng * g, g) && (size_t)m * (size_t)k + (size_t)m * (size_t)nb * 4 + 16 <= kQScratchBytes) {
-        int8_t *q = static_cast<int8_t *>(ctx->qscratch);
-        float *sc = reinterpret_cast<float *>(q + ((size_t)m * (size_t)k + 15) / 16 * 16);
-        if ((st = q8_acts_launch(ctx, x, ldx, m, k, dtype, q, k, sc)) != CUCA_OK) return st;
-        return qmv_launch(ctx, w, w_up, ggml_type, n, k, q, k, sc, m, rows, glu, clamp, out, out_ld, dtype, cap);
-    }
+    // one or two rows whose tile fits the LDS: the decode GEMV, each
+    // workgroup quantising the rows itself
+    if (m <= 2 && qmv_wins(ctx, rows) && qmv_fits(m, ng * g, g))
+        return qmv_launch(ctx, 3, w, w_up, ggml_type, n, k, nullptr, 0, nullptr, x, ldx, m, rows, glu, clamp, out,
+                          out_ld, dtype, cap);
     const int mt = m == 1 ? 1 : m == 2 ? 2 : 4;
     const int mi = mt == 1 ? 0 : mt == 2 ? 1 : 2;
     const int64_t ntile = (m + mt - 1) / mt;
@@ -1192,10 +1179,10 @@ cuca_status cuca_hip_qmm_glu(cuca_hip_ctx *ctx, const void *gate, const void *up
                       out, out_ld, dtype);
 }
 
-static cuca_status qmv_launch(cuca_hip_ctx *ctx, const void *w, const void *w_up, uint32_t ggml_type, int64_t n,
-                              int64_t k, const int8_t *quants, int64_t q_ld, const float *scales, int64_t m,
-                              int64_t rows, int glu, float clamp, void *out, int64_t out_ld, cuca_dtype dtype,
-                              const LogitCap &cap) {
+static cuca_status qmv_launch(cuca_hip_ctx *ctx, int mode, const void *w, const void *w_up, uint32_t ggml_type,
+                              int64_t n, int64_t k, const int8_t *quants, int64_t q_ld, const float *scales,
+                              const void *x, int64_t ldx, int64_t m, int64_t rows, int glu, float clamp, void *out,
+                              int64_t out_ld, cuca_dtype dtype, const LogitCap &cap) {
     int g = 0, gb = 0;
     qfmt(ggml_type, &g, &gb);
     const int64_t nb = k / 32, ng = (nb + g - 1) / g, nbp = ng * g;
@@ -1203,28 +1190,42 @@ static cuca_status qmv_launch(cuca_hip_ctx *ctx, const void *w, const void *w_up
     int64_t grid = (ntask + 3) / 4;
     const int64_t cap_wg = (int64_t)ctx->cu_count * 4; // persistent beyond four workgroups per CU
     if (grid > cap_wg) grid = cap_wg;
-    // [dtype][format][plain, silu, gelu][rows 1, 2]
-    static const Kernel table_k[2][2][3][2] = {
-        {{{cuca_qmv_q4_0_m1_f32, cuca_qmv_q4_0_m2_f32},
-          {cuca_qmv_glu_q4_0_silu_m1_f32, cuca_qmv_glu_q4_0_silu_m2_f32},
-          {cuca_qmv_glu_q4_0_gelu_m1_f32, cuca_qmv_glu_q4_0_gelu_m2_f32}},
-         {{cuca_qmv_q8_0_m1_f32, cuca_qmv_q8_0_m2_f32},
-          {cuca_qmv_glu_q8_0_silu_m1_f32, cuca_qmv_glu_q8_0_silu_m2_f32},
-          {cuca_qmv_glu_q8_0_gelu_m1_f32, cuca_qmv_glu_q8_0_gelu_m2_f32}}},
-        {{{cuca_qmv_q4_0_m1_f16, cuca_qmv_q4_0_m2_f16},
-          {cuca_qmv_glu_q4_0_silu_m1_f16, cuca_qmv_glu_q4_0_silu_m2_f16},
-          {cuca_qmv_glu_q4_0_gelu_m1_f16, cuca_qmv_glu_q4_0_gelu_m2_f16}},
-         {{cuca_qmv_q8_0_m1_f16, cuca_qmv_q8_0_m2_f16},
-          {cuca_qmv_glu_q8_0_silu_m1_f16, cuca_qmv_glu_q8_0_silu_m2_f16},
-          {cuca_qmv_glu_q8_0_gelu_m1_f16, cuca_qmv_glu_q8_0_gelu_m2_f16}}}};
-    const Kernel kk = table_k[dtype == CUCA_F16][ggml_type == CUCA_GGML_Q8_0][glu][m == 2];
+    // [rows of x][dtype][format][plain, silu, gelu][rows 1, 2]
+    static const Kernel table_k[2][2][2][3][2] = {
+        {{{{cuca_qmv_q4_0_m1_f32, cuca_qmv_q4_0_m2_f32},
+           {cuca_qmv_glu_q4_0_silu_m1_f32, cuca_qmv_glu_q4_0_silu_m2_f32},
+           {cuca_qmv_glu_q4_0_gelu_m1_f32, cuca_qmv_glu_q4_0_gelu_m2_f32}},
+          {{cuca_qmv_q8_0_m1_f32, cuca_qmv_q8_0_m2_f32},
+           {cuca_qmv_glu_q8_0_silu_m1_f32, cuca_qmv_glu_q8_0_silu_m2_f32},
+           {cuca_qmv_glu_q8_0_gelu_m1_f32, cuca_qmv_glu_q8_0_gelu_m2_f32}}},
+         {{{cuca_qmv_q4_0_m1_f16, cuca_qmv_q4_0_m2_f16},
+           {cuca_qmv_glu_q4_0_silu_m1_f16, cuca_qmv_glu_q4_0_silu_m2_f16},
+           {cuca_qmv_glu_q4_0_gelu_m1_f16, cuca_qmv_glu_q4_0_gelu_m2_f16}},
+          {{cuca_qmv_q8_0_m1_f16, cuca_qmv_q8_0_m2_f16},
+           {cuca_qmv_glu_q8_0_silu_m1_f16, cuca_qmv_glu_q8_0_silu_m2_f16},
+           {cuca_qmv_glu_q8_0_gelu_m1_f16, cuca_qmv_glu_q8_0_gelu_m2_f16}}}},
+        {{{{cuca_qmvx_q4_0_m1_f32, cuca_qmvx_q4_0_m2_f32},
+           {cuca_qmvx_glu_q4_0_silu_m1_f32, cuca_qmvx_glu_q4_0_silu_m2_f32},
+           {cuca_qmvx_glu_q4_0_gelu_m1_f32, cuca_qmvx_glu_q4_0_gelu_m2_f32}},
+          {{cuca_qmvx_q8_0_m1_f32, cuca_qmvx_q8_0_m2_f32},
+           {cuca_qmvx_glu_q8_0_silu_m1_f32, cuca_qmvx_glu_q8_0_silu_m2_f32},
+           {cuca_qmvx_glu_q8_0_gelu_m1_f32, cuca_qmvx_glu_q8_0_gelu_m2_f32}}},
+         {{{cuca_qmvx_q4_0_m1_f16, cuca_qmvx_q4_0_m2_f16},
+           {cuca_qmvx_glu_q4_0_silu_m1_f16, cuca_qmvx_glu_q4_0_silu_m2_f16},
+           {cuca_qmvx_glu_q4_0_gelu_m1_f16, cuca_qmvx_glu_q4_0_gelu_m2_f16}},
+          {{cuca_qmvx_q8_0_m1_f16, cuca_qmvx_q8_0_m2_f16},
+           {cuca_qmvx_glu_q8_0_silu_m1_f16, cuca_qmvx_glu_q8_0_silu_m2_f16},
+           {cuca_qmvx_glu_q8_0_gelu_m1_f16, cuca_qmvx_glu_q8_0_gelu_m2_f16}}}}};
+    const Kernel kk = table_k[mode == 3][dtype == CUCA_F16][ggml_type == CUCA_GGML_Q8_0][glu][m == 2];
     QmvArgs a{};
     a.w = static_cast<const uint8_t *>(w);
     a.w_up = static_cast<const uint8_t *>(w_up);
     a.quants = quants;
     a.scales = scales;
+    a.x = x;
     a.out = out;
     a.q_ld = q_ld;
+    a.ldx = ldx;
     a.out_ld = out_ld;
     a.row_bytes = ng * gb;
     a.rows = (int32_t)rows;
@@ -1280,8 +1281,8 @@ static cuca_status qmv_common(cuca_hip_ctx *ctx, const void *w, const void *w_up
                     "cuca_hip_qmm takes any)", (long long)m, (long long)k);
     if (!w || !quants || !scales || !out || (glu && !w_up)) return fail(ctx, CUCA_INVALID_ARG, "null pointer");
     if (!al16(w) || (w_up && !al16(w_up))) return fail(ctx, CUCA_INVALID_ARG, "packed weights must be 16-byte aligned");
-    return qmv_launch(ctx, w, w_up, ggml_type, n, k, quants, k, scales, m, rows, glu, clamp, out, out_ld, dtype,
-                      LogitCap());
+    return qmv_launch(ctx, 0, w, w_up, ggml_type, n, k, quants, k, scales, nullptr, 0, m, rows, glu, clamp, out,
+                      out_ld, dtype, LogitCap());
 }
 
 cuca_status cuca_hip_qmv(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type, int64_t n, int64_t k,
@@ -1344,6 +1345,61 @@ static cuca_status moe_common(cuca_hip_ctx *ctx, const void *w, const void *w_up
     // most min(n_experts, pairs) experts hold pairs, each adding at most
     // (mt - 1) / mt of a tile to pairs / mt
     const int64_t ntile = (max_pairs + (mt - 1) * std::min<int64_t>(n_experts, max_pairs)) / mt;
+    // the decode GEMV, a workgroup per (tile, split of the expert's rows),
+    // when the tile's rows fit its LDS, from two tokens' pairs up (16 pairs
+    // over 128 experts; measured at Qwen3-30B-A3B's shapes: 34 vs 36 us at
+    // two tokens, 159 vs 448 us at 32); a single token's pairs keep the
+    // one-pass kernel (25 vs 30 us)
+    if (16 * max_pairs > n_experts && qmv_lds(mt, ng * g, g) <= (64u << 10)) {
+        const int64_t ntask = (n + 3) / 4;
+        int64_t splits = std::max<int64_t>(1, ((int64_t)ctx->cu_count * 4 + ntile - 1) / ntile);
+        splits = std::min<int64_t>(splits, (ntask + 3) / 4);
+        const int64_t tps = ((ntask + splits - 1) / splits + 3) / 4 * 4;
+        splits = (ntask + tps - 1) / tps;
+        if (ntile * splits > 0x7fffffffll) return fail(ctx, CUCA_UNSUPPORTED, "moe: grid too large");
+        // [dtype][format][up silu, up gelu, down][tile rows 1, 2, 4]
+        static const Kernel table_v[2][2][3][3] = {
+            {{{cuca_qmv_moe_up_q4_0_silu_m1_f32, cuca_qmv_moe_up_q4_0_silu_m2_f32, cuca_qmv_moe_up_q4_0_silu_m4_f32},
+              {cuca_qmv_moe_up_q4_0_gelu_m1_f32, cuca_qmv_moe_up_q4_0_gelu_m2_f32, cuca_qmv_moe_up_q4_0_gelu_m4_f32},
+              {cuca_qmv_moe_down_q4_0_m1_f32, cuca_qmv_moe_down_q4_0_m2_f32, cuca_qmv_moe_down_q4_0_m4_f32}},
+             {{cuca_qmv_moe_up_q8_0_silu_m1_f32, cuca_qmv_moe_up_q8_0_silu_m2_f32, cuca_qmv_moe_up_q8_0_silu_m4_f32},
+              {cuca_qmv_moe_up_q8_0_gelu_m1_f32, cuca_qmv_moe_up_q8_0_gelu_m2_f32, cuca_qmv_moe_up_q8_0_gelu_m4_f32},
+              {cuca_qmv_moe_down_q8_0_m1_f32, cuca_qmv_moe_down_q8_0_m2_f32, cuca_qmv_moe_down_q8_0_m4_f32}}},
+            {{{cuca_qmv_moe_up_q4_0_silu_m1_f16, cuca_qmv_moe_up_q4_0_silu_m2_f16, cuca_qmv_moe_up_q4_0_silu_m4_f16},
+              {cuca_qmv_moe_up_q4_0_gelu_m1_f16, cuca_qmv_moe_up_q4_0_gelu_m2_f16, cuca_qmv_moe_up_q4_0_gelu_m4_f16},
+              {cuca_qmv_moe_down_q4_0_m1_f16, cuca_qmv_moe_down_q4_0_m2_f16, cuca_qmv_moe_down_q4_0_m4_f16}},
+             {{cuca_qmv_moe_up_q8_0_silu_m1_f16, cuca_qmv_moe_up_q8_0_silu_m2_f16, cuca_qmv_moe_up_q8_0_silu_m4_f16},
+              {cuca_qmv_moe_up_q8_0_gelu_m1_f16, cuca_qmv_moe_up_q8_0_gelu_m2_f16, cuca_qmv_moe_up_q8_0_gelu_m4_f16},
+              {cuca_qmv_moe_down_q8_0_m1_f16, cuca_qmv_moe_down_q8_0_m2_f16, cuca_qmv_moe_down_q8_0_m4_f16}}}};
+        QmvArgs v{};
+        v.w = static_cast<const uint8_t *>(w);
+        v.w_up = static_cast<const uint8_t *>(w_up);
+        v.x = x;
+        v.out = out;
+        v.offsets = offsets;
+        v.pair_token = pair_token;
+        v.pair_weight = pair_weight;
+        v.status = ctx->status;
+        v.ldx = ldx;
+        v.out_ld = out_ld;
+        v.w_estride = estride;
+        v.row_bytes = ng * gb;
+        v.rows = (int32_t)n;
+        v.m = mt;
+        v.nb = (int32_t)nb;
+        v.ng = (int32_t)ng;
+        v.nbp = (int32_t)(ng * g);
+        v.ntask = (int32_t)ntask;
+        v.n_experts = n_experts;
+        v.max_pairs = (int32_t)max_pairs;
+        v.n_tokens = (int32_t)(up ? n_tokens : max_pairs);
+        v.splits = (int32_t)splits;
+        v.tps = (int32_t)tps;
+        v.clamp = clamp > 0.0f ? clamp : 0.0f;
+        if (up) ctx->last_moe_tokens = n_tokens;
+        return launch(ctx, table_v[dtype == CUCA_F16][ggml_type == CUCA_GGML_Q8_0][up ? up - 1 : 2][mi],
+                      (unsigned)(ntile * splits), CUCA_BLOCK_THREADS, (unsigned)qmv_lds(mt, ng * g, g), v);
+    }
     const int64_t nrb = (n + 15) / 16, nrb8 = (nrb + 7) / 8 * 8;
     if (nrb8 * ntile > 0x7fffffffll) return fail(ctx, CUCA_UNSUPPORTED, "moe: grid too large");
     // [dtype][format][up silu, up gelu, down][tile rows 1, 2, 4]

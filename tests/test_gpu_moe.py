@@ -15,7 +15,9 @@ Bars:
   activation's last-bit differences can move a Q8_0 quant of the hidden row;
   f16 activations round the hidden rows to f16 (the reference is f32
   throughout), checked to 1e-2 as a sanity bound only.
-Covers Q4_0 / Q8_0, f32 / f16, SiLU / GELU-tanh, experts with no pairs,
+Covers Q4_0 / Q8_0, f32 / f16, SiLU / GELU-tanh, both kernels (the decode
+GEMV, and the one-pass kernel for rows too long for its LDS: hidden 8192),
+experts with no pairs,
 Zipf(1.1) routing over 128 experts at the Qwen3-30B-A3B shapes (decode
 batch 64, top 8), and a pair token outside the rows (reported, skipped).
 """
@@ -65,13 +67,16 @@ def glu_floor(g, u, act):
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
 @pytest.mark.parametrize("act", [hip.ACT_SILU, hip.ACT_GELU_TANH])
 @pytest.mark.parametrize("t,n_experts,n_used,n_embd,ff", [(10, 8, 3, 128, 96), (3, 16, 2, 256, 64),
-                                                         (40, 6, 2, 64, 160)])
+                                                         (40, 6, 2, 64, 160), (40, 6, 2, 8192, 96),
+                                                         (1, 64, 2, 128, 96)])
 def test_moe_layer(ctx, qtype, dtype, act, t, n_experts, n_used, n_embd, ff):
     rng = np.random.default_rng(t * 100 + n_experts + ff + act)
     experts, eb = bank(ctx, rng, qtype, n_experts, n_embd, ff)
     per = routing(rng, t, n_experts, n_used)
     npd = np.float16 if dtype == "f16" else np.float32
-    x = rng.standard_normal((t, n_embd)).astype(npd)
+    # activations shrink with the row length, so that the hidden rows (gate
+    # and up sums over n_embd values) stay within f16's range
+    x = (rng.standard_normal((t, n_embd)) * min(1.0, np.sqrt(256.0 / n_embd))).astype(npd)
     glu = ops.Glu(act)
     out, hidden, scratch = eb.expert_sum(ctx.array(x), per, glu, n_used)
     want, want_hidden = O.expert_sum(x, experts, QT[qtype], per, act)
@@ -156,14 +161,17 @@ def test_qwen3_30b_a3b_shapes_zipf_routing(ctx):
     assert np.all(np.abs(got.astype(np.float64) - want) <= 1e-4 * scale)
 
 
-def test_a_pair_token_outside_the_rows_is_reported(ctx):
+@pytest.mark.parametrize("n_experts", [4, 128])
+def test_a_pair_token_outside_the_rows_is_reported(ctx, n_experts):
+    """On both kernels: the decode GEMV (4 pairs over 4 experts) and the
+    one-pass kernel (4 pairs over 128 experts)."""
     rng = np.random.default_rng(9)
-    experts, eb = bank(ctx, rng, "q8_0", 4, 64, 32)
+    experts, eb = bank(ctx, rng, "q8_0", n_experts, 64, 32)
     x = ctx.array(rng.standard_normal((5, 64)).astype(np.float32))
-    offsets = ctx.array(np.array([0, 2, 2, 3, 4], np.int32))
+    offsets = ctx.array(np.array([0, 2, 2, 3] + [4] * (n_experts - 3), np.int32))  # n_experts + 1
     tok = ctx.array(np.array([0, 7, 1, 4], np.int32))
     hidden = ctx.empty((4, 32), np.float32)
-    ctx.moe_up(eb.gate.ptr, eb.up.ptr, eb.stride_gu, hip.GGML_Q8_0, 32, 64, 4, x.ptr, 64, 5,
+    ctx.moe_up(eb.gate.ptr, eb.up.ptr, eb.stride_gu, hip.GGML_Q8_0, 32, 64, n_experts, x.ptr, 64, 5,
                offsets.ptr, tok.ptr, 4, hip.ACT_SILU, 0.0, hidden.ptr, 32, hip.F32)
     with pytest.raises(hip.CucaError, match=r"routed token \(7\) outside the 5 rows"):
         ctx.check_device()

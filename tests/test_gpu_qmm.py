@@ -290,3 +290,23 @@ def test_decode_gemv_waves_that_run_several_tasks(ctx, qtype, glu):
         assert_close(got, O.glu(g, u, hip.ACT_SILU), what="several tasks, glu")
     else:
         assert_bits_equal(w.forward(dx).numpy(), want_out(raw, qtype, n, k, x, n, "f32"), "several tasks")
+
+
+@pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
+def test_decode_gemv_streams_chunks_of_tasks(ctx, qtype):
+    """600000 rows of 64 values: more than 32 four-row tasks per wave of the
+    persistent grid, so a wave streams several chunks of tasks (sums staged
+    in LDS, written per chunk); through the quantised rows (cuca_hip_qmv)
+    and through qmm's routing (the rows of x)."""
+    rng = np.random.default_rng(600000)
+    n, k = 600000, 64
+    raw, w = weight(ctx, rng, qtype, n, k)
+    x = awkward(rng, 2, k, 1.0, huge=100.0)
+    dx = ctx.array(x)
+    want = want_out(raw, qtype, n, k, x, n, "f32")
+    assert_bits_equal(w.forward(dx).numpy(), want, "streamed chunks, rows of x")
+    q, s = ctx.empty((2, k), np.int8), ctx.empty((2, k // 32), np.float32)
+    ctx.q8_acts(dx.ptr, k, 2, k, hip.F32, q.ptr, s.ptr)
+    out = ctx.empty((2, n), np.float32)
+    ctx.qmv(w.packed.ptr, QT[qtype], n, k, q.ptr, s.ptr, 2, n, out.ptr, n, hip.F32)
+    assert_bits_equal(out.numpy(), want, "streamed chunks, quantised rows")
