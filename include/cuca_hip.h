@@ -361,10 +361,13 @@ cuca_status cuca_hip_top_k(cuca_hip_ctx *ctx, const void *logits, int64_t ld, in
  *   -> quants int8 [m][k] (element order) and scales f32 [m][k/32] (the
  *   f16-rounded block scales); quants 16-byte aligned, k a multiple of 32.
  * cuca_hip_qmv / cuca_hip_qmv_glu: cuca_hip_qmm / _qmm_glu on those, the
- *   same bits, for m = 1 or 2 rows whose row length fits the kernel (up to
- *   about 15000 values for one row; CUCA_UNSUPPORTED otherwise).
- * cuca_hip_qmm, _qmm_glu and _lm_head take this path by themselves for one
- * or two rows, quantising into a small scratch the context owns. */
+ *   same bits, for m = 1 or 2 rows whose row length fits the kernel's LDS
+ *   (up to 14336 values for one row, 6144 for two; CUCA_UNSUPPORTED
+ *   otherwise).
+ * cuca_hip_qmm, _qmm_glu and _lm_head use the same kernel by themselves for
+ * one or two rows of a tall matrix (at least 32 four-row tasks per CU: the
+ * LM head), each workgroup quantising the rows itself; the MoE calls use it
+ * from two tokens' pairs up. */
 cuca_status cuca_hip_q8_acts(cuca_hip_ctx *ctx, const void *x, int64_t ldx, int64_t m, int64_t k, cuca_dtype dtype,
                              int8_t *quants, float *scales);
 cuca_status cuca_hip_qmv(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type, int64_t n, int64_t k,
