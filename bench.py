@@ -527,6 +527,155 @@ class DecodeLayersAttn(DecodeLayers):
                           eps, 1.0, n, H, self.x.data_ptr(), self.h.data_ptr(), hip.F32)
 
 
+class DecodeStep:
+    """A whole decode step of the 8B model at batch n (config B shapes:
+    hidden 4096, 32 query / 8 K/V heads of 128, FFN 14336, vocab 128256),
+    f32 activations, every op a kernel of this library:
+      embed (Q8_0 table) ->
+      32 layers of [residual + attention RMSNorm, Q and fused K|V
+        projections (qmm), RoPE + paged K/V store of the new token, paged
+        decode attention over ctx_len keys, o projection, residual + FFN
+        RMSNorm, gate/up projections with SwiGLU (qmm_glu), down projection]
+      -> residual + final RMSNorm -> LM head (Q8_0) -> argmax.
+    Layer weights are Q4_0 (or `qtype`), 32 distinct layers (3.9 GB Q4_0),
+    generated as GGUF bytes on the device and packed once; the K/V pools
+    hold ctx_len keys per sequence in consecutive blocks."""
+
+    def __init__(self, ctx, torch, n, ctx_len, qtype="q4_0", layers=32, seed=3):
+        import numpy as np
+        from cuca_amd import hip
+        from cuca_amd import workloads as W
+        cfg = W.CONFIGS["B"]
+        self.hip, self.ctx, self.torch, self.n, self.cfg, self.layers = hip, ctx, torch, n, cfg, layers
+        H, F, d, nq, nk = cfg["hidden"], cfg["ff"], cfg["head_dim"], cfg["nq"], cfg["nk"]
+        self.vocab = cfg["vocab"]
+        dev = "cuda"
+        gen = torch.Generator(device=dev).manual_seed(seed)
+        T = W.GGML_ID[qtype]
+        self.T = T
+
+        def packed(rows, cols, qt, d_range):
+            raw = W.quant_table_torch(gen, rows, cols, qt, d_range)
+            out = torch.empty(hip.qweight_bytes(W.GGML_ID[qt], rows, cols), dtype=torch.uint8, device=dev)
+            ctx.qweight_pack(raw.data_ptr(), W.GGML_ID[qt], rows, cols, out.data_ptr())
+            torch.cuda.synchronize()
+            del raw
+            return out
+
+        def r(*shape):
+            return torch.randn(shape, device=dev, generator=gen)
+        self.table = W.quant_table_torch(gen, self.vocab, H, "q8_0", cfg["d_range"])
+        self.head = packed(self.vocab, H, "q8_0", (0.001, 0.02))
+        nb_row = (ctx_len + 15) // 16
+        self.n_blocks = n * nb_row
+        self.L = []
+        for _ in range(layers):
+            self.L.append(dict(
+                wq=packed(nq * d, H, qtype, (0.001, 0.01)), wkv=packed(2 * nk * d, H, qtype, (0.001, 0.01)),
+                wo=packed(H, nq * d, qtype, (0.001, 0.01)), wg=packed(F, H, qtype, (0.001, 0.01)),
+                wu=packed(F, H, qtype, (0.001, 0.01)), wd=packed(H, F, qtype, (0.0005, 0.005)),
+                n1=1 + 0.02 * r(H), n2=1 + 0.02 * r(H),
+                pk=r(self.n_blocks, nk, 16, d), pv=r(self.n_blocks, nk, 16, d)))
+        self.nout = 1 + 0.02 * r(H)
+        self.ids = torch.randint(0, self.vocab, (n,), device=dev, generator=gen, dtype=torch.int32)
+        self.x, self.h, self.ffn = r(n, H), r(n, H), r(n, H)
+        self.q, self.kv, self.o, self.attn = r(n, nq * d), r(n, 2 * nk * d), r(n, nq * d), r(n, H)
+        self.act = r(n, F)
+        self.logits = torch.empty((n, self.vocab), device=dev)
+        self.out_ids = torch.empty((n,), device=dev, dtype=torch.int32)
+        cos, sin = hip.rope_tables(hip.ROPE_NORM, d, cfg["theta"], 8192)
+        self.cos, self.sin = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
+        tables = np.arange(self.n_blocks, dtype=np.int32).reshape(n, nb_row)
+        self.tables = torch.from_numpy(tables).to(dev)
+        self.max_blocks = nb_row
+        self.pos = torch.from_numpy(np.full(n, ctx_len - 1, np.int32)).to(dev)
+        slots = np.concatenate([hip.kv_slots(tables[i].astype(np.uint32), ctx_len - 1, 1, self.n_blocks)
+                                for i in range(n)])
+        self.slots = torch.from_numpy(slots).to(dev)
+        self.ranges = torch.from_numpy(np.tile(np.array([0, ctx_len], np.int32), (n, 1))).to(dev)
+        self.ws_bytes = hip.paged_decode_workspace(n, nq, d, nb_row)
+        self.ws = torch.empty(max(self.ws_bytes, 16), dtype=torch.uint8, device=dev)
+        self.scale = 1.0 / float(np.sqrt(d))
+        self.weight_bytes = sum(t.numel() for l in self.L for t in (l["wq"], l["wkv"], l["wo"], l["wg"],
+                                                                      l["wu"], l["wd"]))
+
+    def issue_layers(self):
+        c, hip, cfg, n, T = self.ctx, self.hip, self.cfg, self.n, self.T
+        H, F, d, nq, nk, eps = cfg["hidden"], cfg["ff"], cfg["head_dim"], cfg["nq"], cfg["nk"], cfg["eps"]
+        f32 = hip.F32
+        for l in self.L:
+            c.add_rmsnorm(self.x.data_ptr(), self.ffn.data_ptr(), l["n1"].data_ptr(), None, eps, eps, 1.0,
+                          n, H, self.x.data_ptr(), self.h.data_ptr(), f32)
+            c.qmm(l["wq"].data_ptr(), T, nq * d, H, self.h.data_ptr(), H, n, nq * d, self.q.data_ptr(),
+                  nq * d, f32)
+            c.qmm(l["wkv"].data_ptr(), T, 2 * nk * d, H, self.h.data_ptr(), H, n, 2 * nk * d,
+                  self.kv.data_ptr(), 2 * nk * d, f32)
+            c.rope_store_kv(self.q.data_ptr(), nq * d, self.kv.data_ptr(), 2 * nk * d,
+                            self.kv.data_ptr() + 4 * nk * d, 2 * nk * d, n, nq, nk, d, d, hip.ROPE_NORM,
+                            self.cos.data_ptr(), self.sin.data_ptr(), 8192, self.pos.data_ptr(), None, None,
+                            0, eps, l["pk"].data_ptr(), l["pv"].data_ptr(), self.n_blocks,
+                            self.slots.data_ptr(), f32)
+            c.paged_decode(self.q.data_ptr(), l["pk"].data_ptr(), l["pv"].data_ptr(), self.n_blocks,
+                           self.tables.data_ptr(), self.max_blocks, self.ranges.data_ptr(), n, nq, nk, d,
+                           self.scale, self.ws.data_ptr(), self.ws_bytes, self.o.data_ptr(), f32)
+            c.qmm(l["wo"].data_ptr(), T, H, nq * d, self.o.data_ptr(), nq * d, n, H, self.attn.data_ptr(),
+                  H, f32)
+            c.add_rmsnorm(self.x.data_ptr(), self.attn.data_ptr(), l["n2"].data_ptr(), None, eps, eps, 1.0,
+                          n, H, self.x.data_ptr(), self.h.data_ptr(), f32)
+            c.qmm_glu(l["wg"].data_ptr(), l["wu"].data_ptr(), T, F, H, self.h.data_ptr(), H, n,
+                      hip.ACT_SILU, 0.0, self.act.data_ptr(), F, f32)
+            c.qmm(l["wd"].data_ptr(), T, H, F, self.act.data_ptr(), F, n, H, self.ffn.data_ptr(), H, f32)
+
+    def issue_step(self):
+        c, hip, cfg, n = self.ctx, self.hip, self.cfg, self.n
+        H, eps = cfg["hidden"], cfg["eps"]
+        c.embed_gguf(self.table.data_ptr(), hip.GGML_Q8_0, self.vocab, H, self.out_ids.data_ptr(), n, 1.0,
+                     self.x.data_ptr(), hip.F32)
+        self.issue_layers()
+        c.add_rmsnorm(self.x.data_ptr(), self.ffn.data_ptr(), self.nout.data_ptr(), None, eps, eps, 1.0, n,
+                      H, self.x.data_ptr(), self.h.data_ptr(), hip.F32)
+        c.lm_head(self.head.data_ptr(), hip.GGML_Q8_0, self.vocab, H, self.h.data_ptr(), H, n, self.vocab,
+                  1.0, 1.0, 0.0, self.logits.data_ptr(), self.vocab, hip.F32)
+        c.argmax(self.logits.data_ptr(), self.vocab, n, self.vocab, hip.F32, self.out_ids.data_ptr())
+
+
+def decode_step_bench(ctx, torch, n, ctx_len, replays=10):
+    """DecodeStep's 32 layers and its whole step, each captured in one
+    hipGraph and replayed: microseconds per layer, per step, and tokens/s
+    (n tokens per step).  Checked: the step's ids are the argmax of its own
+    logits, and the logits are finite."""
+    import numpy as np
+    ds = DecodeStep(ctx, torch, n, ctx_len)
+    ds.out_ids.copy_(ds.ids)
+    torch.cuda.synchronize()
+    ds.issue_step()  # eager, once
+    torch.cuda.synchronize()
+    ctx.check_device()
+    ctx.graph_begin()
+    ds.issue_layers()
+    gl = ctx.graph_end()
+    layers_ms = time_steps(torch, gl.launch, replays, 2)
+    gl.destroy()
+    ctx.graph_begin()
+    ds.issue_step()
+    gs = ctx.graph_end()
+    step_ms = time_steps(torch, gs.launch, replays, 2)
+    gs.launch()
+    torch.cuda.synchronize()
+    gs.destroy()
+    lg = ds.logits.cpu().numpy()
+    got = ds.out_ids.cpu().numpy()
+    assert np.all(np.isfinite(lg)), "decode step: non-finite logits"
+    assert got.tolist() == [int(np.argmax(lg[i])) for i in range(n)], "decode step: ids"
+    wb = ds.weight_bytes
+    del ds
+    torch.cuda.empty_cache()
+    return dict(batch=n, ctx_len=ctx_len, layer_weights="q4_0", head="q8_0",
+                us_per_layer=round(layers_ms * 1000 / 32, 2), us_per_step=round(step_ms * 1000, 1),
+                tokens_per_s=round(n / (step_ms / 1e3), 1),
+                layer_weight_gbs=round(wb / (layers_ms / 1e3) / 1e9, 1))
+
+
 def decode_us_per_layer(ctx, torch, n, replays=50, ctx_len=None):
     dl = DecodeLayers(ctx, torch, n) if ctx_len is None else DecodeLayersAttn(ctx, torch, n, ctx_len)
     torch.cuda.synchronize()
@@ -923,6 +1072,11 @@ def main():
                                                                 eager_us_per_layer=round(e_us, 2))
             torch.cuda.empty_cache()
         torch.cuda.empty_cache()
+        if not args.no_qmm:
+            log("whole decode steps (32 layers + head, hipGraph)")
+            for n, clen in ((1, 4096), (32, 1024)):
+                decode[f"step_batch{n}_ctx{clen}"] = decode_step_bench(ctx, torch, n, clen)
+            torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu:
