@@ -537,11 +537,13 @@ class DecodeStep:
         decode attention over ctx_len keys, o projection, residual + FFN
         RMSNorm, gate/up projections with SwiGLU (qmm_glu), down projection]
       -> residual + final RMSNorm -> LM head (Q8_0) -> argmax.
+    The projections run on qmm (the CPU engine's bits) or, with
+    mm="qgemm", on the matrix cores (the GPU engine's arithmetic class).
     Layer weights are Q4_0 (or `qtype`), 32 distinct layers (3.9 GB Q4_0),
     generated as GGUF bytes on the device and packed once; the K/V pools
     hold ctx_len keys per sequence in consecutive blocks."""
 
-    def __init__(self, ctx, torch, n, ctx_len, qtype="q4_0", layers=32, seed=3):
+    def __init__(self, ctx, torch, n, ctx_len, qtype="q4_0", layers=32, seed=3, mm="qmm"):
         import numpy as np
         from cuca_amd import hip
         from cuca_amd import workloads as W
@@ -596,8 +598,24 @@ class DecodeStep:
         self.ws_bytes = hip.paged_decode_workspace(n, nq, d, nb_row)
         self.ws = torch.empty(max(self.ws_bytes, 16), dtype=torch.uint8, device=dev)
         self.scale = 1.0 / float(np.sqrt(d))
+        # the projections: the CPU engine's bits (qmm), or the matrix cores
+        # (qgemm, the GPU engine's arithmetic class) with one workspace
+        self.mm = mm
+        if mm == "qgemm":
+            self.qg_bytes = max([hip.qgemm_workspace(T, rows, cols, n, glu) for rows, cols, glu in (
+                (nq * d, H, False), (2 * nk * d, H, False), (H, nq * d, False), (F, H, True), (H, F, False))]
+                + [hip.qgemm_workspace(hip.GGML_Q8_0, self.vocab, H, n, False)])
+            self.qg_ws = torch.empty(self.qg_bytes, dtype=torch.uint8, device=dev)
         self.weight_bytes = sum(t.numel() for l in self.L for t in (l["wq"], l["wkv"], l["wo"], l["wg"],
                                                                       l["wu"], l["wd"]))
+
+    def mat(self, w, rows, cols, x, out):
+        if self.mm == "qgemm":
+            self.ctx.qgemm(w.data_ptr(), self.T, rows, cols, x.data_ptr(), cols, self.n, rows,
+                           self.qg_ws.data_ptr(), self.qg_bytes, out.data_ptr(), rows, self.hip.F32)
+        else:
+            self.ctx.qmm(w.data_ptr(), self.T, rows, cols, x.data_ptr(), cols, self.n, rows, out.data_ptr(),
+                         rows, self.hip.F32)
 
     def issue_layers(self):
         c, hip, cfg, n, T = self.ctx, self.hip, self.cfg, self.n, self.T
@@ -606,10 +624,8 @@ class DecodeStep:
         for l in self.L:
             c.add_rmsnorm(self.x.data_ptr(), self.ffn.data_ptr(), l["n1"].data_ptr(), None, eps, eps, 1.0,
                           n, H, self.x.data_ptr(), self.h.data_ptr(), f32)
-            c.qmm(l["wq"].data_ptr(), T, nq * d, H, self.h.data_ptr(), H, n, nq * d, self.q.data_ptr(),
-                  nq * d, f32)
-            c.qmm(l["wkv"].data_ptr(), T, 2 * nk * d, H, self.h.data_ptr(), H, n, 2 * nk * d,
-                  self.kv.data_ptr(), 2 * nk * d, f32)
+            self.mat(l["wq"], nq * d, H, self.h, self.q)
+            self.mat(l["wkv"], 2 * nk * d, H, self.h, self.kv)
             c.rope_store_kv(self.q.data_ptr(), nq * d, self.kv.data_ptr(), 2 * nk * d,
                             self.kv.data_ptr() + 4 * nk * d, 2 * nk * d, n, nq, nk, d, d, hip.ROPE_NORM,
                             self.cos.data_ptr(), self.sin.data_ptr(), 8192, self.pos.data_ptr(), None, None,
@@ -618,13 +634,16 @@ class DecodeStep:
             c.paged_decode(self.q.data_ptr(), l["pk"].data_ptr(), l["pv"].data_ptr(), self.n_blocks,
                            self.tables.data_ptr(), self.max_blocks, self.ranges.data_ptr(), n, nq, nk, d,
                            self.scale, self.ws.data_ptr(), self.ws_bytes, self.o.data_ptr(), f32)
-            c.qmm(l["wo"].data_ptr(), T, H, nq * d, self.o.data_ptr(), nq * d, n, H, self.attn.data_ptr(),
-                  H, f32)
+            self.mat(l["wo"], H, nq * d, self.o, self.attn)
             c.add_rmsnorm(self.x.data_ptr(), self.attn.data_ptr(), l["n2"].data_ptr(), None, eps, eps, 1.0,
                           n, H, self.x.data_ptr(), self.h.data_ptr(), f32)
-            c.qmm_glu(l["wg"].data_ptr(), l["wu"].data_ptr(), T, F, H, self.h.data_ptr(), H, n,
-                      hip.ACT_SILU, 0.0, self.act.data_ptr(), F, f32)
-            c.qmm(l["wd"].data_ptr(), T, H, F, self.act.data_ptr(), F, n, H, self.ffn.data_ptr(), H, f32)
+            if self.mm == "qgemm":
+                c.qgemm_glu(l["wg"].data_ptr(), l["wu"].data_ptr(), T, F, H, self.h.data_ptr(), H, n,
+                            hip.ACT_SILU, 0.0, self.qg_ws.data_ptr(), self.qg_bytes, self.act.data_ptr(), F, f32)
+            else:
+                c.qmm_glu(l["wg"].data_ptr(), l["wu"].data_ptr(), T, F, H, self.h.data_ptr(), H, n,
+                          hip.ACT_SILU, 0.0, self.act.data_ptr(), F, f32)
+            self.mat(l["wd"], H, F, self.act, self.ffn)
 
     def issue_step(self):
         c, hip, cfg, n = self.ctx, self.hip, self.cfg, self.n
@@ -634,18 +653,22 @@ class DecodeStep:
         self.issue_layers()
         c.add_rmsnorm(self.x.data_ptr(), self.ffn.data_ptr(), self.nout.data_ptr(), None, eps, eps, 1.0, n,
                       H, self.x.data_ptr(), self.h.data_ptr(), hip.F32)
-        c.lm_head(self.head.data_ptr(), hip.GGML_Q8_0, self.vocab, H, self.h.data_ptr(), H, n, self.vocab,
-                  1.0, 1.0, 0.0, self.logits.data_ptr(), self.vocab, hip.F32)
+        if self.mm == "qgemm":  # no logit scale or soft-cap in this model: the plain matmul
+            c.qgemm(self.head.data_ptr(), hip.GGML_Q8_0, self.vocab, H, self.h.data_ptr(), H, n, self.vocab,
+                    self.qg_ws.data_ptr(), self.qg_bytes, self.logits.data_ptr(), self.vocab, hip.F32)
+        else:
+            c.lm_head(self.head.data_ptr(), hip.GGML_Q8_0, self.vocab, H, self.h.data_ptr(), H, n, self.vocab,
+                      1.0, 1.0, 0.0, self.logits.data_ptr(), self.vocab, hip.F32)
         c.argmax(self.logits.data_ptr(), self.vocab, n, self.vocab, hip.F32, self.out_ids.data_ptr())
 
 
-def decode_step_bench(ctx, torch, n, ctx_len, replays=10):
+def decode_step_bench(ctx, torch, n, ctx_len, replays=10, mm="qmm"):
     """DecodeStep's 32 layers and its whole step, each captured in one
     hipGraph and replayed: microseconds per layer, per step, and tokens/s
     (n tokens per step).  Checked: the step's ids are the argmax of its own
     logits, and the logits are finite."""
     import numpy as np
-    ds = DecodeStep(ctx, torch, n, ctx_len)
+    ds = DecodeStep(ctx, torch, n, ctx_len, mm=mm)
     ds.out_ids.copy_(ds.ids)
     torch.cuda.synchronize()
     ds.issue_step()  # eager, once
@@ -670,7 +693,7 @@ def decode_step_bench(ctx, torch, n, ctx_len, replays=10):
     wb = ds.weight_bytes
     del ds
     torch.cuda.empty_cache()
-    return dict(batch=n, ctx_len=ctx_len, layer_weights="q4_0", head="q8_0",
+    return dict(batch=n, ctx_len=ctx_len, layer_weights="q4_0", head="q8_0", matmul=mm,
                 us_per_layer=round(layers_ms * 1000 / 32, 2), us_per_step=round(step_ms * 1000, 1),
                 tokens_per_s=round(n / (step_ms / 1e3), 1),
                 layer_weight_gbs=round(wb / (layers_ms / 1e3) / 1e9, 1))
@@ -1074,8 +1097,8 @@ def main():
         torch.cuda.empty_cache()
         if not args.no_qmm:
             log("whole decode steps (32 layers + head, hipGraph)")
-            for n, clen in ((1, 4096), (32, 1024)):
-                decode[f"step_batch{n}_ctx{clen}"] = decode_step_bench(ctx, torch, n, clen)
+            for n, clen, mm in ((1, 4096, "qmm"), (32, 1024, "qmm"), (32, 1024, "qgemm")):
+                decode[f"step_batch{n}_ctx{clen}_{mm}"] = decode_step_bench(ctx, torch, n, clen, mm=mm)
             torch.cuda.empty_cache()
 
     cpu = None

@@ -159,6 +159,21 @@ typedef struct {
     int32_t pad2_;
 } QmmArgs;
 
+/* The quantized matmul on the matrix cores (qgemm.hip): out[t][n] =
+ * x[t] . w[n] over f16 weights f16(d * q) and f16 activations, f32
+ * accumulation; workgroups of 128 weight rows x TM tokens. */
+typedef struct {
+    const uint8_t *w, *w_up;    /* packed weights (gate/up for GLU)          */
+    const void *x;              /* [m][ldx] f32 or f16                       */
+    uint16_t *xp;               /* workspace: x in slot order [m][kp] f16    */
+    float *part;                /* workspace: split sums [splits][g,u][m][rows] */
+    void *out;                  /* [m][out_ld]                               */
+    int64_t ldx, out_ld, row_bytes, kp;
+    int32_t rows, m, k, nkc, n_rt, n_ct, kcs, splits;
+    float clamp;
+    int32_t pad_;
+} QGemmArgs;
+
 /* Activation quantisation for the decode GEMV (Acts::new, qmm.rs:1272-1343):
  * x [m][ldx] -> quants [m][q_ld] int8 (element order) and scales [m][nb]. */
 typedef struct {

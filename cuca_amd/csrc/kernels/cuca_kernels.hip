@@ -13,3 +13,4 @@
 #include "qmm.hip"
 #include "pick.hip"
 #include "qmv.hip"
+#include "qgemm.hip"

@@ -1,0 +1,316 @@
+// qgemm.hip -- the quantized matmul for many activation rows (prefill, large
+// decode batches) on gfx950's matrix cores: out[t][n] = x[t] . w[n] with
+// the Q4_0 / Q8_0 weights dequantised to f16 and the activations rounded to
+// f16, f32 accumulation (v_mfma_f32_32x32x16_f16).
+//
+// This is the reference GPU engine's arithmetic class for its dense paths
+// (dense_gemv_kernel / dense_dequant_kernel, moe_kernel.rs:1414-1600: float
+// products of dequantised weights and unquantised activations), not the CPU
+// engine's bits (cuca_hip_qmm keeps those).  Each weight is f16(d * q) and
+// each activation f16(x), one rounding each; the error is bounded by
+// (2^-10 + k 2^-24) sum_i |w_i x_i| and the parity tests hold it to that.
+//
+// The weights are read in the packed layout of qmm.hip.  A dot product may
+// sum its terms in any order, so the k index of the matrix-core operands is
+// the packed layout's own order: a lane's 8 f16 of a k-step come from one
+// or two packed dwords (shift, mask, an f16 bias subtracted, the block scale
+// multiplied, two values at a time), and the activations are staged into
+// LDS in the same order.  Slot j of a lane's 8 values is true position
+// base + 16 j:
+//   Q4_0: k-chunk kc = group kc/4, quarter qq = kc%4; k-step s, half h:
+//         lane chunk l = 4 qq + s/2, dword t = 2 h + s%2,
+//         base = 512 g + 128 t + l; dword t of chunk l holds blocks 4t..4t+3
+//         (pair i = nibbles 4i and 16+4i: elements l and l+16 of block 4t+i)
+//   Q8_0: k-chunk kc = group kc/2, half hh = kc%2; k-step s, half h:
+//         lane chunk l = 8 hh + s, dwords 2h and 2h+1, base = 256 g + 128 h + l
+//         (dword t: biased bytes of elements l, l+16 of blocks 2t, 2t+1)
+//
+// Workgroup: 4 waves, 128 weight rows (32 per wave) x TM tokens (TM / 32
+// accumulator tiles per wave); k in chunks of 128 values (8 k-steps).  The
+// next chunk's weights and activations are loaded into registers while the
+// current chunk computes, and the activations written to the other LDS
+// buffer after it.  The grid is XCD-aware: an XCD's workgroups take row
+// tiles x, x + 8, ... each with all of its token tiles in a row.
+#include "common.h"
+
+typedef _Float16 qg_h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 qg_h8 __attribute__((ext_vector_type(8)));
+typedef float qg_acc __attribute__((ext_vector_type(16)));
+typedef uint32_t qg_u2 __attribute__((ext_vector_type(2)));
+
+#define QG_ROWS 128       // weight rows per workgroup (32 per wave)
+#define QG_KC 128         // values per k-chunk: 8 k-steps of 16
+#define QG_XS (QG_KC + 8) // LDS row stride of the staged activations (f16)
+
+template <int FMT> struct QgFmt;
+template <> struct QgFmt<0> { // Q4_0: 4 lane chunks of a 512-value group per k-chunk
+    static constexpr int NW = 4, GB = 288, SCB = 32, KCG = 4;
+};
+template <> struct QgFmt<1> { // Q8_0: 8 lane chunks of a 256-value group per k-chunk
+    static constexpr int NW = 8, GB = 272, SCB = 16, KCG = 2;
+};
+
+// The weights a lane needs for one k-chunk: its dword pair of each lane
+// chunk, and the scales of its blocks (Q4_0: blocks 8h..8h+7, Q8_0: 4h..4h+3).
+template <int FMT> struct QgA {
+    qg_u2 w[QgFmt<FMT>::NW];
+    u32x4 sc;
+};
+
+template <int FMT>
+__device__ static inline void qg_load_a(const uint8_t *wrow, int kc, int h, QgA<FMT> &o) {
+    using F = QgFmt<FMT>;
+    const int g = kc / F::KCG, part = kc % F::KCG;
+    const uint8_t *grp = wrow + (int64_t)g * F::GB;
+#pragma unroll
+    for (int i = 0; i < F::NW; i++) {
+        const int l = part * F::NW + i;
+        o.w[i] = *reinterpret_cast<const qg_u2 *>(grp + F::SCB + 16 * l + 8 * h);
+    }
+    if (FMT == 0) {
+        o.sc = *reinterpret_cast<const u32x4 *>(grp + 16 * h);
+    } else {
+        const qg_u2 s2 = *reinterpret_cast<const qg_u2 *>(grp + 8 * h);
+        o.sc = u32x4{s2.x, s2.y, 0u, 0u};
+    }
+}
+
+__device__ static inline qg_h2 qg_pair(uint32_t u, qg_h2 bias, _Float16 d) {
+    const qg_h2 p = __builtin_bit_cast(qg_h2, u) - bias;
+    return p * qg_h2{d, d};
+}
+__device__ static inline _Float16 qg_scale(const u32x4 &sc, int i) {
+    const uint32_t w = sc[i >> 1];
+    return __builtin_bit_cast(_Float16, (uint16_t)((i & 1) ? (w >> 16) : (w & 0xffffu)));
+}
+
+// The A operand of k-step s (compile-time s).
+template <int FMT>
+__device__ static inline qg_h8 qg_dequant(const QgA<FMT> &a, int s) {
+    qg_h8 o;
+    if (FMT == 0) {
+        const uint32_t w = a.w[s >> 1][s & 1];
+        const qg_h2 bias = {(_Float16)1032.0f, (_Float16)1032.0f};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t u = ((w >> (4 * i)) & 0x000f000fu) | 0x64006400u;
+            const qg_h2 p = qg_pair(u, bias, qg_scale(a.sc, (s & 1) * 4 + i));
+            o[2 * i] = p.x;
+            o[2 * i + 1] = p.y;
+        }
+    } else {
+        const qg_h2 bias = {(_Float16)1152.0f, (_Float16)1152.0f};
+#pragma unroll
+        for (int idx = 0; idx < 2; idx++) {
+            const uint32_t w = a.w[s][idx];
+            const qg_h2 p0 = qg_pair(__builtin_amdgcn_perm(0x64646464u, w, 0x04020400u), bias, qg_scale(a.sc, 2 * idx));
+            const qg_h2 p1 = qg_pair(__builtin_amdgcn_perm(0x64646464u, w, 0x04030401u), bias, qg_scale(a.sc, 2 * idx + 1));
+            o[4 * idx + 0] = p0.x;
+            o[4 * idx + 1] = p0.y;
+            o[4 * idx + 2] = p1.x;
+            o[4 * idx + 3] = p1.y;
+        }
+    }
+    return o;
+}
+
+// The activations rewritten once per call, before the matmul: f16, in the
+// slot order of the format (xp [m][kp], kp = 128 per k-chunk, zero past k).
+// One thread per unit (token, k-chunk, k-step s, half h) of 8 values:
+// the values at true positions base + 16 j.
+template <typename T, int FMT> __device__ static inline void qgemm_prep_body(const QGemmArgs &a) {
+    using F = QgFmt<FMT>;
+    const int64_t u = (int64_t)blockIdx.x * CUCA_BLOCK + threadIdx.x;
+    const int64_t per_row = (int64_t)a.nkc * 16;
+    if (u >= (int64_t)a.m * per_row) return;
+    const int tok = (int)(u / per_row), rem = (int)(u - (int64_t)tok * per_row);
+    const int kc = rem >> 4, v = rem & 15, s = v >> 1, h = v & 1;
+    const int g = kc / F::KCG, part = kc % F::KCG;
+    int base;
+    if (FMT == 0) base = 512 * g + 128 * (2 * h + (s & 1)) + 4 * part + (s >> 1);
+    else base = 256 * g + 128 * h + 8 * part + s;
+    const T *row = reinterpret_cast<const T *>(a.x) + (int64_t)tok * a.ldx;
+    qg_h8 o;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int k = base + 16 * j;
+        o[j] = k < a.k ? (_Float16)(float)row[k] : (_Float16)0.0f;
+    }
+    *reinterpret_cast<qg_h8 *>(a.xp + (int64_t)tok * a.kp + (int64_t)kc * QG_KC + 8 * (2 * s + h)) = o; // xp: f16 bits
+}
+
+// The staged activations of one k-chunk: TM tokens x 128 f16, 16-byte
+// units, thread tid taking units tid + 256 i (16 units per token).
+template <int TM> struct QgX {
+    u32x4 v[TM / 16];
+};
+template <int TM>
+__device__ static inline void qg_load_x(const QGemmArgs &a, int tok0, int kc, QgX<TM> &o) {
+#pragma unroll
+    for (int it = 0; it < TM / 16; it++) {
+        const int u = threadIdx.x + 256 * it;
+        const int c = u >> 4, v = u & 15;
+        const int tok = tok0 + c < a.m ? tok0 + c : a.m - 1; // rows past m: never stored
+        o.v[it] = *reinterpret_cast<const u32x4 *>(a.xp + (int64_t)tok * a.kp + (int64_t)kc * QG_KC + 8 * v);
+    }
+}
+template <int TM>
+__device__ static inline void qg_store_x(_Float16 (*xs)[QG_XS], const QgX<TM> &o) {
+#pragma unroll
+    for (int it = 0; it < TM / 16; it++) {
+        const int u = threadIdx.x + 256 * it;
+        *reinterpret_cast<u32x4 *>(&xs[u >> 4][8 * (u & 15)]) = o.v[it];
+    }
+}
+
+// SPLIT: workgroup (tile, split) takes k-chunks [split * kcs, ...) and
+// writes its f32 sums to the partial rows of the workspace (qgemm_reduce
+// adds the splits in order and applies the epilogue); otherwise the
+// epilogue is applied here.
+template <typename T, int FMT, int TM, bool GLU, int ACT, bool SPLIT>
+__device__ static inline void qgemm_body(const QGemmArgs &a) {
+    constexpr int NT = TM / 32;
+    __shared__ __attribute__((aligned(16))) _Float16 xs[2][TM][QG_XS];
+    const int split = SPLIT ? (int)blockIdx.y : 0;
+    const int id = blockIdx.x, xcd = id & 7, kq = id >> 3;
+    const int rt = (kq / a.n_ct) * 8 + xcd, ct = kq % a.n_ct;
+    if (rt >= a.n_rt) return;
+    const int kc0 = split * a.kcs;
+    const int kc1 = min(a.nkc, kc0 + a.kcs);
+    if (kc0 >= kc1) return;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r = lane & 31, h = lane >> 5;
+    const int row = rt * QG_ROWS + wave * 32 + r;
+    const int tok0 = ct * TM;
+    const int64_t roff = (int64_t)(row < a.rows ? row : 0) * a.row_bytes;
+    const uint8_t *wg = a.w + roff;
+    const uint8_t *wu = GLU ? a.w_up + roff : nullptr;
+
+    qg_acc acc[NT], accu[NT];
+#pragma unroll
+    for (int i = 0; i < NT; i++) {
+        acc[i] = qg_acc{};
+        accu[i] = qg_acc{};
+    }
+    QgA<FMT> ag, au, ng, nu;
+    QgX<TM> xn;
+    qg_load_a<FMT>(wg, kc0, h, ag);
+    if (GLU) qg_load_a<FMT>(wu, kc0, h, au);
+    qg_load_x<TM>(a, tok0, kc0, xn);
+    qg_store_x<TM>(xs[0], xn);
+    __syncthreads();
+    for (int kc = kc0; kc < kc1; kc++) {
+        const int buf = (kc - kc0) & 1;
+        const bool next = kc + 1 < kc1;
+        if (next) {
+            qg_load_a<FMT>(wg, kc + 1, h, ng);
+            if (GLU) qg_load_a<FMT>(wu, kc + 1, h, nu);
+            qg_load_x<TM>(a, tok0, kc + 1, xn);
+        }
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            const qg_h8 av = qg_dequant<FMT>(ag, s);
+            qg_h8 uv;
+            if (GLU) uv = qg_dequant<FMT>(au, s);
+#pragma unroll
+            for (int i = 0; i < NT; i++) {
+                const qg_h8 bv = *reinterpret_cast<const qg_h8 *>(&xs[buf][i * 32 + r][s * 16 + 8 * h]);
+                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc[i], 0, 0, 0);
+                if (GLU) accu[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(uv, bv, accu[i], 0, 0, 0);
+            }
+        }
+        if (next) qg_store_x<TM>(xs[buf ^ 1], xn);
+        __syncthreads();
+        if (next) {
+            ag = ng;
+            if (GLU) au = nu;
+        }
+    }
+    // accumulator q of lane (r, h): weight row 8 (q / 4) + 4 h + q % 4, token r
+    if (SPLIT) {
+        // partial rows: [split][gate, up][m][rows] f32
+#pragma unroll
+        for (int i = 0; i < NT; i++) {
+            const int tok = tok0 + i * 32 + r;
+            if (tok >= a.m) continue;
+            float *pg = a.part + ((int64_t)split * (GLU ? 2 : 1) * a.m + tok) * a.rows;
+            float *pu = a.part + ((int64_t)(split * 2 + 1) * a.m + tok) * a.rows;
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const int n = rt * QG_ROWS + wave * 32 + 8 * (q >> 2) + 4 * h + (q & 3);
+                if (n >= a.rows) continue;
+                pg[n] = acc[i][q];
+                if (GLU) pu[n] = accu[i][q];
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < NT; i++) {
+        const int tok = tok0 + i * 32 + r;
+        if (tok >= a.m) continue;
+        T *orow = reinterpret_cast<T *>(a.out) + (int64_t)tok * a.out_ld;
+#pragma unroll
+        for (int q = 0; q < 16; q++) {
+            const int n = rt * QG_ROWS + wave * 32 + 8 * (q >> 2) + 4 * h + (q & 3);
+            if (n >= a.rows) continue;
+            float o = acc[i][q];
+            if (GLU) {
+                float g = o, u = accu[i][q];
+                if (a.clamp > 0.0f) { // Glu::apply's clamp (cpu.rs:364-368)
+                    g = fminf(g, a.clamp);
+                    u = fminf(fmaxf(u, -a.clamp), a.clamp);
+                }
+                o = (ACT == 0 ? act_silu(g) : act_gelu_tanh(g)) * u;
+            }
+            orow[n] = (T)o;
+        }
+    }
+}
+
+// The splits' partial rows added in split order, then the epilogue: one
+// thread per output.
+template <typename T, bool GLU, int ACT> __device__ static inline void qgemm_reduce_body(const QGemmArgs &a) {
+    const int64_t e = (int64_t)blockIdx.x * CUCA_BLOCK + threadIdx.x;
+    if (e >= (int64_t)a.m * a.rows) return;
+    const int tok = (int)(e / a.rows), n = (int)(e - (int64_t)tok * a.rows);
+    float g = 0.0f, u = 0.0f;
+    for (int sp = 0; sp < a.splits; sp++) {
+        g = g + a.part[((int64_t)sp * (GLU ? 2 : 1) * a.m + tok) * a.rows + n];
+        if (GLU) u = u + a.part[((int64_t)(sp * 2 + 1) * a.m + tok) * a.rows + n];
+    }
+    float o = g;
+    if (GLU) {
+        if (a.clamp > 0.0f) { // Glu::apply's clamp (cpu.rs:364-368)
+            g = fminf(g, a.clamp);
+            u = fminf(fmaxf(u, -a.clamp), a.clamp);
+        }
+        o = (ACT == 0 ? act_silu(g) : act_gelu_tanh(g)) * u;
+    }
+    reinterpret_cast<T *>(a.out)[(int64_t)tok * a.out_ld + n] = (T)o;
+}
+
+#define CUCA_QGEMM(NAME, BODY, ...)                                                        \
+    extern "C" __global__ __launch_bounds__(256) void NAME(QGemmArgs a) { BODY<__VA_ARGS__>(a); }
+#define CUCA_QGEMM_TM(TN, T, FN, FMT, TM)                                                  \
+    CUCA_QGEMM(cuca_qgemm_##TN##_##FN##_t##TM, qgemm_body, T, FMT, TM, false, 0, false)    \
+    CUCA_QGEMM(cuca_qgemm_glu_##TN##_##FN##_silu_t##TM, qgemm_body, T, FMT, TM, true, 0, false) \
+    CUCA_QGEMM(cuca_qgemm_glu_##TN##_##FN##_gelu_t##TM, qgemm_body, T, FMT, TM, true, 1, false) \
+    CUCA_QGEMM(cuca_qgemm_##TN##_##FN##_t##TM##_split, qgemm_body, T, FMT, TM, false, 0, true) \
+    CUCA_QGEMM(cuca_qgemm_glu_##TN##_##FN##_t##TM##_split, qgemm_body, T, FMT, TM, true, 0, true)
+#define CUCA_QGEMM_SET(TN, T, FN, FMT)                                                     \
+    CUCA_QGEMM(cuca_qgemm_prep_##TN##_##FN, qgemm_prep_body, T, FMT)                        \
+    CUCA_QGEMM_TM(TN, T, FN, FMT, 32)                                                      \
+    CUCA_QGEMM_TM(TN, T, FN, FMT, 64)                                                      \
+    CUCA_QGEMM_TM(TN, T, FN, FMT, 128)
+CUCA_QGEMM_SET(f32, float, q4_0, 0)
+CUCA_QGEMM_SET(f32, float, q8_0, 1)
+CUCA_QGEMM_SET(f16, _Float16, q4_0, 0)
+CUCA_QGEMM_SET(f16, _Float16, q8_0, 1)
+#define CUCA_QGEMM_RED(TN, T)                                                              \
+    CUCA_QGEMM(cuca_qgemm_reduce_##TN, qgemm_reduce_body, T, false, 0)                     \
+    CUCA_QGEMM(cuca_qgemm_reduce_glu_##TN##_silu, qgemm_reduce_body, T, true, 0)           \
+    CUCA_QGEMM(cuca_qgemm_reduce_glu_##TN##_gelu, qgemm_reduce_body, T, true, 1)
+CUCA_QGEMM_RED(f32, float)
+CUCA_QGEMM_RED(f16, _Float16)

@@ -129,25 +129,31 @@ cuca_status use(cuca_hip_ctx *ctx) {
     return CUCA_OK;
 }
 
+// A grid of grid x grid_y workgroups of `block` threads.
 template <typename Args>
-cuca_status launch(cuca_hip_ctx *ctx, Kernel k, unsigned grid, unsigned block, unsigned lds,
-                   Args &args) {
-    if (grid == 0) return CUCA_OK;
+cuca_status launch2(cuca_hip_ctx *ctx, Kernel k, unsigned grid, unsigned grid_y, unsigned block, unsigned lds,
+                    Args &args) {
+    if (grid == 0 || grid_y == 0) return CUCA_OK;
     void *params[] = {&args};
     hipError_t e;
     if (ctx->profiling && !ctx->capturing && ctx->prof_used < ctx->prof_limit) {
         cuca_hip_ctx::ProfRec &r = ctx->prof[ctx->prof_used++];
         r.kernel = k;
         // work sizes in work-items; the events stamp the kernel's own start and end
-        e = hipExtModuleLaunchKernel(ctx->fn[k], grid * block, 1, 1, block, 1, 1, lds, ctx->stream,
+        e = hipExtModuleLaunchKernel(ctx->fn[k], grid * block, grid_y, 1, block, 1, 1, lds, ctx->stream,
                                      params, nullptr, r.start, r.stop, 0);
     } else {
-        e = hipModuleLaunchKernel(ctx->fn[k], grid, 1, 1, block, 1, 1, lds, ctx->stream, params,
+        e = hipModuleLaunchKernel(ctx->fn[k], grid, grid_y, 1, block, 1, 1, lds, ctx->stream, params,
                                   nullptr);
     }
     if (e != hipSuccess) return fail(ctx, CUCA_HIP_ERROR, "launching %s: %s", kKernelNames[k],
                                      hipGetErrorString(e));
     return CUCA_OK;
+}
+
+template <typename Args>
+cuca_status launch(cuca_hip_ctx *ctx, Kernel k, unsigned grid, unsigned block, unsigned lds, Args &args) {
+    return launch2(ctx, k, grid, 1u, block, lds, args);
 }
 
 inline bool al16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -1177,6 +1183,151 @@ cuca_status cuca_hip_qmm_glu(cuca_hip_ctx *ctx, const void *gate, const void *up
         return fail(ctx, CUCA_INVALID_ARG, "bad activation %d", (int)act);
     return qmm_common(ctx, gate, up, ggml_type, ff, k, x, ldx, m, ff, act == CUCA_ACT_SILU ? 1 : 2, clamp,
                       out, out_ld, dtype);
+}
+
+// The matrix-core matmul (qgemm.hip): the workspace holds the activations
+// in slot order (f16, kp values per row) and, up to 2048 rows, the split
+// sums (up to kQgMaxSplits splits of f32 rows, two per output with the GLU)
+// that grids of fewer workgroups than CUs use.
+constexpr int64_t kQgMaxSplits = 8;
+
+static int64_t qgemm_kp(int g, int64_t k) {
+    const int64_t ng = (k / 32 + g - 1) / g;
+    return ng * g * 32;
+}
+static size_t qgemm_ws_bytes(int g, int64_t n, int64_t k, int64_t m, bool glu) {
+    const size_t xp = ((size_t)m * (size_t)qgemm_kp(g, k) * 2 + 255) / 256 * 256;
+    const size_t part = m <= 2048 ? (size_t)kQgMaxSplits * (glu ? 2 : 1) * (size_t)m * (size_t)n * 4 : 0;
+    return xp + part;
+}
+
+cuca_status cuca_hip_qgemm_workspace(uint32_t ggml_type, int64_t n, int64_t k, int64_t m, int32_t glu, size_t *bytes) {
+    if (!bytes) return fail(nullptr, CUCA_INVALID_ARG, "null pointer");
+    int g = 0, gb = 0;
+    if (!qfmt(ggml_type, &g, &gb)) return fail(nullptr, CUCA_UNSUPPORTED, "qgemm: ggml type %u", ggml_type);
+    if (n <= 0 || k <= 0 || k % 32 != 0 || m < 0)
+        return fail(nullptr, CUCA_INVALID_ARG, "qgemm: bad shape %lld x %lld, %lld rows", (long long)n, (long long)k,
+                    (long long)m);
+    *bytes = qgemm_ws_bytes(g, n, k, m, glu != 0);
+    return CUCA_OK;
+}
+
+// glu: 0 plain, 1 SiLU, 2 GELU-tanh.
+static cuca_status qgemm_common(cuca_hip_ctx *ctx, const void *w, const void *w_up, uint32_t ggml_type, int64_t n,
+                                int64_t k, const void *x, int64_t ldx, int64_t m, int64_t rows, int glu, float clamp,
+                                void *ws, size_t ws_bytes, void *out, int64_t out_ld, cuca_dtype dtype) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    int g = 0, gb = 0;
+    if ((st = qweight_shape(ctx, ggml_type, n, k, &g, &gb)) != CUCA_OK) return st;
+    if (!dtype_ok(dtype)) return fail(ctx, CUCA_INVALID_ARG, "bad dtype %d", (int)dtype);
+    if (rows <= 0 || rows > n)
+        return fail(ctx, CUCA_INVALID_ARG, "qgemm: %lld weight rows of %lld", (long long)rows, (long long)n);
+    if (m < 0 || m > 0x7fffffffll) return fail(ctx, CUCA_INVALID_ARG, "qgemm: bad activation row count %lld", (long long)m);
+    if (ldx < k)
+        return fail(ctx, CUCA_INVALID_ARG, "qgemm: activation row stride %lld shorter than %lld", (long long)ldx,
+                    (long long)k);
+    if (out_ld < rows)
+        return fail(ctx, CUCA_INVALID_ARG, "qgemm: output row stride %lld shorter than %lld", (long long)out_ld,
+                    (long long)rows);
+    if (!(clamp == clamp)) return fail(ctx, CUCA_INVALID_ARG, "clamp is NaN");
+    if (m == 0) return CUCA_OK;
+    if (!w || !x || !out || !ws || (glu && !w_up)) return fail(ctx, CUCA_INVALID_ARG, "null pointer");
+    if (!al16(w) || (w_up && !al16(w_up)) || !al16(ws))
+        return fail(ctx, CUCA_INVALID_ARG, "packed weights and the workspace must be 16-byte aligned");
+    const int64_t kp = qgemm_kp(g, k);
+    const size_t xp_bytes = ((size_t)m * (size_t)kp * 2 + 255) / 256 * 256;
+    if (ws_bytes < xp_bytes)
+        return fail(ctx, CUCA_INVALID_ARG, "qgemm: workspace of %zu bytes, %zu needed (cuca_hip_qgemm_workspace)",
+                    ws_bytes, xp_bytes);
+    const int tm = m <= 32 ? 32 : m <= 64 ? 64 : 128;
+    const int ti = tm == 32 ? 0 : tm == 64 ? 1 : 2;
+    const int64_t n_rt = (rows + 127) / 128, n_ct = (m + tm - 1) / tm;
+    const int64_t tiles = (n_rt + 7) / 8 * 8 * n_ct;
+    const int64_t nkc = kp / 128;
+    if (tiles > 0x7fffffffll) return fail(ctx, CUCA_UNSUPPORTED, "qgemm: grid too large");
+    // split k for grids smaller than the CU count: up to two workgroups per
+    // CU, at least 4 k-chunks per split, within the workspace given
+    int64_t splits = 1;
+    const size_t split_row = (size_t)(glu ? 2 : 1) * (size_t)m * (size_t)rows * 4;
+    if (m <= 2048 && tiles < ctx->cu_count) {
+        splits = std::min<int64_t>(kQgMaxSplits, std::min<int64_t>((2 * ctx->cu_count + tiles - 1) / tiles, nkc / 4));
+        splits = std::min<int64_t>(splits, (int64_t)((ws_bytes - xp_bytes) / split_row));
+        if (splits < 2) splits = 1;
+    }
+    const int64_t kcs = (nkc + splits - 1) / splits;
+    splits = (nkc + kcs - 1) / kcs;
+    QGemmArgs a{};
+    a.w = static_cast<const uint8_t *>(w);
+    a.w_up = static_cast<const uint8_t *>(w_up);
+    a.x = x;
+    a.xp = static_cast<uint16_t *>(ws);
+    a.part = reinterpret_cast<float *>(static_cast<char *>(ws) + xp_bytes);
+    a.out = out;
+    a.ldx = ldx;
+    a.out_ld = out_ld;
+    a.row_bytes = (kp / 32 / g) * gb;
+    a.kp = kp;
+    a.rows = (int32_t)rows;
+    a.m = (int32_t)m;
+    a.k = (int32_t)k;
+    a.nkc = (int32_t)nkc;
+    a.n_rt = (int32_t)n_rt;
+    a.n_ct = (int32_t)n_ct;
+    a.kcs = (int32_t)kcs;
+    a.splits = (int32_t)splits;
+    a.clamp = clamp > 0.0f ? clamp : 0.0f;
+    const bool f16 = dtype == CUCA_F16, q8 = ggml_type == CUCA_GGML_Q8_0;
+    static const Kernel prep_k[2][2] = {{cuca_qgemm_prep_f32_q4_0, cuca_qgemm_prep_f32_q8_0},
+                                        {cuca_qgemm_prep_f16_q4_0, cuca_qgemm_prep_f16_q8_0}};
+    if ((st = launch(ctx, prep_k[f16][q8], div_up(m * nkc * 16, CUCA_BLOCK_THREADS), CUCA_BLOCK_THREADS, 0, a)) != CUCA_OK)
+        return st;
+    // [dtype][format][plain, silu, gelu][tokens per tile 32, 64, 128]
+    static const Kernel table_k[2][2][3][3] = {
+        {{{cuca_qgemm_f32_q4_0_t32, cuca_qgemm_f32_q4_0_t64, cuca_qgemm_f32_q4_0_t128},
+          {cuca_qgemm_glu_f32_q4_0_silu_t32, cuca_qgemm_glu_f32_q4_0_silu_t64, cuca_qgemm_glu_f32_q4_0_silu_t128},
+          {cuca_qgemm_glu_f32_q4_0_gelu_t32, cuca_qgemm_glu_f32_q4_0_gelu_t64, cuca_qgemm_glu_f32_q4_0_gelu_t128}},
+         {{cuca_qgemm_f32_q8_0_t32, cuca_qgemm_f32_q8_0_t64, cuca_qgemm_f32_q8_0_t128},
+          {cuca_qgemm_glu_f32_q8_0_silu_t32, cuca_qgemm_glu_f32_q8_0_silu_t64, cuca_qgemm_glu_f32_q8_0_silu_t128},
+          {cuca_qgemm_glu_f32_q8_0_gelu_t32, cuca_qgemm_glu_f32_q8_0_gelu_t64, cuca_qgemm_glu_f32_q8_0_gelu_t128}}},
+        {{{cuca_qgemm_f16_q4_0_t32, cuca_qgemm_f16_q4_0_t64, cuca_qgemm_f16_q4_0_t128},
+          {cuca_qgemm_glu_f16_q4_0_silu_t32, cuca_qgemm_glu_f16_q4_0_silu_t64, cuca_qgemm_glu_f16_q4_0_silu_t128},
+          {cuca_qgemm_glu_f16_q4_0_gelu_t32, cuca_qgemm_glu_f16_q4_0_gelu_t64, cuca_qgemm_glu_f16_q4_0_gelu_t128}},
+         {{cuca_qgemm_f16_q8_0_t32, cuca_qgemm_f16_q8_0_t64, cuca_qgemm_f16_q8_0_t128},
+          {cuca_qgemm_glu_f16_q8_0_silu_t32, cuca_qgemm_glu_f16_q8_0_silu_t64, cuca_qgemm_glu_f16_q8_0_silu_t128},
+          {cuca_qgemm_glu_f16_q8_0_gelu_t32, cuca_qgemm_glu_f16_q8_0_gelu_t64, cuca_qgemm_glu_f16_q8_0_gelu_t128}}}};
+    // [dtype][format][plain, glu][tokens per tile]
+    static const Kernel split_k[2][2][2][3] = {
+        {{{cuca_qgemm_f32_q4_0_t32_split, cuca_qgemm_f32_q4_0_t64_split, cuca_qgemm_f32_q4_0_t128_split},
+          {cuca_qgemm_glu_f32_q4_0_t32_split, cuca_qgemm_glu_f32_q4_0_t64_split, cuca_qgemm_glu_f32_q4_0_t128_split}},
+         {{cuca_qgemm_f32_q8_0_t32_split, cuca_qgemm_f32_q8_0_t64_split, cuca_qgemm_f32_q8_0_t128_split},
+          {cuca_qgemm_glu_f32_q8_0_t32_split, cuca_qgemm_glu_f32_q8_0_t64_split, cuca_qgemm_glu_f32_q8_0_t128_split}}},
+        {{{cuca_qgemm_f16_q4_0_t32_split, cuca_qgemm_f16_q4_0_t64_split, cuca_qgemm_f16_q4_0_t128_split},
+          {cuca_qgemm_glu_f16_q4_0_t32_split, cuca_qgemm_glu_f16_q4_0_t64_split, cuca_qgemm_glu_f16_q4_0_t128_split}},
+         {{cuca_qgemm_f16_q8_0_t32_split, cuca_qgemm_f16_q8_0_t64_split, cuca_qgemm_f16_q8_0_t128_split},
+          {cuca_qgemm_glu_f16_q8_0_t32_split, cuca_qgemm_glu_f16_q8_0_t64_split, cuca_qgemm_glu_f16_q8_0_t128_split}}}};
+    if (splits == 1) return launch(ctx, table_k[f16][q8][glu][ti], (unsigned)tiles, 256, 0, a);
+    if ((st = launch2(ctx, split_k[f16][q8][glu != 0][ti], (unsigned)tiles, (unsigned)splits, 256, 0, a)) != CUCA_OK)
+        return st;
+    static const Kernel red_k[2][3] = {{cuca_qgemm_reduce_f32, cuca_qgemm_reduce_glu_f32_silu, cuca_qgemm_reduce_glu_f32_gelu},
+                                       {cuca_qgemm_reduce_f16, cuca_qgemm_reduce_glu_f16_silu, cuca_qgemm_reduce_glu_f16_gelu}};
+    return launch(ctx, red_k[f16][glu], div_up(m * rows, CUCA_BLOCK_THREADS), CUCA_BLOCK_THREADS, 0, a);
+}
+
+cuca_status cuca_hip_qgemm(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type, int64_t n, int64_t k, const void *x,
+                           int64_t ldx, int64_t m, int64_t rows, void *workspace, size_t workspace_bytes, void *out,
+                           int64_t out_ld, cuca_dtype dtype) {
+    return qgemm_common(ctx, w, nullptr, ggml_type, n, k, x, ldx, m, rows, 0, 0.0f, workspace, workspace_bytes, out,
+                        out_ld, dtype);
+}
+
+cuca_status cuca_hip_qgemm_glu(cuca_hip_ctx *ctx, const void *gate, const void *up, uint32_t ggml_type, int64_t ff,
+                               int64_t k, const void *x, int64_t ldx, int64_t m, cuca_act act, float clamp,
+                               void *workspace, size_t workspace_bytes, void *out, int64_t out_ld, cuca_dtype dtype) {
+    if (act != CUCA_ACT_SILU && act != CUCA_ACT_GELU_TANH)
+        return fail(ctx, CUCA_INVALID_ARG, "bad activation %d", (int)act);
+    return qgemm_common(ctx, gate, up, ggml_type, ff, k, x, ldx, m, ff, act == CUCA_ACT_SILU ? 1 : 2, clamp, workspace,
+                        workspace_bytes, out, out_ld, dtype);
 }
 
 static cuca_status qmv_launch(cuca_hip_ctx *ctx, int mode, const void *w, const void *w_up, uint32_t ggml_type,

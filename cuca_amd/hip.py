@@ -77,6 +77,10 @@ SIGNATURES = {
     "cuca_hip_qmm": (_st, [_p, _p, _u32, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _st]),
     "cuca_hip_qmm_glu": (_st, [_p, _p, _p, _u32, _i64, _i64, _p, _i64, _i64, _st, _f32, _p, _i64,
                                _st]),
+    "cuca_hip_qgemm_workspace": (_st, [_u32, _i64, _i64, _i64, _i32, ctypes.POINTER(ctypes.c_size_t)]),
+    "cuca_hip_qgemm": (_st, [_p, _p, _u32, _i64, _i64, _p, _i64, _i64, _i64, _p, _sz, _p, _i64, _st]),
+    "cuca_hip_qgemm_glu": (_st, [_p, _p, _p, _u32, _i64, _i64, _p, _i64, _i64, _st, _f32, _p, _sz, _p,
+                                 _i64, _st]),
     "cuca_hip_moe_up": (_st, [_p, _p, _p, _i64, _u32, _i64, _i64, _i32, _p, _i64, _i64, _p, _p, _i64,
                               _st, _f32, _p, _i64, _st]),
     "cuca_hip_moe_down": (_st, [_p, _p, _i64, _u32, _i64, _i64, _i32, _p, _i64, _p, _p, _i64, _p,
@@ -340,6 +344,15 @@ class Context:
         self.check(self.L.cuca_hip_qmm(self.ptr, w, ggml_type, n, k, x, ldx, m, rows, out, out_ld,
                                        dtype))
 
+    def qgemm(self, w, ggml_type, n, k, x, ldx, m, rows, ws, ws_bytes, out, out_ld, dtype):
+        self.check(self.L.cuca_hip_qgemm(self.ptr, w, ggml_type, n, k, x, ldx, m, rows, ws, ws_bytes,
+                                         out, out_ld, dtype))
+
+    def qgemm_glu(self, gate, up, ggml_type, ff, k, x, ldx, m, act, clamp, ws, ws_bytes, out, out_ld,
+                  dtype):
+        self.check(self.L.cuca_hip_qgemm_glu(self.ptr, gate, up, ggml_type, ff, k, x, ldx, m, act,
+                                             clamp, ws, ws_bytes, out, out_ld, dtype))
+
     def qmm_glu(self, gate, up, ggml_type, ff, k, x, ldx, m, act, clamp, out, out_ld, dtype):
         self.check(self.L.cuca_hip_qmm_glu(self.ptr, gate, up, ggml_type, ff, k, x, ldx, m, act,
                                            clamp, out, out_ld, dtype))
@@ -409,6 +422,13 @@ class Graph:
 
 KV_BLOCK = 16          # positions per paged K/V block (paged.rs:45)
 NO_BLOCK = 0xFFFFFFFF  # a released block's table entry (paged.rs:49)
+
+
+def qgemm_workspace(ggml_type, n, k, m, glu=False):
+    """Bytes of workspace cuca_hip_qgemm / _qgemm_glu need (host)."""
+    out = _sz(0)
+    _check(lib().cuca_hip_qgemm_workspace(ggml_type, n, k, m, 1 if glu else 0, ctypes.byref(out)), None)
+    return out.value
 
 
 def paged_decode_workspace(rows, n_head, head_dim, max_blocks):

@@ -28,6 +28,7 @@
  *                          (+ _workspace, host)           cpu/paged_attn.rs:105-290
  *   cuca_hip_qmm           QmmWeight::forward_rows        qmm.rs:1810-1838
  *   cuca_hip_qmm_glu       gate/up qmm + Glu::apply       cpu.rs:342-371, 3554-3566
+ *   cuca_hip_qgemm(_glu)   dense_dequant + matmul (GPU)   moe_kernel.rs:1414-1600
  *   cuca_hip_qweight_pack  (the weight upload)            qmm.rs:1763-1783
  *   cuca_hip_moe_up/down/  expert_sum, CpuExpert          cpu.rs:373-419, 3599-3642
  *            _sum          (GPU moe_up/moe_down/moe_sum)  moe_kernel.rs:1163-1385
@@ -314,6 +315,31 @@ cuca_status cuca_hip_qmm(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type, i
 cuca_status cuca_hip_qmm_glu(cuca_hip_ctx *ctx, const void *gate, const void *up, uint32_t ggml_type,
                              int64_t ff, int64_t k, const void *x, int64_t ldx, int64_t m, cuca_act act,
                              float clamp, void *out, int64_t out_ld, cuca_dtype dtype);
+
+/* The quantized matmul for many activation rows (prefill, large decode
+ * batches) on the matrix cores: out[j][r] = x[j] . w[r] with each weight
+ * dequantised to f16 (f16(d * q), one rounding), each activation rounded to
+ * f16 and f32 accumulation.  This is the arithmetic class of the reference
+ * GPU engine's dense paths (dense_gemv_kernel / dense_dequant_kernel,
+ * moe_kernel.rs:1414-1600: float products of dequantised weights and
+ * unquantised activations), not the CPU engine's bits (cuca_hip_qmm): the
+ * error against the exact product is at most (2^-10 + k 2^-24) sum |w x|.
+ * Same packed weights, shapes and errors as cuca_hip_qmm / _qmm_glu
+ * ("qgemm: ..."); activations and outputs need no alignment; |d q| and |x|
+ * within f16's range.
+ * The workspace (device, 16-byte aligned) holds the activations rewritten as
+ * f16 in the kernel's order and, for small batches, the f32 sums of a split
+ * of k that a second launch adds in order (results do not depend on the
+ * split); cuca_hip_qgemm_workspace gives the bytes for n weight rows, k
+ * values and m activation rows (glu != 0 for cuca_hip_qgemm_glu); a smaller
+ * one that still holds the activations is used without splitting. */
+cuca_status cuca_hip_qgemm_workspace(uint32_t ggml_type, int64_t n, int64_t k, int64_t m, int32_t glu, size_t *bytes);
+cuca_status cuca_hip_qgemm(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type, int64_t n, int64_t k, const void *x,
+                           int64_t ldx, int64_t m, int64_t rows, void *workspace, size_t workspace_bytes, void *out,
+                           int64_t out_ld, cuca_dtype dtype);
+cuca_status cuca_hip_qgemm_glu(cuca_hip_ctx *ctx, const void *gate, const void *up, uint32_t ggml_type, int64_t ff,
+                               int64_t k, const void *x, int64_t ldx, int64_t m, cuca_act act, float clamp,
+                               void *workspace, size_t workspace_bytes, void *out, int64_t out_ld, cuca_dtype dtype);
 
 /* The end of a step (Transformer::finish / head / cap_logits,
  * cpu.rs:2495-2617; the final norm is cuca_hip_add_rmsnorm).
