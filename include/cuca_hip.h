@@ -328,9 +328,11 @@ cuca_status cuca_hip_qmm_glu(cuca_hip_ctx *ctx, const void *gate, const void *up
  * ("qgemm: ..."); activations and outputs need no alignment; |d q| and |x|
  * within f16's range.
  * The workspace (device, 16-byte aligned) holds the activations rewritten as
- * f16 in the kernel's order and, for small batches, the f32 sums of a split
- * of k that a second launch adds in order (results do not depend on the
- * split); cuca_hip_qgemm_workspace gives the bytes for n weight rows, k
+ * f16 in the kernel's order and, for small grids, the f32 sums of a split
+ * of k that a second launch adds in a fixed order (deterministic for a
+ * given shape, device and workspace size; the split changes the summation
+ * order, within the same bound); cuca_hip_qgemm_workspace gives the bytes
+ * for n weight rows, k
  * values and m activation rows (glu != 0 for cuca_hip_qgemm_glu); a smaller
  * one that still holds the activations is used without splitting. */
 cuca_status cuca_hip_qgemm_workspace(uint32_t ggml_type, int64_t n, int64_t k, int64_t m, int32_t glu, size_t *bytes);

@@ -99,10 +99,10 @@ def test_qgemm_glu_within_the_bound(ctx, qtype, act, clamp, m):
 
 
 def test_qgemm_weight_row_prefix_split_and_errors(ctx):
-    """A prefix of the weight rows; the same product with k split over a
-    full workspace and unsplit over one that holds only the activations
-    (bit-identical: the split sums are added in order, and a k-chunk's
-    matrix-core sums do not depend on the split); the host's errors."""
+    """A prefix of the weight rows; the same product with k split (a full
+    workspace) and unsplit (one that holds only the activations), both
+    within the bound; a repeated call gives the same bits; the host's
+    errors."""
     raw, wt, x = setup(ctx, "q8_0", 300, 4096, 40, "f32", 5)
     dx = ctx.array(x)
     out = ctx.empty((40, 100), np.float32)
@@ -117,6 +117,9 @@ def test_qgemm_weight_row_prefix_split_and_errors(ctx):
     out2 = ctx.empty((40, 100), np.float32)
     ctx.qgemm(wt.packed.ptr, hip.GGML_Q8_0, 300, 4096, dx.ptr, 4096, 40, 100, ws.ptr, small, out2.ptr, 100, hip.F32)
     assert np.all(np.abs(out2.numpy() - want) <= bound(x.astype(np.float64), w, 4096) + 1e-30)
+    out3 = ctx.empty((40, 100), np.float32)
+    ctx.qgemm(wt.packed.ptr, hip.GGML_Q8_0, 300, 4096, dx.ptr, 4096, 40, 100, ws.ptr, wsb, out3.ptr, 100, hip.F32)
+    assert np.array_equal(out3.numpy().view(np.uint32), got.view(np.uint32))
     with pytest.raises(hip.CucaError, match="weight rows"):
         ctx.qgemm(wt.packed.ptr, hip.GGML_Q8_0, 300, 4096, dx.ptr, 4096, 40, 301, ws.ptr, wsb, out.ptr, 400, hip.F32)
     with pytest.raises(hip.CucaError, match="output row stride"):
