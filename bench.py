@@ -790,6 +790,76 @@ def qmm_bench(ctx, torch, reps=30):
     return res
 
 
+def qgemm_bench(ctx, torch, reps=10):
+    """The matrix-core quantized matmul (cuca_hip_qgemm / _qgemm_glu) at the
+    8B layer shapes, Q4_0, f32 activations, 32, 512 and 4096 rows (a decode
+    batch, a chunk of prefill, a prefill): kernel time of the call (the
+    activation prep, the matmul, the split reduce when there is one), its
+    f16 TFLOP/s against the 2.5 PFLOP/s dense peak.  Weights are generated
+    as GGUF bytes on the device; every output of sampled rows is checked
+    against the f64 product of the dequantised weights within the kernel's
+    bound (2^-10 + k 2^-24) sum |w x|."""
+    import numpy as np
+    from cuca_amd import hip
+    from cuca_amd import workloads as W
+    from oracle import oracle as O
+    gen = torch.Generator(device="cuda").manual_seed(7)
+    T = hip.GGML_Q4_0
+    res = {}
+    for name, n, k, glu in (("gate_up", 14336, 4096, True), ("down", 4096, 14336, False), ("q_o", 4096, 4096, False)):
+        raws = [W.quant_table_torch(gen, n, k, "q4_0", (0.001, 0.02)) for _ in range(2 if glu else 1)]
+        ws = []
+        for r in raws:
+            p = torch.empty(hip.qweight_bytes(T, n, k), dtype=torch.uint8, device="cuda")
+            ctx.qweight_pack(r.data_ptr(), T, n, k, p.data_ptr())
+            ws.append(p)
+        torch.cuda.synchronize()
+        for m in (32, 512, 4096):
+            x = torch.randn(m, k, device="cuda", generator=gen)
+            out = torch.empty(m, n, device="cuda")
+            wsb = hip.qgemm_workspace(T, n, k, m, glu)
+            wsp = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+
+            def call(i, x=x, out=out, wsp=wsp, wsb=wsb, m=m):
+                if glu:
+                    ctx.qgemm_glu(ws[0].data_ptr(), ws[1].data_ptr(), T, n, k, x.data_ptr(), k, m,
+                                  hip.ACT_SILU, 0.0, wsp.data_ptr(), wsb, out.data_ptr(), n, hip.F32)
+                else:
+                    ctx.qgemm(ws[0].data_ptr(), T, n, k, x.data_ptr(), k, m, n, wsp.data_ptr(), wsb,
+                              out.data_ptr(), n, hip.F32)
+            ms, parts = kernel_calls(ctx, call, reps, 2)
+            call(0)
+            torch.cuda.synchronize()
+            # check 3 token rows x 256 weight rows against the f64 product
+            toks = [0, m // 2, m - 1]
+            xs = x[toks].cpu().numpy().astype(np.float64)
+            rb = W.row_bytes("q4_0", k)
+            cols = np.arange(0, n, max(1, n // 256))[:256]
+            sel = torch.from_numpy(cols).to("cuda")
+            dq = []
+            for r in raws:
+                rows_b = r.view(n, rb).index_select(0, sel).cpu().numpy()
+                dq.append(np.stack([O.dequant_row(T, rows_b[i], 1.0, k) for i in range(cols.size)]).astype(np.float64))
+            got = out[toks][:, cols].cpu().numpy().astype(np.float64)
+            g = xs @ dq[0].T
+            bg = (2.0 ** -10 + k * 2.0 ** -24) * (np.abs(xs) @ np.abs(dq[0]).T)
+            if glu:
+                u = xs @ dq[1].T
+                bu = (2.0 ** -10 + k * 2.0 ** -24) * (np.abs(xs) @ np.abs(dq[1]).T)
+                a = g / (1.0 + np.exp(-g))
+                want, tol = a * u, 1.2 * bg * (np.abs(u) + bu) + np.abs(a) * bu + 1e-5 * np.abs(a * u)
+            else:
+                want, tol = g, bg
+            assert np.all(np.abs(got - want) <= tol + 1e-30), f"qgemm {name} m={m}"
+            flops = 2.0 * m * n * k * (2 if glu else 1)
+            res[f"{name}_q4_0_m{m}"] = dict(
+                kernels=[p for p, _ in parts], us=round(ms * 1000, 2), parts_us=[round(t * 1000, 2) for _, t in parts],
+                tflops=round(flops / (ms / 1e3) / 1e12, 1), mfma_frac=round(flops / (ms / 1e3) / 2.5e15, 4))
+        del ws, raws
+        torch.cuda.empty_cache()
+    return res
+
+
 def moe_bench(ctx, torch, reps=30):
     """Routed experts at config E (Qwen3-30B-A3B: 128 experts of ff 768 over
     hidden 2048, Q4_0, top 8): moe_up (gate/up + SwiGLU), moe_down (times the
@@ -1070,10 +1140,12 @@ def main():
             checked_rows += 2
         torch.cuda.empty_cache()
 
-    qmm = moe = head = None
+    qmm = moe = head = qgemm = None
     if not args.no_qmm:
         log("quantized matmuls (8B decode shapes)")
         qmm = qmm_bench(ctx, torch)
+        log("matrix-core quantized matmul (8B shapes, 32 / 512 / 4096 rows)")
+        qgemm = qgemm_bench(ctx, torch)
         log("routed experts (config E decode)")
         moe = moe_bench(ctx, torch)
         log("LM head + greedy / top-k")
@@ -1133,6 +1205,7 @@ def main():
         "rope_store_kv": kv,
         "paged_decode": attn,
         "qmm_decode": qmm,
+        "qgemm": qgemm,
         "moe_decode": moe,
         "end_of_step": head,
         "decode_us_per_layer": decode,
