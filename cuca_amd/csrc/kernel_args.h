@@ -165,13 +165,14 @@ typedef struct {
 typedef struct {
     const uint8_t *w, *w_up;    /* packed weights (gate/up for GLU)          */
     const void *x;              /* [m][ldx] f32 or f16                       */
-    uint16_t *xp;               /* workspace: x in slot order [m][kp] f16    */
+    uint16_t *xp;               /* workspace: x in slot order [mp][kp] f16,  */
+                                /* mp = n_ct * tile tokens, rows past m zero */
     float *part;                /* workspace: split sums [splits][g,u][m][rows] */
     void *out;                  /* [m][out_ld]                               */
     int64_t ldx, out_ld, row_bytes, kp;
     int32_t rows, m, k, nkc, n_rt, n_ct, kcs, splits;
     float clamp;
-    int32_t pad_;
+    int32_t mp;
 } QGemmArgs;
 
 /* Activation quantisation for the decode GEMV (Acts::new, qmm.rs:1272-1343):

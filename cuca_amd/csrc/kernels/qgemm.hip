@@ -26,11 +26,10 @@
 //         (dword t: biased bytes of elements l, l+16 of blocks 2t, 2t+1)
 //
 // Workgroup: 4 waves, 128 weight rows (32 per wave) x TM tokens (TM / 32
-// accumulator tiles per wave); k in chunks of 128 values (8 k-steps).  The
-// next chunk's weights and activations are loaded into registers while the
-// current chunk computes, and the activations written to the other LDS
-// buffer after it.  The grid is XCD-aware: an XCD's workgroups take row
-// tiles x, x + 8, ... each with all of its token tiles in a row.
+// accumulator tiles per wave); k in chunks of 128 values (8 k-steps).  While
+// a chunk computes, the next chunk's weights are loaded into registers and
+// its activations copied into the other LDS buffer.  The grid is XCD-aware
+// and grouped (qgemm_body).
 #include "common.h"
 
 typedef _Float16 qg_h2 __attribute__((ext_vector_type(2)));
@@ -40,7 +39,6 @@ typedef uint32_t qg_u2 __attribute__((ext_vector_type(2)));
 
 #define QG_ROWS 128       // weight rows per workgroup (32 per wave)
 #define QG_KC 128         // values per k-chunk: 8 k-steps of 16
-#define QG_XS (QG_KC + 8) // LDS row stride of the staged activations (f16)
 
 template <int FMT> struct QgFmt;
 template <> struct QgFmt<0> { // Q4_0: 4 lane chunks of a 512-value group per k-chunk
@@ -115,51 +113,83 @@ __device__ static inline qg_h8 qg_dequant(const QgA<FMT> &a, int s) {
 }
 
 // The activations rewritten once per call, before the matmul: f16, in the
-// slot order of the format (xp [m][kp], kp = 128 per k-chunk, zero past k).
-// One thread per unit (token, k-chunk, k-step s, half h) of 8 values:
-// the values at true positions base + 16 j.
+// slot order of the format (xp [n_ct * TM][kp], kp = 128 per k-chunk; zero
+// past k and in the rows past m, up to the whole tile).  One thread per unit
+// (token, k-chunk, k-step s, half h) of 8 values: the values at true
+// positions base + 16 j.
 template <typename T, int FMT> __device__ static inline void qgemm_prep_body(const QGemmArgs &a) {
     using F = QgFmt<FMT>;
     const int64_t u = (int64_t)blockIdx.x * CUCA_BLOCK + threadIdx.x;
     const int64_t per_row = (int64_t)a.nkc * 16;
-    if (u >= (int64_t)a.m * per_row) return;
+    if (u >= (int64_t)a.mp * per_row) return;
     const int tok = (int)(u / per_row), rem = (int)(u - (int64_t)tok * per_row);
     const int kc = rem >> 4, v = rem & 15, s = v >> 1, h = v & 1;
     const int g = kc / F::KCG, part = kc % F::KCG;
     int base;
     if (FMT == 0) base = 512 * g + 128 * (2 * h + (s & 1)) + 4 * part + (s >> 1);
     else base = 256 * g + 128 * h + 8 * part + s;
-    const T *row = reinterpret_cast<const T *>(a.x) + (int64_t)tok * a.ldx;
+    const T *row = reinterpret_cast<const T *>(a.x) + (int64_t)(tok < a.m ? tok : 0) * a.ldx;
     qg_h8 o;
 #pragma unroll
     for (int j = 0; j < 8; j++) {
         const int k = base + 16 * j;
-        o[j] = k < a.k ? (_Float16)(float)row[k] : (_Float16)0.0f;
+        o[j] = tok < a.m && k < a.k ? (_Float16)(float)row[k] : (_Float16)0.0f;
     }
     *reinterpret_cast<qg_h8 *>(a.xp + (int64_t)tok * a.kp + (int64_t)kc * QG_KC + 8 * (2 * s + h)) = o; // xp: f16 bits
 }
 
-// The staged activations of one k-chunk: TM tokens x 128 f16, 16-byte
-// units, thread tid taking units tid + 256 i (16 units per token).
-template <int TM> struct QgX {
-    u32x4 v[TM / 16];
-};
+// The activations of one k-chunk, TM tokens x 128 f16, copied from the
+// workspace straight into LDS (global_load_lds_dwordx4: lane L of a wave
+// writes 16 bytes at the wave's LDS address + 16 L).  A row is 256 bytes,
+// unpadded; its 16-byte unit v sits at position v ^ (row % 16), so that the
+// B-operand reads of 16 rows at one unit fall in different banks.  Wave w's
+// copy it fills rows 16 it + 4 w .. + 3.
+// The lane's part of the source offset, lane_off = (lane / 16) kp + 8 v, is
+// the same for every copy (row % 16 = (4 w + lane / 16) % 16).
 template <int TM>
-__device__ static inline void qg_load_x(const QGemmArgs &a, int tok0, int kc, QgX<TM> &o) {
+__device__ static inline void qg_copy_x(const QGemmArgs &a, int tok0, int kc, int wave, int lane_off,
+                                        _Float16 (*xs)[QG_KC]) {
 #pragma unroll
     for (int it = 0; it < TM / 16; it++) {
-        const int u = threadIdx.x + 256 * it;
-        const int c = u >> 4, v = u & 15;
-        const int tok = tok0 + c < a.m ? tok0 + c : a.m - 1; // rows past m: never stored
-        o.v[it] = *reinterpret_cast<const u32x4 *>(a.xp + (int64_t)tok * a.kp + (int64_t)kc * QG_KC + 8 * v);
+        const int c0 = 16 * it + 4 * wave; // wave-uniform
+        const uint16_t *src = a.xp + ((int64_t)(tok0 + c0) * a.kp + (int64_t)kc * QG_KC);
+        __builtin_amdgcn_global_load_lds(src + lane_off, &xs[c0][0], 16, 0, 0);
     }
 }
-template <int TM>
-__device__ static inline void qg_store_x(_Float16 (*xs)[QG_XS], const QgX<TM> &o) {
+
+// One k-chunk: the MFMAs over xc, while the next chunk's activations are
+// copied into xn and its weights loaded into ng / nu.
+template <int FMT, int TM, bool GLU>
+__device__ static inline void qg_chunk(const QGemmArgs &a, const uint8_t *wg, const uint8_t *wu, int tok0, int kc,
+                                       bool next, int wave, int lane, int lane_off, _Float16 (*xc)[QG_KC],
+                                       _Float16 (*xn)[QG_KC],
+                                       QgA<FMT> &ag, QgA<FMT> &au, qg_acc *acc, qg_acc *accu) {
+    constexpr int NT = TM / 32;
+    const int r = lane & 31, h = lane >> 5;
+    QgA<FMT> ng, nu;
+    if (next) {
+        qg_load_a<FMT>(wg, kc + 1, h, ng);
+        if (GLU) qg_load_a<FMT>(wu, kc + 1, h, nu);
+        qg_copy_x<TM>(a, tok0, kc + 1, wave, lane_off, xn);
+    }
 #pragma unroll
-    for (int it = 0; it < TM / 16; it++) {
-        const int u = threadIdx.x + 256 * it;
-        *reinterpret_cast<u32x4 *>(&xs[u >> 4][8 * (u & 15)]) = o.v[it];
+    for (int s = 0; s < 8; s++) {
+        const qg_h8 av = qg_dequant<FMT>(ag, s);
+        qg_h8 uv;
+        if (GLU) uv = qg_dequant<FMT>(au, s);
+        const int pos = 8 * ((2 * s + h) ^ (r & 15));
+#pragma unroll
+        for (int i = 0; i < NT; i++) {
+            const qg_h8 bv = *reinterpret_cast<const qg_h8 *>(&xc[i * 32 + r][pos]);
+            acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc[i], 0, 0, 0);
+            if (GLU) accu[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(uv, bv, accu[i], 0, 0, 0);
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(0); // the copies into xn have landed
+    __syncthreads();
+    if (next) {
+        ag = ng;
+        if (GLU) au = nu;
     }
 }
 
@@ -170,11 +200,18 @@ __device__ static inline void qg_store_x(_Float16 (*xs)[QG_XS], const QgX<TM> &o
 template <typename T, int FMT, int TM, bool GLU, int ACT, bool SPLIT>
 __device__ static inline void qgemm_body(const QGemmArgs &a) {
     constexpr int NT = TM / 32;
-    __shared__ __attribute__((aligned(16))) _Float16 xs[2][TM][QG_XS];
     const int split = SPLIT ? (int)blockIdx.y : 0;
+    // XCD x (workgroups x, x + 8, ...) takes row tiles x, x + 8, ... in
+    // groups of 8; a group's workgroups take its row tiles in turn, token
+    // tile by token tile, so that the workgroups resident on the XCD at once
+    // share their weight and activation tiles in its L2
     const int id = blockIdx.x, xcd = id & 7, kq = id >> 3;
-    const int rt = (kq / a.n_ct) * 8 + xcd, ct = kq % a.n_ct;
-    if (rt >= a.n_rt) return;
+    const int n_rx = (a.n_rt - xcd + 7) >> 3; // row tiles of this XCD
+    const int g = kq / (8 * a.n_ct), w = kq - g * 8 * a.n_ct;
+    const int gsz = min(8, n_rx - 8 * g);
+    if (gsz <= 0) return;
+    const int ct = w / gsz, rt = (8 * g + (w - ct * gsz)) * 8 + xcd;
+    if (ct >= a.n_ct) return;
     const int kc0 = split * a.kcs;
     const int kc1 = min(a.nkc, kc0 + a.kcs);
     if (kc0 >= kc1) return;
@@ -193,45 +230,32 @@ __device__ static inline void qgemm_body(const QGemmArgs &a) {
         acc[i] = qg_acc{};
         accu[i] = qg_acc{};
     }
-    QgA<FMT> ag, au, ng, nu;
-    QgX<TM> xn;
+    // two LDS buffers, separate objects so that the compiler sees the copy
+    // into one and the reads of the other do not overlap
+    __shared__ __attribute__((aligned(16))) _Float16 xs0[TM][QG_KC];
+    __shared__ __attribute__((aligned(16))) _Float16 xs1[TM][QG_KC];
+    QgA<FMT> ag, au;
     qg_load_a<FMT>(wg, kc0, h, ag);
     if (GLU) qg_load_a<FMT>(wu, kc0, h, au);
-    qg_load_x<TM>(a, tok0, kc0, xn);
-    qg_store_x<TM>(xs[0], xn);
+    const int lane_off = (lane >> 4) * (int)a.kp + 8 * ((lane & 15) ^ ((4 * wave + (lane >> 4)) & 15));
+    qg_copy_x<TM>(a, tok0, kc0, wave, lane_off, xs0);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    for (int kc = kc0; kc < kc1; kc++) {
-        const int buf = (kc - kc0) & 1;
-        const bool next = kc + 1 < kc1;
-        if (next) {
-            qg_load_a<FMT>(wg, kc + 1, h, ng);
-            if (GLU) qg_load_a<FMT>(wu, kc + 1, h, nu);
-            qg_load_x<TM>(a, tok0, kc + 1, xn);
-        }
-#pragma unroll
-        for (int s = 0; s < 8; s++) {
-            const qg_h8 av = qg_dequant<FMT>(ag, s);
-            qg_h8 uv;
-            if (GLU) uv = qg_dequant<FMT>(au, s);
-#pragma unroll
-            for (int i = 0; i < NT; i++) {
-                const qg_h8 bv = *reinterpret_cast<const qg_h8 *>(&xs[buf][i * 32 + r][s * 16 + 8 * h]);
-                acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc[i], 0, 0, 0);
-                if (GLU) accu[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(uv, bv, accu[i], 0, 0, 0);
-            }
-        }
-        if (next) qg_store_x<TM>(xs[buf ^ 1], xn);
-        __syncthreads();
-        if (next) {
-            ag = ng;
-            if (GLU) au = nu;
-        }
+    for (int kc = kc0; kc < kc1; kc += 2) {
+        qg_chunk<FMT, TM, GLU>(a, wg, wu, tok0, kc, kc + 1 < kc1, wave, lane, lane_off, xs0, xs1, ag, au, acc, accu);
+        if (kc + 1 < kc1)
+            qg_chunk<FMT, TM, GLU>(a, wg, wu, tok0, kc + 1, kc + 2 < kc1, wave, lane, lane_off, xs1, xs0, ag, au, acc, accu);
     }
-    // accumulator q of lane (r, h): weight row 8 (q / 4) + 4 h + q % 4, token r
+    // accumulator q of lane (r, h): weight row 8 (q / 4) + 4 h + q % 4, token r.
+    // The empty asm keeps a tile in the accumulator registers until its turn
+    // (after the previous tile's stores): copied out all at once, the tiles
+    // would set the kernel's register count.
     if (SPLIT) {
         // partial rows: [split][gate, up][m][rows] f32
 #pragma unroll
         for (int i = 0; i < NT; i++) {
+            asm volatile("" : "+a"(acc[i]));
+            if (GLU) asm volatile("" : "+a"(accu[i]));
             const int tok = tok0 + i * 32 + r;
             if (tok >= a.m) continue;
             float *pg = a.part + ((int64_t)split * (GLU ? 2 : 1) * a.m + tok) * a.rows;
@@ -248,6 +272,8 @@ __device__ static inline void qgemm_body(const QGemmArgs &a) {
     }
 #pragma unroll
     for (int i = 0; i < NT; i++) {
+        asm volatile("" : "+a"(acc[i]));
+        if (GLU) asm volatile("" : "+a"(accu[i]));
         const int tok = tok0 + i * 32 + r;
         if (tok >= a.m) continue;
         T *orow = reinterpret_cast<T *>(a.out) + (int64_t)tok * a.out_ld;

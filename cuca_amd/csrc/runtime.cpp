@@ -1190,13 +1190,24 @@ cuca_status cuca_hip_qmm_glu(cuca_hip_ctx *ctx, const void *gate, const void *up
 // sums (up to kQgMaxSplits splits of f32 rows, two per output with the GLU)
 // that grids of fewer workgroups than CUs use.
 constexpr int64_t kQgMaxSplits = 8;
+constexpr int64_t kQgMaxK = 1ll << 28; // in-kernel offsets of a few rows of kp values stay within int32
 
 static int64_t qgemm_kp(int g, int64_t k) {
     const int64_t ng = (k / 32 + g - 1) / g;
     return ng * g * 32;
 }
+// tokens per tile, and the activation rows of the workspace: whole tiles,
+// the rows past m zero
+static int qgemm_tm(int64_t m) { return m <= 32 ? 32 : m <= 64 ? 64 : 128; }
+static int64_t qgemm_mp(int64_t m) {
+    const int tm = qgemm_tm(m);
+    return (m + tm - 1) / tm * tm;
+}
+static size_t qgemm_xp_bytes(int g, int64_t k, int64_t m) {
+    return ((size_t)qgemm_mp(m) * (size_t)qgemm_kp(g, k) * 2 + 255) / 256 * 256;
+}
 static size_t qgemm_ws_bytes(int g, int64_t n, int64_t k, int64_t m, bool glu) {
-    const size_t xp = ((size_t)m * (size_t)qgemm_kp(g, k) * 2 + 255) / 256 * 256;
+    const size_t xp = qgemm_xp_bytes(g, k, m);
     const size_t part = m <= 2048 ? (size_t)kQgMaxSplits * (glu ? 2 : 1) * (size_t)m * (size_t)n * 4 : 0;
     return xp + part;
 }
@@ -1205,9 +1216,10 @@ cuca_status cuca_hip_qgemm_workspace(uint32_t ggml_type, int64_t n, int64_t k, i
     if (!bytes) return fail(nullptr, CUCA_INVALID_ARG, "null pointer");
     int g = 0, gb = 0;
     if (!qfmt(ggml_type, &g, &gb)) return fail(nullptr, CUCA_UNSUPPORTED, "qgemm: ggml type %u", ggml_type);
-    if (n <= 0 || k <= 0 || k % 32 != 0 || m < 0)
+    if (n <= 0 || k <= 0 || k % 32 != 0 || m < 0 || m > 0x7fffffffll)
         return fail(nullptr, CUCA_INVALID_ARG, "qgemm: bad shape %lld x %lld, %lld rows", (long long)n, (long long)k,
                     (long long)m);
+    if (k > kQgMaxK) return fail(nullptr, CUCA_UNSUPPORTED, "qgemm: rows of more than %lld values", (long long)kQgMaxK);
     *bytes = qgemm_ws_bytes(g, n, k, m, glu != 0);
     return CUCA_OK;
 }
@@ -1224,6 +1236,7 @@ static cuca_status qgemm_common(cuca_hip_ctx *ctx, const void *w, const void *w_
     if (rows <= 0 || rows > n)
         return fail(ctx, CUCA_INVALID_ARG, "qgemm: %lld weight rows of %lld", (long long)rows, (long long)n);
     if (m < 0 || m > 0x7fffffffll) return fail(ctx, CUCA_INVALID_ARG, "qgemm: bad activation row count %lld", (long long)m);
+    if (k > kQgMaxK) return fail(ctx, CUCA_UNSUPPORTED, "qgemm: rows of more than %lld values", (long long)kQgMaxK);
     if (ldx < k)
         return fail(ctx, CUCA_INVALID_ARG, "qgemm: activation row stride %lld shorter than %lld", (long long)ldx,
                     (long long)k);
@@ -1236,13 +1249,13 @@ static cuca_status qgemm_common(cuca_hip_ctx *ctx, const void *w, const void *w_
     if (!al16(w) || (w_up && !al16(w_up)) || !al16(ws))
         return fail(ctx, CUCA_INVALID_ARG, "packed weights and the workspace must be 16-byte aligned");
     const int64_t kp = qgemm_kp(g, k);
-    const size_t xp_bytes = ((size_t)m * (size_t)kp * 2 + 255) / 256 * 256;
+    const size_t xp_bytes = qgemm_xp_bytes(g, k, m);
     if (ws_bytes < xp_bytes)
         return fail(ctx, CUCA_INVALID_ARG, "qgemm: workspace of %zu bytes, %zu needed (cuca_hip_qgemm_workspace)",
                     ws_bytes, xp_bytes);
-    const int tm = m <= 32 ? 32 : m <= 64 ? 64 : 128;
+    const int tm = qgemm_tm(m);
     const int ti = tm == 32 ? 0 : tm == 64 ? 1 : 2;
-    const int64_t n_rt = (rows + 127) / 128, n_ct = (m + tm - 1) / tm;
+    const int64_t n_rt = (rows + 127) / 128, n_ct = qgemm_mp(m) / tm;
     const int64_t tiles = (n_rt + 7) / 8 * 8 * n_ct;
     const int64_t nkc = kp / 128;
     if (tiles > 0x7fffffffll) return fail(ctx, CUCA_UNSUPPORTED, "qgemm: grid too large");
@@ -1277,10 +1290,12 @@ static cuca_status qgemm_common(cuca_hip_ctx *ctx, const void *w, const void *w_
     a.kcs = (int32_t)kcs;
     a.splits = (int32_t)splits;
     a.clamp = clamp > 0.0f ? clamp : 0.0f;
+    a.mp = (int32_t)(n_ct * tm);
     const bool f16 = dtype == CUCA_F16, q8 = ggml_type == CUCA_GGML_Q8_0;
     static const Kernel prep_k[2][2] = {{cuca_qgemm_prep_f32_q4_0, cuca_qgemm_prep_f32_q8_0},
                                         {cuca_qgemm_prep_f16_q4_0, cuca_qgemm_prep_f16_q8_0}};
-    if ((st = launch(ctx, prep_k[f16][q8], div_up(m * nkc * 16, CUCA_BLOCK_THREADS), CUCA_BLOCK_THREADS, 0, a)) != CUCA_OK)
+    if ((st = launch(ctx, prep_k[f16][q8], div_up((int64_t)a.mp * nkc * 16, CUCA_BLOCK_THREADS), CUCA_BLOCK_THREADS, 0,
+                     a)) != CUCA_OK)
         return st;
     // [dtype][format][plain, silu, gelu][tokens per tile 32, 64, 128]
     static const Kernel table_k[2][2][3][3] = {

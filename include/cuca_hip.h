@@ -328,7 +328,8 @@ cuca_status cuca_hip_qmm_glu(cuca_hip_ctx *ctx, const void *gate, const void *up
  * ("qgemm: ..."); activations and outputs need no alignment; |d q| and |x|
  * within f16's range.
  * The workspace (device, 16-byte aligned) holds the activations rewritten as
- * f16 in the kernel's order and, for small grids, the f32 sums of a split
+ * f16 in the kernel's order (rows padded with zeros to a whole tile of 32,
+ * 64 or 128 rows) and, for small grids, the f32 sums of a split
  * of k that a second launch adds in a fixed order (deterministic for a
  * given shape, device and workspace size; the split changes the summation
  * order, within the same bound); cuca_hip_qgemm_workspace gives the bytes

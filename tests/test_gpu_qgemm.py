@@ -113,7 +113,7 @@ def test_qgemm_weight_row_prefix_split_and_errors(ctx):
     want = x.astype(np.float64) @ w.T
     got = out.numpy()
     assert np.all(np.abs(got - want) <= bound(x.astype(np.float64), w, 4096) + 1e-30)
-    small = (40 * 4096 * 2 + 255) // 256 * 256
+    small = (64 * 4096 * 2 + 255) // 256 * 256  # the activations, padded to a whole tile of 64 rows
     out2 = ctx.empty((40, 100), np.float32)
     ctx.qgemm(wt.packed.ptr, hip.GGML_Q8_0, 300, 4096, dx.ptr, 4096, 40, 100, ws.ptr, small, out2.ptr, 100, hip.F32)
     assert np.all(np.abs(out2.numpy() - want) <= bound(x.astype(np.float64), w, 4096) + 1e-30)
