@@ -128,7 +128,13 @@ template <> __device__ inline void qmm_load8<_Float16>(const _Float16 *p, float 
     for (int i = 0; i < 8; i++) v[i] = (float)a[i];
 }
 
-template <int MT, bool GLU> struct QmmLds {
+// 16-byte aligned, so that every 16-byte operand read is one ds_read_b128:
+// with the 8-byte alignment of its members the compiler split them into
+// ds_read2_b64 pairs, which lost 35-40 % of the LDS cycles to bank
+// conflicts (SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE) at this lane stride;
+// ds_read_b128 reads it conflict-free.  Measured on MI355X: down 4096 x
+// 14336 Q4_0 at one row 17.7 -> 14.9 us, gate+up 23.0 -> 20.0 us.
+template <int MT, bool GLU> struct alignas(16) QmmLds {
     using S = QShape<MT>;
     static constexpr int SB = S::PRE_S ? 2 : 1;   // buffers of s
     static constexpr int WB = S::PRE_S ? 1 : 2;   // buffers of xs, ws
