@@ -532,8 +532,8 @@ class DecodeStep:
     hidden 4096, 32 query / 8 K/V heads of 128, FFN 14336, vocab 128256),
     f32 activations, every op a kernel of this library:
       embed (Q8_0 table) ->
-      32 layers of [residual + attention RMSNorm, Q and fused K|V
-        projections (qmm), RoPE + paged K/V store of the new token, paged
+      32 layers of [residual + attention RMSNorm, the fused Q|K|V
+        projection (qmm), RoPE + paged K/V store of the new token, paged
         decode attention over ctx_len keys, o projection, residual + FFN
         RMSNorm, gate/up projections with SwiGLU (qmm_glu), down projection]
       -> residual + final RMSNorm -> LM head (Q8_0) -> argmax.
@@ -573,7 +573,7 @@ class DecodeStep:
         self.L = []
         for _ in range(layers):
             self.L.append(dict(
-                wq=packed(nq * d, H, qtype, (0.001, 0.01)), wkv=packed(2 * nk * d, H, qtype, (0.001, 0.01)),
+                wqkv=packed((nq + 2 * nk) * d, H, qtype, (0.001, 0.01)),
                 wo=packed(H, nq * d, qtype, (0.001, 0.01)), wg=packed(F, H, qtype, (0.001, 0.01)),
                 wu=packed(F, H, qtype, (0.001, 0.01)), wd=packed(H, F, qtype, (0.0005, 0.005)),
                 n1=1 + 0.02 * r(H), n2=1 + 0.02 * r(H),
@@ -581,7 +581,7 @@ class DecodeStep:
         self.nout = 1 + 0.02 * r(H)
         self.ids = torch.randint(0, self.vocab, (n,), device=dev, generator=gen, dtype=torch.int32)
         self.x, self.h, self.ffn = r(n, H), r(n, H), r(n, H)
-        self.q, self.kv, self.o, self.attn = r(n, nq * d), r(n, 2 * nk * d), r(n, nq * d), r(n, H)
+        self.qkv, self.o, self.attn = r(n, (nq + 2 * nk) * d), r(n, nq * d), r(n, H)
         self.act = r(n, F)
         self.logits = torch.empty((n, self.vocab), device=dev)
         self.out_ids = torch.empty((n,), device=dev, dtype=torch.int32)
@@ -603,11 +603,11 @@ class DecodeStep:
         self.mm = mm
         if mm == "qgemm":
             self.qg_bytes = max([hip.qgemm_workspace(T, rows, cols, n, glu) for rows, cols, glu in (
-                (nq * d, H, False), (2 * nk * d, H, False), (H, nq * d, False), (F, H, True), (H, F, False))]
+                ((nq + 2 * nk) * d, H, False), (H, nq * d, False), (F, H, True), (H, F, False))]
                 + [hip.qgemm_workspace(hip.GGML_Q8_0, self.vocab, H, n, False)])
             self.qg_ws = torch.empty(self.qg_bytes, dtype=torch.uint8, device=dev)
-        self.weight_bytes = sum(t.numel() for l in self.L for t in (l["wq"], l["wkv"], l["wo"], l["wg"],
-                                                                      l["wu"], l["wd"]))
+        self.weight_bytes = sum(t.numel() for l in self.L for t in (l["wqkv"], l["wo"], l["wg"], l["wu"],
+                                                                      l["wd"]))
 
     def mat(self, w, rows, cols, x, out):
         if self.mm == "qgemm":
@@ -624,16 +624,19 @@ class DecodeStep:
         for l in self.L:
             c.add_rmsnorm(self.x.data_ptr(), self.ffn.data_ptr(), l["n1"].data_ptr(), None, eps, eps, 1.0,
                           n, H, self.x.data_ptr(), self.h.data_ptr(), f32)
-            self.mat(l["wq"], nq * d, H, self.h, self.q)
-            self.mat(l["wkv"], 2 * nk * d, H, self.h, self.kv)
-            c.rope_store_kv(self.q.data_ptr(), nq * d, self.kv.data_ptr(), 2 * nk * d,
-                            self.kv.data_ptr() + 4 * nk * d, 2 * nk * d, n, nq, nk, d, d, hip.ROPE_NORM,
-                            self.cos.data_ptr(), self.sin.data_ptr(), 8192, self.pos.data_ptr(), None, None,
-                            0, eps, l["pk"].data_ptr(), l["pv"].data_ptr(), self.n_blocks,
-                            self.slots.data_ptr(), f32)
-            c.paged_decode(self.q.data_ptr(), l["pk"].data_ptr(), l["pv"].data_ptr(), self.n_blocks,
+            # one Q|K|V projection; RoPE, the K/V store and the attention
+            # read their heads in place from its rows
+            qkv_ld = (nq + 2 * nk) * d
+            self.mat(l["wqkv"], qkv_ld, H, self.h, self.qkv)
+            q_ptr = self.qkv.data_ptr()
+            c.rope_store_kv(q_ptr, qkv_ld, q_ptr + 4 * nq * d, qkv_ld, q_ptr + 4 * (nq + nk) * d, qkv_ld,
+                            n, nq, nk, d, d, hip.ROPE_NORM, self.cos.data_ptr(), self.sin.data_ptr(), 8192,
+                            self.pos.data_ptr(), None, None, 0, eps, l["pk"].data_ptr(), l["pv"].data_ptr(),
+                            self.n_blocks, self.slots.data_ptr(), f32)
+            c.paged_decode(q_ptr, l["pk"].data_ptr(), l["pv"].data_ptr(), self.n_blocks,
                            self.tables.data_ptr(), self.max_blocks, self.ranges.data_ptr(), n, nq, nk, d,
-                           self.scale, self.ws.data_ptr(), self.ws_bytes, self.o.data_ptr(), f32)
+                           self.scale, self.ws.data_ptr(), self.ws_bytes, self.o.data_ptr(), f32,
+                           q_ld=qkv_ld)
             self.mat(l["wo"], H, nq * d, self.o, self.attn)
             c.add_rmsnorm(self.x.data_ptr(), self.attn.data_ptr(), l["n2"].data_ptr(), None, eps, eps, 1.0,
                           n, H, self.x.data_ptr(), self.h.data_ptr(), f32)

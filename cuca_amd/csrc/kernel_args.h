@@ -105,7 +105,7 @@ typedef struct {
  * from below (it sizes the workspace). */
 #define CUCA_ATTN_MIN_PART 64
 typedef struct {
-    const void *q;          /* [rows, n_head, d]                            */
+    const void *q;          /* [rows][q_ld]: n_head heads of d per row      */
     const void *pool_k;     /* [n_blocks, n_kv, 16, d]                      */
     const void *pool_v;
     const uint32_t *tables; /* [rows, max_blocks]                           */
@@ -113,6 +113,7 @@ typedef struct {
     float *part;
     void *out;              /* [rows, n_head, d]                            */
     unsigned long long *status;
+    int64_t q_ld;           /* row stride of q in elements                  */
     int64_t n_blocks;
     int32_t rows, n_head, n_kv, head_dim;
     int32_t max_blocks, max_parts;

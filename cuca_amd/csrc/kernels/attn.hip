@@ -91,8 +91,15 @@ __device__ static inline void attn_split_body(const AttnArgs &a) {
     constexpr int LPP = S::LPP, CP = S::CP, CPL = S::CPL;
     constexpr int KCH = D / VP / LPP;      // 16-byte K chunks per lane
     constexpr int VW = CPL * (int)sizeof(T) <= 4 ? 1 : CPL * (int)sizeof(T) / 4; // dwords per value load
-    // the group's query heads: f16 pairs (f16) or f32, as the pools
-    __shared__ __align__(16) uint32_t qs[G * D / (sizeof(T) == 2 ? 2 : 1)];
+    // the group's query heads: f16 pairs (f16) or f32, as the pools, one
+    // slice of SL dwords per (head, lane of a position).  With several lanes
+    // per position the slices are padded by 16 bytes, so that the lanes of a
+    // position read from different banks (unpadded, a 256-byte slice put
+    // them on the same banks: 28 % of the f32 kernel's LDS cycles were bank
+    // conflicts, SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE)
+    constexpr int SL = D / LPP / (sizeof(T) == 2 ? 2 : 1);
+    constexpr int SLP = LPP > 1 ? SL + 4 : SL;
+    __shared__ __align__(16) uint32_t qs[G * LPP * SLP];
     __shared__ __align__(16) float wsh[4][CP][G];        // each wave's weights
     __shared__ __align__(16) float red[4][G][D + 2];     // each wave's partial
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / CUCA_WAVE);
@@ -102,9 +109,9 @@ __device__ static inline void attn_split_body(const AttnArgs &a) {
     const int row = rk / a.n_kv, kvh = rk - row * a.n_kv;
     {
         const uint32_t *qg = reinterpret_cast<const uint32_t *>(
-            reinterpret_cast<const T *>(a.q) + ((int64_t)row * a.n_head + (int64_t)kvh * G) * D);
+            reinterpret_cast<const T *>(a.q) + (int64_t)row * a.q_ld + (int64_t)kvh * G * D);
         constexpr int NW = G * D / (sizeof(T) == 2 ? 2 : 1);
-        for (int i = threadIdx.x; i < NW; i += CUCA_BLOCK) qs[i] = qg[i];
+        for (int i = threadIdx.x; i < NW; i += CUCA_BLOCK) qs[(i / SL) * SLP + i % SL] = qg[i];
     }
     const int lo = a.ranges[2 * row], hi = a.ranges[2 * row + 1];
     const bool valid = attn_range_ok(a, lo, hi);
@@ -177,7 +184,7 @@ __device__ static inline void attn_split_body(const AttnArgs &a) {
 #pragma unroll
         for (int j = 0; j < KCH; j++) {
             if constexpr (sizeof(T) == 2) {
-                const u32x4 qq = *reinterpret_cast<const u32x4 *>(qs + g * (D / 2) + sub * (D / LPP / 2) + j * (VP / 2));
+                const u32x4 qq = *reinterpret_cast<const u32x4 *>(qs + (g * LPP + sub) * SLP + j * (VP / 2));
                 s[g] = __builtin_amdgcn_fdot2(as_h2(kraw[j].x),
                                               as_h2(qq.x), s[g], false);
                 s[g] = __builtin_amdgcn_fdot2(as_h2(kraw[j].y),
@@ -188,7 +195,7 @@ __device__ static inline void attn_split_body(const AttnArgs &a) {
                                               as_h2(qq.w), s[g], false);
             } else {
                 const f32x4 qq = *reinterpret_cast<const f32x4 *>(
-                    reinterpret_cast<const float *>(qs) + g * D + sub * (D / LPP) + j * VP);
+                    reinterpret_cast<const float *>(qs) + (g * LPP + sub) * SLP + j * VP);
                 const f32x4 kk = __builtin_bit_cast(f32x4, kraw[j]);
                 s[g] = fmaf(qq.x, kk.x, s[g]);
                 s[g] = fmaf(qq.y, kk.y, s[g]);
@@ -310,7 +317,7 @@ __device__ static inline void attn_split_generic_body(const AttnArgs &a) {
     bool ok;
     const int64_t prow = attn_pool_row(a, row, kvh, p, ok);
     if (!ok && live) record_bad(a.status + CUCA_STATUS_KV_RANGE, row, (uint32_t)p);
-    const T *qh = reinterpret_cast<const T *>(a.q) + ((int64_t)row * a.n_head + head) * D;
+    const T *qh = reinterpret_cast<const T *>(a.q) + (int64_t)row * a.q_ld + (int64_t)head * D;
     float s = 0.0f;
     for (int e = 0; e < D; e++) s += (float)qh[e] * load1<T>(a.pool_k, prow * D + e);
     const float sc = live ? s * a.scale : -INFINITY;
@@ -328,12 +335,10 @@ __device__ static inline void attn_split_generic_body(const AttnArgs &a) {
     }
 }
 
-// Merge: one wave per (row, query head); lane owns columns lane, lane + 64, ...
+// Merge of one (row, query head) = job by one wave; lane owns columns lane,
+// lane + 64, ...
 template <typename T, int MAXC>
-__device__ static inline void attn_merge_body(const AttnArgs &a) {
-    const int wave = threadIdx.x / CUCA_WAVE, lane = threadIdx.x & (CUCA_WAVE - 1);
-    const int64_t job = (int64_t)blockIdx.x * (CUCA_BLOCK / CUCA_WAVE) + wave;
-    if (job >= (int64_t)a.rows * a.n_head) return;
+__device__ static inline void attn_merge_job(const AttnArgs &a, int64_t job, int lane) {
     const int row = (int)(job / a.n_head);
     const int D = a.head_dim;
     const int lo = a.ranges[2 * row], hi = a.ranges[2 * row + 1];
@@ -387,6 +392,15 @@ __device__ static inline void attn_merge_body(const AttnArgs &a) {
         const int e = lane + k * CUCA_WAVE;
         if (e < D) store1<T>(o, e, acc[k] / total);
     }
+}
+
+// Merge pass: one wave per (row, query head).
+template <typename T, int MAXC>
+__device__ static inline void attn_merge_body(const AttnArgs &a) {
+    const int wave = threadIdx.x / CUCA_WAVE, lane = threadIdx.x & (CUCA_WAVE - 1);
+    const int64_t job = (int64_t)blockIdx.x * (CUCA_BLOCK / CUCA_WAVE) + wave;
+    if (job >= (int64_t)a.rows * a.n_head) return;
+    attn_merge_job<T, MAXC>(a, job, lane);
 }
 
 #define CUCA_ATTN(NAME, BODY, ...)                                                         \

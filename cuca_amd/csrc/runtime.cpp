@@ -756,8 +756,8 @@ cuca_status cuca_hip_paged_decode_workspace(int64_t rows, int32_t n_head, int32_
     return CUCA_OK;
 }
 
-cuca_status cuca_hip_paged_decode(cuca_hip_ctx *ctx, const void *q, const void *pool_k, const void *pool_v,
-                                  int64_t n_blocks, const uint32_t *tables, int64_t max_blocks,
+cuca_status cuca_hip_paged_decode(cuca_hip_ctx *ctx, const void *q, int64_t q_ld, const void *pool_k,
+                                  const void *pool_v, int64_t n_blocks, const uint32_t *tables, int64_t max_blocks,
                                   const int32_t *ranges, int64_t rows, int32_t n_head, int32_t n_kv,
                                   int32_t head_dim, float scale, void *workspace, size_t workspace_bytes,
                                   void *out, cuca_dtype dtype) {
@@ -775,6 +775,11 @@ cuca_status cuca_hip_paged_decode(cuca_hip_ctx *ctx, const void *q, const void *
     if (rows == 0) return CUCA_OK;
     if (!q || !pool_k || !pool_v || !tables || !ranges || !out || !workspace)
         return fail(ctx, CUCA_INVALID_ARG, "null pointer");
+    if (q_ld < (int64_t)n_head * head_dim)
+        return fail(ctx, CUCA_INVALID_ARG, "q row stride %lld below %d heads of %d", (long long)q_ld, n_head,
+                    head_dim);
+    if (((size_t)q_ld * esize(dtype)) % 4 != 0 || (reinterpret_cast<uintptr_t>(q) & 3) != 0)
+        return fail(ctx, CUCA_INVALID_ARG, "q rows must be 4-byte aligned");
     size_t need = 0;
     cuca_hip_paged_decode_workspace(rows, n_head, head_dim, max_blocks, &need);
     if (workspace_bytes < need)
@@ -801,6 +806,7 @@ cuca_status cuca_hip_paged_decode(cuca_hip_ctx *ctx, const void *q, const void *
     if (rows * n_head * parts > 0x7fffffffll) return fail(ctx, CUCA_UNSUPPORTED, "too many attention parts");
     AttnArgs a{};
     a.q = q;
+    a.q_ld = q_ld;
     a.pool_k = pool_k;
     a.pool_v = pool_v;
     a.tables = tables;

@@ -69,8 +69,8 @@ SIGNATURES = {
                                      _st]),
     "cuca_hip_kv_slots": (_st, [_p, _i64, _i64, _i64, _i64, _p]),
     "cuca_hip_paged_decode_workspace": (_st, [_i64, _i32, _i32, _i64, ctypes.POINTER(_sz)]),
-    "cuca_hip_paged_decode": (_st, [_p, _p, _p, _p, _i64, _p, _i64, _p, _i64, _i32, _i32, _i32,
-                                    _f32, _p, _sz, _p, _st]),
+    "cuca_hip_paged_decode": (_st, [_p, _p, _i64, _p, _p, _i64, _p, _i64, _p, _i64, _i32, _i32,
+                                    _i32, _f32, _p, _sz, _p, _st]),
     "cuca_hip_rope_tables": (_st, [ctypes.POINTER(RopeSpecC), _p, _i64, _p, _p]),
     "cuca_hip_qweight_bytes": (_st, [_u32, _i64, _i64, ctypes.POINTER(_sz)]),
     "cuca_hip_qweight_pack": (_st, [_p, _p, _u32, _i64, _i64, _p]),
@@ -323,8 +323,12 @@ class Context:
                                         eps, dtype))
 
     def paged_decode(self, q, pool_k, pool_v, n_blocks, tables, max_blocks, ranges, rows, n_head,
-                     n_kv, head_dim, scale, workspace, workspace_bytes, out, dtype):
-        self.check(self.L.cuca_hip_paged_decode(self.ptr, q, pool_k, pool_v, n_blocks, tables,
+                     n_kv, head_dim, scale, workspace, workspace_bytes, out, dtype, q_ld=None):
+        """q_ld: the row stride of q in elements (default: packed rows of
+        n_head * head_dim)."""
+        if q_ld is None:
+            q_ld = n_head * head_dim
+        self.check(self.L.cuca_hip_paged_decode(self.ptr, q, q_ld, pool_k, pool_v, n_blocks, tables,
                                                 max_blocks, ranges, rows, n_head, n_kv, head_dim,
                                                 scale, workspace, workspace_bytes, out, dtype))
 

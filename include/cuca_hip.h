@@ -250,7 +250,9 @@ cuca_status cuca_hip_kv_slots(const uint32_t *table, int64_t table_len, int64_t 
  * paged_attention_decode, paged_kernel.rs:92-282, on a step's stacked
  * rows, gpu.rs:6002-6011; the CPU's attend_paged_rows for one row,
  * cpu/paged_attn.rs:105-290).
- *   q      : [rows, n_head, head_dim] of dtype
+ *   q      : [rows][q_ld] of dtype, n_head heads of head_dim at the start
+ *            of each row (q_ld = n_head * head_dim when packed; a fused QKV
+ *            projection's row otherwise); rows 4-byte aligned
  *   pools  : [n_blocks, n_kv, 16, head_dim] of dtype
  *   tables : device u32 [rows, max_blocks] block ids; ranges: device int32
  *            [rows, 2] = (lo, hi) key positions relative to the table (the
@@ -266,8 +268,9 @@ cuca_status cuca_hip_kv_slots(const uint32_t *table, int64_t table_len, int64_t 
  * output is then unspecified; zeros for a bad range). */
 cuca_status cuca_hip_paged_decode_workspace(int64_t rows, int32_t n_head, int32_t head_dim,
                                             int64_t max_blocks, size_t *bytes);
-cuca_status cuca_hip_paged_decode(cuca_hip_ctx *ctx, const void *q, const void *pool_k,
-                                  const void *pool_v, int64_t n_blocks, const uint32_t *tables,
+cuca_status cuca_hip_paged_decode(cuca_hip_ctx *ctx, const void *q, int64_t q_ld,
+                                  const void *pool_k, const void *pool_v, int64_t n_blocks,
+                                  const uint32_t *tables,
                                   int64_t max_blocks, const int32_t *ranges, int64_t rows,
                                   int32_t n_head, int32_t n_kv, int32_t head_dim, float scale,
                                   void *workspace, size_t workspace_bytes, void *out,

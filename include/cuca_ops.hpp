@@ -379,7 +379,7 @@ class KvPool {
             workspace = &own;
         }
         Tensor out(ctx, {rows, (int64_t)n_head, d}, q.dtype());
-        ctx.check(cuca_hip_paged_decode(ctx.raw(), q.data(), k_.data(), v_.data(), n_blocks_,
+        ctx.check(cuca_hip_paged_decode(ctx.raw(), q.data(), (int64_t)n_head * d, k_.data(), v_.data(), n_blocks_,
                                         static_cast<const uint32_t *>(tables.data()), max_blocks,
                                         static_cast<const int32_t *>(ranges.data()), rows, n_head,
                                         (int32_t)k_.dim(1), (int32_t)d, scale, workspace->data(),

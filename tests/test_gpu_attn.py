@@ -163,3 +163,95 @@ def test_config_c_at_8192_keys(ctx):
     pv = rng.standard_normal((n_blocks, nk, 16, d)).astype(np.float16)
     q = rng.standard_normal((rows, nq, d)).astype(np.float16)
     check(ctx, q, pk, pv, tables, ranges, nq, 1.0 / np.sqrt(d))
+
+
+def decode_raw(ctx, q_dev, q_ld, pool, tables, ranges, n_head, scale, out, ws, ws_bytes, dtype):
+    ctx.paged_decode(q_dev.ptr, pool.k.ptr, pool.v.ptr, pool.n_blocks, tables.ptr, tables.shape[1],
+                     ranges.ptr, ranges.shape[0], n_head, pool.n_kv_head, pool.head_dim, scale,
+                     ws.ptr, ws_bytes, out.ptr, dtype, q_ld=q_ld)
+
+
+def test_query_rows_read_in_place_from_a_fused_qkv_row(ctx):
+    """q at the start of wider rows (a fused Q|K|V projection's output, row
+    stride q_ld): the same bits as the packed rows."""
+    rng = np.random.default_rng(11)
+    nq, nk, d, n_blocks = 32, 8, 128, 64
+    for dtype in ("f32", "f16"):
+        tables, ranges = make_batch(rng, [300, 17, 64], n_blocks, 24)
+        pk = rng.standard_normal((n_blocks, nk, 16, d)).astype(NP[dtype])
+        pv = rng.standard_normal((n_blocks, nk, 16, d)).astype(NP[dtype])
+        q = rng.standard_normal((3, nq, d)).astype(NP[dtype])
+        packed = run(ctx, q, pk, pv, tables, ranges, nq, 0.09)
+        q_ld = (nq + 2 * nk) * d
+        wide = rng.standard_normal((3, q_ld)).astype(NP[dtype])
+        wide[:, :nq * d] = q.reshape(3, -1)
+        pool = ops.KvPool(ctx, n_blocks, nk, d, NP[dtype])
+        pool.k.upload(pk)
+        pool.v.upload(pv)
+        need = hip.paged_decode_workspace(3, nq, d, tables.shape[1])
+        ws, out = ctx.empty((need,), np.uint8), ctx.empty((3, nq, d), NP[dtype])
+        decode_raw(ctx, ctx.array(wide), q_ld, pool, ctx.array(tables), ctx.array(ranges), nq, 0.09,
+                   out, ws, need, hip.dtype_code(NP[dtype]))
+        ctx.check_device()
+        assert_bits_equal(out.numpy(), packed, f"strided q {dtype}")
+    with pytest.raises(hip.CucaError, match="q row stride"):
+        decode_raw(ctx, ctx.array(wide), nq * d - 1, pool, ctx.array(tables), ctx.array(ranges), nq,
+                   0.09, out, ws, need, hip.F16)
+
+
+def test_many_rows_keep_each_rows_bits(ctx):
+    """8200 rows x 8 KV heads (65600 (row, head) merges, ragged ranges of 1
+    to 608 keys): the first rows carry the bits the same rows get in a call
+    of 64 rows, and sampled rows meet the oracle bar."""
+    rng = np.random.default_rng(12)
+    nh, nk, d, n_blocks, width = 8, 8, 64, 48, 38
+    rows = 8200
+    pk = rng.standard_normal((n_blocks, nk, 16, d)).astype(np.float32)
+    pv = rng.standard_normal((n_blocks, nk, 16, d)).astype(np.float32)
+    tables = np.stack([rng.choice(n_blocks, width, replace=False) for _ in range(rows)]).astype(np.uint32)
+    hi = rng.integers(1, width * 16 + 1, rows)
+    lo = np.where(np.arange(rows) % 4 == 0, np.maximum(hi - 300, 0), 0)
+    ranges = np.stack([lo, hi], 1).astype(np.int32)
+    q = rng.standard_normal((rows, nh, d)).astype(np.float32)
+    big = run(ctx, q, pk, pv, tables, ranges, nh, 0.125)
+    small = run(ctx, q[:64], pk, pv, tables[:64], ranges[:64], nh, 0.125)
+    assert_bits_equal(small, big[:64], "64-row call vs 8200-row call")
+    pick = np.array([0, 1, 2, 3, 4097, rows - 1])
+    want = O.paged_attention(q[pick], tables[pick], ranges[pick], pk, pv, 0.125, threads=8)
+    assert_close(big[pick], want, floor=floor_of(tables[pick], ranges[pick], pv, nh), what="attention")
+
+
+def test_repeated_calls_and_graph_replays_keep_their_bits(ctx):
+    """Calls in a row and replays of a captured call (split and merge
+    launches; eager work and synchronizations between the replays) all give
+    the first call's bits."""
+    rng = np.random.default_rng(13)
+    nq, nk, d, n_blocks = 32, 8, 128, 96
+    tables, ranges = make_batch(rng, [1000, 1, 129, 64, 500], n_blocks, 64)
+    pk = rng.standard_normal((n_blocks, nk, 16, d)).astype(np.float32)
+    pv = rng.standard_normal((n_blocks, nk, 16, d)).astype(np.float32)
+    q = rng.standard_normal((5, nq, d)).astype(np.float32)
+    first = check(ctx, q, pk, pv, tables, ranges, nq, 0.1)
+    pool = ops.KvPool(ctx, n_blocks, nk, d, np.float32)
+    pool.k.upload(pk)
+    pool.v.upload(pv)
+    need = hip.paged_decode_workspace(5, nq, d, tables.shape[1])
+    ws, out = ctx.empty((need,), np.uint8), ctx.empty((5, nq, d), np.float32)
+    dq, dt, dr = ctx.array(q), ctx.array(tables), ctx.array(ranges)
+    for i in range(3):
+        decode_raw(ctx, dq, nq * d, pool, dt, dr, nq, 0.1, out, ws, need, hip.F32)
+        ctx.check_device()
+        assert_bits_equal(out.numpy(), first, f"call {i}")
+    ctx.graph_begin()
+    decode_raw(ctx, dq, nq * d, pool, dt, dr, nq, 0.1, out, ws, need, hip.F32)
+    g = ctx.graph_end()
+    try:
+        for i in range(4):
+            out.upload(np.zeros((5, nq, d), np.float32))
+            g.launch()
+            ctx.sync()
+            assert_bits_equal(out.numpy(), first, f"replay {i}")
+            decode_raw(ctx, dq, nq * d, pool, dt, dr, nq, 0.1, out, ws, need, hip.F32)  # eager between
+            ctx.check_device()
+    finally:
+        g.destroy()
