@@ -335,6 +335,10 @@ __device__ static inline void attn_split_generic_body(const AttnArgs &a) {
     }
 }
 
+// Parts a merge holds in registers per lane (up to 256 parts per row: 32768
+// f16 or 16384 f32 keys at head_dim 128); longer rows walk them in turn.
+#define MERGE_PL 4
+
 // Merge of one (row, query head) = job by one wave; lane owns columns lane,
 // lane + 64, ...
 template <typename T, int MAXC>
@@ -350,39 +354,111 @@ __device__ static inline void attn_merge_job(const AttnArgs &a, int64_t job, int
     const int np = (hi - (lo & ~15) + a.part_positions - 1) / a.part_positions;
     const int64_t stride = D + 2;
     const float *pp = a.part + job * a.max_parts * stride;
-    // the global maximum, then each lane's parts' weighted sums (in order)
-    float mx = -INFINITY;
-    for (int c = lane; c < np; c += CUCA_WAVE) mx = fmaxf(mx, pp[c * stride + D]);
-    const float top = wave_max(mx);
-    float t = 0.0f;
-    for (int c = lane; c < np; c += CUCA_WAVE) t += pp[c * stride + D + 1] * expf(pp[c * stride + D] - top);
-    const float total = group_sum<CUCA_WAVE>(t);
     float acc[MAXC]; // columns per lane: head_dim <= 64 MAXC
 #pragma unroll
     for (int k = 0; k < MAXC; k++) acc[k] = 0.0f;
-    for (int c0 = 0; c0 < np; c0 += CUCA_WAVE) {
-        // lane l holds the weight of part c0 + l
-        const int cl = c0 + lane;
-        const float wl = cl < np ? expf(pp[cl * stride + D] - top) : 0.0f;
-        const int nc = min(CUCA_WAVE, np - c0);
-        for (int j0 = 0; j0 < nc; j0 += 16) {
-            float v[16][MAXC];
+    float total;
+    if (np <= MERGE_PL * CUCA_WAVE) {
+        // Every load is issued at once: this lane's (max, sum) of parts
+        // lane, lane + 64, ... and the values of the first R parts, so the
+        // merge waits for one round of loads (walking the parts' maxima, sums
+        // and values in turn made four).  The arithmetic and its order are
+        // those of the loop below.
+        constexpr int R = MAXC <= 2 ? 32 : MAXC == 4 ? 16 : 0; // whole blocks of 16 parts
+        float mv[MERGE_PL], sv[MERGE_PL];
 #pragma unroll
-            for (int jj = 0; jj < 16; jj++) {
-                const float *pc = pp + (int64_t)(c0 + min(j0 + jj, nc - 1)) * stride;
+        for (int q = 0; q < MERGE_PL; q++) {
+            const int c = lane + q * CUCA_WAVE;
+            mv[q] = c < np ? pp[(int64_t)c * stride + D] : -INFINITY;
+            sv[q] = c < np ? pp[(int64_t)c * stride + D + 1] : 0.0f;
+        }
+        float v0[R > 0 ? R : 1][MAXC];
 #pragma unroll
-                for (int k = 0; k < MAXC; k++) {
-                    const int e = lane + k * CUCA_WAVE;
-                    v[jj][k] = e < D ? pc[e] : 0.0f;
+        for (int jj = 0; jj < R; jj++) {
+            const float *pc = pp + (int64_t)min(jj, np - 1) * stride;
+#pragma unroll
+            for (int k = 0; k < MAXC; k++) {
+                const int e = lane + k * CUCA_WAVE;
+                v0[jj][k] = e < D ? pc[e] : 0.0f;
+            }
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int q = 0; q < MERGE_PL; q++)
+            if (lane + q * CUCA_WAVE < np) mx = fmaxf(mx, mv[q]);
+        const float top = wave_max(mx);
+        float t = 0.0f;
+#pragma unroll
+        for (int q = 0; q < MERGE_PL; q++)
+            if (lane + q * CUCA_WAVE < np) t += sv[q] * expf(mv[q] - top);
+        total = group_sum<CUCA_WAVE>(t);
+#pragma unroll
+        for (int q = 0; q < MERGE_PL; q++) {
+            const int c0 = q * CUCA_WAVE;
+            if (c0 >= np) break;
+            const float wl = c0 + lane < np ? expf(mv[q] - top) : 0.0f;
+            const int nc = min(CUCA_WAVE, np - c0);
+#pragma unroll
+            for (int j0 = 0; j0 < CUCA_WAVE; j0 += 16) {
+                if (j0 >= nc) break;
+                float v[16][MAXC];
+#pragma unroll
+                for (int jj = 0; jj < 16; jj++) {
+                    if (q == 0 && j0 + 16 <= R) {
+#pragma unroll
+                        for (int k = 0; k < MAXC; k++) v[jj][k] = v0[R > 0 ? (j0 + jj) % R : 0][k];
+                    } else {
+                        const float *pc = pp + (int64_t)(c0 + min(j0 + jj, nc - 1)) * stride;
+#pragma unroll
+                        for (int k = 0; k < MAXC; k++) {
+                            const int e = lane + k * CUCA_WAVE;
+                            v[jj][k] = e < D ? pc[e] : 0.0f;
+                        }
+                    }
+                }
+#pragma unroll
+                for (int jj = 0; jj < 16; jj++) {
+                    if (j0 + jj < nc) {
+                        const float wj = __builtin_bit_cast(
+                            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), j0 + jj));
+#pragma unroll
+                        for (int k = 0; k < MAXC; k++) acc[k] += v[jj][k] * wj;
+                    }
                 }
             }
+        }
+    } else {
+        // the global maximum, then each lane's parts' weighted sums (in order)
+        float mx = -INFINITY;
+        for (int c = lane; c < np; c += CUCA_WAVE) mx = fmaxf(mx, pp[c * stride + D]);
+        const float top = wave_max(mx);
+        float t = 0.0f;
+        for (int c = lane; c < np; c += CUCA_WAVE) t += pp[c * stride + D + 1] * expf(pp[c * stride + D] - top);
+        total = group_sum<CUCA_WAVE>(t);
+        for (int c0 = 0; c0 < np; c0 += CUCA_WAVE) {
+            // lane l holds the weight of part c0 + l
+            const int cl = c0 + lane;
+            const float wl = cl < np ? expf(pp[cl * stride + D] - top) : 0.0f;
+            const int nc = min(CUCA_WAVE, np - c0);
+            for (int j0 = 0; j0 < nc; j0 += 16) {
+                float v[16][MAXC];
 #pragma unroll
-            for (int jj = 0; jj < 16; jj++) {
-                if (j0 + jj < nc) {
-                    const float wj = __builtin_bit_cast(
-                        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), j0 + jj));
+                for (int jj = 0; jj < 16; jj++) {
+                    const float *pc = pp + (int64_t)(c0 + min(j0 + jj, nc - 1)) * stride;
 #pragma unroll
-                    for (int k = 0; k < MAXC; k++) acc[k] += v[jj][k] * wj;
+                    for (int k = 0; k < MAXC; k++) {
+                        const int e = lane + k * CUCA_WAVE;
+                        v[jj][k] = e < D ? pc[e] : 0.0f;
+                    }
+                }
+#pragma unroll
+                for (int jj = 0; jj < 16; jj++) {
+                    if (j0 + jj < nc) {
+                        const float wj = __builtin_bit_cast(
+                            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), j0 + jj));
+#pragma unroll
+                        for (int k = 0; k < MAXC; k++) acc[k] += v[jj][k] * wj;
+                    }
                 }
             }
         }

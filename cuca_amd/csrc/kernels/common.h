@@ -89,7 +89,13 @@ template <> struct Chunk<_Float16> {
         for (int i = 0; i < 8; i++) t[i] = (_Float16)v[i];
         __builtin_nontemporal_store(t, reinterpret_cast<f16x8 *>(base) + chunk);
     }
-    __device__ static inline float as_stored(float v) { return (float)(_Float16)v; }
+    // (the f32 value is pinned first: otherwise the compiler may fold the
+    // operation that produced it and this rounding into one v_fma_mix*_f16,
+    // which rounds once to f16 where the f32 result rounded to f16 is asked)
+    __device__ static inline float as_stored(float v) {
+        asm volatile("" : "+v"(v));
+        return (float)(_Float16)v;
+    }
     __device__ static inline u32x4 load_raw(const void *base, int64_t chunk) {
         return reinterpret_cast<const u32x4 *>(base)[chunk];
     }
@@ -99,6 +105,14 @@ template <> struct Chunk<_Float16> {
         for (int i = 0; i < 8; i++) v[i] = (float)t[i];
     }
 };
+
+// v, materialised as an f32 value: an operation written before it cannot be
+// merged with one written after it (a multiply with the next multiply's
+// rounding, or with a conversion to f16 into one v_fma_mix*_f16).
+__device__ static inline float pin_f32(float v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
 
 // Load chunk `c` of `base`, streaming (NT) or cached.
 template <typename T, bool NT, int N>

@@ -139,14 +139,18 @@ __device__ static inline void norm_body(const NormArgs &a) {
         const int c = li + k * TPR;
         if (c < nch) {
             float h[N];
+            // each product rounded to f32 before the store rounds to the
+            // activation type (pinned: the compiler may otherwise fold the
+            // last multiply and the f16 conversion into one v_fma_mixlo_f16,
+            // which rounds once)
             if (a.w) {
                 float w[N];
                 load_w<N>(a.w, c, w);
 #pragma unroll
-                for (int i = 0; i < N; i++) h[i] = v[k][i] * inv * w[i];
+                for (int i = 0; i < N; i++) h[i] = pin_f32(pin_f32(v[k][i] * inv) * w[i]);
             } else {
 #pragma unroll
-                for (int i = 0; i < N; i++) h[i] = v[k][i] * inv;
+                for (int i = 0; i < N; i++) h[i] = pin_f32(v[k][i] * inv);
             }
             Chunk<T>::store_nt(a.h_out, cb + c, h);
         }
