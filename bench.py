@@ -863,6 +863,81 @@ def qgemm_bench(ctx, torch, reps=10):
     return res
 
 
+def gemm_w16_bench(ctx, torch, reps=10):
+    """The dense f16 path for many rows (cuca_hip_qweight_dequant once, then
+    cuca_hip_gemm_w16 / _gemm_w16_glu per call: hipBLASLt's f16 GEMM, f32
+    accumulation) at the 8B layer shapes, 512 and 4096 rows of f32
+    activations: time of the whole call on the stream (the f16 rounding of
+    the activations, the GEMM, the GLU epilogue), its f16 TFLOP/s against
+    the 2.5 PFLOP/s dense peak, and the one-time dequantisation.  Sampled
+    outputs are checked against the f64 product within the qgemm bound."""
+    import numpy as np
+    from cuca_amd import hip
+    from cuca_amd import workloads as W
+    from oracle import oracle as O
+    gen = torch.Generator(device="cuda").manual_seed(9)
+    T = hip.GGML_Q4_0
+    res = {}
+    for name, n, k, glu in (("gate_up", 14336, 4096, True), ("down", 4096, 14336, False), ("q_o", 4096, 4096, False)):
+        raws = [W.quant_table_torch(gen, n, k, "q4_0", (0.001, 0.02)) for _ in range(2 if glu else 1)]
+        w16 = torch.empty((len(raws) * n, k), dtype=torch.float16, device="cuda")
+        packed = torch.empty(hip.qweight_bytes(T, n, k), dtype=torch.uint8, device="cuda")
+        dq_ms = 0.0
+        for i, r in enumerate(raws):
+            ctx.qweight_pack(r.data_ptr(), T, n, k, packed.data_ptr())
+            dq_ms += time_steps(torch, lambda i=i: ctx.qweight_dequant(packed.data_ptr(), T, n, k,
+                                                                       w16.data_ptr() + i * n * k * 2), 3, 1)
+        del packed
+        torch.cuda.synchronize()
+        for m, dt in ((512, "f32"), (4096, "f32"), (4096, "f16")):
+            tdt, code = (torch.float16, hip.F16) if dt == "f16" else (torch.float32, hip.F32)
+            x = torch.randn(m, k, device="cuda", generator=gen).to(tdt)
+            out = torch.empty(m, n, device="cuda", dtype=tdt)
+            wsb = hip.gemm_w16_workspace(n, k, m, glu, code)
+            wsp = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+
+            def call(x=x, out=out, wsp=wsp, wsb=wsb, m=m, code=code):
+                if glu:
+                    ctx.gemm_w16_glu(w16.data_ptr(), n, k, x.data_ptr(), k, m, hip.ACT_SILU, 0.0, wsp.data_ptr(),
+                                     wsb, out.data_ptr(), n, code)
+                else:
+                    ctx.gemm_w16(w16.data_ptr(), n, k, x.data_ptr(), k, m, n, wsp.data_ptr(), wsb, out.data_ptr(),
+                                 n, code)
+            ms = time_steps(torch, call, reps, 3)
+            call()
+            torch.cuda.synchronize()
+            toks = [0, m // 2, m - 1]
+            xs = x[toks].float().cpu().numpy().astype(np.float64)
+            rb = W.row_bytes("q4_0", k)
+            cols = np.arange(0, n, max(1, n // 256))[:256]
+            sel = torch.from_numpy(cols).to("cuda")
+            dq = []
+            for r in raws:
+                rows_b = r.view(n, rb).index_select(0, sel).cpu().numpy()
+                dq.append(np.stack([O.dequant_row(T, rows_b[i], 1.0, k) for i in range(cols.size)]).astype(np.float64))
+            got = out[toks][:, cols].float().cpu().numpy().astype(np.float64)
+            g = xs @ dq[0].T
+            bg = (2.0 ** -10 + k * 2.0 ** -24) * (np.abs(xs) @ np.abs(dq[0]).T)
+            if glu:
+                u = xs @ dq[1].T
+                bu = (2.0 ** -10 + k * 2.0 ** -24) * (np.abs(xs) @ np.abs(dq[1]).T)
+                a = g / (1.0 + np.exp(-g))
+                want, tol = a * u, 1.2 * bg * (np.abs(u) + bu) + np.abs(a) * bu + 1e-5 * np.abs(a * u)
+            else:
+                want, tol = g, bg
+            if dt == "f16":
+                tol = tol + 2.0 ** -11 * np.abs(want)
+            assert np.all(np.abs(got - want) <= tol + 1e-30), f"gemm_w16 {name} m={m} {dt}"
+            flops = 2.0 * m * n * k * (2 if glu else 1)
+            res[f"{name}_q4_0_m{m}_{dt}"] = dict(
+                us=round(ms * 1000, 2), tflops=round(flops / (ms / 1e3) / 1e12, 1),
+                mfma_frac=round(flops / (ms / 1e3) / 2.5e15, 4), dequant_once_us=round(dq_ms * 1000, 1),
+                w16_bytes=int(w16.numel() * 2))
+        del w16, raws
+        torch.cuda.empty_cache()
+    return res
+
+
 def moe_bench(ctx, torch, reps=30):
     """Routed experts at config E (Qwen3-30B-A3B: 128 experts of ff 768 over
     hidden 2048, Q4_0, top 8): moe_up (gate/up + SwiGLU), moe_down (times the
@@ -1143,12 +1218,14 @@ def main():
             checked_rows += 2
         torch.cuda.empty_cache()
 
-    qmm = moe = head = qgemm = None
+    qmm = moe = head = qgemm = gemm16 = None
     if not args.no_qmm:
         log("quantized matmuls (8B decode shapes)")
         qmm = qmm_bench(ctx, torch)
         log("matrix-core quantized matmul (8B shapes, 32 / 512 / 4096 rows)")
         qgemm = qgemm_bench(ctx, torch)
+        log("dense f16 path: dequantised weights + f16 GEMM (8B shapes, 512 / 4096 rows)")
+        gemm16 = gemm_w16_bench(ctx, torch)
         log("routed experts (config E decode)")
         moe = moe_bench(ctx, torch)
         log("LM head + greedy / top-k")
@@ -1209,6 +1286,7 @@ def main():
         "paged_decode": attn,
         "qmm_decode": qmm,
         "qgemm": qgemm,
+        "gemm_w16": gemm16,
         "moe_decode": moe,
         "end_of_step": head,
         "decode_us_per_layer": decode,

@@ -176,6 +176,21 @@ typedef struct {
     int32_t mp;
 } QGemmArgs;
 
+/* The dense f16 path (qgemm.hip): cuca_qdequant_* (packed w [n][ng][GB],
+ * row_bytes each -> out f16 [n][out_ld]), cuca_cvt_f16_f32 (x [m][ldx] f32
+ * -> out f16 [m][out_ld], k values a row) and cuca_gemm_glu_epi_* (x = the
+ * GEMM's f32 rows [m][ldx] holding gate[n] then up[n] -> out [m][out_ld]). */
+typedef struct {
+    const uint8_t *w;
+    const void *x;
+    void *out;
+    int64_t row_bytes, ldx, out_ld;
+    int64_t n;
+    int32_t m, k, nb, ng;
+    float clamp;
+    int32_t pad_;
+} QDequantArgs;
+
 /* Activation quantisation for the decode GEMV (Acts::new, qmm.rs:1272-1343):
  * x [m][ldx] -> quants [m][q_ld] int8 (element order) and scales [m][nb]. */
 typedef struct {

@@ -112,6 +112,13 @@ __device__ static inline qg_h8 qg_dequant(const QgA<FMT> &a, int s) {
     return o;
 }
 
+__device__ static inline void qgemm_load8f(const float *p, float (&v)[8]) {
+    const f32x4 a = reinterpret_cast<const f32x4 *>(p)[0];
+    const f32x4 b = reinterpret_cast<const f32x4 *>(p)[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
 // The activations rewritten once per call, before the matmul: f16, in the
 // slot order of the format (xp [n_ct * TM][kp], kp = 128 per k-chunk; zero
 // past k and in the rows past m, up to the whole tile).  One thread per unit
@@ -340,3 +347,93 @@ CUCA_QGEMM_SET(f16, _Float16, q8_0, 1)
     CUCA_QGEMM(cuca_qgemm_reduce_glu_##TN##_gelu, qgemm_reduce_body, T, true, 1)
 CUCA_QGEMM_RED(f32, float)
 CUCA_QGEMM_RED(f16, _Float16)
+
+// ---------------------------------------------------------------------
+// The dense f16 path for many rows: the weight dequantised once into a
+// resident f16 copy (the reference GPU engine's dense_dequant_kernel,
+// moe_kernel.rs:1560-1600, with f16 output), then a plain f16 GEMM (the
+// library's, f32 accumulation) and, for the GLU, the epilogue below.
+// ---------------------------------------------------------------------
+
+// One thread per (weight row, group, lane chunk l): the 2 G values l and
+// l + 16 of the group's G blocks, w16[row][32 b + e] = f16(d_b * q), one
+// rounding (the product of an f16 scale and a small integer is exact in
+// f32) -- the values qgemm's operands carry.  Blocks past k (a partial last
+// group) are not written.
+template <int FMT> __device__ static inline void qdequant_body(const QDequantArgs &a) {
+    constexpr int G = FMT == 0 ? 16 : 8, GB = FMT == 0 ? 288 : 272, SCB = 2 * G;
+    const int64_t t = (int64_t)blockIdx.x * CUCA_BLOCK + threadIdx.x;
+    if (t >= (int64_t)a.n * a.ng * 16) return;
+    const int l = (int)(t & 15);
+    const int64_t rg = t >> 4;
+    const int g = (int)(rg % a.ng);
+    const int64_t row = rg / a.ng;
+    const uint8_t *grp = a.w + row * a.row_bytes + (int64_t)g * GB;
+    const u32x4 chunk = *reinterpret_cast<const u32x4 *>(grp + SCB + 16 * l);
+    const uint16_t *sc = reinterpret_cast<const uint16_t *>(grp);
+    _Float16 *dst = reinterpret_cast<_Float16 *>(a.out) + row * a.out_ld;
+#pragma unroll
+    for (int b = 0; b < G; b++) {
+        const int blk = g * G + b;
+        if (blk >= a.nb) break;
+        const float d = (float)__builtin_bit_cast(_Float16, sc[b]);
+        int q0, q1; // elements l and l + 16
+        if (FMT == 0) {
+            const uint32_t w = chunk[b >> 2];
+            q0 = (int)((w >> (4 * (b & 3))) & 15u) - 8;
+            q1 = (int)((w >> (16 + 4 * (b & 3))) & 15u) - 8;
+        } else {
+            const uint32_t w = chunk[b >> 1];
+            q0 = (int)((w >> (8 * (b & 1))) & 255u) - 128;
+            q1 = (int)((w >> (16 + 8 * (b & 1))) & 255u) - 128;
+        }
+        dst[32 * blk + l] = (_Float16)(d * (float)q0);
+        dst[32 * blk + l + 16] = (_Float16)(d * (float)q1);
+    }
+}
+extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void cuca_qdequant_q4_0(QDequantArgs a) { qdequant_body<0>(a); }
+extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void cuca_qdequant_q8_0(QDequantArgs a) { qdequant_body<1>(a); }
+
+// Activations rounded to f16 (RNE), the GEMM's operand: x [m][ldx] f32 ->
+// xh [m][k]; eight values per thread (k % 8 == 0).
+extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void cuca_cvt_f16_f32(QDequantArgs a) {
+    const int64_t t = (int64_t)blockIdx.x * CUCA_BLOCK + threadIdx.x;
+    const int64_t per = a.k / 8;
+    if (t >= (int64_t)a.m * per) return;
+    const int64_t r = t / per, c = (t - r * per) * 8;
+    const float *src = reinterpret_cast<const float *>(a.x) + r * a.ldx + c;
+    float v[8];
+    qgemm_load8f(src, v);
+    f16x8 h;
+#pragma unroll
+    for (int i = 0; i < 8; i++) h[i] = (_Float16)v[i];
+    *reinterpret_cast<f16x8 *>(reinterpret_cast<_Float16 *>(a.out) + r * a.out_ld + c) = h;
+}
+
+// The GLU after the dense GEMM: y [m][2 ff] f32 (gate columns, then up),
+// out = act(gate) * up with Glu::apply's clamp -- qgemm's epilogue.
+template <typename T, int ACT> __device__ static inline void gemm_glu_epi_body(const QDequantArgs &a) {
+    const int64_t e = (int64_t)blockIdx.x * CUCA_BLOCK + threadIdx.x;
+    if (e >= (int64_t)a.m * a.n) return;
+    const int64_t tok = e / a.n, c = e - tok * a.n;
+    const float *y = reinterpret_cast<const float *>(a.x) + tok * a.ldx;
+    float g = y[c], u = y[a.n + c];
+    if (a.clamp > 0.0f) { // Glu::apply's clamp (cpu.rs:364-368)
+        g = fminf(g, a.clamp);
+        u = fminf(fmaxf(u, -a.clamp), a.clamp);
+    }
+    const float o = (ACT == 0 ? act_silu(g) : act_gelu_tanh(g)) * u;
+    reinterpret_cast<T *>(a.out)[tok * a.out_ld + c] = (T)pin_f32(o);
+}
+extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void cuca_gemm_glu_epi_f32_silu(QDequantArgs a) {
+    gemm_glu_epi_body<float, 0>(a);
+}
+extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void cuca_gemm_glu_epi_f32_gelu(QDequantArgs a) {
+    gemm_glu_epi_body<float, 1>(a);
+}
+extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void cuca_gemm_glu_epi_f16_silu(QDequantArgs a) {
+    gemm_glu_epi_body<_Float16, 0>(a);
+}
+extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void cuca_gemm_glu_epi_f16_gelu(QDequantArgs a) {
+    gemm_glu_epi_body<_Float16, 1>(a);
+}

@@ -10,6 +10,7 @@
 #include "kernel_args.h"
 
 #include <hip/hip_runtime_api.h>
+#include <hipblaslt/hipblaslt.h>
 
 #include <cmath>
 #include <cstdarg>
@@ -82,6 +83,15 @@ struct cuca_hip_ctx {
     // device scratch for the per-slice results of cuca_hip_argmax / _top_k
     // (allocated with the context: ops never allocate)
     void *pscratch = nullptr;
+    // hipBLASLt for the dense f16 GEMM of many rows (created on first use)
+    // and the algorithms its heuristic picked, per shape
+    hipblasLtHandle_t lt = nullptr;
+    struct LtPlan {
+        int64_t rows, k, m, ldx, ldd;
+        int dtype;
+        hipblasLtMatmulAlgo_t algo;
+    };
+    std::vector<LtPlan> lt_plans;
     int cu_count = 256;
     std::string error;
     // per-kernel timing (cuca_hip_profile_start/stop)
@@ -246,6 +256,7 @@ void cuca_hip_ctx_destroy(cuca_hip_ctx *ctx) {
     }
     if (ctx->status) (void)hipFree(ctx->status);
     if (ctx->pscratch) (void)hipFree(ctx->pscratch);
+    if (ctx->lt) (void)hipblasLtDestroy(ctx->lt);
     if (ctx->module) (void)hipModuleUnload(ctx->module);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
@@ -1189,6 +1200,204 @@ cuca_status cuca_hip_qmm_glu(cuca_hip_ctx *ctx, const void *gate, const void *up
         return fail(ctx, CUCA_INVALID_ARG, "bad activation %d", (int)act);
     return qmm_common(ctx, gate, up, ggml_type, ff, k, x, ldx, m, ff, act == CUCA_ACT_SILU ? 1 : 2, clamp,
                       out, out_ld, dtype);
+}
+
+// ---------------------------------------------------------------------
+// the dense f16 path for many rows: a resident f16 copy of the weight and
+// hipBLASLt's f16 GEMM (f32 accumulation)
+// ---------------------------------------------------------------------
+
+cuca_status cuca_hip_qweight_dequant(cuca_hip_ctx *ctx, const void *packed, uint32_t ggml_type, int64_t n, int64_t k,
+                                     void *w16) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    int g = 0, gb = 0;
+    if ((st = qweight_shape(ctx, ggml_type, n, k, &g, &gb)) != CUCA_OK) return st;
+    if (!packed || !w16) return fail(ctx, CUCA_INVALID_ARG, "null pointer");
+    if (!al16(packed)) return fail(ctx, CUCA_INVALID_ARG, "packed weights must be 16-byte aligned");
+    const int64_t nb = k / 32, ng = (nb + g - 1) / g;
+    if (n * ng * 16 > 0x7fffffffll * 256) return fail(ctx, CUCA_UNSUPPORTED, "dequant: weight too large");
+    QDequantArgs a{};
+    a.w = static_cast<const uint8_t *>(packed);
+    a.out = w16;
+    a.row_bytes = ng * gb;
+    a.out_ld = k;
+    a.n = n;
+    a.k = (int32_t)k;
+    a.nb = (int32_t)nb;
+    a.ng = (int32_t)ng;
+    return launch(ctx, ggml_type == CUCA_GGML_Q8_0 ? cuca_qdequant_q8_0 : cuca_qdequant_q4_0,
+                  (unsigned)div_up(n * ng * 16, CUCA_BLOCK_THREADS), CUCA_BLOCK_THREADS, 0, a);
+}
+
+// hipBLASLt's own workspace within the caller's, and the parts before it
+constexpr size_t kLtWorkspace = 32ull << 20;
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+static size_t gemm_w16_ws_bytes(int64_t n, int64_t k, int64_t m, bool glu, cuca_dtype dtype) {
+    size_t b = kLtWorkspace;
+    if (dtype == CUCA_F32) b += align256((size_t)m * (size_t)k * 2); // activations as f16
+    if (glu) b += align256((size_t)m * (size_t)(2 * n) * 4);          // the f32 gate|up rows
+    return b;
+}
+
+cuca_status cuca_hip_gemm_w16_workspace(int64_t n, int64_t k, int64_t m, int32_t glu, cuca_dtype dtype,
+                                        size_t *bytes) {
+    if (!bytes) return fail(nullptr, CUCA_INVALID_ARG, "null pointer");
+    if (n <= 0 || k <= 0 || k % 32 != 0 || m < 0 || m > 0x7fffffffll || !dtype_ok(dtype))
+        return fail(nullptr, CUCA_INVALID_ARG, "gemm: bad shape %lld x %lld, %lld rows", (long long)n, (long long)k,
+                    (long long)m);
+    *bytes = gemm_w16_ws_bytes(n, k, m, glu != 0, dtype);
+    return CUCA_OK;
+}
+
+static cuca_status lt_fail(cuca_hip_ctx *ctx, hipblasStatus_t s, const char *what) {
+    return fail(ctx, CUCA_HIP_ERROR, "hipBLASLt %s: status %d", what, (int)s);
+}
+
+// D [m][ldd] (row-major) = X [m][ldx] . W [rows][k]^T, f16 operands, f32
+// accumulation, D of type dt.  In hipBLASLt's column-major terms: D^T
+// (rows x m) = op_T(W^T) (rows x k) . X^T (k x m).
+static cuca_status lt_gemm(cuca_hip_ctx *ctx, const void *w16, int64_t rows, int64_t k, const void *xh, int64_t ldx,
+                           int64_t m, void *d, int64_t ldd, hipDataType dt, void *lt_ws) {
+    hipblasStatus_t e;
+    if (!ctx->lt && (e = hipblasLtCreate(&ctx->lt)) != HIPBLAS_STATUS_SUCCESS) {
+        ctx->lt = nullptr;
+        return lt_fail(ctx, e, "create");
+    }
+    hipblasLtMatmulDesc_t op = nullptr;
+    hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, ld = nullptr;
+    cuca_status st = CUCA_OK;
+    do {
+        if ((e = hipblasLtMatmulDescCreate(&op, HIPBLAS_COMPUTE_32F, HIP_R_32F)) != HIPBLAS_STATUS_SUCCESS) {
+            st = lt_fail(ctx, e, "matmul descriptor"); break;
+        }
+        const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
+        hipblasLtMatmulDescSetAttribute(op, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta);
+        hipblasLtMatmulDescSetAttribute(op, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb);
+        if ((e = hipblasLtMatrixLayoutCreate(&la, HIP_R_16F, (uint64_t)k, (uint64_t)rows, k)) != HIPBLAS_STATUS_SUCCESS ||
+            (e = hipblasLtMatrixLayoutCreate(&lb, HIP_R_16F, (uint64_t)k, (uint64_t)m, ldx)) != HIPBLAS_STATUS_SUCCESS ||
+            (e = hipblasLtMatrixLayoutCreate(&ld, dt, (uint64_t)rows, (uint64_t)m, ldd)) != HIPBLAS_STATUS_SUCCESS) {
+            st = lt_fail(ctx, e, "matrix layout"); break;
+        }
+        const hipblasLtMatmulAlgo_t *algo = nullptr;
+        for (const auto &p : ctx->lt_plans)
+            if (p.rows == rows && p.k == k && p.m == m && p.ldx == ldx && p.ldd == ldd && p.dtype == (int)dt) {
+                algo = &p.algo;
+                break;
+            }
+        if (!algo) {
+            hipblasLtMatmulPreference_t pref = nullptr;
+            if ((e = hipblasLtMatmulPreferenceCreate(&pref)) != HIPBLAS_STATUS_SUCCESS) {
+                st = lt_fail(ctx, e, "preference"); break;
+            }
+            const uint64_t wsb = kLtWorkspace;
+            hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb, sizeof wsb);
+            hipblasLtMatmulHeuristicResult_t res[1];
+            int count = 0;
+            e = hipblasLtMatmulAlgoGetHeuristic(ctx->lt, op, la, lb, ld, ld, pref, 1, res, &count);
+            hipblasLtMatmulPreferenceDestroy(pref);
+            if (e != HIPBLAS_STATUS_SUCCESS || count < 1) {
+                st = fail(ctx, CUCA_UNSUPPORTED, "hipBLASLt: no algorithm for %lld x %lld x %lld (status %d)",
+                          (long long)m, (long long)rows, (long long)k, (int)e);
+                break;
+            }
+            ctx->lt_plans.push_back({rows, k, m, ldx, ldd, (int)dt, res[0].algo});
+            algo = &ctx->lt_plans.back().algo;
+        }
+        const float one = 1.0f, zero = 0.0f;
+        if ((e = hipblasLtMatmul(ctx->lt, op, &one, w16, la, xh, lb, &zero, d, ld, d, ld, algo, lt_ws, kLtWorkspace,
+                                 ctx->stream)) != HIPBLAS_STATUS_SUCCESS) {
+            st = lt_fail(ctx, e, "matmul"); break;
+        }
+        if (hipGetLastError() != hipSuccess) { st = fail(ctx, CUCA_HIP_ERROR, "hipBLASLt matmul launch"); break; }
+    } while (0);
+    if (la) hipblasLtMatrixLayoutDestroy(la);
+    if (lb) hipblasLtMatrixLayoutDestroy(lb);
+    if (ld) hipblasLtMatrixLayoutDestroy(ld);
+    if (op) hipblasLtMatmulDescDestroy(op);
+    return st;
+}
+
+// glu: 0 plain, 1 SiLU, 2 GELU-tanh; w16 [n][k] (gate rows, then up rows
+// for the GLU: n = 2 ff).
+static cuca_status gemm_w16_common(cuca_hip_ctx *ctx, const void *w16, int64_t n, int64_t k, const void *x,
+                                   int64_t ldx, int64_t m, int64_t rows, int glu, float clamp, void *ws,
+                                   size_t ws_bytes, void *out, int64_t out_ld, cuca_dtype dtype) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    if (!dtype_ok(dtype)) return fail(ctx, CUCA_INVALID_ARG, "bad dtype %d", (int)dtype);
+    if (n <= 0 || k <= 0 || k % 32 != 0 || k > 0x7fffffffll)
+        return fail(ctx, CUCA_INVALID_ARG, "gemm: bad weight shape %lld x %lld", (long long)n, (long long)k);
+    if (rows <= 0 || rows > n)
+        return fail(ctx, CUCA_INVALID_ARG, "gemm: %lld weight rows of %lld", (long long)rows, (long long)n);
+    if (m < 0 || m > 0x7fffffffll) return fail(ctx, CUCA_INVALID_ARG, "gemm: bad activation row count %lld", (long long)m);
+    if (ldx < k)
+        return fail(ctx, CUCA_INVALID_ARG, "gemm: activation row stride %lld shorter than %lld", (long long)ldx,
+                    (long long)k);
+    if (out_ld < (glu ? n / 2 : rows))
+        return fail(ctx, CUCA_INVALID_ARG, "gemm: output row stride %lld too short", (long long)out_ld);
+    if (!(clamp == clamp)) return fail(ctx, CUCA_INVALID_ARG, "clamp is NaN");
+    if (m == 0) return CUCA_OK;
+    if (!w16 || !x || !out || !ws) return fail(ctx, CUCA_INVALID_ARG, "null pointer");
+    const size_t es = esize(dtype);
+    if (!al16(w16) || !al16(x) || !al16(out) || !al16(ws) || ((size_t)ldx * es) % 16 != 0)
+        return fail(ctx, CUCA_INVALID_ARG, "gemm: weights, rows, output and workspace must be 16-byte aligned");
+    const size_t need = gemm_w16_ws_bytes(glu ? n / 2 : n, k, m, glu != 0, dtype);
+    if (ws_bytes < need)
+        return fail(ctx, CUCA_INVALID_ARG, "gemm: workspace of %zu bytes, %zu needed (cuca_hip_gemm_w16_workspace)",
+                    ws_bytes, need);
+    char *p = static_cast<char *>(ws);
+    void *lt_ws = p;
+    p += kLtWorkspace;
+    const void *xh = x;
+    int64_t ldxh = ldx;
+    if (dtype == CUCA_F32) { // the activations rounded to f16 once
+        QDequantArgs c{};
+        c.x = x;
+        c.out = p;
+        c.ldx = ldx;
+        c.out_ld = k;
+        c.m = (int32_t)m;
+        c.k = (int32_t)k;
+        if ((st = launch(ctx, cuca_cvt_f16_f32, (unsigned)div_up(m * (k / 8), CUCA_BLOCK_THREADS),
+                         CUCA_BLOCK_THREADS, 0, c)) != CUCA_OK)
+            return st;
+        xh = p;
+        ldxh = k;
+        p += align256((size_t)m * (size_t)k * 2);
+    }
+    const hipDataType dt = dtype == CUCA_F16 ? HIP_R_16F : HIP_R_32F;
+    if (!glu) return lt_gemm(ctx, w16, rows, k, xh, ldxh, m, out, out_ld, dt, lt_ws);
+    const int64_t ff = n / 2;
+    if ((st = lt_gemm(ctx, w16, n, k, xh, ldxh, m, p, n, HIP_R_32F, lt_ws)) != CUCA_OK) return st;
+    QDequantArgs e{};
+    e.x = p;
+    e.out = out;
+    e.ldx = n;
+    e.out_ld = out_ld;
+    e.n = ff;
+    e.m = (int32_t)m;
+    e.clamp = clamp > 0.0f ? clamp : 0.0f;
+    static const Kernel epi[2][2] = {{cuca_gemm_glu_epi_f32_silu, cuca_gemm_glu_epi_f32_gelu},
+                                     {cuca_gemm_glu_epi_f16_silu, cuca_gemm_glu_epi_f16_gelu}};
+    return launch(ctx, epi[dtype == CUCA_F16][glu == 2], (unsigned)div_up(m * ff, CUCA_BLOCK_THREADS),
+                  CUCA_BLOCK_THREADS, 0, e);
+}
+
+cuca_status cuca_hip_gemm_w16(cuca_hip_ctx *ctx, const void *w16, int64_t n, int64_t k, const void *x, int64_t ldx,
+                              int64_t m, int64_t rows, void *workspace, size_t workspace_bytes, void *out,
+                              int64_t out_ld, cuca_dtype dtype) {
+    return gemm_w16_common(ctx, w16, n, k, x, ldx, m, rows, 0, 0.0f, workspace, workspace_bytes, out, out_ld, dtype);
+}
+
+cuca_status cuca_hip_gemm_w16_glu(cuca_hip_ctx *ctx, const void *w16, int64_t ff, int64_t k, const void *x,
+                                  int64_t ldx, int64_t m, cuca_act act, float clamp, void *workspace,
+                                  size_t workspace_bytes, void *out, int64_t out_ld, cuca_dtype dtype) {
+    if (act != CUCA_ACT_SILU && act != CUCA_ACT_GELU_TANH)
+        return fail(ctx, CUCA_INVALID_ARG, "bad activation %d", (int)act);
+    if (ff <= 0 || ff > 0x3fffffffll) return fail(ctx, CUCA_INVALID_ARG, "gemm glu: bad ff %lld", (long long)ff);
+    return gemm_w16_common(ctx, w16, 2 * ff, k, x, ldx, m, 2 * ff, act == CUCA_ACT_SILU ? 1 : 2, clamp, workspace,
+                           workspace_bytes, out, out_ld, dtype);
 }
 
 // The matrix-core matmul (qgemm.hip): the workspace holds the activations

@@ -78,6 +78,11 @@ SIGNATURES = {
     "cuca_hip_qmm_glu": (_st, [_p, _p, _p, _u32, _i64, _i64, _p, _i64, _i64, _st, _f32, _p, _i64,
                                _st]),
     "cuca_hip_qgemm_workspace": (_st, [_u32, _i64, _i64, _i64, _i32, ctypes.POINTER(ctypes.c_size_t)]),
+    "cuca_hip_qweight_dequant": (_st, [_p, _p, _u32, _i64, _i64, _p]),
+    "cuca_hip_gemm_w16_workspace": (_st, [_i64, _i64, _i64, _i32, _st, ctypes.POINTER(ctypes.c_size_t)]),
+    "cuca_hip_gemm_w16": (_st, [_p, _p, _i64, _i64, _p, _i64, _i64, _i64, _p, _sz, _p, _i64, _st]),
+    "cuca_hip_gemm_w16_glu": (_st, [_p, _p, _i64, _i64, _p, _i64, _i64, _st, _f32, _p, _sz, _p, _i64,
+                                    _st]),
     "cuca_hip_qgemm": (_st, [_p, _p, _u32, _i64, _i64, _p, _i64, _i64, _i64, _p, _sz, _p, _i64, _st]),
     "cuca_hip_qgemm_glu": (_st, [_p, _p, _p, _u32, _i64, _i64, _p, _i64, _i64, _st, _f32, _p, _sz, _p,
                                  _i64, _st]),
@@ -357,6 +362,17 @@ class Context:
         self.check(self.L.cuca_hip_qgemm_glu(self.ptr, gate, up, ggml_type, ff, k, x, ldx, m, act,
                                              clamp, ws, ws_bytes, out, out_ld, dtype))
 
+    def qweight_dequant(self, packed, ggml_type, n, k, w16):
+        self.check(self.L.cuca_hip_qweight_dequant(self.ptr, packed, ggml_type, n, k, w16))
+
+    def gemm_w16(self, w16, n, k, x, ldx, m, rows, ws, ws_bytes, out, out_ld, dtype):
+        self.check(self.L.cuca_hip_gemm_w16(self.ptr, w16, n, k, x, ldx, m, rows, ws, ws_bytes, out,
+                                            out_ld, dtype))
+
+    def gemm_w16_glu(self, w16, ff, k, x, ldx, m, act, clamp, ws, ws_bytes, out, out_ld, dtype):
+        self.check(self.L.cuca_hip_gemm_w16_glu(self.ptr, w16, ff, k, x, ldx, m, act, clamp, ws,
+                                                ws_bytes, out, out_ld, dtype))
+
     def qmm_glu(self, gate, up, ggml_type, ff, k, x, ldx, m, act, clamp, out, out_ld, dtype):
         self.check(self.L.cuca_hip_qmm_glu(self.ptr, gate, up, ggml_type, ff, k, x, ldx, m, act,
                                            clamp, out, out_ld, dtype))
@@ -432,6 +448,14 @@ def qgemm_workspace(ggml_type, n, k, m, glu=False):
     """Bytes of workspace cuca_hip_qgemm / _qgemm_glu need (host)."""
     out = _sz(0)
     _check(lib().cuca_hip_qgemm_workspace(ggml_type, n, k, m, 1 if glu else 0, ctypes.byref(out)), None)
+    return out.value
+
+
+def gemm_w16_workspace(n, k, m, glu, dtype):
+    """Bytes of workspace cuca_hip_gemm_w16 / _gemm_w16_glu need (host); n is
+    the output width (rows, or ff for the GLU)."""
+    out = _sz(0)
+    _check(lib().cuca_hip_gemm_w16_workspace(n, k, m, 1 if glu else 0, dtype, ctypes.byref(out)), None)
     return out.value
 
 

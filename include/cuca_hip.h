@@ -29,6 +29,8 @@
  *   cuca_hip_qmm           QmmWeight::forward_rows        qmm.rs:1810-1838
  *   cuca_hip_qmm_glu       gate/up qmm + Glu::apply       cpu.rs:342-371, 3554-3566
  *   cuca_hip_qgemm(_glu)   dense_dequant + matmul (GPU)   moe_kernel.rs:1414-1600
+ *   cuca_hip_qweight_      dense_dequant_kernel, then     moe_kernel.rs:1560-1600,
+ *     dequant, _gemm_w16   the dense matmul (GPU engine)  1414-1500
  *   cuca_hip_qweight_pack  (the weight upload)            qmm.rs:1763-1783
  *   cuca_hip_moe_up/down/  expert_sum, CpuExpert          cpu.rs:373-419, 3599-3642
  *            _sum          (GPU moe_up/moe_down/moe_sum)  moe_kernel.rs:1163-1385
@@ -346,6 +348,35 @@ cuca_status cuca_hip_qgemm(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type,
 cuca_status cuca_hip_qgemm_glu(cuca_hip_ctx *ctx, const void *gate, const void *up, uint32_t ggml_type, int64_t ff,
                                int64_t k, const void *x, int64_t ldx, int64_t m, cuca_act act, float clamp,
                                void *workspace, size_t workspace_bytes, void *out, int64_t out_ld, cuca_dtype dtype);
+
+/* The dense f16 path for many activation rows (prefill): the reference GPU
+ * engine's dense_dequant_kernel + matmul (moe_kernel.rs:1414-1600), shaped
+ * for MI355X's 288 GB: the weight is dequantised once into a resident f16
+ * copy (2 bytes a value: 16 GB for an 8B model, next to the Q4_0 weights
+ * the decode kernels read), and each call is one f16 GEMM on the matrix
+ * cores (hipBLASLt, f32 accumulation).  The arithmetic class of
+ * cuca_hip_qgemm (weights f16(d * q), activations f16(x), one rounding
+ * each), held to the same bound.
+ *   cuca_hip_qweight_dequant: packed (cuca_hip_qweight_pack) [n, k] ->
+ *     w16 f16 [n][k] row-major, f16(d * q) per value.
+ *   cuca_hip_gemm_w16: out[m][rows] = x[m] . w16[0..rows)^T; x and out of
+ *     dtype (f32 rows are rounded to f16 into the workspace first).
+ *   cuca_hip_gemm_w16_glu: w16 [2 ff][k] = the gate rows, then the up rows
+ *     (one GEMM); out[m][ff] = act(gate) * up with Glu::apply's clamp, from
+ *     f32 sums.
+ * workspace: device, 16-byte aligned, cuca_hip_gemm_w16_workspace bytes
+ * (n = the output width: rows, or ff for the GLU).  Not for a few rows:
+ * decode batches take cuca_hip_qmm / cuca_hip_qgemm on the packed weight. */
+cuca_status cuca_hip_qweight_dequant(cuca_hip_ctx *ctx, const void *packed, uint32_t ggml_type, int64_t n,
+                                     int64_t k, void *w16);
+cuca_status cuca_hip_gemm_w16_workspace(int64_t n, int64_t k, int64_t m, int32_t glu, cuca_dtype dtype,
+                                        size_t *bytes);
+cuca_status cuca_hip_gemm_w16(cuca_hip_ctx *ctx, const void *w16, int64_t n, int64_t k, const void *x,
+                              int64_t ldx, int64_t m, int64_t rows, void *workspace,
+                              size_t workspace_bytes, void *out, int64_t out_ld, cuca_dtype dtype);
+cuca_status cuca_hip_gemm_w16_glu(cuca_hip_ctx *ctx, const void *w16, int64_t ff, int64_t k, const void *x,
+                                  int64_t ldx, int64_t m, cuca_act act, float clamp, void *workspace,
+                                  size_t workspace_bytes, void *out, int64_t out_ld, cuca_dtype dtype);
 
 /* The end of a step (Transformer::finish / head / cap_logits,
  * cpu.rs:2495-2617; the final norm is cuca_hip_add_rmsnorm).
