@@ -417,7 +417,19 @@ cuca_status cuca_hip_embed_gguf(cuca_hip_ctx *ctx, const void *table, uint32_t g
 // cannot stay in the 256 MiB last-level cache (MALL) anyway, and streaming
 // them keeps it for data that is reused (+5 to +15 % measured at the
 // 16384-token shapes; no gain below the cache size).
-static const int64_t kStreamBytes = 256ll << 20;
+// Norm and SwiGLU calls whose inputs reach these sizes read them with
+// streaming (nontemporal) loads: a prefill-sized op's inputs are read once,
+// and left in the caches (L2, the 256 MB MALL) they displace what the next
+// kernels read.  Set by measurement on MI355X (five-op prefill steps, f16):
+// - at 4096 tokens (norm inputs 64 MiB, SwiGLU 224 MiB) streaming both
+//   took the step from 146 to 134 us (SwiGLU 74 -> 81 % of HBM peak, the
+//   norms 66 -> 70 %); the thresholds were 256 MiB before;
+// - Gemma-2 shapes at 2048 tokens (norm 28 MiB, GeGLU 112 MiB) ran slower
+//   streamed (GeGLU 86 -> 76 %, the norms 59 -> 49 %);
+// - RoPE, which rewrites its rows in place, ran slower streamed at every
+//   size (66 -> 61 % at 4096 tokens), so it never streams.
+static const int64_t kStreamBytes = 48ll << 20;
+static const int64_t kGluStreamBytes = 192ll << 20;
 
 // Launch shape of the vector norm kernel for rows of `nch` 16-byte chunks:
 // `tpr` threads per row, one chunk each, up to 1024 threads (one row per
@@ -546,8 +558,8 @@ static cuca_status glu_common(cuca_hip_ctx *ctx, const void *gate, int64_t gate_
     const bool f16 = dtype == CUCA_F16, gelu = act == CUCA_ACT_GELU_TANH;
     Kernel k;
     int64_t bpr;
-    // dense calls whose gate + up exceed the last-level cache stream them
-    const bool stream = !ragged && 2 * rows * ff * (int64_t)es >= kStreamBytes;
+    // prefill-sized dense calls stream gate and up (kStreamBytes)
+    const bool stream = !ragged && 2 * rows * ff * (int64_t)es >= kGluStreamBytes;
     if (vec) {
         bpr = (ff / N + 255) / 256;
         if (ragged)
