@@ -1390,10 +1390,13 @@ static cuca_status gemm_w16_common(cuca_hip_ctx *ctx, const void *w16, int64_t n
     e.n = ff;
     e.m = (int32_t)m;
     e.clamp = clamp > 0.0f ? clamp : 0.0f;
-    static const Kernel epi[2][2] = {{cuca_gemm_glu_epi_f32_silu, cuca_gemm_glu_epi_f32_gelu},
-                                     {cuca_gemm_glu_epi_f16_silu, cuca_gemm_glu_epi_f16_gelu}};
-    return launch(ctx, epi[dtype == CUCA_F16][glu == 2], (unsigned)div_up(m * ff, CUCA_BLOCK_THREADS),
-                  CUCA_BLOCK_THREADS, 0, e);
+    static const Kernel epi[2][2][2] = {
+        {{cuca_gemm_glu_epi_f32_silu, cuca_gemm_glu_epi_f32_gelu}, {cuca_gemm_glu_epi_f16_silu, cuca_gemm_glu_epi_f16_gelu}},
+        {{cuca_gemm_glu_epi_f32_silu_v4, cuca_gemm_glu_epi_f32_gelu_v4},
+         {cuca_gemm_glu_epi_f16_silu_v4, cuca_gemm_glu_epi_f16_gelu_v4}}};
+    const bool v4 = ff % 4 == 0 && out_ld % 4 == 0;
+    return launch(ctx, epi[v4][dtype == CUCA_F16][glu == 2],
+                  (unsigned)div_up(m * ff / (v4 ? 4 : 1), CUCA_BLOCK_THREADS), CUCA_BLOCK_THREADS, 0, e);
 }
 
 cuca_status cuca_hip_gemm_w16(cuca_hip_ctx *ctx, const void *w16, int64_t n, int64_t k, const void *x, int64_t ldx,

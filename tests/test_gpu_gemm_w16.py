@@ -82,9 +82,9 @@ def test_gemm_within_the_bound(ctx, qtype, dtype, n, k, m):
 @pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
 @pytest.mark.parametrize("act,clamp", [(hip.ACT_SILU, 0.0), (hip.ACT_GELU_TANH, 0.0), (hip.ACT_SILU, 3.0)])
-@pytest.mark.parametrize("m", [7, 256])
-def test_gemm_glu_within_the_bound(ctx, qtype, dtype, act, clamp, m):
-    ff, k = 160, 1536
+@pytest.mark.parametrize("m,ff", [(7, 160), (256, 160), (9, 162)])
+def test_gemm_glu_within_the_bound(ctx, qtype, dtype, act, clamp, m, ff):
+    k = 1536
     rng = np.random.default_rng(m + act * 10 + int(clamp))
     graw = W.quant_table(rng, ff, k, qtype, (0.004, 0.03))
     uraw = W.quant_table(rng, ff, k, qtype, (0.004, 0.03))
