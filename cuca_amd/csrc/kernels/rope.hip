@@ -75,7 +75,8 @@ __device__ static inline void load_tab(const float *t, int64_t first, float (&v)
 // heads are rotated and the V heads (optionally RMS-normalised without a
 // weight) copied into the paged pools, at pool row slots[row] of their KV
 // head; Q stays in place.
-template <typename T, int KIND, bool NORM, bool STORE>
+// NTL: the head chunks are read with streaming (nontemporal) loads.
+template <typename T, int KIND, bool NORM, bool STORE, bool NTL = false>
 __device__ static inline void rope_body(const RopeArgs &a) {
     constexpr int VP = Chunk<T>::N;
     constexpr int NC = KIND == 2 ? 2 : 1;       // chunks per lane
@@ -125,7 +126,9 @@ __device__ static inline void rope_body(const RopeArgs &a) {
     const int32_t slot = STORE ? a.slots[row] : 0;
     u32x4 raw[NC];
 #pragma unroll
-    for (int k = 0; k < NC; k++) raw[k] = Chunk<T>::load_raw(src, e[k] / VP);
+    for (int k = 0; k < NC; k++)
+        raw[k] = NTL ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(src) + e[k] / VP)
+                     : Chunk<T>::load_raw(src, e[k] / VP);
     const bool pos_ok = pos >= 0 && (int64_t)pos < a.table_rows;
     const bool slot_ok = !STORE || (slot >= 0 && (int64_t)slot < a.n_slots);
     const int64_t t0 = (rot && pos_ok) ? (int64_t)pos * half + (KIND == 2 ? e[0] : (e[0] >> 1)) : 0;
@@ -280,6 +283,11 @@ __device__ static inline void rope_generic_body(const RopeArgs &a) {
     extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void NAME(RopeArgs a) {            \
         rope_body<T, KIND, NORM, STORE>(a);                                                \
     }
+// streaming variants of the QK-norm kernels (see the runtime's rope launch)
+#define CUCA_ROPE_NT(NAME, T, KIND, STORE)                                                 \
+    extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void NAME(RopeArgs a) {            \
+        rope_body<T, KIND, true, STORE, true>(a);                                          \
+    }
 #define CUCA_ROPE_SET(TN, T)                                                               \
     CUCA_ROPE(cuca_rope_##TN##_norm, T, 0, false, false)                                   \
     CUCA_ROPE(cuca_rope_##TN##_neox, T, 2, false, false)                                   \
@@ -289,6 +297,10 @@ __device__ static inline void rope_generic_body(const RopeArgs &a) {
     CUCA_ROPE(cuca_rope_##TN##_neox_kv, T, 2, false, true)                                 \
     CUCA_ROPE(cuca_rope_##TN##_norm_qkn_kv, T, 0, true, true)                              \
     CUCA_ROPE(cuca_rope_##TN##_neox_qkn_kv, T, 2, true, true)                              \
+    CUCA_ROPE_NT(cuca_rope_##TN##_norm_qkn_nt, T, 0, false)                                \
+    CUCA_ROPE_NT(cuca_rope_##TN##_neox_qkn_nt, T, 2, false)                                \
+    CUCA_ROPE_NT(cuca_rope_##TN##_norm_qkn_kv_nt, T, 0, true)                              \
+    CUCA_ROPE_NT(cuca_rope_##TN##_neox_qkn_kv_nt, T, 2, true)                              \
     extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void cuca_rope_##TN##_generic(     \
         RopeArgs a) {                                                                      \
         rope_generic_body<T>(a);                                                           \

@@ -711,7 +711,13 @@ static cuca_status rope_common(cuca_hip_ctx *ctx, void *q, int64_t q_ld, const v
          {{cuca_rope_f32_neox, cuca_rope_f32_neox_kv}, {cuca_rope_f32_neox_qkn, cuca_rope_f32_neox_qkn_kv}}},
         {{{cuca_rope_f16_norm, cuca_rope_f16_norm_kv}, {cuca_rope_f16_norm_qkn, cuca_rope_f16_norm_qkn_kv}},
          {{cuca_rope_f16_neox, cuca_rope_f16_neox_kv}, {cuca_rope_f16_neox_qkn, cuca_rope_f16_neox_qkn_kv}}}};
-    const Kernel kk = table_k[f16][neox][norm][store];
+    static const Kernel table_nt[2][2][2] = {
+        {{cuca_rope_f32_norm_qkn_nt, cuca_rope_f32_norm_qkn_kv_nt}, {cuca_rope_f32_neox_qkn_nt, cuca_rope_f32_neox_qkn_kv_nt}},
+        {{cuca_rope_f16_norm_qkn_nt, cuca_rope_f16_norm_qkn_kv_nt}, {cuca_rope_f16_neox_qkn_nt, cuca_rope_f16_neox_qkn_kv_nt}}};
+    // prefill-sized QK-norm calls stream their head rows (measured: plain
+    // RoPE runs slower streamed, QK-norm RoPE and the kernels after it faster)
+    const bool stream = norm && heads * (int64_t)head_dim * (int64_t)esize(dtype) >= kStreamBytes;
+    const Kernel kk = stream ? table_nt[f16][neox][store] : table_k[f16][neox][norm][store];
     return launch(ctx, kk, div_up(heads, 256 / tph), 256, 0, a);
 }
 
