@@ -107,11 +107,21 @@ __device__ static inline void attn_split_body(const AttnArgs &a) {
     const int rk = blockIdx.x / a.max_parts;
     const int part = blockIdx.x - rk * a.max_parts;
     const int row = rk / a.n_kv, kvh = rk - row * a.n_kv;
+    // The query dwords are loaded into registers first and written to LDS
+    // only after the K/V loads are issued: waiting for them before the
+    // range, block-table and K/V loads put one more memory latency in front
+    // of the part's bulk reads.
+    constexpr int NW = G * D / (sizeof(T) == 2 ? 2 : 1);
+    constexpr int NQ = (NW + CUCA_BLOCK - 1) / CUCA_BLOCK;
+    uint32_t qv[NQ];
     {
         const uint32_t *qg = reinterpret_cast<const uint32_t *>(
             reinterpret_cast<const T *>(a.q) + (int64_t)row * a.q_ld + (int64_t)kvh * G * D);
-        constexpr int NW = G * D / (sizeof(T) == 2 ? 2 : 1);
-        for (int i = threadIdx.x; i < NW; i += CUCA_BLOCK) qs[(i / SL) * SLP + i % SL] = qg[i];
+#pragma unroll
+        for (int k = 0; k < NQ; k++) {
+            const int i = (int)threadIdx.x + k * CUCA_BLOCK;
+            qv[k] = i < NW ? qg[i] : 0u;
+        }
     }
     const int lo = a.ranges[2 * row], hi = a.ranges[2 * row + 1];
     const bool valid = attn_range_ok(a, lo, hi);
@@ -169,6 +179,11 @@ __device__ static inline void attn_split_body(const AttnArgs &a) {
         }
     }
     __builtin_amdgcn_sched_barrier(0); // every load above is issued first
+#pragma unroll
+    for (int k = 0; k < NQ; k++) {
+        const int i = (int)threadIdx.x + k * CUCA_BLOCK;
+        if (i < NW) qs[(i / SL) * SLP + i % SL] = qv[k];
+    }
     __syncthreads();                   // qs is staged
 #pragma unroll
     for (int j = 0; j < KCH; j++) pin(kraw[j]);
