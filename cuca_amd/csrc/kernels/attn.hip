@@ -356,10 +356,50 @@ __device__ static inline void attn_split_generic_body(const AttnArgs &a) {
 
 // Merge of one (row, query head) = job by one wave; lane owns columns lane,
 // lane + 64, ...
+// This lane's (max, sum) of parts lane, lane + 64, ... below lim and the
+// values of parts 0 .. R-1 (the last part below lim repeated past it).
+template <int MAXC, int R>
+__device__ static inline void attn_merge_preload(const float *pp, int64_t stride, int D, int lim, int lane,
+                                                 float (&mv)[MERGE_PL], float (&sv)[MERGE_PL],
+                                                 float (&v0)[R > 0 ? R : 1][MAXC]) {
+#pragma unroll
+    for (int q = 0; q < MERGE_PL; q++) {
+        const int c = lane + q * CUCA_WAVE;
+        mv[q] = c < lim ? pp[(int64_t)c * stride + D] : -INFINITY;
+        sv[q] = c < lim ? pp[(int64_t)c * stride + D + 1] : 0.0f;
+    }
+#pragma unroll
+    for (int jj = 0; jj < R; jj++) {
+        const float *pc = pp + (int64_t)min(jj, lim - 1) * stride;
+#pragma unroll
+        for (int k = 0; k < MAXC; k++) {
+            const int e = lane + k * CUCA_WAVE;
+            v0[jj][k] = e < D ? pc[e] : 0.0f;
+        }
+    }
+}
+
 template <typename T, int MAXC>
 __device__ static inline void attn_merge_job(const AttnArgs &a, int64_t job, int lane) {
     const int row = (int)(job / a.n_head);
     const int D = a.head_dim;
+    const int64_t stride = D + 2;
+    const float *pp = a.part + job * a.max_parts * stride;
+    // Every load of the short path is issued at once: this lane's (max, sum)
+    // of parts lane, lane + 64, ... and the values of the first R parts, so
+    // the merge waits for one round of loads (walking the parts' maxima, sums
+    // and values in turn made four).  When a row can have no more parts than
+    // that path takes (max_parts <= MERGE_PL * 64), they are loaded before the
+    // row's range, up to max_parts: the range and the parts then arrive in
+    // the same round.  Those loads stay inside the workspace, which holds
+    // max_parts parts per (row, head), and a part past the row's count is
+    // loaded but never used.  The arithmetic and its order are those of the
+    // loop below.
+    constexpr int R = MAXC <= 2 ? 32 : MAXC == 4 ? 16 : 0; // whole blocks of 16 parts
+    float mv[MERGE_PL], sv[MERGE_PL];
+    float v0[R > 0 ? R : 1][MAXC];
+    const bool early = a.max_parts <= MERGE_PL * CUCA_WAVE; // uniform
+    if (early) attn_merge_preload<MAXC, R>(pp, stride, D, a.max_parts, lane, mv, sv, v0);
     const int lo = a.ranges[2 * row], hi = a.ranges[2 * row + 1];
     T *o = reinterpret_cast<T *>(a.out) + job * D;
     if (!attn_range_ok(a, lo, hi)) {
@@ -367,36 +407,12 @@ __device__ static inline void attn_merge_job(const AttnArgs &a, int64_t job, int
         return;
     }
     const int np = (hi - (lo & ~15) + a.part_positions - 1) / a.part_positions;
-    const int64_t stride = D + 2;
-    const float *pp = a.part + job * a.max_parts * stride;
     float acc[MAXC]; // columns per lane: head_dim <= 64 MAXC
 #pragma unroll
     for (int k = 0; k < MAXC; k++) acc[k] = 0.0f;
     float total;
     if (np <= MERGE_PL * CUCA_WAVE) {
-        // Every load is issued at once: this lane's (max, sum) of parts
-        // lane, lane + 64, ... and the values of the first R parts, so the
-        // merge waits for one round of loads (walking the parts' maxima, sums
-        // and values in turn made four).  The arithmetic and its order are
-        // those of the loop below.
-        constexpr int R = MAXC <= 2 ? 32 : MAXC == 4 ? 16 : 0; // whole blocks of 16 parts
-        float mv[MERGE_PL], sv[MERGE_PL];
-#pragma unroll
-        for (int q = 0; q < MERGE_PL; q++) {
-            const int c = lane + q * CUCA_WAVE;
-            mv[q] = c < np ? pp[(int64_t)c * stride + D] : -INFINITY;
-            sv[q] = c < np ? pp[(int64_t)c * stride + D + 1] : 0.0f;
-        }
-        float v0[R > 0 ? R : 1][MAXC];
-#pragma unroll
-        for (int jj = 0; jj < R; jj++) {
-            const float *pc = pp + (int64_t)min(jj, np - 1) * stride;
-#pragma unroll
-            for (int k = 0; k < MAXC; k++) {
-                const int e = lane + k * CUCA_WAVE;
-                v0[jj][k] = e < D ? pc[e] : 0.0f;
-            }
-        }
+        if (!early) attn_merge_preload<MAXC, R>(pp, stride, D, np, lane, mv, sv, v0);
         float mx = -INFINITY;
 #pragma unroll
         for (int q = 0; q < MERGE_PL; q++)
