@@ -8,8 +8,12 @@
    FP32 instructions disabled.
 2. The kernel names in csrc/kernel_list.inc are checked against the code
    object's symbols.
-3. g++ compiles csrc/runtime.cpp (host code only) with the code object
-   embedded (.incbin) into libcuca_hip.so, linked to libamdhip64.
+3. hipcc compiles csrc/noalloc.hip (host and gfx950 device code: the
+   allocation-free entry points' scratch array, a registered __device__
+   variable) into a position-independent object.
+4. g++ compiles csrc/runtime.cpp (host code only) with the code object
+   embedded (.incbin) and links it with that object into libcuca_hip.so,
+   linked to libamdhip64.
 
 Both outputs are written in-tree (cuca_amd/), so the .so travels with the
 repository snapshot to the GPU box; nothing is JIT-compiled at run time.
@@ -83,11 +87,16 @@ def build(verbose: bool = False) -> str:
     if missing or unlisted:
         raise RuntimeError(f"kernel_list.inc and the code object disagree: missing {missing}, "
                            f"unlisted {unlisted}")
+    noalloc_obj = os.path.join(BUILD, "noalloc.o")
+    _run([os.path.join(ROCM, "bin/hipcc"), "--offload-arch=gfx950", "-O2", "-std=c++17", "-fPIC",
+          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wall",
+          f"-I{os.path.join(ROOT, 'include')}", f"-I{CSRC}", "-c",
+          os.path.join(CSRC, "noalloc.hip"), "-o", noalloc_obj], verbose)
     lib_tmp = LIB + ".tmp"
     _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-Wall", "-Wextra",
           "-D__HIP_PLATFORM_AMD__", f"-DCUCA_CODE_OBJECT=\"{CODE_OBJECT}\"",
           f"-I{os.path.join(ROOT, 'include')}", f"-I{CSRC}", f"-I{ROCM}/include",
-          os.path.join(CSRC, "runtime.cpp"), "-o", lib_tmp,
+          os.path.join(CSRC, "runtime.cpp"), noalloc_obj, "-o", lib_tmp,
           f"-L{ROCM}/lib", "-lamdhip64", "-lhipblaslt", f"-Wl,-rpath,{ROCM}/lib",
           "-Wl,--no-undefined"], verbose)
     os.replace(lib_tmp, LIB)

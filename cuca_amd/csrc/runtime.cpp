@@ -5,9 +5,12 @@
 // context loads it with hipModuleLoadData, resolves every kernel once with
 // hipModuleGetFunction and launches with hipModuleLaunchKernel, each kernel
 // taking one by-value argument block (kernel_args.h).  Host code only: no
-// device code is compiled into this file.
+// device code is compiled into this file.  The one device variable of the
+// library, the allocation-free entry points' scratch array, is defined in
+// noalloc.hip; this file takes only its per-device address.
 #include "cuca_hip.h"
 #include "kernel_args.h"
+#include "noalloc.h"
 
 #include <hip/hip_runtime_api.h>
 #include <hipblaslt/hipblaslt.h>
@@ -83,6 +86,11 @@ struct cuca_hip_ctx {
     // device scratch for the per-slice results of cuca_hip_argmax / _top_k
     // (allocated with the context: ops never allocate)
     void *pscratch = nullptr;
+    // this device's copy of the allocation-free entry points' scratch array
+    // (noalloc.hip), resolved at creation; its failure, if any, is reported
+    // by those entry points only
+    void *noalloc = nullptr;
+    std::string noalloc_error;
     // hipBLASLt for the dense f16 GEMM of many rows (created on first use)
     // and the algorithms its heuristic picked, per shape
     hipblasLtHandle_t lt = nullptr;
@@ -231,6 +239,12 @@ cuca_status cuca_hip_ctx_create(int device, cuca_hip_ctx **out) {
         }
         if ((e = hipEventCreate(&ctx->t0)) != hipSuccess || (e = hipEventCreate(&ctx->t1)) != hipSuccess) {
             st = hip_fail(ctx, e, "hipEventCreate"); break;
+        }
+        // the device is current: resolve its copy of the allocation-free scratch
+        if ((e = cuca_noalloc_scratch(device, &ctx->noalloc)) != hipSuccess) {
+            ctx->noalloc = nullptr;
+            ctx->noalloc_error = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e);
+            (void)hipGetLastError();
         }
     } while (0);
     if (st != CUCA_OK) {
@@ -785,11 +799,13 @@ cuca_status cuca_hip_paged_decode_workspace(int64_t rows, int32_t n_head, int32_
     return CUCA_OK;
 }
 
-cuca_status cuca_hip_paged_decode(cuca_hip_ctx *ctx, const void *q, int64_t q_ld, const void *pool_k,
-                                  const void *pool_v, int64_t n_blocks, const uint32_t *tables, int64_t max_blocks,
-                                  const int32_t *ranges, int64_t rows, int32_t n_head, int32_t n_kv,
-                                  int32_t head_dim, float scale, void *workspace, size_t workspace_bytes,
-                                  void *out, cuca_dtype dtype) {
+// The paged decode of a caller's workspace (noalloc false) or of the
+// library's scratch array (noalloc true: workspace is ignored).
+static cuca_status paged_decode_run(cuca_hip_ctx *ctx, const void *q, int64_t q_ld, const void *pool_k,
+                                    const void *pool_v, int64_t n_blocks, const uint32_t *tables,
+                                    int64_t max_blocks, const int32_t *ranges, int64_t rows, int32_t n_head,
+                                    int32_t n_kv, int32_t head_dim, float scale, void *workspace,
+                                    size_t workspace_bytes, bool noalloc, void *out, cuca_dtype dtype) {
     cuca_status st = use(ctx);
     if (st != CUCA_OK) return st;
     if (!dtype_ok(dtype)) return fail(ctx, CUCA_INVALID_ARG, "bad dtype %d", (int)dtype);
@@ -802,18 +818,20 @@ cuca_status cuca_hip_paged_decode(cuca_hip_ctx *ctx, const void *q, int64_t q_ld
         return fail(ctx, CUCA_INVALID_ARG, "bad block table width %lld", (long long)max_blocks);
     if (n_blocks <= 0) return fail(ctx, CUCA_INVALID_ARG, "bad pool size %lld blocks", (long long)n_blocks);
     if (rows == 0) return CUCA_OK;
-    if (!q || !pool_k || !pool_v || !tables || !ranges || !out || !workspace)
+    if (!q || !pool_k || !pool_v || !tables || !ranges || !out || (!noalloc && !workspace))
         return fail(ctx, CUCA_INVALID_ARG, "null pointer");
     if (q_ld < (int64_t)n_head * head_dim)
         return fail(ctx, CUCA_INVALID_ARG, "q row stride %lld below %d heads of %d", (long long)q_ld, n_head,
                     head_dim);
     if (((size_t)q_ld * esize(dtype)) % 4 != 0 || (reinterpret_cast<uintptr_t>(q) & 3) != 0)
         return fail(ctx, CUCA_INVALID_ARG, "q rows must be 4-byte aligned");
-    size_t need = 0;
-    cuca_hip_paged_decode_workspace(rows, n_head, head_dim, max_blocks, &need);
-    if (workspace_bytes < need)
-        return fail(ctx, CUCA_INVALID_ARG, "workspace of %zu bytes, %zu needed", workspace_bytes, need);
-    if (!al16(workspace)) return fail(ctx, CUCA_INVALID_ARG, "workspace must be 16-byte aligned");
+    if (!noalloc) {
+        size_t need = 0;
+        cuca_hip_paged_decode_workspace(rows, n_head, head_dim, max_blocks, &need);
+        if (workspace_bytes < need)
+            return fail(ctx, CUCA_INVALID_ARG, "workspace of %zu bytes, %zu needed", workspace_bytes, need);
+        if (!al16(workspace)) return fail(ctx, CUCA_INVALID_ARG, "workspace must be 16-byte aligned");
+    }
     const bool f16 = dtype == CUCA_F16;
     const size_t es = esize(dtype);
     const int G = n_head / n_kv;
@@ -833,6 +851,19 @@ cuca_status cuca_hip_paged_decode(cuca_hip_ctx *ctx, const void *q, int64_t q_ld
     }
     const int64_t parts = attn_max_parts(max_blocks, part_positions);
     if (rows * n_head * parts > 0x7fffffffll) return fail(ctx, CUCA_UNSUPPORTED, "too many attention parts");
+    if (noalloc) {
+        // the partials this call writes and reads: [rows, n_head, parts, head_dim + 2] f32
+        const double used = (double)rows * (double)n_head * (double)parts * (double)(head_dim + 2) * 4.0;
+        if (used > (double)CUCA_NOALLOC_SCRATCH_BYTES)
+            return fail(ctx, CUCA_INVALID_ARG,
+                        "paged_decode_noalloc: %lld rows x %d heads x %lld parts of %d values need %.0f bytes "
+                        "of scratch, above the library's %u (use cuca_hip_paged_decode with a workspace)",
+                        (long long)rows, n_head, (long long)parts, head_dim + 2, used,
+                        (unsigned)CUCA_NOALLOC_SCRATCH_BYTES);
+        if (!ctx->noalloc) return fail(ctx, CUCA_HIP_ERROR, "paged_decode_noalloc: no scratch on device %d: %s",
+                                       ctx->device, ctx->noalloc_error.c_str());
+        workspace = ctx->noalloc;
+    }
     AttnArgs a{};
     a.q = q;
     a.q_ld = q_ld;
@@ -880,6 +911,24 @@ cuca_status cuca_hip_paged_decode(cuca_hip_ctx *ctx, const void *q, int64_t q_ld
     const int cpl = (head_dim + 63) / 64;
     const int ci = cpl <= 1 ? 0 : cpl <= 2 ? 1 : cpl <= 4 ? 2 : 3;
     return launch(ctx, km[f16][ci], div_up(rows * n_head, 4), 256, 0, a);
+}
+
+cuca_status cuca_hip_paged_decode(cuca_hip_ctx *ctx, const void *q, int64_t q_ld, const void *pool_k,
+                                  const void *pool_v, int64_t n_blocks, const uint32_t *tables, int64_t max_blocks,
+                                  const int32_t *ranges, int64_t rows, int32_t n_head, int32_t n_kv,
+                                  int32_t head_dim, float scale, void *workspace, size_t workspace_bytes,
+                                  void *out, cuca_dtype dtype) {
+    return paged_decode_run(ctx, q, q_ld, pool_k, pool_v, n_blocks, tables, max_blocks, ranges, rows, n_head,
+                            n_kv, head_dim, scale, workspace, workspace_bytes, false, out, dtype);
+}
+
+cuca_status cuca_hip_paged_decode_noalloc(cuca_hip_ctx *ctx, const void *q, int64_t q_ld, const void *pool_k,
+                                          const void *pool_v, int64_t n_blocks, const uint32_t *tables,
+                                          int64_t max_blocks, const int32_t *ranges, int64_t rows, int32_t n_head,
+                                          int32_t n_kv, int32_t head_dim, float scale, void *out,
+                                          cuca_dtype dtype) {
+    return paged_decode_run(ctx, q, q_ld, pool_k, pool_v, n_blocks, tables, max_blocks, ranges, rows, n_head,
+                            n_kv, head_dim, scale, nullptr, 0, true, out, dtype);
 }
 
 // ---------------------------------------------------------------------

@@ -71,6 +71,8 @@ SIGNATURES = {
     "cuca_hip_paged_decode_workspace": (_st, [_i64, _i32, _i32, _i64, ctypes.POINTER(_sz)]),
     "cuca_hip_paged_decode": (_st, [_p, _p, _i64, _p, _p, _i64, _p, _i64, _p, _i64, _i32, _i32,
                                     _i32, _f32, _p, _sz, _p, _st]),
+    "cuca_hip_paged_decode_noalloc": (_st, [_p, _p, _i64, _p, _p, _i64, _p, _i64, _p, _i64, _i32,
+                                            _i32, _i32, _f32, _p, _st]),
     "cuca_hip_rope_tables": (_st, [ctypes.POINTER(RopeSpecC), _p, _i64, _p, _p]),
     "cuca_hip_qweight_bytes": (_st, [_u32, _i64, _i64, ctypes.POINTER(_sz)]),
     "cuca_hip_qweight_pack": (_st, [_p, _p, _u32, _i64, _i64, _p]),
@@ -337,6 +339,16 @@ class Context:
                                                 max_blocks, ranges, rows, n_head, n_kv, head_dim,
                                                 scale, workspace, workspace_bytes, out, dtype))
 
+    def paged_decode_noalloc(self, q, pool_k, pool_v, n_blocks, tables, max_blocks, ranges, rows,
+                             n_head, n_kv, head_dim, scale, out, dtype, q_ld=None):
+        """cuca_hip_paged_decode without a workspace: the partials go to the
+        library's per-device scratch array (no allocation in the call)."""
+        if q_ld is None:
+            q_ld = n_head * head_dim
+        self.check(self.L.cuca_hip_paged_decode_noalloc(self.ptr, q, q_ld, pool_k, pool_v, n_blocks,
+                                                        tables, max_blocks, ranges, rows, n_head, n_kv,
+                                                        head_dim, scale, out, dtype))
+
     def rope_store_kv(self, q, q_ld, k, k_ld, v, v_ld, rows, nq, nk, head_dim, n_dims, kind, cos,
                       sin, table_rows, positions, q_norm_w, k_norm_w, v_norm, eps, pool_k, pool_v,
                       n_blocks, slots, dtype):
@@ -442,6 +454,7 @@ class Graph:
 
 KV_BLOCK = 16          # positions per paged K/V block (paged.rs:45)
 NO_BLOCK = 0xFFFFFFFF  # a released block's table entry (paged.rs:49)
+NOALLOC_SCRATCH_BYTES = 64 << 20  # CUCA_NOALLOC_SCRATCH_BYTES
 
 
 def qgemm_workspace(ggml_type, n, k, m, glu=False):

@@ -240,6 +240,21 @@ class KvPool:
                               workspace.nbytes, out.ptr, hip.dtype_code(q.dtype))
         return out
 
+    def decode_noalloc(self, q, tables, ranges, n_head, scale, out=None):
+        """`decode` through cuca_hip_paged_decode_noalloc: no workspace, the
+        call allocates nothing on the device (`out`, a DeviceArray [rows,
+        n_head, d], may be passed in; else one is made here, outside the
+        call)."""
+        rows, nh, d = q.shape
+        if nh != n_head or d != self.head_dim:
+            raise CucaError(hip.INVALID_ARG, "attention: query shape mismatch")
+        if out is None:
+            out = self.ctx.empty((rows, n_head, d), q.dtype)
+        self.ctx.paged_decode_noalloc(q.ptr, self.k.ptr, self.v.ptr, self.n_blocks, tables.ptr,
+                                      tables.shape[1], ranges.ptr, rows, n_head, self.n_kv_head, d,
+                                      scale, out.ptr, hip.dtype_code(q.dtype))
+        return out
+
     def read(self, slots):
         """The rows `slots` name, the inverse of the store (KvPool::read,
         gpu.rs:1808-1830): host (k, v) [len(slots), n_kv_head, head_dim]."""

@@ -278,6 +278,29 @@ cuca_status cuca_hip_paged_decode(cuca_hip_ctx *ctx, const void *q, int64_t q_ld
                                   void *workspace, size_t workspace_bytes, void *out,
                                   cuca_dtype dtype);
 
+/* No counterpart in the reference.  cuca_hip_paged_decode without a
+ * workspace, for callers that cannot allocate (code under HIP graph capture,
+ * serving loops or harnesses that forbid hipMalloc): the split pass's
+ * partials go to a library-owned device array of CUCA_NOALLOC_SCRATCH_BYTES,
+ * one per GPU, held from the first context on that GPU until the process
+ * ends.  The call allocates nothing; the caller passes the inputs and the
+ * output, as to cuca_hip_paged_decode, and gets the same bits.  A call whose
+ * partials need more than the maximum -- rows * n_head * parts * (head_dim +
+ * 2) * 4 bytes, parts = ceil(max_blocks * 16 / part length), the part length
+ * 64 to 256 positions by dtype, head_dim and group -- fails with
+ * CUCA_INVALID_ARG before any launch.  Nothing in the array has to start at
+ * zero (every partial a merge reads is written by the same call's split);
+ * it keeps the last call's contents.  Every call on one GPU shares the
+ * array: calls that overlap on one GPU (other streams, other contexts or
+ * threads) race and must be ordered by the caller. */
+#define CUCA_NOALLOC_SCRATCH_BYTES (64u << 20)
+cuca_status cuca_hip_paged_decode_noalloc(cuca_hip_ctx *ctx, const void *q, int64_t q_ld,
+                                          const void *pool_k, const void *pool_v, int64_t n_blocks,
+                                          const uint32_t *tables, int64_t max_blocks,
+                                          const int32_t *ranges, int64_t rows, int32_t n_head,
+                                          int32_t n_kv, int32_t head_dim, float scale, void *out,
+                                          cuca_dtype dtype);
+
 /* ------------------------------------------------------------------ */
 /* Quantized matmul (the CPU engine's QmmWeight, qmm.rs)               */
 /* ------------------------------------------------------------------ */
