@@ -181,12 +181,23 @@ class LayerStep:
         def host(t, idx=st):
             return t[idx].cpu().numpy()
 
+        raw = {}
+
         def close(got, want, what, floor=0.0):
+            # the bar, and the raw error before the floor: max relative error
+            # (f32) or f16 ulps, and the values inside the bar only by the floor
             g, w = got.astype(np.float64), want.astype(np.float64)
-            tol = (2 * np.spacing(np.abs(w).astype(np.float16)).astype(np.float64) if f16
-                   else 1e-5 * np.abs(w)) + floor + 1e-37
-            bad = np.abs(g - w) > tol
+            ulp = np.spacing(np.abs(w).astype(np.float16)).astype(np.float64) if f16 else None
+            plain = (2 * ulp if f16 else 1e-5 * np.abs(w)) + 1e-37
+            d = np.abs(g - w)
+            bad = d > plain + floor
             assert not bad.any(), f"{self.name} n={n} {what}: {bad.sum()} values outside tolerance"
+            err = d / np.where(ulp > 0, ulp, 1.0) if f16 else d / np.maximum(np.abs(w), 1e-30)
+            r = raw.setdefault(what, {"max_ulp" if f16 else "max_rel": 0.0, "floored": 0, "n": 0})
+            k = "max_ulp" if f16 else "max_rel"
+            r[k] = max(r[k], float(err.max()))
+            r["floored"] += int(np.count_nonzero(d > plain))
+            r["n"] += int(d.size)
 
         rb = (18 if cfg["qtype"] == "q4_0" else 34) * H // 32
         sub = self.table.view(cfg["vocab"], rb)[self.ids[st].long()].cpu().numpy().reshape(-1)
@@ -214,7 +225,12 @@ class LayerStep:
                 assert np.array_equal(host(t).view(np.uint8), w.view(np.uint8)), "rope"
             else:
                 w = O.rope(host(t0), cos, sin, pos, self.kind, norm_w=nw.cpu().numpy(), eps=cfg["eps"])
-                mag = np.sqrt((w.astype(np.float64) ** 2).sum(-1, keepdims=True) / d)
+                # 1e-5 of each rotated pair's magnitude (a*c - b*s cancels)
+                w64 = w.astype(np.float64)
+                ia = np.arange(d // 2) if self.kind == self.hip.ROPE_NEOX else 2 * np.arange(d // 2)
+                ib = ia + d // 2 if self.kind == self.hip.ROPE_NEOX else ia + 1
+                mag = np.zeros_like(w64)
+                mag[..., ia] = mag[..., ib] = np.hypot(w64[..., ia], w64[..., ib])
                 close(host(t), w, "normed rope", 1e-5 * mag)
         gs = np.unique(np.concatenate([[0, self.rows_glu - 1],
                                        rng.integers(0, self.rows_glu, rows)]))
@@ -228,7 +244,11 @@ class LayerStep:
                    O.GELU_TANH if self.act == self.hip.ACT_GELU_TANH else O.SILU)
         fl = 2.0 ** -22 * np.abs(0.5 * g.astype(np.float64) * u.astype(np.float64))
         close(host(self.out, gst), wa, "glu", fl if self.act == self.hip.ACT_GELU_TANH else 0.0)
-        return int(s.size + gs.size)
+        for r in raw.values():
+            for k in ("max_rel", "max_ulp"):
+                if k in r:
+                    r[k] = float(f"{r[k]:.3g}")
+        return int(s.size + gs.size), raw
 
 
 def time_steps(torch, fn, steps, warmup):
@@ -1151,6 +1171,8 @@ def main():
     copy_gbs = 2 * cal_n * 2 / (cal_ms / 1e3) / 1e9
     del cal_src, cal_dst
 
+    parity_raw = {}
+
     def run_size(n, steps, warmup, name="C", dtype="f16"):
         log(f"config {name}: step buffers, {n} tokens, {dtype}")
         st = LayerStep(ctx, torch, name, n, dtype)
@@ -1166,7 +1188,8 @@ def main():
                           frac=round(st.bytes[name] / (t / 1e3) / 1e9 / HBM_PEAK_GBS, 4))
                for name, (k, t) in per.items()}
         log("verify sampled rows against the oracle")
-        rows = st.verify()
+        rows, raw = st.verify()
+        parity_raw[f"{name}_{n}_{dtype}"] = raw
         step_bytes = sum(st.bytes.values())
         del st
         torch.cuda.empty_cache()
@@ -1279,6 +1302,7 @@ def main():
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),
         "copy_gbs": round(copy_gbs, 1),
         "verified_rows": checked_rows,
+        "parity_raw": parity_raw,
         "ops": ops,
         "prefill_16384": big,
         "configs": configs,

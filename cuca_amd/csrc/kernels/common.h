@@ -22,6 +22,14 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 #define CUCA_BLOCK 256
 
 // A 16-byte chunk of activations of type T, widened to f32 in registers.
+// v, materialised as an f32 value: an operation written before it cannot be
+// merged with one written after it (a multiply with the next multiply's
+// rounding, or with a conversion to f16 into one v_fma_mix*_f16).
+__device__ static inline float pin_f32(float v) {
+    asm volatile("" : "+v"(v));
+    return v;
+}
+
 template <typename T> struct Chunk;
 
 template <> struct Chunk<float> {
@@ -77,16 +85,18 @@ template <> struct Chunk<_Float16> {
 #pragma unroll
         for (int i = 0; i < 8; i++) v[i] = (float)t[i];
     }
+    // (each f32 value is pinned before its conversion, so the f16 output is
+    // the f32 result rounded once more, never a single fused rounding)
     __device__ static inline void store(void *base, int64_t chunk, const float (&v)[8]) {
         f16x8 t;
 #pragma unroll
-        for (int i = 0; i < 8; i++) t[i] = (_Float16)v[i];
+        for (int i = 0; i < 8; i++) t[i] = (_Float16)pin_f32(v[i]);
         reinterpret_cast<f16x8 *>(base)[chunk] = t;
     }
     __device__ static inline void store_nt(void *base, int64_t chunk, const float (&v)[8]) {
         f16x8 t;
 #pragma unroll
-        for (int i = 0; i < 8; i++) t[i] = (_Float16)v[i];
+        for (int i = 0; i < 8; i++) t[i] = (_Float16)pin_f32(v[i]);
         __builtin_nontemporal_store(t, reinterpret_cast<f16x8 *>(base) + chunk);
     }
     // (the f32 value is pinned first: otherwise the compiler may fold the
@@ -106,14 +116,6 @@ template <> struct Chunk<_Float16> {
     }
 };
 
-// v, materialised as an f32 value: an operation written before it cannot be
-// merged with one written after it (a multiply with the next multiply's
-// rounding, or with a conversion to f16 into one v_fma_mix*_f16).
-__device__ static inline float pin_f32(float v) {
-    asm volatile("" : "+v"(v));
-    return v;
-}
-
 // Load chunk `c` of `base`, streaming (NT) or cached.
 template <typename T, bool NT, int N>
 __device__ static inline void load_chunk(const void *base, int64_t c, float (&v)[N]) {
@@ -125,8 +127,13 @@ __device__ static inline void load_chunk(const void *base, int64_t c, float (&v)
 template <typename T> __device__ static inline float load1(const void *p, int64_t i) {
     return (float)reinterpret_cast<const T *>(p)[i];
 }
+// The value stored as T: an f16 store rounds the pinned f32 value.
+template <typename T> __device__ static inline T to_stored(float v) {
+    if constexpr (sizeof(T) == 2) return (T)pin_f32(v);
+    else return (T)v;
+}
 template <typename T> __device__ static inline void store1(void *p, int64_t i, float v) {
-    reinterpret_cast<T *>(p)[i] = (T)v;
+    reinterpret_cast<T *>(p)[i] = to_stored<T>(v);
 }
 
 // Sum over aligned groups of G lanes (G a power of two <= 64).  A butterfly:

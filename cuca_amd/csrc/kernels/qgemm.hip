@@ -297,7 +297,7 @@ __device__ static inline void qgemm_body(const QGemmArgs &a) {
                 }
                 o = (ACT == 0 ? act_silu(g) : act_gelu_tanh(g)) * u;
             }
-            orow[n] = (T)o;
+            orow[n] = to_stored<T>(o);
         }
     }
 }
@@ -321,7 +321,7 @@ template <typename T, bool GLU, int ACT> __device__ static inline void qgemm_red
         }
         o = (ACT == 0 ? act_silu(g) : act_gelu_tanh(g)) * u;
     }
-    reinterpret_cast<T *>(a.out)[(int64_t)tok * a.out_ld + n] = (T)o;
+    reinterpret_cast<T *>(a.out)[(int64_t)tok * a.out_ld + n] = to_stored<T>(o);
 }
 
 #define CUCA_QGEMM(NAME, BODY, ...)                                                        \

@@ -559,7 +559,7 @@ __device__ static inline void qmm_body(const QmmArgs &a) {
             if (MODE == 2) // CpuExpert::add_picks: y * weight (cpu.rs:400-417)
                 reinterpret_cast<float *>(a.out)[tl.orow[j] + row] = o * tl.weight[j];
             else
-                reinterpret_cast<T *>(a.out)[tl.orow[j] + row] = (T)o;
+                reinterpret_cast<T *>(a.out)[tl.orow[j] + row] = to_stored<T>(o);
         }
     }
 }
@@ -601,7 +601,7 @@ template <typename T> __device__ static inline void moe_sum_body(const MoeSumArg
     T *dst = reinterpret_cast<T *>(a.out) + (int64_t)t * a.out_ld + h0;
 #pragma unroll
     for (int e = 0; e < 4; e++)
-        if (h0 + e < a.n_embd) dst[e] = (T)acc[e];
+        if (h0 + e < a.n_embd) dst[e] = to_stored<T>(acc[e]);
 }
 
 extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void cuca_moe_sum_f32(MoeSumArgs a) { moe_sum_body<float>(a); }

@@ -354,7 +354,7 @@ __device__ static inline void qmv_body(const QmvArgs &a) {
             if (MODE == 2) // CpuExpert::add_picks: y * weight (cpu.rs:400-417)
                 reinterpret_cast<float *>(a.out)[(int64_t)(p0 + j) * a.out_ld + row] = o * a.pair_weight[p0 + j];
             else
-                reinterpret_cast<TO *>(a.out)[(int64_t)(p0 + j) * a.out_ld + row] = (TO)o;
+                reinterpret_cast<TO *>(a.out)[(int64_t)(p0 + j) * a.out_ld + row] = to_stored<TO>(o);
         }
         __builtin_amdgcn_wave_barrier();
     }

@@ -28,3 +28,38 @@ def ctx():
     c = hip.Context(0)
     yield c
     c.close()
+
+
+@pytest.fixture(autouse=True)
+def _name_the_test(request):
+    """Tag the raw-error records of assert_close with the running test."""
+    import helpers
+    helpers.CURRENT_TEST[0] = request.node.nodeid
+    yield
+
+
+def pytest_terminal_summary(terminalreporter):
+    """The unfloored errors behind the tolerance bars: per op family (test
+    file), the maximum relative error (f32) and f16 ulps, and how many
+    elements passed only through a stated floor."""
+    try:
+        import helpers
+    except ImportError:
+        return
+    if not helpers.RAW:
+        return
+    fam = {}
+    for test, what, st in helpers.RAW:
+        key = (test.split("::")[0].split("/")[-1], st["dtype"])
+        f = fam.setdefault(key, {"n": 0, "worst": 0.0, "floored": 0, "at": ""})
+        v = st.get("max_rel", st.get("max_ulp", 0.0))
+        f["n"] += st["n"]
+        f["floored"] += st["floored"]
+        if v > f["worst"]:
+            f["worst"], f["at"] = v, f"{test.split('::')[-1]} {what}"
+    tr = terminalreporter
+    tr.section("raw errors before floors (f32: max relative error; f16: max ulps)")
+    for (file, dt), f in sorted(fam.items()):
+        unit = "rel" if dt == "f32" else "ulp"
+        tr.write_line(f"{file:28s} {dt}  max {unit} {f['worst']:.3g}  values {f['n']}  "
+                      f"within the bar only by a floor {f['floored']}  (worst: {f['at']})")

@@ -18,7 +18,22 @@ def _f64(a):
 
 
 def ulp16(v):
-    return np.spacing(np.abs(_f64(v)).astype(np.float16)).astype(np.float64)
+    with np.errstate(invalid="ignore", over="ignore"):
+        return np.spacing(np.abs(_f64(v)).astype(np.float16)).astype(np.float64)
+
+
+def pair_floor(want, kind_neox, n_dims):
+    """1e-5 x the magnitude of each rotated pair of a QK-normed RoPE output,
+    broadcast to its two values (a*c - b*s cancels; the rotation keeps the
+    pair's magnitude)."""
+    w = _f64(want)
+    half = n_dims // 2
+    a = np.arange(half) if kind_neox else 2 * np.arange(half)
+    b = a + half if kind_neox else a + 1
+    mag = np.zeros_like(w)
+    m = np.hypot(w[..., a], w[..., b])
+    mag[..., a], mag[..., b] = m, m
+    return 1e-5 * mag
 
 
 def assert_bits_equal(got, want, what=""):
@@ -33,25 +48,63 @@ def assert_bits_equal(got, want, what=""):
                              f"got {got[tuple(idx[0])]!r} want {want[tuple(idx[0])]!r}")
 
 
+# Raw (unfloored) errors of every assert_close of the session, for the
+# summary conftest prints at the end of the run: (test, what, dtype, stats).
+RAW = []
+CURRENT_TEST = [""]
+
+
+def error_stats(got, want, floor=None, rel=1e-5, ulps=2):
+    """The error against the north star's plain bar, before any floor:
+    f32 -> the maximum relative error |got - want| / |want|; f16 -> the
+    maximum error in f16 ulps of want.  `floored` counts the elements within
+    the bar only because of the floor (outside rel |want| or ulps ulp, inside
+    the bar plus the floor)."""
+    g, w = _f64(got), _f64(want)
+    with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
+        ok = np.isfinite(g) & np.isfinite(w)
+        d = np.where(ok, np.abs(g - w), 0.0)
+        f16 = np.asarray(got).dtype == np.float16
+        if f16:
+            u = ulp16(want)
+            base = ulps * u
+            err = np.where(ok & (u > 0), d / np.where(u > 0, u, 1.0), 0.0)
+        else:
+            base = rel * np.abs(w)
+            err = np.where(ok, d / np.maximum(np.abs(w), 1e-30), 0.0)
+        plain = base + 1e-37
+        fl = 0.0 if floor is None else floor
+        floored = int(np.count_nonzero(ok & (d > plain) & (d <= plain + fl)))
+    return {"dtype": "f16" if f16 else "f32", "n": int(g.size),
+            "max_ulp" if f16 else "max_rel": float(err.max()) if err.size else 0.0,
+            "floored": floored}
+
+
 def assert_close(got, want, floor=None, rel=1e-5, ulps=2, what=""):
     """f32: |got - want| <= rel |want| + floor; f16: <= ulps * ulp16(want) +
-    floor.  `want` is the oracle's output in the same dtype."""
+    floor.  `want` is the oracle's output in the same dtype.  Returns the
+    raw error statistics (error_stats) and records them for the session
+    summary."""
     g, w = _f64(got), _f64(want)
     assert g.shape == w.shape, (g.shape, w.shape)
-    if np.asarray(got).dtype == np.float16:
-        tol = ulps * ulp16(want)
-    else:
-        tol = rel * np.abs(w)
-    tol = tol + 1e-37
-    if floor is not None:
-        tol = tol + floor
-    same_nan = np.isnan(g) & np.isnan(w)
-    bad = (np.abs(g - w) > tol) & ~same_nan
+    with np.errstate(invalid="ignore", over="ignore"):
+        if np.asarray(got).dtype == np.float16:
+            tol = ulps * ulp16(want)
+        else:
+            tol = rel * np.abs(w)
+        tol = tol + 1e-37
+        if floor is not None:
+            tol = tol + floor
+        same_nan = np.isnan(g) & np.isnan(w)
+        bad = (np.abs(g - w) > tol) & ~same_nan
     if bad.any():
         i = tuple(np.argwhere(bad)[0])
         worst = np.max(np.abs(g - w)[bad] / np.maximum(tol[bad], 1e-300))
         raise AssertionError(f"{what}: {bad.sum()} of {bad.size} outside tolerance "
                              f"(worst {worst:.2f}x); first at {list(i)}: got {g[i]!r} want {w[i]!r}")
+    st = error_stats(got, want, floor, rel, ulps)
+    RAW.append((CURRENT_TEST[0], what, st))
+    return st
 
 
 def max_rel(got, want):

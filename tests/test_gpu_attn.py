@@ -255,3 +255,42 @@ def test_repeated_calls_and_graph_replays_keep_their_bits(ctx):
             ctx.check_device()
     finally:
         g.destroy()
+
+
+@pytest.mark.parametrize("dtype,nq,nk,d", [("f32", 6, 2, 40), ("f32", 32, 8, 128)])
+def test_wide_tables_take_the_late_and_the_long_merge(ctx, dtype, nq, nk, d):
+    """A block table wide enough that a row may have more than 256 parts
+    (2200 blocks = 35200 keys: 550 parts of the generic kernel's 64
+    positions, 275 of the f32 d128 kernel's 128), so the merge cannot issue
+    its loads before the range is known (the late short path), and rows
+    long enough for the long path (more than 256 parts: 20000 keys for the
+    generic kernel, 34000 for d128).  The workspace starts filled with NaN,
+    so parts past a row's count must be selected away, not multiplied by 0.
+    A short row gives the same bits with a narrow table."""
+    rng = np.random.default_rng(14 + d)
+    n_blocks, width = 2200, 2200
+    lengths = [300, 20000, 34000, 1, 4097]
+    tables = np.full((len(lengths), width), O.NO_BLOCK, np.uint32)
+    ranges = np.zeros((len(lengths), 2), np.int32)
+    for r, hi in enumerate(lengths):
+        nb = (hi + 15) // 16
+        tables[r, :nb] = rng.choice(n_blocks, nb, replace=False)
+        lo = hi - 1000 if r == 4 else 0   # one row with a window floor
+        tables[r, :lo // 16] = O.NO_BLOCK
+        ranges[r] = (lo, hi)
+    pk = rng.standard_normal((n_blocks, nk, 16, d)).astype(NP[dtype])
+    pv = rng.standard_normal((n_blocks, nk, 16, d)).astype(NP[dtype])
+    q = (2.0 * rng.standard_normal((len(lengths), nq, d))).astype(NP[dtype])
+    pool = ops.KvPool(ctx, n_blocks, nk, d, NP[dtype])
+    pool.k.upload(pk)
+    pool.v.upload(pv)
+    need = hip.paged_decode_workspace(len(lengths), nq, d, width)
+    ws = ctx.array(np.full(need // 4, np.nan, np.float32))
+    dt, dr = ctx.array(tables), ctx.array(ranges)
+    got = pool.decode(ctx.array(q), dt, dr, nq, 1.0 / np.sqrt(d), workspace=ws).numpy()
+    ctx.check_device()
+    want = O.paged_attention(q, tables, ranges, pk, pv, 1.0 / np.sqrt(d), threads=8)
+    assert_close(got, want, floor=floor_of(tables, ranges, pv, nq), what="wide-table attention")
+    # the 300-key row with a 20-block table: the early short path, same bits
+    narrow = run(ctx, q[:1], pk, pv, tables[:1, :20], ranges[:1], nq, 1.0 / np.sqrt(d))
+    assert_bits_equal(narrow[0], got[0], "narrow vs wide table")
