@@ -36,7 +36,7 @@ typedef struct {
     int32_t hidden;
     int32_t n;
     float scale;
-    int32_t pad_;
+    float norm_eps;         /* the _norm kernels: rms_norm_rows' eps       */
 } EmbedArgs;
 
 typedef struct {

@@ -27,10 +27,74 @@
 
 #include "common.h"
 
+// Issue the loads of a round's units: lane unit u = u0 + lane + 64 k holds
+// the block's f16 scale (dq) and the 4 (Q4_0) or 8 (Q8_0) quant bytes of its
+// 8 values (w, four 16-bit words).  A lane past the row end reloads the
+// last unit.
+template <int QT, int UPL>
+__device__ static inline void embed_load(const uint16_t *s16, int u0, int lane, int nu, uint32_t (&dq)[UPL],
+                                         uint32_t (&w)[UPL][4]) {
+    constexpr int BS = QT == 2 ? 18 : 34; // bytes per 32-value block
+#pragma unroll
+    for (int k = 0; k < UPL; k++) {
+        int u = u0 + lane + CUCA_WAVE * k;
+        u = u < nu ? u : nu - 1;
+        const int e0 = u * 8;
+        const int ob = (e0 >> 5) * BS; // byte offset of the block (even)
+        const int p = e0 & 31;         // first value within the block
+        dq[k] = s16[ob >> 1];
+        // Q4_0: byte j holds value j (low nibble) and j + 16 (high);
+        // Q8_0: 32 signed bytes
+        const int q0 = (ob + 2 + (QT == 2 ? (p & 15) : p)) >> 1;
+#pragma unroll
+        for (int j = 0; j < 4; j++) w[k][j] = s16[q0 + j];
+    }
+}
+
+// The 8 values of unit u: d' = f32(d) * scale, then f32(q) * d'.
+template <int QT>
+__device__ static inline void embed_dequant(int u, uint32_t dq, const uint32_t (&w)[4], float scale,
+                                            float (&v)[8]) {
+    const int p = (u * 8) & 31;
+    const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)dq) * scale;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        if (QT == 2) {
+            const int sh = p >= 16 ? 4 : 0;
+            v[2 * j] = (float)((int)((w[j] >> sh) & 0xfu) - 8) * d;
+            v[2 * j + 1] = (float)((int)((w[j] >> (8 + sh)) & 0xfu) - 8) * d;
+        } else {
+            v[2 * j] = (float)(int8_t)(w[j] & 0xffu) * d;
+            v[2 * j + 1] = (float)(int8_t)(w[j] >> 8) * d;
+        }
+    }
+}
+
+template <typename OutT>
+__device__ static inline void embed_store(OutT *orow, int u, const float (&v)[8]) {
+    constexpr int CPU = 8 / Chunk<OutT>::N; // output chunks per unit
+    if (CPU == 1) {
+        Chunk<OutT>::store_nt(orow, u, reinterpret_cast<const float(&)[Chunk<OutT>::N]>(v));
+    } else {
+        Chunk<OutT>::store_nt(orow, 2 * u, reinterpret_cast<const float(&)[Chunk<OutT>::N]>(v[0]));
+        Chunk<OutT>::store_nt(orow, 2 * u + 1, reinterpret_cast<const float(&)[Chunk<OutT>::N]>(v[4]));
+    }
+}
+
+// An id the host could not see: a zero row, no read outside the table,
+// and the id reported.
+template <typename OutT>
+__device__ static inline void embed_bad_id(const EmbedArgs &a, OutT *orow, int tok, uint32_t id, int lane) {
+    constexpr int CPU = 8 / Chunk<OutT>::N;
+    if (lane == 0) record_bad(a.status + CUCA_STATUS_EMBED_ID, (uint32_t)tok, id);
+    float z[Chunk<OutT>::N];
+#pragma unroll
+    for (int i = 0; i < Chunk<OutT>::N; i++) z[i] = 0.0f;
+    for (int c = lane; c < a.hidden / 8 * CPU; c += CUCA_WAVE) Chunk<OutT>::store_nt(orow, c, z);
+}
+
 template <int QT, typename OutT, int UPL>
 __device__ static inline void embed_body(const EmbedArgs &a) {
-    constexpr int BS = QT == 2 ? 18 : 34;     // bytes per 32-value block
-    constexpr int CPU = 8 / Chunk<OutT>::N;   // output chunks per unit
     const int tok = blockIdx.x * (CUCA_BLOCK / CUCA_WAVE) + (int)(threadIdx.x / CUCA_WAVE);
     const int lane = threadIdx.x & (CUCA_WAVE - 1);
     if (tok >= a.n) return; // whole wave
@@ -38,70 +102,130 @@ __device__ static inline void embed_body(const EmbedArgs &a) {
     OutT *orow = reinterpret_cast<OutT *>(a.out) + (int64_t)tok * a.hidden;
     const uint32_t id = a.ids[tok];
     if ((int64_t)id >= a.vocab) {
-        // The host could not see this id; write a zero row, never read
-        // outside the table, and report it.
-        if (lane == 0) record_bad(a.status + CUCA_STATUS_EMBED_ID, (uint32_t)tok, id);
-        float z[Chunk<OutT>::N];
-#pragma unroll
-        for (int i = 0; i < Chunk<OutT>::N; i++) z[i] = 0.0f;
-        for (int c = lane; c < nu * CPU; c += CUCA_WAVE) Chunk<OutT>::store_nt(orow, c, z);
+        embed_bad_id<OutT>(a, orow, tok, id, lane);
         return;
     }
     const uint16_t *s16 = reinterpret_cast<const uint16_t *>(a.table + (int64_t)id * a.row_bytes);
     for (int u0 = 0; u0 < nu; u0 += CUCA_WAVE * UPL) {
         uint32_t dq[UPL], w[UPL][4];
-#pragma unroll
-        for (int k = 0; k < UPL; k++) {
-            int u = u0 + lane + CUCA_WAVE * k;
-            u = u < nu ? u : nu - 1; // a lane past the row end reloads the last unit
-            const int e0 = u * 8;
-            const int ob = (e0 >> 5) * BS; // byte offset of the block (even)
-            const int p = e0 & 31;         // first value within the block
-            dq[k] = s16[ob >> 1];
-            // Q4_0: byte j holds value j (low nibble) and j + 16 (high);
-            // Q8_0: 32 signed bytes
-            const int q0 = (ob + 2 + (QT == 2 ? (p & 15) : p)) >> 1;
-#pragma unroll
-            for (int j = 0; j < 4; j++) w[k][j] = s16[q0 + j];
-        }
+        embed_load<QT, UPL>(s16, u0, lane, nu, dq, w);
 #pragma unroll
         for (int k = 0; k < UPL; k++) {
             const int u = u0 + lane + CUCA_WAVE * k;
-            const int p = (u * 8) & 31;
-            const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)dq[k]) * a.scale;
             float v[8];
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                if (QT == 2) {
-                    const int sh = p >= 16 ? 4 : 0;
-                    v[2 * j] = (float)((int)((w[k][j] >> sh) & 0xfu) - 8) * d;
-                    v[2 * j + 1] = (float)((int)((w[k][j] >> (8 + sh)) & 0xfu) - 8) * d;
-                } else {
-                    v[2 * j] = (float)(int8_t)(w[k][j] & 0xffu) * d;
-                    v[2 * j + 1] = (float)(int8_t)(w[k][j] >> 8) * d;
-                }
-            }
-            if (u < nu) {
-                if (CPU == 1) {
-                    Chunk<OutT>::store_nt(orow, u, reinterpret_cast<const float(&)[Chunk<OutT>::N]>(v));
-                } else {
-                    Chunk<OutT>::store_nt(orow, 2 * u, reinterpret_cast<const float(&)[Chunk<OutT>::N]>(v[0]));
-                    Chunk<OutT>::store_nt(orow, 2 * u + 1, reinterpret_cast<const float(&)[Chunk<OutT>::N]>(v[4]));
-                }
-            }
+            embed_dequant<QT>(u, dq[k], w[k], a.scale, v);
+            if (u < nu) embed_store<OutT>(orow, u, v);
         }
     }
 }
 
-#define CUCA_EMBED(NAME, QT, OUT, UPL)                                                     \
+// rms_norm_rows (quant.rs:324-339) after the gather, for the archs whose
+// looked-up rows get the scale-less norm (Hparams::norm_embeddings,
+// params.rs:374-379): sum = the f64 squares of the row's f32 values summed
+// in index order, inv = (f32)(1 / sqrt(sum / hidden + f64(eps))), x * inv.
+//
+// The wave sums the squares in its own order (per lane, then a butterfly).
+// Every square is exact in f64, so any order's sum is within
+// (hidden - 1) 2^-53 sum of the exact one, and the reference's sequential
+// sum too: the two differ by less than B = 2.02 hidden 2^-53 sum.  inv as a
+// function of the sum is monotone (every step is a correctly rounded
+// monotone operation), so when inv(sum + B) and inv(sum - B), each widened
+// by 2^-50 for the division and root, round to the same f32, that f32 is
+// the reference's inv.  Otherwise (about 2^-17 of the rows of 4096) lane 0
+// re-reads the row and sums in the reference's order.
+template <int QT>
+__device__ static inline float embed_norm_inv(const uint16_t *s16, double sum, int hidden, float scale,
+                                              float eps, int lane) {
+    const double n = (double)hidden, e = (double)eps;
+    const double b = sum * (2.02 * n * 0x1p-53);
+    const float lo = (float)((1.0 / __builtin_sqrt((sum + b) / n + e)) * (1.0 - 0x1p-50));
+    const float hi = (float)((1.0 / __builtin_sqrt((sum - b) / n + e)) * (1.0 + 0x1p-50));
+    if (lo == hi) return lo; // wave-uniform: every lane holds the same sum
+    double s = 0.0;
+    if (lane == 0) {
+        constexpr int BS = QT == 2 ? 18 : 34;
+        const uint8_t *row = reinterpret_cast<const uint8_t *>(s16);
+        for (int blk = 0; blk < hidden / 32; blk++) {
+            const uint8_t *p = row + blk * BS;
+            const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)(p[0] | (p[1] << 8))) * scale;
+            for (int j = 0; j < 32; j++) {
+                int q;
+                if (QT == 2) q = (int)((j < 16 ? p[2 + j] : p[2 + j - 16] >> 4) & 0xf) - 8;
+                else q = (int)(int8_t)p[2 + j];
+                const float x = (float)q * d;
+                s = s + (double)x * (double)x;
+            }
+        }
+    }
+    s = __shfl(s, 0, CUCA_WAVE);
+    return (float)(1.0 / __builtin_sqrt(s / n + e));
+}
+
+template <int QT, typename OutT, int UPL>
+__device__ static inline void embed_norm_body(const EmbedArgs &a) {
+    const int tok = blockIdx.x * (CUCA_BLOCK / CUCA_WAVE) + (int)(threadIdx.x / CUCA_WAVE);
+    const int lane = threadIdx.x & (CUCA_WAVE - 1);
+    if (tok >= a.n) return; // whole wave
+    const int nu = a.hidden / 8;
+    OutT *orow = reinterpret_cast<OutT *>(a.out) + (int64_t)tok * a.hidden;
+    const uint32_t id = a.ids[tok];
+    if ((int64_t)id >= a.vocab) {
+        embed_bad_id<OutT>(a, orow, tok, id, lane);
+        return;
+    }
+    const uint16_t *s16 = reinterpret_cast<const uint16_t *>(a.table + (int64_t)id * a.row_bytes);
+    // pass 1: the squares; a row of one round keeps its values in registers
+    const bool one_round = nu <= CUCA_WAVE * UPL;
+    float v[UPL][8];
+    double sum = 0.0;
+    for (int u0 = 0; u0 < nu; u0 += CUCA_WAVE * UPL) {
+        uint32_t dq[UPL], w[UPL][4];
+        embed_load<QT, UPL>(s16, u0, lane, nu, dq, w);
+#pragma unroll
+        for (int k = 0; k < UPL; k++) {
+            const int u = u0 + lane + CUCA_WAVE * k;
+            embed_dequant<QT>(u, dq[k], w[k], a.scale, v[k]);
+            if (u < nu) {
+#pragma unroll
+                for (int j = 0; j < 8; j++) sum += (double)v[k][j] * (double)v[k][j];
+            }
+        }
+    }
+#pragma unroll
+    for (int off = CUCA_WAVE / 2; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, CUCA_WAVE);
+    const float inv = embed_norm_inv<QT>(s16, sum, a.hidden, a.scale, a.norm_eps, lane);
+    // pass 2: x * inv, from registers or re-read (the row is in cache)
+    for (int u0 = 0; u0 < nu; u0 += CUCA_WAVE * UPL) {
+        if (!one_round) {
+            uint32_t dq[UPL], w[UPL][4];
+            embed_load<QT, UPL>(s16, u0, lane, nu, dq, w);
+#pragma unroll
+            for (int k = 0; k < UPL; k++) embed_dequant<QT>(u0 + lane + CUCA_WAVE * k, dq[k], w[k], a.scale, v[k]);
+        }
+#pragma unroll
+        for (int k = 0; k < UPL; k++) {
+            const int u = u0 + lane + CUCA_WAVE * k;
+            float y[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) y[j] = v[k][j] * inv;
+            if (u < nu) embed_store<OutT>(orow, u, y);
+        }
+    }
+}
+
+#define CUCA_EMBED(NAME, BODY, QT, OUT, UPL)                                               \
     extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void NAME(EmbedArgs a) {           \
-        embed_body<QT, OUT, UPL>(a);                                                       \
+        BODY<QT, OUT, UPL>(a);                                                             \
     }
 #define CUCA_EMBED_SET(NAME, QT, OUT)                                                      \
-    CUCA_EMBED(NAME##_u1, QT, OUT, 1)                                                      \
-    CUCA_EMBED(NAME##_u2, QT, OUT, 2)                                                      \
-    CUCA_EMBED(NAME##_u4, QT, OUT, 4)                                                      \
-    CUCA_EMBED(NAME##_u8, QT, OUT, 8)
+    CUCA_EMBED(NAME##_u1, embed_body, QT, OUT, 1)                                          \
+    CUCA_EMBED(NAME##_u2, embed_body, QT, OUT, 2)                                          \
+    CUCA_EMBED(NAME##_u4, embed_body, QT, OUT, 4)                                          \
+    CUCA_EMBED(NAME##_u8, embed_body, QT, OUT, 8)                                          \
+    CUCA_EMBED(NAME##_norm_u1, embed_norm_body, QT, OUT, 1)                                \
+    CUCA_EMBED(NAME##_norm_u2, embed_norm_body, QT, OUT, 2)                                \
+    CUCA_EMBED(NAME##_norm_u4, embed_norm_body, QT, OUT, 4)                                \
+    CUCA_EMBED(NAME##_norm_u8, embed_norm_body, QT, OUT, 8)
 
 CUCA_EMBED_SET(cuca_embed_q4_0_f32, 2, float)
 CUCA_EMBED_SET(cuca_embed_q4_0_f16, 2, _Float16)

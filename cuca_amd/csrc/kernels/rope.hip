@@ -213,6 +213,155 @@ __device__ static inline void rope_body(const RopeArgs &a) {
     }
 }
 
+// Full-width QK-norm (the qk_norm_full archs, OLMo 2: cpu.rs:2838-2843 for
+// Q, 3042-3045 for K; GPU gpu.rs:5233-5236): the norm runs over a row's
+// whole Q (and K) projection, weights [nq * head_dim] / [nk * head_dim],
+// before the heads are split and rotated.  One workgroup per row, its
+// threads taking the row's (head, lane) slots of the layout above, thread t
+// the slots t, t + blockDim, ... (RF_SLOTS at most).  blockDim is a power of
+// two of at least 64, so a head's TPH slots sit on consecutive lanes of one
+// wave (V's per-head norm stays a butterfly), and the Q and K sums are one
+// block reduction each, in a fixed order.  The chunks stay in registers
+// between the two passes; the tables and weights are read in the second.
+#define RF_SLOTS 4
+template <typename T, int KIND, bool STORE>
+__device__ static inline void rope_full_body(const RopeArgs &a) {
+    constexpr int VP = Chunk<T>::N;
+    constexpr int NC = KIND == 2 ? 2 : 1;       // chunks per lane
+    constexpr int NT = KIND == 2 ? VP : VP / 2; // cos/sin entries per lane
+    __shared__ float red[2][CUCA_WAVE];
+    const int tl = a.tph_log2;
+    const int tph = 1 << tl;
+    const uint32_t row = blockIdx.x;
+    const int nqk = a.nq + a.nk;
+    const int total = (nqk + (STORE ? a.nv : 0)) << tl;
+    const int D = a.head_dim, half = a.n_dims >> 1;
+    const int32_t pos = a.pos[row];
+    const int32_t slot = STORE ? a.slots[row] : 0;
+    const bool pos_ok = pos >= 0 && (int64_t)pos < a.table_rows;
+    const bool slot_ok = !STORE || (slot >= 0 && (int64_t)slot < a.n_slots);
+    if (!pos_ok || !slot_ok) { // uniform: the row is left untouched
+        if (threadIdx.x == 0) {
+            if (!pos_ok) record_bad(a.status + CUCA_STATUS_ROPE_POS, row, (uint32_t)pos);
+            if (!slot_ok) record_bad(a.status + CUCA_STATUS_KV_SLOT, row, (uint32_t)slot);
+        }
+        return;
+    }
+    // this thread's slots: head h, lane u, kind hk (0 Q, 1 K, 2 V), chunks e
+    auto head_src = [&](int h, int hk) -> const T * {
+        return hk == 0 ? reinterpret_cast<const T *>(a.q) + (int64_t)row * a.q_ld + (int64_t)h * D
+             : hk == 1 ? reinterpret_cast<const T *>(a.k) + (int64_t)row * a.k_ld + (int64_t)(h - a.nq) * D
+                       : reinterpret_cast<const T *>(a.v) + (int64_t)row * a.v_ld + (int64_t)(h - nqk) * D;
+    };
+    auto lane_chunks = [&](int u, int (&e)[NC]) -> bool { // returns: rotated
+        if (KIND == 2) {
+            const int nr = half / VP;
+            if (u < nr) { e[0] = u * VP; e[NC - 1] = e[0] + half; return true; }
+            e[0] = a.n_dims + (u - nr) * 2 * VP; e[NC - 1] = e[0] + VP; return false;
+        }
+        e[0] = u * VP;
+        return e[0] < a.n_dims;
+    };
+    u32x4 raw[RF_SLOTS][NC];
+    float vss[RF_SLOTS]; // V: the head's sum of squares
+    float ssq = 0.0f, ssk = 0.0f;
+#pragma unroll
+    for (int j = 0; j < RF_SLOTS; j++) {
+        const int sl = (int)threadIdx.x + j * (int)blockDim.x;
+        const bool live = sl < total;
+        const int h = live ? sl >> tl : 0, u = sl & (tph - 1);
+        const int hk = h < a.nq ? 0 : (h < nqk ? 1 : 2);
+        int e[NC];
+        (void)lane_chunks(u, e);
+        const T *src = head_src(h, hk);
+#pragma unroll
+        for (int k = 0; k < NC; k++) raw[j][k] = Chunk<T>::load_raw(src, e[k] / VP);
+        float part = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NC; k++) {
+            float v[VP];
+            Chunk<T>::widen(raw[j][k], v);
+#pragma unroll
+            for (int i = 0; i < VP; i++) part += v[i] * v[i];
+        }
+        if (live && hk == 0) ssq += part;
+        if (live && hk == 1) ssk += part;
+        vss[j] = group_sum_rt(live && hk == 2 ? part : 0.0f, tph);
+    }
+    // the Q and K sums: a wave butterfly, then the waves in order
+    ssq = group_sum<CUCA_WAVE>(ssq);
+    ssk = group_sum<CUCA_WAVE>(ssk);
+    const int wave = threadIdx.x / CUCA_WAVE, nw = blockDim.x / CUCA_WAVE;
+    if ((threadIdx.x & (CUCA_WAVE - 1)) == 0) {
+        red[0][wave] = ssq;
+        red[1][wave] = ssk;
+    }
+    __syncthreads();
+    float sq = 0.0f, sk = 0.0f;
+    for (int i = 0; i < nw; i++) {
+        sq += red[0][i];
+        sk += red[1][i];
+    }
+    // the norm kernel's reciprocal form, x * (1 / sqrt(mean + eps)) * w
+    const float invq = 1.0f / sqrtf(sq / (float)(a.nq * D) + a.eps);
+    const float invk = 1.0f / sqrtf(sk / (float)(a.nk > 0 ? a.nk * D : 1) + a.eps);
+#pragma unroll
+    for (int j = 0; j < RF_SLOTS; j++) {
+        const int sl = (int)threadIdx.x + j * (int)blockDim.x;
+        if (sl >= total) continue;
+        const int h = sl >> tl, u = sl & (tph - 1);
+        const int hk = h < a.nq ? 0 : (h < nqk ? 1 : 2);
+        int e[NC];
+        const bool rot = lane_chunks(u, e) && hk != 2;
+        const float *nw = hk == 0 ? a.q_norm_w : (hk == 1 ? a.k_norm_w : nullptr);
+        const int64_t wbase = hk == 0 ? (int64_t)h * D : (int64_t)(h - a.nq) * D;
+        const bool scale_h = hk == 2 ? a.v_norm != 0 : nw != nullptr;
+        const float inv = hk == 0 ? invq : hk == 1 ? invk : 1.0f / sqrtf(vss[j] / (float)D + a.eps);
+        float v[NC][VP];
+#pragma unroll
+        for (int k = 0; k < NC; k++) {
+            Chunk<T>::widen(raw[j][k], v[k]);
+            float w[VP];
+            if (nw) load_tab<VP>(nw, wbase + e[k], w);
+#pragma unroll
+            for (int i = 0; i < VP; i++) v[k][i] = scale_h ? v[k][i] * inv * (nw ? w[i] : 1.0f) : v[k][i];
+        }
+        if (rot) {
+            float c[NT], s[NT];
+            const int64_t t0 = (int64_t)pos * half + (KIND == 2 ? e[0] : (e[0] >> 1));
+            load_tab<NT>(a.cos_t, t0, c);
+            load_tab<NT>(a.sin_t, t0, s);
+            if (KIND == 2) {
+#pragma unroll
+                for (int i = 0; i < VP; i++) {
+                    const float x0 = v[0][i], x1 = v[NC - 1][i];
+                    v[0][i] = x0 * c[i] - x1 * s[i];
+                    v[NC - 1][i] = x0 * s[i] + x1 * c[i];
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < VP / 2; i++) {
+                    const float x0 = v[0][2 * i], x1 = v[0][2 * i + 1];
+                    v[0][2 * i] = x0 * c[i] - x1 * s[i];
+                    v[0][2 * i + 1] = x0 * s[i] + x1 * c[i];
+                }
+            }
+        }
+        T *dst;
+        if (STORE && hk != 0) {
+            const int kvh = hk == 1 ? h - a.nq : h - nqk;
+            const int64_t prow = ((int64_t)(slot >> 4) * a.nk + kvh) * 16 + (slot & 15);
+            dst = reinterpret_cast<T *>(hk == 1 ? a.pool_k : a.pool_v) + prow * D;
+        } else {
+            dst = const_cast<T *>(head_src(h, hk));
+        }
+        if (rot || scale_h || (STORE && hk != 0)) {
+#pragma unroll
+            for (int k = 0; k < NC; k++) Chunk<T>::store_nt(dst, e[k] / VP, v[k]);
+        }
+    }
+}
+
 template <typename T>
 __device__ static inline void rope_generic_body(const RopeArgs &a) {
     const int lane = threadIdx.x & (CUCA_WAVE - 1);
@@ -283,6 +432,11 @@ __device__ static inline void rope_generic_body(const RopeArgs &a) {
     extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void NAME(RopeArgs a) {            \
         rope_body<T, KIND, NORM, STORE>(a);                                                \
     }
+// full-width QK-norm: a workgroup of up to 1024 threads per row
+#define CUCA_ROPE_FULL(NAME, T, KIND, STORE)                                               \
+    extern "C" __global__ __launch_bounds__(1024) void NAME(RopeArgs a) {                  \
+        rope_full_body<T, KIND, STORE>(a);                                                 \
+    }
 // streaming variants of the QK-norm kernels (see the runtime's rope launch)
 #define CUCA_ROPE_NT(NAME, T, KIND, STORE)                                                 \
     extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void NAME(RopeArgs a) {            \
@@ -304,7 +458,11 @@ __device__ static inline void rope_generic_body(const RopeArgs &a) {
     extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void cuca_rope_##TN##_generic(     \
         RopeArgs a) {                                                                      \
         rope_generic_body<T>(a);                                                           \
-    }
+    }                                                                                      \
+    CUCA_ROPE_FULL(cuca_rope_##TN##_norm_full, T, 0, false)                                \
+    CUCA_ROPE_FULL(cuca_rope_##TN##_neox_full, T, 2, false)                                \
+    CUCA_ROPE_FULL(cuca_rope_##TN##_norm_full_kv, T, 0, true)                              \
+    CUCA_ROPE_FULL(cuca_rope_##TN##_neox_full_kv, T, 2, true)
 
 CUCA_ROPE_SET(f32, float)
 CUCA_ROPE_SET(f16, _Float16)

@@ -379,9 +379,9 @@ cuca_status cuca_hip_check_device(cuca_hip_ctx *ctx) {
 // embedding
 // ---------------------------------------------------------------------
 
-cuca_status cuca_hip_embed_gguf(cuca_hip_ctx *ctx, const void *table, uint32_t ggml_type,
-                                int64_t vocab, int64_t hidden, const uint32_t *ids, int64_t n,
-                                float scale, void *out, cuca_dtype out_dtype) {
+static cuca_status embed_common(cuca_hip_ctx *ctx, const void *table, uint32_t ggml_type, int64_t vocab,
+                                int64_t hidden, const uint32_t *ids, int64_t n, float scale, bool norm,
+                                float norm_eps, void *out, cuca_dtype out_dtype) {
     cuca_status st = use(ctx);
     if (st != CUCA_OK) return st;
     if (ggml_type != CUCA_GGML_Q4_0 && ggml_type != CUCA_GGML_Q8_0)
@@ -399,16 +399,25 @@ cuca_status cuca_hip_embed_gguf(cuca_hip_ctx *ctx, const void *table, uint32_t g
     const int64_t row_bytes = hidden / 32 * (ggml_type == CUCA_GGML_Q4_0 ? 18 : 34);
     if (hidden > (1 << 28)) return fail(ctx, CUCA_UNSUPPORTED, "hidden size %lld too large", (long long)hidden);
     if (reinterpret_cast<uintptr_t>(table) & 1u) return fail(ctx, CUCA_INVALID_ARG, "table must be 2-byte aligned");
+    if (norm && !(norm_eps >= 0.0f)) return fail(ctx, CUCA_INVALID_ARG, "embedding norm eps must be >= 0");
     const bool f16 = out_dtype == CUCA_F16;
     // a wave per token, lane units of 8 values, up to 8 units per lane per round
     const int64_t per_lane = (hidden / 8 + 63) / 64;
     const int ui = per_lane <= 1 ? 0 : per_lane <= 2 ? 1 : per_lane <= 4 ? 2 : 3;
-    static const Kernel table_k[2][2][4] = {
-        {{cuca_embed_q4_0_f32_u1, cuca_embed_q4_0_f32_u2, cuca_embed_q4_0_f32_u4, cuca_embed_q4_0_f32_u8},
-         {cuca_embed_q4_0_f16_u1, cuca_embed_q4_0_f16_u2, cuca_embed_q4_0_f16_u4, cuca_embed_q4_0_f16_u8}},
-        {{cuca_embed_q8_0_f32_u1, cuca_embed_q8_0_f32_u2, cuca_embed_q8_0_f32_u4, cuca_embed_q8_0_f32_u8},
-         {cuca_embed_q8_0_f16_u1, cuca_embed_q8_0_f16_u2, cuca_embed_q8_0_f16_u4, cuca_embed_q8_0_f16_u8}}};
-    const Kernel k = table_k[ggml_type == CUCA_GGML_Q8_0][f16][ui];
+    static const Kernel table_k[2][2][2][4] = {
+        {{{cuca_embed_q4_0_f32_u1, cuca_embed_q4_0_f32_u2, cuca_embed_q4_0_f32_u4, cuca_embed_q4_0_f32_u8},
+          {cuca_embed_q4_0_f16_u1, cuca_embed_q4_0_f16_u2, cuca_embed_q4_0_f16_u4, cuca_embed_q4_0_f16_u8}},
+         {{cuca_embed_q8_0_f32_u1, cuca_embed_q8_0_f32_u2, cuca_embed_q8_0_f32_u4, cuca_embed_q8_0_f32_u8},
+          {cuca_embed_q8_0_f16_u1, cuca_embed_q8_0_f16_u2, cuca_embed_q8_0_f16_u4, cuca_embed_q8_0_f16_u8}}},
+        {{{cuca_embed_q4_0_f32_norm_u1, cuca_embed_q4_0_f32_norm_u2, cuca_embed_q4_0_f32_norm_u4,
+           cuca_embed_q4_0_f32_norm_u8},
+          {cuca_embed_q4_0_f16_norm_u1, cuca_embed_q4_0_f16_norm_u2, cuca_embed_q4_0_f16_norm_u4,
+           cuca_embed_q4_0_f16_norm_u8}},
+         {{cuca_embed_q8_0_f32_norm_u1, cuca_embed_q8_0_f32_norm_u2, cuca_embed_q8_0_f32_norm_u4,
+           cuca_embed_q8_0_f32_norm_u8},
+          {cuca_embed_q8_0_f16_norm_u1, cuca_embed_q8_0_f16_norm_u2, cuca_embed_q8_0_f16_norm_u4,
+           cuca_embed_q8_0_f16_norm_u8}}}};
+    const Kernel k = table_k[norm][ggml_type == CUCA_GGML_Q8_0][f16][ui];
     EmbedArgs a{};
     a.table = static_cast<const uint8_t *>(table);
     a.ids = ids;
@@ -419,8 +428,21 @@ cuca_status cuca_hip_embed_gguf(cuca_hip_ctx *ctx, const void *table, uint32_t g
     a.hidden = (int32_t)hidden;
     a.n = (int32_t)n;
     a.scale = scale;
+    a.norm_eps = norm_eps;
     ctx->last_vocab = vocab;
     return launch(ctx, k, div_up(n, 4), 256, 0, a); // 4 waves, one token each
+}
+
+cuca_status cuca_hip_embed_gguf(cuca_hip_ctx *ctx, const void *table, uint32_t ggml_type,
+                                int64_t vocab, int64_t hidden, const uint32_t *ids, int64_t n,
+                                float scale, void *out, cuca_dtype out_dtype) {
+    return embed_common(ctx, table, ggml_type, vocab, hidden, ids, n, scale, false, 0.0f, out, out_dtype);
+}
+
+cuca_status cuca_hip_embed_gguf_norm(cuca_hip_ctx *ctx, const void *table, uint32_t ggml_type,
+                                     int64_t vocab, int64_t hidden, const uint32_t *ids, int64_t n,
+                                     float scale, float norm_eps, void *out, cuca_dtype out_dtype) {
+    return embed_common(ctx, table, ggml_type, vocab, hidden, ids, n, scale, true, norm_eps, out, out_dtype);
 }
 
 // ---------------------------------------------------------------------
@@ -636,7 +658,7 @@ static cuca_status rope_common(cuca_hip_ctx *ctx, void *q, int64_t q_ld, const v
                                const float *sin, int64_t table_rows, const int32_t *positions,
                                const float *q_norm_w, const float *k_norm_w, int32_t v_norm, float eps,
                                void *pool_k, void *pool_v, int64_t n_blocks, const int32_t *slots,
-                               cuca_dtype dtype) {
+                               cuca_dtype dtype, bool full = false) {
     cuca_status st = use(ctx);
     if (st != CUCA_OK) return st;
     const bool store = slots != nullptr;
@@ -712,6 +734,26 @@ static cuca_status rope_common(cuca_hip_ctx *ctx, void *q, int64_t q_ld, const v
                       (al16(v) && (v_ld * es) % 16 == 0 && al16(pool_k) && al16(pool_v)));
     const bool f16 = dtype == CUCA_F16, neox = kind == CUCA_ROPE_NEOX;
     const int64_t heads = rows * (nq + nk + nv);
+    if (full) {
+        // a workgroup per row over its (head, lane) slots, 4 per thread
+        if (!vec)
+            return fail(ctx, CUCA_UNSUPPORTED,
+                        "full-width QK-norm needs head_dim and n_dims in whole 16-byte chunks per lane "
+                        "and 16-byte aligned rows, tables and weights");
+        const int64_t total = (int64_t)(nq + nk + nv) * tph;
+        if (total > 4096)
+            return fail(ctx, CUCA_UNSUPPORTED, "full-width QK-norm: %lld head lanes per row, above 4096",
+                        (long long)total);
+        int lg = 0;
+        while ((1 << lg) < tph) lg++;
+        a.tph_log2 = lg;
+        unsigned block = 64;
+        while ((int64_t)block * 4 < total) block <<= 1;
+        static const Kernel table_f[2][2][2] = {
+            {{cuca_rope_f32_norm_full, cuca_rope_f32_norm_full_kv}, {cuca_rope_f32_neox_full, cuca_rope_f32_neox_full_kv}},
+            {{cuca_rope_f16_norm_full, cuca_rope_f16_norm_full_kv}, {cuca_rope_f16_neox_full, cuca_rope_f16_neox_full_kv}}};
+        return launch(ctx, table_f[f16][neox][store], (unsigned)rows, block, 0, a);
+    }
     if (!vec) {
         Kernel kk = f16 ? cuca_rope_f16_generic : cuca_rope_f32_generic;
         return launch(ctx, kk, div_up(heads, 4), 256, 0, a);
@@ -741,6 +783,28 @@ cuca_status cuca_hip_rope(cuca_hip_ctx *ctx, void *q, int64_t q_ld, void *k, int
                           const float *q_norm_w, const float *k_norm_w, float eps, cuca_dtype dtype) {
     return rope_common(ctx, q, q_ld, k, k_ld, nullptr, 0, rows, nq, nk, head_dim, n_dims, kind, cos, sin,
                        table_rows, positions, q_norm_w, k_norm_w, 0, eps, nullptr, nullptr, 0, nullptr, dtype);
+}
+
+cuca_status cuca_hip_rope_full(cuca_hip_ctx *ctx, void *q, int64_t q_ld, void *k, int64_t k_ld, int64_t rows,
+                               int32_t nq, int32_t nk, int32_t head_dim, int32_t n_dims, cuca_rope_kind kind,
+                               const float *cos, const float *sin, int64_t table_rows, const int32_t *positions,
+                               const float *q_norm_w, const float *k_norm_w, float eps, cuca_dtype dtype) {
+    return rope_common(ctx, q, q_ld, k, k_ld, nullptr, 0, rows, nq, nk, head_dim, n_dims, kind, cos, sin,
+                       table_rows, positions, q_norm_w, k_norm_w, 0, eps, nullptr, nullptr, 0, nullptr, dtype,
+                       true);
+}
+
+cuca_status cuca_hip_rope_store_kv_full(cuca_hip_ctx *ctx, void *q, int64_t q_ld, const void *k, int64_t k_ld,
+                                        const void *v, int64_t v_ld, int64_t rows, int32_t nq, int32_t nk,
+                                        int32_t head_dim, int32_t n_dims, cuca_rope_kind kind, const float *cos,
+                                        const float *sin, int64_t table_rows, const int32_t *positions,
+                                        const float *q_norm_w, const float *k_norm_w, int32_t v_norm, float eps,
+                                        void *pool_k, void *pool_v, int64_t n_blocks, const int32_t *slots,
+                                        cuca_dtype dtype) {
+    if (!slots) return fail(ctx, CUCA_INVALID_ARG, "null slots");
+    return rope_common(ctx, q, q_ld, k, k_ld, v, v_ld, rows, nq, nk, head_dim, n_dims, kind, cos, sin,
+                       table_rows, positions, q_norm_w, k_norm_w, v_norm, eps, pool_k, pool_v, n_blocks,
+                       slots, dtype, true);
 }
 
 cuca_status cuca_hip_rope_store_kv(cuca_hip_ctx *ctx, void *q, int64_t q_ld, const void *k, int64_t k_ld,

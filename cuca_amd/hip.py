@@ -58,6 +58,7 @@ SIGNATURES = {
     "cuca_hip_stream_sync": (_st, [_p]),
     "cuca_hip_check_device": (_st, [_p]),
     "cuca_hip_embed_gguf": (_st, [_p, _p, _u32, _i64, _i64, _p, _i64, _f32, _p, _st]),
+    "cuca_hip_embed_gguf_norm": (_st, [_p, _p, _u32, _i64, _i64, _p, _i64, _f32, _f32, _p, _st]),
     "cuca_hip_add_rmsnorm": (_st, [_p, _p, _p, _p, _p, _f32, _f32, _f32, _i64, _i64, _p, _p, _st]),
     "cuca_hip_glu": (_st, [_p, _p, _i64, _p, _i64, _i64, _i64, _st, _f32, _p, _i64, _st]),
     "cuca_hip_glu_ragged": (_st, [_p, _p, _i64, _p, _i64, _p, _i32, _i64, _i64, _st, _f32, _p,
@@ -67,6 +68,11 @@ SIGNATURES = {
     "cuca_hip_rope_store_kv": (_st, [_p, _p, _i64, _p, _i64, _p, _i64, _i64, _i32, _i32, _i32, _i32,
                                      _st, _p, _p, _i64, _p, _p, _p, _i32, _f32, _p, _p, _i64, _p,
                                      _st]),
+    "cuca_hip_rope_full": (_st, [_p, _p, _i64, _p, _i64, _i64, _i32, _i32, _i32, _i32, _st, _p, _p,
+                                 _i64, _p, _p, _p, _f32, _st]),
+    "cuca_hip_rope_store_kv_full": (_st, [_p, _p, _i64, _p, _i64, _p, _i64, _i64, _i32, _i32, _i32,
+                                          _i32, _st, _p, _p, _i64, _p, _p, _p, _i32, _f32, _p, _p,
+                                          _i64, _p, _st]),
     "cuca_hip_kv_slots": (_st, [_p, _i64, _i64, _i64, _i64, _p]),
     "cuca_hip_paged_decode_workspace": (_st, [_i64, _i32, _i32, _i64, ctypes.POINTER(_sz)]),
     "cuca_hip_paged_decode": (_st, [_p, _p, _i64, _p, _p, _i64, _p, _i64, _p, _i64, _i32, _i32,
@@ -308,6 +314,11 @@ class Context:
         self.check(self.L.cuca_hip_embed_gguf(self.ptr, table, ggml_type, vocab, hidden, ids, n,
                                               scale, out, out_dtype))
 
+    def embed_gguf_norm(self, table, ggml_type, vocab, hidden, ids, n, scale, norm_eps, out,
+                        out_dtype):
+        self.check(self.L.cuca_hip_embed_gguf_norm(self.ptr, table, ggml_type, vocab, hidden, ids,
+                                                   n, scale, norm_eps, out, out_dtype))
+
     def add_rmsnorm(self, x, branch, w, w_post, eps, post_eps, residual_scale, rows, hidden,
                     x_out, h_out, dtype):
         self.check(self.L.cuca_hip_add_rmsnorm(self.ptr, x, branch, w, w_post, eps, post_eps,
@@ -328,6 +339,20 @@ class Context:
         self.check(self.L.cuca_hip_rope(self.ptr, q, q_ld, k, k_ld, rows, nq, nk, head_dim, n_dims,
                                         kind, cos, sin, table_rows, positions, q_norm_w, k_norm_w,
                                         eps, dtype))
+
+    def rope_full(self, q, q_ld, k, k_ld, rows, nq, nk, head_dim, n_dims, kind, cos, sin, table_rows,
+                  positions, q_norm_w, k_norm_w, eps, dtype):
+        self.check(self.L.cuca_hip_rope_full(self.ptr, q, q_ld, k, k_ld, rows, nq, nk, head_dim, n_dims,
+                                             kind, cos, sin, table_rows, positions, q_norm_w, k_norm_w,
+                                             eps, dtype))
+
+    def rope_store_kv_full(self, q, q_ld, k, k_ld, v, v_ld, rows, nq, nk, head_dim, n_dims, kind, cos,
+                           sin, table_rows, positions, q_norm_w, k_norm_w, v_norm, eps, pool_k, pool_v,
+                           n_blocks, slots, dtype):
+        self.check(self.L.cuca_hip_rope_store_kv_full(self.ptr, q, q_ld, k, k_ld, v, v_ld, rows, nq, nk,
+                                                      head_dim, n_dims, kind, cos, sin, table_rows,
+                                                      positions, q_norm_w, k_norm_w, int(v_norm), eps,
+                                                      pool_k, pool_v, n_blocks, slots, dtype))
 
     def paged_decode(self, q, pool_k, pool_v, n_blocks, tables, max_blocks, ranges, rows, n_head,
                      n_kv, head_dim, scale, workspace, workspace_bytes, out, dtype, q_ld=None):

@@ -59,9 +59,12 @@ class TokenEmbedding:
         self.row_bytes = row_bytes
         self.table = ctx.array(data)
 
-    def rows(self, tokens, scale, out_dtype=np.float32):
+    def rows(self, tokens, scale, out_dtype=np.float32, norm_eps=None):
         """Embedding rows of `tokens`, concatenated and multiplied by `scale`
-        (quant.rs:391-411): a DeviceArray [len(tokens), row_len]."""
+        (quant.rs:391-411): a DeviceArray [len(tokens), row_len].  With
+        norm_eps (the archs with embd_norm), each row then gets
+        norm_embeddings' scale-less norm (params.rs:374-379) in the same
+        pass."""
         ids = np.asarray(tokens, dtype=np.int64).reshape(-1)
         for i in ids:  # quant.rs:395-400, before anything runs
             if i < 0 or i >= self.rows_n:
@@ -69,14 +72,18 @@ class TokenEmbedding:
                                 f"of {self.rows_n} rows")
         dev_ids = self.ctx.array(ids.astype(np.uint32))
         out = self.ctx.empty((ids.size, self.row_len), out_dtype)
-        self.rows_device(dev_ids, scale, out)
+        self.rows_device(dev_ids, scale, out, norm_eps)
         return out
 
-    def rows_device(self, ids, scale, out):
+    def rows_device(self, ids, scale, out, norm_eps=None):
         """The gather for ids already on the device (u32 DeviceArray); bad ids
         are reported by ctx.check_device()."""
-        self.ctx.embed_gguf(self.table.ptr, self.dtype, self.rows_n, self.row_len, ids.ptr,
-                            ids.size, scale, out.ptr, hip.dtype_code(out.dtype))
+        if norm_eps is None:
+            self.ctx.embed_gguf(self.table.ptr, self.dtype, self.rows_n, self.row_len, ids.ptr,
+                                ids.size, scale, out.ptr, hip.dtype_code(out.dtype))
+        else:
+            self.ctx.embed_gguf_norm(self.table.ptr, self.dtype, self.rows_n, self.row_len, ids.ptr,
+                                     ids.size, scale, norm_eps, out.ptr, hip.dtype_code(out.dtype))
         return out
 
 
@@ -172,15 +179,20 @@ def apply_rope(x, cos, sin, kind, n_dims, positions, norm_w=None, eps=1e-6):
     return x
 
 
-def rope_qk(q, k, cos, sin, kind, n_dims, positions, q_norm_w=None, k_norm_w=None, eps=1e-6):
-    """Q and K of one attention call in one launch, with the optional QK-norm."""
+def rope_qk(q, k, cos, sin, kind, n_dims, positions, q_norm_w=None, k_norm_w=None, eps=1e-6,
+            qk_norm_full=False):
+    """Q and K of one attention call in one launch, with the optional QK-norm:
+    per head (weights [head_dim]), or with qk_norm_full over each row's whole
+    Q and K projection (weights [nq * head_dim], [nk * head_dim]; the OLMo 2
+    path, cpu.rs:2838-2843, 3042-3045)."""
     rows, nq, d = q.shape
     nk = 0 if k is None else k.shape[1]
     ctx = q.ctx
     qw, kw = _w(ctx, q_norm_w), _w(ctx, k_norm_w)
-    ctx.rope(q.ptr, nq * d, None if k is None else k.ptr, nk * d, rows, nq, nk, d, n_dims, kind,
-             cos.ptr, sin.ptr, cos.shape[0], positions.ptr, None if qw is None else qw.ptr,
-             None if kw is None else kw.ptr, eps, hip.dtype_code(q.dtype))
+    call = ctx.rope_full if qk_norm_full else ctx.rope
+    call(q.ptr, nq * d, None if k is None else k.ptr, nk * d, rows, nq, nk, d, n_dims, kind,
+         cos.ptr, sin.ptr, cos.shape[0], positions.ptr, None if qw is None else qw.ptr,
+         None if kw is None else kw.ptr, eps, hip.dtype_code(q.dtype))
     return q, k
 
 
@@ -202,11 +214,12 @@ class KvPool:
         return hip.kv_slots(table, start, t, self.n_blocks)
 
     def store_kv(self, q, k, v, cos, sin, kind, n_dims, positions, slots, q_norm_w=None,
-                 k_norm_w=None, v_norm=False, eps=1e-6):
+                 k_norm_w=None, v_norm=False, eps=1e-6, qk_norm_full=False):
         """Normalise and rotate q [rows, nq, d] in place, and k [rows, nk, d]
         into the pool, with v (normalised without a weight when v_norm) beside
         it (store_kv, cpu.rs:3028-3097), in one launch.  slots: device int32
-        [rows] from `slots`."""
+        [rows] from `slots`.  qk_norm_full: the Q/K norms span each row's whole
+        projection (weights [nq * d], [nk * d])."""
         rows, nq, d = q.shape
         nk = k.shape[1]
         if k.shape != (rows, nk, d) or v.shape != (rows, nk, d) or nk != self.n_kv_head \
@@ -214,11 +227,12 @@ class KvPool:
             raise CucaError(hip.INVALID_ARG, "store_kv: row shape mismatch")
         ctx = q.ctx
         qw, kw = _w(ctx, q_norm_w), _w(ctx, k_norm_w)
-        ctx.rope_store_kv(q.ptr, nq * d, k.ptr, nk * d, v.ptr, nk * d, rows, nq, nk, d, n_dims, kind,
-                          cos.ptr, sin.ptr, cos.shape[0], positions.ptr,
-                          None if qw is None else qw.ptr, None if kw is None else kw.ptr, v_norm,
-                          eps, self.k.ptr, self.v.ptr, self.n_blocks, slots.ptr,
-                          hip.dtype_code(q.dtype))
+        call = ctx.rope_store_kv_full if qk_norm_full else ctx.rope_store_kv
+        call(q.ptr, nq * d, k.ptr, nk * d, v.ptr, nk * d, rows, nq, nk, d, n_dims, kind,
+             cos.ptr, sin.ptr, cos.shape[0], positions.ptr,
+             None if qw is None else qw.ptr, None if kw is None else kw.ptr, v_norm,
+             eps, self.k.ptr, self.v.ptr, self.n_blocks, slots.ptr,
+             hip.dtype_code(q.dtype))
         return q
 
     def decode(self, q, tables, ranges, n_head, scale, workspace=None):

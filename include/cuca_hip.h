@@ -8,6 +8,8 @@
  *   cuca_hip_embed_gguf    TokenEmbedding::rows           quant.rs:391-411
  *                          (GPU engine: RowTable::rows +  quant.rs:477-501,
  *                           upload in forward_stage)      gpu.rs:2976-2982, 4589-4598
+ *   cuca_hip_embed_gguf_   the same + norm_embeddings     params.rs:374-379,
+ *     norm                 (rms_norm_rows)                quant.rs:324-339
  *   cuca_hip_add_rmsnorm   rms / residual add in block    cpu.rs:2650-2711, 3652
  *                          GPU rms, attn_tail, ffn_half,  gpu.rs:5420-5483, 5883-5896
  *                          ffn_tail
@@ -18,6 +20,8 @@
  *   cuca_hip_rope          apply_rope / rotate_calls,     cpu.rs:2837-2871, 2996-3026,
  *                          with the per-head QK-norm      3040-3055, 3672-3688
  *                          GPU rope                       gpu.rs:5922-5964
+ *   cuca_hip_rope_full,    the same with the full-width   cpu.rs:2838-2843, 3042-3045,
+ *   _rope_store_kv_full    QK-norm (qk_norm_full)         gpu.rs:5233-5236
  *   cuca_hip_rope_tables   RopeSpec::tables (host)        rope.rs:118-151, mod.rs:460-472
  *   cuca_hip_rope_store_kv QK-norm + RoPE + the paged     cpu.rs:3028-3097,
  *                          K/V store of store_kv          cpu/paged_attn.rs:370-400
@@ -147,6 +151,21 @@ cuca_status cuca_hip_embed_gguf(cuca_hip_ctx *ctx, const void *table, uint32_t g
                                 int64_t vocab, int64_t hidden, const uint32_t *ids,
                                 int64_t n, float scale, void *out, cuca_dtype out_dtype);
 
+/* cuca_hip_embed_gguf followed by the scale-less norm of the archs with
+ * embd_norm (Hparams::norm_embeddings, params.rs:374-379 -> rms_norm_rows,
+ * quant.rs:324-339; run right after the gather in forward_stage,
+ * cpu.rs:1881-1882, gpu.rs:2976-2981), in the same pass over the row:
+ *   sum = f64 squares of the row's f32 values (after `scale`), index order
+ *   inv = (f32)(1 / sqrt(sum / hidden + f64(norm_eps)))
+ *   out[t, :] = row * inv (f32; f16 output rounds that once)
+ * Bit-exact with the reference: the device sums in its own order and
+ * proves from an error bound that the f32 inv is the sequential sum's, and
+ * re-sums in index order the rare row where it cannot. */
+cuca_status cuca_hip_embed_gguf_norm(cuca_hip_ctx *ctx, const void *table, uint32_t ggml_type,
+                                     int64_t vocab, int64_t hidden, const uint32_t *ids,
+                                     int64_t n, float scale, float norm_eps, void *out,
+                                     cuca_dtype out_dtype);
+
 /* Fused residual add + RMSNorm (Transformer::block, cpu.rs:2650-2711, with
  * rms = candle_nn::ops::rms_norm, cpu.rs:3652; GPU attn_tail / ffn_half /
  * ffn_tail, gpu.rs:5420-5483):
@@ -209,6 +228,23 @@ cuca_status cuca_hip_rope(cuca_hip_ctx *ctx, void *q, int64_t q_ld, void *k, int
                           const float *q_norm_w, const float *k_norm_w, float eps,
                           cuca_dtype dtype);
 
+/* cuca_hip_rope with the full-width QK-norm of the qk_norm_full archs
+ * (OLMo 2; cpu.rs:2838-2843 for Q, 3042-3045 for K; GPU gpu.rs:5233-5236):
+ * q_norm_w is f32 [nq * head_dim] and normalises a row's whole Q projection,
+ * k_norm_w [nk * head_dim] its whole K projection, before the heads are
+ * split and rotated:
+ *   q' = q / sqrt(mean over the nq * head_dim values + eps) * q_norm_w
+ * in f32, then the rotation as cuca_hip_rope (no rounding in between).
+ * Needs the vector layout (head_dim and n_dims in whole 16-byte chunks per
+ * lane, 16-byte aligned rows, tables and weights) and at most 4096 head
+ * lanes per row; CUCA_UNSUPPORTED otherwise. */
+cuca_status cuca_hip_rope_full(cuca_hip_ctx *ctx, void *q, int64_t q_ld, void *k, int64_t k_ld,
+                               int64_t rows, int32_t nq, int32_t nk, int32_t head_dim,
+                               int32_t n_dims, cuca_rope_kind kind, const float *cos,
+                               const float *sin, int64_t table_rows, const int32_t *positions,
+                               const float *q_norm_w, const float *k_norm_w, float eps,
+                               cuca_dtype dtype);
+
 /* Positions per paged K/V block (paged.rs:45, BLOCK_SIZE), and the block
  * table entry of a released block (paged.rs:49, NO_BLOCK). */
 #define CUCA_KV_BLOCK 16
@@ -237,6 +273,18 @@ cuca_status cuca_hip_rope_store_kv(cuca_hip_ctx *ctx, void *q, int64_t q_ld, con
                                    const float *q_norm_w, const float *k_norm_w, int32_t v_norm,
                                    float eps, void *pool_k, void *pool_v, int64_t n_blocks,
                                    const int32_t *slots, cuca_dtype dtype);
+
+/* cuca_hip_rope_store_kv with the full-width QK-norm of cuca_hip_rope_full
+ * (q_norm_w [nq * head_dim], k_norm_w [nk * head_dim]); V's weightless norm
+ * (v_norm) stays per head, as gpu.rs:5277 runs it. */
+cuca_status cuca_hip_rope_store_kv_full(cuca_hip_ctx *ctx, void *q, int64_t q_ld, const void *k,
+                                        int64_t k_ld, const void *v, int64_t v_ld, int64_t rows,
+                                        int32_t nq, int32_t nk, int32_t head_dim, int32_t n_dims,
+                                        cuca_rope_kind kind, const float *cos, const float *sin,
+                                        int64_t table_rows, const int32_t *positions,
+                                        const float *q_norm_w, const float *k_norm_w,
+                                        int32_t v_norm, float eps, void *pool_k, void *pool_v,
+                                        int64_t n_blocks, const int32_t *slots, cuca_dtype dtype);
 
 /* Host-side: the pool slots of cache indices start..start+t of a sequence
  * whose block table is table[table_len] (position p -> block table[p/16],

@@ -92,39 +92,82 @@ static inline void store_el(void *p, int64_t i, float v, int dtype) {
 
 typedef void (*range_fn)(void *ctx, int64_t begin, int64_t end);
 
-typedef struct {
+/* A persistent pool: worker threads are started once, on the first
+ * parallel call, and wait between calls (starting threads per call would
+ * dominate a CPU timing of these memory-bound loops).  One call runs at a
+ * time (the pool's lock is held for the whole call). */
+#define POOL_MAX 256
+static struct {
+    pthread_mutex_t call_lock, mu;
+    pthread_cond_t go, done;
+    int started;            /* workers running */
+    uint64_t generation;    /* bumped per call  */
+    int active;             /* workers in this call (1..started) */
+    int pending;            /* workers not finished yet */
     range_fn fn;
     void *ctx;
-    int64_t begin, end;
-} range_job;
+    int64_t n, per, extra;
+} g_pool = {PTHREAD_MUTEX_INITIALIZER, PTHREAD_MUTEX_INITIALIZER, PTHREAD_COND_INITIALIZER,
+            PTHREAD_COND_INITIALIZER, 0, 0, 0, 0, NULL, NULL, 0, 0, 0};
 
-static void *range_thread(void *arg) {
-    range_job *j = (range_job *)arg;
-    j->fn(j->ctx, j->begin, j->end);
+static void pool_chunk(int t, int64_t *b, int64_t *e) {
+    int64_t per = g_pool.per, extra = g_pool.extra;
+    *b = t * per + (t < extra ? t : extra);
+    *e = *b + per + (t < extra ? 1 : 0);
+}
+
+static void *pool_worker(void *arg) {
+    const int t = (int)(intptr_t)arg;  /* this worker runs chunk t (>= 1) */
+    uint64_t seen = 0;
+    pthread_mutex_lock(&g_pool.mu);
+    for (;;) {
+        while (g_pool.generation == seen) pthread_cond_wait(&g_pool.go, &g_pool.mu);
+        seen = g_pool.generation;
+        if (t >= g_pool.active) continue;
+        range_fn fn = g_pool.fn;
+        void *ctx = g_pool.ctx;
+        int64_t b, e;
+        pool_chunk(t, &b, &e);
+        pthread_mutex_unlock(&g_pool.mu);
+        if (b < e) fn(ctx, b, e);
+        pthread_mutex_lock(&g_pool.mu);
+        if (--g_pool.pending == 0) pthread_cond_signal(&g_pool.done);
+    }
     return NULL;
 }
 
+/* Split rows [0, n) into nthreads contiguous chunks; chunk 0 runs on the
+ * calling thread. */
 static void parallel_rows(int nthreads, int64_t n, range_fn fn, void *ctx) {
     if (nthreads <= 1 || n < 2) { fn(ctx, 0, n); return; }
     if (nthreads > n) nthreads = (int)n;
-    if (nthreads > 256) nthreads = 256;
-    pthread_t th[256];
-    range_job jobs[256];
-    int64_t per = n / nthreads, extra = n % nthreads, at = 0;
-    for (int t = 0; t < nthreads; t++) {
-        int64_t len = per + (t < extra ? 1 : 0);
-        jobs[t] = (range_job){fn, ctx, at, at + len};
-        at += len;
+    if (nthreads > POOL_MAX) nthreads = POOL_MAX;
+    pthread_mutex_lock(&g_pool.call_lock);
+    pthread_mutex_lock(&g_pool.mu);
+    while (g_pool.started < nthreads - 1) {
+        pthread_t th;
+        if (pthread_create(&th, NULL, pool_worker, (void *)(intptr_t)(g_pool.started + 1)) != 0) break;
+        pthread_detach(th);
+        g_pool.started++;
     }
-    int started = 0;
-    for (int t = 1; t < nthreads; t++) {
-        if (pthread_create(&th[t], NULL, range_thread, &jobs[t]) != 0) break;
-        started = t;
-    }
-    /* run job 0 here, and any job a thread could not be started for */
-    range_thread(&jobs[0]);
-    for (int t = started + 1; t < nthreads; t++) range_thread(&jobs[t]);
-    for (int t = 1; t <= started; t++) pthread_join(th[t], NULL);
+    const int active = g_pool.started + 1 < nthreads ? g_pool.started + 1 : nthreads;
+    g_pool.fn = fn;
+    g_pool.ctx = ctx;
+    g_pool.n = n;
+    g_pool.per = n / active;
+    g_pool.extra = n % active;
+    g_pool.active = active;
+    g_pool.pending = active - 1;
+    g_pool.generation++;
+    pthread_cond_broadcast(&g_pool.go);
+    int64_t b, e;
+    pool_chunk(0, &b, &e);
+    pthread_mutex_unlock(&g_pool.mu);
+    fn(ctx, b, e);
+    pthread_mutex_lock(&g_pool.mu);
+    while (g_pool.pending > 0) pthread_cond_wait(&g_pool.done, &g_pool.mu);
+    pthread_mutex_unlock(&g_pool.mu);
+    pthread_mutex_unlock(&g_pool.call_lock);
 }
 
 /* ------------------------------------------------------------------ */
@@ -165,12 +208,30 @@ int oracle_dequant_row(uint32_t ggml_type, const uint8_t *bytes, int64_t nbytes,
     return 0;
 }
 
+/* rms_norm_rows (quant.rs:324-339), the scale-less norm of
+ * Hparams::norm_embeddings (params.rs:374-379): per row, the squares of the
+ * f32 values are summed in f64 in index order from 0 (Iterator::sum),
+ * mean = sum / row_len, inv = (1 / sqrt(mean + f64(eps))) as f32, and every
+ * value is multiplied by inv in f32. */
+void oracle_rms_norm_rows(float *rows, int64_t n_rows, int64_t row_len, float eps) {
+    for (int64_t r = 0; r < n_rows; r++) {
+        float *row = rows + r * row_len;
+        double sum = 0.0;
+        for (int64_t i = 0; i < row_len; i++) sum += (double)row[i] * (double)row[i];
+        const double mean = sum / (double)row_len;
+        const float inv = (float)(1.0 / sqrt(mean + (double)eps));
+        for (int64_t i = 0; i < row_len; i++) row[i] *= inv;
+    }
+}
+
 typedef struct {
     const uint8_t *table;
     uint32_t type;
     int64_t hidden, row_bytes;
     const uint32_t *ids;
     float scale;
+    int norm;
+    float norm_eps;
     void *out;
     int dtype;
 } embed_ctx;
@@ -181,6 +242,7 @@ static void embed_range(void *c, int64_t begin, int64_t end) {
     for (int64_t t = begin; t < end; t++) {
         const uint8_t *src = e->table + (int64_t)e->ids[t] * e->row_bytes;
         oracle_dequant_row(e->type, src, e->row_bytes, e->scale, row, e->hidden);
+        if (e->norm) oracle_rms_norm_rows(row, 1, e->hidden, e->norm_eps);
         if (e->dtype == OR_F16) {
             oracle_f32_to_f16_n(row, (uint16_t *)e->out + t * e->hidden, e->hidden);
         } else {
@@ -193,9 +255,10 @@ static void embed_range(void *c, int64_t begin, int64_t end) {
 /* TokenEmbedding::rows (quant.rs:391-411): bounds-check every id first
  * (the reference returns before writing anything useful), then dequantize
  * each row times `scale`. */
-int oracle_embed(const uint8_t *table, uint32_t ggml_type, int64_t vocab,
-                 int64_t hidden, const uint32_t *ids, int64_t n_tok, float scale,
-                 void *out, int out_dtype, int nthreads, int64_t *bad_index) {
+int oracle_embed_norm(const uint8_t *table, uint32_t ggml_type, int64_t vocab,
+                      int64_t hidden, const uint32_t *ids, int64_t n_tok, float scale,
+                      int norm, float norm_eps, void *out, int out_dtype, int nthreads,
+                      int64_t *bad_index) {
     int64_t rb = oracle_row_bytes(ggml_type, hidden);
     if (rb < 0) return -1;
     for (int64_t t = 0; t < n_tok; t++) {
@@ -204,9 +267,16 @@ int oracle_embed(const uint8_t *table, uint32_t ggml_type, int64_t vocab,
             return -2;
         }
     }
-    embed_ctx c = {table, ggml_type, hidden, rb, ids, scale, out, out_dtype};
+    embed_ctx c = {table, ggml_type, hidden, rb, ids, scale, norm, norm_eps, out, out_dtype};
     parallel_rows(nthreads, n_tok, embed_range, &c);
     return 0;
+}
+
+int oracle_embed(const uint8_t *table, uint32_t ggml_type, int64_t vocab,
+                 int64_t hidden, const uint32_t *ids, int64_t n_tok, float scale,
+                 void *out, int out_dtype, int nthreads, int64_t *bad_index) {
+    return oracle_embed_norm(table, ggml_type, vocab, hidden, ids, n_tok, scale, 0, 0.0f, out,
+                             out_dtype, nthreads, bad_index);
 }
 
 /* ------------------------------------------------------------------ */
@@ -372,6 +442,7 @@ typedef struct {
     const float *norm_w;
     float eps;
     int dtype;
+    int full;   /* norm_w spans the whole row (heads * d): qk_norm_full */
 } rope_ctx;
 
 static void rope_range(void *c, int64_t begin, int64_t end) {
@@ -379,14 +450,27 @@ static void rope_range(void *c, int64_t begin, int64_t end) {
     int half = p->n_dims / 2;
     float *v = (float *)malloc(sizeof(float) * (size_t)p->d * 2);
     float *o = v + p->d;
+    float *rowv = p->full ? (float *)malloc(sizeof(float) * (size_t)p->d * (size_t)p->heads) : NULL;
     for (int64_t r = begin; r < end; r++) {
         const float *cs = p->cos_t + (int64_t)p->pos[r] * half;
         const float *sn = p->sin_t + (int64_t)p->pos[r] * half;
+        if (p->full) {
+            /* the full-width QK-norm: rms over the whole projection row with
+             * weights [heads * d], before the heads are split (cpu.rs:2838-2843,
+             * 3042-3045) */
+            int64_t w = (int64_t)p->heads * p->d;
+            for (int64_t i = 0; i < w; i++) rowv[i] = load_el(p->x, r * p->ld + i, p->dtype);
+            if (p->norm_w) rms_row(rowv, p->norm_w, p->eps, w, rowv);
+        }
         for (int h = 0; h < p->heads; h++) {
             int64_t at = r * p->ld + (int64_t)h * p->d;
-            for (int i = 0; i < p->d; i++) v[i] = load_el(p->x, at + i, p->dtype);
-            /* QK-norm per head: rms(q.reshape(1,t,nh,d), w[d]) (cpu.rs:2864) */
-            if (p->norm_w) rms_row(v, p->norm_w, p->eps, p->d, v);
+            if (p->full) {
+                memcpy(v, rowv + (int64_t)h * p->d, sizeof(float) * (size_t)p->d);
+            } else {
+                for (int i = 0; i < p->d; i++) v[i] = load_el(p->x, at + i, p->dtype);
+                /* QK-norm per head: rms(q.reshape(1,t,nh,d), w[d]) (cpu.rs:2864) */
+                if (p->norm_w) rms_row(v, p->norm_w, p->eps, p->d, v);
+            }
             memcpy(o, v, sizeof(float) * (size_t)p->d);
             /* candle rope / rope_i = rotate_reference (rope.rs:158-171) */
             for (int i = 0; i < half; i++) {
@@ -399,6 +483,7 @@ static void rope_range(void *c, int64_t begin, int64_t end) {
         }
     }
     free(v);
+    free(rowv);
 }
 
 void oracle_rope(void *x, int64_t ld, int64_t rows, int heads, int head_dim,
@@ -406,7 +491,16 @@ void oracle_rope(void *x, int64_t ld, int64_t rows, int heads, int head_dim,
                  const int32_t *positions, const float *norm_w, float eps,
                  int dtype, int nthreads) {
     rope_ctx c = {x, ld, heads, head_dim, n_dims, kind, cos_t, sin_t,
-                  positions, norm_w, eps, dtype};
+                  positions, norm_w, eps, dtype, 0};
+    parallel_rows(nthreads, rows, rope_range, &c);
+}
+
+void oracle_rope_full(void *x, int64_t ld, int64_t rows, int heads, int head_dim,
+                      int n_dims, int kind, const float *cos_t, const float *sin_t,
+                      const int32_t *positions, const float *norm_w, float eps,
+                      int dtype, int nthreads) {
+    rope_ctx c = {x, ld, heads, head_dim, n_dims, kind, cos_t, sin_t,
+                  positions, norm_w, eps, dtype, 1};
     parallel_rows(nthreads, rows, rope_range, &c);
 }
 

@@ -55,6 +55,22 @@ int oracle_embed(const uint8_t *table, uint32_t ggml_type, int64_t vocab,
                  int64_t hidden, const uint32_t *ids, int64_t n_tok, float scale,
                  void *out, int out_dtype, int nthreads, int64_t *bad_index);
 
+/* rms_norm_rows (quant.rs:324-339), applied by Hparams::norm_embeddings
+ * (params.rs:374-379) to the looked-up rows of archs with embd_norm
+ * (arch.rs:229-231): per row of row_len f32 values, in place,
+ *   sum  = sum of f64(x) * f64(x), in index order, from 0
+ *   inv  = (f32)(1 / sqrt(sum / row_len + f64(eps)))
+ *   x    = x * inv (f32). */
+void oracle_rms_norm_rows(float *rows, int64_t n_rows, int64_t row_len, float eps);
+
+/* oracle_embed, then (norm != 0) rms_norm_rows on each f32 row before the
+ * output rounding (forward_stage: rows(tokens, embd_scale) then
+ * norm_embeddings, cpu.rs:1881-1882, gpu.rs:2976-2981). */
+int oracle_embed_norm(const uint8_t *table, uint32_t ggml_type, int64_t vocab,
+                      int64_t hidden, const uint32_t *ids, int64_t n_tok, float scale,
+                      int norm, float norm_eps, void *out, int out_dtype, int nthreads,
+                      int64_t *bad_index);
+
 /* Fused residual add + RMSNorm, restating Transformer::block
  * (cpu.rs:2650-2711) with candle's rms_norm (cpu.rs:3652):
  *   b'  = w_post ? rms(branch, w_post, post_eps) : branch
@@ -97,6 +113,16 @@ void oracle_rope(void *x, int64_t ld, int64_t rows, int heads, int head_dim,
                  int n_dims, int kind, const float *cos_t, const float *sin_t,
                  const int32_t *positions, const float *norm_w, float eps,
                  int dtype, int nthreads);
+
+/* oracle_rope with the full-width QK-norm of the qk_norm_full archs (OLMo 2,
+ * cpu.rs:2838-2843 for Q, 3042-3045 for K): rms over each row's whole
+ * heads * head_dim projection with norm_w [heads * head_dim] (f32, as
+ * rms_row), then every head rotated from those f32 values, one rounding on
+ * output. */
+void oracle_rope_full(void *x, int64_t ld, int64_t rows, int heads, int head_dim,
+                      int n_dims, int kind, const float *cos_t, const float *sin_t,
+                      const int32_t *positions, const float *norm_w, float eps,
+                      int dtype, int nthreads);
 
 /* Paged K/V pools (cpu/paged_attn.rs:1-38): [n_blocks][n_kv][16][d]
  * elements of `dtype` (1 = f16, else f32); position p of a sequence is row

@@ -50,6 +50,10 @@ def lib():
         L.oracle_embed.restype = _int
         L.oracle_embed.argtypes = [_p, ctypes.c_uint32, _i64, _i64, _p, _i64, _f32,
                                    _p, _int, _int, ctypes.POINTER(_i64)]
+        L.oracle_embed_norm.restype = _int
+        L.oracle_embed_norm.argtypes = [_p, ctypes.c_uint32, _i64, _i64, _p, _i64, _f32, _int,
+                                        _f32, _p, _int, _int, ctypes.POINTER(_i64)]
+        L.oracle_rms_norm_rows.argtypes = [_p, _i64, _i64, _f32]
         L.oracle_add_rmsnorm.argtypes = [_p, _p, _p, _p, _f32, _f32, _f32, _i64, _i64,
                                          _p, _p, _int, _int]
         L.oracle_glu.argtypes = [_p, _i64, _p, _i64, _i64, _i64, _int, _f32, _p, _i64,
@@ -58,6 +62,7 @@ def lib():
                                          _p, _i64, _p, _p]
         L.oracle_rope.argtypes = [_p, _i64, _i64, _int, _int, _int, _int, _p, _p, _p, _p,
                                   _f32, _int, _int]
+        L.oracle_rope_full.argtypes = L.oracle_rope.argtypes
         L.oracle_store_rows.restype = _int
         L.oracle_store_rows.argtypes = [_p, _i64, _i64, _i64, _p, _p, _i64, _int, _int, _int]
         L.oracle_paged_attention.restype = _int
@@ -127,13 +132,25 @@ class OracleError(ValueError):
     pass
 
 
-def embed(table, ggml_type, vocab, hidden, ids, scale, out_dtype=np.float32, threads=1):
+def rms_norm_rows(rows, eps):
+    """rms_norm_rows (quant.rs:324-339) on a copy of f32 rows [n, row_len]."""
+    r = np.array(rows, dtype=np.float32, copy=True, order="C")
+    lib().oracle_rms_norm_rows(_ptr(r), r.shape[0], r.shape[1], eps)
+    return r
+
+
+def embed(table, ggml_type, vocab, hidden, ids, scale, out_dtype=np.float32, threads=1,
+          norm_eps=None):
+    """TokenEmbedding::rows; norm_eps given: then norm_embeddings'
+    rms_norm_rows with that eps (the embd_norm archs)."""
     table = np.ascontiguousarray(table, dtype=np.uint8)
     ids = np.ascontiguousarray(ids, dtype=np.uint32)
     out = np.empty((ids.size, hidden), out_dtype)
     bad = _i64(-1)
-    rc = lib().oracle_embed(_ptr(table), ggml_type, vocab, hidden, _ptr(ids), ids.size,
-                            scale, _ptr(out), _dtype_code(out), threads, ctypes.byref(bad))
+    norm = norm_eps is not None
+    rc = lib().oracle_embed_norm(_ptr(table), ggml_type, vocab, hidden, _ptr(ids), ids.size,
+                                 scale, 1 if norm else 0, norm_eps if norm else 0.0, _ptr(out),
+                                 _dtype_code(out), threads, ctypes.byref(bad))
     if rc == -1:
         raise OracleError(f"row length {hidden} is not a whole number of blocks")
     if rc == -2:
@@ -185,8 +202,11 @@ def rope_tables(n_dims, base, positions, freq_scale=1.0, yarn=None, attn_factor=
     return cos, sin
 
 
-def rope(x, cos, sin, positions, kind, n_dims=None, norm_w=None, eps=1e-6, threads=1):
-    """Rotate a copy of x [rows, heads, d] (returned); optional fused QK-norm."""
+def rope(x, cos, sin, positions, kind, n_dims=None, norm_w=None, eps=1e-6, threads=1,
+         full=False):
+    """Rotate a copy of x [rows, heads, d] (returned); optional fused QK-norm,
+    per head (norm_w [d]) or, with full, over the row's whole projection
+    (norm_w [heads * d], the qk_norm_full archs)."""
     x = np.array(x, copy=True, order="C")
     rows, heads, d = x.shape
     n_dims = d if n_dims is None else n_dims
@@ -194,8 +214,9 @@ def rope(x, cos, sin, positions, kind, n_dims=None, norm_w=None, eps=1e-6, threa
     sin = np.ascontiguousarray(sin, dtype=np.float32)
     pos = np.ascontiguousarray(positions, dtype=np.int32)
     nw = None if norm_w is None else np.ascontiguousarray(norm_w, dtype=np.float32)
-    lib().oracle_rope(_ptr(x), heads * d, rows, heads, d, n_dims, kind, _ptr(cos),
-                      _ptr(sin), _ptr(pos), _ptr(nw), eps, _dtype_code(x), threads)
+    fn = lib().oracle_rope_full if full else lib().oracle_rope
+    fn(_ptr(x), heads * d, rows, heads, d, n_dims, kind, _ptr(cos), _ptr(sin), _ptr(pos),
+       _ptr(nw), eps, _dtype_code(x), threads)
     return x
 
 
@@ -237,20 +258,21 @@ def gather(table, lo, hi, pool):
 
 
 def store_kv(q, k, v, cos, sin, kind, n_dims, calls, pool_k, pool_v, q_norm_w=None,
-             k_norm_w=None, v_norm=False, eps=1e-6, threads=1):
+             k_norm_w=None, v_norm=False, eps=1e-6, threads=1, full=False):
     """store_kv (cpu.rs:3028-3097) for the rows of several calls: q, k, v
     [rows, heads, d]; calls = [(offset, start, rope_start, t, table)], the
     call's rows offset.. at cache indices start.. and RoPE positions
     rope_start.. (AttnCall, cpu.rs:1314-1325).  Q and K are normalised
     (per head) and rotated, V normalised without a weight when v_norm
     (gpu.rs:5277), K and V stored into the pools (modified in place).
-    Returns the rotated Q."""
+    With full, the Q and K norms span each row's whole projection
+    (qk_norm_full, cpu.rs:2838-2843, 3042-3045).  Returns the rotated Q."""
     rows, nk, d = k.shape
     pos = np.zeros(rows, np.int32)
     for off, start, rope_start, t, table in calls:
         pos[off:off + t] = np.arange(rope_start, rope_start + t)
-    qr = rope(q, cos, sin, pos, kind, n_dims, norm_w=q_norm_w, eps=eps, threads=threads)
-    kr = rope(k, cos, sin, pos, kind, n_dims, norm_w=k_norm_w, eps=eps, threads=threads)
+    qr = rope(q, cos, sin, pos, kind, n_dims, norm_w=q_norm_w, eps=eps, threads=threads, full=full)
+    kr = rope(k, cos, sin, pos, kind, n_dims, norm_w=k_norm_w, eps=eps, threads=threads, full=full)
     vv = np.ascontiguousarray(v)
     if v_norm:
         _, h = add_rmsnorm(vv.reshape(rows * nk, d), None, None, eps, threads=threads, write_x=False)

@@ -124,3 +124,85 @@ def test_full_size_config_c_sampled_rows(ctx):
     want = O.embed(sub_table, O.Q8_0, sample.size, hidden, np.arange(sample.size, dtype=np.uint32),
                    1.0, out_dtype=np.float16)
     assert_bits_equal(got, want, "config C full-size sample")
+
+
+# ---------------------------------------------------------------------------
+# the gather fused with norm_embeddings' rms_norm_rows (params.rs:374-379,
+# quant.rs:324-339): bit-exact with the oracle's sequential f64 sum
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("qname", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("out", [np.float32, np.float16])
+@pytest.mark.parametrize("hidden,eps,scale", [
+    (1024, 1e-6, 1.0), (2048, 1e-6, 1.0), (3584, 1e-6, float(np.float32(np.sqrt(3584.0)))),
+    (4096, 1e-5, 1.0), (5120, 1e-5, 1.0), (8192, 1e-6, 0.5), (32, 1e-5, 1.0), (96, 0.0, 2.0)])
+def test_embed_norm_bit_exact(ctx, qname, out, hidden, eps, scale):
+    rng = np.random.default_rng(hidden + (qname == "q8_0"))
+    vocab = 512
+    table = W.quant_table(rng, vocab, hidden, qname, (0.001, 0.05))
+    ty = W.GGML_ID[qname]
+    ids = rng.integers(0, vocab, 67).astype(np.uint32)
+    emb = ops.TokenEmbedding(ctx, ty, table, vocab, hidden)
+    got = emb.rows(ids, scale, out_dtype=out, norm_eps=eps).numpy()
+    ctx.check_device()
+    want = O.embed(table, ty, vocab, hidden, ids, scale, out_dtype=out, norm_eps=eps)
+    assert_bits_equal(got, want, f"embed+norm {qname} {hidden}")
+
+
+def test_embed_norm_fallback_row_bit_exact(ctx):
+    """A row built so that the device's error bound cannot decide the f32
+    scale (tests/test_oracle_embed_norm.py checks that on the CPU): the
+    kernel re-sums it in index order and must still give the oracle's bits,
+    alone and among ordinary rows."""
+    from test_oracle_embed_norm import fallback_case
+    row, eps = fallback_case()
+    rng = np.random.default_rng(3)
+    others = W.quant_table(rng, 7, 4096, "q8_0", (0.001, 0.02))
+    table = np.concatenate([others, row])
+    emb = ops.TokenEmbedding(ctx, hip.GGML_Q8_0, table, 8, 4096)
+    ids = np.array([7, 0, 7, 3, 6, 7], np.uint32)
+    for out in (np.float32, np.float16):
+        got = emb.rows(ids, 1.0, out_dtype=out, norm_eps=eps).numpy()
+        ctx.check_device()
+        want = O.embed(table, O.Q8_0, 8, 4096, ids, 1.0, out_dtype=out, norm_eps=eps)
+        assert_bits_equal(got, want, "fallback row")
+
+
+def test_embed_norm_bad_id_zero_row(ctx):
+    rng = np.random.default_rng(4)
+    table = W.quant_table(rng, 16, 256, "q4_0", (0.001, 0.05))
+    emb = ops.TokenEmbedding(ctx, hip.GGML_Q4_0, table, 16, 256)
+    ids = ctx.array(np.array([3, 16, 5], np.uint32))
+    out = ctx.empty((3, 256), np.float32)
+    emb.rows_device(ids, 1.0, out, norm_eps=1e-6)
+    with pytest.raises(hip.CucaError, match="token id 16 outside the embedding table of 16 rows"):
+        ctx.check_device()
+    got = out.numpy()
+    assert np.all(got[1] == 0)
+    want = O.embed(table, O.Q4_0, 16, 256, np.array([3, 5], np.uint32), 1.0, norm_eps=1e-6)
+    assert_bits_equal(got[[0, 2]], want)
+    with pytest.raises(hip.CucaError, match="eps"):
+        emb.rows_device(ids, 1.0, out, norm_eps=-1.0)
+
+
+def test_embed_norm_full_table_sampled_rows(ctx):
+    """A 151936 x 2048 Q4_0 table (config E's shape) and 8192 ids gathered
+    with the norm, checked on sampled rows."""
+    torch = pytest.importorskip("torch")
+    cfg = W.CONFIGS["E"]
+    gen = torch.Generator(device="cuda").manual_seed(9)
+    table = W.quant_table_torch(gen, cfg["vocab"], cfg["hidden"], "q4_0", cfg["d_range"])
+    ids = torch.randint(0, cfg["vocab"], (8192,), device="cuda", generator=gen, dtype=torch.int32)
+    out = torch.empty((8192, cfg["hidden"]), device="cuda", dtype=torch.float16)
+    torch.cuda.synchronize()
+    ctx.embed_gguf_norm(table.data_ptr(), hip.GGML_Q4_0, cfg["vocab"], cfg["hidden"], ids.data_ptr(),
+                        8192, 1.0, 1e-6, out.data_ptr(), hip.F16)
+    ctx.sync()
+    ctx.check_device()
+    s = np.unique(np.concatenate([[0, 8191], np.random.default_rng(10).integers(0, 8192, 62)]))
+    st = torch.from_numpy(s).cuda()
+    rb = 18 * cfg["hidden"] // 32
+    sub = table.view(cfg["vocab"], rb)[ids[st].long()].cpu().numpy().reshape(-1)
+    want = O.embed(sub, O.Q4_0, s.size, cfg["hidden"], np.arange(s.size, dtype=np.uint32), 1.0,
+                   out_dtype=np.float16, norm_eps=1e-6)
+    assert_bits_equal(out[st].cpu().numpy(), want, "full table + norm")

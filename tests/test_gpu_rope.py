@@ -156,3 +156,65 @@ def test_full_size_config_c_sampled_rows(ctx):
     wk = O.rope(k0[st].cpu().numpy(), cos, sin, s.astype(np.int32), hip.ROPE_NORM)
     assert_bits_equal(q[st].cpu().numpy(), wq)
     assert_bits_equal(k[st].cpu().numpy(), wk)
+
+
+# ---------------------------------------------------------------------------
+# full-width QK-norm (qk_norm_full: OLMo 2 / OLMoE, cpu.rs:2838-2843, 3042-3045)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+@pytest.mark.parametrize("nq,nk,d,kind,n_dims,rows", [
+    (32, 32, 128, hip.ROPE_NEOX, 128, 33),     # OLMo-2-7B
+    (16, 16, 128, hip.ROPE_NEOX, 128, 200),    # OLMoE-1B-7B
+    (32, 8, 128, hip.ROPE_NORM, 128, 5),       # GQA, interleaved
+    (8, 2, 64, hip.ROPE_NEOX, 32, 17),         # partial rotary
+    (40, 8, 128, hip.ROPE_NEOX, 128, 1)])      # decode row
+def test_full_width_qk_norm(ctx, dtype, nq, nk, d, kind, n_dims, rows):
+    rng = np.random.default_rng(nq + nk + d + rows)
+    q = (rng.standard_normal((rows, nq, d)) * rng.uniform(0.5, 3, (1, nq, 1))).astype(NP[dtype])
+    k = rng.standard_normal((rows, nk, d)).astype(NP[dtype])
+    qw = (1 + 0.02 * rng.standard_normal(nq * d)).astype(np.float32)
+    kw = (1 + 0.02 * rng.standard_normal(nk * d)).astype(np.float32)
+    cos, sin = hip.rope_tables(kind, n_dims, 5e5, 4096)
+    pos = rng.integers(0, 4096, rows).astype(np.int32)
+    dq, dk = ctx.array(q), ctx.array(k)
+    ops.rope_qk(dq, dk, ctx.array(cos), ctx.array(sin), kind, n_dims, ctx.array(pos), q_norm_w=qw,
+                k_norm_w=kw, eps=1e-6, qk_norm_full=True)
+    ctx.check_device()
+    wq = O.rope(q, cos, sin, pos, kind, n_dims, norm_w=qw, eps=1e-6, full=True)
+    wk = O.rope(k, cos, sin, pos, kind, n_dims, norm_w=kw, eps=1e-6, full=True)
+    assert_close(dq.numpy(), wq, floor=pair_floor(wq, kind, n_dims), what="full-norm q")
+    assert_close(dk.numpy(), wk, floor=pair_floor(wk, kind, n_dims), what="full-norm k")
+    # only Q normalised (no K weights): K is rotated, not normalised
+    dq, dk = ctx.array(q), ctx.array(k)
+    ops.rope_qk(dq, dk, ctx.array(cos), ctx.array(sin), kind, n_dims, ctx.array(pos), q_norm_w=qw,
+                eps=1e-6, qk_norm_full=True)
+    assert_bits_equal(dk.numpy(), O.rope(k, cos, sin, pos, kind, n_dims), "unnormed k")
+
+
+def test_full_width_qk_norm_inside_a_fused_qkv_row_and_bad_shapes(ctx):
+    rng = np.random.default_rng(40)
+    n, nq, nk, d = 9, 16, 16, 128
+    qkv = rng.standard_normal((n, (nq + 2 * nk) * d)).astype(np.float32)
+    qw = (1 + 0.02 * rng.standard_normal(nq * d)).astype(np.float32)
+    kw = (1 + 0.02 * rng.standard_normal(nk * d)).astype(np.float32)
+    pos = np.arange(n, dtype=np.int32)
+    cos, sin = hip.rope_tables(hip.ROPE_NEOX, d, 1e4, 16)
+    buf, dcos, dsin, dpos = ctx.array(qkv), ctx.array(cos), ctx.array(sin), ctx.array(pos)
+    dqw, dkw = ctx.array(qw), ctx.array(kw)
+    ld = (nq + 2 * nk) * d
+    ctx.rope_full(buf.ptr, ld, buf.ptr + nq * d * 4, ld, n, nq, nk, d, d, hip.ROPE_NEOX, dcos.ptr, dsin.ptr,
+                  16, dpos.ptr, dqw.ptr, dkw.ptr, 1e-6, hip.F32)
+    got = buf.numpy()
+    wq = O.rope(qkv[:, :nq * d].reshape(n, nq, d), cos, sin, pos, hip.ROPE_NEOX, norm_w=qw, full=True)
+    wk = O.rope(qkv[:, nq * d:(nq + nk) * d].reshape(n, nk, d), cos, sin, pos, hip.ROPE_NEOX, norm_w=kw,
+                full=True)
+    assert_close(got[:, :nq * d].reshape(n, nq, d), wq, floor=pair_floor(wq, hip.ROPE_NEOX, d))
+    assert_close(got[:, nq * d:(nq + nk) * d].reshape(n, nk, d), wk, floor=pair_floor(wk, hip.ROPE_NEOX, d))
+    assert_bits_equal(got[:, (nq + nk) * d:], qkv[:, (nq + nk) * d:])   # V untouched
+    with pytest.raises(hip.CucaError, match="full-width QK-norm needs"):
+        q80 = ctx.array(np.zeros((2, 2, 80), np.float32))
+        c80, s80 = hip.rope_tables(hip.ROPE_NEOX, 80, 1e4, 4)
+        ops.rope_qk(q80, None, ctx.array(c80), ctx.array(s80), hip.ROPE_NEOX, 80,
+                    ctx.array(np.zeros(2, np.int32)), q_norm_w=np.ones(160, np.float32),
+                    qk_norm_full=True)

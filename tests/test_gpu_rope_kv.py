@@ -248,3 +248,35 @@ def test_full_size_config_c_sampled_rows(ctx):
     b, r = torch.from_numpy(slots[s] // 16).cuda(), torch.from_numpy(slots[s] % 16).cuda()
     assert_bits_equal(pk[b, :, r].cpu().numpy(), wk, "pool k")
     assert_bits_equal(pv[b, :, r].cpu().numpy(), v[st].cpu().numpy(), "pool v")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+@pytest.mark.parametrize("nq,nk,d,lengths", [(32, 32, 128, [17, 40]), (16, 16, 128, [1, 1, 1]),
+                                             (32, 8, 128, [64])])
+def test_full_width_qk_norm_store(ctx, dtype, nq, nk, d, lengths):
+    """The K/V store with the full-width QK-norm (OLMo 2 / OLMoE, qk_norm_full,
+    cpu.rs:2838-2843, 3042-3045): Q and the pool's K within the normed-RoPE
+    bar of the oracle's store_kv(full=True); V's weightless per-head norm
+    within 1e-5 / 2 f16 ulps."""
+    rng = np.random.default_rng(nq + nk + sum(lengths))
+    n_blocks = 32
+    calls, slots, pos = make_calls(rng, lengths, n_blocks)
+    n = sum(lengths)
+    q = rng.standard_normal((n, nq, d)).astype(NP[dtype])
+    k = (rng.standard_normal((n, nk, d)) * rng.uniform(0.5, 2, (1, nk, 1))).astype(NP[dtype])
+    v = rng.standard_normal((n, nk, d)).astype(NP[dtype])
+    qw = (1 + 0.02 * rng.standard_normal(nq * d)).astype(np.float32)
+    kw = (1 + 0.02 * rng.standard_normal(nk * d)).astype(np.float32)
+    cos, sin = hip.rope_tables(hip.ROPE_NEOX, d, 5e5, int(pos.max()) + 1)
+    pool = ops.KvPool(ctx, n_blocks, nk, d, NP[dtype])
+    dq, dk, dv = ctx.array(q), ctx.array(k), ctx.array(v)
+    pool.store_kv(dq, dk, dv, ctx.array(cos), ctx.array(sin), hip.ROPE_NEOX, d, ctx.array(pos),
+                  ctx.array(slots), q_norm_w=qw, k_norm_w=kw, v_norm=True, eps=1e-6, qk_norm_full=True)
+    ctx.check_device()
+    pk = np.zeros((n_blocks, nk, 16, d), NP[dtype])
+    pv = np.zeros_like(pk)
+    wq = O.store_kv(q, k, v, cos, sin, hip.ROPE_NEOX, d, calls, pk, pv, q_norm_w=qw, k_norm_w=kw,
+                    v_norm=True, eps=1e-6, full=True)
+    assert_close(dq.numpy(), wq, floor=pair_floor(wq, hip.ROPE_NEOX, d), what="full-norm q")
+    assert_close(pool.k.numpy(), pk, floor=pair_floor(pk, hip.ROPE_NEOX, d), what="full-norm pool k")
+    assert_close(pool.v.numpy(), pv, what="pool v")

@@ -135,3 +135,46 @@ def test_qk_norm_then_rotation():
     c, s = cos[pos][:, None, :].astype(np.float64), sin[pos][:, None, :].astype(np.float64)
     want = np.concatenate([a * c - b * s, a * s + b * c], -1)
     assert np.max(np.abs(got - want)) < 1e-5
+
+
+# ---------------------------------------------------------------------------
+# the full-width QK-norm of the qk_norm_full archs (OLMo 2, OLMoE: cpu.rs:2838-2843
+# for Q, 3042-3045 for K): rms over the whole projection row, then the rotation
+# ---------------------------------------------------------------------------
+
+def test_full_width_norm_is_the_row_norm_then_the_rotation():
+    rng = np.random.default_rng(31)
+    rows, heads, d = 7, 6, 32
+    x = rng.standard_normal((rows, heads, d)).astype(np.float32)
+    w = (1 + 0.02 * rng.standard_normal(heads * d)).astype(np.float32)
+    cos, sin = O.rope_tables(d, 1e4, 16)
+    pos = rng.integers(0, 16, rows).astype(np.int32)
+    got = O.rope(x, cos, sin, pos, O.ROPE_NEOX, norm_w=w, eps=1e-6, full=True)
+    _, h = O.add_rmsnorm(x.reshape(rows, heads * d), None, w, 1e-6, write_x=False)
+    want = O.rope(h.reshape(rows, heads, d), cos, sin, pos, O.ROPE_NEOX)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # f64: normalise over the row, rotate the pairs
+    x64 = x.astype(np.float64).reshape(rows, heads * d)
+    n64 = (x64 / np.sqrt((x64 ** 2).mean(-1, keepdims=True) + 1e-6) * w).reshape(rows, heads, d)
+    c, s = cos[pos].astype(np.float64)[:, None], sin[pos].astype(np.float64)[:, None]
+    a, b = n64[..., : d // 2], n64[..., d // 2:]
+    f64 = np.concatenate([a * c - b * s, a * s + b * c], -1)
+    assert np.max(np.abs(got - f64)) < 2e-6 * np.max(np.abs(f64))
+
+
+def test_full_width_norm_is_not_the_per_head_norm():
+    """A planted mistake: the per-head norm with the same weights gives
+    other values whenever the heads' scales differ."""
+    rng = np.random.default_rng(32)
+    rows, heads, d = 3, 4, 16
+    x = (rng.standard_normal((rows, heads, d)) * np.array([1, 2, 4, 8])[None, :, None]).astype(np.float32)
+    w = np.ones(heads * d, np.float32)
+    cos, sin = O.rope_tables(d, 1e4, 4)
+    pos = np.zeros(rows, np.int32)
+    full = O.rope(x, cos, sin, pos, O.ROPE_NEOX, norm_w=w, full=True)
+    per_head = O.rope(x, cos, sin, pos, O.ROPE_NEOX, norm_w=w[:d])
+    assert np.max(np.abs(full - per_head)) > 0.1
+    # position 0 rotates nothing: the full-width result is the row norm itself
+    x64 = x.astype(np.float64).reshape(rows, -1)
+    want = (x64 / np.sqrt((x64 ** 2).mean(-1, keepdims=True) + 1e-6)).reshape(rows, heads, d)
+    assert np.max(np.abs(full - want)) < 2e-6 * np.max(np.abs(want))
