@@ -37,7 +37,9 @@ and stop events the C ABI's profile attaches to every kernel
 reports), against the 8 TB/s HBM peak.
 
 cpu_baseline: the oracle's C restatement of the reference's candle CPU path
-(oracle/), on the host's cores, over a bounded sample of the same step.
+(oracle/) over the same 4096-token step, on the step's own inputs, with the
+CPUs this process is given (the CPU model and counts are recorded); each op
+timed alone, per-op GB/s beside the GPU's.
 """
 import argparse
 import json
@@ -1071,50 +1073,108 @@ def head_bench(ctx, torch, reps=30):
     return res
 
 
-def cpu_baseline(seconds=10.0, n=64):
-    """The oracle (candle-equivalent C restatement) over the same step's ops
-    on n tokens, repeated for about `seconds`, on the host's cores."""
+def host_cpu():
+    """(CPU model, logical CPUs of the host, CPUs this process may run on,
+    threads the baseline uses).  The threads are the CPUs this process is
+    given -- a GPU box grants one GPU's job a share of its host (the
+    OMP_NUM_THREADS it exports), not the whole machine."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    total = os.cpu_count() or 1
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else total
+    try:
+        share = int(os.environ.get("OMP_NUM_THREADS", "") or avail)
+    except ValueError:
+        share = avail
+    return model, total, avail, max(1, min(avail, share))
+
+
+def cpu_baseline(st, seconds=12.0):
+    """The oracle -- the candle-equivalent C restatement of the reference's
+    CPU path -- over the same step as the GPU line: config C at st.n tokens,
+    on the very inputs the GPU step read (copied from the device), with
+    preallocated outputs and the oracle's persistent thread pool.  Each op is
+    repeated for about seconds / 5 and its median call time taken; per-op
+    GB/s use the GPU ops' algorithmic bytes, and the step time is the sum of
+    the ops' medians."""
+    import ctypes
     import numpy as np
-    from cuca_amd import workloads as W
     from oracle import oracle as O
-    cfg = W.CONFIGS["C"]
+    L = O.lib()
+    model, total, avail, threads = host_cpu()
+    cfg, n = st.cfg, st.n
     H, F, d, nq, nk = cfg["hidden"], cfg["ff"], cfg["head_dim"], cfg["nq"], cfg["nk"]
-    threads = max(1, min(16, os.cpu_count() or 1))
-    rng = np.random.default_rng(2)
-    vocab = 4096  # the gather touches n rows; a smaller table holds them
-    table = W.quant_table(rng, vocab, H, cfg["qtype"], cfg["d_range"])
-    ids = rng.integers(0, vocab, n).astype(np.uint32)
-    f16 = np.float16
-    x, b = rng.standard_normal((n, H)).astype(f16), rng.standard_normal((n, H)).astype(f16)
-    w = (1 + 0.02 * rng.standard_normal(H)).astype(np.float32)
-    q, k = rng.standard_normal((n, nq, d)).astype(f16), rng.standard_normal((n, nk, d)).astype(f16)
-    cos, sin = O.rope_tables(d, cfg["theta"], n)
-    pos = np.arange(n, dtype=np.int32)
-    gu = rng.standard_normal((n, 2 * F)).astype(f16)
-    step_bytes = (n * (34 * H // 32 + 4 + 2 * H) + 2 * (n * 8 * H + 4 * H)
-                  + n * (4 * (nq + nk) * d + 4 * d) + n * 6 * F)
+    f16 = st.dt == st.hip.F16
+    dt = O.F16 if f16 else O.F32
+    npdt = np.float16 if f16 else np.float32
 
-    def step():
-        O.embed(table, O.Q8_0, vocab, H, ids, 1.0, out_dtype=f16, threads=threads)
-        O.add_rmsnorm(x, b, w, cfg["eps"], threads=threads)
-        O.rope(q, cos, sin, pos, O.ROPE_NORM, threads=threads)
-        O.rope(k, cos, sin, pos, O.ROPE_NORM, threads=threads)
-        O.glu(gu[:, :F], gu[:, F:], O.SILU, threads=threads)
-        O.add_rmsnorm(x, b, w, cfg["eps"], threads=threads)
+    def host(t):
+        return np.ascontiguousarray(t.cpu().numpy())
 
-    step()
-    iters, t0 = 0, time.perf_counter()
-    while True:
-        step()
-        iters += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    return dict(value=round(step_bytes * iters / el / 1e9, 3), unit="GB/s", cores=threads,
-                kind="port",
-                sample=f"{iters} repetitions of the step on {n} tokens (config C shapes, f16 "
-                       f"activations, Q8_0 table of {vocab} rows), {el:.1f} s, oracle/ C "
-                       f"restatement of the candle CPU path, {threads} threads")
+    def ptr(a):
+        return a.ctypes.data
+
+    table, ids = host(st.table), host(st.ids).astype(np.uint32)
+    emb = np.empty((n, H), npdt)
+    bad = ctypes.c_int64(-1)
+    norm = [dict(x=host(b["x"]), b=host(b["b"]), w=host(b["w"]), xo=np.empty((n, H), npdt),
+                 h=np.empty((n, H), npdt)) for b in st.norm]
+    q, k = host(st.q0), host(st.k0)
+    cos, sin, pos = host(st.cos), host(st.sin), host(st.pos).astype(np.int32)
+    gu = host(st.gu)
+    out = np.empty((n, F), npdt)
+    kind = O.ROPE_NEOX if st.kind == st.hip.ROPE_NEOX else O.ROPE_NORM
+    act = O.GELU_TANH if st.act == st.hip.ACT_GELU_TANH else O.SILU
+    es = 2 if f16 else 4
+
+    def embed():
+        L.oracle_embed(ptr(table), st.qtype, cfg["vocab"], H, ptr(ids), n, cfg["embd_scale"], ptr(emb), dt,
+                       threads, ctypes.byref(bad))
+
+    def add_rmsnorm(b):
+        return lambda: L.oracle_add_rmsnorm(ptr(b["x"]), ptr(b["b"]), ptr(b["w"]), None, cfg["eps"],
+                                            cfg["eps"], 1.0, n, H, ptr(b["xo"]), ptr(b["h"]), dt, threads)
+
+    def rope():
+        L.oracle_rope(ptr(q), nq * d, n, nq, d, d, kind, ptr(cos), ptr(sin), ptr(pos), None, cfg["eps"], dt,
+                      threads)
+        L.oracle_rope(ptr(k), nk * d, n, nk, d, d, kind, ptr(cos), ptr(sin), ptr(pos), None, cfg["eps"], dt,
+                      threads)
+
+    def glu():
+        L.oracle_glu(ptr(gu), 2 * F, gu.ctypes.data + F * es, 2 * F, n, F, act, 0.0, ptr(out), F, dt, threads)
+
+    fns = {"embed": embed, "add_rmsnorm_attn": add_rmsnorm(norm[0]), "rope": rope, "glu": glu,
+           "add_rmsnorm_ffn": add_rmsnorm(norm[1])}
+    ops, total_s, calls = {}, 0.0, 0
+    for name, fn in fns.items():
+        fn()  # first touch of the outputs
+        times, t_end = [], time.perf_counter() + seconds / len(fns)
+        while len(times) < 3 or time.perf_counter() < t_end:
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        med = float(np.median(times))
+        total_s += sum(times)
+        calls += len(times)
+        ops[name] = dict(ms=round(med * 1e3, 3), gbs=round(st.bytes[name] / med / 1e9, 2), calls=len(times))
+    step_s = sum(o["ms"] for o in ops.values()) / 1e3
+    step_bytes = sum(st.bytes.values())
+    return dict(value=round(step_bytes / step_s / 1e9, 3), unit="GB/s", cores=threads, kind="port",
+                cpu_model=model, host_cpus=total, cpus_available=avail, ms_per_step=round(step_s * 1e3, 2),
+                ops=ops,
+                sample=f"config C step at {n} tokens ({cfg['qtype']} table of {cfg['vocab']} rows, "
+                       f"{'f16' if f16 else 'f32'} activations), the GPU step's own inputs; each op "
+                       f"timed alone, median of {calls} calls in {total_s:.1f} s; oracle/ C "
+                       f"restatement of the candle CPU path on {threads} threads (persistent pool) of "
+                       f"{avail} available, {model}")
 
 
 def traffic_from_profiles():
@@ -1133,7 +1193,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--tokens", type=int, default=4096)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-large", action="store_true", help="skip the 16384-token step")
@@ -1173,7 +1233,7 @@ def main():
 
     parity_raw = {}
 
-    def run_size(n, steps, warmup, name="C", dtype="f16"):
+    def run_size(n, steps, warmup, name="C", dtype="f16", cpu_hook=None):
         log(f"config {name}: step buffers, {n} tokens, {dtype}")
         st = LayerStep(ctx, torch, name, n, dtype)
         torch.cuda.synchronize()
@@ -1191,11 +1251,23 @@ def main():
         rows, raw = st.verify()
         parity_raw[f"{name}_{n}_{dtype}"] = raw
         step_bytes = sum(st.bytes.values())
+        if cpu_hook is not None:
+            cpu_hook(st)
         del st
         torch.cuda.empty_cache()
         return ms, step_bytes, ops, rows, ms_plain
 
-    ms_prof, step_bytes, ops, checked_rows, ms = run_size(args.tokens, args.steps, args.warmup)
+    cpu = None
+    cpu_box = {}
+
+    def cpu_leg(st):
+        if not args.no_cpu:
+            log("cpu baseline (the same step on the host's cores)")
+            cpu_box["cpu"] = cpu_baseline(st, args.cpu_seconds)
+
+    ms_prof, step_bytes, ops, checked_rows, ms = run_size(args.tokens, args.steps, args.warmup,
+                                                          cpu_hook=cpu_leg)
+    cpu = cpu_box.get("cpu")
     value = step_bytes / (ms / 1e3) / 1e9
     glu = ops["glu"]
     big = None
@@ -1275,11 +1347,6 @@ def main():
             for n, clen, mm in ((1, 4096, "qmm"), (32, 1024, "qmm"), (32, 1024, "qgemm")):
                 decode[f"step_batch{n}_ctx{clen}_{mm}"] = decode_step_bench(ctx, torch, n, clen, mm=mm)
             torch.cuda.empty_cache()
-
-    cpu = None
-    if not args.no_cpu:
-        log("cpu baseline")
-        cpu = cpu_baseline(args.cpu_seconds)
 
     out = {
         "metric": "fused layer-op HBM GB/s & % of 8 TB/s peak; per-layer non-matmul us at decode",

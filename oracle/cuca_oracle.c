@@ -68,12 +68,62 @@ uint16_t oracle_f32_to_f16(float f) {
     return sign | (uint16_t)h;
 }
 
+/* Bulk conversions, with the x86 F16C instructions when the CPU has them
+ * (as the `half` crate's conversions do, by runtime detection): the same
+ * values as the scalar restatement above -- exact widening, and rounding to
+ * nearest-even with the MXCSR rounding overridden -- which the tests check
+ * exhaustively for f16 -> f32 and over millions of f32 values. */
+#if defined(__x86_64__)
+#include <immintrin.h>
+__attribute__((target("avx,f16c"))) static void h2f_f16c(const uint16_t *h, float *f, int64_t n) {
+    int64_t i = 0;
+    for (; i + 8 <= n; i += 8)
+        _mm256_storeu_ps(f + i, _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(h + i))));
+    for (; i < n; i++) f[i] = oracle_f16_to_f32(h[i]);
+}
+__attribute__((target("avx,f16c"))) static void f2h_f16c(const float *f, uint16_t *h, int64_t n) {
+    int64_t i = 0;
+    for (; i + 8 <= n; i += 8)
+        _mm_storeu_si128((__m128i *)(h + i),
+                         _mm256_cvtps_ph(_mm256_loadu_ps(f + i), _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC));
+    for (; i < n; i++) h[i] = oracle_f32_to_f16(f[i]);
+}
+static int have_f16c(void) {
+    static int v = -1;
+    if (v < 0) v = __builtin_cpu_supports("f16c") && __builtin_cpu_supports("avx") ? 1 : 0;
+    return v;
+}
+#endif
+
 void oracle_f16_to_f32_n(const uint16_t *h, float *f, int64_t n) {
+#if defined(__x86_64__)
+    if (have_f16c()) { h2f_f16c(h, f, n); return; }
+#endif
     for (int64_t i = 0; i < n; i++) f[i] = oracle_f16_to_f32(h[i]);
 }
 
 void oracle_f32_to_f16_n(const float *f, uint16_t *h, int64_t n) {
+#if defined(__x86_64__)
+    if (have_f16c()) { f2h_f16c(f, h, n); return; }
+#endif
     for (int64_t i = 0; i < n; i++) h[i] = oracle_f32_to_f16(f[i]);
+}
+
+/* The scalar restatement over n values (the tests compare both paths). */
+void oracle_f16_to_f32_soft_n(const uint16_t *h, float *f, int64_t n) {
+    for (int64_t i = 0; i < n; i++) f[i] = oracle_f16_to_f32(h[i]);
+}
+
+void oracle_f32_to_f16_soft_n(const float *f, uint16_t *h, int64_t n) {
+    for (int64_t i = 0; i < n; i++) h[i] = oracle_f32_to_f16(f[i]);
+}
+
+int oracle_has_f16c(void) {
+#if defined(__x86_64__)
+    return have_f16c();
+#else
+    return 0;
+#endif
 }
 
 static inline float load_el(const void *p, int64_t i, int dtype) {
@@ -84,6 +134,17 @@ static inline float load_el(const void *p, int64_t i, int dtype) {
 static inline void store_el(void *p, int64_t i, float v, int dtype) {
     if (dtype == OR_F16) ((uint16_t *)p)[i] = oracle_f32_to_f16(v);
     else ((float *)p)[i] = v;
+}
+
+/* n values of a row starting at element `at`, widened to f32 / rounded back */
+static void load_row(const void *p, int64_t at, int64_t n, int dtype, float *dst) {
+    if (dtype == OR_F16) oracle_f16_to_f32_n((const uint16_t *)p + at, dst, n);
+    else memcpy(dst, (const float *)p + at, sizeof(float) * (size_t)n);
+}
+
+static void store_row(void *p, int64_t at, int64_t n, int dtype, const float *src) {
+    if (dtype == OR_F16) oracle_f32_to_f16_n(src, (uint16_t *)p + at, n);
+    else memcpy((float *)p + at, src, sizeof(float) * (size_t)n);
 }
 
 /* ------------------------------------------------------------------ */
@@ -305,12 +366,13 @@ typedef struct {
 static void norm_range(void *c, int64_t begin, int64_t end) {
     norm_ctx *n = (norm_ctx *)c;
     int64_t H = n->H;
-    float *xv = (float *)malloc(sizeof(float) * (size_t)H * 3);
+    float *xv = (float *)malloc(sizeof(float) * (size_t)H * 3 + sizeof(uint16_t) * (size_t)H);
     float *bv = xv + H, *hv = bv + H;
+    uint16_t *x16 = (uint16_t *)(hv + H);
     for (int64_t r = begin; r < end; r++) {
-        for (int64_t i = 0; i < H; i++) xv[i] = load_el(n->x, r * H + i, n->dtype);
+        load_row(n->x, r * H, H, n->dtype, xv);
         if (n->branch) {
-            for (int64_t i = 0; i < H; i++) bv[i] = load_el(n->branch, r * H + i, n->dtype);
+            load_row(n->branch, r * H, H, n->dtype, bv);
             /* Gemma sandwich: post_attn_norm / post_ffw_norm on the branch
              * (cpu.rs:2675-2677, 2690-2692) */
             if (n->w_post) rms_row(bv, n->w_post, n->post_eps, H, bv);
@@ -321,12 +383,13 @@ static void norm_range(void *c, int64_t begin, int64_t end) {
         }
         /* the residual stream is held in the activation type: the norm reads
          * x' as stored */
-        for (int64_t i = 0; i < H; i++) {
-            if (n->dtype == OR_F16) xv[i] = oracle_f16_to_f32(oracle_f32_to_f16(xv[i]));
-            if (n->x_out) store_el(n->x_out, r * H + i, xv[i], n->dtype);
+        if (n->dtype == OR_F16) {
+            oracle_f32_to_f16_n(xv, x16, H);
+            oracle_f16_to_f32_n(x16, xv, H);
         }
+        if (n->x_out) store_row(n->x_out, r * H, H, n->dtype, xv);
         rms_row(xv, n->w, n->eps, H, hv);
-        for (int64_t i = 0; i < H; i++) store_el(n->h_out, r * H + i, hv[i], n->dtype);
+        store_row(n->h_out, r * H, H, n->dtype, hv);
     }
     free(xv);
 }
@@ -363,18 +426,23 @@ typedef struct {
 
 static void glu_range(void *c, int64_t begin, int64_t end) {
     glu_ctx *g = (glu_ctx *)c;
+    float *gb = (float *)malloc(sizeof(float) * (size_t)g->ff * 2);
+    float *ub = gb + g->ff;
     for (int64_t r = begin; r < end; r++) {
+        load_row(g->gate, r * g->gate_ld, g->ff, g->dtype, gb);
+        load_row(g->up, r * g->up_ld, g->ff, g->dtype, ub);
         for (int64_t j = 0; j < g->ff; j++) {
-            float gv = load_el(g->gate, r * g->gate_ld + j, g->dtype);
-            float uv = load_el(g->up, r * g->up_ld + j, g->dtype);
+            float gv = gb[j], uv = ub[j];
             if (g->clamp > 0.0f) { /* Glu::apply clamp (cpu.rs:364-368) */
                 gv = gv < g->clamp ? gv : g->clamp;
                 uv = uv > -g->clamp ? uv : -g->clamp;
                 uv = uv < g->clamp ? uv : g->clamp;
             }
-            store_el(g->out, r * g->out_ld + j, act_f32(gv, g->act) * uv, g->dtype);
+            gb[j] = act_f32(gv, g->act) * uv;
         }
+        store_row(g->out, r * g->out_ld, g->ff, g->dtype, gb);
     }
+    free(gb);
 }
 
 void oracle_glu(const void *gate, int64_t gate_ld, const void *up, int64_t up_ld,
@@ -459,7 +527,7 @@ static void rope_range(void *c, int64_t begin, int64_t end) {
              * weights [heads * d], before the heads are split (cpu.rs:2838-2843,
              * 3042-3045) */
             int64_t w = (int64_t)p->heads * p->d;
-            for (int64_t i = 0; i < w; i++) rowv[i] = load_el(p->x, r * p->ld + i, p->dtype);
+            load_row(p->x, r * p->ld, w, p->dtype, rowv);
             if (p->norm_w) rms_row(rowv, p->norm_w, p->eps, w, rowv);
         }
         for (int h = 0; h < p->heads; h++) {
@@ -467,7 +535,7 @@ static void rope_range(void *c, int64_t begin, int64_t end) {
             if (p->full) {
                 memcpy(v, rowv + (int64_t)h * p->d, sizeof(float) * (size_t)p->d);
             } else {
-                for (int i = 0; i < p->d; i++) v[i] = load_el(p->x, at + i, p->dtype);
+                load_row(p->x, at, p->d, p->dtype, v);
                 /* QK-norm per head: rms(q.reshape(1,t,nh,d), w[d]) (cpu.rs:2864) */
                 if (p->norm_w) rms_row(v, p->norm_w, p->eps, p->d, v);
             }
@@ -479,7 +547,7 @@ static void rope_range(void *c, int64_t begin, int64_t end) {
                 o[a] = v[a] * cs[i] - v[b] * sn[i];
                 o[b] = v[a] * sn[i] + v[b] * cs[i];
             }
-            for (int i = 0; i < p->d; i++) store_el(p->x, at + i, o[i], p->dtype);
+            store_row(p->x, at, p->d, p->dtype, o);
         }
     }
     free(v);

@@ -36,6 +36,12 @@ float oracle_f16_to_f32(uint16_t h);
 uint16_t oracle_f32_to_f16(float f);
 void oracle_f16_to_f32_n(const uint16_t *h, float *f, int64_t n);
 void oracle_f32_to_f16_n(const float *f, uint16_t *h, int64_t n);
+/* The _n conversions use the x86 F16C instructions when the CPU has them
+ * (oracle_has_f16c), the scalar restatement otherwise; the _soft_n forms are
+ * always the scalar restatement. */
+void oracle_f16_to_f32_soft_n(const uint16_t *h, float *f, int64_t n);
+void oracle_f32_to_f16_soft_n(const float *f, uint16_t *h, int64_t n);
+int oracle_has_f16c(void);
 
 /* Bytes per row of `hidden` values of a Q4_0 / Q8_0 tensor, or -1 when the
  * row is not a whole number of 32-value blocks (quant.rs:110-118). */

@@ -43,6 +43,9 @@ def lib():
         L.oracle_f32_to_f16.argtypes = [_f32]
         L.oracle_f16_to_f32_n.argtypes = [_p, _p, _i64]
         L.oracle_f32_to_f16_n.argtypes = [_p, _p, _i64]
+        L.oracle_f16_to_f32_soft_n.argtypes = [_p, _p, _i64]
+        L.oracle_f32_to_f16_soft_n.argtypes = [_p, _p, _i64]
+        L.oracle_has_f16c.restype = _int
         L.oracle_row_bytes.restype = _i64
         L.oracle_row_bytes.argtypes = [ctypes.c_uint32, _i64]
         L.oracle_dequant_row.restype = _int
