@@ -14,6 +14,7 @@
 
 #include <hip/hip_runtime_api.h>
 #include <hipblaslt/hipblaslt.h>
+#include <hipblaslt/hipblaslt-ext.hpp>
 
 #include <cmath>
 #include <cstdarg>
@@ -1430,6 +1431,26 @@ static cuca_status lt_gemm(cuca_hip_ctx *ctx, const void *w16, int64_t rows, int
             if (e != HIPBLAS_STATUS_SUCCESS || count < 1) {
                 st = fail(ctx, CUCA_UNSUPPORTED, "hipBLASLt: no algorithm for %lld x %lld x %lld (status %d)",
                           (long long)m, (long long)rows, (long long)k, (int)e);
+                break;
+            }
+            // Use an answer only when the library itself confirms it for this
+            // exact problem and it fits the workspace passed to every call: its
+            // heuristic state, its stated workspace, and AlgoCheck's verdict and
+            // workspace.  Otherwise refuse the shape rather than launch it.
+            const float one = 1.0f, zero = 0.0f;
+            size_t chk_ws = 0;
+            const hipblasStatus_t ce =
+                res[0].state == HIPBLAS_STATUS_SUCCESS
+                    ? hipblaslt_ext::matmulIsAlgoSupported(ctx->lt, op, &one, la, lb, &zero, ld, ld, res[0].algo,
+                                                           chk_ws)
+                    : res[0].state;
+            if (res[0].state != HIPBLAS_STATUS_SUCCESS || res[0].workspaceSize > kLtWorkspace ||
+                ce != HIPBLAS_STATUS_SUCCESS || chk_ws > kLtWorkspace) {
+                st = fail(ctx, CUCA_UNSUPPORTED,
+                          "hipBLASLt: the algorithm for %lld x %lld x %lld is not confirmed (state %d, check %d, "
+                          "workspace %zu/%zu of %zu bytes)",
+                          (long long)m, (long long)rows, (long long)k, (int)res[0].state, (int)ce,
+                          (size_t)res[0].workspaceSize, chk_ws, (size_t)kLtWorkspace);
                 break;
             }
             ctx->lt_plans.push_back({rows, k, m, ldx, ldd, (int)dt, res[0].algo});
