@@ -565,7 +565,7 @@ class DecodeStep:
     generated as GGUF bytes on the device and packed once; the K/V pools
     hold ctx_len keys per sequence in consecutive blocks."""
 
-    def __init__(self, ctx, torch, n, ctx_len, qtype="q4_0", layers=32, seed=3, mm="qmm"):
+    def __init__(self, ctx, torch, n, ctx_len, qtype="q4_0", layers=32, seed=3, mm="qmm", fuse_rope=False):
         import numpy as np
         from cuca_amd import hip
         from cuca_amd import workloads as W
@@ -623,6 +623,9 @@ class DecodeStep:
         # the projections: the CPU engine's bits (qmm), or the matrix cores
         # (qgemm, the GPU engine's arithmetic class) with one workspace
         self.mm = mm
+        # the Q|K|V projection carries RoPE and the K/V store in its epilogue
+        # (cuca_hip_qmm_rope_store_kv) instead of a launch of its own
+        self.fuse_rope = fuse_rope and mm == "qmm"
         if mm == "qgemm":
             self.qg_bytes = max([hip.qgemm_workspace(T, rows, cols, n, glu) for rows, cols, glu in (
                 ((nq + 2 * nk) * d, H, False), (H, nq * d, False), (F, H, True), (H, F, False))]
@@ -649,12 +652,18 @@ class DecodeStep:
             # one Q|K|V projection; RoPE, the K/V store and the attention
             # read their heads in place from its rows
             qkv_ld = (nq + 2 * nk) * d
-            self.mat(l["wqkv"], qkv_ld, H, self.h, self.qkv)
             q_ptr = self.qkv.data_ptr()
-            c.rope_store_kv(q_ptr, qkv_ld, q_ptr + 4 * nq * d, qkv_ld, q_ptr + 4 * (nq + nk) * d, qkv_ld,
-                            n, nq, nk, d, d, hip.ROPE_NORM, self.cos.data_ptr(), self.sin.data_ptr(), 8192,
-                            self.pos.data_ptr(), None, None, 0, eps, l["pk"].data_ptr(), l["pv"].data_ptr(),
-                            self.n_blocks, self.slots.data_ptr(), f32)
+            if self.fuse_rope:
+                c.qmm_rope_store_kv(l["wqkv"].data_ptr(), T, H, self.h.data_ptr(), H, n, nq, nk, d, d,
+                                    hip.ROPE_NORM, self.cos.data_ptr(), self.sin.data_ptr(), 8192,
+                                    self.pos.data_ptr(), q_ptr, qkv_ld, l["pk"].data_ptr(), l["pv"].data_ptr(),
+                                    self.n_blocks, self.slots.data_ptr(), f32)
+            else:
+                self.mat(l["wqkv"], qkv_ld, H, self.h, self.qkv)
+                c.rope_store_kv(q_ptr, qkv_ld, q_ptr + 4 * nq * d, qkv_ld, q_ptr + 4 * (nq + nk) * d, qkv_ld,
+                                n, nq, nk, d, d, hip.ROPE_NORM, self.cos.data_ptr(), self.sin.data_ptr(), 8192,
+                                self.pos.data_ptr(), None, None, 0, eps, l["pk"].data_ptr(), l["pv"].data_ptr(),
+                                self.n_blocks, self.slots.data_ptr(), f32)
             c.paged_decode(q_ptr, l["pk"].data_ptr(), l["pv"].data_ptr(), self.n_blocks,
                            self.tables.data_ptr(), self.max_blocks, self.ranges.data_ptr(), n, nq, nk, d,
                            self.scale, self.ws.data_ptr(), self.ws_bytes, self.o.data_ptr(), f32,
@@ -687,18 +696,43 @@ class DecodeStep:
         c.argmax(self.logits.data_ptr(), self.vocab, n, self.vocab, hip.F32, self.out_ids.data_ptr())
 
 
-def decode_step_bench(ctx, torch, n, ctx_len, replays=10, mm="qmm"):
+# The kernels of a decode layer by role, from their symbol names.
+def kernel_role(name):
+    if name.startswith(("cuca_qmm_rope_kv",)):
+        return "qkv_rope_kv"
+    if name.startswith(("cuca_qmm", "cuca_qgemm", "cuca_qmv", "cuca_q8_acts")):
+        return "matmul"
+    if name.startswith("cuca_attn"):
+        return "attention"
+    if name.startswith(("cuca_norm", "cuca_rope", "cuca_glu")):
+        return "non_matmul"
+    return "other"
+
+
+def decode_step_bench(ctx, torch, n, ctx_len, replays=10, mm="qmm", fuse_rope=False):
     """DecodeStep's 32 layers and its whole step, each captured in one
     hipGraph and replayed: microseconds per layer, per step, and tokens/s
-    (n tokens per step).  Checked: the step's ids are the argmax of its own
-    logits, and the logits are finite."""
+    (n tokens per step).  The step's own kernels, timed on the device
+    (kernel timestamps of one eager step), give the per-layer split: the
+    non-matmul sequence (residual + RMSNorm twice, RoPE + K/V store when it
+    is a launch of its own, a separate activation), the matmuls, the fused
+    Q|K|V + RoPE + K/V-store launch, attention.  Checked: the step's ids are
+    the argmax of its own logits, and the logits are finite."""
     import numpy as np
-    ds = DecodeStep(ctx, torch, n, ctx_len, mm=mm)
+    ds = DecodeStep(ctx, torch, n, ctx_len, mm=mm, fuse_rope=fuse_rope)
     ds.out_ids.copy_(ds.ids)
     torch.cuda.synchronize()
     ds.issue_step()  # eager, once
     torch.cuda.synchronize()
     ctx.check_device()
+    ctx.profile_start(16 * ds.layers + 16)
+    ds.issue_layers()
+    recs = ctx.profile_stop()
+    roles = {}
+    for k, ms in recs:
+        r = kernel_role(k)
+        roles[r] = roles.get(r, 0.0) + ms
+    split = {r + "_us_per_layer": round(t * 1000 / ds.layers, 2) for r, t in roles.items()}
     ctx.graph_begin()
     ds.issue_layers()
     gl = ctx.graph_end()
@@ -719,9 +753,10 @@ def decode_step_bench(ctx, torch, n, ctx_len, replays=10, mm="qmm"):
     del ds
     torch.cuda.empty_cache()
     return dict(batch=n, ctx_len=ctx_len, layer_weights="q4_0", head="q8_0", matmul=mm,
+                rope_in_qkv_epilogue=bool(fuse_rope and mm == "qmm"),
                 us_per_layer=round(layers_ms * 1000 / 32, 2), us_per_step=round(step_ms * 1000, 1),
                 tokens_per_s=round(n / (step_ms / 1e3), 1),
-                layer_weight_gbs=round(wb / (layers_ms / 1e3) / 1e9, 1))
+                layer_weight_gbs=round(wb / (layers_ms / 1e3) / 1e9, 1), **split)
 
 
 def decode_us_per_layer(ctx, torch, n, replays=50, ctx_len=None):
@@ -1344,8 +1379,10 @@ def main():
         torch.cuda.empty_cache()
         if not args.no_qmm:
             log("whole decode steps (32 layers + head, hipGraph)")
-            for n, clen, mm in ((1, 4096, "qmm"), (32, 1024, "qmm"), (32, 1024, "qgemm")):
-                decode[f"step_batch{n}_ctx{clen}_{mm}"] = decode_step_bench(ctx, torch, n, clen, mm=mm)
+            for n, clen, mm, fuse in ((1, 4096, "qmm", False), (1, 4096, "qmm", True), (32, 1024, "qmm", True),
+                                      (32, 1024, "qgemm", False)):
+                key = f"step_batch{n}_ctx{clen}_{mm}" + ("_rope_in_qkv" if fuse else "")
+                decode[key] = decode_step_bench(ctx, torch, n, clen, mm=mm, fuse_rope=fuse)
             torch.cuda.empty_cache()
 
     out = {

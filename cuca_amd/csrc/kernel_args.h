@@ -158,6 +158,15 @@ typedef struct {
     int32_t cap_flags;
     float mul1, mul2, softcap_inv, softcap;
     int32_t pad2_;
+    /* Q|K|V projection with RoPE and the paged K/V store in the epilogue
+     * (qmm_rope_kv kernels): weight rows [0, nq * d) are the Q heads, then
+     * nk K heads and nk V heads of d rows; Q is rotated into out, K rotated
+     * and V copied into the pools [n_blocks, nk, 16, d] at slots[j].       */
+    const float *cos_t, *sin_t;     /* [table_rows, n_dims / 2]              */
+    const int32_t *pos, *slots;     /* [m]                                   */
+    void *pool_k, *pool_v;
+    int64_t table_rows, n_slots;
+    int32_t nq, nk, head_dim, n_dims;
 } QmmArgs;
 
 /* The quantized matmul on the matrix cores (qgemm.hip): out[t][n] =

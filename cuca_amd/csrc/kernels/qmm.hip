@@ -447,9 +447,58 @@ __device__ static inline bool qmm_moe_tile(const QmmArgs &a, int tile, int *expe
     return moe_tile_lookup<MT>(a.offsets, a.n_experts, a.max_pairs, tile, expert, p0, p1);
 }
 
+// The Q|K|V epilogue (MODE 3): the output o of weight row `row` for
+// activation row j, as the plain kernel would store it, then what
+// rope_store_kv (rope.hip; store_kv, cpu.rs:3028-3097) does to it: Q and K
+// rotated in NORM pairs (2i, 2i+1) -- rows row and row ^ 1, held by the
+// lanes 16 apart in this wave -- as a' = a c - b s, b' = a s + b c with
+// each product rounded on its own; Q stored in place of the plain output,
+// K and V written to their pools at pool row slots[j].  The same bits as
+// cuca_hip_qmm followed by cuca_hip_rope_store_kv.  A row whose position
+// or slot is bad keeps Q unrotated and stores no K/V (as rope_store_kv
+// leaves it), and is reported.
+template <typename T>
+__device__ static inline void qmm_rope_kv_store(const QmmArgs &a, int jg, bool valid, int64_t orow, int row,
+                                                int lane, float o) {
+    // the value the plain kernel stores, widened back (exact)
+    const float v = (float)to_stored<T>(o);
+    const float pv = __shfl_xor(v, 16, CUCA_WAVE); // row ^ 1: the pair partner
+    if (lane != 0 || row >= a.rows || !valid) return;
+    const int D = a.head_dim, half = a.n_dims >> 1;
+    const int h = row / D, e = row - h * D;
+    const int hk = h < a.nq ? 0 : (h < a.nq + a.nk ? 1 : 2); // Q, K or V head
+    const int32_t pos = a.pos[jg], slot = a.slots[jg];
+    const bool ok = pos >= 0 && (int64_t)pos < a.table_rows && slot >= 0 && (int64_t)slot < a.n_slots;
+    if (!ok) {
+        if (row == 0) {
+            if (!(pos >= 0 && (int64_t)pos < a.table_rows))
+                record_bad(a.status + CUCA_STATUS_ROPE_POS, (uint32_t)jg, (uint32_t)pos);
+            else
+                record_bad(a.status + CUCA_STATUS_KV_SLOT, (uint32_t)jg, (uint32_t)slot);
+        }
+        if (hk == 0) reinterpret_cast<T *>(a.out)[orow + row] = to_stored<T>(v);
+        return;
+    }
+    float r = v;
+    if (hk != 2 && e < a.n_dims) {
+        const int64_t t = (int64_t)pos * half + (e >> 1);
+        const float c = a.cos_t[t], s = a.sin_t[t];
+        // a' = a c - b s (even element), b' = a s + b c (odd element)
+        r = (e & 1) ? pv * s + v * c : v * c - pv * s;
+    }
+    if (hk == 0) {
+        reinterpret_cast<T *>(a.out)[orow + row] = to_stored<T>(r);
+    } else {
+        const int kvh = h - a.nq - (hk == 2 ? a.nk : 0);
+        const int64_t prow = ((int64_t)(slot >> 4) * a.nk + kvh) * 16 + (slot & 15);
+        reinterpret_cast<T *>(hk == 1 ? a.pool_k : a.pool_v)[prow * D + e] = to_stored<T>(r);
+    }
+}
+
 // MODE 0: dense (x rows j0.., out rows j0..); 1: MoE up (act row of pair p =
 // x row pair_token[p], output row p); 2: MoE down (act row p of x, output
-// row p of an f32 scratch, times pair_weight[p]).
+// row p of an f32 scratch, times pair_weight[p]); 3: dense Q|K|V with RoPE
+// (NORM pairs) and the paged K/V store in the epilogue.
 template <typename T, int FMT, int MT, bool GLU, int ACT, int MODE>
 __device__ static inline void qmm_body(const QmmArgs &a) {
     using F = QFmt<FMT>;
@@ -469,7 +518,7 @@ __device__ static inline void qmm_body(const QmmArgs &a) {
     const int nch = (a.ng * F::G + S::CB - 1) / S::CB;
 
     QTile<MT> tl;
-    if constexpr (MODE == 0) {
+    if constexpr (MODE == 0 || MODE == 3) {
         const int j0 = tile * MT;
 #pragma unroll
         for (int j = 0; j < MT; j++) {
@@ -554,6 +603,10 @@ __device__ static inline void qmm_body(const QmmArgs &a) {
             if (a.cap_flags & 1) o = o * a.mul1 + 0.0f;
             if (a.cap_flags & 2) o = o * a.mul2 + 0.0f;
             if (a.cap_flags & 4) o = tanhf(o * a.softcap_inv + 0.0f) * a.softcap + 0.0f;
+        }
+        if constexpr (MODE == 3) {
+            qmm_rope_kv_store<T>(a, tile * MT + j, tl.xrow[j] >= 0, tl.orow[j], row, lane, o);
+            continue;
         }
         if (lane == 0 && row < a.rows && tl.xrow[j] >= 0) {
             if (MODE == 2) // CpuExpert::add_picks: y * weight (cpu.rs:400-417)
@@ -684,7 +737,8 @@ extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void cuca_qpack_q8_0(QPackAr
     CUCA_QMM(cuca_qmm_glu_##TN##_##FN##_gelu_m##MT, T, FMT, MT, true, 1, 0)                \
     CUCA_QMM(cuca_moe_up_##TN##_##FN##_silu_m##MT, T, FMT, MT, true, 0, 1)                 \
     CUCA_QMM(cuca_moe_up_##TN##_##FN##_gelu_m##MT, T, FMT, MT, true, 1, 1)                 \
-    CUCA_QMM(cuca_moe_down_##TN##_##FN##_m##MT, T, FMT, MT, false, 0, 2)
+    CUCA_QMM(cuca_moe_down_##TN##_##FN##_m##MT, T, FMT, MT, false, 0, 2)                  \
+    CUCA_QMM(cuca_qmm_rope_kv_##TN##_##FN##_m##MT, T, FMT, MT, false, 0, 3)
 #define CUCA_QMM_SET(TN, T, FN, FMT)                                                       \
     CUCA_QMM_MT(TN, T, FN, FMT, 1)                                                         \
     CUCA_QMM_MT(TN, T, FN, FMT, 2)                                                         \

@@ -1173,6 +1173,86 @@ static cuca_status qmm_common(cuca_hip_ctx *ctx, const void *w, const void *w_up
     return launch(ctx, kk, (unsigned)(nrb8 * ntile), CUCA_BLOCK_THREADS, 0, a);
 }
 
+cuca_status cuca_hip_qmm_rope_store_kv(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type, int64_t k, const void *x,
+                                       int64_t ldx, int64_t m, int32_t nq, int32_t nk, int32_t head_dim,
+                                       int32_t n_dims, cuca_rope_kind kind, const float *cos, const float *sin,
+                                       int64_t table_rows, const int32_t *positions, void *q_out, int64_t q_ld,
+                                       void *pool_k, void *pool_v, int64_t n_blocks, const int32_t *slots,
+                                       cuca_dtype dtype) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    if (kind != CUCA_ROPE_NORM)
+        return fail(ctx, kind == CUCA_ROPE_NEOX ? CUCA_UNSUPPORTED : CUCA_INVALID_ARG,
+                    "qmm_rope_store_kv: only NORM (adjacent-pair) RoPE rides in the matmul's epilogue; NEOX "
+                    "models take cuca_hip_qmm + cuca_hip_rope_store_kv");
+    if (nq <= 0 || nk <= 0 || head_dim <= 0 || head_dim % 2 != 0 || n_dims <= 0 || n_dims > head_dim ||
+        n_dims % 2 != 0)
+        return fail(ctx, CUCA_INVALID_ARG, "qmm_rope_store_kv: bad heads %d/%d x %d, n_dims %d", nq, nk, head_dim,
+                    n_dims);
+    const int64_t n = (int64_t)(nq + 2 * nk) * head_dim;
+    int g = 0, gb = 0;
+    if ((st = qweight_shape(ctx, ggml_type, n, k, &g, &gb)) != CUCA_OK) return st;
+    if (!dtype_ok(dtype)) return fail(ctx, CUCA_INVALID_ARG, "bad dtype %d", (int)dtype);
+    if (m < 0 || m > 0x7fffffffll) return fail(ctx, CUCA_INVALID_ARG, "qmm: bad activation row count %lld", (long long)m);
+    if (ldx < k) return fail(ctx, CUCA_INVALID_ARG, "qmm: activation row stride %lld shorter than %lld",
+                             (long long)ldx, (long long)k);
+    if (q_ld < (int64_t)nq * head_dim)
+        return fail(ctx, CUCA_INVALID_ARG, "q row stride %lld shorter than %d heads of %d", (long long)q_ld, nq,
+                    head_dim);
+    if (n_blocks <= 0 || n_blocks > 0x7fffffffll / CUCA_KV_BLOCK)
+        return fail(ctx, CUCA_INVALID_ARG, "bad pool size %lld blocks", (long long)n_blocks);
+    if (m == 0) return CUCA_OK;
+    if (!w || !x || !q_out || !cos || !sin || !positions || !pool_k || !pool_v || !slots)
+        return fail(ctx, CUCA_INVALID_ARG, "null pointer");
+    if (table_rows <= 0) return fail(ctx, CUCA_INVALID_ARG, "empty rope table");
+    const size_t es = esize(dtype);
+    if (!al16(w)) return fail(ctx, CUCA_INVALID_ARG, "packed weights must be 16-byte aligned");
+    if (!al16(x) || ((size_t)ldx * es) % 16 != 0)
+        return fail(ctx, CUCA_INVALID_ARG, "qmm: activation rows must start 16-byte aligned");
+    const int64_t nb = k / 32, ng = (nb + g - 1) / g;
+    const int mt = m == 1 ? 1 : m == 2 ? 2 : 4;
+    const int mi = mt == 1 ? 0 : mt == 2 ? 1 : 2;
+    const int64_t ntile = (m + mt - 1) / mt;
+    const int64_t nrb = (n + 15) / 16;
+    const int64_t nrb8 = (nrb + 7) / 8 * 8;
+    if (nrb8 * ntile > 0x7fffffffll) return fail(ctx, CUCA_UNSUPPORTED, "qmm: grid too large");
+    static const Kernel table_k[2][2][3] = {
+        {{cuca_qmm_rope_kv_f32_q4_0_m1, cuca_qmm_rope_kv_f32_q4_0_m2, cuca_qmm_rope_kv_f32_q4_0_m4},
+         {cuca_qmm_rope_kv_f32_q8_0_m1, cuca_qmm_rope_kv_f32_q8_0_m2, cuca_qmm_rope_kv_f32_q8_0_m4}},
+        {{cuca_qmm_rope_kv_f16_q4_0_m1, cuca_qmm_rope_kv_f16_q4_0_m2, cuca_qmm_rope_kv_f16_q4_0_m4},
+         {cuca_qmm_rope_kv_f16_q8_0_m1, cuca_qmm_rope_kv_f16_q8_0_m2, cuca_qmm_rope_kv_f16_q8_0_m4}}};
+    QmmArgs a{};
+    a.w = static_cast<const uint8_t *>(w);
+    a.x = x;
+    a.out = q_out;
+    a.ldx = ldx;
+    a.out_ld = q_ld;
+    a.row_bytes = ng * gb;
+    a.rows = (int32_t)n;
+    a.m = (int32_t)m;
+    a.nb = (int32_t)nb;
+    a.ng = (int32_t)ng;
+    a.nrb = (int32_t)nrb;
+    a.ntile = (int32_t)ntile;
+    a.status = ctx->status;
+    a.cos_t = cos;
+    a.sin_t = sin;
+    a.pos = positions;
+    a.slots = slots;
+    a.pool_k = pool_k;
+    a.pool_v = pool_v;
+    a.table_rows = table_rows;
+    a.n_slots = n_blocks * CUCA_KV_BLOCK;
+    a.nq = nq;
+    a.nk = nk;
+    a.head_dim = head_dim;
+    a.n_dims = n_dims;
+    ctx->last_table_rows = table_rows;
+    ctx->last_kv_blocks = n_blocks;
+    return launch(ctx, table_k[dtype == CUCA_F16][ggml_type == CUCA_GGML_Q8_0][mi], (unsigned)(nrb8 * ntile),
+                  CUCA_BLOCK_THREADS, 0, a);
+}
+
 cuca_status cuca_hip_lm_head(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type, int64_t vocab, int64_t n_embd,
                              const void *x, int64_t ldx, int64_t m, int64_t rows, float logit_scale,
                              float logit_mult, float softcap, void *logits, int64_t logits_ld, cuca_dtype dtype) {

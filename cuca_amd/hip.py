@@ -83,6 +83,8 @@ SIGNATURES = {
     "cuca_hip_qweight_bytes": (_st, [_u32, _i64, _i64, ctypes.POINTER(_sz)]),
     "cuca_hip_qweight_pack": (_st, [_p, _p, _u32, _i64, _i64, _p]),
     "cuca_hip_qmm": (_st, [_p, _p, _u32, _i64, _i64, _p, _i64, _i64, _i64, _p, _i64, _st]),
+    "cuca_hip_qmm_rope_store_kv": (_st, [_p, _p, _u32, _i64, _p, _i64, _i64, _i32, _i32, _i32, _i32,
+                                         _st, _p, _p, _i64, _p, _p, _i64, _p, _p, _i64, _p, _st]),
     "cuca_hip_qmm_glu": (_st, [_p, _p, _p, _u32, _i64, _i64, _p, _i64, _i64, _st, _f32, _p, _i64,
                                _st]),
     "cuca_hip_qgemm_workspace": (_st, [_u32, _i64, _i64, _i64, _i32, ctypes.POINTER(ctypes.c_size_t)]),
@@ -409,6 +411,12 @@ class Context:
     def gemm_w16_glu(self, w16, ff, k, x, ldx, m, act, clamp, ws, ws_bytes, out, out_ld, dtype):
         self.check(self.L.cuca_hip_gemm_w16_glu(self.ptr, w16, ff, k, x, ldx, m, act, clamp, ws,
                                                 ws_bytes, out, out_ld, dtype))
+
+    def qmm_rope_store_kv(self, w, ggml_type, k, x, ldx, m, nq, nk, head_dim, n_dims, kind, cos, sin,
+                          table_rows, positions, q_out, q_ld, pool_k, pool_v, n_blocks, slots, dtype):
+        self.check(self.L.cuca_hip_qmm_rope_store_kv(self.ptr, w, ggml_type, k, x, ldx, m, nq, nk, head_dim,
+                                                     n_dims, kind, cos, sin, table_rows, positions, q_out,
+                                                     q_ld, pool_k, pool_v, n_blocks, slots, dtype))
 
     def qmm_glu(self, gate, up, ggml_type, ff, k, x, ldx, m, act, clamp, out, out_ld, dtype):
         self.check(self.L.cuca_hip_qmm_glu(self.ptr, gate, up, ggml_type, ff, k, x, ldx, m, act,

@@ -32,6 +32,8 @@
  *                          (+ _workspace, host)           cpu/paged_attn.rs:105-290
  *   cuca_hip_qmm           QmmWeight::forward_rows        qmm.rs:1810-1838
  *   cuca_hip_qmm_glu       gate/up qmm + Glu::apply       cpu.rs:342-371, 3554-3566
+ *   cuca_hip_qmm_rope_     Q|K|V qmm + store_kv (RoPE,    cpu.rs:3028-3097,
+ *     store_kv             paged K/V store)               gpu.rs:5266-5285
  *   cuca_hip_qgemm(_glu)   dense_dequant + matmul (GPU)   moe_kernel.rs:1414-1600
  *   cuca_hip_qweight_      dense_dequant_kernel, then     moe_kernel.rs:1560-1600,
  *     dequant, _gemm_w16   the dense matmul (GPU engine)  1414-1500
@@ -379,6 +381,28 @@ cuca_status cuca_hip_qweight_pack(cuca_hip_ctx *ctx, const void *gguf, uint32_t 
 cuca_status cuca_hip_qmm(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type, int64_t n, int64_t k,
                          const void *x, int64_t ldx, int64_t m, int64_t rows, void *out, int64_t out_ld,
                          cuca_dtype dtype);
+
+/* The fused Q|K|V projection of a K/V-owning layer with RoPE and the paged
+ * K/V store in its epilogue: cuca_hip_qmm over w = the Q, K and V rows
+ * ((nq + 2 nk) * head_dim rows of k values, Q heads first), then what
+ * cuca_hip_rope_store_kv does to its output (store_kv, cpu.rs:3028-3097),
+ * in one launch and with the same bits:
+ *   Q heads: rotated, written to q_out [m][q_ld] (the first nq * head_dim
+ *            values of each row);
+ *   K heads: rotated, written to pool_k at pool row slots[j] of their KV
+ *            head; V heads: written to pool_v there (pools as
+ *            cuca_hip_rope_store_kv's, [n_blocks, nk, 16, head_dim]).
+ * Only NORM RoPE (adjacent pairs, Llama-family) and no QK-norm: a pair's two
+ * rows then belong to one workgroup (CUCA_UNSUPPORTED for NEOX).  A row whose
+ * position or slot is bad keeps Q unrotated and stores no K/V, and is
+ * reported by cuca_hip_check_device. */
+cuca_status cuca_hip_qmm_rope_store_kv(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type, int64_t k,
+                                       const void *x, int64_t ldx, int64_t m, int32_t nq, int32_t nk,
+                                       int32_t head_dim, int32_t n_dims, cuca_rope_kind kind,
+                                       const float *cos, const float *sin, int64_t table_rows,
+                                       const int32_t *positions, void *q_out, int64_t q_ld,
+                                       void *pool_k, void *pool_v, int64_t n_blocks,
+                                       const int32_t *slots, cuca_dtype dtype);
 
 /* The dense FFN's gate and up projections with the gated activation fused in
  * (FfnWeights::forward GateUp::Split + Glu::apply, cpu.rs:342-371,

@@ -362,6 +362,31 @@ extern "C" {
         out_ld: i64,
         dtype: cuca_dtype,
     ) -> cuca_status;
+    pub fn cuca_hip_qmm_rope_store_kv(
+        ctx: *mut cuca_hip_ctx,
+        w: *const c_void,
+        ggml_type: u32,
+        k: i64,
+        x: *const c_void,
+        ldx: i64,
+        m: i64,
+        nq: i32,
+        nk: i32,
+        head_dim: i32,
+        n_dims: i32,
+        kind: cuca_rope_kind,
+        cos: *const f32,
+        sin: *const f32,
+        table_rows: i64,
+        positions: *const i32,
+        q_out: *mut c_void,
+        q_ld: i64,
+        pool_k: *mut c_void,
+        pool_v: *mut c_void,
+        n_blocks: i64,
+        slots: *const i32,
+        dtype: cuca_dtype,
+    ) -> cuca_status;
     pub fn cuca_hip_qmm_glu(
         ctx: *mut cuca_hip_ctx,
         gate: *const c_void,

@@ -310,3 +310,87 @@ def test_decode_gemv_streams_chunks_of_tasks(ctx, qtype):
     out = ctx.empty((2, n), np.float32)
     ctx.qmv(w.packed.ptr, QT[qtype], n, k, q.ptr, s.ptr, 2, n, out.ptr, n, hip.F32)
     assert_bits_equal(out.numpy(), want, "streamed chunks, quantised rows")
+
+
+# ---------------------------------------------------------------------------
+# the Q|K|V projection with RoPE and the paged K/V store in its epilogue
+# (cuca_hip_qmm_rope_store_kv): the bits of qmm followed by rope_store_kv
+# ---------------------------------------------------------------------------
+
+def qkv_fused_vs_unfused(ctx, rng, qtype, dtype, nq, nk, d, k, m, n_dims=None, bad_row=None):
+    n_dims = d if n_dims is None else n_dims
+    n = (nq + 2 * nk) * d
+    raw, w = weight(ctx, rng, qtype, n, k)
+    x = awkward(rng, m, k, huge=1e30 if dtype == "f32" else 1e4).astype(NP[dtype])
+    n_blocks = 8 + m
+    cos, sin = hip.rope_tables(hip.ROPE_NORM, n_dims, 5e5, 8192)
+    pos = rng.integers(0, 8192, m).astype(np.int32)
+    slots = rng.permutation(n_blocks * 16)[:m].astype(np.int32)
+    if bad_row is not None:
+        slots[bad_row] = n_blocks * 16 + 3            # outside the pool
+    dcos, dsin, dpos, dslots = ctx.array(cos), ctx.array(sin), ctx.array(pos), ctx.array(slots)
+    dx = ctx.array(x)
+    init = rng.standard_normal((n_blocks, nk, 16, d)).astype(NP[dtype])
+    # unfused: qmm into a [m, n] Q|K|V buffer, then rope_store_kv reading it in place
+    pool = ops.KvPool(ctx, n_blocks, nk, d, NP[dtype])
+    pool.k.upload(init)
+    pool.v.upload(init)
+    qkv = w.forward(dx)
+    es = np.dtype(NP[dtype]).itemsize
+    ctx.rope_store_kv(qkv.ptr, n, qkv.ptr + nq * d * es, n, qkv.ptr + (nq + nk) * d * es, n, m, nq, nk, d,
+                      n_dims, hip.ROPE_NORM, dcos.ptr, dsin.ptr, 8192, dpos.ptr, None, None, 0, 1e-6,
+                      pool.k.ptr, pool.v.ptr, n_blocks, dslots.ptr, hip.dtype_code(NP[dtype]))
+    if bad_row is not None:
+        with pytest.raises(hip.CucaError, match="K/V slot"):
+            ctx.check_device()
+    ctx.check_device()
+    want_q, want_k, want_v = qkv.numpy()[:, :nq * d], pool.k.numpy(), pool.v.numpy()
+    # fused
+    fpool = ops.KvPool(ctx, n_blocks, nk, d, NP[dtype])
+    fpool.k.upload(init)
+    fpool.v.upload(init)
+    q_out = ctx.empty((m, nq * d), NP[dtype])
+    ctx.qmm_rope_store_kv(w.packed.ptr, QT[qtype], k, dx.ptr, k, m, nq, nk, d, n_dims, hip.ROPE_NORM,
+                          dcos.ptr, dsin.ptr, 8192, dpos.ptr, q_out.ptr, nq * d, fpool.k.ptr, fpool.v.ptr,
+                          n_blocks, dslots.ptr, hip.dtype_code(NP[dtype]))
+    if bad_row is not None:
+        with pytest.raises(hip.CucaError, match="K/V slot"):
+            ctx.check_device()
+    ctx.check_device()
+    assert_bits_equal(q_out.numpy(), want_q, "fused q")
+    assert_bits_equal(fpool.k.numpy(), want_k, "fused pool k")
+    assert_bits_equal(fpool.v.numpy(), want_v, "fused pool v")
+    return raw, x, pos, slots, cos, sin, q_out.numpy(), fpool
+
+
+@pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("dtype", ["f32", "f16"])
+@pytest.mark.parametrize("nq,nk,d,k,m", [(32, 8, 128, 4096, 1), (32, 8, 128, 4096, 2), (32, 8, 128, 4096, 5),
+                                         (4, 2, 64, 512, 3), (6, 2, 16, 256, 1)])
+def test_qkv_rope_store_fused_is_qmm_then_rope_store(ctx, qtype, dtype, nq, nk, d, k, m):
+    rng = np.random.default_rng(nq + nk + d + k + m)
+    qkv_fused_vs_unfused(ctx, rng, qtype, dtype, nq, nk, d, k, m)
+
+
+def test_qkv_rope_store_fused_partial_rotary_bad_slot_and_oracle(ctx):
+    rng = np.random.default_rng(77)
+    # partial rotary: values past n_dims pass through
+    qkv_fused_vs_unfused(ctx, rng, "q4_0", "f32", 4, 2, 64, 512, 2, n_dims=32)
+    # a bad slot: the row keeps Q unrotated and stores no K/V, reported
+    qkv_fused_vs_unfused(ctx, rng, "q8_0", "f32", 4, 2, 32, 256, 3, bad_row=1)
+    # against the oracle directly: qmm, then store_kv
+    nq, nk, d, k, m = 4, 2, 32, 256, 3
+    raw, x, pos, slots, cos, sin, got_q, fpool = qkv_fused_vs_unfused(ctx, rng, "q4_0", "f32", nq, nk, d, k, m)
+    n = (nq + 2 * nk) * d
+    y = O.qmm(raw, hip.GGML_Q4_0, n, k, x, rows=n, threads=4)
+    wq = O.rope(y[:, :nq * d].reshape(m, nq, d), cos, sin, pos, O.ROPE_NORM)
+    assert_bits_equal(got_q.reshape(m, nq, d), wq, "oracle q")
+    wk = O.rope(y[:, nq * d:(nq + nk) * d].reshape(m, nk, d), cos, sin, pos, O.ROPE_NORM)
+    pk = fpool.k.numpy()
+    for j in range(m):
+        b, r = slots[j] // 16, slots[j] % 16
+        assert_bits_equal(pk[b, :, r], wk[j], "oracle pool k")
+    with pytest.raises(hip.CucaError, match="only NORM"):
+        ctx.qmm_rope_store_kv(fpool.k.ptr, hip.GGML_Q4_0, k, fpool.k.ptr, k, m, nq, nk, d, d, hip.ROPE_NEOX,
+                              fpool.k.ptr, fpool.k.ptr, 8192, fpool.k.ptr, fpool.k.ptr, nq * d, fpool.k.ptr,
+                              fpool.v.ptr, 8, fpool.k.ptr, hip.F32)
