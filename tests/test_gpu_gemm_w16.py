@@ -9,8 +9,9 @@ cuca_hip_gemm_w16, cuca_hip_gemm_w16_glu) through the C ABI.
   the same bar against the f64 product of the oracle's dequantised weights:
       |got - want| <= (2^-10 + k 2^-24) sum_i |w_i x_i|   (+ 2^-11 |want| for f16 output)
   and for the GLU the same bounds carried through act(g) * u.
-Covers Q4_0 / Q8_0, f32 / f16 activations, 1 to 512 rows, weight-row
-prefixes, a row stride wider than k, repeated calls, and the host's checks.
+Covers Q4_0 / Q8_0, f32 / f16 activations, 1 to 2048 rows (ragged tails of
+rows and columns), weight-row prefixes, a row stride wider than k, repeated
+calls, and the host's checks.
 """
 import numpy as np
 import pytest
@@ -54,7 +55,7 @@ def test_dequant_is_bit_exact(ctx, qtype, n, k):
 @pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
 @pytest.mark.parametrize("n,k,m", [(130, 512, 1), (257, 768, 33), (300, 2048, 64), (96, 4096, 200),
-                                   (512, 1024, 512)])
+                                   (512, 1024, 512), (300, 512, 1100), (520, 256, 2048)])
 def test_gemm_within_the_bound(ctx, qtype, dtype, n, k, m):
     rng = np.random.default_rng(n * 7 + k + m)
     raw = W.quant_table(rng, n, k, qtype, (0.004, 0.03))
@@ -82,7 +83,7 @@ def test_gemm_within_the_bound(ctx, qtype, dtype, n, k, m):
 @pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
 @pytest.mark.parametrize("act,clamp", [(hip.ACT_SILU, 0.0), (hip.ACT_GELU_TANH, 0.0), (hip.ACT_SILU, 3.0)])
-@pytest.mark.parametrize("m,ff", [(7, 160), (256, 160), (9, 162)])
+@pytest.mark.parametrize("m,ff", [(7, 160), (256, 160), (9, 162), (1030, 200)])
 def test_gemm_glu_within_the_bound(ctx, qtype, dtype, act, clamp, m, ff):
     k = 1536
     rng = np.random.default_rng(m + act * 10 + int(clamp))
