@@ -8,9 +8,10 @@ per-layer non-matmul microseconds at decode.
 
 Workload (config.workload): the Llama-3-8B layer ops.  One step is one pass
 of the hot path over one batch of 4096 prefill tokens with f16 activations
-(configs[2] at its smaller size): the Q8_0 embedding gather of the batch,
-the attention-side residual add + RMSNorm, RoPE on Q 32x128 / K 8x128, the
-SwiGLU over F 14336, and the FFN-side residual add + RMSNorm.  `value` is
+(configs[2] at its smaller size): the Q8_0 embedding gather of the batch
+fused with the first block's attention RMSNorm (x and h in one pass), a
+block's attention-side residual add + RMSNorm, RoPE on Q 32x128 / K 8x128,
+the SwiGLU over F 14336, and the FFN-side residual add + RMSNorm.  `value` is
 the algorithmic bytes of a step divided by its time (K steps between two HIP
 events, synchronized on both sides), with every input resident in HBM
 (synthetic data generated on the device).  The decode figure
@@ -19,7 +20,7 @@ batch 1 and 32 in f32, 32 layers captured in one hipGraph and
 replayed, in microseconds per layer.
 
 Algorithmic bytes per unit (s = bytes per activation, H 4096, F 14336):
-  embed       34 H/32 + 4 + s H        per token (block bytes, id, output)
+  embed_rms   34 H/32 + 4 + 2 s H      per token (block bytes, id, x and h out)
   add_rmsnorm 4 s H                    per row   (x, branch in; x', h out)
   rope        2 s (nq + nk) D + 4 D    per row   (Q, K in and out; cos+sin)
   glu         3 s F                    per row   (gate, up in; out)
@@ -57,7 +58,7 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-STEP_OPS = ("embed", "add_rmsnorm_attn", "rope", "glu", "add_rmsnorm_ffn")
+STEP_OPS = ("embed_rms", "add_rmsnorm_attn", "rope", "glu", "add_rmsnorm_ffn")
 
 
 class LayerStep:
@@ -120,10 +121,13 @@ class LayerStep:
             self.rows_glu = n
             self.gu = act(n, 2 * F)
         self.out = torch.empty((self.rows_glu, F), device=dev, dtype=tdt)
+        # the first block's attention norm, fused with the gather
+        self.emb_h = torch.empty((n, H), device=dev, dtype=tdt)
+        self.emb_w = gamma(H)
         bb = 18 if cfg["qtype"] == "q4_0" else 34
         nw = 2 if cfg.get("sandwich") else 1
         self.bytes = {
-            "embed": n * (bb * H // 32 + 4 + s * H),
+            "embed_rms": n * (bb * H // 32 + 4 + 2 * s * H) + 4 * H,
             "add_rmsnorm_attn": n * 4 * s * H + nw * 4 * H,
             "rope": n * (2 * s * (nq + nk) * d + 4 * d) + (8 * d if cfg.get("qk_norm") else 0),
             "glu": self.rows_glu * 3 * s * F,
@@ -134,9 +138,10 @@ class LayerStep:
         c, hip, cfg, n, dt = self.ctx, self.hip, self.cfg, self.n, self.dt
         H, F, d, nq, nk = cfg["hidden"], cfg["ff"], cfg["head_dim"], cfg["nq"], cfg["nk"]
         es = 2 if dt == hip.F16 else 4
-        if name == "embed":
-            c.embed_gguf(self.table.data_ptr(), self.qtype, cfg["vocab"], H, self.ids.data_ptr(), n,
-                         cfg["embd_scale"], self.emb.data_ptr(), dt)
+        if name == "embed_rms":
+            c.embed_gguf_rms(self.table.data_ptr(), self.qtype, cfg["vocab"], H, self.ids.data_ptr(), n,
+                             cfg["embd_scale"], self.emb_w.data_ptr(), cfg["eps"], self.emb.data_ptr(),
+                             self.emb_h.data_ptr(), dt)
         elif name.startswith("add_rmsnorm"):
             b = self.norm[0 if name.endswith("attn") else 1]
             c.add_rmsnorm(b["x"].data_ptr(), b["b"].data_ptr(), b["w"].data_ptr(),
@@ -206,6 +211,8 @@ class LayerStep:
         want = O.embed(sub, self.qtype, s.size, H, np.arange(s.size, dtype=np.uint32),
                        cfg["embd_scale"], out_dtype=npdt)
         assert np.array_equal(host(self.emb).view(np.uint8), want.view(np.uint8)), "embed"
+        _, wh = O.add_rmsnorm(want, None, self.emb_w.cpu().numpy(), cfg["eps"], write_x=False)
+        close(host(self.emb_h), wh, "embed h")
         for b in self.norm:
             x, br = host(b["x"]), host(b["b"])
             wp = None if b["wp"] is None else b["wp"].cpu().numpy()
@@ -1158,6 +1165,8 @@ def cpu_baseline(st, seconds=12.0):
 
     table, ids = host(st.table), host(st.ids).astype(np.uint32)
     emb = np.empty((n, H), npdt)
+    emb_h = np.empty((n, H), npdt)
+    emb_w = host(st.emb_w)
     bad = ctypes.c_int64(-1)
     norm = [dict(x=host(b["x"]), b=host(b["b"]), w=host(b["w"]), xo=np.empty((n, H), npdt),
                  h=np.empty((n, H), npdt)) for b in st.norm]
@@ -1169,9 +1178,11 @@ def cpu_baseline(st, seconds=12.0):
     act = O.GELU_TANH if st.act == st.hip.ACT_GELU_TANH else O.SILU
     es = 2 if f16 else 4
 
-    def embed():
+    def embed_rms():
         L.oracle_embed(ptr(table), st.qtype, cfg["vocab"], H, ptr(ids), n, cfg["embd_scale"], ptr(emb), dt,
                        threads, ctypes.byref(bad))
+        L.oracle_add_rmsnorm(ptr(emb), None, ptr(emb_w), None, cfg["eps"], cfg["eps"], 1.0, n, H, None,
+                             ptr(emb_h), dt, threads)
 
     def add_rmsnorm(b):
         return lambda: L.oracle_add_rmsnorm(ptr(b["x"]), ptr(b["b"]), ptr(b["w"]), None, cfg["eps"],
@@ -1186,7 +1197,7 @@ def cpu_baseline(st, seconds=12.0):
     def glu():
         L.oracle_glu(ptr(gu), 2 * F, gu.ctypes.data + F * es, 2 * F, n, F, act, 0.0, ptr(out), F, dt, threads)
 
-    fns = {"embed": embed, "add_rmsnorm_attn": add_rmsnorm(norm[0]), "rope": rope, "glu": glu,
+    fns = {"embed_rms": embed_rms, "add_rmsnorm_attn": add_rmsnorm(norm[0]), "rope": rope, "glu": glu,
            "add_rmsnorm_ffn": add_rmsnorm(norm[1])}
     ops, total_s, calls = {}, 0.0, 0
     for name, fn in fns.items():
@@ -1399,8 +1410,8 @@ def main():
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic (device-generated, seeded)",
-        "config": {"workload": "llama3-8b layer ops: prefill step (embed Q8_0, add_rmsnorm x2, "
-                               "rope, swiglu) + decode graph",
+        "config": {"workload": "llama3-8b layer ops: prefill step (embed Q8_0 + first-block rmsnorm, "
+                               "add_rmsnorm x2, rope, swiglu) + decode graph",
                    "tokens": args.tokens, "hidden": 4096, "ff": 14336, "heads": "32q/8k x 128",
                    "activations": "f16 (decode: f32)", "bytes_per_step": step_bytes},
         "hbm_frac": round(value / HBM_PEAK_GBS, 4),

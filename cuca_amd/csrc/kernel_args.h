@@ -37,6 +37,10 @@ typedef struct {
     int32_t n;
     float scale;
     float norm_eps;         /* the _norm kernels: rms_norm_rows' eps       */
+    void *h_out;            /* the _rms kernels: [n, hidden] rms(x, w)     */
+    const float *rms_w;     /* the _rms kernels: [hidden] or NULL          */
+    float rms_eps;          /* the _rms kernels                            */
+    int32_t pad_;
 } EmbedArgs;
 
 typedef struct {

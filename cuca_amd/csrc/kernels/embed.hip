@@ -213,6 +213,215 @@ __device__ static inline void embed_norm_body(const EmbedArgs &a) {
     }
 }
 
+// The gather fused with the first block's attention norm (cpu.rs:2670-2673:
+// h = rms(x, attn_norm, eps) over the block's input, which for the first
+// block is the gathered row): x is stored as the plain gather stores it
+// (bit-identical), and h = x * (1 / sqrt(mean(x^2) + eps)) * w is computed
+// from the stored values -- what the norm kernel would read back -- in the
+// norm kernel's form, each product rounded to f32 before the store rounds
+// it.  The sum of squares is the wave's own order (per lane in unit order,
+// then a butterfly): within the norm's bar of the reference, not its bits.
+// The weights are read while the token id is in flight; a row of more than
+// one round re-reads the table row (in cache) for h.
+template <int QT, typename OutT, int UPL>
+__device__ static inline void embed_rms_body(const EmbedArgs &a) {
+    const int tok = blockIdx.x * (CUCA_BLOCK / CUCA_WAVE) + (int)(threadIdx.x / CUCA_WAVE);
+    const int lane = threadIdx.x & (CUCA_WAVE - 1);
+    if (tok >= a.n) return; // whole wave
+    const int nu = a.hidden / 8;
+    OutT *orow = reinterpret_cast<OutT *>(a.out) + (int64_t)tok * a.hidden;
+    OutT *hrow = reinterpret_cast<OutT *>(a.h_out) + (int64_t)tok * a.hidden;
+    const uint32_t id = a.ids[tok];
+    const bool one_round = nu <= CUCA_WAVE * UPL;
+    // up to 4 units per lane the weights are read up front (64 more
+    // registers at 8 units would cost half the waves)
+    constexpr bool PRE = UPL <= 4;
+    float wv[UPL][8];
+    if (PRE && one_round && a.rms_w) {
+#pragma unroll
+        for (int k = 0; k < UPL; k++) {
+            int u = lane + CUCA_WAVE * k;
+            u = u < nu ? u : 0;
+            const f32x4 *wp = reinterpret_cast<const f32x4 *>(a.rms_w) + 2 * u;
+            const f32x4 w0 = wp[0], w1 = wp[1];
+            wv[k][0] = w0.x; wv[k][1] = w0.y; wv[k][2] = w0.z; wv[k][3] = w0.w;
+            wv[k][4] = w1.x; wv[k][5] = w1.y; wv[k][6] = w1.z; wv[k][7] = w1.w;
+        }
+    }
+    if ((int64_t)id >= a.vocab) {
+        embed_bad_id<OutT>(a, orow, tok, id, lane);
+        float z[Chunk<OutT>::N];
+#pragma unroll
+        for (int i = 0; i < Chunk<OutT>::N; i++) z[i] = 0.0f;
+        constexpr int CPU = 8 / Chunk<OutT>::N;
+        for (int c = lane; c < nu * CPU; c += CUCA_WAVE) Chunk<OutT>::store_nt(hrow, c, z);
+        return;
+    }
+    const uint16_t *s16 = reinterpret_cast<const uint16_t *>(a.table + (int64_t)id * a.row_bytes);
+    float v[UPL][8];
+    float ss = 0.0f;
+    for (int u0 = 0; u0 < nu; u0 += CUCA_WAVE * UPL) {
+        uint32_t dq[UPL], w[UPL][4];
+        embed_load<QT, UPL>(s16, u0, lane, nu, dq, w);
+#pragma unroll
+        for (int k = 0; k < UPL; k++) {
+            const int u = u0 + lane + CUCA_WAVE * k;
+            embed_dequant<QT>(u, dq[k], w[k], a.scale, v[k]);
+            if (u < nu) {
+                embed_store<OutT>(orow, u, v[k]);
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    v[k][j] = Chunk<OutT>::as_stored(v[k][j]);
+                    ss += v[k][j] * v[k][j];
+                }
+            }
+        }
+    }
+    ss = group_sum<CUCA_WAVE>(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)a.hidden + a.rms_eps);
+    for (int u0 = 0; u0 < nu; u0 += CUCA_WAVE * UPL) {
+        if (!one_round) {
+            uint32_t dq[UPL], w[UPL][4];
+            embed_load<QT, UPL>(s16, u0, lane, nu, dq, w);
+#pragma unroll
+            for (int k = 0; k < UPL; k++) {
+                embed_dequant<QT>(u0 + lane + CUCA_WAVE * k, dq[k], w[k], a.scale, v[k]);
+#pragma unroll
+                for (int j = 0; j < 8; j++) v[k][j] = Chunk<OutT>::as_stored(v[k][j]);
+            }
+        }
+        if ((!one_round || !PRE) && a.rms_w) {
+            {
+#pragma unroll
+                for (int k = 0; k < UPL; k++) {
+                    int u = u0 + lane + CUCA_WAVE * k;
+                    u = u < nu ? u : 0;
+                    const f32x4 *wp = reinterpret_cast<const f32x4 *>(a.rms_w) + 2 * u;
+                    const f32x4 w0 = wp[0], w1 = wp[1];
+                    wv[k][0] = w0.x; wv[k][1] = w0.y; wv[k][2] = w0.z; wv[k][3] = w0.w;
+                    wv[k][4] = w1.x; wv[k][5] = w1.y; wv[k][6] = w1.z; wv[k][7] = w1.w;
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < UPL; k++) {
+            const int u = u0 + lane + CUCA_WAVE * k;
+            float y[8];
+            if (a.rms_w) {
+#pragma unroll
+                for (int j = 0; j < 8; j++) y[j] = pin_f32(pin_f32(v[k][j] * inv) * wv[k][j]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; j++) y[j] = pin_f32(v[k][j] * inv);
+            }
+            if (u < nu) embed_store<OutT>(hrow, u, y);
+        }
+    }
+}
+
+// The same with a workgroup per token: TPR threads (a power of two, 64 to
+// 1024), thread t owning units t, t + TPR, ... (NU of them), the sum of
+// squares a butterfly per wave and an LDS sum over the waves in wave order.
+// Each thread holds one or two units, so many tokens are in flight per CU.
+template <int QT, typename OutT, int TPR, int NU>
+__device__ static inline void embed_rms_tpr_body(const EmbedArgs &a) {
+    constexpr int NW = TPR / CUCA_WAVE;
+    __shared__ float red[NW];
+    const int tok = blockIdx.x;
+    const int t = threadIdx.x, lane = t & (CUCA_WAVE - 1), wave = t / CUCA_WAVE;
+    const int nu = a.hidden / 8;
+    OutT *orow = reinterpret_cast<OutT *>(a.out) + (int64_t)tok * a.hidden;
+    OutT *hrow = reinterpret_cast<OutT *>(a.h_out) + (int64_t)tok * a.hidden;
+    const uint32_t id = a.ids[tok];
+    float wv[NU][8];
+    if (a.rms_w) {
+#pragma unroll
+        for (int k = 0; k < NU; k++) {
+            int u = t + TPR * k;
+            u = u < nu ? u : 0;
+            const f32x4 *wp = reinterpret_cast<const f32x4 *>(a.rms_w) + 2 * u;
+            const f32x4 w0 = wp[0], w1 = wp[1];
+            wv[k][0] = w0.x; wv[k][1] = w0.y; wv[k][2] = w0.z; wv[k][3] = w0.w;
+            wv[k][4] = w1.x; wv[k][5] = w1.y; wv[k][6] = w1.z; wv[k][7] = w1.w;
+        }
+    }
+    constexpr int CPU = 8 / Chunk<OutT>::N;
+    if ((int64_t)id >= a.vocab) { // uniform over the workgroup
+        if (t == 0) record_bad(a.status + CUCA_STATUS_EMBED_ID, (uint32_t)tok, id);
+        float z[Chunk<OutT>::N];
+#pragma unroll
+        for (int i = 0; i < Chunk<OutT>::N; i++) z[i] = 0.0f;
+        for (int c = t; c < nu * CPU; c += TPR) {
+            Chunk<OutT>::store_nt(orow, c, z);
+            Chunk<OutT>::store_nt(hrow, c, z);
+        }
+        return;
+    }
+    const uint16_t *s16 = reinterpret_cast<const uint16_t *>(a.table + (int64_t)id * a.row_bytes);
+    uint32_t dq[NU], w[NU][4];
+#pragma unroll
+    for (int k = 0; k < NU; k++) {
+        uint32_t d1[1], w1[1][4];
+        embed_load<QT, 1>(s16, TPR * k + (t - lane), lane, nu, d1, w1);
+        dq[k] = d1[0];
+#pragma unroll
+        for (int j = 0; j < 4; j++) w[k][j] = w1[0][j];
+    }
+    float v[NU][8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NU; k++) {
+        const int u = t + TPR * k;
+        embed_dequant<QT>(u, dq[k], w[k], a.scale, v[k]);
+        if (u < nu) {
+            embed_store<OutT>(orow, u, v[k]);
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                v[k][j] = Chunk<OutT>::as_stored(v[k][j]);
+                ss += v[k][j] * v[k][j];
+            }
+        }
+    }
+    ss = group_sum<CUCA_WAVE>(ss);
+    if (NW > 1) {
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NW; i++) ss += red[i];
+    }
+    const float inv = 1.0f / sqrtf(ss / (float)a.hidden + a.rms_eps);
+#pragma unroll
+    for (int k = 0; k < NU; k++) {
+        const int u = t + TPR * k;
+        float y[8];
+        if (a.rms_w) {
+#pragma unroll
+            for (int j = 0; j < 8; j++) y[j] = pin_f32(pin_f32(v[k][j] * inv) * wv[k][j]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) y[j] = pin_f32(v[k][j] * inv);
+        }
+        if (u < nu) embed_store<OutT>(hrow, u, y);
+    }
+}
+
+#define CUCA_EMBED_TPR(NAME, QT, OUT, TPR, NU)                                             \
+    extern "C" __global__ __launch_bounds__(TPR) void NAME(EmbedArgs a) {                  \
+        embed_rms_tpr_body<QT, OUT, TPR, NU>(a);                                           \
+    }
+#define CUCA_EMBED_TPR_SET(NAME, QT, OUT)                                                  \
+    CUCA_EMBED_TPR(NAME##_rms_t64, QT, OUT, 64, 1)                                         \
+    CUCA_EMBED_TPR(NAME##_rms_t128, QT, OUT, 128, 1)                                       \
+    CUCA_EMBED_TPR(NAME##_rms_t256, QT, OUT, 256, 1)                                       \
+    CUCA_EMBED_TPR(NAME##_rms_t512, QT, OUT, 512, 1)                                       \
+    CUCA_EMBED_TPR(NAME##_rms_t1024, QT, OUT, 1024, 1)                                     \
+    CUCA_EMBED_TPR(NAME##_rms_t1024_c2, QT, OUT, 1024, 2)
+CUCA_EMBED_TPR_SET(cuca_embed_q4_0_f32, 2, float)
+CUCA_EMBED_TPR_SET(cuca_embed_q4_0_f16, 2, _Float16)
+CUCA_EMBED_TPR_SET(cuca_embed_q8_0_f32, 8, float)
+CUCA_EMBED_TPR_SET(cuca_embed_q8_0_f16, 8, _Float16)
+
 #define CUCA_EMBED(NAME, BODY, QT, OUT, UPL)                                               \
     extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void NAME(EmbedArgs a) {           \
         BODY<QT, OUT, UPL>(a);                                                             \
@@ -225,7 +434,11 @@ __device__ static inline void embed_norm_body(const EmbedArgs &a) {
     CUCA_EMBED(NAME##_norm_u1, embed_norm_body, QT, OUT, 1)                                \
     CUCA_EMBED(NAME##_norm_u2, embed_norm_body, QT, OUT, 2)                                \
     CUCA_EMBED(NAME##_norm_u4, embed_norm_body, QT, OUT, 4)                                \
-    CUCA_EMBED(NAME##_norm_u8, embed_norm_body, QT, OUT, 8)
+    CUCA_EMBED(NAME##_norm_u8, embed_norm_body, QT, OUT, 8)                                \
+    CUCA_EMBED(NAME##_rms_u1, embed_rms_body, QT, OUT, 1)                                  \
+    CUCA_EMBED(NAME##_rms_u2, embed_rms_body, QT, OUT, 2)                                  \
+    CUCA_EMBED(NAME##_rms_u4, embed_rms_body, QT, OUT, 4)                                  \
+    CUCA_EMBED(NAME##_rms_u8, embed_rms_body, QT, OUT, 8)
 
 CUCA_EMBED_SET(cuca_embed_q4_0_f32, 2, float)
 CUCA_EMBED_SET(cuca_embed_q4_0_f16, 2, _Float16)

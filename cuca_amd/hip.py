@@ -59,6 +59,7 @@ SIGNATURES = {
     "cuca_hip_check_device": (_st, [_p]),
     "cuca_hip_embed_gguf": (_st, [_p, _p, _u32, _i64, _i64, _p, _i64, _f32, _p, _st]),
     "cuca_hip_embed_gguf_norm": (_st, [_p, _p, _u32, _i64, _i64, _p, _i64, _f32, _f32, _p, _st]),
+    "cuca_hip_embed_gguf_rms": (_st, [_p, _p, _u32, _i64, _i64, _p, _i64, _f32, _p, _f32, _p, _p, _st]),
     "cuca_hip_add_rmsnorm": (_st, [_p, _p, _p, _p, _p, _f32, _f32, _f32, _i64, _i64, _p, _p, _st]),
     "cuca_hip_glu": (_st, [_p, _p, _i64, _p, _i64, _i64, _i64, _st, _f32, _p, _i64, _st]),
     "cuca_hip_glu_ragged": (_st, [_p, _p, _i64, _p, _i64, _p, _i32, _i64, _i64, _st, _f32, _p,
@@ -320,6 +321,11 @@ class Context:
                         out_dtype):
         self.check(self.L.cuca_hip_embed_gguf_norm(self.ptr, table, ggml_type, vocab, hidden, ids,
                                                    n, scale, norm_eps, out, out_dtype))
+
+    def embed_gguf_rms(self, table, ggml_type, vocab, hidden, ids, n, scale, w, eps, x_out, h_out,
+                       out_dtype):
+        self.check(self.L.cuca_hip_embed_gguf_rms(self.ptr, table, ggml_type, vocab, hidden, ids, n,
+                                                  scale, w, eps, x_out, h_out, out_dtype))
 
     def add_rmsnorm(self, x, branch, w, w_post, eps, post_eps, residual_scale, rows, hidden,
                     x_out, h_out, dtype):

@@ -75,6 +75,25 @@ class TokenEmbedding:
         self.rows_device(dev_ids, scale, out, norm_eps)
         return out
 
+    def rows_rms(self, tokens, scale, weight, eps, out_dtype=np.float32):
+        """The gather fused with the first block's attention norm: returns
+        (x, h), x the embedding rows of `tokens` times `scale` (as rows()),
+        h = rms(x, weight, eps) (Transformer::block, cpu.rs:2670-2673).
+        weight None is the weightless norm."""
+        ids = np.asarray(tokens, dtype=np.int64).reshape(-1)
+        for i in ids:  # quant.rs:395-400, before anything runs
+            if i < 0 or i >= self.rows_n:
+                raise CucaError(hip.OUT_OF_RANGE, f"token id {int(i)} outside the embedding table "
+                                f"of {self.rows_n} rows")
+        dev_ids = self.ctx.array(ids.astype(np.uint32))
+        x = self.ctx.empty((ids.size, self.row_len), out_dtype)
+        h = self.ctx.empty((ids.size, self.row_len), out_dtype)
+        w = _w(self.ctx, weight)
+        self.ctx.embed_gguf_rms(self.table.ptr, self.dtype, self.rows_n, self.row_len, dev_ids.ptr,
+                                ids.size, scale, None if w is None else w.ptr, eps, x.ptr, h.ptr,
+                                hip.dtype_code(out_dtype))
+        return x, h
+
     def rows_device(self, ids, scale, out, norm_eps=None):
         """The gather for ids already on the device (u32 DeviceArray); bad ids
         are reported by ctx.check_device()."""

@@ -168,6 +168,21 @@ cuca_status cuca_hip_embed_gguf_norm(cuca_hip_ctx *ctx, const void *table, uint3
                                      int64_t n, float scale, float norm_eps, void *out,
                                      cuca_dtype out_dtype);
 
+/* The gather fused with the first block's attention norm: TokenEmbedding::rows
+ * (quant.rs:391-411) into x_out, then h = rms(x, w, eps) (Transformer::block's
+ * first step, cpu.rs:2670-2673, whose input for the first block is the
+ * gathered rows) into h_out, in one pass.  x_out is bit-identical to
+ * cuca_hip_embed_gguf's output; h is computed from x as stored, as
+ * cuca_hip_add_rmsnorm with branch == NULL would, and meets the same bar
+ * (the sum of squares is summed in this kernel's own order).  w == NULL is
+ * the weightless norm.  x_out, h_out: [n, hidden] of out_dtype, 16-byte
+ * aligned; w: f32[hidden], 16-byte aligned.  Bad ids: as cuca_hip_embed_gguf,
+ * with zero rows in both outputs. */
+cuca_status cuca_hip_embed_gguf_rms(cuca_hip_ctx *ctx, const void *table, uint32_t ggml_type,
+                                    int64_t vocab, int64_t hidden, const uint32_t *ids, int64_t n,
+                                    float scale, const float *w, float eps, void *x_out,
+                                    void *h_out, cuca_dtype out_dtype);
+
 /* Fused residual add + RMSNorm (Transformer::block, cpu.rs:2650-2711, with
  * rms = candle_nn::ops::rms_norm, cpu.rs:3652; GPU attn_tail / ffn_half /
  * ffn_tail, gpu.rs:5420-5483):

@@ -143,6 +143,21 @@ extern "C" {
         out: *mut c_void,
         out_dtype: cuca_dtype,
     ) -> cuca_status;
+    pub fn cuca_hip_embed_gguf_rms(
+        ctx: *mut cuca_hip_ctx,
+        table: *const c_void,
+        ggml_type: u32,
+        vocab: i64,
+        hidden: i64,
+        ids: *const u32,
+        n: i64,
+        scale: f32,
+        w: *const f32,
+        eps: f32,
+        x_out: *mut c_void,
+        h_out: *mut c_void,
+        out_dtype: cuca_dtype,
+    ) -> cuca_status;
     pub fn cuca_hip_add_rmsnorm(
         ctx: *mut cuca_hip_ctx,
         x: *const c_void,

@@ -206,3 +206,109 @@ def test_embed_norm_full_table_sampled_rows(ctx):
     want = O.embed(sub, O.Q4_0, s.size, cfg["hidden"], np.arange(s.size, dtype=np.uint32), 1.0,
                    out_dtype=np.float16, norm_eps=1e-6)
     assert_bits_equal(out[st].cpu().numpy(), want, "full table + norm")
+
+
+# The gather fused with the first block's attention norm
+# (cuca_hip_embed_gguf_rms): x bit-identical to the plain gather (the
+# oracle's TokenEmbedding::rows), h = rms(x, w, eps) within the norm's bar
+# (1e-5 relative in f32, 2 f16 ulps) of the oracle's norm of that x, and of
+# the separate cuca_hip_add_rmsnorm call.
+@pytest.mark.parametrize("qname", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("out", [np.float32, np.float16])
+@pytest.mark.parametrize("hidden,eps,scale,weighted", [
+    (4096, 1e-5, 1.0, True), (2048, 1e-6, 1.0, True), (3584, 1e-6, float(np.float32(np.sqrt(3584.0))), True),
+    (1024, 1e-6, 1.0, False), (8192 + 96, 1e-5, 0.5, True), (96, 0.0, 2.0, True), (32, 1e-5, 1.0, True),
+    (20000, 1e-6, 1.0, True)])
+def test_embed_rms_matches_gather_then_norm(ctx, qname, out, hidden, eps, scale, weighted):
+    """Rows of 1 to 1024 units take a workgroup per token (one unit per
+    thread), 1025 to 2048 units 1024 threads of two, and wider rows the
+    wave-per-token kernel (several rounds, the row re-read for h)."""
+    from helpers import assert_close
+    rng = np.random.default_rng(hidden * 3 + (qname == "q8_0"))
+    vocab = 300
+    table = W.quant_table(rng, vocab, hidden, qname, (0.001, 0.05))
+    ty = W.GGML_ID[qname]
+    ids = rng.integers(0, vocab, 45).astype(np.uint32)
+    w = (1 + 0.02 * rng.standard_normal(hidden)).astype(np.float32) if weighted else None
+    emb = ops.TokenEmbedding(ctx, ty, table, vocab, hidden)
+    x, h = emb.rows_rms(ids, scale, w, eps, out_dtype=out)
+    x, h = x.numpy(), h.numpy()
+    ctx.check_device()
+    want_x = O.embed(table, ty, vocab, hidden, ids, scale, out_dtype=out)
+    assert_bits_equal(x, want_x, f"embed_rms x {qname} {hidden}")
+    _, want_h = O.add_rmsnorm(want_x, None, w, eps, write_x=False)
+    assert_close(h, want_h, what=f"embed_rms h {qname} {hidden}")
+    # the unfused pair on the device
+    _, h2 = ops.add_rms(ctx.array(want_x), None, w, eps, write_x=False)
+    assert_close(h, h2.numpy(), what="embed_rms h vs add_rmsnorm")
+
+
+@pytest.mark.parametrize("out", [np.float32, np.float16])
+def test_embed_rms_many_tokens_wave_kernel(ctx, out):
+    """More than 8192 tokens take the wave-per-token kernel."""
+    from helpers import assert_close
+    rng = np.random.default_rng(5)
+    vocab, hidden = 64, 256
+    table = W.quant_table(rng, vocab, hidden, "q4_0", (0.001, 0.05))
+    ids = rng.integers(0, vocab, 8200).astype(np.uint32)
+    w = (1 + 0.02 * rng.standard_normal(hidden)).astype(np.float32)
+    emb = ops.TokenEmbedding(ctx, hip.GGML_Q4_0, table, vocab, hidden)
+    x, h = emb.rows_rms(ids, 1.0, w, 1e-6, out_dtype=out)
+    ctx.check_device()
+    want_x = O.embed(table, hip.GGML_Q4_0, vocab, hidden, ids, 1.0, out_dtype=out)
+    assert_bits_equal(x.numpy(), want_x, "wave kernel x")
+    _, want_h = O.add_rmsnorm(want_x, None, w, 1e-6, write_x=False)
+    assert_close(h.numpy(), want_h, what="wave kernel h")
+
+
+def test_embed_rms_bad_id_and_checks(ctx):
+    rng = np.random.default_rng(11)
+    table = W.quant_table(rng, 16, 256, "q8_0", (0.001, 0.05))
+    emb = ops.TokenEmbedding(ctx, hip.GGML_Q8_0, table, 16, 256)
+    ids = ctx.array(np.array([3, 16, 5], np.uint32))
+    x = ctx.empty((3, 256), np.float16)
+    h = ctx.empty((3, 256), np.float16)
+    w = ctx.array(np.ones(256, np.float32))
+    ctx.embed_gguf_rms(emb.table.ptr, hip.GGML_Q8_0, 16, 256, ids.ptr, 3, 1.0, w.ptr, 1e-6, x.ptr, h.ptr,
+                       hip.F16)
+    with pytest.raises(hip.CucaError, match="token id 16 outside the embedding table of 16 rows"):
+        ctx.check_device()
+    assert np.all(x.numpy()[1] == 0) and np.all(h.numpy()[1] == 0)
+    want = O.embed(table, O.Q8_0, 16, 256, np.array([3, 5], np.uint32), 1.0, out_dtype=np.float16)
+    assert_bits_equal(x.numpy()[[0, 2]], want)
+    with pytest.raises(hip.CucaError, match="eps"):
+        ctx.embed_gguf_rms(emb.table.ptr, hip.GGML_Q8_0, 16, 256, ids.ptr, 3, 1.0, w.ptr, -1.0, x.ptr, h.ptr,
+                           hip.F16)
+    with pytest.raises(hip.CucaError, match="null h_out"):
+        ctx.embed_gguf_rms(emb.table.ptr, hip.GGML_Q8_0, 16, 256, ids.ptr, 3, 1.0, w.ptr, 1e-6, x.ptr, None,
+                           hip.F16)
+
+
+def test_embed_rms_full_size_config_c_sampled_rows(ctx):
+    """Config C at 4096 tokens (128256 x 4096 Q8_0 table, f16), sampled rows
+    against the oracle."""
+    torch = pytest.importorskip("torch")
+    from helpers import assert_close
+    cfg = W.CONFIGS["C"]
+    n, H = 4096, cfg["hidden"]
+    gen = torch.Generator(device="cuda").manual_seed(21)
+    table = W.quant_table_torch(gen, cfg["vocab"], H, cfg["qtype"], cfg["d_range"])
+    ids = torch.randint(0, cfg["vocab"], (n,), device="cuda", generator=gen, dtype=torch.int32)
+    w = (1 + 0.02 * torch.randn(H, device="cuda", generator=gen)).float()
+    x = torch.empty((n, H), device="cuda", dtype=torch.float16)
+    h = torch.empty_like(x)
+    torch.cuda.synchronize()
+    ctx.embed_gguf_rms(table.data_ptr(), W.GGML_ID[cfg["qtype"]], cfg["vocab"], H, ids.data_ptr(), n,
+                       cfg["embd_scale"], w.data_ptr(), cfg["eps"], x.data_ptr(), h.data_ptr(), hip.F16)
+    ctx.sync()
+    ctx.check_device()
+    rows = np.array([0, 1, 777, 2048, n - 1])
+    sel = torch.from_numpy(rows).cuda()
+    rb = W.row_bytes(cfg["qtype"], H)
+    ids_np = ids.cpu().numpy().astype(np.uint32)[rows]
+    tab_rows = table.view(cfg["vocab"], rb).index_select(0, torch.from_numpy(ids_np.astype(np.int64)).cuda())
+    want_x = O.embed(tab_rows.cpu().numpy(), W.GGML_ID[cfg["qtype"]], rows.size, H, np.arange(rows.size, dtype=np.uint32),
+                     cfg["embd_scale"], out_dtype=np.float16)
+    assert_bits_equal(x.index_select(0, sel).cpu().numpy(), want_x, "C x")
+    _, want_h = O.add_rmsnorm(want_x, None, w.cpu().numpy(), cfg["eps"], write_x=False)
+    assert_close(h.index_select(0, sel).cpu().numpy(), want_h, what="C h")
