@@ -1006,7 +1006,7 @@ def moe_bench(ctx, torch, reps=30):
     """Routed experts at config E (Qwen3-30B-A3B: 128 experts of ff 768 over
     hidden 2048, Q4_0, top 8): moe_up (gate/up + SwiGLU), moe_down (times the
     routing weight), moe_sum, f32, at decode batches of 1 and 32 tokens with
-    uniform routing.  Algorithmic bytes: the weights of the experts the
+    uniform routing; and at an 8192-token prefill (below).  Algorithmic bytes: the weights of the experts the
     batch touches, the tokens' rows in, the hidden rows out and back in, the
     output rows.  Checked against the oracle's expert_sum to 1e-4 of each
     token's largest |output| (the bar of the layer test)."""
@@ -1054,6 +1054,55 @@ def moe_bench(ctx, torch, reps=30):
                                      frac=round(b / (ms / 1e3) / 1e9 / HBM_PEAK_GBS, 4))
         keep.clear()
         dx.free()
+    # prefill: 8192 tokens of f16 activations, Zipf(1.1) routing (65536
+    # pairs, a few hot experts), the up and down projections as grouped GEMMs
+    # on the matrix cores (cuca_hip_moe_up_qgemm / _down_qgemm) against the
+    # decode GEMV path at the same size.  FLOPs: 2 pairs (2 ff H + H ff).
+    # Checked: four tokens' outputs against their f64 value over the
+    # dequantised weights (1e-2 of the token's largest |output|).
+    t = 8192
+    p = 1.0 / np.arange(1, n_exp + 1) ** 1.1
+    p = p / p.sum()
+    per = [[] for _ in range(n_exp)]
+    for tok in range(t):
+        for e, w in zip(sorted(rng.choice(n_exp, n_used, replace=False, p=p)),
+                        rng.uniform(0.05, 1.0, n_used).astype(np.float32)):
+            per[e].append((tok, float(w)))
+    x = (rng.standard_normal((t, H)) * 0.35).astype(np.float16)
+    dx = ctx.array(x)
+    pairs = t * n_used
+    flops = 2.0 * pairs * (2 * F * H + H * F)
+    for mm, reps_mm in (("qgemm", 10), ("qmm", 2)):
+        keep = []
+
+        def call(i, mm=mm):
+            keep.append(bank.expert_sum(dx, per, ops.Glu(hip.ACT_SILU), n_used, mm=mm))
+            if len(keep) > 2:
+                keep.pop(0)
+        ms, parts = kernel_calls(ctx, call, reps_mm, 1)
+        entry = dict(kernels=[k for k, _ in parts], us=round(ms * 1000, 2),
+                     parts_us=[round(v * 1000, 2) for _, v in parts], pairs=pairs,
+                     max_pairs_per_expert=max(len(q) for q in per),
+                     tflops=round(flops / (ms / 1e3) / 1e12, 1), mfma_frac=round(flops / (ms / 1e3) / 2.5e15, 4))
+        if mm == "qgemm":
+            out = keep[-1][0].numpy()
+            deq = [tuple(np.stack([O.dequant_row(W.GGML_ID[qtype], m[i * W.row_bytes(qtype, k):(i + 1) *
+                                                                     W.row_bytes(qtype, k)], 1.0, k)
+                                   for i in range(n)]).astype(np.float64)
+                         for m, n, k in ((b[0], F, H), (b[1], F, H), (b[2], H, F))) for b in base]
+            for tok in (0, 1, t // 2, t - 1):
+                want = np.zeros(H)
+                for e, picks in enumerate(per):
+                    for tt, w in picks:
+                        if tt == tok:
+                            wg, wu, wd = deq[e % 8]
+                            xr = x[tok].astype(np.float64)
+                            g, u = wg @ xr, wu @ xr
+                            want += (wd @ (g / (1.0 + np.exp(-g)) * u)) * w
+                assert np.all(np.abs(out[tok] - want) <= 1e-2 * np.abs(want).max()), "moe qgemm"
+        res[f"E_prefill_t{t}_{mm}"] = entry
+        keep.clear()
+    dx.free()
     for p in (bank.gate, bank.up, bank.down):
         p.free()
     return res

@@ -187,6 +187,19 @@ typedef struct {
     int32_t rows, m, k, nkc, n_rt, n_ct, kcs, splits;
     float clamp;
     int32_t mp;
+    /* routed experts (the qgemm_moe kernels): expert e's packed matrices at
+     * w (w_up) + e * estride; token tile ct holds pairs [tile_p0[ct],
+     * tile_p0[ct] + tile_n[ct]) of expert tile_e[ct] (-1 past the last
+     * tile), written by cuca_moe_plan from offsets; up: activation row of
+     * pair p = x[pair_token[p]] (m = n_tokens), out = hidden [pairs][out_ld];
+     * down: activation row = x[p] (m = max_pairs), out = f32 scratch
+     * [pairs][out_ld] times pair_weight[p].                                */
+    const int32_t *offsets, *pair_token;
+    const float *pair_weight;
+    int32_t *tile_e, *tile_p0, *tile_n;
+    unsigned long long *status;
+    int64_t estride;
+    int32_t n_experts, max_pairs, tm, moe_up;
 } QGemmArgs;
 
 /* The dense f16 path (qgemm.hip): cuca_qdequant_* (packed w [n][ng][GB],

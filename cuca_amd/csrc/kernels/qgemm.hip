@@ -204,7 +204,7 @@ __device__ static inline void qg_chunk(const QGemmArgs &a, const uint8_t *wg, co
 // writes its f32 sums to the partial rows of the workspace (qgemm_reduce
 // adds the splits in order and applies the epilogue); otherwise the
 // epilogue is applied here.
-template <typename T, int FMT, int TM, bool GLU, int ACT, bool SPLIT>
+template <typename T, int FMT, int TM, bool GLU, int ACT, bool SPLIT, int MOE = 0>
 __device__ static inline void qgemm_body(const QGemmArgs &a) {
     constexpr int NT = TM / 32;
     const int split = SPLIT ? (int)blockIdx.y : 0;
@@ -219,6 +219,15 @@ __device__ static inline void qgemm_body(const QGemmArgs &a) {
     if (gsz <= 0) return;
     const int ct = w / gsz, rt = (8 * g + (w - ct * gsz)) * 8 + xcd;
     if (ct >= a.n_ct) return;
+    // routed experts: the tile's expert and pairs (uniform); tiles past the
+    // last are empty
+    int ex = 0, p0 = 0, np = 0;
+    if (MOE) {
+        ex = a.tile_e[ct];
+        if (ex < 0) return;
+        p0 = a.tile_p0[ct];
+        np = a.tile_n[ct];
+    }
     const int kc0 = split * a.kcs;
     const int kc1 = min(a.nkc, kc0 + a.kcs);
     if (kc0 >= kc1) return;
@@ -227,7 +236,7 @@ __device__ static inline void qgemm_body(const QGemmArgs &a) {
     const int r = lane & 31, h = lane >> 5;
     const int row = rt * QG_ROWS + wave * 32 + r;
     const int tok0 = ct * TM;
-    const int64_t roff = (int64_t)(row < a.rows ? row : 0) * a.row_bytes;
+    const int64_t roff = (int64_t)(row < a.rows ? row : 0) * a.row_bytes + (MOE ? (int64_t)ex * a.estride : 0);
     const uint8_t *wg = a.w + roff;
     const uint8_t *wu = GLU ? a.w_up + roff : nullptr;
 
@@ -273,6 +282,36 @@ __device__ static inline void qgemm_body(const QGemmArgs &a) {
                 if (n >= a.rows) continue;
                 pg[n] = acc[i][q];
                 if (GLU) pu[n] = accu[i][q];
+            }
+        }
+        return;
+    }
+    if (MOE) {
+        // pair p0 + local of the tile: up, act(g) * u into hidden row p; down,
+        // the f32 product times the pair's routing weight into scratch row p
+#pragma unroll
+        for (int i = 0; i < NT; i++) {
+            asm volatile("" : "+a"(acc[i]));
+            if (GLU) asm volatile("" : "+a"(accu[i]));
+            const int local = i * 32 + r;
+            if (local >= np) continue;
+            const int64_t p = p0 + local;
+            const float pw = MOE == 2 ? a.pair_weight[p] : 1.0f;
+#pragma unroll
+            for (int q = 0; q < 16; q++) {
+                const int n = rt * QG_ROWS + wave * 32 + 8 * (q >> 2) + 4 * h + (q & 3);
+                if (n >= a.rows) continue;
+                float o = acc[i][q];
+                if (GLU) {
+                    float gg = o, u = accu[i][q];
+                    if (a.clamp > 0.0f) { // Glu::apply's clamp (cpu.rs:364-368)
+                        gg = fminf(gg, a.clamp);
+                        u = fminf(fmaxf(u, -a.clamp), a.clamp);
+                    }
+                    o = (ACT == 0 ? act_silu(gg) : act_gelu_tanh(gg)) * u;
+                }
+                if (MOE == 2) reinterpret_cast<float *>(a.out)[p * a.out_ld + n] = o * pw;
+                else reinterpret_cast<T *>(a.out)[p * a.out_ld + n] = to_stored<T>(o);
             }
         }
         return;
@@ -324,6 +363,96 @@ template <typename T, bool GLU, int ACT> __device__ static inline void qgemm_red
     reinterpret_cast<T *>(a.out)[(int64_t)tok * a.out_ld + n] = to_stored<T>(o);
 }
 
+// Routed experts: the token tiles of the grouped GEMM.  One workgroup:
+// thread 0 walks the experts (offsets clamped into [0, max_pairs] and made
+// non-decreasing, so no pair index leaves the pair arrays), giving expert e
+// ceil(n_e / tm) tiles from tile ts[e] on; then every tile c < n_ct gets
+// its expert (a binary search over ts), first pair and pair count, or -1
+// past the last tile.
+#define QG_MOE_MAX_EXPERTS 4096
+__device__ static inline void qgemm_moe_plan_body(const QGemmArgs &a) {
+    __shared__ int ts[QG_MOE_MAX_EXPERTS + 1], lo[QG_MOE_MAX_EXPERTS + 1];
+    const int E = a.n_experts, tm = a.tm;
+    if (threadIdx.x == 0) {
+        int prev = 0, t = 0;
+        for (int e = 0; e < E; e++) {
+            int l = a.offsets[e], hh = a.offsets[e + 1];
+            l = min(max(l, prev), a.max_pairs);
+            hh = min(max(hh, l), a.max_pairs);
+            ts[e] = t;
+            lo[e] = l;
+            t += (hh - l + tm - 1) / tm;
+            prev = hh;
+        }
+        ts[E] = t;
+        lo[E] = prev;
+    }
+    __syncthreads();
+    for (int c = threadIdx.x; c < a.n_ct; c += blockDim.x) {
+        if (c >= ts[E]) {
+            a.tile_e[c] = -1;
+            a.tile_p0[c] = 0;
+            a.tile_n[c] = 0;
+            continue;
+        }
+        int l = 0, hh = E - 1; // the last e with ts[e] <= c (experts without pairs share ts)
+        while (l < hh) {
+            const int mid = (l + hh + 1) >> 1;
+            if (ts[mid] <= c) l = mid;
+            else hh = mid - 1;
+        }
+        const int p0 = lo[l] + (c - ts[l]) * tm;
+        const int end = lo[l + 1]; // the clamped end of expert l's pairs
+        a.tile_e[c] = l;
+        a.tile_p0[c] = p0;
+        a.tile_n[c] = min(tm, end - p0);
+    }
+}
+
+// The activation rows of the routed pairs, rewritten as qgemm_prep_body does
+// into the tile layout: padded row ct * tm + i holds pair tile_p0[ct] + i of
+// the tile (zero past tile_n[ct]); up reads row pair_token[p] of x (a token
+// outside [0, m) gives a zero row, reported), down row p.  Tiles past the
+// last are not written (the GEMM skips them).
+template <typename T, int FMT> __device__ static inline void qgemm_moe_prep_body(const QGemmArgs &a) {
+    using F = QgFmt<FMT>;
+    const int64_t u = (int64_t)blockIdx.x * CUCA_BLOCK + threadIdx.x;
+    const int64_t per_row = (int64_t)a.nkc * 16;
+    if (u >= (int64_t)a.mp * per_row) return;
+    const int prow = (int)(u / per_row), rem = (int)(u - (int64_t)prow * per_row);
+    const int ct = prow / a.tm, i = prow - ct * a.tm;
+    if (a.tile_e[ct] < 0) return;
+    const int kc = rem >> 4, v = rem & 15, s = v >> 1, h = v & 1;
+    const int g = kc / F::KCG, part = kc % F::KCG;
+    int base;
+    if (FMT == 0) base = 512 * g + 128 * (2 * h + (s & 1)) + 4 * part + (s >> 1);
+    else base = 256 * g + 128 * h + 8 * part + s;
+    bool valid = i < a.tile_n[ct];
+    int64_t src = 0;
+    if (valid) {
+        const int p = a.tile_p0[ct] + i;
+        if (a.moe_up) {
+            const int tok = a.pair_token[p];
+            if (tok < 0 || tok >= a.m) {
+                valid = false;
+                if (rem == 0) record_bad(a.status + CUCA_STATUS_MOE_PAIR, (uint32_t)p, (uint32_t)tok);
+            } else {
+                src = tok;
+            }
+        } else {
+            src = p;
+        }
+    }
+    const T *row = reinterpret_cast<const T *>(a.x) + src * a.ldx;
+    qg_h8 o;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int k = base + 16 * j;
+        o[j] = valid && k < a.k ? (_Float16)(float)row[k] : (_Float16)0.0f;
+    }
+    *reinterpret_cast<qg_h8 *>(a.xp + (int64_t)prow * a.kp + (int64_t)kc * QG_KC + 8 * (2 * s + h)) = o;
+}
+
 #define CUCA_QGEMM(NAME, BODY, ...)                                                        \
     extern "C" __global__ __launch_bounds__(256) void NAME(QGemmArgs a) { BODY<__VA_ARGS__>(a); }
 #define CUCA_QGEMM_TM(TN, T, FN, FMT, TM)                                                  \
@@ -341,6 +470,19 @@ CUCA_QGEMM_SET(f32, float, q4_0, 0)
 CUCA_QGEMM_SET(f32, float, q8_0, 1)
 CUCA_QGEMM_SET(f16, _Float16, q4_0, 0)
 CUCA_QGEMM_SET(f16, _Float16, q8_0, 1)
+extern "C" __global__ __launch_bounds__(256) void cuca_qgemm_moe_plan(QGemmArgs a) { qgemm_moe_plan_body(a); }
+#define CUCA_QGEMM_MOE_TM(TN, T, FN, FMT, TM)                                              \
+    CUCA_QGEMM(cuca_qgemm_moe_up_##TN##_##FN##_silu_t##TM, qgemm_body, T, FMT, TM, true, 0, false, 1) \
+    CUCA_QGEMM(cuca_qgemm_moe_up_##TN##_##FN##_gelu_t##TM, qgemm_body, T, FMT, TM, true, 1, false, 1) \
+    CUCA_QGEMM(cuca_qgemm_moe_down_##TN##_##FN##_t##TM, qgemm_body, T, FMT, TM, false, 0, false, 2)
+#define CUCA_QGEMM_MOE_SET(TN, T, FN, FMT)                                                 \
+    CUCA_QGEMM(cuca_qgemm_moe_prep_##TN##_##FN, qgemm_moe_prep_body, T, FMT)               \
+    CUCA_QGEMM_MOE_TM(TN, T, FN, FMT, 64)                                                  \
+    CUCA_QGEMM_MOE_TM(TN, T, FN, FMT, 128)
+CUCA_QGEMM_MOE_SET(f32, float, q4_0, 0)
+CUCA_QGEMM_MOE_SET(f32, float, q8_0, 1)
+CUCA_QGEMM_MOE_SET(f16, _Float16, q4_0, 0)
+CUCA_QGEMM_MOE_SET(f16, _Float16, q8_0, 1)
 #define CUCA_QGEMM_RED(TN, T)                                                              \
     CUCA_QGEMM(cuca_qgemm_reduce_##TN, qgemm_reduce_body, T, false, 0)                     \
     CUCA_QGEMM(cuca_qgemm_reduce_glu_##TN##_silu, qgemm_reduce_body, T, true, 0)           \

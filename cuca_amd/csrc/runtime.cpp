@@ -2166,6 +2166,160 @@ cuca_status cuca_hip_moe_sum(cuca_hip_ctx *ctx, const float *scratch, int64_t sc
                   CUCA_BLOCK_THREADS, 0, a);
 }
 
+// Routed experts on the matrix cores (qgemm.hip, the qgemm_moe kernels): a
+// plan of the token tiles (cuca_qgemm_moe_plan), the pairs' activation rows
+// rewritten into the tile layout, then one grouped GEMM launch over (weight
+// row tile, token tile), each token tile one expert's.  Tiles of 128 pairs
+// from a mean of 96 pairs per expert, else 64.  The tile count is bounded
+// by ceil(max_pairs / tm) + min(n_experts, max_pairs) (each expert with
+// pairs adds at most one partial tile).
+static int moe_qgemm_tm(int64_t max_pairs, int32_t n_experts) {
+    return (double)max_pairs / (double)n_experts >= 96.0 ? 128 : 64;
+}
+static int64_t moe_qgemm_tiles(int64_t max_pairs, int32_t n_experts, int tm) {
+    return (max_pairs + tm - 1) / tm + std::min<int64_t>(n_experts, max_pairs);
+}
+static size_t moe_qgemm_ws_bytes(int g, int64_t k, int32_t n_experts, int64_t max_pairs) {
+    const int tm = moe_qgemm_tm(max_pairs, n_experts);
+    const int64_t tiles = moe_qgemm_tiles(max_pairs, n_experts, tm);
+    const size_t plan = ((size_t)tiles * 3 * 4 + 255) / 256 * 256;
+    return plan + (size_t)tiles * (size_t)tm * (size_t)qgemm_kp(g, k) * 2;
+}
+
+cuca_status cuca_hip_moe_qgemm_workspace(uint32_t ggml_type, int64_t k, int32_t n_experts, int64_t max_pairs,
+                                         size_t *bytes) {
+    if (!bytes) return fail(nullptr, CUCA_INVALID_ARG, "null pointer");
+    int g = 0, gb = 0;
+    if (!qfmt(ggml_type, &g, &gb)) return fail(nullptr, CUCA_UNSUPPORTED, "moe qgemm: ggml type %u", ggml_type);
+    if (k <= 0 || k % 32 != 0 || k > kQgMaxK || n_experts <= 0 || max_pairs < 0 || max_pairs > 0x7fffffffll)
+        return fail(nullptr, CUCA_INVALID_ARG, "moe qgemm: bad shape");
+    *bytes = moe_qgemm_ws_bytes(g, k, n_experts, max_pairs);
+    return CUCA_OK;
+}
+
+// up: 1 SiLU, 2 GELU-tanh; 0 down.
+static cuca_status moe_qgemm_common(cuca_hip_ctx *ctx, const void *w, const void *w_up, int64_t estride,
+                                    uint32_t ggml_type, int64_t n, int64_t k, int32_t n_experts, const void *x,
+                                    int64_t ldx, int64_t n_tokens, const int32_t *offsets, const int32_t *pair_token,
+                                    const float *pair_weight, int64_t max_pairs, int up, float clamp, void *ws,
+                                    size_t ws_bytes, void *out, int64_t out_ld, cuca_dtype dtype) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    int g = 0, gb = 0;
+    if ((st = qweight_shape(ctx, ggml_type, n, k, &g, &gb)) != CUCA_OK) return st;
+    if (!dtype_ok(dtype)) return fail(ctx, CUCA_INVALID_ARG, "bad dtype %d", (int)dtype);
+    if (n_experts <= 0 || n_experts > 4096)
+        return fail(ctx, CUCA_INVALID_ARG, "moe qgemm: %d experts (1 to 4096)", n_experts);
+    if (max_pairs < 0 || max_pairs > 0x7fffffffll)
+        return fail(ctx, CUCA_INVALID_ARG, "moe: bad pair capacity %lld", (long long)max_pairs);
+    if (k > kQgMaxK) return fail(ctx, CUCA_UNSUPPORTED, "moe qgemm: rows of more than %lld values", (long long)kQgMaxK);
+    if (ldx < k) return fail(ctx, CUCA_INVALID_ARG, "moe: activation row stride %lld shorter than %lld",
+                             (long long)ldx, (long long)k);
+    if (out_ld < n) return fail(ctx, CUCA_INVALID_ARG, "moe: output row stride %lld shorter than %lld",
+                                (long long)out_ld, (long long)n);
+    if (!(clamp == clamp)) return fail(ctx, CUCA_INVALID_ARG, "clamp is NaN");
+    if (max_pairs == 0) return CUCA_OK;
+    if (!w || !x || !out || !offsets || !ws || (up && (!w_up || !pair_token)) || (!up && !pair_weight))
+        return fail(ctx, CUCA_INVALID_ARG, "null pointer");
+    if (up && (n_tokens <= 0 || n_tokens > 0x7fffffffll))
+        return fail(ctx, CUCA_INVALID_ARG, "moe: bad token count %lld", (long long)n_tokens);
+    const int64_t nb = k / 32, ng = (nb + g - 1) / g;
+    const int64_t packed = n * ng * gb;
+    if (estride < packed || estride % 16 != 0)
+        return fail(ctx, CUCA_INVALID_ARG, "moe: expert stride %lld bytes, at least %lld (a multiple of 16) needed",
+                    (long long)estride, (long long)packed);
+    if (!al16(w) || (w_up && !al16(w_up)) || !al16(ws))
+        return fail(ctx, CUCA_INVALID_ARG, "packed weights and the workspace must be 16-byte aligned");
+    const size_t need = moe_qgemm_ws_bytes(g, k, n_experts, max_pairs);
+    if (ws_bytes < need)
+        return fail(ctx, CUCA_INVALID_ARG, "moe qgemm: workspace of %zu bytes, %zu needed (cuca_hip_moe_qgemm_workspace)",
+                    ws_bytes, need);
+    const int tm = moe_qgemm_tm(max_pairs, n_experts);
+    const int64_t tiles = moe_qgemm_tiles(max_pairs, n_experts, tm);
+    const int64_t kp = qgemm_kp(g, k), nkc = kp / 128;
+    const int64_t n_rt = (n + 127) / 128;
+    const int64_t grid = (n_rt + 7) / 8 * 8 * tiles;
+    if (grid > 0x7fffffffll || tiles * tm * nkc * 16 / CUCA_BLOCK_THREADS + 1 > 0x7fffffffll)
+        return fail(ctx, CUCA_UNSUPPORTED, "moe qgemm: grid too large");
+    const size_t plan = ((size_t)tiles * 3 * 4 + 255) / 256 * 256;
+    QGemmArgs a{};
+    a.w = static_cast<const uint8_t *>(w);
+    a.w_up = static_cast<const uint8_t *>(w_up);
+    a.x = x;
+    a.tile_e = static_cast<int32_t *>(ws);
+    a.tile_p0 = a.tile_e + tiles;
+    a.tile_n = a.tile_p0 + tiles;
+    a.xp = reinterpret_cast<uint16_t *>(static_cast<char *>(ws) + plan);
+    a.out = out;
+    a.ldx = ldx;
+    a.out_ld = out_ld;
+    a.row_bytes = (kp / 32 / g) * gb;
+    a.kp = kp;
+    a.rows = (int32_t)n;
+    a.m = up ? (int32_t)n_tokens : (int32_t)max_pairs;
+    a.k = (int32_t)k;
+    a.nkc = (int32_t)nkc;
+    a.n_rt = (int32_t)n_rt;
+    a.n_ct = (int32_t)tiles;
+    a.kcs = (int32_t)nkc;
+    a.splits = 1;
+    a.clamp = clamp > 0.0f ? clamp : 0.0f;
+    a.mp = (int32_t)(tiles * tm);
+    a.offsets = offsets;
+    a.pair_token = pair_token;
+    a.pair_weight = pair_weight;
+    a.status = ctx->status;
+    a.estride = estride;
+    a.n_experts = n_experts;
+    a.max_pairs = (int32_t)max_pairs;
+    a.tm = tm;
+    a.moe_up = up ? 1 : 0;
+    if ((st = launch(ctx, cuca_qgemm_moe_plan, 1, CUCA_BLOCK_THREADS, 0, a)) != CUCA_OK) return st;
+    const bool f16 = dtype == CUCA_F16, q8 = ggml_type == CUCA_GGML_Q8_0;
+    static const Kernel prep_k[2][2] = {{cuca_qgemm_moe_prep_f32_q4_0, cuca_qgemm_moe_prep_f32_q8_0},
+                                        {cuca_qgemm_moe_prep_f16_q4_0, cuca_qgemm_moe_prep_f16_q8_0}};
+    if ((st = launch(ctx, prep_k[f16][q8], div_up((int64_t)a.mp * nkc * 16, CUCA_BLOCK_THREADS), CUCA_BLOCK_THREADS,
+                     0, a)) != CUCA_OK)
+        return st;
+    // [dtype][format][down, up silu, up gelu][tile pairs 64, 128]
+    static const Kernel table_k[2][2][3][2] = {
+        {{{cuca_qgemm_moe_down_f32_q4_0_t64, cuca_qgemm_moe_down_f32_q4_0_t128},
+          {cuca_qgemm_moe_up_f32_q4_0_silu_t64, cuca_qgemm_moe_up_f32_q4_0_silu_t128},
+          {cuca_qgemm_moe_up_f32_q4_0_gelu_t64, cuca_qgemm_moe_up_f32_q4_0_gelu_t128}},
+         {{cuca_qgemm_moe_down_f32_q8_0_t64, cuca_qgemm_moe_down_f32_q8_0_t128},
+          {cuca_qgemm_moe_up_f32_q8_0_silu_t64, cuca_qgemm_moe_up_f32_q8_0_silu_t128},
+          {cuca_qgemm_moe_up_f32_q8_0_gelu_t64, cuca_qgemm_moe_up_f32_q8_0_gelu_t128}}},
+        {{{cuca_qgemm_moe_down_f16_q4_0_t64, cuca_qgemm_moe_down_f16_q4_0_t128},
+          {cuca_qgemm_moe_up_f16_q4_0_silu_t64, cuca_qgemm_moe_up_f16_q4_0_silu_t128},
+          {cuca_qgemm_moe_up_f16_q4_0_gelu_t64, cuca_qgemm_moe_up_f16_q4_0_gelu_t128}},
+         {{cuca_qgemm_moe_down_f16_q8_0_t64, cuca_qgemm_moe_down_f16_q8_0_t128},
+          {cuca_qgemm_moe_up_f16_q8_0_silu_t64, cuca_qgemm_moe_up_f16_q8_0_silu_t128},
+          {cuca_qgemm_moe_up_f16_q8_0_gelu_t64, cuca_qgemm_moe_up_f16_q8_0_gelu_t128}}}};
+    return launch(ctx, table_k[f16][q8][up][tm == 128], (unsigned)grid, CUCA_BLOCK_THREADS, 0, a);
+}
+
+cuca_status cuca_hip_moe_up_qgemm(cuca_hip_ctx *ctx, const void *gate, const void *up, int64_t expert_stride,
+                                  uint32_t ggml_type, int64_t ff, int64_t n_embd, int32_t n_experts, const void *x,
+                                  int64_t ldx, int64_t n_tokens, const int32_t *offsets, const int32_t *pair_token,
+                                  int64_t max_pairs, cuca_act act, float clamp, void *workspace,
+                                  size_t workspace_bytes, void *hidden, int64_t hidden_ld, cuca_dtype dtype) {
+    if (act != CUCA_ACT_SILU && act != CUCA_ACT_GELU_TANH)
+        return fail(ctx, CUCA_INVALID_ARG, "bad activation %d", (int)act);
+    return moe_qgemm_common(ctx, gate, up, expert_stride, ggml_type, ff, n_embd, n_experts, x, ldx, n_tokens,
+                            offsets, pair_token, nullptr, max_pairs, act == CUCA_ACT_SILU ? 1 : 2, clamp, workspace,
+                            workspace_bytes, hidden, hidden_ld, dtype);
+}
+
+cuca_status cuca_hip_moe_down_qgemm(cuca_hip_ctx *ctx, const void *down, int64_t expert_stride, uint32_t ggml_type,
+                                    int64_t n_embd, int64_t ff, int32_t n_experts, const void *hidden,
+                                    int64_t hidden_ld, const int32_t *offsets, const float *pair_weight,
+                                    int64_t max_pairs, void *workspace, size_t workspace_bytes, float *scratch,
+                                    int64_t scratch_ld, cuca_dtype dtype) {
+    return moe_qgemm_common(ctx, down, nullptr, expert_stride, ggml_type, n_embd, ff, n_experts, hidden, hidden_ld, 0,
+                            offsets, nullptr, pair_weight, max_pairs, 0, 0.0f, workspace, workspace_bytes, scratch,
+                            scratch_ld, dtype);
+}
+
 // RopeSpec::tables (rope.rs:118-151): f64 angles with the platform libm,
 // `cos(theta) * mscale` rounded to f32.
 cuca_status cuca_hip_rope_tables(const cuca_rope_spec *spec, const float *factors, int64_t positions,

@@ -101,6 +101,11 @@ SIGNATURES = {
                               _st, _f32, _p, _i64, _st]),
     "cuca_hip_moe_down": (_st, [_p, _p, _i64, _u32, _i64, _i64, _i32, _p, _i64, _p, _p, _i64, _p,
                                 _i64, _st]),
+    "cuca_hip_moe_qgemm_workspace": (_st, [_u32, _i64, _i32, _i64, _p]),
+    "cuca_hip_moe_up_qgemm": (_st, [_p, _p, _p, _i64, _u32, _i64, _i64, _i32, _p, _i64, _i64, _p, _p, _i64,
+                                    _st, _f32, _p, _sz, _p, _i64, _st]),
+    "cuca_hip_moe_down_qgemm": (_st, [_p, _p, _i64, _u32, _i64, _i64, _i32, _p, _i64, _p, _p, _i64, _p, _sz,
+                                      _p, _i64, _st]),
     "cuca_hip_moe_sum": (_st, [_p, _p, _i64, _i64, _p, _i32, _i64, _i64, _p, _i64, _st]),
     "cuca_hip_q8_acts": (_st, [_p, _p, _i64, _i64, _i64, _st, _p, _p]),
     "cuca_hip_qmv": (_st, [_p, _p, _u32, _i64, _i64, _p, _p, _i64, _i64, _p, _i64, _st]),
@@ -441,6 +446,18 @@ class Context:
                                             hidden, hidden_ld, offsets, pair_weight, max_pairs, scratch,
                                             scratch_ld, dtype))
 
+    def moe_up_qgemm(self, gate, up, estride, ggml_type, ff, n_embd, n_experts, x, ldx, n_tokens, offsets,
+                     pair_token, max_pairs, act, clamp, ws, ws_bytes, hidden, hidden_ld, dtype):
+        self.check(self.L.cuca_hip_moe_up_qgemm(self.ptr, gate, up, estride, ggml_type, ff, n_embd, n_experts,
+                                                x, ldx, n_tokens, offsets, pair_token, max_pairs, act, clamp,
+                                                ws, ws_bytes, hidden, hidden_ld, dtype))
+
+    def moe_down_qgemm(self, down, estride, ggml_type, n_embd, ff, n_experts, hidden, hidden_ld, offsets,
+                       pair_weight, max_pairs, ws, ws_bytes, scratch, scratch_ld, dtype):
+        self.check(self.L.cuca_hip_moe_down_qgemm(self.ptr, down, estride, ggml_type, n_embd, ff, n_experts,
+                                                  hidden, hidden_ld, offsets, pair_weight, max_pairs, ws,
+                                                  ws_bytes, scratch, scratch_ld, dtype))
+
     def moe_sum(self, scratch, scratch_ld, max_pairs, token_pairs, n_used, n_tokens, n_embd, out,
                 out_ld, dtype):
         self.check(self.L.cuca_hip_moe_sum(self.ptr, scratch, scratch_ld, max_pairs, token_pairs,
@@ -500,6 +517,14 @@ def qgemm_workspace(ggml_type, n, k, m, glu=False):
     """Bytes of workspace cuca_hip_qgemm / _qgemm_glu need (host)."""
     out = _sz(0)
     _check(lib().cuca_hip_qgemm_workspace(ggml_type, n, k, m, 1 if glu else 0, ctypes.byref(out)), None)
+    return out.value
+
+
+def moe_qgemm_workspace(ggml_type, k, n_experts, max_pairs):
+    """Bytes of workspace cuca_hip_moe_up_qgemm / _down_qgemm need (host):
+    k = n_embd for up, ff for down."""
+    out = _sz(0)
+    _check(lib().cuca_hip_moe_qgemm_workspace(ggml_type, k, n_experts, max_pairs, ctypes.byref(out)), None)
     return out.value
 
 

@@ -437,12 +437,14 @@ class ExpertBank:
             offsets[e + 1] = len(tok)
         return (offsets, np.asarray(tok, np.int32), np.asarray(wt, np.float32), token_pairs)
 
-    def expert_sum(self, x, per_expert, glu, n_used):
+    def expert_sum(self, x, per_expert, glu, n_used, mm="qmm"):
         """The routed experts' output over the rows x ([t, n_embd] DeviceArray)
         for `per_expert` = [(token, weight)] per expert: moe_up, moe_down,
         moe_sum.  The per-pair hidden activations are held in x's dtype (f32
-        keeps the reference CPU engine's values).  Returns (out [t, n_embd] in
-        x's dtype, hidden, scratch)."""
+        keeps the reference CPU engine's values).  mm="qgemm" runs the up and
+        down projections as grouped GEMMs on the matrix cores (the GPU
+        engine's arithmetic class, for prefill-sized pair counts).  Returns
+        (out [t, n_embd] in x's dtype, hidden, scratch)."""
         hidden_dtype = x.dtype
         ctx = self.ctx
         t = x.shape[0]
@@ -454,14 +456,27 @@ class ExpertBank:
         hidden = ctx.empty((pairs, self.ff), hidden_dtype)
         scratch = ctx.empty((pairs, self.n_embd), np.float32)
         out = ctx.empty((t, self.n_embd), x.dtype)
-        ctx.moe_up(self.gate.ptr, self.up.ptr, self.stride_gu, self.dtype, self.ff, self.n_embd,
-                   self.n_experts, x.ptr, self.n_embd, t, d_off.ptr, d_tok.ptr, len(tok), glu.act,
-                   glu.clamp or 0.0, hidden.ptr, self.ff, hip.dtype_code(hidden_dtype))
-        ctx.moe_down(self.down.ptr, self.stride_d, self.dtype, self.n_embd, self.ff, self.n_experts,
-                     hidden.ptr, self.ff, d_off.ptr, d_wt.ptr, len(tok), scratch.ptr, self.n_embd,
-                     hip.dtype_code(hidden_dtype))
+        keep = ()
+        if mm == "qgemm":
+            wsb = max(hip.moe_qgemm_workspace(self.dtype, self.n_embd, self.n_experts, len(tok)),
+                      hip.moe_qgemm_workspace(self.dtype, self.ff, self.n_experts, len(tok)), 16)
+            ws = ctx.empty((wsb,), np.uint8)
+            keep = (ws,)
+            ctx.moe_up_qgemm(self.gate.ptr, self.up.ptr, self.stride_gu, self.dtype, self.ff, self.n_embd,
+                             self.n_experts, x.ptr, self.n_embd, t, d_off.ptr, d_tok.ptr, len(tok), glu.act,
+                             glu.clamp or 0.0, ws.ptr, wsb, hidden.ptr, self.ff, hip.dtype_code(hidden_dtype))
+            ctx.moe_down_qgemm(self.down.ptr, self.stride_d, self.dtype, self.n_embd, self.ff, self.n_experts,
+                               hidden.ptr, self.ff, d_off.ptr, d_wt.ptr, len(tok), ws.ptr, wsb, scratch.ptr,
+                               self.n_embd, hip.dtype_code(hidden_dtype))
+        else:
+            ctx.moe_up(self.gate.ptr, self.up.ptr, self.stride_gu, self.dtype, self.ff, self.n_embd,
+                       self.n_experts, x.ptr, self.n_embd, t, d_off.ptr, d_tok.ptr, len(tok), glu.act,
+                       glu.clamp or 0.0, hidden.ptr, self.ff, hip.dtype_code(hidden_dtype))
+            ctx.moe_down(self.down.ptr, self.stride_d, self.dtype, self.n_embd, self.ff, self.n_experts,
+                         hidden.ptr, self.ff, d_off.ptr, d_wt.ptr, len(tok), scratch.ptr, self.n_embd,
+                         hip.dtype_code(hidden_dtype))
         ctx.moe_sum(scratch.ptr, self.n_embd, len(tok), d_tp.ptr, n_used, t, self.n_embd, out.ptr,
                     self.n_embd, hip.dtype_code(x.dtype))
         # the routing arrays live as long as the output the queued kernels write
-        out.keep = (d_off, d_tok, d_wt, d_tp)
+        out.keep = (d_off, d_tok, d_wt, d_tp) + keep
         return out, hidden, scratch

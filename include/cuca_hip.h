@@ -10,6 +10,8 @@
  *                           upload in forward_stage)      gpu.rs:2976-2982, 4589-4598
  *   cuca_hip_embed_gguf_   the same + norm_embeddings     params.rs:374-379,
  *     norm                 (rms_norm_rows)                quant.rs:324-339
+ *   cuca_hip_embed_gguf_   the gather + the first block's cpu.rs:2670-2673
+ *     rms                  attention norm
  *   cuca_hip_add_rmsnorm   rms / residual add in block    cpu.rs:2650-2711, 3652
  *                          GPU rms, attn_tail, ffn_half,  gpu.rs:5420-5483, 5883-5896
  *                          ffn_tail
@@ -40,6 +42,8 @@
  *   cuca_hip_qweight_pack  (the weight upload)            qmm.rs:1763-1783
  *   cuca_hip_moe_up/down/  expert_sum, CpuExpert          cpu.rs:373-419, 3599-3642
  *            _sum          (GPU moe_up/moe_down/moe_sum)  moe_kernel.rs:1163-1385
+ *   cuca_hip_moe_up/down_  the same as grouped GEMMs on   moe_kernel.rs:1163-1300
+ *     qgemm                the matrix cores (prefill)
  *   cuca_hip_lm_head       head + cap_logits              cpu.rs:2588-2617
  *   cuca_hip_argmax        greedy                         sampler.rs:44-56
  *   cuca_hip_top_k         select_top_k                   sampler.rs:254-286
@@ -581,6 +585,37 @@ cuca_status cuca_hip_moe_down(cuca_hip_ctx *ctx, const void *down, int64_t exper
 cuca_status cuca_hip_moe_sum(cuca_hip_ctx *ctx, const float *scratch, int64_t scratch_ld, int64_t max_pairs,
                              const int32_t *token_pairs, int32_t n_used, int64_t n_tokens, int64_t n_embd,
                              void *out, int64_t out_ld, cuca_dtype dtype);
+
+/* Routed experts at prefill on the matrix cores: moe_up / moe_down as one
+ * grouped GEMM launch each over the expert-sorted pairs, in the arithmetic
+ * class of cuca_hip_qgemm (the reference GPU engine's MoE kernels,
+ * moe_kernel.rs:1163-1300, with f32 sums of products of f16(d * q) weights
+ * and f16 activations), not the CPU engine's bits (cuca_hip_moe_up/_down):
+ *   up:   hidden[p] = act(gate_e . x[pair_token[p]]) * (up_e . x[...]),
+ *         the GLU applied to the f32 sums, Glu::apply's clamp;
+ *   down: scratch[p] = (down_e . hidden[p]) * pair_weight[p], f32.
+ * Each product is within (2^-10 + k 2^-24) sum |w x| of the exact one.
+ * Arguments as cuca_hip_moe_up / _down (expert e's pairs are
+ * [offsets[e], offsets[e + 1]), read on the device, clamped into
+ * [0, max_pairs] and made non-decreasing; a pair token outside
+ * [0, n_tokens) gives a zero activation row and is reported by
+ * cuca_hip_check_device), plus a device workspace (16-byte aligned) of
+ * cuca_hip_moe_qgemm_workspace bytes for k = n_embd (up) or ff (down),
+ * n_experts and max_pairs.  Up to 4096 experts.  moe_sum then adds the
+ * scratch rows as for the other path.  For a few pairs per expert the
+ * GEMV path (cuca_hip_moe_up/_down) is the faster one. */
+cuca_status cuca_hip_moe_qgemm_workspace(uint32_t ggml_type, int64_t k, int32_t n_experts, int64_t max_pairs,
+                                         size_t *bytes);
+cuca_status cuca_hip_moe_up_qgemm(cuca_hip_ctx *ctx, const void *gate, const void *up, int64_t expert_stride,
+                                  uint32_t ggml_type, int64_t ff, int64_t n_embd, int32_t n_experts, const void *x,
+                                  int64_t ldx, int64_t n_tokens, const int32_t *offsets, const int32_t *pair_token,
+                                  int64_t max_pairs, cuca_act act, float clamp, void *workspace,
+                                  size_t workspace_bytes, void *hidden, int64_t hidden_ld, cuca_dtype dtype);
+cuca_status cuca_hip_moe_down_qgemm(cuca_hip_ctx *ctx, const void *down, int64_t expert_stride, uint32_t ggml_type,
+                                    int64_t n_embd, int64_t ff, int32_t n_experts, const void *hidden,
+                                    int64_t hidden_ld, const int32_t *offsets, const float *pair_weight,
+                                    int64_t max_pairs, void *workspace, size_t workspace_bytes, float *scratch,
+                                    int64_t scratch_ld, cuca_dtype dtype);
 
 /* RopeSpec (rope.rs:62-79). yarn_ext_factor == 0 disables YaRN. */
 typedef struct {

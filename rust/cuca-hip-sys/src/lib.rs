@@ -633,6 +633,55 @@ extern "C" {
         scratch_ld: i64,
         dtype: cuca_dtype,
     ) -> cuca_status;
+    pub fn cuca_hip_moe_qgemm_workspace(
+        ggml_type: u32,
+        k: i64,
+        n_experts: i32,
+        max_pairs: i64,
+        bytes: *mut usize,
+    ) -> cuca_status;
+    pub fn cuca_hip_moe_up_qgemm(
+        ctx: *mut cuca_hip_ctx,
+        gate: *const c_void,
+        up: *const c_void,
+        expert_stride: i64,
+        ggml_type: u32,
+        ff: i64,
+        n_embd: i64,
+        n_experts: i32,
+        x: *const c_void,
+        ldx: i64,
+        n_tokens: i64,
+        offsets: *const i32,
+        pair_token: *const i32,
+        max_pairs: i64,
+        act: cuca_act,
+        clamp: f32,
+        workspace: *mut c_void,
+        workspace_bytes: usize,
+        hidden: *mut c_void,
+        hidden_ld: i64,
+        dtype: cuca_dtype,
+    ) -> cuca_status;
+    pub fn cuca_hip_moe_down_qgemm(
+        ctx: *mut cuca_hip_ctx,
+        down: *const c_void,
+        expert_stride: i64,
+        ggml_type: u32,
+        n_embd: i64,
+        ff: i64,
+        n_experts: i32,
+        hidden: *const c_void,
+        hidden_ld: i64,
+        offsets: *const i32,
+        pair_weight: *const f32,
+        max_pairs: i64,
+        workspace: *mut c_void,
+        workspace_bytes: usize,
+        scratch: *mut f32,
+        scratch_ld: i64,
+        dtype: cuca_dtype,
+    ) -> cuca_status;
     pub fn cuca_hip_moe_sum(
         ctx: *mut cuca_hip_ctx,
         scratch: *const f32,
