@@ -705,9 +705,9 @@ class DecodeStep:
 
 # The kernels of a decode layer by role, from their symbol names.
 def kernel_role(name):
-    if name.startswith(("cuca_qmm_rope_kv",)):
+    if name.startswith(("cuca_qmm_rope_kv", "cuca_qmd_rope_kv")):
         return "qkv_rope_kv"
-    if name.startswith(("cuca_qmm", "cuca_qgemm", "cuca_qmv", "cuca_q8_acts")):
+    if name.startswith(("cuca_qmm", "cuca_qmd", "cuca_qgemm", "cuca_qmv", "cuca_q8_acts")):
         return "matmul"
     if name.startswith("cuca_attn"):
         return "attention"

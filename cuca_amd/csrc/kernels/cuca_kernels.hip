@@ -13,4 +13,5 @@
 #include "qmm.hip"
 #include "pick.hip"
 #include "qmv.hip"
+#include "qmd.hip"
 #include "qgemm.hip"

@@ -1,0 +1,279 @@
+// qmd.hip -- the decode matmul of one activation row: the CPU engine's
+// quantized matmul (QmmWeight, qmm.rs) bit for bit, as qmm.hip computes it,
+// shaped for m = 1 at the layer shapes of a decode step.
+//
+// The arithmetic is qmm.hip's: sixteen lane chains per weight row, lane l
+// adding block by block, in row order, (float)P * (dw * dx) with the
+// product and the sum rounded separately, P the exact integer pair sum of
+// v_dot2_f32_f16 over magic-number pairs; the fixed hsum tree at the end.
+// Only the data movement differs:
+//
+//  * One wave is four weight rows x 16 lanes, each thread one chain over
+//    the whole row; a workgroup is four waves and the grid holds every row
+//    (no persistent loop): at one activation row the chains are the only
+//    parallelism, so the chip needs all of them resident.
+//  * Weight groups (G blocks: the lane's 16-byte chunk and the dword with
+//    its block's f16 scale) stream through a ring of D slots in registers.
+//    The first D loads are issued before anything else, so the workgroup's
+//    quantisation of the activation row runs under their latency; after
+//    that every consumed slot is refilled with the group D ahead.  D
+//    divides the group count and the last round is peeled off, so every
+//    load is used and the loop body has one path (exact wait counts).
+//  * The activation row is quantised once per workgroup into LDS, as
+//    qmv.hip does (Acts::new, qmm.rs:1217-1343): per (lane, block) the f16
+//    pair and the dot's constant C, and the block scales.
+//  * dw * dx: lane l of each row computes the product of block l of the
+//    group, and the chain of block b reads it from lane b of its row by a
+//    DPP row broadcast folded into the multiply (v_mul_f32_dpp
+//    row_newbcast:b), so the per-block scale costs no LDS traffic and no
+//    instruction of its own.  Per block and chain that leaves the pair
+//    (one v_bfi_b32; Q4_0 adds a shift per four blocks), the dot, the
+//    multiply and the add, and one 8-byte LDS read shared by the chains a
+//    thread runs (gate and up for the GLU).
+#include "common.h"
+
+template <int V> struct QmdInt { static constexpr int value = V; };
+template <int I, int N, typename Fn> __device__ static inline void qmd_for(Fn &&fn) {
+    if constexpr (I < N) {
+        fn(QmdInt<I>{});
+        qmd_for<I + 1, N>(fn);
+    }
+}
+
+// The value of v in lane B of each row of 16 lanes (DPP row_newbcast,
+// gfx90a and later); the compiler folds it into the instruction that reads
+// it.
+template <int B> __device__ static inline float qmd_bcast(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x150 + B, 0xf,
+                                                                 0xf, false));
+}
+
+#define QMD_RSRC_W3 0x00020000 // buffer resource word 3 (raw buffer, 32-bit data)
+
+// One ring slot: the lane's chunk of a group and the dword holding the
+// f16 scale of block l (gate; up for the GLU).
+struct QmdSlot {
+    u32x4 w, u;
+    uint32_t sw, su;
+};
+
+// Bytes of LDS: the expanded row (16 lanes x (ng G + 2) entries of 8
+// bytes) and its block scales (padded by a group: the stream reads one
+// group ahead).
+#define QMD_LDS_BYTES(NG, G) (16 * ((NG) * (G) + 2) * 8 + ((NG) + 1) * (G) * 4)
+
+// MODE 0: plain (out[row], the LM head's cap when asked); 3: the Q|K|V
+// projection with RoPE and the paged K/V store in the epilogue (qmm.hip's
+// qmm_rope_kv_store).  D: ring slots; NI: activation items (8 values) per
+// thread, NI * 256 >= 4 ng G.  The grid is ceil(rows / 16) workgroups of
+// 256.
+template <typename T, int FMT, bool GLU, int ACT, int MODE, int D, int NI>
+__device__ static inline void qmd_body(const QmmArgs &a) {
+    using F = QFmt<FMT>;
+    constexpr int G = F::G;
+    extern __shared__ __attribute__((aligned(16))) unsigned char qmd_lds[];
+    const int ng = a.ng, nbp = ng * G, xstr = nbp + 2;
+    qmm_u2 *xe = reinterpret_cast<qmm_u2 *>(qmd_lds);
+    float *xsc = reinterpret_cast<float *>(xe + 16 * xstr);
+    const int tid = threadIdx.x, lt = tid & (CUCA_WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(tid / CUCA_WAVE);
+    const int r = lt >> 4, l = lt & 15;
+    const int row = (blockIdx.x * 4 + wave) * 4 + r;
+    // a row past the matrix streams the last row; its result is not stored
+    const int lrow = row < a.rows ? row : a.rows - 1;
+    const uint32_t nrec = (uint32_t)((int64_t)a.rows * a.row_bytes);
+    const __amdgpu_buffer_rsrc_t rw =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(a.w), 0, (int)nrec, QMD_RSRC_W3);
+    const __amdgpu_buffer_rsrc_t ru =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t *>(GLU ? a.w_up : a.w), 0, (int)nrec, QMD_RSRC_W3);
+    const uint32_t rbase = (uint32_t)lrow * (uint32_t)a.row_bytes;
+    const uint32_t vchunk = rbase + F::SCB + 16 * l;
+    const uint32_t vscale = rbase + 4 * ((l % G) >> 1);
+
+    // 1. The activation row's loads: item it * 256 + tid is values
+    // 8 (item % 4) .. +7 of block item / 4 (zero past the row).
+    const int nitems = 4 * nbp, sub = tid & 3;
+    float xv[NI][8];
+#pragma unroll
+    for (int it = 0; it < NI; it++) {
+        const int item = it * CUCA_BLOCK + tid, b = item >> 2;
+        if (item < nitems && b < a.nb) {
+            qmm_load8<T>(reinterpret_cast<const T *>(a.x) + (int64_t)b * 32 + sub * 8, xv[it]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++) xv[it][e] = 0.0f;
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. The ring's first D groups, issued behind the activations (loads
+    // complete in order, so the quantisation below waits for its own loads
+    // only) and in slot order, as the loop refills them (the loop's wait
+    // counts, which merge this path with its own, then need no more than
+    // the slot's own loads).  A refill past the row's last group (in the
+    // round before the last) reads that group again, and is not consumed.
+    QmdSlot ring[D];
+    auto load = [&](QmdSlot &s, int g) {
+        const int so = (g < ng ? g : ng - 1) * F::GB; // wave-uniform: the scalar offset
+        s.w = __builtin_amdgcn_raw_buffer_load_b128(rw, vchunk, so, 0);
+        s.sw = __builtin_amdgcn_raw_buffer_load_b32(rw, vscale, so, 0);
+        if constexpr (GLU) {
+            s.u = __builtin_amdgcn_raw_buffer_load_b128(ru, vchunk, so, 0);
+            s.su = __builtin_amdgcn_raw_buffer_load_b32(ru, vscale, so, 0);
+        }
+    };
+    qmd_for<0, D>([&](auto I) {
+        load(ring[I.value], I.value);
+        __builtin_amdgcn_sched_barrier(0);
+    });
+
+    // 3. Quantise (Acts::new, qmm.rs:1217-1240: the four threads of a block
+    // share its maximum) and expand: per (lane, block) the f16 pair
+    // (q[l], q[l+16]) and C = -K (q[l] + q[l+16]); the block scales.
+    {
+        const qmm_h2 negk = {(_Float16)(-F::K), (_Float16)(-F::K)};
+        const bool low = sub < 2;
+        const int base = 8 * (sub & 1) + (low ? 0 : 4);
+#pragma unroll
+        for (int it = 0; it < NI; it++) {
+            const int item = it * CUCA_BLOCK + tid, b = item >> 2;
+            float amax = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(xv[it][e]));
+            amax = fmaxf(amax, __shfl_xor(amax, 1, CUCA_WAVE));
+            amax = fmaxf(amax, __shfl_xor(amax, 2, CUCA_WAVE));
+            const float d = amax / 127.0f;
+            const float id = d != 0.0f ? 1.0f / d : 0.0f;
+            uint32_t own[4], other[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                own[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(qmm_quant(xv[it][2 * i] * id),
+                                                                                 qmm_quant(xv[it][2 * i + 1] * id)));
+                other[i] = (uint32_t)__shfl_xor((int)own[i], 2, CUCA_WAVE);
+            }
+            if (item < nitems) {
+                // threads 0/1 own elements 0-7 / 8-15, threads 2/3 16-23 /
+                // 24-31; sub < 2 writes lanes 8s..8s+3, sub >= 2 lanes
+                // 8s+4..8s+7 (s = sub & 1)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const uint32_t lo = low ? own[q >> 1] : other[2 + (q >> 1)];
+                    const uint32_t hi = low ? other[q >> 1] : own[2 + (q >> 1)];
+                    const uint32_t xp = __builtin_amdgcn_perm(hi, lo, (q & 1) ? 0x07060302u : 0x05040100u);
+                    const float cc = __builtin_amdgcn_fdot2(__builtin_bit_cast(qmm_h2, xp), negk, 0.0f, false);
+                    xe[(base + q) * xstr + b] = qmm_u2{xp, __builtin_bit_cast(uint32_t, cc)};
+                }
+                if (sub == 0) xsc[b] = b < a.nb ? (float)(_Float16)d : 0.0f;
+            }
+        }
+        if (tid < G) xsc[nbp + tid] = 0.0f; // the group past the row
+    }
+    __syncthreads();
+
+    // 4. The stream.  Lane l's scale is block l's of the group (the odd
+    // Q4_0 blocks' dw / 16); the LDS operands of the next four blocks, and
+    // the next group's dx, are read one step ahead.
+    const int sh = 16 * (l & 1);
+    const float kmul = (FMT == 0 && (l & 1)) ? 0.0625f : 1.0f;
+    const qmm_u2 *xl = xe + l * xstr;
+    const float *xsl = xsc + (l % G);
+    constexpr int NS = G / 4; // steps of four blocks per group
+    float acc = 0.0f, accu = 0.0f;
+    u32x4 cx01 = *reinterpret_cast<const u32x4 *>(xl);
+    u32x4 cx23 = *reinterpret_cast<const u32x4 *>(xl + 2);
+    float cdx = xsl[0];
+    auto consume = [&](const QmdSlot &s, int g) {
+        const float sg = (qmv_h2f(s.sw >> sh) * kmul) * cdx;
+        const float su = GLU ? (qmv_h2f(s.su >> sh) * kmul) * cdx : 0.0f;
+        cdx = xsl[(g + 1) * G];
+        qmd_for<0, NS>([&](auto S4) {
+            constexpr int b0 = 4 * S4.value;
+            const qmm_u2 *xn = xl + g * G + b0 + 4; // the next step's (the next group's first)
+            const u32x4 nx01 = *reinterpret_cast<const u32x4 *>(xn);
+            const u32x4 nx23 = *reinterpret_cast<const u32x4 *>(xn + 2);
+            const uint32_t xp[4] = {cx01.x, cx01.z, cx23.x, cx23.z};
+            const uint32_t xc[4] = {cx01.y, cx01.w, cx23.y, cx23.w};
+            float pg[4], pu[4];
+            qmd_for<0, 4>([&](auto Q) {
+                constexpr int b = b0 + Q.value;
+                const float cc = __builtin_bit_cast(float, xc[Q.value]);
+                pg[Q.value] = qmm_dot(F::pair(s.w, b), xp[Q.value], cc);
+                if constexpr (GLU) pu[Q.value] = qmm_dot(F::pair(s.u, b), xp[Q.value], cc);
+            });
+            // the dots, then the products into registers of their own, then
+            // the sums: a DPP multiply waits two cycles for a register (its
+            // operand or its destination) written just before it
+            __builtin_amdgcn_sched_barrier(0);
+            float qg[4], qu[4];
+            qmd_for<0, 4>([&](auto Q) {
+                constexpr int b = b0 + Q.value;
+                qg[Q.value] = pg[Q.value] * qmd_bcast<b>(sg);
+                if constexpr (GLU) qu[Q.value] = pu[Q.value] * qmd_bcast<b>(su);
+            });
+            __builtin_amdgcn_sched_barrier(0);
+            qmd_for<0, 4>([&](auto Q) {
+                acc = acc + qg[Q.value];
+                if constexpr (GLU) accu = accu + qu[Q.value];
+            });
+            // pin these four blocks' arithmetic here (the chains are read
+            // only at the end, so the compiler would sink it)
+            asm volatile("" : "+v"(acc));
+            if constexpr (GLU) asm volatile("" : "+v"(accu));
+            __builtin_amdgcn_sched_barrier(0);
+            cx01 = nx01;
+            cx23 = nx23;
+        });
+    };
+    const int nr = (ng + D - 1) / D;
+    for (int R = 0; R + 1 < nr; R++) {
+        qmd_for<0, D>([&](auto I) {
+            consume(ring[I.value], R * D + I.value);
+            load(ring[I.value], (R + 1) * D + I.value);
+        });
+    }
+    const int rem = ng - (nr - 1) * D; // 1..D groups in the last round
+    qmd_for<0, D>([&](auto I) {
+        if (I.value < rem) consume(ring[I.value], (nr - 1) * D + I.value);
+    });
+
+    float o = qmm_hsum(acc);
+    if constexpr (GLU) {
+        float g = o, u = qmm_hsum(accu);
+        if (a.clamp > 0.0f) { // Glu::apply's clamp (cpu.rs:364-368)
+            g = fminf(g, a.clamp);
+            u = fminf(fmaxf(u, -a.clamp), a.clamp);
+        }
+        o = (ACT == 0 ? act_silu(g) : act_gelu_tanh(g)) * u;
+    } else if (MODE == 0 && a.cap_flags) { // cap_logits (cpu.rs:2603-2617)
+        if (a.cap_flags & 1) o = o * a.mul1 + 0.0f;
+        if (a.cap_flags & 2) o = o * a.mul2 + 0.0f;
+        if (a.cap_flags & 4) o = tanhf(o * a.softcap_inv + 0.0f) * a.softcap + 0.0f;
+    }
+    if constexpr (MODE == 3) {
+        qmm_rope_kv_store<T>(a, 0, true, 0, row, l, o);
+    } else {
+        if (l == 0 && row < a.rows) reinterpret_cast<T *>(a.out)[row] = to_stored<T>(o);
+    }
+}
+
+#define CUCA_QMD(NAME, ...)                                                                \
+    extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void NAME(QmmArgs a) {             \
+        qmd_body<__VA_ARGS__>(a);                                                          \
+    }
+// [act dtype][format][row length: n2 for k <= 4096, n8 for k <= 16384]:
+// plain, SwiGLU, GeGLU-tanh, Q|K|V with RoPE and the K/V store.  Ring
+// depths DP (plain) / DG (GLU, two matrices a slot) measured best at the
+// Llama-3-8B decode shapes.
+#define CUCA_QMD_SET(TN, T, FN, FMT, NI, DP, DG)                                           \
+    CUCA_QMD(cuca_qmd_##TN##_##FN##_n##NI, T, FMT, false, 0, 0, DP, NI)                    \
+    CUCA_QMD(cuca_qmd_glu_##TN##_##FN##_silu_n##NI, T, FMT, true, 0, 0, DG, NI)            \
+    CUCA_QMD(cuca_qmd_glu_##TN##_##FN##_gelu_n##NI, T, FMT, true, 1, 0, DG, NI)            \
+    CUCA_QMD(cuca_qmd_rope_kv_##TN##_##FN##_n##NI, T, FMT, false, 0, 3, DP, NI)
+CUCA_QMD_SET(f32, float, q4_0, 0, 2, 4, 2)
+CUCA_QMD_SET(f32, float, q4_0, 0, 8, 8, 2)
+CUCA_QMD_SET(f32, float, q8_0, 1, 2, 8, 4)
+CUCA_QMD_SET(f32, float, q8_0, 1, 8, 8, 4)
+CUCA_QMD_SET(f16, _Float16, q4_0, 0, 2, 4, 2)
+CUCA_QMD_SET(f16, _Float16, q4_0, 0, 8, 8, 2)
+CUCA_QMD_SET(f16, _Float16, q8_0, 1, 2, 8, 4)
+CUCA_QMD_SET(f16, _Float16, q8_0, 1, 8, 8, 4)

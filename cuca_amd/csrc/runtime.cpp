@@ -1150,6 +1150,40 @@ static cuca_status qmv_launch(cuca_hip_ctx *ctx, int mode, const void *w, const 
                               const void *x, int64_t ldx, int64_t m, int64_t rows, int glu, float clamp, void *out,
                               int64_t out_ld, cuca_dtype dtype, const LogitCap &cap);
 
+// The decode matmul of one activation row (qmd.hip): rows up to 16384
+// values (n2 kernels to 4096), the workgroup's LDS copy of the expanded row
+// within 64 KiB, and the weight rows' bytes addressable by a 32-bit buffer
+// offset.  mode 0: plain / GLU (glu 1 SiLU, 2 GELU-tanh); 3: Q|K|V with RoPE
+// and the K/V store (a carries the epilogue's fields).
+static size_t qmd_lds(int64_t ng, int g) { return (size_t)(16 * (ng * g + 2) * 8 + (ng + 1) * g * 4); }
+static bool qmd_fits(int64_t m, int64_t k, int64_t ng, int g, int64_t rows, int64_t row_bytes) {
+    return m == 1 && k <= 16384 && qmd_lds(ng, g) <= (64u << 10) && rows * row_bytes < (1ll << 31);
+}
+static cuca_status qmd_launch(cuca_hip_ctx *ctx, int mode, int glu, uint32_t ggml_type, int64_t k, int g,
+                              cuca_dtype dtype, QmmArgs &a) {
+    // [dtype][format][n2, n8][plain, silu, gelu, rope_kv]
+    static const Kernel table_k[2][2][2][4] = {
+        {{{cuca_qmd_f32_q4_0_n2, cuca_qmd_glu_f32_q4_0_silu_n2, cuca_qmd_glu_f32_q4_0_gelu_n2,
+           cuca_qmd_rope_kv_f32_q4_0_n2},
+          {cuca_qmd_f32_q4_0_n8, cuca_qmd_glu_f32_q4_0_silu_n8, cuca_qmd_glu_f32_q4_0_gelu_n8,
+           cuca_qmd_rope_kv_f32_q4_0_n8}},
+         {{cuca_qmd_f32_q8_0_n2, cuca_qmd_glu_f32_q8_0_silu_n2, cuca_qmd_glu_f32_q8_0_gelu_n2,
+           cuca_qmd_rope_kv_f32_q8_0_n2},
+          {cuca_qmd_f32_q8_0_n8, cuca_qmd_glu_f32_q8_0_silu_n8, cuca_qmd_glu_f32_q8_0_gelu_n8,
+           cuca_qmd_rope_kv_f32_q8_0_n8}}},
+        {{{cuca_qmd_f16_q4_0_n2, cuca_qmd_glu_f16_q4_0_silu_n2, cuca_qmd_glu_f16_q4_0_gelu_n2,
+           cuca_qmd_rope_kv_f16_q4_0_n2},
+          {cuca_qmd_f16_q4_0_n8, cuca_qmd_glu_f16_q4_0_silu_n8, cuca_qmd_glu_f16_q4_0_gelu_n8,
+           cuca_qmd_rope_kv_f16_q4_0_n8}},
+         {{cuca_qmd_f16_q8_0_n2, cuca_qmd_glu_f16_q8_0_silu_n2, cuca_qmd_glu_f16_q8_0_gelu_n2,
+           cuca_qmd_rope_kv_f16_q8_0_n2},
+          {cuca_qmd_f16_q8_0_n8, cuca_qmd_glu_f16_q8_0_silu_n8, cuca_qmd_glu_f16_q8_0_gelu_n8,
+           cuca_qmd_rope_kv_f16_q8_0_n8}}}};
+    const int kind = mode == 3 ? 3 : glu;
+    const Kernel kk = table_k[dtype == CUCA_F16][ggml_type == CUCA_GGML_Q8_0][k > 4096][kind];
+    return launch(ctx, kk, div_up(a.rows, 16), CUCA_BLOCK_THREADS, (unsigned)qmd_lds(a.ng, g), a);
+}
+
 // glu: 0 plain, 1 SiLU, 2 GELU-tanh
 static cuca_status qmm_common(cuca_hip_ctx *ctx, const void *w, const void *w_up, uint32_t ggml_type,
                               int64_t n, int64_t k, const void *x, int64_t ldx, int64_t m, int64_t rows,
@@ -1184,6 +1218,7 @@ static cuca_status qmm_common(cuca_hip_ctx *ctx, const void *w, const void *w_up
     if (m <= 2 && qmv_wins(ctx, rows) && qmv_fits(m, ng * g, g))
         return qmv_launch(ctx, 3, w, w_up, ggml_type, n, k, nullptr, 0, nullptr, x, ldx, m, rows, glu, clamp, out,
                           out_ld, dtype, cap);
+    const bool qmd = qmd_fits(m, k, ng, g, rows, ng * gb);
     const int mt = m == 1 ? 1 : m == 2 ? 2 : 4;
     const int mi = mt == 1 ? 0 : mt == 2 ? 1 : 2;
     const int64_t ntile = (m + mt - 1) / mt;
@@ -1228,6 +1263,8 @@ static cuca_status qmm_common(cuca_hip_ctx *ctx, const void *w, const void *w_up
         a.softcap_inv = (float)(1.0 / (double)cap.softcap);
         a.softcap = cap.softcap;
     }
+    // one activation row: the decode matmul (the same bits)
+    if (qmd) return qmd_launch(ctx, 0, glu, ggml_type, k, g, dtype, a);
     return launch(ctx, kk, (unsigned)(nrb8 * ntile), CUCA_BLOCK_THREADS, 0, a);
 }
 
@@ -1307,6 +1344,7 @@ cuca_status cuca_hip_qmm_rope_store_kv(cuca_hip_ctx *ctx, const void *w, uint32_
     a.n_dims = n_dims;
     ctx->last_table_rows = table_rows;
     ctx->last_kv_blocks = n_blocks;
+    if (qmd_fits(m, k, ng, g, n, ng * gb)) return qmd_launch(ctx, 3, 0, ggml_type, k, g, dtype, a);
     return launch(ctx, table_k[dtype == CUCA_F16][ggml_type == CUCA_GGML_Q8_0][mi], (unsigned)(nrb8 * ntile),
                   CUCA_BLOCK_THREADS, 0, a);
 }
