@@ -59,7 +59,8 @@ struct QmdSlot {
 
 // Bytes of LDS: the expanded row (16 lanes x (ng G + 2) entries of 8
 // bytes) and its block scales (padded by a group: the stream reads one
-// group ahead).
+// group ahead, and up to eight entries past a lane's row, which stay inside
+// the allocation).
 #define QMD_LDS_BYTES(NG, G) (16 * ((NG) * (G) + 2) * 8 + ((NG) + 1) * (G) * 4)
 
 // MODE 0: plain (out[row], the LM head's cap when asked); 3: the Q|K|V
@@ -67,7 +68,7 @@ struct QmdSlot {
 // qmm_rope_kv_store).  D: ring slots; NI: activation items (8 values) per
 // thread, NI * 256 >= 4 ng G.  The grid is ceil(rows / 16) workgroups of
 // 256.
-template <typename T, int FMT, bool GLU, int ACT, int MODE, int D, int NI>
+template <typename T, int FMT, bool GLU, int ACT, int MODE, int D, int NI, int PF = 1>
 __device__ static inline void qmd_body(const QmmArgs &a) {
     using F = QFmt<FMT>;
     constexpr int G = F::G;
@@ -179,8 +180,14 @@ __device__ static inline void qmd_body(const QmmArgs &a) {
     const float *xsl = xsc + (l % G);
     constexpr int NS = G / 4; // steps of four blocks per group
     float acc = 0.0f, accu = 0.0f;
+    // the LDS operands of the current step and, with PF = 2, the next
     u32x4 cx01 = *reinterpret_cast<const u32x4 *>(xl);
     u32x4 cx23 = *reinterpret_cast<const u32x4 *>(xl + 2);
+    u32x4 px01 = cx01, px23 = cx23;
+    if constexpr (PF == 2) {
+        px01 = *reinterpret_cast<const u32x4 *>(xl + 4);
+        px23 = *reinterpret_cast<const u32x4 *>(xl + 6);
+    }
     float cdx = xsl[0];
     auto consume = [&](const QmdSlot &s, int g) {
         const float sg = (qmv_h2f(s.sw >> sh) * kmul) * cdx;
@@ -188,7 +195,8 @@ __device__ static inline void qmd_body(const QmmArgs &a) {
         cdx = xsl[(g + 1) * G];
         qmd_for<0, NS>([&](auto S4) {
             constexpr int b0 = 4 * S4.value;
-            const qmm_u2 *xn = xl + g * G + b0 + 4; // the next step's (the next group's first)
+            // the operands PF steps ahead (into the next group at its end)
+            const qmm_u2 *xn = xl + g * G + b0 + 4 * PF;
             const u32x4 nx01 = *reinterpret_cast<const u32x4 *>(xn);
             const u32x4 nx23 = *reinterpret_cast<const u32x4 *>(xn + 2);
             const uint32_t xp[4] = {cx01.x, cx01.z, cx23.x, cx23.z};
@@ -220,8 +228,15 @@ __device__ static inline void qmd_body(const QmmArgs &a) {
             asm volatile("" : "+v"(acc));
             if constexpr (GLU) asm volatile("" : "+v"(accu));
             __builtin_amdgcn_sched_barrier(0);
-            cx01 = nx01;
-            cx23 = nx23;
+            if constexpr (PF == 2) {
+                cx01 = px01;
+                cx23 = px23;
+                px01 = nx01;
+                px23 = nx23;
+            } else {
+                cx01 = nx01;
+                cx23 = nx23;
+            }
         });
     };
     const int nr = (ng + D - 1) / D;

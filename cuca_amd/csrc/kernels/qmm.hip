@@ -108,11 +108,16 @@ __device__ static inline float qmm_dot(uint32_t w, uint32_t x, float c) {
 }
 
 // round_away (qmm.rs:1194-1201) then Rust's saturating `as i8` (NaN -> 0),
-// as an exact integer-valued float.
+// as an exact integer-valued float.  Rounding half away from zero is
+// trunc(t + copysign(0.5 - 2^-25, t)): the same bits as roundf for every
+// finite f32 (checked exhaustively on the host, all 2^32 patterns), in two
+// instructions fewer.  NaN is tested on t itself: the clamp's min / max
+// return their other operand for a NaN, so a test after it never fires (it
+// did not: a NaN activation quantised to -128).
 __device__ static inline float qmm_quant(float t) {
-    float r = roundf(t);
-    r = fminf(fmaxf(r, -128.0f), 127.0f);
-    return r == r ? r : 0.0f;
+    const float r = __builtin_truncf(t + __builtin_copysignf(0.49999997f, t));
+    const float c = fminf(fmaxf(r, -128.0f), 127.0f);
+    return t == t ? c : 0.0f;
 }
 
 template <typename T> __device__ static inline void qmm_load8(const T *p, float (&v)[8]);

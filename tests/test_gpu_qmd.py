@@ -95,3 +95,22 @@ def test_one_row_qkv_partial_rotary_and_bad_slot(ctx):
     rng = np.random.default_rng(91)
     qkv_fused_vs_unfused(ctx, rng, "q4_0", "f32", 4, 2, 64, 512, 1, n_dims=32)
     qkv_fused_vs_unfused(ctx, rng, "q8_0", "f32", 4, 2, 32, 256, 1, bad_row=0)
+
+
+@pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("m,n,k", [(1, 40, 544), (1, 24, 4128), (3, 40, 544), (2, 256 * 16 * 4 * 2, 64)])
+def test_nan_activations_quantise_to_zero(ctx, qtype, m, n, k):
+    """Acts::new: a NaN is ignored by the block maximum and quantises to 0
+    (Rust's saturating `as i8`), so the outputs stay finite and equal the
+    oracle's.  One row (the decode matmul), three (the one-pass kernel), and
+    two rows of a tall matrix (the decode GEMV)."""
+    rng = np.random.default_rng(m * 31 + k)
+    raw, w = weight(ctx, rng, qtype, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    x[:, 5] = np.nan
+    x[:, 32 + 31] = np.nan
+    x[0, 34] = -np.nan
+    got = w.forward(ctx.array(x)).numpy()
+    want = want_out(raw, qtype, n, k, x, n, "f32")
+    assert np.all(np.isfinite(want))
+    assert_bits_equal(got, want, f"{qtype} m={m} {n}x{k} NaN activations")
