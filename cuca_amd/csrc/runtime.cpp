@@ -522,7 +522,8 @@ cuca_status cuca_hip_embed_gguf_rms(cuca_hip_ctx *ctx, const void *table, uint32
 // - Gemma-2 shapes at 2048 tokens (norm 28 MiB, GeGLU 112 MiB) ran slower
 //   streamed (GeGLU 86 -> 76 %, the norms 59 -> 49 %);
 // - RoPE, which rewrites its rows in place, ran slower streamed at every
-//   size (66 -> 61 % at 4096 tokens), so it never streams.
+//   size (66 -> 61 % at 4096 tokens); it reads with device-scope loads
+//   instead (rope_common), except the prefill-sized QK-norm calls.
 static const int64_t kStreamBytes = 48ll << 20;
 static const int64_t kGluStreamBytes = 192ll << 20;
 
@@ -820,19 +821,31 @@ static cuca_status rope_common(cuca_hip_ctx *ctx, void *q, int64_t q_ld, const v
     int lg = 0;
     while ((1 << lg) < tph) lg++;
     a.tph_log2 = lg;
-    // [dtype][kind][norm][store]
-    static const Kernel table_k[2][2][2][2] = {
-        {{{cuca_rope_f32_norm, cuca_rope_f32_norm_kv}, {cuca_rope_f32_norm_qkn, cuca_rope_f32_norm_qkn_kv}},
-         {{cuca_rope_f32_neox, cuca_rope_f32_neox_kv}, {cuca_rope_f32_neox_qkn, cuca_rope_f32_neox_qkn_kv}}},
-        {{{cuca_rope_f16_norm, cuca_rope_f16_norm_kv}, {cuca_rope_f16_norm_qkn, cuca_rope_f16_norm_qkn_kv}},
-         {{cuca_rope_f16_neox, cuca_rope_f16_neox_kv}, {cuca_rope_f16_neox_qkn, cuca_rope_f16_neox_qkn_kv}}}};
+    // [device-scope loads][dtype][kind][norm][store]: the device-scope
+    // kernels address a row's chunks by 32-bit byte offsets from q, k and v
+    static const Kernel table_k[2][2][2][2][2] = {
+        {{{{cuca_rope_f32_norm_g, cuca_rope_f32_norm_kv_g}, {cuca_rope_f32_norm_qkn_g, cuca_rope_f32_norm_qkn_kv_g}},
+          {{cuca_rope_f32_neox_g, cuca_rope_f32_neox_kv_g}, {cuca_rope_f32_neox_qkn_g, cuca_rope_f32_neox_qkn_kv_g}}},
+         {{{cuca_rope_f16_norm_g, cuca_rope_f16_norm_kv_g}, {cuca_rope_f16_norm_qkn_g, cuca_rope_f16_norm_qkn_kv_g}},
+          {{cuca_rope_f16_neox_g, cuca_rope_f16_neox_kv_g}, {cuca_rope_f16_neox_qkn_g, cuca_rope_f16_neox_qkn_kv_g}}}},
+        {{{{cuca_rope_f32_norm, cuca_rope_f32_norm_kv}, {cuca_rope_f32_norm_qkn, cuca_rope_f32_norm_qkn_kv}},
+          {{cuca_rope_f32_neox, cuca_rope_f32_neox_kv}, {cuca_rope_f32_neox_qkn, cuca_rope_f32_neox_qkn_kv}}},
+         {{{cuca_rope_f16_norm, cuca_rope_f16_norm_kv}, {cuca_rope_f16_norm_qkn, cuca_rope_f16_norm_qkn_kv}},
+          {{cuca_rope_f16_neox, cuca_rope_f16_neox_kv}, {cuca_rope_f16_neox_qkn, cuca_rope_f16_neox_qkn_kv}}}}};
+    const int64_t lim = 1ll << 32;
+    const bool dev = (nq == 0 || rows * q_ld * (int64_t)es <= lim) && (nk == 0 || rows * k_ld * (int64_t)es <= lim) &&
+                     (!store || nk == 0 || rows * v_ld * (int64_t)es <= lim);
     static const Kernel table_nt[2][2][2] = {
         {{cuca_rope_f32_norm_qkn_nt, cuca_rope_f32_norm_qkn_kv_nt}, {cuca_rope_f32_neox_qkn_nt, cuca_rope_f32_neox_qkn_kv_nt}},
         {{cuca_rope_f16_norm_qkn_nt, cuca_rope_f16_norm_qkn_kv_nt}, {cuca_rope_f16_neox_qkn_nt, cuca_rope_f16_neox_qkn_kv_nt}}};
-    // prefill-sized QK-norm calls stream their head rows (measured: plain
-    // RoPE runs slower streamed, QK-norm RoPE and the kernels after it faster)
+    // Head chunks are read with device-scope loads (the rope kernels' load
+    // policies), except that prefill-sized QK-norm calls stream them with
+    // nontemporal loads.  Measured on MI355X in the config E prefill step
+    // (8192 tokens, QK-norm NEOX RoPE): RoPE takes 31.4 us either way, but
+    // with device-scope loads the ragged SwiGLU after it slows from 48.3 to
+    // 54.7 us and the next gather from 15.4 to 20.8 us.
     const bool stream = norm && heads * (int64_t)head_dim * (int64_t)esize(dtype) >= kStreamBytes;
-    const Kernel kk = stream ? table_nt[f16][neox][store] : table_k[f16][neox][norm][store];
+    const Kernel kk = stream ? table_nt[f16][neox][store] : table_k[dev][f16][neox][norm][store];
     return launch(ctx, kk, div_up(heads, 256 / tph), 256, 0, a);
 }
 
