@@ -40,7 +40,8 @@ typedef struct {
     void *h_out;            /* the _rms kernels: [n, hidden] rms(x, w)     */
     const float *rms_w;     /* the _rms kernels: [hidden] or NULL          */
     float rms_eps;          /* the _rms kernels                            */
-    int32_t pad_;
+    int32_t tpw;            /* the _rms_lds kernels: tokens per wave; a
+                               workgroup of 4 waves covers 4 tpw tokens   */
 } EmbedArgs;
 
 typedef struct {

@@ -258,21 +258,23 @@ __device__ static inline void embed_rms_body(const EmbedArgs &a) {
         return;
     }
     const uint16_t *s16 = reinterpret_cast<const uint16_t *>(a.table + (int64_t)id * a.row_bytes);
-    float v[UPL][8];
+    // a row of one round keeps its raw blocks (5 registers per unit) and
+    // dequantises them again for h: the same bits as the first time
+    uint32_t dq[UPL], w[UPL][4];
     float ss = 0.0f;
     for (int u0 = 0; u0 < nu; u0 += CUCA_WAVE * UPL) {
-        uint32_t dq[UPL], w[UPL][4];
         embed_load<QT, UPL>(s16, u0, lane, nu, dq, w);
 #pragma unroll
         for (int k = 0; k < UPL; k++) {
             const int u = u0 + lane + CUCA_WAVE * k;
-            embed_dequant<QT>(u, dq[k], w[k], a.scale, v[k]);
+            float v[8];
+            embed_dequant<QT>(u, dq[k], w[k], a.scale, v);
             if (u < nu) {
-                embed_store<OutT>(orow, u, v[k]);
+                embed_store<OutT>(orow, u, v);
 #pragma unroll
                 for (int j = 0; j < 8; j++) {
-                    v[k][j] = Chunk<OutT>::as_stored(v[k][j]);
-                    ss += v[k][j] * v[k][j];
+                    const float x = Chunk<OutT>::as_stored(v[j]);
+                    ss += x * x;
                 }
             }
         }
@@ -280,39 +282,116 @@ __device__ static inline void embed_rms_body(const EmbedArgs &a) {
     ss = group_sum<CUCA_WAVE>(ss);
     const float inv = 1.0f / sqrtf(ss / (float)a.hidden + a.rms_eps);
     for (int u0 = 0; u0 < nu; u0 += CUCA_WAVE * UPL) {
-        if (!one_round) {
-            uint32_t dq[UPL], w[UPL][4];
-            embed_load<QT, UPL>(s16, u0, lane, nu, dq, w);
+        if (!one_round) embed_load<QT, UPL>(s16, u0, lane, nu, dq, w);
+        if ((!one_round || !PRE) && a.rms_w) {
 #pragma unroll
             for (int k = 0; k < UPL; k++) {
-                embed_dequant<QT>(u0 + lane + CUCA_WAVE * k, dq[k], w[k], a.scale, v[k]);
-#pragma unroll
-                for (int j = 0; j < 8; j++) v[k][j] = Chunk<OutT>::as_stored(v[k][j]);
-            }
-        }
-        if ((!one_round || !PRE) && a.rms_w) {
-            {
-#pragma unroll
-                for (int k = 0; k < UPL; k++) {
-                    int u = u0 + lane + CUCA_WAVE * k;
-                    u = u < nu ? u : 0;
-                    const f32x4 *wp = reinterpret_cast<const f32x4 *>(a.rms_w) + 2 * u;
-                    const f32x4 w0 = wp[0], w1 = wp[1];
-                    wv[k][0] = w0.x; wv[k][1] = w0.y; wv[k][2] = w0.z; wv[k][3] = w0.w;
-                    wv[k][4] = w1.x; wv[k][5] = w1.y; wv[k][6] = w1.z; wv[k][7] = w1.w;
-                }
+                int u = u0 + lane + CUCA_WAVE * k;
+                u = u < nu ? u : 0;
+                const f32x4 *wp = reinterpret_cast<const f32x4 *>(a.rms_w) + 2 * u;
+                const f32x4 w0 = wp[0], w1 = wp[1];
+                wv[k][0] = w0.x; wv[k][1] = w0.y; wv[k][2] = w0.z; wv[k][3] = w0.w;
+                wv[k][4] = w1.x; wv[k][5] = w1.y; wv[k][6] = w1.z; wv[k][7] = w1.w;
             }
         }
 #pragma unroll
         for (int k = 0; k < UPL; k++) {
             const int u = u0 + lane + CUCA_WAVE * k;
-            float y[8];
+            float v[8], y[8];
+            embed_dequant<QT>(u, dq[k], w[k], a.scale, v);
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = Chunk<OutT>::as_stored(v[j]);
             if (a.rms_w) {
 #pragma unroll
-                for (int j = 0; j < 8; j++) y[j] = pin_f32(pin_f32(v[k][j] * inv) * wv[k][j]);
+                for (int j = 0; j < 8; j++) y[j] = pin_f32(pin_f32(v[j] * inv) * wv[k][j]);
             } else {
 #pragma unroll
-                for (int j = 0; j < 8; j++) y[j] = pin_f32(v[k][j] * inv);
+                for (int j = 0; j < 8; j++) y[j] = pin_f32(v[j] * inv);
+            }
+            if (u < nu) embed_store<OutT>(hrow, u, y);
+        }
+    }
+}
+
+// The fused gather for many tokens: the norm weights staged in LDS once per
+// workgroup, each wave looping over a.tpw tokens.  Lane l owns the units l,
+// l + 64, ... (UPL of them, one round: hidden <= 512 UPL) and keeps only
+// their raw blocks between the two passes, dequantising again for h (the
+// same bits as the first time).  A token's weights come from LDS, not from
+// the L2 (16 KB per token at hidden 4096, as many bytes as the token's
+// output), and the small register set keeps 7 waves per SIMD.
+template <int QT, typename OutT, int UPL>
+__device__ static inline void embed_rms_lds_body(const EmbedArgs &a) {
+    extern __shared__ float wsh[]; // [hidden]
+    const int lane = threadIdx.x & (CUCA_WAVE - 1), wave = threadIdx.x / CUCA_WAVE;
+    const int nu = a.hidden / 8;
+    const bool has_w = a.rms_w != nullptr;
+    if (has_w) {
+        const f32x4 *src = reinterpret_cast<const f32x4 *>(a.rms_w);
+        f32x4 *dst = reinterpret_cast<f32x4 *>(wsh);
+        for (int i = threadIdx.x; i < a.hidden / 4; i += CUCA_BLOCK) dst[i] = src[i];
+        __syncthreads();
+    }
+    constexpr int WPB = CUCA_BLOCK / CUCA_WAVE;
+    for (int it = 0; it < a.tpw; it++) {
+        // consecutive waves of a workgroup on consecutive tokens
+        const int tok = (blockIdx.x * a.tpw + it) * WPB + wave;
+        if (tok >= a.n) return; // the wave's later tokens are further on
+        OutT *orow = reinterpret_cast<OutT *>(a.out) + (int64_t)tok * a.hidden;
+        OutT *hrow = reinterpret_cast<OutT *>(a.h_out) + (int64_t)tok * a.hidden;
+        const uint32_t id = a.ids[tok];
+        if ((int64_t)id >= a.vocab) {
+            embed_bad_id<OutT>(a, orow, tok, id, lane);
+            float z[Chunk<OutT>::N];
+#pragma unroll
+            for (int i = 0; i < Chunk<OutT>::N; i++) z[i] = 0.0f;
+            constexpr int CPU = 8 / Chunk<OutT>::N;
+            for (int c = lane; c < nu * CPU; c += CUCA_WAVE) Chunk<OutT>::store_nt(hrow, c, z);
+            continue;
+        }
+        const uint16_t *s16 = reinterpret_cast<const uint16_t *>(a.table + (int64_t)id * a.row_bytes);
+        uint32_t dq[UPL], w[UPL][4];
+        embed_load<QT, UPL>(s16, 0, lane, nu, dq, w);
+        float ss = 0.0f;
+#pragma unroll
+        for (int k = 0; k < UPL; k++) {
+            const int u = lane + CUCA_WAVE * k;
+            float v[8];
+            embed_dequant<QT>(u, dq[k], w[k], a.scale, v);
+            if (u < nu) {
+                embed_store<OutT>(orow, u, v);
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float x = Chunk<OutT>::as_stored(v[j]);
+                    ss += x * x;
+                }
+            }
+        }
+        ss = group_sum<CUCA_WAVE>(ss);
+        const float inv = 1.0f / sqrtf(ss / (float)a.hidden + a.rms_eps);
+        // opaque to the compiler, so the second dequantisation is computed
+        // again instead of keeping the first pass's 8 UPL values live
+#pragma unroll
+        for (int k = 0; k < UPL; k++) {
+            asm volatile("" : "+v"(dq[k]));
+#pragma unroll
+            for (int j = 0; j < 4; j++) asm volatile("" : "+v"(w[k][j]));
+        }
+#pragma unroll
+        for (int k = 0; k < UPL; k++) {
+            const int u = lane + CUCA_WAVE * k;
+            float v[8], y[8];
+            embed_dequant<QT>(u, dq[k], w[k], a.scale, v);
+            if (has_w) {
+                const int ul = u < nu ? u : 0;
+                const f32x4 w0 = reinterpret_cast<const f32x4 *>(wsh)[2 * ul];
+                const f32x4 w1 = reinterpret_cast<const f32x4 *>(wsh)[2 * ul + 1];
+                const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+                for (int j = 0; j < 8; j++) y[j] = pin_f32(pin_f32(Chunk<OutT>::as_stored(v[j]) * inv) * wv[j]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; j++) y[j] = pin_f32(Chunk<OutT>::as_stored(v[j]) * inv);
             }
             if (u < nu) embed_store<OutT>(hrow, u, y);
         }
@@ -426,6 +505,10 @@ CUCA_EMBED_TPR_SET(cuca_embed_q8_0_f16, 8, _Float16)
     extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void NAME(EmbedArgs a) {           \
         BODY<QT, OUT, UPL>(a);                                                             \
     }
+#define CUCA_EMBED_LDS(NAME, QT, OUT, UPL)                                                 \
+    extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void NAME(EmbedArgs a) {           \
+        embed_rms_lds_body<QT, OUT, UPL>(a);                                               \
+    }
 #define CUCA_EMBED_SET(NAME, QT, OUT)                                                      \
     CUCA_EMBED(NAME##_u1, embed_body, QT, OUT, 1)                                          \
     CUCA_EMBED(NAME##_u2, embed_body, QT, OUT, 2)                                          \
@@ -438,7 +521,10 @@ CUCA_EMBED_TPR_SET(cuca_embed_q8_0_f16, 8, _Float16)
     CUCA_EMBED(NAME##_rms_u1, embed_rms_body, QT, OUT, 1)                                  \
     CUCA_EMBED(NAME##_rms_u2, embed_rms_body, QT, OUT, 2)                                  \
     CUCA_EMBED(NAME##_rms_u4, embed_rms_body, QT, OUT, 4)                                  \
-    CUCA_EMBED(NAME##_rms_u8, embed_rms_body, QT, OUT, 8)
+    CUCA_EMBED(NAME##_rms_u8, embed_rms_body, QT, OUT, 8)                                  \
+    CUCA_EMBED_LDS(NAME##_rms_lds_u2, QT, OUT, 2)                                          \
+    CUCA_EMBED_LDS(NAME##_rms_lds_u4, QT, OUT, 4)                                          \
+    CUCA_EMBED_LDS(NAME##_rms_lds_u8, QT, OUT, 8)
 
 CUCA_EMBED_SET(cuca_embed_q4_0_f32, 2, float)
 CUCA_EMBED_SET(cuca_embed_q4_0_f16, 2, _Float16)

@@ -478,6 +478,26 @@ static cuca_status embed_common(cuca_hip_ctx *ctx, const void *table, uint32_t g
     a.rms_w = rms_w;
     a.rms_eps = rms_eps;
     ctx->last_vocab = vocab;
+    // [q8][f16][u2, u4, u8]
+    static const Kernel table_l[2][2][3] = {
+        {{cuca_embed_q4_0_f32_rms_lds_u2, cuca_embed_q4_0_f32_rms_lds_u4, cuca_embed_q4_0_f32_rms_lds_u8},
+         {cuca_embed_q4_0_f16_rms_lds_u2, cuca_embed_q4_0_f16_rms_lds_u4, cuca_embed_q4_0_f16_rms_lds_u8}},
+        {{cuca_embed_q8_0_f32_rms_lds_u2, cuca_embed_q8_0_f32_rms_lds_u4, cuca_embed_q8_0_f32_rms_lds_u8},
+         {cuca_embed_q8_0_f16_rms_lds_u2, cuca_embed_q8_0_f16_rms_lds_u4, cuca_embed_q8_0_f16_rms_lds_u8}}};
+    // Beyond 8192 tokens (rows of up to 512 units per lane round) the fused
+    // norm stages its weights in LDS once per workgroup and each wave loops
+    // over tpw tokens (about 1024 workgroups, 4 per CU).  Measured in the
+    // config C prefill step at 16384 tokens on MI355X: 65.8 us against 72-73
+    // for the wave-per-token kernel (tpw 1: 67.6, 2: 67.0, 4: 65.8); at 4096
+    // and 8192 tokens it is slower than the workgroup-per-token kernel (18.1
+    // against 15.3, 17.1 against 15.5 us), too few tokens per CU to hide
+    // the staging.
+    if (mode == 2 && per_lane <= 8 && n > 8192) {
+        const int li = per_lane <= 2 ? 0 : per_lane <= 4 ? 1 : 2;
+        a.tpw = (int32_t)std::max<int64_t>(1, std::min<int64_t>(8, n / 4096));
+        return launch(ctx, table_l[ggml_type == CUCA_GGML_Q8_0][f16][li], div_up(n, 4 * a.tpw), 256,
+                      rms_w ? (unsigned)(hidden * 4) : 0u, a);
+    }
     if (tpr_i >= 0)
         return launch(ctx, table_t[ggml_type == CUCA_GGML_Q8_0][f16][tpr_i], (unsigned)n, (unsigned)tpr, 0, a);
     return launch(ctx, k, div_up(n, 4), 256, 0, a); // 4 waves, one token each

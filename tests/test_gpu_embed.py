@@ -244,21 +244,47 @@ def test_embed_rms_matches_gather_then_norm(ctx, qname, out, hidden, eps, scale,
 
 
 @pytest.mark.parametrize("out", [np.float32, np.float16])
-def test_embed_rms_many_tokens_wave_kernel(ctx, out):
-    """More than 8192 tokens take the wave-per-token kernel."""
+@pytest.mark.parametrize("hidden,n,weighted,bad", [
+    (256, 8200, True, False), (256, 20001, False, False), (2048, 8200, True, True), (4096, 8193, True, False),
+    (4096, 9000, False, True), (4128, 8200, True, False)])
+def test_embed_rms_many_tokens(ctx, out, hidden, n, weighted, bad):
+    """More than 8192 tokens take the LDS-staged kernel (weights in LDS once
+    per workgroup, each wave looping over tpw tokens: 2 at 8200 tokens, 4 at
+    20001, the last workgroup partial) for rows of up to 4096; wider rows the
+    wave-per-token kernel.  An id outside the table gives zero rows of x and
+    h and is reported, the other rows unchanged."""
     from helpers import assert_close
-    rng = np.random.default_rng(5)
-    vocab, hidden = 64, 256
-    table = W.quant_table(rng, vocab, hidden, "q4_0", (0.001, 0.05))
-    ids = rng.integers(0, vocab, 8200).astype(np.uint32)
-    w = (1 + 0.02 * rng.standard_normal(hidden)).astype(np.float32)
-    emb = ops.TokenEmbedding(ctx, hip.GGML_Q4_0, table, vocab, hidden)
-    x, h = emb.rows_rms(ids, 1.0, w, 1e-6, out_dtype=out)
-    ctx.check_device()
-    want_x = O.embed(table, hip.GGML_Q4_0, vocab, hidden, ids, 1.0, out_dtype=out)
-    assert_bits_equal(x.numpy(), want_x, "wave kernel x")
+    rng = np.random.default_rng(hidden + n)
+    vocab = 64
+    qname = "q8_0" if hidden == 4096 else "q4_0"
+    ty = W.GGML_ID[qname]
+    table = W.quant_table(rng, vocab, hidden, qname, (0.001, 0.05))
+    ids = rng.integers(0, vocab, n).astype(np.uint32)
+    if bad:
+        ids[n // 3] = vocab + 7
+    w = (1 + 0.02 * rng.standard_normal(hidden)).astype(np.float32) if weighted else None
+    emb = ops.TokenEmbedding(ctx, ty, table, vocab, hidden)
+    dids = ctx.array(ids)
+    x = ctx.empty((n, hidden), out)
+    h = ctx.empty((n, hidden), out)
+    dw = ctx.array(w) if weighted else None
+    ctx.embed_gguf_rms(emb.table.ptr, ty, vocab, hidden, dids.ptr, n, 1.0, dw.ptr if weighted else None, 1e-6,
+                       x.ptr, h.ptr, hip.F32 if out == np.float32 else hip.F16)
+    if bad:
+        with pytest.raises(hip.CucaError, match=f"token id {vocab + 7} outside"):
+            ctx.check_device()
+    else:
+        ctx.check_device()
+    good = np.ones(n, bool)
+    if bad:
+        good[n // 3] = False
+        assert np.all(x.numpy()[n // 3] == 0) and np.all(h.numpy()[n // 3] == 0)
+    ids_ok = np.where(good, ids, 0).astype(np.uint32)
+    want_x = O.embed(table, ty, vocab, hidden, ids_ok, 1.0, out_dtype=out)[good]
+    xs, hs = x.numpy()[good], h.numpy()[good]
+    assert_bits_equal(xs, want_x, f"many tokens x {hidden} {n}")
     _, want_h = O.add_rmsnorm(want_x, None, w, 1e-6, write_x=False)
-    assert_close(h.numpy(), want_h, what="wave kernel h")
+    assert_close(hs, want_h, what=f"many tokens h {hidden} {n}")
 
 
 def test_embed_rms_bad_id_and_checks(ctx):
