@@ -1272,14 +1272,24 @@ def cpu_baseline(st, seconds=12.0):
                        f"{avail} available, {model}")
 
 
-def traffic_from_profiles():
-    """HBM bytes per SwiGLU launch measured by rocprofv3 --pmc (FETCH_SIZE,
-    WRITE_SIZE, scaled by a copy kernel's reading), when that summary exists."""
+def traffic_from_profiles(kernel):
+    """HBM bytes per launch of the roofline kernel measured by rocprofv3
+    --pmc (FETCH_SIZE, WRITE_SIZE, scaled by a copy kernel's reading), from
+    the committed summary -- but only while the kernel's machine code is the
+    code that was measured (the summary records its SHA-256): (bytes or
+    None, why None)."""
+    from cuca_amd import build
     p = os.path.join(ROOT, "profiles", "swiglu_traffic.json")
     if not os.path.exists(p):
-        return None
+        return None, "no traffic summary"
     with open(p) as f:
-        return json.load(f).get("hbm_bytes_per_launch")
+        rec = json.load(f)
+    if rec.get("kernel") != kernel:
+        return None, f"the summary measured {rec.get('kernel')}, the roofline kernel is {kernel}"
+    now = build.kernel_code_sha256(kernel)
+    if now is None or now != rec.get("code_sha256"):
+        return None, "the kernel's code changed since the counters were read"
+    return rec.get("hbm_bytes_per_launch"), None
 
 
 def main():
@@ -1445,6 +1455,9 @@ def main():
                 decode[key] = decode_step_bench(ctx, torch, n, clen, mm=mm, fuse_rope=fuse)
             torch.cuda.empty_cache()
 
+    traffic, why = traffic_from_profiles(glu["kernel"])
+    traffic_src = ("profiles/swiglu_traffic.json (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; same kernel code)"
+                   if traffic is not None else why)
     out = {
         "metric": "fused layer-op HBM GB/s & % of 8 TB/s peak; per-layer non-matmul us at decode",
         "value": round(value, 1),
@@ -1480,7 +1493,8 @@ def main():
         "decode_us_per_layer": decode,
         "roofline": {"kernel": glu["kernel"], "bound": "hbm",
                      "achieved": glu["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": glu["frac"], "traffic": traffic_from_profiles(),
+                     "frac": glu["frac"], "traffic": traffic,
+                     "traffic_source": traffic_src,
                      "algorithmic_bytes_per_launch": glu["bytes"], "avg_launch_us": glu["us"]},
         "cpu_baseline": cpu,
     }

@@ -74,6 +74,39 @@ def code_object_kernels(path):
     return syms
 
 
+def kernel_code_sha256(name, path=CODE_OBJECT):
+    """SHA-256 of one kernel's machine code in the code object (its function
+    symbol's bytes in the ELF), or None when the object or the symbol is
+    missing.  A measurement recorded against a kernel names this hash, so
+    it can be recognised as stale once the kernel's code changes."""
+    import hashlib
+    import struct
+    try:
+        with open(path, "rb") as f:
+            elf = f.read()
+    except OSError:
+        return None
+    if elf[:4] != b"\x7fELF" or elf[4] != 2:  # 64-bit ELF
+        return None
+    shoff, = struct.unpack_from("<Q", elf, 0x28)
+    shentsize, shnum = struct.unpack_from("<HH", elf, 0x3A)
+    secs = [struct.unpack_from("<IIQQQQIIQQ", elf, shoff + i * shentsize) for i in range(shnum)]
+    for sec in secs:
+        if sec[1] != 2:  # SHT_SYMTAB
+            continue
+        strtab = secs[sec[6]]
+        for off in range(sec[4], sec[4] + sec[5], sec[9]):
+            st_name, st_info, _, st_shndx, st_value, st_size = struct.unpack_from("<IBBHQQ", elf, off)
+            start = strtab[4] + st_name
+            end = elf.index(b"\0", start)
+            if elf[start:end].decode() != name or (st_info & 0xF) != 2 or st_shndx >= shnum:  # STT_FUNC
+                continue
+            text = secs[st_shndx]
+            pos = text[4] + (st_value - text[3])  # file offset: sh_offset + (value - sh_addr)
+            return hashlib.sha256(elf[pos:pos + st_size]).hexdigest()
+    return None
+
+
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     co_tmp = CODE_OBJECT + ".tmp"
