@@ -44,6 +44,15 @@ typedef struct {
                                workgroup of 4 waves covers 4 tpw tokens   */
 } EmbedArgs;
 
+/* Self-test of the wave reductions (cuca_selftest_group_sum): out holds 12
+ * arrays of n: for each group size 2, 4, ..., 64 the library's group_sum,
+ * then the __shfl_xor butterfly, of in[i] over its aligned group. */
+typedef struct {
+    const float *in;
+    float *out;
+    int64_t n;
+} SelftestArgs;
+
 typedef struct {
     const void *x;          /* [rows, hidden]                              */
     const void *branch;     /* [rows, hidden] or NULL                      */

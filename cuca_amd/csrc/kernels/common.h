@@ -140,14 +140,65 @@ template <typename T> __device__ static inline void store1(void *p, int64_t i, f
 // at every step lane i adds lane i^off, and float addition is commutative,
 // so every lane of a group ends with the same bits; the order is fixed by
 // the lane layout alone, so a row's result never depends on its neighbours.
+//
+// Each step takes lane i ^ off's value without a trip through LDS memory
+// (__shfl_xor compiles to ds_bpermute, an LDS-pipe round trip per step):
+//   off 32, 16: v_permlane32_swap / v_permlane16_swap (gfx950) of v with
+//               itself give each lane its own value and its partner's, in
+//               one order or the other (a + b == b + a in IEEE arithmetic);
+//   off 8:      DPP row_ror:8 (rotating a 16-lane row by 8 is xor 8);
+//   off 4:      ds_swizzle in bit mode (xor 4 within 32 lanes);
+//   off 2, 1:   DPP quad_perm [2,3,0,1] / [1,0,3,2].
+// The partner and the order are the butterfly's, so the bits are those of
+// the __shfl_xor form.  Every lane of the group must be active.
+template <int OFF> __device__ static inline float xor_add(float v) {
+    const int b = __builtin_bit_cast(int, v);
+    if constexpr (OFF == 32) {
+        const auto r = __builtin_amdgcn_permlane32_swap(b, b, false, false);
+        return __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
+    } else if constexpr (OFF == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+        return __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
+    } else if constexpr (OFF == 8) {
+        return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, b, 0x128, 0xF, 0xF, false));
+    } else if constexpr (OFF == 4) {
+        return v + __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(b, 0x1F | (4 << 10)));
+    } else if constexpr (OFF == 2) {
+        return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, b, 0x4E, 0xF, 0xF, false));
+    } else {
+        static_assert(OFF == 1, "xor offsets 1 to 32");
+        return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, b, 0xB1, 0xF, 0xF, false));
+    }
+}
+
 template <int G> __device__ static inline float group_sum(float v) {
-#pragma unroll
-    for (int off = G / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, CUCA_WAVE);
+    if constexpr (G >= 64) v = xor_add<32>(v);
+    if constexpr (G >= 32) v = xor_add<16>(v);
+    if constexpr (G >= 16) v = xor_add<8>(v);
+    if constexpr (G >= 8) v = xor_add<4>(v);
+    if constexpr (G >= 4) v = xor_add<2>(v);
+    if constexpr (G >= 2) v = xor_add<1>(v);
     return v;
 }
 
+// g a power of two up to 64, uniform over the wave
 __device__ static inline float group_sum_rt(float v, int g) {
-    for (int off = g / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, CUCA_WAVE);
+    switch (g) {
+    case 64: return group_sum<64>(v);
+    case 32: return group_sum<32>(v);
+    case 16: return group_sum<16>(v);
+    case 8: return group_sum<8>(v);
+    case 4: return group_sum<4>(v);
+    case 2: return group_sum<2>(v);
+    default: return v;
+    }
+}
+
+// The reference form of group_sum (kept for the test kernel that checks
+// the two give the same bits).
+template <int G> __device__ static inline float group_sum_shfl(float v) {
+#pragma unroll
+    for (int off = G / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, CUCA_WAVE);
     return v;
 }
 

@@ -242,3 +242,23 @@ CUCA_NORM_SET(f16, _Float16)
 // 8 chunks per thread: f32 rows of up to 32768 values fit in registers; f16
 // rows that wide would spill and take the generic kernel.
 CUCA_NORM(cuca_norm_f32_t1024_c8, float, 1024, 8, false)
+
+// Self-test of group_sum: every group size, the library's reduction and the
+// __shfl_xor butterfly side by side (the two must give the same bits).
+extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void cuca_selftest_group_sum(SelftestArgs a) {
+    const int64_t i = (int64_t)blockIdx.x * CUCA_BLOCK + threadIdx.x; // n is a multiple of 256
+    const float v = a.in[i];
+    float *o = a.out;
+    o[0 * a.n + i] = group_sum<2>(v);
+    o[1 * a.n + i] = group_sum_shfl<2>(v);
+    o[2 * a.n + i] = group_sum<4>(v);
+    o[3 * a.n + i] = group_sum_shfl<4>(v);
+    o[4 * a.n + i] = group_sum<8>(v);
+    o[5 * a.n + i] = group_sum_shfl<8>(v);
+    o[6 * a.n + i] = group_sum<16>(v);
+    o[7 * a.n + i] = group_sum_shfl<16>(v);
+    o[8 * a.n + i] = group_sum<32>(v);
+    o[9 * a.n + i] = group_sum_shfl<32>(v);
+    o[10 * a.n + i] = group_sum<64>(v);
+    o[11 * a.n + i] = group_sum_shfl<64>(v);
+}

@@ -645,6 +645,19 @@ cuca_status cuca_hip_add_rmsnorm(cuca_hip_ctx *ctx, const void *x, const void *b
     return launch(ctx, k, div_up(rows, rows_per_block), tpr > 64 ? (unsigned)tpr : 256u, 0, a);
 }
 
+cuca_status cuca_hip_selftest_group_sum(cuca_hip_ctx *ctx, const float *input, int64_t n, float *out) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    if (n <= 0 || n % 256 != 0 || n > (1ll << 30))
+        return fail(ctx, CUCA_INVALID_ARG, "self-test length %lld must be a positive multiple of 256", (long long)n);
+    if (!input || !out) return fail(ctx, CUCA_INVALID_ARG, "null pointer");
+    SelftestArgs a{};
+    a.in = input;
+    a.out = out;
+    a.n = n;
+    return launch(ctx, cuca_selftest_group_sum, (unsigned)(n / 256), 256, 0, a);
+}
+
 // ---------------------------------------------------------------------
 // gated activation
 // ---------------------------------------------------------------------

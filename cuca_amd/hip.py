@@ -57,6 +57,7 @@ SIGNATURES = {
     "cuca_hip_memcpy_d2d_async": (_st, [_p, _p, _p, _sz]),
     "cuca_hip_stream_sync": (_st, [_p]),
     "cuca_hip_check_device": (_st, [_p]),
+    "cuca_hip_selftest_group_sum": (_st, [_p, _p, _i64, _p]),
     "cuca_hip_embed_gguf": (_st, [_p, _p, _u32, _i64, _i64, _p, _i64, _f32, _p, _st]),
     "cuca_hip_embed_gguf_norm": (_st, [_p, _p, _u32, _i64, _i64, _p, _i64, _f32, _f32, _p, _st]),
     "cuca_hip_embed_gguf_rms": (_st, [_p, _p, _u32, _i64, _i64, _p, _i64, _f32, _p, _f32, _p, _p, _st]),
@@ -272,6 +273,9 @@ class Context:
 
     def check_device(self):
         self.check(self.L.cuca_hip_check_device(self.ptr))
+
+    def selftest_group_sum(self, inp, n, out):
+        self.check(self.L.cuca_hip_selftest_group_sum(self.ptr, inp, n, out))
 
     def array(self, arr, dtype=None):
         """Upload a numpy array."""

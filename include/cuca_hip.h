@@ -140,6 +140,13 @@ cuca_status cuca_hip_stream_sync(cuca_hip_ctx *ctx);
  * its pool). */
 cuca_status cuca_hip_check_device(cuca_hip_ctx *ctx);
 
+/* Self-test of the kernels' wave reductions (no counterpart in the
+ * reference): for input[n] (n a positive multiple of 256) writes out[12 * n],
+ * for each group size 2, 4, ..., 64 the sum of each value's aligned group
+ * as the kernels compute it (DPP, swizzle and permlane partners) and as the
+ * __shfl_xor butterfly computes it; the two must agree bit for bit. */
+cuca_status cuca_hip_selftest_group_sum(cuca_hip_ctx *ctx, const float *input, int64_t n, float *out);
+
 /* ------------------------------------------------------------------ */
 /* Ops                                                                  */
 /* ------------------------------------------------------------------ */

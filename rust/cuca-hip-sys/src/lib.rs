@@ -118,6 +118,12 @@ extern "C" {
     ) -> cuca_status;
     pub fn cuca_hip_stream_sync(ctx: *mut cuca_hip_ctx) -> cuca_status;
     pub fn cuca_hip_check_device(ctx: *mut cuca_hip_ctx) -> cuca_status;
+    pub fn cuca_hip_selftest_group_sum(
+        ctx: *mut cuca_hip_ctx,
+        input: *const f32,
+        n: i64,
+        out: *mut f32,
+    ) -> cuca_status;
     pub fn cuca_hip_embed_gguf(
         ctx: *mut cuca_hip_ctx,
         table: *const c_void,

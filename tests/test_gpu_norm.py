@@ -13,7 +13,7 @@ kernel, misaligned buffers) and the full config C size on sampled rows.
 import numpy as np
 import pytest
 
-from cuca_amd import ops
+from cuca_amd import hip, ops
 from helpers import assert_bits_equal, assert_close
 from oracle import oracle as O
 
@@ -137,3 +137,32 @@ def test_full_size_config_c_sampled_rows(ctx):
     wx, wh = O.add_rmsnorm(xs, bs, w.cpu().numpy(), 1e-5)
     assert_bits_equal(xo[sample].cpu().numpy(), wx)
     assert_close(h[sample].cpu().numpy(), wh)
+
+
+def test_group_sum_matches_shfl_butterfly(ctx):
+    """The kernels' wave reductions (DPP, ds_swizzle and permlane partners)
+    give the bits of the __shfl_xor butterfly (partner i ^ off, off = g/2
+    down to 1) for every group size, and both equal that butterfly in numpy
+    f32: values spread over 2^-40..2^40 so the order of the additions shows,
+    with denormals, signed zeros and overflow to infinity."""
+    rng = np.random.default_rng(3)
+    n = 1 << 16
+    x = (rng.standard_normal(n) * np.exp2(rng.integers(-40, 40, n))).astype(np.float32)
+    x[0:4] = [0.0, -0.0, 1e-45, -1e-45]
+    x[64:66] = [3.4e38, 3.4e38]           # a group that overflows to +inf
+    x[128] = -np.inf
+    dx = ctx.array(x)
+    out = ctx.empty((12, n), np.float32)
+    ctx.selftest_group_sum(dx.ptr, n, out.ptr)
+    o = out.numpy()
+    with np.errstate(over="ignore"):
+        for gi, g in enumerate((2, 4, 8, 16, 32, 64)):
+            want = x.copy()
+            off = g // 2
+            while off >= 1:
+                want = (want + want[np.arange(n) ^ off]).astype(np.float32)
+                off //= 2
+            assert_bits_equal(o[2 * gi + 1], want, f"shfl butterfly, groups of {g}")
+            assert_bits_equal(o[2 * gi], want, f"group_sum, groups of {g}")
+    with pytest.raises(hip.CucaError, match="multiple of 256"):
+        ctx.selftest_group_sum(dx.ptr, 100, out.ptr)
