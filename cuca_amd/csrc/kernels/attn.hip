@@ -54,7 +54,7 @@ __device__ static inline f16x2 as_h2(uint32_t u) { return __builtin_bit_cast(f16
 
 __device__ static inline float wave_max(float v) {
 #pragma unroll
-    for (int off = CUCA_WAVE / 2; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, CUCA_WAVE));
+    for (int off = CUCA_WAVE / 2; off >= 1; off >>= 1) v = fmaxf(v, xor_partner(v, off));
     return v;
 }
 
@@ -223,7 +223,7 @@ __device__ static inline void attn_split_body(const AttnArgs &a) {
 #pragma unroll
     for (int g = 0; g < G; g++)
 #pragma unroll
-        for (int off = 1; off < LPP; off <<= 1) s[g] += __shfl_xor(s[g], off, CUCA_WAVE);
+        for (int off = 1; off < LPP; off <<= 1) s[g] += xor_partner(s[g], off);
 
     // the wave's softmax pieces; the weights go to LDS for every lane
     float m[G], sum[G];

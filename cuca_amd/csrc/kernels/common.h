@@ -171,6 +171,31 @@ template <int OFF> __device__ static inline float xor_add(float v) {
     }
 }
 
+// The bits of lane i ^ off's value, for off a power of two up to 32 known
+// at compile time (after unrolling), every lane of the wave active: DPP
+// quad_perm (1, 2) and row_ror:8 (8), ds_swizzle in bit mode (4, 16), and
+// v_permlane32_swap plus a select (32), in place of __shfl_xor's
+// ds_bpermute.  The caller combines the partner with its own value in the
+// order it always did, so results keep their bits whatever the operation.
+__device__ static inline uint32_t xor_partner_bits(uint32_t b, int off) {
+    const int x = (int)b;
+    switch (off) {
+    case 1: return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0xB1, 0xF, 0xF, false);
+    case 2: return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x4E, 0xF, 0xF, false);
+    case 4: return (uint32_t)__builtin_amdgcn_ds_swizzle(x, 0x1F | (4 << 10));
+    case 8: return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x128, 0xF, 0xF, false);
+    case 16: return (uint32_t)__builtin_amdgcn_ds_swizzle(x, 0x1F | (16 << 10));
+    default: {
+        const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+        return (uint32_t)(__lane_id() < 32 ? r[1] : r[0]);
+    }
+    }
+}
+
+__device__ static inline float xor_partner(float v, int off) {
+    return __builtin_bit_cast(float, xor_partner_bits(__builtin_bit_cast(uint32_t, v), off));
+}
+
 template <int G> __device__ static inline float group_sum(float v) {
     if constexpr (G >= 64) v = xor_add<32>(v);
     if constexpr (G >= 32) v = xor_add<16>(v);

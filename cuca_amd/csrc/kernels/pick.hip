@@ -59,8 +59,8 @@ __device__ static inline u64 argmax_pack(float v, uint32_t id) {
 __device__ static inline void argmax_wave(float &best, uint32_t &bi) {
 #pragma unroll
     for (int off = CUCA_WAVE / 2; off >= 1; off >>= 1) {
-        const float ov = __shfl_xor(best, off, CUCA_WAVE);
-        const uint32_t oi = (uint32_t)__shfl_xor((int)bi, off, CUCA_WAVE);
+        const float ov = xor_partner(best, off);
+        const uint32_t oi = xor_partner_bits(bi, off);
         argmax_merge(best, bi, ov, oi);
     }
 }
@@ -141,7 +141,7 @@ __device__ static inline int pick_nonzero(PickLds &L, const u64 (&e)[PICK_PER]) 
 #pragma unroll
     for (int i = 0; i < PICK_PER; i++) n += e[i] != 0ull;
 #pragma unroll
-    for (int off = CUCA_WAVE / 2; off >= 1; off >>= 1) n += __shfl_xor(n, off, CUCA_WAVE);
+    for (int off = CUCA_WAVE / 2; off >= 1; off >>= 1) n += (int)xor_partner_bits((uint32_t)n, off);
     if ((threadIdx.x & (CUCA_WAVE - 1)) == 0 && n) atomicAdd(&L.count, n);
     __syncthreads();
     const int r = L.count;

@@ -141,8 +141,8 @@ __device__ static inline void qmd_body(const QmmArgs &a) {
             float amax = 0.0f;
 #pragma unroll
             for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(xv[it][e]));
-            amax = fmaxf(amax, __shfl_xor(amax, 1, CUCA_WAVE));
-            amax = fmaxf(amax, __shfl_xor(amax, 2, CUCA_WAVE));
+            amax = fmaxf(amax, xor_partner(amax, 1));
+            amax = fmaxf(amax, xor_partner(amax, 2));
             const float d = amax / 127.0f;
             const float id = d != 0.0f ? 1.0f / d : 0.0f;
             uint32_t own[4], other[4];
@@ -150,7 +150,7 @@ __device__ static inline void qmd_body(const QmmArgs &a) {
             for (int i = 0; i < 4; i++) {
                 own[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(qmm_quant(xv[it][2 * i] * id),
                                                                                  qmm_quant(xv[it][2 * i + 1] * id)));
-                other[i] = (uint32_t)__shfl_xor((int)own[i], 2, CUCA_WAVE);
+                other[i] = xor_partner_bits(own[i], 2);
             }
             if (item < nitems) {
                 // threads 0/1 own elements 0-7 / 8-15, threads 2/3 16-23 /

@@ -228,8 +228,8 @@ __device__ static inline void qmm_stage_a(const QmmArgs &a, QmmLds<MT, GLU> &L, 
         float amax = 0.0f;
 #pragma unroll
         for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(p.x[it][e]));
-        amax = fmaxf(amax, __shfl_xor(amax, 1, CUCA_WAVE));
-        amax = fmaxf(amax, __shfl_xor(amax, 2, CUCA_WAVE));
+        amax = fmaxf(amax, xor_partner(amax, 1));
+        amax = fmaxf(amax, xor_partner(amax, 2));
         const float d = amax / 127.0f;
         const float id = d != 0.0f ? 1.0f / d : 0.0f;
         // own quants as f16 pairs of consecutive elements (exact integers)
@@ -238,7 +238,7 @@ __device__ static inline void qmm_stage_a(const QmmArgs &a, QmmLds<MT, GLU> &L, 
         for (int i = 0; i < 4; i++) {
             own[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(qmm_quant(p.x[it][2 * i] * id),
                                                                              qmm_quant(p.x[it][2 * i + 1] * id)));
-            other[i] = (uint32_t)__shfl_xor((int)own[i], 2, CUCA_WAVE);
+            other[i] = xor_partner_bits(own[i], 2);
         }
         // threads 0/1 own elements 0-7 / 8-15, threads 2/3 own 16-23 / 24-31;
         // sub < 2 writes lanes 8s..8s+3, sub >= 2 lanes 8s+4..8s+7 (s = sub & 1)
@@ -387,10 +387,10 @@ __device__ static inline void qmm_chunk(const QmmLds<MT, GLU> &L, int buf, int r
 
 // hsum (qmm.rs:1345-1353) over the 16 lanes of a row: xor 8, 4, 1, 2.
 __device__ static inline float qmm_hsum(float v) {
-    v = v + __shfl_xor(v, 8, CUCA_WAVE);
-    v = v + __shfl_xor(v, 4, CUCA_WAVE);
-    v = v + __shfl_xor(v, 1, CUCA_WAVE);
-    v = v + __shfl_xor(v, 2, CUCA_WAVE);
+    v = v + xor_partner(v, 8);
+    v = v + xor_partner(v, 4);
+    v = v + xor_partner(v, 1);
+    v = v + xor_partner(v, 2);
     return v;
 }
 
@@ -467,7 +467,7 @@ __device__ static inline void qmm_rope_kv_store(const QmmArgs &a, int jg, bool v
                                                 int lane, float o) {
     // the value the plain kernel stores, widened back (exact)
     const float v = (float)to_stored<T>(o);
-    const float pv = __shfl_xor(v, 16, CUCA_WAVE); // row ^ 1: the pair partner
+    const float pv = xor_partner(v, 16); // row ^ 1: the pair partner
     if (lane != 0 || row >= a.rows || !valid) return;
     const int D = a.head_dim, half = a.n_dims >> 1;
     const int h = row / D, e = row - h * D;
