@@ -106,7 +106,7 @@ __device__ static inline void load_tab(const float *t, int64_t first, float (&v)
 // LP: the load policy of the head chunks (LP_DEV, LP_NT, LP_CACHED above).
 // LP_DEV addresses a row's chunks by 32-bit byte offsets from q, k and v:
 // the host checks that rows * row stride fits.
-template <typename T, int KIND, bool NORM, bool STORE, int LP>
+template <typename T, int KIND, bool NORM, bool STORE, int LP, int HPL = 1>
 __device__ static inline void rope_body(const RopeArgs &a) {
     constexpr int VP = Chunk<T>::N;
     constexpr int NC = KIND == 2 ? 2 : 1;       // chunks per lane
@@ -116,10 +116,13 @@ __device__ static inline void rope_body(const RopeArgs &a) {
     const uint32_t gh = blockIdx.x * (uint32_t)(CUCA_BLOCK >> tl) + (threadIdx.x >> tl);
     const int u = threadIdx.x & (tph - 1);
     const int nqk = a.nq + a.nk;
+    // a lane takes HPL consecutive heads of one projection (the host checks
+    // that HPL divides nq and nk): gh counts groups of them
     const uint32_t heads = (uint32_t)(nqk + (STORE ? a.nv : 0));
-    const bool live = gh < (uint32_t)a.rows * heads;
-    const uint32_t row = live ? gh / heads : 0;
-    const int h = live ? (int)(gh - row * heads) : 0;
+    const uint32_t groups = heads / HPL;
+    const bool live = gh < (uint32_t)a.rows * groups;
+    const uint32_t row = live ? gh / groups : 0;
+    const int h = live ? (int)(gh - row * groups) * HPL : 0;
     const int hk = h < a.nq ? 0 : (h < nqk ? 1 : 2); // Q, K or V head
     const int D = a.head_dim;
     const T *src = hk == 0 ? reinterpret_cast<const T *>(a.q) + (int64_t)row * a.q_ld + (int64_t)h * D
@@ -154,7 +157,7 @@ __device__ static inline void rope_body(const RopeArgs &a) {
     // (56-63 us against 53.5 us per 16384 f16 rows of 40 heads).
     const int32_t pos = a.pos[row];
     const int32_t slot = STORE ? a.slots[row] : 0;
-    u32x4 raw[NC];
+    u32x4 raw[HPL][NC];
     if constexpr (LP == LP_DEV) {
         // the byte offset of the head in its projection; one load per
         // projection, so each resource stays wave-uniform
@@ -163,17 +166,22 @@ __device__ static inline void rope_body(const RopeArgs &a) {
                                                 : (int64_t)row * a.v_ld + (int64_t)(h - nqk) * D) *
                             (uint32_t)sizeof(T);
 #pragma unroll
-        for (int k = 0; k < NC; k++) {
-            const uint32_t off = ho + (uint32_t)(e[k] * (int)sizeof(T));
-            if (hk == 0) raw[k] = load_dev16(rsrc_4g(a.q), off);
-            else if (hk == 1) raw[k] = load_dev16(rsrc_4g(a.k), off);
-            else raw[k] = load_dev16(rsrc_4g(a.v), off);
-        }
+        for (int j = 0; j < HPL; j++)
+#pragma unroll
+            for (int k = 0; k < NC; k++) {
+                const uint32_t off = ho + (uint32_t)((j * D + e[k]) * (int)sizeof(T));
+                if (hk == 0) raw[j][k] = load_dev16(rsrc_4g(a.q), off);
+                else if (hk == 1) raw[j][k] = load_dev16(rsrc_4g(a.k), off);
+                else raw[j][k] = load_dev16(rsrc_4g(a.v), off);
+            }
     } else {
 #pragma unroll
-        for (int k = 0; k < NC; k++)
-            raw[k] = LP == LP_NT ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(src) + e[k] / VP)
-                                 : Chunk<T>::load_raw(src, e[k] / VP);
+        for (int j = 0; j < HPL; j++)
+#pragma unroll
+            for (int k = 0; k < NC; k++)
+                raw[j][k] = LP == LP_NT
+                                ? __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(src + j * D) + e[k] / VP)
+                                : Chunk<T>::load_raw(src + j * D, e[k] / VP);
     }
     const bool pos_ok = pos >= 0 && (int64_t)pos < a.table_rows;
     const bool slot_ok = !STORE || (slot >= 0 && (int64_t)slot < a.n_slots);
@@ -192,14 +200,17 @@ __device__ static inline void rope_body(const RopeArgs &a) {
     __builtin_amdgcn_sched_barrier(0); // every load above is issued first
     pin(c);
     pin(s);
+#pragma unroll
+    for (int j = 0; j < HPL; j++)
+#pragma unroll
+        for (int k = 0; k < NC; k++) pin(raw[j][k]);
+#pragma unroll
+    for (int j = 0; j < HPL; j++) {
     float v[NC][VP];
 #pragma unroll
-    for (int k = 0; k < NC; k++) {
-        pin(raw[k]);
-        Chunk<T>::widen(raw[k], v[k]);
-    }
+    for (int k = 0; k < NC; k++) Chunk<T>::widen(raw[j][k], v[k]);
     if (NORM) {
-        if (any_w) {
+        if (any_w && j == 0) {
 #pragma unroll
             for (int k = 0; k < NC; k++) pin(w[k]);
         }
@@ -243,15 +254,16 @@ __device__ static inline void rope_body(const RopeArgs &a) {
     T *dst;
     if (STORE && hk != 0) {
         // pool [n_blocks, nk, 16, d]: block slot / 16, KV head, row slot % 16
-        const int kvh = hk == 1 ? h - a.nq : h - nqk;
+        const int kvh = (hk == 1 ? h - a.nq : h - nqk) + j;
         const int64_t prow = ((int64_t)(slot >> 4) * a.nk + kvh) * 16 + (slot & 15);
         dst = reinterpret_cast<T *>(hk == 1 ? a.pool_k : a.pool_v) + prow * D;
     } else {
-        dst = const_cast<T *>(src);
+        dst = const_cast<T *>(src) + j * D;
     }
     if (live && pos_ok && slot_ok && (rot || scale_h || (STORE && hk != 0))) {
 #pragma unroll
         for (int k = 0; k < NC; k++) Chunk<T>::store_nt(dst, e[k] / VP, v[k]);
+    }
     }
     if (live && u == 0 && h == 0) {
         if (!pos_ok) record_bad(a.status + CUCA_STATUS_ROPE_POS, row, (uint32_t)pos);
@@ -478,6 +490,9 @@ __device__ static inline void rope_generic_body(const RopeArgs &a) {
     extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void NAME(RopeArgs a) {            \
         rope_body<T, KIND, NORM, STORE, LP_DEV>(a);                                        \
     }                                                                                      \
+    extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void NAME##_h2(RopeArgs a) {       \
+        rope_body<T, KIND, NORM, STORE, LP_DEV, 2>(a);                                     \
+    }                                                                                      \
     extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void NAME##_g(RopeArgs a) {        \
         rope_body<T, KIND, NORM, STORE, LP_CACHED>(a);                                     \
     }
@@ -490,6 +505,9 @@ __device__ static inline void rope_generic_body(const RopeArgs &a) {
 #define CUCA_ROPE_NT(NAME, T, KIND, STORE)                                                 \
     extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void NAME(RopeArgs a) {            \
         rope_body<T, KIND, true, STORE, LP_NT>(a);                                         \
+    }                                                                                      \
+    extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void NAME##_h2(RopeArgs a) {       \
+        rope_body<T, KIND, true, STORE, LP_NT, 2>(a);                                      \
     }
 #define CUCA_ROPE_SET(TN, T)                                                               \
     CUCA_ROPE(cuca_rope_##TN##_norm, T, 0, false, false)                                   \

@@ -879,6 +879,25 @@ static cuca_status rope_common(cuca_hip_ctx *ctx, void *q, int64_t q_ld, const v
     // 54.7 us and the next gather from 15.4 to 20.8 us.
     const bool stream = norm && heads * (int64_t)head_dim * (int64_t)esize(dtype) >= kStreamBytes;
     const Kernel kk = stream ? table_nt[f16][neox][store] : table_k[dev][f16][neox][norm][store];
+    static const Kernel table_h2[2][2][2][2] = {
+        {{{cuca_rope_f32_norm_h2, cuca_rope_f32_norm_kv_h2}, {cuca_rope_f32_norm_qkn_h2, cuca_rope_f32_norm_qkn_kv_h2}},
+         {{cuca_rope_f32_neox_h2, cuca_rope_f32_neox_kv_h2}, {cuca_rope_f32_neox_qkn_h2, cuca_rope_f32_neox_qkn_kv_h2}}},
+        {{{cuca_rope_f16_norm_h2, cuca_rope_f16_norm_kv_h2}, {cuca_rope_f16_norm_qkn_h2, cuca_rope_f16_norm_qkn_kv_h2}},
+         {{cuca_rope_f16_neox_h2, cuca_rope_f16_neox_kv_h2}, {cuca_rope_f16_neox_qkn_h2, cuca_rope_f16_neox_qkn_kv_h2}}}};
+    static const Kernel table_nt_h2[2][2][2] = {
+        {{cuca_rope_f32_norm_qkn_nt_h2, cuca_rope_f32_norm_qkn_kv_nt_h2}, {cuca_rope_f32_neox_qkn_nt_h2, cuca_rope_f32_neox_qkn_kv_nt_h2}},
+        {{cuca_rope_f16_norm_qkn_nt_h2, cuca_rope_f16_norm_qkn_kv_nt_h2}, {cuca_rope_f16_neox_qkn_nt_h2, cuca_rope_f16_neox_qkn_kv_nt_h2}}};
+    // Two heads per lane when both projections have an even head count: a
+    // lane then loads its cos/sin entries and norm weights once for two heads
+    // of a row.  Measured on MI355X in the prefill steps: config C RoPE
+    // 15.3 -> 14.1 us at 4096 tokens and 54.6 -> 49.4 us at 16384, the fused
+    // K/V store 17.9 -> 16.7 and 65.1 -> 59.5 us, config E's QK-norm RoPE
+    // 29.8 -> 27.9 us and its fused store 31.4 -> 30.4 us; four heads per
+    // lane ran config E's QK-norm kernels slower (99 registers).
+    if (dev && nq % 2 == 0 && nk % 2 == 0) {
+        const Kernel k2 = stream ? table_nt_h2[f16][neox][store] : table_h2[f16][neox][norm][store];
+        return launch(ctx, k2, div_up(heads / 2, 256 / tph), 256, 0, a);
+    }
     return launch(ctx, kk, div_up(heads, 256 / tph), 256, 0, a);
 }
 

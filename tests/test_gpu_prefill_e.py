@@ -6,8 +6,8 @@ they run the nontemporal kernels that the smaller tests never reach.  Each
 test names the kernel it means to cover and checks, from the C ABI's
 per-kernel profile, that the call launched exactly that kernel:
   add_rmsnorm, H 2048: 2 x 8192 x 2048 f16 in = 64 MiB -> cuca_norm_f16_t256_nt
-  QK-norm RoPE, Q 32 + K 4 heads x 128: 72 MiB  -> cuca_rope_f16_neox_qkn_nt
-  the same + the paged K/V store (V 4 heads): 80 MiB -> cuca_rope_f16_neox_qkn_kv_nt
+  QK-norm RoPE, Q 32 + K 4 heads x 128: 72 MiB  -> cuca_rope_f16_neox_qkn_nt_h2 (two heads per lane)
+  the same + the paged K/V store (V 4 heads): 80 MiB -> cuca_rope_f16_neox_qkn_kv_nt_h2
   the SwiGLU over the 65536 expert-grouped rows of width 768 (Zipf(1.1)
   routing, 8 of 128 experts per token) -> cuca_glu_f16_silu_ragged
 Bars as everywhere (cpu.rs:2840-2864 for Q, 3040-3055 for K, 3652 for the
@@ -80,7 +80,7 @@ def test_qk_norm_rope_streaming_kernel_at_8192_tokens(ctx, torch):
                                            hip.ROPE_NEOX, dcos.data_ptr(), dsin.data_ptr(), N,
                                            pos.data_ptr(), qw.data_ptr(), kw.data_ptr(), CFG["eps"],
                                            hip.F16))
-    assert names == ["cuca_rope_f16_neox_qkn_nt"], names
+    assert names == ["cuca_rope_f16_neox_qkn_nt_h2"], names
     ctx.check_device()
     s = sample(N, 43)
     st = torch.from_numpy(s).cuda()
@@ -113,7 +113,7 @@ def test_qk_norm_rope_kv_store_streaming_kernel_at_8192_tokens(ctx, torch):
         q.data_ptr(), nq * d, k.data_ptr(), nk * d, v.data_ptr(), nk * d, N, nq, nk, d, d,
         hip.ROPE_NEOX, dcos.data_ptr(), dsin.data_ptr(), N, pos.data_ptr(), qw.data_ptr(),
         kw.data_ptr(), 1, eps, pk.data_ptr(), pv.data_ptr(), n_blocks, dslots.data_ptr(), hip.F16))
-    assert names == ["cuca_rope_f16_neox_qkn_kv_nt"], names
+    assert names == ["cuca_rope_f16_neox_qkn_kv_nt_h2"], names
     ctx.check_device()
     s = sample(N, 46, extra=(15, 16))
     st = torch.from_numpy(s).cuda()
