@@ -572,7 +572,8 @@ class DecodeStep:
     generated as GGUF bytes on the device and packed once; the K/V pools
     hold ctx_len keys per sequence in consecutive blocks."""
 
-    def __init__(self, ctx, torch, n, ctx_len, qtype="q4_0", layers=32, seed=3, mm="qmm", fuse_rope=False):
+    def __init__(self, ctx, torch, n, ctx_len, qtype="q4_0", layers=32, seed=3, mm="qmm", fuse_rope=False,
+                 fuse_norm=False):
         import numpy as np
         from cuca_amd import hip
         from cuca_amd import workloads as W
@@ -633,6 +634,12 @@ class DecodeStep:
         # the Q|K|V projection carries RoPE and the K/V store in its epilogue
         # (cuca_hip_qmm_rope_store_kv) instead of a launch of its own
         self.fuse_rope = fuse_rope and mm == "qmm"
+        # the two residual + RMSNorm launches ride in the prologue of the
+        # matmul that reads them (cuca_hip_add_rmsnorm_qmm_rope_store_kv,
+        # _qmm_glu); the layer's mid residual then goes to x_mid (the fused
+        # call's outputs may not overlap its inputs)
+        self.fuse_norm = fuse_norm and self.fuse_rope
+        self.x_mid = r(n, H)
         if mm == "qgemm":
             self.qg_bytes = max([hip.qgemm_workspace(T, rows, cols, n, glu) for rows, cols, glu in (
                 ((nq + 2 * nk) * d, H, False), (H, nq * d, False), (F, H, True), (H, F, False))]
@@ -654,36 +661,50 @@ class DecodeStep:
         H, F, d, nq, nk, eps = cfg["hidden"], cfg["ff"], cfg["head_dim"], cfg["nq"], cfg["nk"], cfg["eps"]
         f32 = hip.F32
         for l in self.L:
-            c.add_rmsnorm(self.x.data_ptr(), self.ffn.data_ptr(), l["n1"].data_ptr(), None, eps, eps, 1.0,
-                          n, H, self.x.data_ptr(), self.h.data_ptr(), f32)
             # one Q|K|V projection; RoPE, the K/V store and the attention
             # read their heads in place from its rows
             qkv_ld = (nq + 2 * nk) * d
             q_ptr = self.qkv.data_ptr()
-            if self.fuse_rope:
-                c.qmm_rope_store_kv(l["wqkv"].data_ptr(), T, H, self.h.data_ptr(), H, n, nq, nk, d, d,
-                                    hip.ROPE_NORM, self.cos.data_ptr(), self.sin.data_ptr(), 8192,
-                                    self.pos.data_ptr(), q_ptr, qkv_ld, l["pk"].data_ptr(), l["pv"].data_ptr(),
-                                    self.n_blocks, self.slots.data_ptr(), f32)
+            if self.fuse_norm:
+                c.add_rmsnorm_qmm_rope_store_kv(self.x.data_ptr(), self.ffn.data_ptr(), l["n1"].data_ptr(), eps,
+                                                1.0, self.x_mid.data_ptr(), self.h.data_ptr(), l["wqkv"].data_ptr(),
+                                                T, H, n, nq, nk, d, d, hip.ROPE_NORM, self.cos.data_ptr(),
+                                                self.sin.data_ptr(), 8192, self.pos.data_ptr(), q_ptr, qkv_ld,
+                                                l["pk"].data_ptr(), l["pv"].data_ptr(), self.n_blocks,
+                                                self.slots.data_ptr(), f32)
             else:
-                self.mat(l["wqkv"], qkv_ld, H, self.h, self.qkv)
-                c.rope_store_kv(q_ptr, qkv_ld, q_ptr + 4 * nq * d, qkv_ld, q_ptr + 4 * (nq + nk) * d, qkv_ld,
-                                n, nq, nk, d, d, hip.ROPE_NORM, self.cos.data_ptr(), self.sin.data_ptr(), 8192,
-                                self.pos.data_ptr(), None, None, 0, eps, l["pk"].data_ptr(), l["pv"].data_ptr(),
-                                self.n_blocks, self.slots.data_ptr(), f32)
+                c.add_rmsnorm(self.x.data_ptr(), self.ffn.data_ptr(), l["n1"].data_ptr(), None, eps, eps, 1.0,
+                              n, H, self.x.data_ptr(), self.h.data_ptr(), f32)
+                if self.fuse_rope:
+                    c.qmm_rope_store_kv(l["wqkv"].data_ptr(), T, H, self.h.data_ptr(), H, n, nq, nk, d, d,
+                                        hip.ROPE_NORM, self.cos.data_ptr(), self.sin.data_ptr(), 8192,
+                                        self.pos.data_ptr(), q_ptr, qkv_ld, l["pk"].data_ptr(), l["pv"].data_ptr(),
+                                        self.n_blocks, self.slots.data_ptr(), f32)
+                else:
+                    self.mat(l["wqkv"], qkv_ld, H, self.h, self.qkv)
+                    c.rope_store_kv(q_ptr, qkv_ld, q_ptr + 4 * nq * d, qkv_ld, q_ptr + 4 * (nq + nk) * d, qkv_ld,
+                                    n, nq, nk, d, d, hip.ROPE_NORM, self.cos.data_ptr(), self.sin.data_ptr(), 8192,
+                                    self.pos.data_ptr(), None, None, 0, eps, l["pk"].data_ptr(),
+                                    l["pv"].data_ptr(), self.n_blocks, self.slots.data_ptr(), f32)
             c.paged_decode(q_ptr, l["pk"].data_ptr(), l["pv"].data_ptr(), self.n_blocks,
                            self.tables.data_ptr(), self.max_blocks, self.ranges.data_ptr(), n, nq, nk, d,
                            self.scale, self.ws.data_ptr(), self.ws_bytes, self.o.data_ptr(), f32,
                            q_ld=qkv_ld)
             self.mat(l["wo"], H, nq * d, self.o, self.attn)
-            c.add_rmsnorm(self.x.data_ptr(), self.attn.data_ptr(), l["n2"].data_ptr(), None, eps, eps, 1.0,
-                          n, H, self.x.data_ptr(), self.h.data_ptr(), f32)
-            if self.mm == "qgemm":
-                c.qgemm_glu(l["wg"].data_ptr(), l["wu"].data_ptr(), T, F, H, self.h.data_ptr(), H, n,
-                            hip.ACT_SILU, 0.0, self.qg_ws.data_ptr(), self.qg_bytes, self.act.data_ptr(), F, f32)
+            if self.fuse_norm:
+                c.add_rmsnorm_qmm_glu(self.x_mid.data_ptr(), self.attn.data_ptr(), l["n2"].data_ptr(), eps, 1.0,
+                                      self.x.data_ptr(), self.h.data_ptr(), l["wg"].data_ptr(), l["wu"].data_ptr(),
+                                      T, F, H, n, hip.ACT_SILU, 0.0, self.act.data_ptr(), F, f32)
             else:
-                c.qmm_glu(l["wg"].data_ptr(), l["wu"].data_ptr(), T, F, H, self.h.data_ptr(), H, n,
-                          hip.ACT_SILU, 0.0, self.act.data_ptr(), F, f32)
+                c.add_rmsnorm(self.x.data_ptr(), self.attn.data_ptr(), l["n2"].data_ptr(), None, eps, eps, 1.0,
+                              n, H, self.x.data_ptr(), self.h.data_ptr(), f32)
+                if self.mm == "qgemm":
+                    c.qgemm_glu(l["wg"].data_ptr(), l["wu"].data_ptr(), T, F, H, self.h.data_ptr(), H, n,
+                                hip.ACT_SILU, 0.0, self.qg_ws.data_ptr(), self.qg_bytes, self.act.data_ptr(), F,
+                                f32)
+                else:
+                    c.qmm_glu(l["wg"].data_ptr(), l["wu"].data_ptr(), T, F, H, self.h.data_ptr(), H, n,
+                              hip.ACT_SILU, 0.0, self.act.data_ptr(), F, f32)
             self.mat(l["wd"], H, F, self.act, self.ffn)
 
     def issue_step(self):
@@ -716,7 +737,7 @@ def kernel_role(name):
     return "other"
 
 
-def decode_step_bench(ctx, torch, n, ctx_len, replays=10, mm="qmm", fuse_rope=False):
+def decode_step_bench(ctx, torch, n, ctx_len, replays=10, mm="qmm", fuse_rope=False, fuse_norm=False):
     """DecodeStep's 32 layers and its whole step, each captured in one
     hipGraph and replayed: microseconds per layer, per step, and tokens/s
     (n tokens per step).  The step's own kernels, timed on the device
@@ -726,7 +747,7 @@ def decode_step_bench(ctx, torch, n, ctx_len, replays=10, mm="qmm", fuse_rope=Fa
     Q|K|V + RoPE + K/V-store launch, attention.  Checked: the step's ids are
     the argmax of its own logits, and the logits are finite."""
     import numpy as np
-    ds = DecodeStep(ctx, torch, n, ctx_len, mm=mm, fuse_rope=fuse_rope)
+    ds = DecodeStep(ctx, torch, n, ctx_len, mm=mm, fuse_rope=fuse_rope, fuse_norm=fuse_norm)
     ds.out_ids.copy_(ds.ids)
     torch.cuda.synchronize()
     ds.issue_step()  # eager, once
@@ -761,6 +782,7 @@ def decode_step_bench(ctx, torch, n, ctx_len, replays=10, mm="qmm", fuse_rope=Fa
     torch.cuda.empty_cache()
     return dict(batch=n, ctx_len=ctx_len, layer_weights="q4_0", head="q8_0", matmul=mm,
                 rope_in_qkv_epilogue=bool(fuse_rope and mm == "qmm"),
+                norm_in_matmul_prologue=bool(fuse_norm and fuse_rope and mm == "qmm"),
                 us_per_layer=round(layers_ms * 1000 / 32, 2), us_per_step=round(step_ms * 1000, 1),
                 tokens_per_s=round(n / (step_ms / 1e3), 1),
                 layer_weight_gbs=round(wb / (layers_ms / 1e3) / 1e9, 1), **split)
@@ -1449,10 +1471,15 @@ def main():
         torch.cuda.empty_cache()
         if not args.no_qmm:
             log("whole decode steps (32 layers + head, hipGraph)")
-            for n, clen, mm, fuse in ((1, 4096, "qmm", False), (1, 4096, "qmm", True), (32, 1024, "qmm", True),
-                                      (32, 1024, "qgemm", False)):
-                key = f"step_batch{n}_ctx{clen}_{mm}" + ("_rope_in_qkv" if fuse else "")
-                decode[key] = decode_step_bench(ctx, torch, n, clen, mm=mm, fuse_rope=fuse)
+            # fuse: "" none; "rope": RoPE + K/V store in the Q|K|V epilogue;
+            # "norm": that and both residual + RMSNorm launches in the
+            # prologues of the Q|K|V and gate/up matmuls
+            for n, clen, mm, fuse in ((1, 4096, "qmm", ""), (1, 4096, "qmm", "rope"), (1, 4096, "qmm", "norm"),
+                                      (32, 1024, "qmm", "rope"), (32, 1024, "qgemm", "")):
+                key = f"step_batch{n}_ctx{clen}_{mm}" + {"": "", "rope": "_rope_in_qkv",
+                                                         "norm": "_norm_rope_in_qkv"}[fuse]
+                decode[key] = decode_step_bench(ctx, torch, n, clen, mm=mm, fuse_rope=fuse != "",
+                                                fuse_norm=fuse == "norm")
             torch.cuda.empty_cache()
 
     traffic, why = traffic_from_profiles(glu["kernel"])

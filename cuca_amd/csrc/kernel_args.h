@@ -181,6 +181,16 @@ typedef struct {
     void *pool_k, *pool_v;
     int64_t table_rows, n_slots;
     int32_t nq, nk, head_dim, n_dims;
+    /* residual add + RMSNorm in the prologue (qmd *_rn kernels, one row):
+     * x' = x + rs * branch (branch nullable) -> rn_x_out, h = rms(x', rn_w,
+     * eps) -> rn_h_out (both written by workgroup 0, either nullable), and
+     * the matmul runs on h.  The sum of squares follows the add_rmsnorm
+     * vector kernel of rn_tpr threads x rn_per chunks per row.             */
+    const void *rn_branch;
+    const float *rn_w;
+    void *rn_x_out, *rn_h_out;
+    float rn_eps, rn_rs;
+    int32_t rn_tpr, rn_per;
 } QmmArgs;
 
 /* The quantized matmul on the matrix cores (qgemm.hip): out[t][n] =

@@ -63,12 +63,150 @@ struct QmdSlot {
 // the allocation).
 #define QMD_LDS_BYTES(NG, G) (16 * ((NG) * (G) + 2) * 8 + ((NG) + 1) * (G) * 4)
 
+// The residual add + RMSNorm prologue (RN kernels): the row x' = x + rs *
+// branch, as cuca_hip_add_rmsnorm's vector kernel computes it, and h =
+// rms(x') with that kernel's bits.  Its sum of squares is per thread (TPR
+// threads of NCH chunks of CN values: chunks li, li + TPR, ..., values in
+// order), a butterfly over the thread's wave (or its group of TPR < 64
+// lanes) and, for TPR > 64, the waves' sums added in wave order.  Thread
+// tid here plays the kernel's threads tid, tid + 256, ...: their lane in a
+// wave is tid's own, so the butterfly runs on the same partners.  x' is
+// staged in LDS (over the expanded row, which is written only after the
+// last read of it) for the per-thread sums.  xv holds x on entry (bv the
+// branch, wv the weights) and h on exit, as the matmul reads h stored as T.
+//
+// Fast path, for one chunk a thread and rows of whole waves (per == 1, TPR
+// >= 64: hidden 256 .. 4096 f32, 512 .. 8192 f16): the sums come straight
+// from the registers, with no LDS staging and one barrier.  An f16 item is
+// one chunk, so item i is the kernel's thread i, in the same lane: the
+// butterfly is group_sum<64> of the item's sum.  An f32 item holds chunks
+// 2i and 2i + 1, the kernel's lanes 2 (q % 32) + e of its wave i / 32 (q
+// = this lane): its partners at distance 32, 16, 8, 4, 2 are this lane's
+// at 16, 8, 4, 2, 1 (same e), and its last step (distance 1) adds the
+// item's two sums.  Measured on MI355X (Llama-3-8B decode, batch 1): the
+// LDS-staged form made the fused kernels about 2 us slower each.
+template <typename T, int NI>
+__device__ static inline void qmd_rms_prologue(const QmmArgs &a, float (&xv)[NI][8], const float (&bv)[NI][8],
+                                               const float (&wv)[NI][8], float *vl) {
+    __shared__ float rn_red[16];
+    constexpr int CN = Chunk<T>::N;
+    const int tid = threadIdx.x, lane = tid & (CUCA_WAVE - 1);
+    const int nitems = 4 * a.nb; // 8 values an item
+    const bool w0 = blockIdx.x == 0;
+    const int H = a.nb * 32, nch = H / CN, tpr = a.rn_tpr, per = a.rn_per;
+    const bool fast = per == 1 && tpr >= CUCA_WAVE && NI * CUCA_BLOCK * (8 / CN) >= tpr;
+#pragma unroll
+    for (int it = 0; it < NI; it++) {
+        const int item = it * CUCA_BLOCK + tid;
+        if (item < nitems) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                float v = xv[it][e];
+                if (a.rn_branch) {
+                    float b = bv[it][e];
+                    if (a.rn_rs != 1.0f) b = b * a.rn_rs + 0.0f; // `scaled`: branch.affine(rs, 0)
+                    v = Chunk<T>::as_stored(v + b);
+                }
+                xv[it][e] = v;
+                if (!fast) vl[8 * item + e] = v;
+            }
+            if (w0 && a.rn_x_out) {
+                T *xo = reinterpret_cast<T *>(a.rn_x_out) + 8 * (int64_t)item;
+#pragma unroll
+                for (int e = 0; e < 8; e++) xo[e] = to_stored<T>(xv[it][e]);
+            }
+        }
+    }
+    if (fast) {
+#pragma unroll
+        for (int it = 0; it < NI; it++) {
+            const int item = it * CUCA_BLOCK + tid;
+            if constexpr (CN == 8) {
+                float ss = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; e++) ss += xv[it][e] * xv[it][e];
+                ss = group_sum<CUCA_WAVE>(ss);
+                const int nw = item / CUCA_WAVE;
+                if (lane == 0 && nw < tpr / CUCA_WAVE) rn_red[nw] = ss;
+            } else {
+                float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 4; e++) s0 += xv[it][e] * xv[it][e];
+#pragma unroll
+                for (int e = 4; e < 8; e++) s1 += xv[it][e] * xv[it][e];
+                s0 = xor_add<16>(s0); s1 = xor_add<16>(s1);
+                s0 = xor_add<8>(s0); s1 = xor_add<8>(s1);
+                s0 = xor_add<4>(s0); s1 = xor_add<4>(s1);
+                s0 = xor_add<2>(s0); s1 = xor_add<2>(s1);
+                s0 = xor_add<1>(s0); s1 = xor_add<1>(s1);
+                const float ws = s0 + s1;
+                const int nw = item / (CUCA_WAVE / 2);
+                if ((lane & 31) == 0 && nw < tpr / CUCA_WAVE) rn_red[nw] = ws;
+            }
+        }
+        __syncthreads();
+    } else { // x' staged in LDS
+        __syncthreads();
+        // the kernel's per-thread sums, then its butterfly
+        auto thread_ss = [&](int li) {
+            float ss = 0.0f;
+            for (int k = 0; k < per; k++) {
+                const int c = li + k * tpr;
+                if (c < nch) {
+#pragma unroll
+                    for (int i = 0; i < CN; i++) ss += vl[c * CN + i] * vl[c * CN + i];
+                }
+            }
+            return ss;
+        };
+        if (tpr <= CUCA_WAVE) {
+            if (tid < CUCA_WAVE) { // wave 0: lanes below tpr are the kernel's threads
+                const float ss = group_sum_rt(tid < tpr ? thread_ss(tid) : 0.0f, tpr);
+                if (tid == 0) rn_red[0] = ss;
+            }
+        } else {
+            for (int j = 0; j < 4; j++) {
+                const int li = tid + j * CUCA_BLOCK; // wave-uniform test: tpr is a multiple of 64
+                if (li < tpr) {
+                    const float ss = group_sum<CUCA_WAVE>(thread_ss(li));
+                    if (lane == 0) rn_red[li / CUCA_WAVE] = ss;
+                }
+            }
+        }
+        __syncthreads(); // also: every read of vl is done
+    }
+    float s;
+    if (tpr <= CUCA_WAVE) {
+        s = rn_red[0];
+    } else {
+        s = 0.0f;
+        for (int i = 0; i < tpr / CUCA_WAVE; i++) s += rn_red[i];
+    }
+    const float inv = 1.0f / sqrtf(s / (float)H + a.rn_eps);
+#pragma unroll
+    for (int it = 0; it < NI; it++) {
+        const int item = it * CUCA_BLOCK + tid;
+        if (item < nitems) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                float h = a.rn_w ? pin_f32(pin_f32(xv[it][e] * inv) * wv[it][e]) : pin_f32(xv[it][e] * inv);
+                xv[it][e] = (float)to_stored<T>(h);
+            }
+            if (w0 && a.rn_h_out) {
+                T *ho = reinterpret_cast<T *>(a.rn_h_out) + 8 * (int64_t)item;
+#pragma unroll
+                for (int e = 0; e < 8; e++) ho[e] = (T)xv[it][e];
+            }
+        }
+    }
+}
+
 // MODE 0: plain (out[row], the LM head's cap when asked); 3: the Q|K|V
 // projection with RoPE and the paged K/V store in the epilogue (qmm.hip's
 // qmm_rope_kv_store).  D: ring slots; NI: activation items (8 values) per
 // thread, NI * 256 >= 4 ng G.  The grid is ceil(rows / 16) workgroups of
-// 256.
-template <typename T, int FMT, bool GLU, int ACT, int MODE, int D, int NI, int PF = 1>
+// 256.  RN: the residual add + RMSNorm prologue.
+template <typename T, int FMT, bool GLU, int ACT, int MODE, int D, int NI, int PF = 1, bool RN = false>
 __device__ static inline void qmd_body(const QmmArgs &a) {
     using F = QFmt<FMT>;
     constexpr int G = F::G;
@@ -95,11 +233,18 @@ __device__ static inline void qmd_body(const QmmArgs &a) {
     // 8 (item % 4) .. +7 of block item / 4 (zero past the row).
     const int nitems = 4 * nbp, sub = tid & 3;
     float xv[NI][8];
+    // RN: the branch and the norm weights of the same values
+    float bv[RN ? NI : 1][8], wv[RN ? NI : 1][8];
 #pragma unroll
     for (int it = 0; it < NI; it++) {
         const int item = it * CUCA_BLOCK + tid, b = item >> 2;
         if (item < nitems && b < a.nb) {
             qmm_load8<T>(reinterpret_cast<const T *>(a.x) + (int64_t)b * 32 + sub * 8, xv[it]);
+            if constexpr (RN) {
+                if (a.rn_branch)
+                    qmm_load8<T>(reinterpret_cast<const T *>(a.rn_branch) + (int64_t)b * 32 + sub * 8, bv[it]);
+                if (a.rn_w) qmm_load8<float>(a.rn_w + (int64_t)b * 32 + sub * 8, wv[it]);
+            }
         } else {
 #pragma unroll
             for (int e = 0; e < 8; e++) xv[it][e] = 0.0f;
@@ -127,6 +272,7 @@ __device__ static inline void qmd_body(const QmmArgs &a) {
         load(ring[I.value], I.value);
         __builtin_amdgcn_sched_barrier(0);
     });
+    if constexpr (RN) qmd_rms_prologue<T, NI>(a, xv, bv, wv, reinterpret_cast<float *>(qmd_lds));
 
     // 3. Quantise (Acts::new, qmm.rs:1217-1240: the four threads of a block
     // share its maximum) and expand: per (lane, block) the f16 pair
@@ -284,6 +430,12 @@ __device__ static inline void qmd_body(const QmmArgs &a) {
     CUCA_QMD(cuca_qmd_glu_##TN##_##FN##_silu_n##NI, T, FMT, true, 0, 0, DG, NI)            \
     CUCA_QMD(cuca_qmd_glu_##TN##_##FN##_gelu_n##NI, T, FMT, true, 1, 0, DG, NI)            \
     CUCA_QMD(cuca_qmd_rope_kv_##TN##_##FN##_n##NI, T, FMT, false, 0, 3, DP, NI)
+// The same with the residual add + RMSNorm prologue (_rn).
+#define CUCA_QMD_RN_SET(TN, T, FN, FMT, NI, DP, DG)                                        \
+    CUCA_QMD(cuca_qmd_##TN##_##FN##_n##NI##_rn, T, FMT, false, 0, 0, DP, NI, 1, true)       \
+    CUCA_QMD(cuca_qmd_glu_##TN##_##FN##_silu_n##NI##_rn, T, FMT, true, 0, 0, DG, NI, 1, true) \
+    CUCA_QMD(cuca_qmd_glu_##TN##_##FN##_gelu_n##NI##_rn, T, FMT, true, 1, 0, DG, NI, 1, true) \
+    CUCA_QMD(cuca_qmd_rope_kv_##TN##_##FN##_n##NI##_rn, T, FMT, false, 0, 3, DP, NI, 1, true)
 CUCA_QMD_SET(f32, float, q4_0, 0, 2, 4, 2)
 CUCA_QMD_SET(f32, float, q4_0, 0, 8, 8, 2)
 CUCA_QMD_SET(f32, float, q8_0, 1, 2, 8, 4)
@@ -292,3 +444,11 @@ CUCA_QMD_SET(f16, _Float16, q4_0, 0, 2, 4, 2)
 CUCA_QMD_SET(f16, _Float16, q4_0, 0, 8, 8, 2)
 CUCA_QMD_SET(f16, _Float16, q8_0, 1, 2, 8, 4)
 CUCA_QMD_SET(f16, _Float16, q8_0, 1, 8, 8, 4)
+CUCA_QMD_RN_SET(f32, float, q4_0, 0, 2, 4, 2)
+CUCA_QMD_RN_SET(f32, float, q4_0, 0, 8, 8, 2)
+CUCA_QMD_RN_SET(f32, float, q8_0, 1, 2, 8, 4)
+CUCA_QMD_RN_SET(f32, float, q8_0, 1, 8, 8, 4)
+CUCA_QMD_RN_SET(f16, _Float16, q4_0, 0, 2, 4, 2)
+CUCA_QMD_RN_SET(f16, _Float16, q4_0, 0, 8, 8, 2)
+CUCA_QMD_RN_SET(f16, _Float16, q8_0, 1, 2, 8, 4)
+CUCA_QMD_RN_SET(f16, _Float16, q8_0, 1, 8, 8, 4)

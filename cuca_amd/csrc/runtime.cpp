@@ -1225,7 +1225,7 @@ static bool qmd_fits(int64_t m, int64_t k, int64_t ng, int g, int64_t rows, int6
     return m == 1 && k <= 16384 && qmd_lds(ng, g) <= (64u << 10) && rows * row_bytes < (1ll << 31);
 }
 static cuca_status qmd_launch(cuca_hip_ctx *ctx, int mode, int glu, uint32_t ggml_type, int64_t k, int g,
-                              cuca_dtype dtype, QmmArgs &a) {
+                              cuca_dtype dtype, QmmArgs &a, bool rn = false) {
     // [dtype][format][n2, n8][plain, silu, gelu, rope_kv]
     static const Kernel table_k[2][2][2][4] = {
         {{{cuca_qmd_f32_q4_0_n2, cuca_qmd_glu_f32_q4_0_silu_n2, cuca_qmd_glu_f32_q4_0_gelu_n2,
@@ -1244,16 +1244,92 @@ static cuca_status qmd_launch(cuca_hip_ctx *ctx, int mode, int glu, uint32_t ggm
            cuca_qmd_rope_kv_f16_q8_0_n2},
           {cuca_qmd_f16_q8_0_n8, cuca_qmd_glu_f16_q8_0_silu_n8, cuca_qmd_glu_f16_q8_0_gelu_n8,
            cuca_qmd_rope_kv_f16_q8_0_n8}}}};
+    // the same with the residual add + RMSNorm prologue
+    static const Kernel table_rn[2][2][2][4] = {
+        {{{cuca_qmd_f32_q4_0_n2_rn, cuca_qmd_glu_f32_q4_0_silu_n2_rn, cuca_qmd_glu_f32_q4_0_gelu_n2_rn,
+           cuca_qmd_rope_kv_f32_q4_0_n2_rn},
+          {cuca_qmd_f32_q4_0_n8_rn, cuca_qmd_glu_f32_q4_0_silu_n8_rn, cuca_qmd_glu_f32_q4_0_gelu_n8_rn,
+           cuca_qmd_rope_kv_f32_q4_0_n8_rn}},
+         {{cuca_qmd_f32_q8_0_n2_rn, cuca_qmd_glu_f32_q8_0_silu_n2_rn, cuca_qmd_glu_f32_q8_0_gelu_n2_rn,
+           cuca_qmd_rope_kv_f32_q8_0_n2_rn},
+          {cuca_qmd_f32_q8_0_n8_rn, cuca_qmd_glu_f32_q8_0_silu_n8_rn, cuca_qmd_glu_f32_q8_0_gelu_n8_rn,
+           cuca_qmd_rope_kv_f32_q8_0_n8_rn}}},
+        {{{cuca_qmd_f16_q4_0_n2_rn, cuca_qmd_glu_f16_q4_0_silu_n2_rn, cuca_qmd_glu_f16_q4_0_gelu_n2_rn,
+           cuca_qmd_rope_kv_f16_q4_0_n2_rn},
+          {cuca_qmd_f16_q4_0_n8_rn, cuca_qmd_glu_f16_q4_0_silu_n8_rn, cuca_qmd_glu_f16_q4_0_gelu_n8_rn,
+           cuca_qmd_rope_kv_f16_q4_0_n8_rn}},
+         {{cuca_qmd_f16_q8_0_n2_rn, cuca_qmd_glu_f16_q8_0_silu_n2_rn, cuca_qmd_glu_f16_q8_0_gelu_n2_rn,
+           cuca_qmd_rope_kv_f16_q8_0_n2_rn},
+          {cuca_qmd_f16_q8_0_n8_rn, cuca_qmd_glu_f16_q8_0_silu_n8_rn, cuca_qmd_glu_f16_q8_0_gelu_n8_rn,
+           cuca_qmd_rope_kv_f16_q8_0_n8_rn}}}};
     const int kind = mode == 3 ? 3 : glu;
-    const Kernel kk = table_k[dtype == CUCA_F16][ggml_type == CUCA_GGML_Q8_0][k > 4096][kind];
+    const Kernel kk = (rn ? table_rn : table_k)[dtype == CUCA_F16][ggml_type == CUCA_GGML_Q8_0][k > 4096][kind];
     return launch(ctx, kk, div_up(a.rows, 16), CUCA_BLOCK_THREADS, (unsigned)qmd_lds(a.ng, g), a);
+}
+
+// The residual add + RMSNorm in front of a matmul (the
+// cuca_hip_add_rmsnorm_qmm* entry points): cuca_hip_add_rmsnorm(x, branch,
+// w, eps, rs) into x_out and h_out, then the matmul of h_out.
+struct NormIn {
+    const void *x, *branch;
+    const float *w;
+    float eps, rs;
+    void *x_out, *h_out;
+};
+
+static bool ranges_overlap(const void *p, const void *q, size_t bytes) {
+    if (!p || !q) return false;
+    const uintptr_t a = (uintptr_t)p, b = (uintptr_t)q;
+    return a < b + bytes && b < a + bytes;
+}
+
+// What cuca_hip_add_rmsnorm checks, and that neither output overlaps an
+// input (workgroup 0 writes them while the others still read x and branch).
+static cuca_status norm_in_check(cuca_hip_ctx *ctx, const NormIn &rn, int64_t m, int64_t k, cuca_dtype dtype) {
+    if (!rn.x || !rn.h_out) return fail(ctx, CUCA_INVALID_ARG, "null x or h_out");
+    if (!(rn.eps >= 0.0f)) return fail(ctx, CUCA_INVALID_ARG, "eps must be >= 0");
+    if (!dtype_ok(dtype)) return fail(ctx, CUCA_INVALID_ARG, "bad dtype %d", (int)dtype);
+    const size_t bytes = (size_t)m * (size_t)k * esize(dtype);
+    if (ranges_overlap(rn.x_out, rn.x, bytes) || ranges_overlap(rn.x_out, rn.branch, bytes) ||
+        ranges_overlap(rn.h_out, rn.x, bytes) || ranges_overlap(rn.h_out, rn.branch, bytes) ||
+        ranges_overlap(rn.h_out, rn.x_out, bytes))
+        return fail(ctx, CUCA_INVALID_ARG, "add_rmsnorm_qmm: x_out and h_out must not overlap x, branch or each other");
+    return CUCA_OK;
+}
+
+// Whether the one-row matmul can run the norm as its prologue (with the
+// bits of cuca_hip_add_rmsnorm's vector kernel: its shape goes into a).
+static bool norm_prologue(const NormIn &rn, int64_t m, int64_t k, cuca_dtype dtype, QmmArgs &a) {
+    const int N = chunk_elems(dtype);
+    const size_t es = esize(dtype);
+    const bool vec = m == 1 && k % N == 0 && al16(rn.x) && al16(rn.h_out) && (!rn.branch || al16(rn.branch)) &&
+                     (!rn.x_out || al16(rn.x_out)) && (!rn.w || al16(rn.w)) && ((size_t)k * es) % 16 == 0;
+    int tpr = 0, per = 0;
+    if (!vec || !norm_shape(k / N, &tpr, &per) || norm_kernel(dtype == CUCA_F16, tpr, per, false) == KERNEL_COUNT)
+        return false;
+    a.x = rn.x;
+    a.rn_branch = rn.branch;
+    a.rn_w = rn.w;
+    a.rn_x_out = rn.x_out;
+    a.rn_h_out = rn.h_out;
+    a.rn_eps = rn.eps;
+    a.rn_rs = rn.rs;
+    a.rn_tpr = tpr;
+    a.rn_per = per;
+    return true;
+}
+
+// The norm as a launch of its own (when the matmul does not take it).
+static cuca_status norm_in_launch(cuca_hip_ctx *ctx, const NormIn &rn, int64_t m, int64_t k, cuca_dtype dtype) {
+    return cuca_hip_add_rmsnorm(ctx, rn.x, rn.branch, rn.w, nullptr, rn.eps, rn.eps, rn.rs, m, k, rn.x_out,
+                                rn.h_out, dtype);
 }
 
 // glu: 0 plain, 1 SiLU, 2 GELU-tanh
 static cuca_status qmm_common(cuca_hip_ctx *ctx, const void *w, const void *w_up, uint32_t ggml_type,
                               int64_t n, int64_t k, const void *x, int64_t ldx, int64_t m, int64_t rows,
                               int glu, float clamp, void *out, int64_t out_ld, cuca_dtype dtype,
-                              const LogitCap &cap = LogitCap()) {
+                              const LogitCap &cap = LogitCap(), const NormIn *rn = nullptr) {
     cuca_status st = use(ctx);
     if (st != CUCA_OK) return st;
     int g = 0, gb = 0;
@@ -1280,9 +1356,12 @@ static cuca_status qmm_common(cuca_hip_ctx *ctx, const void *w, const void *w_up
     const int64_t nb = k / 32, ng = (nb + g - 1) / g;
     // one or two rows whose tile fits the LDS: the decode GEMV, each
     // workgroup quantising the rows itself
-    if (m <= 2 && qmv_wins(ctx, rows) && qmv_fits(m, ng * g, g))
+    const bool qmv = m <= 2 && qmv_wins(ctx, rows) && qmv_fits(m, ng * g, g);
+    if (qmv) {
+        if (rn && (st = norm_in_launch(ctx, *rn, m, k, dtype)) != CUCA_OK) return st;
         return qmv_launch(ctx, 3, w, w_up, ggml_type, n, k, nullptr, 0, nullptr, x, ldx, m, rows, glu, clamp, out,
                           out_ld, dtype, cap);
+    }
     const bool qmd = qmd_fits(m, k, ng, g, rows, ng * gb);
     const int mt = m == 1 ? 1 : m == 2 ? 2 : 4;
     const int mi = mt == 1 ? 0 : mt == 2 ? 1 : 2;
@@ -1328,17 +1407,20 @@ static cuca_status qmm_common(cuca_hip_ctx *ctx, const void *w, const void *w_up
         a.softcap_inv = (float)(1.0 / (double)cap.softcap);
         a.softcap = cap.softcap;
     }
-    // one activation row: the decode matmul (the same bits)
-    if (qmd) return qmd_launch(ctx, 0, glu, ggml_type, k, g, dtype, a);
+    // one activation row: the decode matmul (the same bits), with the norm
+    // as its prologue when asked and its shape allows
+    const bool fused = rn && qmd && norm_prologue(*rn, m, k, dtype, a);
+    if (rn && !fused && (st = norm_in_launch(ctx, *rn, m, k, dtype)) != CUCA_OK) return st;
+    if (qmd) return qmd_launch(ctx, 0, glu, ggml_type, k, g, dtype, a, fused);
     return launch(ctx, kk, (unsigned)(nrb8 * ntile), CUCA_BLOCK_THREADS, 0, a);
 }
 
-cuca_status cuca_hip_qmm_rope_store_kv(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type, int64_t k, const void *x,
-                                       int64_t ldx, int64_t m, int32_t nq, int32_t nk, int32_t head_dim,
-                                       int32_t n_dims, cuca_rope_kind kind, const float *cos, const float *sin,
-                                       int64_t table_rows, const int32_t *positions, void *q_out, int64_t q_ld,
-                                       void *pool_k, void *pool_v, int64_t n_blocks, const int32_t *slots,
-                                       cuca_dtype dtype) {
+static cuca_status qmm_rope_kv_common(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type, int64_t k,
+                                      const void *x, int64_t ldx, int64_t m, int32_t nq, int32_t nk,
+                                      int32_t head_dim, int32_t n_dims, cuca_rope_kind kind, const float *cos,
+                                      const float *sin, int64_t table_rows, const int32_t *positions, void *q_out,
+                                      int64_t q_ld, void *pool_k, void *pool_v, int64_t n_blocks,
+                                      const int32_t *slots, cuca_dtype dtype, const NormIn *rn) {
     cuca_status st = use(ctx);
     if (st != CUCA_OK) return st;
     if (kind != CUCA_ROPE_NORM)
@@ -1409,9 +1491,38 @@ cuca_status cuca_hip_qmm_rope_store_kv(cuca_hip_ctx *ctx, const void *w, uint32_
     a.n_dims = n_dims;
     ctx->last_table_rows = table_rows;
     ctx->last_kv_blocks = n_blocks;
-    if (qmd_fits(m, k, ng, g, n, ng * gb)) return qmd_launch(ctx, 3, 0, ggml_type, k, g, dtype, a);
+    const bool qmd = qmd_fits(m, k, ng, g, n, ng * gb);
+    const bool fused = rn && qmd && norm_prologue(*rn, m, k, dtype, a);
+    if (rn && !fused && (st = norm_in_launch(ctx, *rn, m, k, dtype)) != CUCA_OK) return st;
+    if (qmd) return qmd_launch(ctx, 3, 0, ggml_type, k, g, dtype, a, fused);
     return launch(ctx, table_k[dtype == CUCA_F16][ggml_type == CUCA_GGML_Q8_0][mi], (unsigned)(nrb8 * ntile),
                   CUCA_BLOCK_THREADS, 0, a);
+}
+
+cuca_status cuca_hip_qmm_rope_store_kv(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type, int64_t k, const void *x,
+                                       int64_t ldx, int64_t m, int32_t nq, int32_t nk, int32_t head_dim,
+                                       int32_t n_dims, cuca_rope_kind kind, const float *cos, const float *sin,
+                                       int64_t table_rows, const int32_t *positions, void *q_out, int64_t q_ld,
+                                       void *pool_k, void *pool_v, int64_t n_blocks, const int32_t *slots,
+                                       cuca_dtype dtype) {
+    return qmm_rope_kv_common(ctx, w, ggml_type, k, x, ldx, m, nq, nk, head_dim, n_dims, kind, cos, sin, table_rows,
+                              positions, q_out, q_ld, pool_k, pool_v, n_blocks, slots, dtype, nullptr);
+}
+
+cuca_status cuca_hip_add_rmsnorm_qmm_rope_store_kv(cuca_hip_ctx *ctx, const void *x, const void *branch,
+                                                   const float *norm_w, float eps, float residual_scale,
+                                                   void *x_out, void *h_out, const void *w, uint32_t ggml_type,
+                                                   int64_t k, int64_t m, int32_t nq, int32_t nk, int32_t head_dim,
+                                                   int32_t n_dims, cuca_rope_kind kind, const float *cos,
+                                                   const float *sin, int64_t table_rows, const int32_t *positions,
+                                                   void *q_out, int64_t q_ld, void *pool_k, void *pool_v,
+                                                   int64_t n_blocks, const int32_t *slots, cuca_dtype dtype) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    const NormIn rn{x, branch, norm_w, eps, residual_scale, x_out, h_out};
+    if (m > 0 && (st = norm_in_check(ctx, rn, m, k, dtype)) != CUCA_OK) return st;
+    return qmm_rope_kv_common(ctx, w, ggml_type, k, h_out, k, m, nq, nk, head_dim, n_dims, kind, cos, sin, table_rows,
+                              positions, q_out, q_ld, pool_k, pool_v, n_blocks, slots, dtype, &rn);
 }
 
 cuca_status cuca_hip_lm_head(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type, int64_t vocab, int64_t n_embd,
@@ -1573,6 +1684,32 @@ cuca_status cuca_hip_qmm_glu(cuca_hip_ctx *ctx, const void *gate, const void *up
         return fail(ctx, CUCA_INVALID_ARG, "bad activation %d", (int)act);
     return qmm_common(ctx, gate, up, ggml_type, ff, k, x, ldx, m, ff, act == CUCA_ACT_SILU ? 1 : 2, clamp,
                       out, out_ld, dtype);
+}
+
+cuca_status cuca_hip_add_rmsnorm_qmm(cuca_hip_ctx *ctx, const void *x, const void *branch, const float *norm_w,
+                                     float eps, float residual_scale, void *x_out, void *h_out, const void *w,
+                                     uint32_t ggml_type, int64_t n, int64_t k, int64_t m, int64_t rows, void *out,
+                                     int64_t out_ld, cuca_dtype dtype) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    const NormIn rn{x, branch, norm_w, eps, residual_scale, x_out, h_out};
+    if (m > 0 && (st = norm_in_check(ctx, rn, m, k, dtype)) != CUCA_OK) return st;
+    return qmm_common(ctx, w, nullptr, ggml_type, n, k, h_out, k, m, rows, 0, 0.0f, out, out_ld, dtype, LogitCap(),
+                      &rn);
+}
+
+cuca_status cuca_hip_add_rmsnorm_qmm_glu(cuca_hip_ctx *ctx, const void *x, const void *branch, const float *norm_w,
+                                         float eps, float residual_scale, void *x_out, void *h_out, const void *gate,
+                                         const void *up, uint32_t ggml_type, int64_t ff, int64_t k, int64_t m,
+                                         cuca_act act, float clamp, void *out, int64_t out_ld, cuca_dtype dtype) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    if (act != CUCA_ACT_SILU && act != CUCA_ACT_GELU_TANH)
+        return fail(ctx, CUCA_INVALID_ARG, "bad activation %d", (int)act);
+    const NormIn rn{x, branch, norm_w, eps, residual_scale, x_out, h_out};
+    if (m > 0 && (st = norm_in_check(ctx, rn, m, k, dtype)) != CUCA_OK) return st;
+    return qmm_common(ctx, gate, up, ggml_type, ff, k, h_out, k, m, ff, act == CUCA_ACT_SILU ? 1 : 2, clamp, out,
+                      out_ld, dtype, LogitCap(), &rn);
 }
 
 // ---------------------------------------------------------------------

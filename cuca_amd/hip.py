@@ -89,6 +89,13 @@ SIGNATURES = {
                                          _st, _p, _p, _i64, _p, _p, _i64, _p, _p, _i64, _p, _st]),
     "cuca_hip_qmm_glu": (_st, [_p, _p, _p, _u32, _i64, _i64, _p, _i64, _i64, _st, _f32, _p, _i64,
                                _st]),
+    "cuca_hip_add_rmsnorm_qmm": (_st, [_p, _p, _p, _p, _f32, _f32, _p, _p, _p, _u32, _i64, _i64, _i64,
+                                       _i64, _p, _i64, _st]),
+    "cuca_hip_add_rmsnorm_qmm_glu": (_st, [_p, _p, _p, _p, _f32, _f32, _p, _p, _p, _p, _u32, _i64, _i64,
+                                           _i64, _st, _f32, _p, _i64, _st]),
+    "cuca_hip_add_rmsnorm_qmm_rope_store_kv": (_st, [_p, _p, _p, _p, _f32, _f32, _p, _p, _p, _u32, _i64,
+                                                     _i64, _i32, _i32, _i32, _i32, _st, _p, _p, _i64, _p,
+                                                     _p, _i64, _p, _p, _i64, _p, _st]),
     "cuca_hip_qgemm_workspace": (_st, [_u32, _i64, _i64, _i64, _i32, ctypes.POINTER(ctypes.c_size_t)]),
     "cuca_hip_qweight_dequant": (_st, [_p, _p, _u32, _i64, _i64, _p]),
     "cuca_hip_gemm_w16_workspace": (_st, [_i64, _i64, _i64, _i32, _st, ctypes.POINTER(ctypes.c_size_t)]),
@@ -436,6 +443,25 @@ class Context:
     def qmm_glu(self, gate, up, ggml_type, ff, k, x, ldx, m, act, clamp, out, out_ld, dtype):
         self.check(self.L.cuca_hip_qmm_glu(self.ptr, gate, up, ggml_type, ff, k, x, ldx, m, act,
                                            clamp, out, out_ld, dtype))
+
+    # the residual add + RMSNorm fused into the projection that reads it
+    def add_rmsnorm_qmm(self, x, branch, norm_w, eps, residual_scale, x_out, h_out, w, ggml_type, n, k, m,
+                        rows, out, out_ld, dtype):
+        self.check(self.L.cuca_hip_add_rmsnorm_qmm(self.ptr, x, branch, norm_w, eps, residual_scale, x_out,
+                                                   h_out, w, ggml_type, n, k, m, rows, out, out_ld, dtype))
+
+    def add_rmsnorm_qmm_glu(self, x, branch, norm_w, eps, residual_scale, x_out, h_out, gate, up, ggml_type,
+                            ff, k, m, act, clamp, out, out_ld, dtype):
+        self.check(self.L.cuca_hip_add_rmsnorm_qmm_glu(self.ptr, x, branch, norm_w, eps, residual_scale, x_out,
+                                                       h_out, gate, up, ggml_type, ff, k, m, act, clamp, out,
+                                                       out_ld, dtype))
+
+    def add_rmsnorm_qmm_rope_store_kv(self, x, branch, norm_w, eps, residual_scale, x_out, h_out, w, ggml_type,
+                                      k, m, nq, nk, head_dim, n_dims, kind, cos, sin, table_rows, positions,
+                                      q_out, q_ld, pool_k, pool_v, n_blocks, slots, dtype):
+        self.check(self.L.cuca_hip_add_rmsnorm_qmm_rope_store_kv(
+            self.ptr, x, branch, norm_w, eps, residual_scale, x_out, h_out, w, ggml_type, k, m, nq, nk, head_dim,
+            n_dims, kind, cos, sin, table_rows, positions, q_out, q_ld, pool_k, pool_v, n_blocks, slots, dtype))
 
 
     def moe_up(self, gate, up, estride, ggml_type, ff, n_embd, n_experts, x, ldx, n_tokens, offsets,

@@ -36,6 +36,9 @@
  *   cuca_hip_qmm_glu       gate/up qmm + Glu::apply       cpu.rs:342-371, 3554-3566
  *   cuca_hip_qmm_rope_     Q|K|V qmm + store_kv (RoPE,    cpu.rs:3028-3097,
  *     store_kv             paged K/V store)               gpu.rs:5266-5285
+ *   cuca_hip_add_rmsnorm_  the block's residual add +     cpu.rs:2650-2711, 342-371,
+ *     qmm(_glu, _rope_     rms, then the next projection  3028-3097; gpu.rs:5420-5483
+ *     store_kv)            (one launch at one row)
  *   cuca_hip_qgemm(_glu)   dense_dequant + matmul (GPU)   moe_kernel.rs:1414-1600
  *   cuca_hip_qweight_      dense_dequant_kernel, then     moe_kernel.rs:1560-1600,
  *     dequant, _gemm_w16   the dense matmul (GPU engine)  1414-1500
@@ -441,6 +444,45 @@ cuca_status cuca_hip_qmm_rope_store_kv(cuca_hip_ctx *ctx, const void *w, uint32_
 cuca_status cuca_hip_qmm_glu(cuca_hip_ctx *ctx, const void *gate, const void *up, uint32_t ggml_type,
                              int64_t ff, int64_t k, const void *x, int64_t ldx, int64_t m, cuca_act act,
                              float clamp, void *out, int64_t out_ld, cuca_dtype dtype);
+
+/* The residual add + RMSNorm fused into the projection that reads it (a
+ * block's attention norm before the Q|K|V projection, its FFN norm before
+ * gate/up: Transformer::block, cpu.rs:2650-2711; GPU attn_tail / ffn_half,
+ * gpu.rs:5420-5483), with the bits of the two calls it replaces:
+ *   cuca_hip_add_rmsnorm(x, branch, norm_w, NULL, eps, eps, residual_scale,
+ *                        m, k, x_out, h_out, dtype)
+ *   then cuca_hip_qmm / _qmm_glu / _qmm_rope_store_kv on h_out (ldx = k).
+ * At one activation row the matmul's workgroups each compute the norm of the
+ * row themselves (workgroup 0 also writes x_out and h_out), so the norm costs
+ * no launch of its own; otherwise the two calls run in turn.  x, branch,
+ * x_out, h_out: [m][k] of dtype, k the hidden size; branch and norm_w
+ * (f32[k]) nullable, x_out nullable; the Gemma post-norm (w_post) is not
+ * offered here.  x_out and h_out must not overlap x, branch or each other
+ * (CUCA_INVALID_ARG): the norm's outputs are written while other workgroups
+ * still read its inputs.  Other arguments and errors as the matmul's. */
+cuca_status cuca_hip_add_rmsnorm_qmm(cuca_hip_ctx *ctx, const void *x, const void *branch,
+                                     const float *norm_w, float eps, float residual_scale,
+                                     void *x_out, void *h_out, const void *w, uint32_t ggml_type,
+                                     int64_t n, int64_t k, int64_t m, int64_t rows, void *out,
+                                     int64_t out_ld, cuca_dtype dtype);
+cuca_status cuca_hip_add_rmsnorm_qmm_glu(cuca_hip_ctx *ctx, const void *x, const void *branch,
+                                         const float *norm_w, float eps, float residual_scale,
+                                         void *x_out, void *h_out, const void *gate, const void *up,
+                                         uint32_t ggml_type, int64_t ff, int64_t k, int64_t m,
+                                         cuca_act act, float clamp, void *out, int64_t out_ld,
+                                         cuca_dtype dtype);
+cuca_status cuca_hip_add_rmsnorm_qmm_rope_store_kv(cuca_hip_ctx *ctx, const void *x,
+                                                   const void *branch, const float *norm_w,
+                                                   float eps, float residual_scale, void *x_out,
+                                                   void *h_out, const void *w, uint32_t ggml_type,
+                                                   int64_t k, int64_t m, int32_t nq, int32_t nk,
+                                                   int32_t head_dim, int32_t n_dims,
+                                                   cuca_rope_kind kind, const float *cos,
+                                                   const float *sin, int64_t table_rows,
+                                                   const int32_t *positions, void *q_out,
+                                                   int64_t q_ld, void *pool_k, void *pool_v,
+                                                   int64_t n_blocks, const int32_t *slots,
+                                                   cuca_dtype dtype);
 
 /* The quantized matmul for many activation rows (prefill, large decode
  * batches) on the matrix cores: out[j][r] = x[j] . w[r] with each weight

@@ -424,6 +424,76 @@ extern "C" {
         out_ld: i64,
         dtype: cuca_dtype,
     ) -> cuca_status;
+    pub fn cuca_hip_add_rmsnorm_qmm(
+        ctx: *mut cuca_hip_ctx,
+        x: *const c_void,
+        branch: *const c_void,
+        norm_w: *const f32,
+        eps: f32,
+        residual_scale: f32,
+        x_out: *mut c_void,
+        h_out: *mut c_void,
+        w: *const c_void,
+        ggml_type: u32,
+        n: i64,
+        k: i64,
+        m: i64,
+        rows: i64,
+        out: *mut c_void,
+        out_ld: i64,
+        dtype: cuca_dtype,
+    ) -> cuca_status;
+    pub fn cuca_hip_add_rmsnorm_qmm_glu(
+        ctx: *mut cuca_hip_ctx,
+        x: *const c_void,
+        branch: *const c_void,
+        norm_w: *const f32,
+        eps: f32,
+        residual_scale: f32,
+        x_out: *mut c_void,
+        h_out: *mut c_void,
+        gate: *const c_void,
+        up: *const c_void,
+        ggml_type: u32,
+        ff: i64,
+        k: i64,
+        m: i64,
+        act: cuca_act,
+        clamp: f32,
+        out: *mut c_void,
+        out_ld: i64,
+        dtype: cuca_dtype,
+    ) -> cuca_status;
+    pub fn cuca_hip_add_rmsnorm_qmm_rope_store_kv(
+        ctx: *mut cuca_hip_ctx,
+        x: *const c_void,
+        branch: *const c_void,
+        norm_w: *const f32,
+        eps: f32,
+        residual_scale: f32,
+        x_out: *mut c_void,
+        h_out: *mut c_void,
+        w: *const c_void,
+        ggml_type: u32,
+        k: i64,
+        m: i64,
+        nq: i32,
+        nk: i32,
+        head_dim: i32,
+        n_dims: i32,
+        kind: cuca_rope_kind,
+        cos: *const f32,
+        sin: *const f32,
+        table_rows: i64,
+        positions: *const i32,
+        q_out: *mut c_void,
+        q_ld: i64,
+        pool_k: *mut c_void,
+        pool_v: *mut c_void,
+        n_blocks: i64,
+        slots: *const i32,
+        dtype: cuca_dtype,
+    ) -> cuca_status;
     pub fn cuca_hip_qgemm_workspace(
         ggml_type: u32,
         n: i64,
