@@ -85,7 +85,7 @@ struct QmdSlot {
 // at 16, 8, 4, 2, 1 (same e), and its last step (distance 1) adds the
 // item's two sums.  Measured on MI355X (Llama-3-8B decode, batch 1): the
 // LDS-staged form made the fused kernels about 2 us slower each.
-template <typename T, int NI>
+template <typename T, int NI, int BT>
 __device__ static inline void qmd_rms_prologue(const QmmArgs &a, float (&xv)[NI][8], const float (&bv)[NI][8],
                                                const float (&wv)[NI][8], float *vl) {
     __shared__ float rn_red[16];
@@ -94,10 +94,10 @@ __device__ static inline void qmd_rms_prologue(const QmmArgs &a, float (&xv)[NI]
     const int nitems = 4 * a.nb; // 8 values an item
     const bool w0 = blockIdx.x == 0;
     const int H = a.nb * 32, nch = H / CN, tpr = a.rn_tpr, per = a.rn_per;
-    const bool fast = per == 1 && tpr >= CUCA_WAVE && NI * CUCA_BLOCK * (8 / CN) >= tpr;
+    const bool fast = per == 1 && tpr >= CUCA_WAVE && NI * BT * (8 / CN) >= tpr;
 #pragma unroll
     for (int it = 0; it < NI; it++) {
-        const int item = it * CUCA_BLOCK + tid;
+        const int item = it * BT + tid;
         if (item < nitems) {
 #pragma unroll
             for (int e = 0; e < 8; e++) {
@@ -120,7 +120,7 @@ __device__ static inline void qmd_rms_prologue(const QmmArgs &a, float (&xv)[NI]
     if (fast) {
 #pragma unroll
         for (int it = 0; it < NI; it++) {
-            const int item = it * CUCA_BLOCK + tid;
+            const int item = it * BT + tid;
             if constexpr (CN == 8) {
                 float ss = 0.0f;
 #pragma unroll
@@ -165,8 +165,8 @@ __device__ static inline void qmd_rms_prologue(const QmmArgs &a, float (&xv)[NI]
                 if (tid == 0) rn_red[0] = ss;
             }
         } else {
-            for (int j = 0; j < 4; j++) {
-                const int li = tid + j * CUCA_BLOCK; // wave-uniform test: tpr is a multiple of 64
+            for (int j = 0; j < 1024 / BT; j++) {
+                const int li = tid + j * BT; // wave-uniform test: tpr is a multiple of 64
                 if (li < tpr) {
                     const float ss = group_sum<CUCA_WAVE>(thread_ss(li));
                     if (lane == 0) rn_red[li / CUCA_WAVE] = ss;
@@ -185,7 +185,7 @@ __device__ static inline void qmd_rms_prologue(const QmmArgs &a, float (&xv)[NI]
     const float inv = 1.0f / sqrtf(s / (float)H + a.rn_eps);
 #pragma unroll
     for (int it = 0; it < NI; it++) {
-        const int item = it * CUCA_BLOCK + tid;
+        const int item = it * BT + tid;
         if (item < nitems) {
 #pragma unroll
             for (int e = 0; e < 8; e++) {
@@ -203,13 +203,15 @@ __device__ static inline void qmd_rms_prologue(const QmmArgs &a, float (&xv)[NI]
 
 // MODE 0: plain (out[row], the LM head's cap when asked); 3: the Q|K|V
 // projection with RoPE and the paged K/V store in the epilogue (qmm.hip's
-// qmm_rope_kv_store).  D: ring slots; NI: activation items (8 values) per
-// thread, NI * 256 >= 4 ng G.  The grid is ceil(rows / 16) workgroups of
-// 256.  RN: the residual add + RMSNorm prologue.
-template <typename T, int FMT, bool GLU, int ACT, int MODE, int D, int NI, int PF = 1, bool RN = false>
+// qmm_rope_kv_store).  D: ring slots; WB: waves a workgroup; NI:
+// activation items (8 values) per thread, NI * 64 WB >= 4 ng G.  The grid
+// is ceil(rows / (4 WB)) workgroups of 64 WB threads.  RN: the residual add
+// + RMSNorm prologue.
+template <typename T, int FMT, bool GLU, int ACT, int MODE, int D, int NI, int PF = 1, bool RN = false, int WB = 4>
 __device__ static inline void qmd_body(const QmmArgs &a) {
     using F = QFmt<FMT>;
     constexpr int G = F::G;
+    constexpr int BT = WB * CUCA_WAVE; // threads a workgroup
     extern __shared__ __attribute__((aligned(16))) unsigned char qmd_lds[];
     const int ng = a.ng, nbp = ng * G, xstr = nbp + 2;
     qmm_u2 *xe = reinterpret_cast<qmm_u2 *>(qmd_lds);
@@ -217,7 +219,7 @@ __device__ static inline void qmd_body(const QmmArgs &a) {
     const int tid = threadIdx.x, lt = tid & (CUCA_WAVE - 1);
     const int wave = __builtin_amdgcn_readfirstlane(tid / CUCA_WAVE);
     const int r = lt >> 4, l = lt & 15;
-    const int row = (blockIdx.x * 4 + wave) * 4 + r;
+    const int row = (blockIdx.x * WB + wave) * 4 + r;
     // a row past the matrix streams the last row; its result is not stored
     const int lrow = row < a.rows ? row : a.rows - 1;
     const uint32_t nrec = (uint32_t)((int64_t)a.rows * a.row_bytes);
@@ -237,7 +239,7 @@ __device__ static inline void qmd_body(const QmmArgs &a) {
     float bv[RN ? NI : 1][8], wv[RN ? NI : 1][8];
 #pragma unroll
     for (int it = 0; it < NI; it++) {
-        const int item = it * CUCA_BLOCK + tid, b = item >> 2;
+        const int item = it * BT + tid, b = item >> 2;
         if (item < nitems && b < a.nb) {
             qmm_load8<T>(reinterpret_cast<const T *>(a.x) + (int64_t)b * 32 + sub * 8, xv[it]);
             if constexpr (RN) {
@@ -272,7 +274,7 @@ __device__ static inline void qmd_body(const QmmArgs &a) {
         load(ring[I.value], I.value);
         __builtin_amdgcn_sched_barrier(0);
     });
-    if constexpr (RN) qmd_rms_prologue<T, NI>(a, xv, bv, wv, reinterpret_cast<float *>(qmd_lds));
+    if constexpr (RN) qmd_rms_prologue<T, NI, BT>(a, xv, bv, wv, reinterpret_cast<float *>(qmd_lds));
 
     // 3. Quantise (Acts::new, qmm.rs:1217-1240: the four threads of a block
     // share its maximum) and expand: per (lane, block) the f16 pair
@@ -283,7 +285,7 @@ __device__ static inline void qmd_body(const QmmArgs &a) {
         const int base = 8 * (sub & 1) + (low ? 0 : 4);
 #pragma unroll
         for (int it = 0; it < NI; it++) {
-            const int item = it * CUCA_BLOCK + tid, b = item >> 2;
+            const int item = it * BT + tid, b = item >> 2;
             float amax = 0.0f;
 #pragma unroll
             for (int e = 0; e < 8; e++) amax = fmaxf(amax, fabsf(xv[it][e]));
@@ -436,6 +438,22 @@ __device__ static inline void qmd_body(const QmmArgs &a) {
     CUCA_QMD(cuca_qmd_glu_##TN##_##FN##_silu_n##NI##_rn, T, FMT, true, 0, 0, DG, NI, 1, true) \
     CUCA_QMD(cuca_qmd_glu_##TN##_##FN##_gelu_n##NI##_rn, T, FMT, true, 1, 0, DG, NI, 1, true) \
     CUCA_QMD(cuca_qmd_rope_kv_##TN##_##FN##_n##NI##_rn, T, FMT, false, 0, 3, DP, NI, 1, true)
+// The GLU as workgroups of 8 waves (32 rows; NI8 items a thread for rows
+// to 4096 / 16384 values, named n2 / n8 as their 4-wave counterparts): for
+// matrices of at least 32 rows per compute unit.  Every workgroup quantises
+// (and, _rn, normalises) the whole activation row, so halving the
+// workgroups per compute unit halves that work on each SIMD.  Measured on
+// MI355X (Llama-3-8B gate/up, Q4_0, batch-1 decode step): 64.7 -> 62.4 us
+// per layer with the norm in the prologue, 65.6-66.6 -> 63.5-64.8 without.
+#define CUCA_QMD_W8(NAME, ...)                                                             \
+    extern "C" __global__ __launch_bounds__(8 * CUCA_WAVE) void NAME(QmmArgs a) {          \
+        qmd_body<__VA_ARGS__>(a);                                                          \
+    }
+#define CUCA_QMD_W8_SET(TN, T, FN, FMT, NI, NI8, DG)                                       \
+    CUCA_QMD_W8(cuca_qmd_glu_##TN##_##FN##_silu_n##NI##w8, T, FMT, true, 0, 0, DG, NI8, 1, false, 8)   \
+    CUCA_QMD_W8(cuca_qmd_glu_##TN##_##FN##_gelu_n##NI##w8, T, FMT, true, 1, 0, DG, NI8, 1, false, 8)   \
+    CUCA_QMD_W8(cuca_qmd_glu_##TN##_##FN##_silu_n##NI##w8_rn, T, FMT, true, 0, 0, DG, NI8, 1, true, 8) \
+    CUCA_QMD_W8(cuca_qmd_glu_##TN##_##FN##_gelu_n##NI##w8_rn, T, FMT, true, 1, 0, DG, NI8, 1, true, 8)
 CUCA_QMD_SET(f32, float, q4_0, 0, 2, 4, 2)
 CUCA_QMD_SET(f32, float, q4_0, 0, 8, 8, 2)
 CUCA_QMD_SET(f32, float, q8_0, 1, 2, 8, 4)
@@ -452,3 +470,11 @@ CUCA_QMD_RN_SET(f16, _Float16, q4_0, 0, 2, 4, 2)
 CUCA_QMD_RN_SET(f16, _Float16, q4_0, 0, 8, 8, 2)
 CUCA_QMD_RN_SET(f16, _Float16, q8_0, 1, 2, 8, 4)
 CUCA_QMD_RN_SET(f16, _Float16, q8_0, 1, 8, 8, 4)
+CUCA_QMD_W8_SET(f32, float, q4_0, 0, 2, 1, 2)
+CUCA_QMD_W8_SET(f32, float, q4_0, 0, 8, 4, 2)
+CUCA_QMD_W8_SET(f32, float, q8_0, 1, 2, 1, 4)
+CUCA_QMD_W8_SET(f32, float, q8_0, 1, 8, 4, 4)
+CUCA_QMD_W8_SET(f16, _Float16, q4_0, 0, 2, 1, 2)
+CUCA_QMD_W8_SET(f16, _Float16, q4_0, 0, 8, 4, 2)
+CUCA_QMD_W8_SET(f16, _Float16, q8_0, 1, 2, 1, 4)
+CUCA_QMD_W8_SET(f16, _Float16, q8_0, 1, 8, 4, 4)

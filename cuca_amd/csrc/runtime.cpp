@@ -1263,6 +1263,14 @@ static cuca_status qmd_launch(cuca_hip_ctx *ctx, int mode, int glu, uint32_t ggm
           {cuca_qmd_f16_q8_0_n8_rn, cuca_qmd_glu_f16_q8_0_silu_n8_rn, cuca_qmd_glu_f16_q8_0_gelu_n8_rn,
            cuca_qmd_rope_kv_f16_q8_0_n8_rn}}}};
     const int kind = mode == 3 ? 3 : glu;
+    // the GLU as 8-wave workgroups (32 rows each) when every compute unit
+    // gets one: half the workgroups quantise (and normalise) the row
+    if ((kind == 1 || kind == 2) && div_up(a.rows, 32) >= (int64_t)ctx->cu_count) {
+        // [rn][dtype][format][n2, n8][silu, gelu]
+        static const Kernel table_w8[2][2][2][2][2] = {{{{{cuca_qmd_glu_f32_q4_0_silu_n2w8,cuca_qmd_glu_f32_q4_0_gelu_n2w8},{cuca_qmd_glu_f32_q4_0_silu_n8w8,cuca_qmd_glu_f32_q4_0_gelu_n8w8}},{{cuca_qmd_glu_f32_q8_0_silu_n2w8,cuca_qmd_glu_f32_q8_0_gelu_n2w8},{cuca_qmd_glu_f32_q8_0_silu_n8w8,cuca_qmd_glu_f32_q8_0_gelu_n8w8}}},{{{cuca_qmd_glu_f16_q4_0_silu_n2w8,cuca_qmd_glu_f16_q4_0_gelu_n2w8},{cuca_qmd_glu_f16_q4_0_silu_n8w8,cuca_qmd_glu_f16_q4_0_gelu_n8w8}},{{cuca_qmd_glu_f16_q8_0_silu_n2w8,cuca_qmd_glu_f16_q8_0_gelu_n2w8},{cuca_qmd_glu_f16_q8_0_silu_n8w8,cuca_qmd_glu_f16_q8_0_gelu_n8w8}}}},{{{{cuca_qmd_glu_f32_q4_0_silu_n2w8_rn,cuca_qmd_glu_f32_q4_0_gelu_n2w8_rn},{cuca_qmd_glu_f32_q4_0_silu_n8w8_rn,cuca_qmd_glu_f32_q4_0_gelu_n8w8_rn}},{{cuca_qmd_glu_f32_q8_0_silu_n2w8_rn,cuca_qmd_glu_f32_q8_0_gelu_n2w8_rn},{cuca_qmd_glu_f32_q8_0_silu_n8w8_rn,cuca_qmd_glu_f32_q8_0_gelu_n8w8_rn}}},{{{cuca_qmd_glu_f16_q4_0_silu_n2w8_rn,cuca_qmd_glu_f16_q4_0_gelu_n2w8_rn},{cuca_qmd_glu_f16_q4_0_silu_n8w8_rn,cuca_qmd_glu_f16_q4_0_gelu_n8w8_rn}},{{cuca_qmd_glu_f16_q8_0_silu_n2w8_rn,cuca_qmd_glu_f16_q8_0_gelu_n2w8_rn},{cuca_qmd_glu_f16_q8_0_silu_n8w8_rn,cuca_qmd_glu_f16_q8_0_gelu_n8w8_rn}}}}};
+        const Kernel k8 = table_w8[rn][dtype == CUCA_F16][ggml_type == CUCA_GGML_Q8_0][k > 4096][kind - 1];
+        return launch(ctx, k8, div_up(a.rows, 32), 8 * 64, (unsigned)qmd_lds(a.ng, g), a);
+    }
     const Kernel kk = (rn ? table_rn : table_k)[dtype == CUCA_F16][ggml_type == CUCA_GGML_Q8_0][k > 4096][kind];
     return launch(ctx, kk, div_up(a.rows, 16), CUCA_BLOCK_THREADS, (unsigned)qmd_lds(a.ng, g), a);
 }

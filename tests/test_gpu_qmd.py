@@ -57,8 +57,10 @@ def test_weight_row_prefix(ctx, qtype, k):
 @pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
 @pytest.mark.parametrize("act", [hip.ACT_SILU, hip.ACT_GELU_TANH])
-@pytest.mark.parametrize("ff,k,clamp", [(1, 32, 0.0), (37, 544, 0.0), (200, 4096, 2.0), (50, 14336, 0.0)])
+@pytest.mark.parametrize("ff,k,clamp", [(1, 32, 0.0), (37, 544, 0.0), (200, 4096, 2.0), (50, 14336, 0.0),
+                                         (8200, 4096, 0.0), (8200, 4160, 1.0)])
 def test_one_row_glu(ctx, qtype, dtype, act, ff, k, clamp):
+    """(8200 rows: the 8-wave workgroups, a partial last one.)"""
     rng = np.random.default_rng(ff + k + act)
     graw, gw = weight(ctx, rng, qtype, ff, k, (0.01, 0.05))
     uraw, uw = weight(ctx, rng, qtype, ff, k, (0.01, 0.05))

@@ -79,7 +79,7 @@ def test_plain_is_norm_then_qmm(ctx, k, dtype, qtype):
                                                       QT[qtype], n, k, m, n, out.ptr, n,
                                                       hip.dtype_code(NP[dtype])))
     if k < 16384:
-        assert len(names) == 1 and names[0].endswith("_rn"), names
+        assert len(names) == 1 and "_rn" in names[0], names
     else:  # the expanded row outgrows the one-row kernel's LDS: the norm, then the chunked matmul
         assert len(names) == 2 and names[0].startswith("cuca_norm"), names
     assert_bits_equal(xo.numpy(), wx.numpy(), f"x' {k} {dtype}")
@@ -108,7 +108,7 @@ def test_glu_options(ctx, branch, norm_w, rs, x_out, k, dtype):
     names = launches(ctx, lambda: ctx.add_rmsnorm_qmm_glu(dx.ptr, ptr(db), ptr(dw), eps, rs, ptr(xo), h.ptr,
                                                           gw.packed.ptr, uw.packed.ptr, QT[qtype], ff, k, m,
                                                           hip.ACT_SILU, 0.0, out.ptr, ff, dt))
-    assert len(names) == 1 and names[0].startswith("cuca_qmd_glu") and names[0].endswith("_rn"), names
+    assert len(names) == 1 and names[0].startswith("cuca_qmd_glu") and "_rn" in names[0], names
     if x_out:
         assert_bits_equal(xo.numpy(), wx.numpy(), "x'")
     assert_bits_equal(h.numpy(), wh.numpy(), "h")
@@ -133,6 +133,32 @@ def test_glu_act_clamp_and_two_rows(ctx, act, clamp, m):
                                                           gw.packed.ptr, uw.packed.ptr, QT[qtype], ff, k, m, act,
                                                           clamp, out.ptr, ff, dt))
     assert len(names) == m, names  # one row: one launch; two: the norm, then the matmul
+    assert_bits_equal(xo.numpy(), wx.numpy(), "x'")
+    assert_bits_equal(h.numpy(), wh.numpy(), "h")
+    assert_bits_equal(out.numpy(), want.numpy(), "glu out")
+
+
+@pytest.mark.parametrize("k,dtype,qtype", [(4096, "f32", "q4_0"), (4096, "f16", "q8_0"), (8192, "f32", "q4_0"),
+                                           (2048, "f32", "q8_0")])
+def test_glu_eight_wave_workgroups(ctx, k, dtype, qtype):
+    """A GLU of at least 32 rows per compute unit runs as 8-wave workgroups
+    (one activation item a thread to 4096 values): the same bits."""
+    rng = np.random.default_rng(k + len(dtype) + len(qtype))
+    m, ff, eps = 1, 8200, 1e-5
+    _, gw = weight(ctx, rng, qtype, ff, k, (0.01, 0.05))
+    _, uw = weight(ctx, rng, qtype, ff, k, (0.01, 0.05))
+    x, dx, db, dw = inputs(ctx, rng, m, k, dtype)
+    wx, wh = ref_norm(ctx, dx, db, dw, eps, 1.0, m, k, dtype)
+    dt = hip.dtype_code(NP[dtype])
+    want = ctx.empty((m, ff), NP[dtype])
+    names = launches(ctx, lambda: ctx.qmm_glu(gw.packed.ptr, uw.packed.ptr, QT[qtype], ff, k, wh.ptr, k, m,
+                                              hip.ACT_SILU, 0.0, want.ptr, ff, dt))
+    assert names == [f"cuca_qmd_glu_{dtype}_{qtype}_silu_n{2 if k <= 4096 else 8}w8"], names
+    xo, h, out = ctx.empty((m, k), NP[dtype]), ctx.empty((m, k), NP[dtype]), ctx.empty((m, ff), NP[dtype])
+    names = launches(ctx, lambda: ctx.add_rmsnorm_qmm_glu(dx.ptr, db.ptr, dw.ptr, eps, 1.0, xo.ptr, h.ptr,
+                                                          gw.packed.ptr, uw.packed.ptr, QT[qtype], ff, k, m,
+                                                          hip.ACT_SILU, 0.0, out.ptr, ff, dt))
+    assert len(names) == 1 and names[0].endswith("w8_rn"), names
     assert_bits_equal(xo.numpy(), wx.numpy(), "x'")
     assert_bits_equal(h.numpy(), wh.numpy(), "h")
     assert_bits_equal(out.numpy(), want.numpy(), "glu out")
