@@ -11,7 +11,8 @@
 // Split pass: a workgroup of 4 waves per (row, KV head, part of 4 CP key
 // positions); wave w takes the part's CP positions w*CP.. (CP = 64 / LPP,
 // LPP lanes per position: a K row slice of at most 256 bytes per lane, 128
-// for a group of 8).  Chunks start at the range's first block (positions
+// for a group of 8).  Groups of 4 at head_dim 64 / 128 take 8 waves of
+// twice the lanes per position: the same part length.  Chunks start at the range's first block (positions
 // before lo are masked), so a wave's positions are CP / 16 whole blocks and
 // every value row is one of CP / 16 scalar block bases plus a constant
 // offset.  The group's query heads (the GQA group) are staged once in LDS
@@ -74,19 +75,20 @@ __device__ static inline int64_t attn_pool_row(const AttnArgs &a, int row, int k
 // Lanes per key position for a d-wide row of T and a group of G query
 // heads: a lane's K slice is at most 256 bytes (64 VGPRs), and at most 128
 // for G = 8 (whose scores and weights need the registers).
-template <typename T, int D, int G> struct AttnShape {
+template <typename T, int D, int G, int LPPO = 0> struct AttnShape {
     static constexpr int ROWB = D * (int)sizeof(T);
     static constexpr int LPP0 = ROWB > 256 ? ROWB / 256 : 1;
-    static constexpr int LPP = G >= 8 && LPP0 < 2 ? 2 : LPP0;
+    static constexpr int LPP = LPPO ? LPPO : G >= 8 && LPP0 < 2 ? 2 : LPP0;
     static constexpr int CP = CUCA_WAVE / LPP; // positions per wave
     static constexpr int CPL = D / CUCA_WAVE;  // value columns per lane
 };
 
 __device__ static inline void pin_u(uint32_t &x) { asm volatile("" : "+v"(x)); }
 
-template <typename T, int D, int G>
+template <typename T, int D, int G, int WPB = 4, int LPPO = 0>
 __device__ static inline void attn_split_body(const AttnArgs &a) {
-    using S = AttnShape<T, D, G>;
+    using S = AttnShape<T, D, G, LPPO>;
+    constexpr int BT = WPB * CUCA_WAVE;
     constexpr int VP = Chunk<T>::N;        // values per 16-byte chunk
     constexpr int LPP = S::LPP, CP = S::CP, CPL = S::CPL;
     constexpr int KCH = D / VP / LPP;      // 16-byte K chunks per lane
@@ -100,8 +102,8 @@ __device__ static inline void attn_split_body(const AttnArgs &a) {
     constexpr int SL = D / LPP / (sizeof(T) == 2 ? 2 : 1);
     constexpr int SLP = LPP > 1 ? SL + 4 : SL;
     __shared__ __align__(16) uint32_t qs[G * LPP * SLP];
-    __shared__ __align__(16) float wsh[4][CP][G];        // each wave's weights
-    __shared__ __align__(16) float red[4][G][D + 2];     // each wave's partial
+    __shared__ __align__(16) float wsh[WPB][CP][G];      // each wave's weights
+    __shared__ __align__(16) float red[WPB][G][D + 2];   // each wave's partial
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / CUCA_WAVE);
     const int lane = threadIdx.x & (CUCA_WAVE - 1);
     const int rk = blockIdx.x / a.max_parts;
@@ -112,14 +114,14 @@ __device__ static inline void attn_split_body(const AttnArgs &a) {
     // range, block-table and K/V loads put one more memory latency in front
     // of the part's bulk reads.
     constexpr int NW = G * D / (sizeof(T) == 2 ? 2 : 1);
-    constexpr int NQ = (NW + CUCA_BLOCK - 1) / CUCA_BLOCK;
+    constexpr int NQ = (NW + BT - 1) / BT;
     uint32_t qv[NQ];
     {
         const uint32_t *qg = reinterpret_cast<const uint32_t *>(
             reinterpret_cast<const T *>(a.q) + (int64_t)row * a.q_ld + (int64_t)kvh * G * D);
 #pragma unroll
         for (int k = 0; k < NQ; k++) {
-            const int i = (int)threadIdx.x + k * CUCA_BLOCK;
+            const int i = (int)threadIdx.x + k * BT;
             qv[k] = i < NW ? qg[i] : 0u;
         }
     }
@@ -130,8 +132,8 @@ __device__ static inline void attn_split_body(const AttnArgs &a) {
     // Chunks start at lo rounded down to a block, so a wave's CP positions
     // are CP / 16 whole blocks; positions before lo or from hi on are masked.
     const int lo_al = lo & ~15;
-    if (valid && part * 4 * CP >= hi - lo_al) return; // a part past this row's range (whole workgroup)
-    const int p0 = lo_al + (part * 4 + wave) * CP;   // wave-uniform, a block boundary
+    if (valid && part * WPB * CP >= hi - lo_al) return; // a part past this row's range (whole workgroup)
+    const int p0 = lo_al + (part * WPB + wave) * CP;   // wave-uniform, a block boundary
     const bool wave_live = valid && p0 < hi;
     const int pi = lane / LPP, sub = lane - pi * LPP;
     const int p = p0 + pi;
@@ -181,7 +183,7 @@ __device__ static inline void attn_split_body(const AttnArgs &a) {
     __builtin_amdgcn_sched_barrier(0); // every load above is issued first
 #pragma unroll
     for (int k = 0; k < NQ; k++) {
-        const int i = (int)threadIdx.x + k * CUCA_BLOCK;
+        const int i = (int)threadIdx.x + k * BT;
         if (i < NW) qs[(i / SL) * SLP + i % SL] = qv[k];
     }
     __syncthreads();                   // qs is staged
@@ -273,7 +275,7 @@ __device__ static inline void attn_split_body(const AttnArgs &a) {
             }
         }
     }
-    // combine the 4 waves in LDS, in wave order
+    // combine the WPB waves in LDS, in wave order
 #pragma unroll
     for (int g = 0; g < G; g++) {
 #pragma unroll
@@ -285,12 +287,12 @@ __device__ static inline void attn_split_body(const AttnArgs &a) {
     }
     __syncthreads();
     if (!valid) return;
-    // wave w combines query heads w, w + 4, ...
-    for (int g = wave; g < G; g += 4) {
+    // wave w combines query heads w, w + WPB, ...
+    for (int g = wave; g < G; g += WPB) {
         float top = red[0][g][D];
-        for (int w2 = 1; w2 < 4; w2++) top = fmaxf(top, red[w2][g][D]);
-        float tot = 0.0f, f[4];
-        for (int w2 = 0; w2 < 4; w2++) {
+        for (int w2 = 1; w2 < WPB; w2++) top = fmaxf(top, red[w2][g][D]);
+        float tot = 0.0f, f[WPB];
+        for (int w2 = 0; w2 < WPB; w2++) {
             f[w2] = red[w2][g][D + 1] > 0.0f ? expf(red[w2][g][D] - top) : 0.0f;
             tot += red[w2][g][D + 1] * f[w2];
         }
@@ -298,7 +300,7 @@ __device__ static inline void attn_split_body(const AttnArgs &a) {
         float *pp = a.part + (((int64_t)row * a.n_head + head) * a.max_parts + part) * (D + 2);
         for (int e = lane; e < D; e += CUCA_WAVE) {
             float v = 0.0f;
-            for (int w2 = 0; w2 < 4; w2++) v += red[w2][g][e] * f[w2];
+            for (int w2 = 0; w2 < WPB; w2++) v += red[w2][g][e] * f[w2];
             pp[e] = v;
         }
         if (lane == 0) {
@@ -514,14 +516,27 @@ __device__ static inline void attn_merge_body(const AttnArgs &a) {
     extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void NAME(AttnArgs a) {            \
         BODY<__VA_ARGS__>(a);                                                              \
     }
+// Group-4 splits at head_dim 64 and 128 run as 8 waves of half the
+// positions each (twice the lanes per position), so a part covers the same
+// positions as the 4-wave form and a SIMD holds two waves.  Measured on
+// MI355X (32/8 heads of 128): 1 row, 4096 f32 keys 16.4 -> 15.0 us, 8192
+// f16 keys 19.4 -> 16.5 us; 32 rows x 1024 f32 keys 51.4 -> 50.5 us; 32-64
+// rows x 8192 keys 1.5-2.5 % slower.  The form does not depend on the batch,
+// so a row's bits do not either.
+#define CUCA_ATTN_W8(NAME, ...)                                                            \
+    extern "C" __global__ __launch_bounds__(8 * CUCA_WAVE) void NAME(AttnArgs a) {         \
+        attn_split_body<__VA_ARGS__>(a);                                                   \
+    }
 #define CUCA_ATTN_D(TN, T, D)                                                              \
     CUCA_ATTN(cuca_attn_split_##TN##_d##D##_g1, attn_split_body, T, D, 1)                  \
-    CUCA_ATTN(cuca_attn_split_##TN##_d##D##_g2, attn_split_body, T, D, 2)                  \
-    CUCA_ATTN(cuca_attn_split_##TN##_d##D##_g4, attn_split_body, T, D, 4)
+    CUCA_ATTN(cuca_attn_split_##TN##_d##D##_g2, attn_split_body, T, D, 2)
 #define CUCA_ATTN_SET(TN, T)                                                               \
     CUCA_ATTN_D(TN, T, 64)                                                                 \
     CUCA_ATTN_D(TN, T, 128)                                                                \
     CUCA_ATTN_D(TN, T, 256)                                                                \
+    CUCA_ATTN_W8(cuca_attn_split_##TN##_d64_g4, T, 64, 4, 8, 2 * AttnShape<T, 64, 4>::LPP)  \
+    CUCA_ATTN_W8(cuca_attn_split_##TN##_d128_g4, T, 128, 4, 8, 2 * AttnShape<T, 128, 4>::LPP) \
+    CUCA_ATTN(cuca_attn_split_##TN##_d256_g4, attn_split_body, T, 256, 4)                  \
     CUCA_ATTN(cuca_attn_split_##TN##_d64_g8, attn_split_body, T, 64, 8)                    \
     CUCA_ATTN(cuca_attn_split_##TN##_d128_g8, attn_split_body, T, 128, 8)                  \
     CUCA_ATTN(cuca_attn_split_##TN##_generic, attn_split_generic_body, T)                  \

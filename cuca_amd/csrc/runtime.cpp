@@ -1028,7 +1028,8 @@ static cuca_status paged_decode_run(cuca_hip_ctx *ctx, const void *q, int64_t q_
     const bool vec = di >= 0 && gi >= 0 && !(di == 2 && gi == 3) && al16(pool_k) && al16(pool_v) &&
                      ((size_t)head_dim * es) % 16 == 0;
     // vector kernel: a part = 4 waves x CP positions, CP = 64 / LPP with
-    // LPP = max(1, row bytes / 256), and at least 2 for a group of 8;
+    // LPP = max(1, row bytes / 256), and at least 2 for a group of 8 (the
+    // 8-wave group-4 kernels: 8 waves x CP / 2, the same length);
     // generic: a part = 64 positions
     int64_t part_positions = CUCA_ATTN_MIN_PART;
     if (vec) {
@@ -1092,7 +1093,9 @@ static cuca_status paged_decode_run(cuca_hip_ctx *ctx, const void *q, int64_t q_
         split = f16 ? cuca_attn_split_f16_generic : cuca_attn_split_f32_generic;
         grid = div_up(rows * n_head * parts, 4); // a wave per (row, head, part)
     }
-    if ((st = launch(ctx, split, grid, 256, 0, a)) != CUCA_OK) return st;
+    // (group-4 splits at head_dim 64 / 128 are 8-wave workgroups)
+    const unsigned split_threads = vec && gi == 2 && di < 2 ? 512u : 256u;
+    if ((st = launch(ctx, split, grid, split_threads, 0, a)) != CUCA_OK) return st;
     static const Kernel km[2][4] = {
         {cuca_attn_merge_f32_c1, cuca_attn_merge_f32_c2, cuca_attn_merge_f32_c4, cuca_attn_merge_f32_c8},
         {cuca_attn_merge_f16_c1, cuca_attn_merge_f16_c2, cuca_attn_merge_f16_c4, cuca_attn_merge_f16_c8}};
