@@ -454,6 +454,13 @@ __device__ static inline void qmd_body(const QmmArgs &a) {
     CUCA_QMD_W8(cuca_qmd_glu_##TN##_##FN##_gelu_n##NI##w8, T, FMT, true, 1, 0, DG, NI8, 1, false, 8)   \
     CUCA_QMD_W8(cuca_qmd_glu_##TN##_##FN##_silu_n##NI##w8_rn, T, FMT, true, 0, 0, DG, NI8, 1, true, 8) \
     CUCA_QMD_W8(cuca_qmd_glu_##TN##_##FN##_gelu_n##NI##w8_rn, T, FMT, true, 1, 0, DG, NI8, 1, true, 8)
+// The Q|K|V projection with the norm prologue as 8-wave workgroups, at any
+// row count: the prologue is the larger share of its time, and halving the
+// workgroups that repeat it paid even with compute units left idle (8B
+// batch-1 step, 6144 rows in 192 workgroups: 61.7 -> 59.9 us per layer; the
+// projection without the prologue gained nothing, so it keeps 4 waves).
+#define CUCA_QMD_W8_QKV(TN, T, FN, FMT, NI, NI8, DP)                                        \
+    CUCA_QMD_W8(cuca_qmd_rope_kv_##TN##_##FN##_n##NI##w8_rn, T, FMT, false, 0, 3, DP, NI8, 1, true, 8)
 CUCA_QMD_SET(f32, float, q4_0, 0, 2, 4, 2)
 CUCA_QMD_SET(f32, float, q4_0, 0, 8, 8, 2)
 CUCA_QMD_SET(f32, float, q8_0, 1, 2, 8, 4)
@@ -478,3 +485,11 @@ CUCA_QMD_W8_SET(f16, _Float16, q4_0, 0, 2, 1, 2)
 CUCA_QMD_W8_SET(f16, _Float16, q4_0, 0, 8, 4, 2)
 CUCA_QMD_W8_SET(f16, _Float16, q8_0, 1, 2, 1, 4)
 CUCA_QMD_W8_SET(f16, _Float16, q8_0, 1, 8, 4, 4)
+CUCA_QMD_W8_QKV(f32, float, q4_0, 0, 2, 1, 4)
+CUCA_QMD_W8_QKV(f32, float, q4_0, 0, 8, 4, 8)
+CUCA_QMD_W8_QKV(f32, float, q8_0, 1, 2, 1, 8)
+CUCA_QMD_W8_QKV(f32, float, q8_0, 1, 8, 4, 8)
+CUCA_QMD_W8_QKV(f16, _Float16, q4_0, 0, 2, 1, 4)
+CUCA_QMD_W8_QKV(f16, _Float16, q4_0, 0, 8, 4, 8)
+CUCA_QMD_W8_QKV(f16, _Float16, q8_0, 1, 2, 1, 8)
+CUCA_QMD_W8_QKV(f16, _Float16, q8_0, 1, 8, 4, 8)

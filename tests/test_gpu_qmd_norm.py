@@ -166,8 +166,10 @@ def test_glu_eight_wave_workgroups(ctx, k, dtype, qtype):
 
 @pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
-@pytest.mark.parametrize("nq,nk,d,k,m", [(32, 8, 128, 4096, 1), (4, 2, 64, 512, 1), (4, 2, 64, 512, 3)])
+@pytest.mark.parametrize("nq,nk,d,k,m", [(32, 8, 128, 4096, 1), (4, 2, 64, 512, 1), (4, 2, 64, 512, 3),
+                                         (6, 2, 64, 8192, 1)])
 def test_qkv_rope_store(ctx, qtype, dtype, nq, nk, d, k, m):
+    """At one row the 8-wave kernels (rows to 4096 values, and beyond)."""
     rng = np.random.default_rng(nq + nk + d + k + m + len(qtype))
     n, eps = (nq + 2 * nk) * d, 1e-5
     _, w = weight(ctx, rng, qtype, n, k)
@@ -190,6 +192,8 @@ def test_qkv_rope_store(ctx, qtype, dtype, nq, nk, d, k, m):
                 hip.ROPE_NORM, dcos.ptr, dsin.ptr, 8192, dpos.ptr, q.ptr, nq * d, pk.ptr, pv.ptr, n_blocks,
                 dslots.ptr, dt))
             assert len(names) == (1 if m == 1 else 2), names
+            if m == 1:
+                assert names[0].endswith("w8_rn"), names
         else:
             ctx.add_rmsnorm(dx.ptr, db.ptr, dw.ptr, None, eps, eps, 1.0, m, k, xo.ptr, h.ptr, dt)
             ctx.qmm_rope_store_kv(w.packed.ptr, QT[qtype], k, h.ptr, k, m, nq, nk, d, d, hip.ROPE_NORM, dcos.ptr,
