@@ -133,6 +133,8 @@ typedef struct {
     int32_t max_blocks, max_parts;
     int32_t part_positions; /* key positions per partial                    */
     float scale;
+    int32_t direct;         /* one part a row: the split writes out itself  */
+    int32_t pad_;
 } AttnArgs;
 
 /* Quantized matmul (qmm.hip): packed weights [n][ng][GB] (see there),

@@ -34,6 +34,11 @@
 // streaming copy's 80 %).  16-byte value loads (4 rows per instruction)
 // measured slower (53 % loads-only).
 //
+// When no row can have more than one part (max_parts == 1, short
+// contexts), the split writes each head's output itself and there is no
+// merge launch: the merge of one part multiplies by e^0 = 1 and divides by
+// the part's own sum, so the bits are the same.
+//
 // Merge pass: one wave per (row, query head) combines the row's parts in
 // part order -- the global maximum M, then sum_p acc_p e^(m_p - M) /
 // sum_p sum_p e^(m_p - M), the reference's merge (paged_kernel.rs:
@@ -286,7 +291,13 @@ __device__ static inline void attn_split_body(const AttnArgs &a) {
         }
     }
     __syncthreads();
-    if (!valid) return;
+    if (!valid) {
+        if (a.direct) { // the merge's zero rows for a bad range
+            T *o = reinterpret_cast<T *>(a.out) + ((int64_t)row * a.n_head + kvh * G) * D;
+            for (int e = threadIdx.x; e < G * D; e += BT) store1<T>(o, e, 0.0f);
+        }
+        return;
+    }
     // wave w combines query heads w, w + WPB, ...
     for (int g = wave; g < G; g += WPB) {
         float top = red[0][g][D];
@@ -298,12 +309,15 @@ __device__ static inline void attn_split_body(const AttnArgs &a) {
         }
         const int head = kvh * G + g;
         float *pp = a.part + (((int64_t)row * a.n_head + head) * a.max_parts + part) * (D + 2);
+        T *o = reinterpret_cast<T *>(a.out) + ((int64_t)row * a.n_head + head) * D;
         for (int e = lane; e < D; e += CUCA_WAVE) {
             float v = 0.0f;
             for (int w2 = 0; w2 < WPB; w2++) v += red[w2][g][e] * f[w2];
-            pp[e] = v;
+            // one part: what the merge computes from it, acc e^0 / (sum e^0)
+            if (a.direct) store1<T>(o, e, v / tot);
+            else pp[e] = v;
         }
-        if (lane == 0) {
+        if (lane == 0 && !a.direct) {
             pp[D] = top;
             pp[D + 1] = tot;
         }

@@ -1072,6 +1072,8 @@ static cuca_status paged_decode_run(cuca_hip_ctx *ctx, const void *q, int64_t q_
     a.max_parts = (int32_t)parts;
     a.part_positions = (int32_t)part_positions;
     a.scale = scale;
+    // one part a row (short contexts): the split writes the outputs itself
+    a.direct = vec && parts == 1 ? 1 : 0;
     Kernel split;
     unsigned grid;
     if (vec) {
@@ -1096,6 +1098,7 @@ static cuca_status paged_decode_run(cuca_hip_ctx *ctx, const void *q, int64_t q_
     // (group-4 splits at head_dim 64 / 128 are 8-wave workgroups)
     const unsigned split_threads = vec && gi == 2 && di < 2 ? 512u : 256u;
     if ((st = launch(ctx, split, grid, split_threads, 0, a)) != CUCA_OK) return st;
+    if (a.direct) return CUCA_OK;
     static const Kernel km[2][4] = {
         {cuca_attn_merge_f32_c1, cuca_attn_merge_f32_c2, cuca_attn_merge_f32_c4, cuca_attn_merge_f32_c8},
         {cuca_attn_merge_f16_c1, cuca_attn_merge_f16_c2, cuca_attn_merge_f16_c4, cuca_attn_merge_f16_c8}};

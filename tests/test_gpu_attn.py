@@ -123,6 +123,48 @@ def test_a_row_is_bit_identical_alone_and_in_a_batch(ctx):
         assert_bits_equal(one[0], all_rows[r], f"row {r}")
 
 
+@pytest.mark.parametrize("dtype,width", [("f32", 8), ("f16", 16)])
+def test_one_part_rows_skip_the_merge(ctx, dtype, width):
+    """A call whose rows all fit one part (a table of at most one part's
+    blocks: 128 f32 / 256 f16 keys at 32/8 heads of 128) has the split write
+    the outputs: one launch, the bits of the merge path (the same rows next
+    to a long row), within the oracle's bar; a bad range gives the merge
+    path's zero row."""
+    rng = np.random.default_rng(width)
+    nq, nk, d, n_blocks = 32, 8, 128, 96
+    lengths = [1, 5, 16, 17, 100, width * 16]
+    tables, ranges = make_batch(rng, lengths, n_blocks, width)
+    pk = rng.standard_normal((n_blocks, nk, 16, d)).astype(NP[dtype])
+    pv = rng.standard_normal((n_blocks, nk, 16, d)).astype(NP[dtype])
+    q = (2.0 * rng.standard_normal((len(lengths), nq, d))).astype(NP[dtype])
+    ctx.sync()
+    ctx.profile_start(8)
+    got = check(ctx, q, pk, pv, tables, ranges, nq, 1.0 / np.sqrt(d))
+    names = [k for k, _ in ctx.profile_stop()]
+    assert len(names) == 1 and names[0].startswith("cuca_attn_split"), names
+    # the same rows in a call with a long row take the merge
+    lt, lr = make_batch(rng, [700], n_blocks, 48)
+    wide = np.full((len(lengths) + 1, 48), O.NO_BLOCK, np.uint32)
+    wide[:len(lengths), :width] = tables
+    wide[len(lengths)] = lt[0]
+    ql = (2.0 * rng.standard_normal((1, nq, d))).astype(NP[dtype])
+    merged = run(ctx, np.concatenate([q, ql]), pk, pv, wide, np.concatenate([ranges, lr]), nq, 1.0 / np.sqrt(d))
+    assert_bits_equal(got, merged[:len(lengths)], "one-part rows vs the merge path")
+    # a bad range: zeros, as the merge writes them, and reported
+    bad = ranges.copy()
+    bad[2] = (9, 9)
+    for tb, rg, qq in ((tables, bad, q), (wide, np.concatenate([bad, lr]), np.concatenate([q, ql]))):
+        with pytest.raises(hip.CucaError, match="empty key range"):
+            run(ctx, qq, pk, pv, tb, rg, nq, 0.1)
+        pool = ops.KvPool(ctx, n_blocks, nk, d, NP[dtype])
+        pool.k.upload(pk)
+        pool.v.upload(pv)
+        out = pool.decode(ctx.array(qq), ctx.array(tb.astype(np.uint32)), ctx.array(rg.astype(np.int32)), nq, 0.1)
+        with pytest.raises(hip.CucaError):
+            ctx.check_device()
+        assert not np.any(out.numpy()[2]), "bad row not zero"
+
+
 def test_bad_blocks_and_ranges_are_reported(ctx):
     rng = np.random.default_rng(9)
     pk = rng.standard_normal((4, 1, 16, 64)).astype(np.float32)
