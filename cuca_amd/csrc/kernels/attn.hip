@@ -11,7 +11,7 @@
 // Split pass: a workgroup of 4 waves per (row, KV head, part of 4 CP key
 // positions); wave w takes the part's CP positions w*CP.. (CP = 64 / LPP,
 // LPP lanes per position: a K row slice of at most 256 bytes per lane, 128
-// for a group of 8).  Groups of 4 at head_dim 64 / 128 take 8 waves of
+// for a group of 8).  f16 groups of 4 at head_dim 64 / 128 take 8 waves of
 // twice the lanes per position: the same part length.  Chunks start at the range's first block (positions
 // before lo are masked), so a wave's positions are CP / 16 whole blocks and
 // every value row is one of CP / 16 scalar block bases plus a constant
@@ -530,13 +530,15 @@ __device__ static inline void attn_merge_body(const AttnArgs &a) {
     extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void NAME(AttnArgs a) {            \
         BODY<__VA_ARGS__>(a);                                                              \
     }
-// Group-4 splits at head_dim 64 and 128 run as 8 waves of half the
+// f16 group-4 splits at head_dim 64 and 128 run as 8 waves of half the
 // positions each (twice the lanes per position), so a part covers the same
 // positions as the 4-wave form and a SIMD holds two waves.  Measured on
-// MI355X (32/8 heads of 128): 1 row, 4096 f32 keys 16.4 -> 15.0 us, 8192
-// f16 keys 19.4 -> 16.5 us; 32 rows x 1024 f32 keys 51.4 -> 50.5 us; 32-64
-// rows x 8192 keys 1.5-2.5 % slower.  The form does not depend on the batch,
-// so a row's bits do not either.
+// MI355X (32/8 heads of 128): 1 row x 8192 f16 keys 19.4 -> 16.5 us; 32-64
+// rows x 8192 f16 keys 1.5-2.5 % slower.  For f32 pools the 8-wave form was
+// faster at one row (4096 keys 16.4 -> 15.0 us) but slower in the 8B decode
+// step at 32 rows x 1024 keys (attention 58.3 -> 62.2 us per layer), so f32
+// keeps 4 waves.  The form depends on (dtype, head_dim, group) only, never
+// on the batch, so a row's bits do not either.
 #define CUCA_ATTN_W8(NAME, ...)                                                            \
     extern "C" __global__ __launch_bounds__(8 * CUCA_WAVE) void NAME(AttnArgs a) {         \
         attn_split_body<__VA_ARGS__>(a);                                                   \
@@ -544,12 +546,17 @@ __device__ static inline void attn_merge_body(const AttnArgs &a) {
 #define CUCA_ATTN_D(TN, T, D)                                                              \
     CUCA_ATTN(cuca_attn_split_##TN##_d##D##_g1, attn_split_body, T, D, 1)                  \
     CUCA_ATTN(cuca_attn_split_##TN##_d##D##_g2, attn_split_body, T, D, 2)
+#define CUCA_ATTN_G4_f32                                                                   \
+    CUCA_ATTN(cuca_attn_split_f32_d64_g4, attn_split_body, float, 64, 4)                   \
+    CUCA_ATTN(cuca_attn_split_f32_d128_g4, attn_split_body, float, 128, 4)
+#define CUCA_ATTN_G4_f16                                                                   \
+    CUCA_ATTN_W8(cuca_attn_split_f16_d64_g4, _Float16, 64, 4, 8, 2 * AttnShape<_Float16, 64, 4>::LPP) \
+    CUCA_ATTN_W8(cuca_attn_split_f16_d128_g4, _Float16, 128, 4, 8, 2 * AttnShape<_Float16, 128, 4>::LPP)
 #define CUCA_ATTN_SET(TN, T)                                                               \
     CUCA_ATTN_D(TN, T, 64)                                                                 \
     CUCA_ATTN_D(TN, T, 128)                                                                \
     CUCA_ATTN_D(TN, T, 256)                                                                \
-    CUCA_ATTN_W8(cuca_attn_split_##TN##_d64_g4, T, 64, 4, 8, 2 * AttnShape<T, 64, 4>::LPP)  \
-    CUCA_ATTN_W8(cuca_attn_split_##TN##_d128_g4, T, 128, 4, 8, 2 * AttnShape<T, 128, 4>::LPP) \
+    CUCA_ATTN_G4_##TN                                                                      \
     CUCA_ATTN(cuca_attn_split_##TN##_d256_g4, attn_split_body, T, 256, 4)                  \
     CUCA_ATTN(cuca_attn_split_##TN##_d64_g8, attn_split_body, T, 64, 8)                    \
     CUCA_ATTN(cuca_attn_split_##TN##_d128_g8, attn_split_body, T, 128, 8)                  \

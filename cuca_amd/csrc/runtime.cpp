@@ -1029,7 +1029,7 @@ static cuca_status paged_decode_run(cuca_hip_ctx *ctx, const void *q, int64_t q_
                      ((size_t)head_dim * es) % 16 == 0;
     // vector kernel: a part = 4 waves x CP positions, CP = 64 / LPP with
     // LPP = max(1, row bytes / 256), and at least 2 for a group of 8 (the
-    // 8-wave group-4 kernels: 8 waves x CP / 2, the same length);
+    // 8-wave f16 group-4 kernels: 8 waves x CP / 2, the same length);
     // generic: a part = 64 positions
     int64_t part_positions = CUCA_ATTN_MIN_PART;
     if (vec) {
@@ -1095,8 +1095,8 @@ static cuca_status paged_decode_run(cuca_hip_ctx *ctx, const void *q, int64_t q_
         split = f16 ? cuca_attn_split_f16_generic : cuca_attn_split_f32_generic;
         grid = div_up(rows * n_head * parts, 4); // a wave per (row, head, part)
     }
-    // (group-4 splits at head_dim 64 / 128 are 8-wave workgroups)
-    const unsigned split_threads = vec && gi == 2 && di < 2 ? 512u : 256u;
+    // (f16 group-4 splits at head_dim 64 / 128 are 8-wave workgroups)
+    const unsigned split_threads = vec && f16 && gi == 2 && di < 2 ? 512u : 256u;
     if ((st = launch(ctx, split, grid, split_threads, 0, a)) != CUCA_OK) return st;
     if (a.direct) return CUCA_OK;
     static const Kernel km[2][4] = {
