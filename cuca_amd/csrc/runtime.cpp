@@ -1269,6 +1269,14 @@ static cuca_status qmd_launch(cuca_hip_ctx *ctx, int mode, int glu, uint32_t ggm
           {cuca_qmd_f16_q8_0_n8_rn, cuca_qmd_glu_f16_q8_0_silu_n8_rn, cuca_qmd_glu_f16_q8_0_gelu_n8_rn,
            cuca_qmd_rope_kv_f16_q8_0_n8_rn}}}};
     const int kind = mode == 3 ? 3 : glu;
+    // a plain matmul of at least 32 rows per compute unit (the LM head) as
+    // 8-wave workgroups
+    if (kind == 0 && !rn && div_up(a.rows, 32) >= (int64_t)ctx->cu_count) {
+        // [dtype][format][n2, n8]
+        static const Kernel table_p8[2][2][2] = {{{cuca_qmd_f32_q4_0_n2w8,cuca_qmd_f32_q4_0_n8w8},{cuca_qmd_f32_q8_0_n2w8,cuca_qmd_f32_q8_0_n8w8}},{{cuca_qmd_f16_q4_0_n2w8,cuca_qmd_f16_q4_0_n8w8},{cuca_qmd_f16_q8_0_n2w8,cuca_qmd_f16_q8_0_n8w8}}};
+        return launch(ctx, table_p8[dtype == CUCA_F16][ggml_type == CUCA_GGML_Q8_0][k > 4096], div_up(a.rows, 32),
+                      8 * 64, (unsigned)qmd_lds(a.ng, g), a);
+    }
     // the Q|K|V with the norm prologue as 8-wave workgroups
     if (kind == 3 && rn) {
         // [dtype][format][n2, n8]
@@ -1375,9 +1383,13 @@ static cuca_status qmm_common(cuca_hip_ctx *ctx, const void *w, const void *w_up
     if (!al16(x) || ((size_t)ldx * es) % 16 != 0)
         return fail(ctx, CUCA_INVALID_ARG, "qmm: activation rows must start 16-byte aligned");
     const int64_t nb = k / 32, ng = (nb + g - 1) / g;
-    // one or two rows whose tile fits the LDS: the decode GEMV, each
-    // workgroup quantising the rows itself
-    const bool qmv = m <= 2 && qmv_wins(ctx, rows) && qmv_fits(m, ng * g, g);
+    // one or two rows of a tall matrix whose tile fits the LDS: the decode
+    // GEMV stream, each workgroup quantising the rows itself -- except that
+    // one row the one-row kernel takes runs there (measured on MI355X, the
+    // 128256 x 4096 LM head at one row: Q8_0 101-103 -> 88-89 us, Q4_0 59-60
+    // -> 51 us as 8-wave workgroups)
+    const bool qmv = m <= 2 && qmv_wins(ctx, rows) && qmv_fits(m, ng * g, g) &&
+                     !(m == 1 && qmd_fits(m, k, ng, g, rows, ng * gb));
     if (qmv) {
         if (rn && (st = norm_in_launch(ctx, *rn, m, k, dtype)) != CUCA_OK) return st;
         return qmv_launch(ctx, 3, w, w_up, ggml_type, n, k, nullptr, 0, nullptr, x, ldx, m, rows, glu, clamp, out,

@@ -254,8 +254,9 @@ def test_rows_too_long_for_the_decode_gemv_take_the_chunked_kernel(ctx, qtype, m
 
 @pytest.mark.parametrize("m", [1, 2])
 def test_lm_head_on_the_decode_gemv(ctx, m):
-    """A vocabulary tall enough (40000 rows) for qmm to route one or two rows
-    to the decode GEMV, each wave running several tasks."""
+    """A vocabulary tall enough (40000 rows) for the many-row routes: two
+    rows take the decode GEMV (each wave running several tasks), one row the
+    one-row kernel's 8-wave workgroups."""
     rng = np.random.default_rng(m)
     vocab, k = 40000, 512
     raw, w = weight(ctx, rng, "q8_0", vocab, k, (0.01, 0.05))
@@ -275,8 +276,8 @@ def test_lm_head_on_the_decode_gemv(ctx, m):
 @pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
 @pytest.mark.parametrize("glu", [False, True])
 def test_decode_gemv_waves_that_run_several_tasks(ctx, qtype, glu):
-    """40000 rows: more four-row tasks than the persistent grid has waves, so
-    a wave runs several tasks one after the other (the LM head's case)."""
+    """40000 rows at one activation row: the one-row kernel's 8-wave
+    workgroups (plain and GLU), the LM head's route."""
     rng = np.random.default_rng(40000 + glu)
     n, k = 40000, 256
     raw, w = weight(ctx, rng, qtype, n, k)
