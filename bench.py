@@ -713,6 +713,12 @@ class DecodeStep:
         c.embed_gguf(self.table.data_ptr(), hip.GGML_Q8_0, self.vocab, H, self.out_ids.data_ptr(), n, 1.0,
                      self.x.data_ptr(), hip.F32)
         self.issue_layers()
+        if self.fuse_norm:  # the final norm in the LM head's prologue (no logit scale or soft-cap here)
+            c.add_rmsnorm_qmm(self.x.data_ptr(), self.ffn.data_ptr(), self.nout.data_ptr(), eps, 1.0, None,
+                              self.h.data_ptr(), self.head.data_ptr(), hip.GGML_Q8_0, self.vocab, H, n, self.vocab,
+                              self.logits.data_ptr(), self.vocab, hip.F32)
+            c.argmax(self.logits.data_ptr(), self.vocab, n, self.vocab, hip.F32, self.out_ids.data_ptr())
+            return
         c.add_rmsnorm(self.x.data_ptr(), self.ffn.data_ptr(), self.nout.data_ptr(), None, eps, eps, 1.0, n,
                       H, self.x.data_ptr(), self.h.data_ptr(), hip.F32)
         if self.mm == "qgemm":  # no logit scale or soft-cap in this model: the plain matmul

@@ -460,11 +460,13 @@ __device__ static inline void qmd_body(const QmmArgs &a) {
 // batch-1 step, 6144 rows in 192 workgroups: 61.7 -> 59.9 us per layer; the
 // projection without the prologue gained nothing, so it keeps 4 waves).
 // A plain matmul of at least 32 rows per compute unit (the LM head) as
-// 8-wave workgroups: the 128256-row head at one row, Q4_0 55-59 -> 51 us
+// 8-wave workgroups, with or without the norm prologue (the final norm in
+// front of the head): the 128256-row head at one row, Q4_0 55-59 -> 51 us
 // (the decode GEMV stream took 59-60 us; Q8_0 88-89 us either way against
 // its 101-103 us).
 #define CUCA_QMD_W8_PLAIN(TN, T, FN, FMT, NI, NI8, DP)                                      \
-    CUCA_QMD_W8(cuca_qmd_##TN##_##FN##_n##NI##w8, T, FMT, false, 0, 0, DP, NI8, 1, false, 8)
+    CUCA_QMD_W8(cuca_qmd_##TN##_##FN##_n##NI##w8, T, FMT, false, 0, 0, DP, NI8, 1, false, 8) \
+    CUCA_QMD_W8(cuca_qmd_##TN##_##FN##_n##NI##w8_rn, T, FMT, false, 0, 0, DP, NI8, 1, true, 8)
 #define CUCA_QMD_W8_QKV(TN, T, FN, FMT, NI, NI8, DP)                                        \
     CUCA_QMD_W8(cuca_qmd_rope_kv_##TN##_##FN##_n##NI##w8_rn, T, FMT, false, 0, 3, DP, NI8, 1, true, 8)
 CUCA_QMD_SET(f32, float, q4_0, 0, 2, 4, 2)

@@ -1269,18 +1269,28 @@ static cuca_status qmd_launch(cuca_hip_ctx *ctx, int mode, int glu, uint32_t ggm
           {cuca_qmd_f16_q8_0_n8_rn, cuca_qmd_glu_f16_q8_0_silu_n8_rn, cuca_qmd_glu_f16_q8_0_gelu_n8_rn,
            cuca_qmd_rope_kv_f16_q8_0_n8_rn}}}};
     const int kind = mode == 3 ? 3 : glu;
-    // a plain matmul of at least 32 rows per compute unit (the LM head) as
-    // 8-wave workgroups
-    if (kind == 0 && !rn && div_up(a.rows, 32) >= (int64_t)ctx->cu_count) {
-        // [dtype][format][n2, n8]
-        static const Kernel table_p8[2][2][2] = {{{cuca_qmd_f32_q4_0_n2w8,cuca_qmd_f32_q4_0_n8w8},{cuca_qmd_f32_q8_0_n2w8,cuca_qmd_f32_q8_0_n8w8}},{{cuca_qmd_f16_q4_0_n2w8,cuca_qmd_f16_q4_0_n8w8},{cuca_qmd_f16_q8_0_n2w8,cuca_qmd_f16_q8_0_n8w8}}};
-        return launch(ctx, table_p8[dtype == CUCA_F16][ggml_type == CUCA_GGML_Q8_0][k > 4096], div_up(a.rows, 32),
+    // a plain matmul of at least 32 rows per compute unit (the LM head, or
+    // the final norm and the head) as 8-wave workgroups
+    if (kind == 0 && div_up(a.rows, 32) >= (int64_t)ctx->cu_count) {
+        // [norm prologue][dtype][format][n2, n8]
+        static const Kernel table_p8[2][2][2][2] = {{{{cuca_qmd_f32_q4_0_n2w8, cuca_qmd_f32_q4_0_n8w8},
+            {cuca_qmd_f32_q8_0_n2w8, cuca_qmd_f32_q8_0_n8w8}},
+            {{cuca_qmd_f16_q4_0_n2w8, cuca_qmd_f16_q4_0_n8w8},
+            {cuca_qmd_f16_q8_0_n2w8, cuca_qmd_f16_q8_0_n8w8}}},
+            {{{cuca_qmd_f32_q4_0_n2w8_rn, cuca_qmd_f32_q4_0_n8w8_rn},
+            {cuca_qmd_f32_q8_0_n2w8_rn, cuca_qmd_f32_q8_0_n8w8_rn}},
+            {{cuca_qmd_f16_q4_0_n2w8_rn, cuca_qmd_f16_q4_0_n8w8_rn},
+            {cuca_qmd_f16_q8_0_n2w8_rn, cuca_qmd_f16_q8_0_n8w8_rn}}}};
+        return launch(ctx, table_p8[rn][dtype == CUCA_F16][ggml_type == CUCA_GGML_Q8_0][k > 4096], div_up(a.rows, 32),
                       8 * 64, (unsigned)qmd_lds(a.ng, g), a);
     }
     // the Q|K|V with the norm prologue as 8-wave workgroups
     if (kind == 3 && rn) {
         // [dtype][format][n2, n8]
-        static const Kernel table_q8[2][2][2] = {{{cuca_qmd_rope_kv_f32_q4_0_n2w8_rn,cuca_qmd_rope_kv_f32_q4_0_n8w8_rn},{cuca_qmd_rope_kv_f32_q8_0_n2w8_rn,cuca_qmd_rope_kv_f32_q8_0_n8w8_rn}},{{cuca_qmd_rope_kv_f16_q4_0_n2w8_rn,cuca_qmd_rope_kv_f16_q4_0_n8w8_rn},{cuca_qmd_rope_kv_f16_q8_0_n2w8_rn,cuca_qmd_rope_kv_f16_q8_0_n8w8_rn}}};
+        static const Kernel table_q8[2][2][2] = {{{cuca_qmd_rope_kv_f32_q4_0_n2w8_rn, cuca_qmd_rope_kv_f32_q4_0_n8w8_rn},
+            {cuca_qmd_rope_kv_f32_q8_0_n2w8_rn, cuca_qmd_rope_kv_f32_q8_0_n8w8_rn}},
+            {{cuca_qmd_rope_kv_f16_q4_0_n2w8_rn, cuca_qmd_rope_kv_f16_q4_0_n8w8_rn},
+            {cuca_qmd_rope_kv_f16_q8_0_n2w8_rn, cuca_qmd_rope_kv_f16_q8_0_n8w8_rn}}};
         return launch(ctx, table_q8[dtype == CUCA_F16][ggml_type == CUCA_GGML_Q8_0][k > 4096], div_up(a.rows, 32),
                       8 * 64, (unsigned)qmd_lds(a.ng, g), a);
     }
@@ -1288,7 +1298,22 @@ static cuca_status qmd_launch(cuca_hip_ctx *ctx, int mode, int glu, uint32_t ggm
     // gets one: half the workgroups quantise (and normalise) the row
     if ((kind == 1 || kind == 2) && div_up(a.rows, 32) >= (int64_t)ctx->cu_count) {
         // [rn][dtype][format][n2, n8][silu, gelu]
-        static const Kernel table_w8[2][2][2][2][2] = {{{{{cuca_qmd_glu_f32_q4_0_silu_n2w8,cuca_qmd_glu_f32_q4_0_gelu_n2w8},{cuca_qmd_glu_f32_q4_0_silu_n8w8,cuca_qmd_glu_f32_q4_0_gelu_n8w8}},{{cuca_qmd_glu_f32_q8_0_silu_n2w8,cuca_qmd_glu_f32_q8_0_gelu_n2w8},{cuca_qmd_glu_f32_q8_0_silu_n8w8,cuca_qmd_glu_f32_q8_0_gelu_n8w8}}},{{{cuca_qmd_glu_f16_q4_0_silu_n2w8,cuca_qmd_glu_f16_q4_0_gelu_n2w8},{cuca_qmd_glu_f16_q4_0_silu_n8w8,cuca_qmd_glu_f16_q4_0_gelu_n8w8}},{{cuca_qmd_glu_f16_q8_0_silu_n2w8,cuca_qmd_glu_f16_q8_0_gelu_n2w8},{cuca_qmd_glu_f16_q8_0_silu_n8w8,cuca_qmd_glu_f16_q8_0_gelu_n8w8}}}},{{{{cuca_qmd_glu_f32_q4_0_silu_n2w8_rn,cuca_qmd_glu_f32_q4_0_gelu_n2w8_rn},{cuca_qmd_glu_f32_q4_0_silu_n8w8_rn,cuca_qmd_glu_f32_q4_0_gelu_n8w8_rn}},{{cuca_qmd_glu_f32_q8_0_silu_n2w8_rn,cuca_qmd_glu_f32_q8_0_gelu_n2w8_rn},{cuca_qmd_glu_f32_q8_0_silu_n8w8_rn,cuca_qmd_glu_f32_q8_0_gelu_n8w8_rn}}},{{{cuca_qmd_glu_f16_q4_0_silu_n2w8_rn,cuca_qmd_glu_f16_q4_0_gelu_n2w8_rn},{cuca_qmd_glu_f16_q4_0_silu_n8w8_rn,cuca_qmd_glu_f16_q4_0_gelu_n8w8_rn}},{{cuca_qmd_glu_f16_q8_0_silu_n2w8_rn,cuca_qmd_glu_f16_q8_0_gelu_n2w8_rn},{cuca_qmd_glu_f16_q8_0_silu_n8w8_rn,cuca_qmd_glu_f16_q8_0_gelu_n8w8_rn}}}}};
+        static const Kernel table_w8[2][2][2][2][2] = {{{{{cuca_qmd_glu_f32_q4_0_silu_n2w8, cuca_qmd_glu_f32_q4_0_gelu_n2w8},
+            {cuca_qmd_glu_f32_q4_0_silu_n8w8, cuca_qmd_glu_f32_q4_0_gelu_n8w8}},
+            {{cuca_qmd_glu_f32_q8_0_silu_n2w8, cuca_qmd_glu_f32_q8_0_gelu_n2w8},
+            {cuca_qmd_glu_f32_q8_0_silu_n8w8, cuca_qmd_glu_f32_q8_0_gelu_n8w8}}},
+            {{{cuca_qmd_glu_f16_q4_0_silu_n2w8, cuca_qmd_glu_f16_q4_0_gelu_n2w8},
+            {cuca_qmd_glu_f16_q4_0_silu_n8w8, cuca_qmd_glu_f16_q4_0_gelu_n8w8}},
+            {{cuca_qmd_glu_f16_q8_0_silu_n2w8, cuca_qmd_glu_f16_q8_0_gelu_n2w8},
+            {cuca_qmd_glu_f16_q8_0_silu_n8w8, cuca_qmd_glu_f16_q8_0_gelu_n8w8}}}},
+            {{{{cuca_qmd_glu_f32_q4_0_silu_n2w8_rn, cuca_qmd_glu_f32_q4_0_gelu_n2w8_rn},
+            {cuca_qmd_glu_f32_q4_0_silu_n8w8_rn, cuca_qmd_glu_f32_q4_0_gelu_n8w8_rn}},
+            {{cuca_qmd_glu_f32_q8_0_silu_n2w8_rn, cuca_qmd_glu_f32_q8_0_gelu_n2w8_rn},
+            {cuca_qmd_glu_f32_q8_0_silu_n8w8_rn, cuca_qmd_glu_f32_q8_0_gelu_n8w8_rn}}},
+            {{{cuca_qmd_glu_f16_q4_0_silu_n2w8_rn, cuca_qmd_glu_f16_q4_0_gelu_n2w8_rn},
+            {cuca_qmd_glu_f16_q4_0_silu_n8w8_rn, cuca_qmd_glu_f16_q4_0_gelu_n8w8_rn}},
+            {{cuca_qmd_glu_f16_q8_0_silu_n2w8_rn, cuca_qmd_glu_f16_q8_0_gelu_n2w8_rn},
+            {cuca_qmd_glu_f16_q8_0_silu_n8w8_rn, cuca_qmd_glu_f16_q8_0_gelu_n8w8_rn}}}}};
         const Kernel k8 = table_w8[rn][dtype == CUCA_F16][ggml_type == CUCA_GGML_Q8_0][k > 4096][kind - 1];
         return launch(ctx, k8, div_up(a.rows, 32), 8 * 64, (unsigned)qmd_lds(a.ng, g), a);
     }

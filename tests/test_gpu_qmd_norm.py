@@ -164,6 +164,29 @@ def test_glu_eight_wave_workgroups(ctx, k, dtype, qtype):
     assert_bits_equal(out.numpy(), want.numpy(), "glu out")
 
 
+@pytest.mark.parametrize("qtype,dtype,k", [("q8_0", "f32", 4096), ("q4_0", "f16", 2048), ("q4_0", "f32", 8192)])
+def test_tall_plain_the_final_norm_and_head(ctx, qtype, dtype, k):
+    """The final norm in front of the LM head: a plain matmul of at least 32
+    rows per compute unit runs as 8-wave workgroups with the prologue."""
+    rng = np.random.default_rng(k + len(qtype))
+    m, n, eps = 1, 9000, 1e-5
+    raw, w = weight(ctx, rng, qtype, n, k)
+    x, dx, db, dw = inputs(ctx, rng, m, k, dtype)
+    wx, wh = ref_norm(ctx, dx, db, dw, eps, 1.0, m, k, dtype)
+    dt = hip.dtype_code(NP[dtype])
+    want = ctx.empty((m, n), NP[dtype])
+    ctx.qmm(w.packed.ptr, QT[qtype], n, k, wh.ptr, k, m, n, want.ptr, n, dt)
+    h, out = ctx.empty((m, k), NP[dtype]), ctx.empty((m, n), NP[dtype])
+    names = launches(ctx, lambda: ctx.add_rmsnorm_qmm(dx.ptr, db.ptr, dw.ptr, eps, 1.0, None, h.ptr, w.packed.ptr,
+                                                      QT[qtype], n, k, m, n, out.ptr, n, dt))
+    assert names == [f"cuca_qmd_{dtype}_{qtype}_n{2 if k <= 4096 else 8}w8_rn"], names
+    assert_bits_equal(h.numpy(), wh.numpy(), "h")
+    got = out.numpy()
+    assert_bits_equal(got, want.numpy(), "head out")
+    if dtype == "f32":
+        assert_bits_equal(got, O.qmm(raw, QT[qtype], n, k, h.numpy(), rows=n, threads=8), "oracle qmm of h")
+
+
 @pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
 @pytest.mark.parametrize("nq,nk,d,k,m", [(32, 8, 128, 4096, 1), (4, 2, 64, 512, 1), (4, 2, 64, 512, 3),
