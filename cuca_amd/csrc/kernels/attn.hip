@@ -371,7 +371,32 @@ __device__ static inline void attn_split_generic_body(const AttnArgs &a) {
 #define MERGE_PL 4
 
 // Merge of one (row, query head) = job by one wave; lane owns columns lane,
-// lane + 64, ...
+// lane + 64, ... -- or, for two columns a lane (an even head_dim of
+// 66..128), the adjacent columns 2 lane and 2 lane + 1, read with one
+// 8-byte load: the
+// preload of 32 parts is then 32 loads, not 64, and with the (max, sum)
+// loads stays under the 63 loads a wave can have in flight (past that the
+// wave waits for its first loads before it issues the rest: two memory
+// round trips instead of one).  Each column still sums the parts in order.
+template <int MAXC> __device__ static inline int merge_col(int lane, int k) {
+    return MAXC == 2 ? 2 * lane + k : lane + k * CUCA_WAVE;
+}
+template <int MAXC>
+__device__ static inline void merge_load(const float *pc, int D, int lane, float (&v)[MAXC]) {
+    if constexpr (MAXC == 2) { // an even head_dim (the host's choice): 8-byte aligned part rows
+        const int e = 2 * lane;
+        const float2 t = e < D ? *reinterpret_cast<const float2 *>(pc + e) : make_float2(0.0f, 0.0f);
+        v[0] = t.x;
+        v[1] = t.y;
+    } else {
+#pragma unroll
+        for (int k = 0; k < MAXC; k++) {
+            const int e = lane + k * CUCA_WAVE;
+            v[k] = e < D ? pc[e] : 0.0f;
+        }
+    }
+}
+
 // This lane's (max, sum) of parts lane, lane + 64, ... below lim and the
 // values of parts 0 .. R-1 (the last part below lim repeated past it).
 template <int MAXC, int R>
@@ -385,14 +410,7 @@ __device__ static inline void attn_merge_preload(const float *pp, int64_t stride
         sv[q] = c < lim ? pp[(int64_t)c * stride + D + 1] : 0.0f;
     }
 #pragma unroll
-    for (int jj = 0; jj < R; jj++) {
-        const float *pc = pp + (int64_t)min(jj, lim - 1) * stride;
-#pragma unroll
-        for (int k = 0; k < MAXC; k++) {
-            const int e = lane + k * CUCA_WAVE;
-            v0[jj][k] = e < D ? pc[e] : 0.0f;
-        }
-    }
+    for (int jj = 0; jj < R; jj++) merge_load<MAXC>(pp + (int64_t)min(jj, lim - 1) * stride, D, lane, v0[jj]);
 }
 
 template <typename T, int MAXC>
@@ -455,12 +473,7 @@ __device__ static inline void attn_merge_job(const AttnArgs &a, int64_t job, int
 #pragma unroll
                         for (int k = 0; k < MAXC; k++) v[jj][k] = v0[R > 0 ? (j0 + jj) % R : 0][k];
                     } else {
-                        const float *pc = pp + (int64_t)(c0 + min(j0 + jj, nc - 1)) * stride;
-#pragma unroll
-                        for (int k = 0; k < MAXC; k++) {
-                            const int e = lane + k * CUCA_WAVE;
-                            v[jj][k] = e < D ? pc[e] : 0.0f;
-                        }
+                        merge_load<MAXC>(pp + (int64_t)(c0 + min(j0 + jj, nc - 1)) * stride, D, lane, v[jj]);
                     }
                 }
 #pragma unroll
@@ -490,14 +503,8 @@ __device__ static inline void attn_merge_job(const AttnArgs &a, int64_t job, int
             for (int j0 = 0; j0 < nc; j0 += 16) {
                 float v[16][MAXC];
 #pragma unroll
-                for (int jj = 0; jj < 16; jj++) {
-                    const float *pc = pp + (int64_t)(c0 + min(j0 + jj, nc - 1)) * stride;
-#pragma unroll
-                    for (int k = 0; k < MAXC; k++) {
-                        const int e = lane + k * CUCA_WAVE;
-                        v[jj][k] = e < D ? pc[e] : 0.0f;
-                    }
-                }
+                for (int jj = 0; jj < 16; jj++)
+                    merge_load<MAXC>(pp + (int64_t)(c0 + min(j0 + jj, nc - 1)) * stride, D, lane, v[jj]);
 #pragma unroll
                 for (int jj = 0; jj < 16; jj++) {
                     if (j0 + jj < nc) {
@@ -512,7 +519,7 @@ __device__ static inline void attn_merge_job(const AttnArgs &a, int64_t job, int
     }
 #pragma unroll
     for (int k = 0; k < MAXC; k++) {
-        const int e = lane + k * CUCA_WAVE;
+        const int e = merge_col<MAXC>(lane, k);
         if (e < D) store1<T>(o, e, acc[k] / total);
     }
 }

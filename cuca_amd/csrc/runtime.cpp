@@ -1103,7 +1103,9 @@ static cuca_status paged_decode_run(cuca_hip_ctx *ctx, const void *q, int64_t q_
         {cuca_attn_merge_f32_c1, cuca_attn_merge_f32_c2, cuca_attn_merge_f32_c4, cuca_attn_merge_f32_c8},
         {cuca_attn_merge_f16_c1, cuca_attn_merge_f16_c2, cuca_attn_merge_f16_c4, cuca_attn_merge_f16_c8}};
     const int cpl = (head_dim + 63) / 64;
-    const int ci = cpl <= 1 ? 0 : cpl <= 2 ? 1 : cpl <= 4 ? 2 : 3;
+    // (the two-column merge reads column pairs: an even head_dim; an odd one
+    // takes the four-column kernel, whose columns sum in the same order)
+    const int ci = cpl <= 1 ? 0 : (cpl <= 2 && head_dim % 2 == 0) ? 1 : cpl <= 4 ? 2 : 3;
     return launch(ctx, km[f16][ci], div_up(rows * n_head, 4), 256, 0, a);
 }
 
