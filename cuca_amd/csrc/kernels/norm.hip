@@ -36,30 +36,32 @@ __device__ static inline void load_w(const float *w, int64_t c, float (&v)[N]) {
 // is one row of TPR threads.
 // Rows wider than a wave reduce through LDS (one slot per wave), in a fixed
 // order, so every thread of the row gets the same bits.
-template <int TPR>
+// RPB rows of TPR > 64 threads share a block, each with its own W slots.
+template <int TPR, int RPB = 1>
 __device__ static inline float row_sum(float v, float *red) {
     if (TPR <= CUCA_WAVE) return group_sum<TPR>(v);
-    constexpr int W = TPR / CUCA_WAVE; // waves per row (one row per block)
+    constexpr int W = TPR / CUCA_WAVE; // waves per row
     v = group_sum<CUCA_WAVE>(v);
-    const int wave = threadIdx.x / CUCA_WAVE;
+    const int wave = threadIdx.x / CUCA_WAVE; // = row in block * W + the row's wave
     if ((threadIdx.x & (CUCA_WAVE - 1)) == 0) red[wave] = v;
     __syncthreads();
+    const float *rr = red + (RPB > 1 ? (int)(threadIdx.x / TPR) * W : 0);
     float s = 0.0f;
 #pragma unroll
-    for (int i = 0; i < W; i++) s += red[i];
+    for (int i = 0; i < W; i++) s += rr[i];
     return s;
 }
 
-template <typename T, int TPR, int NCH, bool NTL>
+template <typename T, int TPR, int NCH, bool NTL, int RPB = 1>
 __device__ static inline void norm_body(const NormArgs &a) {
     constexpr int N = Chunk<T>::N;
-    constexpr int B = TPR > CUCA_WAVE ? TPR : CUCA_BLOCK;
-    __shared__ float red_post[TPR > CUCA_WAVE ? TPR / CUCA_WAVE : 1];
-    __shared__ float red_main[TPR > CUCA_WAVE ? TPR / CUCA_WAVE : 1];
+    constexpr int B = TPR > CUCA_WAVE ? TPR * RPB : CUCA_BLOCK;
+    __shared__ float red_post[TPR > CUCA_WAVE ? RPB * TPR / CUCA_WAVE : 1];
+    __shared__ float red_main[TPR > CUCA_WAVE ? RPB * TPR / CUCA_WAVE : 1];
     const int li = threadIdx.x & (TPR - 1);
     const int64_t row = (int64_t)blockIdx.x * (B / TPR) + threadIdx.x / TPR;
-    // TPR > 64: the whole block is one row, so `live` is uniform and every
-    // thread reaches the barriers of row_sum
+    // TPR > 64: the block is RPB whole rows, so `live` is uniform over a
+    // row, and no thread returns before the barriers of row_sum
     const bool live = row < a.rows;
     const int H = a.hidden;
     const int nch = H / N;
@@ -94,7 +96,7 @@ __device__ static inline void norm_body(const NormArgs &a) {
             for (int k = 0; k < NCH; k++)
 #pragma unroll
                 for (int i = 0; i < N; i++) ss += b[k][i] * b[k][i];
-            ss = row_sum<TPR>(ss, red_post);
+            ss = row_sum<TPR, RPB>(ss, red_post);
             const float inv = 1.0f / sqrtf(ss / (float)H + a.post_eps);
 #pragma unroll
             for (int k = 0; k < NCH; k++) {
@@ -130,7 +132,7 @@ __device__ static inline void norm_body(const NormArgs &a) {
     for (int k = 0; k < NCH; k++)
 #pragma unroll
         for (int i = 0; i < N; i++) ss += v[k][i] * v[k][i];
-    ss = row_sum<TPR>(ss, red_main);
+    ss = row_sum<TPR, RPB>(ss, red_main);
     // y = x * (1 / sqrt(mean + eps)) * w, the GPU mirror's form (gpu.rs:5883-5896)
     const float inv = 1.0f / sqrtf(ss / (float)H + a.eps);
     if (!live) return;
@@ -210,6 +212,14 @@ __device__ static inline void norm_generic_body(const NormArgs &a) {
         NormArgs a) {                                                                      \
         norm_body<T, TPR, NCH, NTL>(a);                                                    \
     }
+// Rows of 256 threads go two to a block of 512.  Measured on MI355X in config
+// E's prefill step (8192 f16 rows of 2048): the norms unchanged (0.70-0.71),
+// the step 140.8-143.8 -> 139.2-141.9 us, the kernels after the norms running
+// faster (SwiGLU 0.77-0.79 -> 0.81-0.82 of the HBM peak).  The bits are the same.
+#define CUCA_NORM_R2(NAME, T, TPR, NCH, NTL)                                               \
+    extern "C" __global__ __launch_bounds__(2 * TPR) void NAME(NormArgs a) {               \
+        norm_body<T, TPR, NCH, NTL, 2>(a);                                                 \
+    }
 // Shapes: TPR = 2^k threads per row with one chunk each up to 1024 (every
 // hidden size up to 1024 chunks: 4096 f32, 8192 f16), then 1024 threads with
 // 2 or 4 chunks (8 for f32); "nt" variants stream x and the branch.
@@ -222,13 +232,13 @@ __device__ static inline void norm_generic_body(const NormArgs &a) {
     CUCA_NORM(cuca_norm_##TN##_t32, T, 32, 1, false)                                       \
     CUCA_NORM(cuca_norm_##TN##_t64, T, 64, 1, false)                                       \
     CUCA_NORM(cuca_norm_##TN##_t128, T, 128, 1, false)                                     \
-    CUCA_NORM(cuca_norm_##TN##_t256, T, 256, 1, false)                                     \
+    CUCA_NORM_R2(cuca_norm_##TN##_t256, T, 256, 1, false)                                     \
     CUCA_NORM(cuca_norm_##TN##_t512, T, 512, 1, false)                                     \
     CUCA_NORM(cuca_norm_##TN##_t1024, T, 1024, 1, false)                                   \
     CUCA_NORM(cuca_norm_##TN##_t1024_c2, T, 1024, 2, false)                                \
     CUCA_NORM(cuca_norm_##TN##_t1024_c4, T, 1024, 4, false)                                \
     CUCA_NORM(cuca_norm_##TN##_t128_nt, T, 128, 1, true)                                   \
-    CUCA_NORM(cuca_norm_##TN##_t256_nt, T, 256, 1, true)                                   \
+    CUCA_NORM_R2(cuca_norm_##TN##_t256_nt, T, 256, 1, true)                                   \
     CUCA_NORM(cuca_norm_##TN##_t512_nt, T, 512, 1, true)                                   \
     CUCA_NORM(cuca_norm_##TN##_t1024_nt, T, 1024, 1, true)                                 \
     CUCA_NORM(cuca_norm_##TN##_t1024_c2_nt, T, 1024, 2, true)                              \

@@ -641,8 +641,10 @@ cuca_status cuca_hip_add_rmsnorm(cuca_hip_ctx *ctx, const void *x, const void *b
     const Kernel k = vec && norm_shape(nch, &tpr, &per) ? norm_kernel(f16, tpr, per, stream) : KERNEL_COUNT;
     if (k == KERNEL_COUNT)
         return launch(ctx, f16 ? cuca_norm_f16_generic : cuca_norm_f32_generic, (unsigned)rows, 256, 0, a);
-    const int64_t rows_per_block = tpr > 64 ? 1 : 256 / tpr;
-    return launch(ctx, k, div_up(rows, rows_per_block), tpr > 64 ? (unsigned)tpr : 256u, 0, a);
+    // (rows of 256 threads go two to a block: the _t256 kernels)
+    const int64_t rows_per_block = tpr == 256 ? 2 : tpr > 64 ? 1 : 256 / tpr;
+    const unsigned threads = tpr == 256 ? 512u : tpr > 64 ? (unsigned)tpr : 256u;
+    return launch(ctx, k, div_up(rows, rows_per_block), threads, 0, a);
 }
 
 cuca_status cuca_hip_selftest_group_sum(cuca_hip_ctx *ctx, const float *input, int64_t n, float *out) {
