@@ -767,6 +767,8 @@ def decode_step_bench(ctx, torch, n, ctx_len, replays=10, mm="qmm", fuse_rope=Fa
         r = kernel_role(k)
         roles[r] = roles.get(r, 0.0) + ms
     split = {r + "_us_per_layer": round(t * 1000 / ds.layers, 2) for r, t in roles.items()}
+    # with every non-matmul op fused into a matmul there is no launch of that role
+    split.setdefault("non_matmul_us_per_layer", 0.0)
     ctx.graph_begin()
     ds.issue_layers()
     gl = ctx.graph_end()
@@ -789,6 +791,10 @@ def decode_step_bench(ctx, torch, n, ctx_len, replays=10, mm="qmm", fuse_rope=Fa
     return dict(batch=n, ctx_len=ctx_len, layer_weights="q4_0", head="q8_0", matmul=mm,
                 rope_in_qkv_epilogue=bool(fuse_rope and mm == "qmm"),
                 norm_in_matmul_prologue=bool(fuse_norm and fuse_rope and mm == "qmm"),
+                non_matmul_ops_fused_into=("the Q|K|V, gate/up and LM head prologues (residual + RMSNorm), the Q|K|V "
+                                           "epilogue (RoPE + K/V store)" if fuse_norm and fuse_rope and mm == "qmm"
+                                           else "the Q|K|V epilogue (RoPE + K/V store)" if fuse_rope and mm == "qmm"
+                                           else None),
                 us_per_layer=round(layers_ms * 1000 / 32, 2), us_per_step=round(step_ms * 1000, 1),
                 tokens_per_s=round(n / (step_ms / 1e3), 1),
                 layer_weight_gbs=round(wb / (layers_ms / 1e3) / 1e9, 1), **split)
