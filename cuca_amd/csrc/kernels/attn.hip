@@ -130,6 +130,15 @@ __device__ static inline void attn_split_body(const AttnArgs &a) {
             qv[k] = i < NW ? qg[i] : 0u;
         }
     }
+    constexpr int NB = CP / 16;
+    const uint32_t *tab = a.tables + (int64_t)row * a.max_blocks;
+    // The table entries of the wave's blocks for a range that starts in the
+    // first block (lo < 16, every decode row without a window), loaded
+    // beside the range so that the K/V loads wait for one load, not two.
+    const int s0 = (part * WPB + wave) * (CP / 16);
+    uint32_t sblk[NB];
+#pragma unroll
+    for (int k = 0; k < NB; k++) sblk[k] = tab[min(s0 + k, a.max_blocks - 1)];
     const int lo = a.ranges[2 * row], hi = a.ranges[2 * row + 1];
     const bool valid = attn_range_ok(a, lo, hi);
     if (!valid && kvh == 0 && part == 0 && threadIdx.x == 0)
@@ -143,19 +152,19 @@ __device__ static inline void attn_split_body(const AttnArgs &a) {
     const int pi = lane / LPP, sub = lane - pi * LPP;
     const int p = p0 + pi;
     const bool live = wave_live && p >= lo && p < hi;
-    const uint32_t *tab = a.tables + (int64_t)row * a.max_blocks;
-    // the pool row of each block's first position (blocks past the range
-    // reuse its last one; a missing block reads block 0 and is recorded)
-    constexpr int NB = CP / 16;
-    const int last_b = wave_live ? (hi - 1) >> 4 : 0;
+    // the pool row of each block's first position (a missing block in the
+    // range reads block 0 and is recorded; blocks past the range, whose
+    // positions are all masked, read any existing block)
+    const int last_b = (hi - 1) >> 4;
     int64_t brow[NB];
 #pragma unroll
     for (int k = 0; k < NB; k++) {
-        const int bi = wave_live ? min((p0 >> 4) + k, last_b) : 0;
-        const uint32_t blk = tab[bi];
+        const int bk = (p0 >> 4) + k;
+        const bool in = wave_live && bk <= last_b;
+        const uint32_t blk = lo_al == 0 || !in ? sblk[k] : tab[bk]; // (bk == s0 + k when lo_al is 0)
         const bool ok = (int64_t)blk < a.n_blocks;
-        if (!ok && wave_live && (p0 >> 4) + k <= last_b && lane == 0)
-            record_bad(a.status + CUCA_STATUS_KV_RANGE, row, (uint32_t)max(bi * 16, lo));
+        if (!ok && in && lane == 0)
+            record_bad(a.status + CUCA_STATUS_KV_RANGE, row, (uint32_t)max(bk * 16, lo));
         brow[k] = ((int64_t)(ok ? blk : 0) * a.n_kv + kvh) * 16;
     }
 
