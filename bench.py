@@ -7,8 +7,9 @@ Metric (BASELINE.json): fused layer-op HBM GB/s and % of the 8 TB/s peak;
 per-layer non-matmul microseconds at decode.
 
 Workload (config.workload): the Llama-3-8B layer ops.  One step is one pass
-of the hot path over one batch of 4096 prefill tokens with f16 activations
-(configs[2] at its smaller size): the Q8_0 embedding gather of the batch
+of the hot path over one batch of 16384 prefill tokens with f16 activations
+(configs[2] at its larger size, the largest single-GPU configuration; the
+4096-token step is measured beside it): the Q8_0 embedding gather of the batch
 fused with the first block's attention RMSNorm (x and h in one pass), a
 block's attention-side residual add + RMSNorm, RoPE on Q 32x128 / K 8x128,
 the SwiGLU over F 14336, and the FFN-side residual add + RMSNorm.  `value` is
@@ -30,6 +31,9 @@ Per-call constants (gamma, norm weights) are counted once.
 B Llama-3-8B decode batch, D Gemma-2-9B with the sandwich norms, GeGLU and
 interleaved RoPE, E Qwen3-30B-A3B with QK-norm RoPE and the ragged
 expert-grouped SwiGLU), each op's kernel GB/s from its timestamps.
+`prefill_bar` (near the end of the line) gathers every op's fraction of
+the HBM peak at the sizes of the 70 % bar (config C at 4096 and 16384
+tokens, config E at 8192), `decode_bar` the batch-1 decode figures.
 
 roofline: the dominant kernel (SwiGLU) -- its algorithmic bytes per launch
 divided by its average launch duration over the timed steps, from the start
@@ -38,7 +42,7 @@ and stop events the C ABI's profile attaches to every kernel
 reports), against the 8 TB/s HBM peak.
 
 cpu_baseline: the oracle's C restatement of the reference's candle CPU path
-(oracle/) over the same 4096-token step, on the step's own inputs, with the
+(oracle/) over the same 16384-token step, on the step's own inputs, with the
 CPUs this process is given (the CPU model and counts are recorded); each op
 timed alone, per-op GB/s beside the GPU's.
 """
@@ -193,8 +197,18 @@ class LayerStep:
         def close(got, want, what, floor=0.0):
             # the bar, and the raw error before the floor: max relative error
             # (f32) or f16 ulps, and the values inside the bar only by the floor
+            # (an expected NaN needs a NaN, an expected inf the same inf, an
+            # expected finite value a finite one: no tolerance sees those)
             g, w = got.astype(np.float64), want.astype(np.float64)
+            nonfinite = np.where(np.isnan(w), ~np.isnan(g),
+                                 np.where(np.isinf(w), g != w, ~np.isfinite(g)))
+            assert not nonfinite.any(), \
+                f"{self.name} n={n} {what}: {nonfinite.sum()} values with a different NaN/inf pattern"
+            fin = np.isfinite(w)
+            g, w = g[fin], w[fin]
             ulp = np.spacing(np.abs(w).astype(np.float16)).astype(np.float64) if f16 else None
+            if np.ndim(floor):
+                floor = np.broadcast_to(floor, fin.shape)[fin]
             plain = (2 * ulp if f16 else 1e-5 * np.abs(w)) + 1e-37
             d = np.abs(g - w)
             bad = d > plain + floor
@@ -202,7 +216,7 @@ class LayerStep:
             err = d / np.where(ulp > 0, ulp, 1.0) if f16 else d / np.maximum(np.abs(w), 1e-30)
             r = raw.setdefault(what, {"max_ulp" if f16 else "max_rel": 0.0, "floored": 0, "n": 0})
             k = "max_ulp" if f16 else "max_rel"
-            r[k] = max(r[k], float(err.max()))
+            r[k] = max(r[k], float(err.max()) if err.size else 0.0)
             r["floored"] += int(np.count_nonzero(d > plain))
             r["n"] += int(d.size)
 
@@ -386,6 +400,7 @@ def kv_store_bench(ctx, torch, name, n, dtype, steps=20, warmup=5):
             assert np.array_equal(g.view(np.uint16 if dtype == "f16" else np.uint32),
                                   w.view(np.uint16 if dtype == "f16" else np.uint32)), what
         else:
+            assert np.all(np.isfinite(w)) and np.all(np.isfinite(g)), (what, "non-finite")
             err = np.abs(g.astype(np.float64) - w) / (np.abs(w.astype(np.float64)).max(-1, keepdims=True))
             assert err.max() <= (4e-3 if dtype == "f16" else 1e-5), (what, err.max())
     b = n * (2 * s * (nq + 2 * nk) * d + 4 * d) + (8 * d if qn is not None else 0)
@@ -1306,7 +1321,7 @@ def cpu_baseline(st, seconds=12.0):
                        f"{avail} available, {model}")
 
 
-def traffic_from_profiles(kernel):
+def traffic_from_profiles(kernel, algorithmic_bytes):
     """HBM bytes per launch of the roofline kernel measured by rocprofv3
     --pmc (FETCH_SIZE, WRITE_SIZE, scaled by a copy kernel's reading), from
     the committed summary -- but only while the kernel's machine code is the
@@ -1320,10 +1335,53 @@ def traffic_from_profiles(kernel):
         rec = json.load(f)
     if rec.get("kernel") != kernel:
         return None, f"the summary measured {rec.get('kernel')}, the roofline kernel is {kernel}"
+    if rec.get("algorithmic_bytes_per_launch") != algorithmic_bytes:
+        return None, (f"the summary measured launches of {rec.get('algorithmic_bytes_per_launch')} "
+                      f"algorithmic bytes, this run's are {algorithmic_bytes}")
     now = build.kernel_code_sha256(kernel)
     if now is None or now != rec.get("code_sha256"):
         return None, "the kernel's code changed since the counters were read"
     return rec.get("hbm_bytes_per_launch"), None
+
+
+def prefill_bar(ops, tokens, big, configs):
+    """Every fused op's fraction of the HBM peak at the prefill sizes the
+    north star's 70 % bar covers (>= 4096 tokens: config C at both sizes,
+    config E at 8192), and the smallest of them."""
+    bar = {}
+
+    def take(key, o):
+        if o:
+            bar[key] = {name: r["frac"] for name, r in o.items()}
+    take(f"C_{tokens}", ops)
+    if big:
+        take(f"C_{big['tokens']}", big["ops"])
+    if configs and "E_8192_f16" in configs:
+        take("E_8192", configs["E_8192_f16"]["ops"])
+    fr = [f for o in bar.values() for f in o.values()]
+    bar["min"] = min(fr) if fr else None
+    bar["all_at_least_0.70"] = bool(fr) and min(fr) >= 0.70
+    return bar
+
+
+def decode_bar(decode, attn):
+    """The batch-1 decode figures in brief: the fully fused step's tokens/s,
+    its per-layer attention and non-matmul time (the norms' in-kernel cost
+    when they ride in the matmul prologues), and the non-matmul sequence of
+    a layer as its own launches in a graph."""
+    if not decode:
+        return None
+    out = {}
+    f = decode.get("step_batch1_ctx4096_qmm_norm_rope_in_qkv")
+    if f:
+        out["step_batch1_fused_tokens_per_s"] = f["tokens_per_s"]
+        out["step_batch1_fused_attention_us_per_layer"] = f.get("attention_us_per_layer")
+        out["step_batch1_fused_non_matmul_us_per_layer"] = f.get("non_matmul_us_per_layer")
+        out["step_batch1_fused_us_per_layer"] = f["us_per_layer"]
+    b1 = decode.get("batch1")
+    if b1:
+        out["non_matmul_sequence_batch1_graph_us_per_layer"] = b1["graph_us_per_layer"]
+    return out
 
 
 def main():
@@ -1331,11 +1389,12 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--tokens", type=int, default=4096)
+    ap.add_argument("--tokens", type=int, default=16384)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
-    ap.add_argument("--no-large", action="store_true", help="skip the 16384-token step")
+    ap.add_argument("--no-large", action="store_true",
+                    help="skip the second config C size (4096 tokens beside the 16384-token headline)")
     ap.add_argument("--no-configs", action="store_true", help="skip the A/B/D/E config steps")
     ap.add_argument("--no-kv", action="store_true", help="skip the fused RoPE + paged K/V store")
     ap.add_argument("--no-attn", action="store_true", help="skip the paged decode attention")
@@ -1409,11 +1468,11 @@ def main():
     cpu = cpu_box.get("cpu")
     value = step_bytes / (ms / 1e3) / 1e9
     glu = ops["glu"]
-    big = None
-    if args.tokens != 16384 and not args.no_large:
-        _, bytes_l, ops_l, rows_l, ms_l = run_size(16384, max(5, args.steps // 4), 3)
+    big, other = None, (4096 if args.tokens != 4096 else 16384)
+    if not args.no_large:
+        _, bytes_l, ops_l, rows_l, ms_l = run_size(other, args.steps, args.warmup)
         checked_rows += rows_l
-        big = dict(tokens=16384, us_per_step=round(ms_l * 1000, 1),
+        big = dict(tokens=other, us_per_step=round(ms_l * 1000, 1),
                    gbs=round(bytes_l / (ms_l / 1e3) / 1e9, 1),
                    frac=round(bytes_l / (ms_l / 1e3) / 1e9 / HBM_PEAK_GBS, 4), ops=ops_l)
 
@@ -1493,8 +1552,21 @@ def main():
                 decode[key] = decode_step_bench(ctx, torch, n, clen, mm=mm, fuse_rope=fuse != "",
                                                 fuse_norm=fuse == "norm")
             torch.cuda.empty_cache()
+            # With both norms in the matmul prologues no launch is a non-matmul
+            # op, but the norms still cost time inside those matmuls: their
+            # cost is the fused step's matmul time (Q|K|V + RoPE/K/V-store,
+            # the others) minus the same launches without the prologue.
+            fused = decode.get("step_batch1_ctx4096_qmm_norm_rope_in_qkv")
+            plain = decode.get("step_batch1_ctx4096_qmm_rope_in_qkv")
+            if fused is not None and plain is not None:
+                def mm_us(r):
+                    return r.get("matmul_us_per_layer", 0.0) + r.get("qkv_rope_kv_us_per_layer", 0.0)
+                fused["non_matmul_launch_us_per_layer"] = fused.pop("non_matmul_us_per_layer", 0.0)
+                fused["norm_prologue_us_per_layer"] = round(mm_us(fused) - mm_us(plain), 2)
+                fused["non_matmul_us_per_layer"] = round(fused["non_matmul_launch_us_per_layer"]
+                                                         + fused["norm_prologue_us_per_layer"], 2)
 
-    traffic, why = traffic_from_profiles(glu["kernel"])
+    traffic, why = traffic_from_profiles(glu["kernel"], glu["bytes"])
     traffic_src = ("profiles/swiglu_traffic.json (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; same kernel code)"
                    if traffic is not None else why)
     out = {
@@ -1520,7 +1592,7 @@ def main():
         "verified_rows": checked_rows,
         "parity_raw": parity_raw,
         "ops": ops,
-        "prefill_16384": big,
+        f"prefill_{other}": big,
         "configs": configs,
         "rope_store_kv": kv,
         "paged_decode": attn,
@@ -1530,6 +1602,8 @@ def main():
         "moe_decode": moe,
         "end_of_step": head,
         "decode_us_per_layer": decode,
+        "prefill_bar": prefill_bar(ops, args.tokens, big, configs),
+        "decode_bar": decode_bar(decode, attn),
         "roofline": {"kernel": glu["kernel"], "bound": "hbm",
                      "achieved": glu["gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": glu["frac"], "traffic": traffic,

@@ -40,8 +40,9 @@ def _name_the_test(request):
 
 def pytest_terminal_summary(terminalreporter):
     """The unfloored errors behind the tolerance bars: per op family (test
-    file), the maximum relative error (f32) and f16 ulps, and how many
-    elements passed only through a stated floor."""
+    file), the maximum relative error (f32) and f16 ulps, how many
+    elements passed only through a stated floor, and how many expected
+    values were NaN or inf (each matched by value, not by a tolerance)."""
     try:
         import helpers
     except ImportError:
@@ -51,10 +52,11 @@ def pytest_terminal_summary(terminalreporter):
     fam = {}
     for test, what, st in helpers.RAW:
         key = (test.split("::")[0].split("/")[-1], st["dtype"])
-        f = fam.setdefault(key, {"n": 0, "worst": 0.0, "floored": 0, "at": ""})
+        f = fam.setdefault(key, {"n": 0, "worst": 0.0, "floored": 0, "nonfinite": 0, "at": ""})
         v = st.get("max_rel", st.get("max_ulp", 0.0))
         f["n"] += st["n"]
         f["floored"] += st["floored"]
+        f["nonfinite"] += st.get("nonfinite", 0)
         if v > f["worst"]:
             f["worst"], f["at"] = v, f"{test.split('::')[-1]} {what}"
     tr = terminalreporter
@@ -62,4 +64,5 @@ def pytest_terminal_summary(terminalreporter):
     for (file, dt), f in sorted(fam.items()):
         unit = "rel" if dt == "f32" else "ulp"
         tr.write_line(f"{file:28s} {dt}  max {unit} {f['worst']:.3g}  values {f['n']}  "
-                      f"within the bar only by a floor {f['floored']}  (worst: {f['at']})")
+                      f"within the bar only by a floor {f['floored']}  "
+                      f"expected NaN/inf (matched by value) {f['nonfinite']}  (worst: {f['at']})")

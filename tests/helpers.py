@@ -54,12 +54,26 @@ RAW = []
 CURRENT_TEST = [""]
 
 
+def nonfinite_mismatch(got, want):
+    """Elements whose non-finite pattern differs from the oracle's: where
+    `want` is NaN, `got` must be NaN; where `want` is +-inf, `got` must be
+    the same-signed inf; where `want` is finite, `got` must be finite.  (A
+    tolerance test alone passes all of these: |got - want| > tol is False
+    whenever a NaN is involved, and an infinite `want` makes tol infinite.)"""
+    g, w = _f64(got), _f64(want)
+    return np.where(np.isnan(w), ~np.isnan(g),
+                    np.where(np.isinf(w), g != w, ~np.isfinite(g)))
+
+
 def error_stats(got, want, floor=None, rel=1e-5, ulps=2):
     """The error against the north star's plain bar, before any floor:
     f32 -> the maximum relative error |got - want| / |want|; f16 -> the
-    maximum error in f16 ulps of want.  `floored` counts the elements within
-    the bar only because of the floor (outside rel |want| or ulps ulp, inside
-    the bar plus the floor)."""
+    maximum error in f16 ulps of want, over the elements where both are
+    finite.  `floored` counts the elements within the bar only because of
+    the floor (outside rel |want| or ulps ulp, inside the bar plus the
+    floor); `nonfinite` counts the expected NaN/inf values (each checked
+    for the same value), `nonfinite_bad` the elements whose non-finite
+    pattern differs (nonfinite_mismatch)."""
     g, w = _f64(got), _f64(want)
     with np.errstate(invalid="ignore", over="ignore", divide="ignore"):
         ok = np.isfinite(g) & np.isfinite(w)
@@ -77,7 +91,8 @@ def error_stats(got, want, floor=None, rel=1e-5, ulps=2):
         floored = int(np.count_nonzero(ok & (d > plain) & (d <= plain + fl)))
     return {"dtype": "f16" if f16 else "f32", "n": int(g.size),
             "max_ulp" if f16 else "max_rel": float(err.max()) if err.size else 0.0,
-            "floored": floored}
+            "floored": floored, "nonfinite": int(np.count_nonzero(~np.isfinite(w))),
+            "nonfinite_bad": int(np.count_nonzero(nonfinite_mismatch(g, w)))}
 
 
 def assert_close(got, want, floor=None, rel=1e-5, ulps=2, what=""):
@@ -95,13 +110,17 @@ def assert_close(got, want, floor=None, rel=1e-5, ulps=2, what=""):
         tol = tol + 1e-37
         if floor is not None:
             tol = tol + floor
-        same_nan = np.isnan(g) & np.isnan(w)
-        bad = (np.abs(g - w) > tol) & ~same_nan
+        both = np.isfinite(g) & np.isfinite(w)
+        bad = (both & (np.abs(g - w) > tol)) | nonfinite_mismatch(g, w)
     if bad.any():
         i = tuple(np.argwhere(bad)[0])
-        worst = np.max(np.abs(g - w)[bad] / np.maximum(tol[bad], 1e-300))
+        nf = int(np.count_nonzero(nonfinite_mismatch(g, w)))
+        with np.errstate(invalid="ignore", over="ignore"):
+            fin = bad & np.isfinite(g) & np.isfinite(w)
+            worst = np.max(np.abs(g - w)[fin] / np.maximum(tol[fin], 1e-300)) if fin.any() else 0.0
         raise AssertionError(f"{what}: {bad.sum()} of {bad.size} outside tolerance "
-                             f"(worst {worst:.2f}x); first at {list(i)}: got {g[i]!r} want {w[i]!r}")
+                             f"({nf} with a different NaN/inf pattern; worst finite {worst:.2f}x); "
+                             f"first at {list(i)}: got {g[i]!r} want {w[i]!r}")
     st = error_stats(got, want, floor, rel, ulps)
     RAW.append((CURRENT_TEST[0], what, st))
     return st

@@ -76,6 +76,27 @@ def test_one_row_glu(ctx, qtype, dtype, act, ff, k, clamp):
 
 
 @pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("act", [hip.ACT_SILU, hip.ACT_GELU_TANH])
+@pytest.mark.parametrize("ff,k,clamp", [(37, 544, 0.0), (50, 14336, 0.0), (8200, 4096, 0.0), (8200, 4160, 1.0)])
+def test_one_row_glu_f16_finite(ctx, qtype, act, ff, k, clamp):
+    """f16 outputs that all stay within f16 range (smaller weight scales than
+    test_one_row_glu, whose Q8_0 cases overflow for a third of the rows), so
+    the one-row GLU and its 8-wave form are checked on finite values."""
+    rng = np.random.default_rng(3 * ff + k + act)
+    graw, gw = weight(ctx, rng, qtype, ff, k, (0.001, 0.004))
+    uraw, uw = weight(ctx, rng, qtype, ff, k, (0.001, 0.004))
+    x = awkward(rng, 1, k, 1.0, huge=1.0).astype(np.float16)
+    got = ops.QmmWeight.glu(gw, uw, ctx.array(x), ops.Glu(act, clamp)).numpy()
+    g = O.qmm(graw, QT[qtype], ff, k, x, threads=8)
+    u = O.qmm(uraw, QT[qtype], ff, k, x, threads=8)
+    want = O.glu(g, u, act, clamp=clamp).astype(np.float16)
+    assert np.all(np.isfinite(want))
+    gc = np.minimum(g, clamp) if clamp > 0 else g
+    uc = np.clip(u, -clamp, clamp) if clamp > 0 else u
+    assert_close(got, want, floor=glu_floor(gc, uc, act), what=f"glu {qtype} f16 finite {ff}x{k}")
+
+
+@pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
 @pytest.mark.parametrize("nq,nk,d,k", [(32, 8, 128, 4096), (4, 2, 64, 4128), (6, 2, 16, 256)])
 def test_one_row_qkv_rope_store(ctx, qtype, dtype, nq, nk, d, k):

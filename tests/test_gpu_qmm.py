@@ -170,6 +170,28 @@ def test_qmm_glu(ctx, qtype, dtype, act, ff, k, m, clamp):
         assert_close(got, want, floor=glu_floor(gc, uc, act), what=f"glu {qtype} f32")
 
 
+@pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("act", [hip.ACT_SILU, hip.ACT_GELU_TANH])
+@pytest.mark.parametrize("ff,k,m,clamp", [(200, 256, 3, 0.0), (48, 768, 5, 0.0), (64, 1024, 2, 2.0),
+                                          (1000, 2048, 4, 0.0)])
+def test_qmm_glu_f16_finite(ctx, qtype, act, ff, k, m, clamp):
+    """f16 GLU outputs that all stay within f16 range (smaller weight scales
+    than test_qmm_glu, whose Q8_0 f16 cases overflow), so the f16 epilogue
+    is checked on finite values too."""
+    rng = np.random.default_rng(5 * ff + k + m + act)
+    graw, gw = weight(ctx, rng, qtype, ff, k, (0.001, 0.004))
+    uraw, uw = weight(ctx, rng, qtype, ff, k, (0.001, 0.004))
+    x = awkward(rng, m, k, 1.0, huge=1.0).astype(np.float16)
+    got = ops.QmmWeight.glu(gw, uw, ctx.array(x), ops.Glu(act, clamp)).numpy()
+    g = O.qmm(graw, QT[qtype], ff, k, x, threads=8)
+    u = O.qmm(uraw, QT[qtype], ff, k, x, threads=8)
+    want = O.glu(g, u, act, clamp=clamp).astype(np.float16)
+    assert np.all(np.isfinite(want))
+    gc = np.minimum(g, clamp) if clamp > 0 else g
+    uc = np.clip(u, -clamp, clamp) if clamp > 0 else u
+    assert_close(got, want, floor=glu_floor(gc, uc, act), what=f"glu {qtype} f16 finite")
+
+
 @pytest.mark.parametrize("qtype,name,n,k", [("q4_0", "ffn_gate", 14336, 4096),
                                             ("q8_0", "ffn_down", 4096, 14336),
                                             ("q4_0", "attn_q", 4096, 4096)])
