@@ -398,6 +398,144 @@ __device__ static inline void embed_rms_lds_body(const EmbedArgs &a) {
     }
 }
 
+// Unit u of a row as two words: its block's f16 scale (d) and its 8 quant
+// bytes (q, packed; for Q4_0 the 8 bytes whose low or high nibbles hold the
+// unit's values).  The 8-byte load is 2-byte aligned (a block is 18 or 34
+// bytes), which global loads allow.
+typedef uint32_t u32x2_a2 __attribute__((ext_vector_type(2), aligned(2)));
+template <int QT>
+__device__ static inline void embed_unit_load(const uint8_t *row, int u, uint32_t &d, u32x2_a2 &q) {
+    constexpr int BS = QT == 2 ? 18 : 34;
+    const int e0 = u * 8, ob = (e0 >> 5) * BS, p = e0 & 31;
+    d = *reinterpret_cast<const uint16_t *>(row + ob);
+    q = *reinterpret_cast<const u32x2_a2 *>(row + ob + 2 + (QT == 2 ? (p & 15) : p));
+}
+// The unit's 8 values from the packed words: the same arithmetic as
+// embed_dequant (d' = f32(d) * scale, then f32(q) * d').
+template <int QT>
+__device__ static inline void embed_unit_dequant(int u, uint32_t dq, u32x2_a2 q, float scale, float (&v)[8]) {
+    const int p = (u * 8) & 31;
+    const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)dq) * scale;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const uint32_t b = (q[i >> 2] >> (8 * (i & 3))) & 0xffu;
+        if (QT == 2) v[i] = (float)((int)((b >> (p >= 16 ? 4 : 0)) & 0xfu) - 8) * d;
+        else v[i] = (float)(int8_t)b * d;
+    }
+}
+
+// The fused gather for many tokens, as persistent workgroups: TPR threads
+// per token (thread t owns unit t: hidden = 8 TPR), each workgroup taking
+// TPW tokens it * gridDim.x + blockIdx.x (it < TPW; the launch sizes the
+// grid to what the device holds at once, so every iteration of the grid
+// covers a contiguous range of tokens).  A thread's 8 norm weights stay in
+// registers for all its tokens, and the token ids come in one load.  The
+// loop is unrolled, and the next token's unit is loaded before the current
+// token's stores.  The sum of squares is the workgroup-per-token kernel's
+// order (per thread, a wave butterfly, an LDS sum in wave order), so h has
+// its bits; x is the plain gather's.  36 registers: 8 waves per SIMD.
+// Measured in the config C prefill step on MI355X (16384 Q8_0 tokens of 4096
+// -> f16): 61.3-61.6 us against 65.2-65.4 for the LDS-weights wave-per-token
+// kernel (0.69 against 0.65 of the HBM peak); 8 tokens per workgroup (two
+// rounds of workgroups) 64.6, 4 tokens 68.5; two units per thread 65.7.
+template <int QT, typename OutT, int TPR, int TPW>
+__device__ static inline void embed_rms_persist_body(const EmbedArgs &a) {
+    constexpr int NW = TPR / CUCA_WAVE;
+    static_assert(TPW <= CUCA_WAVE, "one lane per token id");
+    __shared__ float red[2][NW];
+    const int t = threadIdx.x, lane = t & (CUCA_WAVE - 1), wave = t / CUCA_WAVE;
+    const int G = gridDim.x;
+    const bool has_w = a.rms_w != nullptr;
+    float wv[8];
+    if (has_w) {
+        const f32x4 *wp = reinterpret_cast<const f32x4 *>(a.rms_w) + 2 * t;
+        const f32x4 w0 = wp[0], w1 = wp[1];
+        wv[0] = w0.x; wv[1] = w0.y; wv[2] = w0.z; wv[3] = w0.w;
+        wv[4] = w1.x; wv[5] = w1.y; wv[6] = w1.z; wv[7] = w1.w;
+    }
+    // lane i holds the id of the workgroup's token i (tokens past n read
+    // the last token's id, so every load below stays inside the table)
+    uint32_t idv;
+    {
+        const int tk = (lane < TPW ? lane : 0) * G + (int)blockIdx.x;
+        idv = a.ids[tk < a.n ? tk : a.n - 1];
+    }
+    auto id_at = [&](int it) -> uint32_t { return (uint32_t)__builtin_amdgcn_readlane((int)idv, it); };
+    auto row_of = [&](uint32_t id) {
+        return a.table + (int64_t)((int64_t)id < a.vocab ? id : 0u) * a.row_bytes;
+    };
+    uint32_t dq[TPW];
+    u32x2_a2 q[TPW];
+    embed_unit_load<QT>(row_of(id_at(0)), t, dq[0], q[0]);
+#pragma unroll
+    for (int it = 0; it < TPW; it++) {
+        const int tok = it * G + (int)blockIdx.x;
+        const uint32_t id = id_at(it);
+        // (opaque until here: otherwise the byte extraction of a unit loaded
+        // ahead is hoisted next to its load, which then waits for it)
+        asm volatile("" : "+v"(dq[it]), "+v"(q[it]));
+        if (it + 1 < TPW) embed_unit_load<QT>(row_of(id_at(it + 1)), t, dq[it + 1], q[it + 1]);
+        if (tok < a.n) { // uniform over the workgroup
+            OutT *orow = reinterpret_cast<OutT *>(a.out) + (int64_t)tok * a.hidden;
+            OutT *hrow = reinterpret_cast<OutT *>(a.h_out) + (int64_t)tok * a.hidden;
+            const bool bad = (int64_t)id >= a.vocab;
+            if (bad && t == 0) record_bad(a.status + CUCA_STATUS_EMBED_ID, (uint32_t)tok, id);
+            float v[8];
+            embed_unit_dequant<QT>(t, dq[it], q[it], a.scale, v);
+            if (bad) {
+#pragma unroll
+                for (int j = 0; j < 8; j++) v[j] = 0.0f;
+            }
+            embed_store<OutT>(orow, t, v);
+            float ss = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                v[j] = Chunk<OutT>::as_stored(v[j]);
+                ss += v[j] * v[j];
+            }
+            ss = group_sum<CUCA_WAVE>(ss);
+            // two slots, alternating: a wave that runs ahead writes the other
+            // slot, and cannot come back to this one before every wave has
+            // passed the next barrier (so has read this one)
+            if (lane == 0) red[it & 1][wave] = ss;
+            __syncthreads();
+            ss = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NW; i++) ss += red[it & 1][i];
+            const float inv = 1.0f / sqrtf(ss / (float)a.hidden + a.rms_eps);
+            float y[8];
+            if (has_w) {
+#pragma unroll
+                for (int j = 0; j < 8; j++) y[j] = pin_f32(pin_f32(v[j] * inv) * wv[j]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; j++) y[j] = pin_f32(v[j] * inv);
+            }
+            if (bad) {
+#pragma unroll
+                for (int j = 0; j < 8; j++) y[j] = 0.0f;
+            }
+            embed_store<OutT>(hrow, t, y);
+        }
+    }
+}
+
+#define CUCA_EMBED_P(NAME, QT, OUT, TPR, TPW)                                              \
+    extern "C" __global__ __launch_bounds__(TPR) void NAME(EmbedArgs a) {                  \
+        embed_rms_persist_body<QT, OUT, TPR, TPW>(a);                                      \
+    }
+#define CUCA_EMBED_P_SET(NAME, QT, OUT)                                                    \
+    CUCA_EMBED_P(NAME##_rms_p256_w8, QT, OUT, 256, 8)                                      \
+    CUCA_EMBED_P(NAME##_rms_p256_w16, QT, OUT, 256, 16)                                    \
+    CUCA_EMBED_P(NAME##_rms_p256_w32, QT, OUT, 256, 32)                                    \
+    CUCA_EMBED_P(NAME##_rms_p512_w8, QT, OUT, 512, 8)                                      \
+    CUCA_EMBED_P(NAME##_rms_p512_w16, QT, OUT, 512, 16)                                    \
+    CUCA_EMBED_P(NAME##_rms_p512_w32, QT, OUT, 512, 32)
+CUCA_EMBED_P_SET(cuca_embed_q4_0_f32, 2, float)
+CUCA_EMBED_P_SET(cuca_embed_q4_0_f16, 2, _Float16)
+CUCA_EMBED_P_SET(cuca_embed_q8_0_f32, 8, float)
+CUCA_EMBED_P_SET(cuca_embed_q8_0_f16, 8, _Float16)
+
 // The same with a workgroup per token: TPR threads (a power of two, 64 to
 // 1024), thread t owning units t, t + TPR, ... (NU of them), the sum of
 // squares a butterfly per wave and an LDS sum over the waves in wave order.

@@ -492,6 +492,31 @@ static cuca_status embed_common(cuca_hip_ctx *ctx, const void *table, uint32_t g
     // and 8192 tokens it is slower than the workgroup-per-token kernel (18.1
     // against 15.3, 17.1 against 15.5 us), too few tokens per CU to hide
     // the staging.
+    // Beyond 8192 tokens, rows of 256 or 512 units (hidden 2048 or 4096) take
+    // persistent workgroups of one thread per unit, each workgroup looping
+    // over TPW tokens, with a grid the device holds at once (8 waves per
+    // SIMD): TPW the smallest of 8, 16, 32 that fits the tokens in that grid.
+    // Measured in the config C prefill step at 16384 tokens on MI355X:
+    // 61.3-61.6 us against 65.2-65.4 for the LDS-weights kernel below.
+    const int64_t nu = hidden / 8;
+    if (mode == 2 && n > 8192 && (nu == 256 || nu == 512)) {
+        // [q8][f16][tpr 512][tpw 8, 16, 32]
+        static const Kernel table_p[2][2][2][3] = {
+            {{{cuca_embed_q4_0_f32_rms_p256_w8, cuca_embed_q4_0_f32_rms_p256_w16, cuca_embed_q4_0_f32_rms_p256_w32},
+              {cuca_embed_q4_0_f32_rms_p512_w8, cuca_embed_q4_0_f32_rms_p512_w16, cuca_embed_q4_0_f32_rms_p512_w32}},
+             {{cuca_embed_q4_0_f16_rms_p256_w8, cuca_embed_q4_0_f16_rms_p256_w16, cuca_embed_q4_0_f16_rms_p256_w32},
+              {cuca_embed_q4_0_f16_rms_p512_w8, cuca_embed_q4_0_f16_rms_p512_w16, cuca_embed_q4_0_f16_rms_p512_w32}}},
+            {{{cuca_embed_q8_0_f32_rms_p256_w8, cuca_embed_q8_0_f32_rms_p256_w16, cuca_embed_q8_0_f32_rms_p256_w32},
+              {cuca_embed_q8_0_f32_rms_p512_w8, cuca_embed_q8_0_f32_rms_p512_w16, cuca_embed_q8_0_f32_rms_p512_w32}},
+             {{cuca_embed_q8_0_f16_rms_p256_w8, cuca_embed_q8_0_f16_rms_p256_w16, cuca_embed_q8_0_f16_rms_p256_w32},
+              {cuca_embed_q8_0_f16_rms_p512_w8, cuca_embed_q8_0_f16_rms_p512_w16, cuca_embed_q8_0_f16_rms_p512_w32}}}};
+        const int tpr = (int)nu;
+        const int64_t resident = (int64_t)ctx->cu_count * (2048 / tpr);
+        int wi = 0, tpw = 8;
+        while (wi < 2 && div_up(n, tpw) > resident) { wi++; tpw <<= 1; }
+        return launch(ctx, table_p[ggml_type == CUCA_GGML_Q8_0][f16][tpr == 512][wi], (unsigned)div_up(n, tpw),
+                      (unsigned)tpr, 0u, a);
+    }
     if (mode == 2 && per_lane <= 8 && n > 8192) {
         const int li = per_lane <= 2 ? 0 : per_lane <= 4 ? 1 : 2;
         a.tpw = (int32_t)std::max<int64_t>(1, std::min<int64_t>(8, n / 4096));

@@ -246,11 +246,15 @@ def test_embed_rms_matches_gather_then_norm(ctx, qname, out, hidden, eps, scale,
 @pytest.mark.parametrize("out", [np.float32, np.float16])
 @pytest.mark.parametrize("hidden,n,weighted,bad", [
     (256, 8200, True, False), (256, 20001, False, False), (2048, 8200, True, True), (4096, 8193, True, False),
-    (4096, 9000, False, True), (4128, 8200, True, False)])
+    (4096, 9000, False, True), (4128, 8200, True, False), (4096, 16384, True, True), (2048, 40000, True, False),
+    (4096, 40000, False, False)])
 def test_embed_rms_many_tokens(ctx, out, hidden, n, weighted, bad):
-    """More than 8192 tokens take the LDS-staged kernel (weights in LDS once
-    per workgroup, each wave looping over tpw tokens: 2 at 8200 tokens, 4 at
-    20001, the last workgroup partial) for rows of up to 4096; wider rows the
+    """More than 8192 tokens: rows of 256 or 512 units (hidden 2048, 4096)
+    take the persistent kernels (a thread per unit, each workgroup looping
+    over 8, 16 or 32 tokens; 40000 tokens of 4096 need more than one round
+    of workgroups), other rows of up to 4096 the LDS-staged kernel (weights
+    in LDS once per workgroup, each wave looping over tpw tokens: 2 at 8200
+    tokens, 4 at 20001, the last workgroup partial), wider rows the
     wave-per-token kernel.  An id outside the table gives zero rows of x and
     h and is reported, the other rows unchanged."""
     from helpers import assert_close
