@@ -1510,7 +1510,7 @@ def main():
     if not args.no_kv:
         log("rope + paged K/V store")
         kv = {}
-        for name, n, dtype in (("C", args.tokens, "f16"), ("C", 16384, "f16"), ("E", 8192, "f16"),
+        for name, n, dtype in (("C", 4096, "f16"), ("C", 16384, "f16"), ("E", 8192, "f16"),
                                ("B", 32, "f32")):
             r = kv_store_bench(ctx, torch, name, n, dtype)
             checked_rows += r.pop("verified_rows")
