@@ -137,6 +137,25 @@ typedef struct {
     int32_t pad_;
 } AttnArgs;
 
+/* Paged attention of many query rows of one sequence (attn_rows.hip): row
+ * r of q attends to the positions ranges[r] = [lo, hi) of the sequence's
+ * block table.  Values: pool_v, or (pool_v NULL, the latent form) the first
+ * v_width columns of the key rows themselves. */
+typedef struct {
+    const void *q;          /* [rows][q_ld]: n_head heads of head_dim        */
+    const void *pool_k;     /* [n_blocks, n_kv, 16, head_dim]                */
+    const void *pool_v;     /* the same, or NULL (values = key prefix)       */
+    const uint32_t *table;  /* [max_blocks]                                  */
+    const int32_t *ranges;  /* [rows, 2]                                     */
+    void *out;              /* [rows][out_ld]: n_head heads of v_width       */
+    unsigned long long *status;
+    int64_t q_ld, out_ld;   /* row strides in elements                       */
+    int64_t n_blocks;
+    int32_t rows, n_head, n_kv, head_dim, v_width, max_blocks;
+    float scale;
+    int32_t pad_;
+} AttnRowsArgs;
+
 /* Quantized matmul (qmm.hip): packed weights [n][ng][GB] (see there),
  * activations x [m][ldx], out [m][out_ld] in the activation type.  The
  * grid is nrb8 * ntile workgroups (nrb8 = nrb rounded up to a multiple of

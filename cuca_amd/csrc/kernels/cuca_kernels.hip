@@ -15,3 +15,4 @@
 #include "qmv.hip"
 #include "qmd.hip"
 #include "qgemm.hip"
+#include "attn_rows.hip"

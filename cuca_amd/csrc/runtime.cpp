@@ -1155,6 +1155,108 @@ cuca_status cuca_hip_paged_decode_noalloc(cuca_hip_ctx *ctx, const void *q, int6
 }
 
 // ---------------------------------------------------------------------
+// paged attention of many rows of one sequence (attend_paged_rows)
+// ---------------------------------------------------------------------
+
+// pool_v NULL: the latent form (values = the key rows' first v_width columns)
+static cuca_status attend_rows_run(cuca_hip_ctx *ctx, const void *q, int64_t q_ld, const void *pool_k,
+                                   const void *pool_v, int64_t n_blocks, const uint32_t *table, int64_t max_blocks,
+                                   const int32_t *ranges, int64_t rows, int32_t n_head, int32_t n_kv,
+                                   int32_t head_dim, int32_t v_width, float scale, void *out, int64_t out_ld,
+                                   cuca_dtype dtype) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    if (!dtype_ok(dtype)) return fail(ctx, CUCA_INVALID_ARG, "bad dtype %d", (int)dtype);
+    if (rows < 0 || rows > 0x7fffffffll) return fail(ctx, CUCA_INVALID_ARG, "bad row count %lld", (long long)rows);
+    if (n_head <= 0 || n_kv <= 0 || n_head % n_kv != 0)
+        return fail(ctx, CUCA_INVALID_ARG, "attention: query shape mismatch (%d heads over %d KV heads)",
+                    n_head, n_kv);
+    if (head_dim <= 0 || head_dim > 1024)
+        return fail(ctx, CUCA_UNSUPPORTED, "head_dim %d above 1024", head_dim);
+    if (v_width <= 0 || v_width > head_dim) return fail(ctx, CUCA_INVALID_ARG, "attention: bad latent value width");
+    if (v_width > 512) return fail(ctx, CUCA_UNSUPPORTED, "value width %d above 512", v_width);
+    if (max_blocks <= 0 || max_blocks > (1 << 22))
+        return fail(ctx, CUCA_INVALID_ARG, "bad block table width %lld", (long long)max_blocks);
+    if (n_blocks <= 0) return fail(ctx, CUCA_INVALID_ARG, "bad pool size %lld blocks", (long long)n_blocks);
+    if (rows == 0) return CUCA_OK;
+    if (!q || !pool_k || !table || !ranges || !out) return fail(ctx, CUCA_INVALID_ARG, "null pointer");
+    if (q_ld < (int64_t)n_head * head_dim)
+        return fail(ctx, CUCA_INVALID_ARG, "q row stride %lld below %d heads of %d", (long long)q_ld, n_head,
+                    head_dim);
+    if (out_ld < (int64_t)n_head * v_width)
+        return fail(ctx, CUCA_INVALID_ARG, "out row stride %lld below %d heads of %d", (long long)out_ld, n_head,
+                    v_width);
+    const size_t es = esize(dtype);
+    if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(out)) % es != 0)
+        return fail(ctx, CUCA_INVALID_ARG, "q and out must be aligned to their element");
+    const bool f16 = dtype == CUCA_F16;
+    const int G = n_head / n_kv;
+    const int di = head_dim == 64 ? 0 : head_dim == 128 ? 1 : head_dim == 256 ? 2 : -1;
+    const int gi = G == 1 ? 0 : G == 2 ? 1 : G == 4 ? 2 : G == 8 ? 3 : -1;
+    // the matrix-core kernel: its own value pool, 16-byte pool rows and
+    // loads, 8-byte (f16) or 16-byte (f32) query and output pieces
+    const uintptr_t qa = reinterpret_cast<uintptr_t>(q), oa = reinterpret_cast<uintptr_t>(out);
+    const bool mfma = pool_v && di >= 0 && gi >= 0 && al16(pool_k) && al16(pool_v) &&
+                      (f16 ? (qa % 8 == 0 && q_ld % 4 == 0 && oa % 8 == 0 && out_ld % 4 == 0)
+                           : (oa % 16 == 0 && out_ld % 4 == 0));
+    AttnRowsArgs a{};
+    a.q = q;
+    a.pool_k = pool_k;
+    a.pool_v = pool_v;
+    a.table = table;
+    a.ranges = ranges;
+    a.out = out;
+    a.status = ctx->status;
+    a.q_ld = q_ld;
+    a.out_ld = out_ld;
+    a.n_blocks = n_blocks;
+    a.rows = (int32_t)rows;
+    a.n_head = n_head;
+    a.n_kv = n_kv;
+    a.head_dim = head_dim;
+    a.v_width = v_width;
+    a.max_blocks = (int32_t)max_blocks;
+    a.scale = scale;
+    if (mfma) {
+        // [f16][head_dim 64/128/256][group 1/2/4/8]
+        static const Kernel table_k[2][3][4] = {
+            {{cuca_attn_rows_f32_d64_g1, cuca_attn_rows_f32_d64_g2, cuca_attn_rows_f32_d64_g4, cuca_attn_rows_f32_d64_g8},
+             {cuca_attn_rows_f32_d128_g1, cuca_attn_rows_f32_d128_g2, cuca_attn_rows_f32_d128_g4,
+              cuca_attn_rows_f32_d128_g8},
+             {cuca_attn_rows_f32_d256_g1, cuca_attn_rows_f32_d256_g2, cuca_attn_rows_f32_d256_g4,
+              cuca_attn_rows_f32_d256_g8}},
+            {{cuca_attn_rows_f16_d64_g1, cuca_attn_rows_f16_d64_g2, cuca_attn_rows_f16_d64_g4, cuca_attn_rows_f16_d64_g8},
+             {cuca_attn_rows_f16_d128_g1, cuca_attn_rows_f16_d128_g2, cuca_attn_rows_f16_d128_g4,
+              cuca_attn_rows_f16_d128_g8},
+             {cuca_attn_rows_f16_d256_g1, cuca_attn_rows_f16_d256_g2, cuca_attn_rows_f16_d256_g4,
+              cuca_attn_rows_f16_d256_g8}}};
+        const int64_t tiles = (rows + 15) / 16;
+        if (tiles * n_kv > 0x7fffffffll) return fail(ctx, CUCA_UNSUPPORTED, "too many attention tiles");
+        return launch(ctx, table_k[f16][di][gi], (unsigned)(tiles * n_kv), (unsigned)(64 * G), 0u, a);
+    }
+    const int64_t jobs = rows * n_head;
+    if ((jobs + 3) / 4 > 0x7fffffffll) return fail(ctx, CUCA_UNSUPPORTED, "too many attention rows");
+    return launch(ctx, f16 ? cuca_attn_rows_f16_generic : cuca_attn_rows_f32_generic, div_up(jobs, 4), 256u, 0u, a);
+}
+
+cuca_status cuca_hip_attend_rows(cuca_hip_ctx *ctx, const void *q, int64_t q_ld, const void *pool_k,
+                                 const void *pool_v, int64_t n_blocks, const uint32_t *table, int64_t max_blocks,
+                                 const int32_t *ranges, int64_t rows, int32_t n_head, int32_t n_kv, int32_t head_dim,
+                                 float scale, void *out, int64_t out_ld, cuca_dtype dtype) {
+    if (!pool_v) return fail(ctx, CUCA_INVALID_ARG, "null pointer");
+    return attend_rows_run(ctx, q, q_ld, pool_k, pool_v, n_blocks, table, max_blocks, ranges, rows, n_head, n_kv,
+                           head_dim, head_dim, scale, out, out_ld, dtype);
+}
+
+cuca_status cuca_hip_attend_latent_rows(cuca_hip_ctx *ctx, const void *q, int64_t q_ld, const void *pool,
+                                        int64_t n_blocks, const uint32_t *table, int64_t max_blocks,
+                                        const int32_t *ranges, int64_t rows, int32_t n_head, int32_t head_dim,
+                                        int32_t v_width, float scale, void *out, int64_t out_ld, cuca_dtype dtype) {
+    return attend_rows_run(ctx, q, q_ld, pool, nullptr, n_blocks, table, max_blocks, ranges, rows, n_head, 1,
+                           head_dim, v_width, scale, out, out_ld, dtype);
+}
+
+// ---------------------------------------------------------------------
 // quantized matmul (QmmWeight, qmm.rs)
 // ---------------------------------------------------------------------
 

@@ -81,6 +81,10 @@ SIGNATURES = {
                                     _i32, _f32, _p, _sz, _p, _st]),
     "cuca_hip_paged_decode_noalloc": (_st, [_p, _p, _i64, _p, _p, _i64, _p, _i64, _p, _i64, _i32,
                                             _i32, _i32, _f32, _p, _st]),
+    "cuca_hip_attend_rows": (_st, [_p, _p, _i64, _p, _p, _i64, _p, _i64, _p, _i64, _i32, _i32, _i32,
+                                   _f32, _p, _i64, _st]),
+    "cuca_hip_attend_latent_rows": (_st, [_p, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _i32, _i32,
+                                          _i32, _f32, _p, _i64, _st]),
     "cuca_hip_rope_tables": (_st, [ctypes.POINTER(RopeSpecC), _p, _i64, _p, _p]),
     "cuca_hip_qweight_bytes": (_st, [_u32, _i64, _i64, ctypes.POINTER(_sz)]),
     "cuca_hip_qweight_pack": (_st, [_p, _p, _u32, _i64, _i64, _p]),
@@ -397,6 +401,18 @@ class Context:
         self.check(self.L.cuca_hip_paged_decode_noalloc(self.ptr, q, q_ld, pool_k, pool_v, n_blocks,
                                                         tables, max_blocks, ranges, rows, n_head, n_kv,
                                                         head_dim, scale, out, dtype))
+
+    def attend_rows(self, q, q_ld, pool_k, pool_v, n_blocks, table, max_blocks, ranges, rows, n_head,
+                    n_kv, head_dim, scale, out, out_ld, dtype):
+        self.check(self.L.cuca_hip_attend_rows(self.ptr, q, q_ld, pool_k, pool_v, n_blocks, table,
+                                               max_blocks, ranges, rows, n_head, n_kv, head_dim, scale,
+                                               out, out_ld, dtype))
+
+    def attend_latent_rows(self, q, q_ld, pool, n_blocks, table, max_blocks, ranges, rows, n_head,
+                           head_dim, v_width, scale, out, out_ld, dtype):
+        self.check(self.L.cuca_hip_attend_latent_rows(self.ptr, q, q_ld, pool, n_blocks, table,
+                                                      max_blocks, ranges, rows, n_head, head_dim,
+                                                      v_width, scale, out, out_ld, dtype))
 
     def rope_store_kv(self, q, q_ld, k, k_ld, v, v_ld, rows, nq, nk, head_dim, n_dims, kind, cos,
                       sin, table_rows, positions, q_norm_w, k_norm_w, v_norm, eps, pool_k, pool_v,

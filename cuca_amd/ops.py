@@ -254,6 +254,20 @@ class KvPool:
              hip.dtype_code(q.dtype))
         return q
 
+    def attend_rows(self, q, table, ranges, n_head, scale):
+        """Attention of q [rows, n_head, d], rows of ONE sequence, over this
+        pool (attend_paged_rows, cpu/paged_attn.rs:177-213): table device u32
+        [max_blocks], ranges device int32 [rows, 2] (lo, hi).  Returns a
+        DeviceArray [rows, n_head, d]."""
+        rows, nh, d = q.shape
+        if nh != n_head or d != self.head_dim:
+            raise CucaError(hip.INVALID_ARG, "attention: query shape mismatch")
+        out = self.ctx.empty((rows, n_head, d), q.dtype)
+        self.ctx.attend_rows(q.ptr, n_head * d, self.k.ptr, self.v.ptr, self.n_blocks, table.ptr,
+                             table.shape[0], ranges.ptr, rows, n_head, self.n_kv_head, d, scale, out.ptr,
+                             n_head * d, hip.dtype_code(q.dtype))
+        return out
+
     def decode(self, q, tables, ranges, n_head, scale, workspace=None):
         """Paged decode attention of q [rows, n_head, d] (one query row per
         sequence) over this pool (paged_kernel.rs decode, gpu.rs:6002-6011):

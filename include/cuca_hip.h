@@ -30,6 +30,10 @@
  *                          GPU k/v branch, KvPool::write  gpu.rs:5266-5285, 1786-1806
  *   cuca_hip_kv_slots      block-table positions -> pool  paged.rs:9-16, gpu.rs:1940-1975
  *                          rows (host)
+ *   cuca_hip_attend_rows   attention of a sequence's rows cpu/paged_attn.rs:177-213,
+ *                          over its paged cache (prefill) paged_kernel.rs:6-8
+ *   cuca_hip_attend_       the latent (MLA) form          cpu/paged_attn.rs:215-251,
+ *     latent_rows                                         paged_kernel.rs:21-31
  *   cuca_hip_paged_decode  paged decode attention         paged_kernel.rs:92-282,
  *                          (+ _workspace, host)           cpu/paged_attn.rs:105-290
  *   cuca_hip_qmm           QmmWeight::forward_rows        qmm.rs:1810-1838
@@ -356,6 +360,42 @@ cuca_status cuca_hip_paged_decode(cuca_hip_ctx *ctx, const void *q, int64_t q_ld
                                   int32_t n_head, int32_t n_kv, int32_t head_dim, float scale,
                                   void *workspace, size_t workspace_bytes, void *out,
                                   cuca_dtype dtype);
+
+/* Attention of many query rows of ONE sequence over its paged cache: a
+ * prefill chunk, or speculative verification rows (attend_paged_rows,
+ * cpu/paged_attn.rs:177-213, 257-309; the GPU engine gathers the blocks and
+ * multiplies, paged_kernel.rs:6-8).
+ *   q      : [rows][q_ld] of dtype, n_head heads of head_dim at the start
+ *            of each row, rows aligned to the element
+ *   pools  : [n_blocks, n_kv, 16, head_dim] of dtype (pool_v NULL is an error)
+ *   table  : device u32 [max_blocks], the sequence's block table
+ *   ranges : device int32 [rows, 2] = (lo, hi): row r attends to positions
+ *            lo..hi-1 of the table (causal prefill: hi = its position + 1)
+ *   out    : [rows][out_ld] of dtype, n_head heads of head_dim
+ * Query head h reads KV head h / (n_head / n_kv); out = softmax(q.k *
+ * scale) . v over the row's positions, block by block with a running
+ * maximum, f32 throughout (f16 pools: exact f16 products on the matrix
+ * cores).  A row's result does not depend on the other rows of the call.
+ * An empty range, a range past the table, or a position of a range whose
+ * block id is >= n_blocks, is reported by cuca_hip_check_device, the row's
+ * output then zeros.  No workspace. */
+cuca_status cuca_hip_attend_rows(cuca_hip_ctx *ctx, const void *q, int64_t q_ld, const void *pool_k,
+                                 const void *pool_v, int64_t n_blocks, const uint32_t *table,
+                                 int64_t max_blocks, const int32_t *ranges, int64_t rows, int32_t n_head,
+                                 int32_t n_kv, int32_t head_dim, float scale, void *out, int64_t out_ld,
+                                 cuca_dtype dtype);
+
+/* The latent (multi-head latent attention) form: one pool of head_dim
+ * columns per position (n_kv 1) whose first v_width columns are also the
+ * value (attend_latent_rows, cpu/paged_attn.rs:215-251; the GPU decode's
+ * PagedCall::v_width, paged_kernel.rs:21-31).  out: [rows][out_ld], n_head
+ * heads of v_width.  v_width 0 or above head_dim is CUCA_INVALID_ARG
+ * ("attention: bad latent value width", as the reference). */
+cuca_status cuca_hip_attend_latent_rows(cuca_hip_ctx *ctx, const void *q, int64_t q_ld, const void *pool,
+                                        int64_t n_blocks, const uint32_t *table, int64_t max_blocks,
+                                        const int32_t *ranges, int64_t rows, int32_t n_head,
+                                        int32_t head_dim, int32_t v_width, float scale, void *out,
+                                        int64_t out_ld, cuca_dtype dtype);
 
 /* No counterpart in the reference.  cuca_hip_paged_decode without a
  * workspace, for callers that cannot allocate (code under HIP graph capture,

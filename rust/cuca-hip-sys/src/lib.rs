@@ -342,6 +342,43 @@ extern "C" {
         out: *mut c_void,
         dtype: cuca_dtype,
     ) -> cuca_status;
+    pub fn cuca_hip_attend_rows(
+        ctx: *mut cuca_hip_ctx,
+        q: *const c_void,
+        q_ld: i64,
+        pool_k: *const c_void,
+        pool_v: *const c_void,
+        n_blocks: i64,
+        table: *const u32,
+        max_blocks: i64,
+        ranges: *const i32,
+        rows: i64,
+        n_head: i32,
+        n_kv: i32,
+        head_dim: i32,
+        scale: f32,
+        out: *mut c_void,
+        out_ld: i64,
+        dtype: cuca_dtype,
+    ) -> cuca_status;
+    pub fn cuca_hip_attend_latent_rows(
+        ctx: *mut cuca_hip_ctx,
+        q: *const c_void,
+        q_ld: i64,
+        pool: *const c_void,
+        n_blocks: i64,
+        table: *const u32,
+        max_blocks: i64,
+        ranges: *const i32,
+        rows: i64,
+        n_head: i32,
+        head_dim: i32,
+        v_width: i32,
+        scale: f32,
+        out: *mut c_void,
+        out_ld: i64,
+        dtype: cuca_dtype,
+    ) -> cuca_status;
     pub fn cuca_hip_paged_decode_noalloc(
         ctx: *mut cuca_hip_ctx,
         q: *const c_void,
