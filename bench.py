@@ -844,15 +844,15 @@ def decode_us_per_layer(ctx, torch, n, replays=50, ctx_len=None):
     return graph_ms * 1000.0 / dl.layers, eager_ms * 1000.0 / dl.layers
 
 
-def kernel_calls(ctx, call, reps, warmup=5):
+def kernel_calls(ctx, call, reps, warmup=5, per_call=8):
     """Run call(i) `reps` times with per-kernel timestamps: returns (median
     of the per-call kernel-time sums in ms, [(kernel, median ms)] of one
-    call's launches)."""
+    call's launches).  per_call: the most launches one call makes."""
     import numpy as np
     for i in range(warmup):
         call(i)
     ctx.sync()
-    ctx.profile_start(8 * reps)
+    ctx.profile_start(per_call * reps)
     for i in range(reps):
         call(i)
     recs = ctx.profile_stop()
@@ -991,6 +991,132 @@ def qgemm_bench(ctx, torch, reps=10):
         del ws, raws
         torch.cuda.empty_cache()
     return res
+
+
+def prefill_layer_bench(ctx, torch, name="C", n=4096, reps=5):
+    """A whole prefill layer of config `name` at n f16 tokens on this
+    library, end to end: the fused gather + first-block norm, the Q|K|V
+    projection (cuca_hip_qgemm, Q4_0), RoPE + paged K/V store, the causal
+    attention of the n rows over the cache they were just stored in
+    (cuca_hip_attend_rows), the output projection, residual + norm, the
+    gate/up projection with the SwiGLU in its epilogue (cuca_hip_qgemm_glu),
+    down, residual + norm.  Per op: kernel time (per-kernel timestamps,
+    median of `reps` layers); the attention also as TFLOP/s of its causal
+    products (4 d heads per (row, key) pair).  Checked: sampled attention
+    rows against the oracle's attend_paged_rows, finite outputs."""
+    import numpy as np
+    from cuca_amd import hip
+    from cuca_amd import workloads as W
+    from oracle import oracle as O
+    cfg = W.CONFIGS[name]
+    H, F, nq, nk, d, eps = cfg["hidden"], cfg["ff"], cfg["nq"], cfg["nk"], cfg["head_dim"], cfg["eps"]
+    T, f16 = hip.GGML_Q4_0, hip.F16
+    dev, hf = "cuda", torch.float16
+    gen = torch.Generator(device=dev).manual_seed(cfg["seed"] * 31 + n)
+    nqkv = (nq + 2 * nk) * d
+
+    def weight(rows, k):
+        raw = W.quant_table_torch(gen, rows, k, "q4_0", (0.001, 0.02))
+        p = torch.empty(hip.qweight_bytes(T, rows, k), dtype=torch.uint8, device=dev)
+        ctx.qweight_pack(raw.data_ptr(), T, rows, k, p.data_ptr())
+        return p
+    wqkv, wo, wg, wu, wd = weight(nqkv, H), weight(H, nq * d), weight(F, H), weight(F, H), weight(H, F)
+    table_e = W.quant_table_torch(gen, cfg["vocab"], H, cfg["qtype"], cfg["d_range"])
+    ids = torch.randint(0, cfg["vocab"], (n,), device=dev, generator=gen, dtype=torch.int32)
+    wn = [(1 + 0.02 * torch.randn(H, device=dev, generator=gen)).float() for _ in range(3)]
+    x, h = torch.empty((n, H), device=dev, dtype=hf), torch.empty((n, H), device=dev, dtype=hf)
+    qkv = torch.empty((n, nqkv), device=dev, dtype=hf)
+    attn = torch.empty((n, nq * d), device=dev, dtype=hf)
+    br = torch.empty((n, H), device=dev, dtype=hf)
+    act = torch.empty((n, F), device=dev, dtype=hf)
+    n_blocks = n // 16 + 8
+    pk = torch.zeros((n_blocks, nk, 16, d), device=dev, dtype=hf)
+    pv = torch.zeros_like(pk)
+    rng = np.random.default_rng(cfg["seed"] + n)
+    table = rng.permutation(n_blocks)[: (n + 15) // 16].astype(np.uint32)
+    slots = torch.from_numpy(hip.kv_slots(table, 0, n, n_blocks)).to(dev)
+    dtab = torch.from_numpy(table.view(np.int32)).to(dev)
+    ranges_np = np.stack([np.zeros(n), np.arange(n) + 1], 1).astype(np.int32)
+    ranges = torch.from_numpy(ranges_np).to(dev)
+    pos = torch.arange(n, dtype=torch.int32, device=dev)
+    kind = hip.ROPE_NEOX if cfg["rope"] == "neox" else hip.ROPE_NORM
+    cos, sin = hip.rope_tables(kind, d, cfg["theta"], n)
+    dcos, dsin = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
+    qn = kn = None
+    if cfg.get("qk_norm"):
+        qn = (1 + 0.02 * torch.randn(d, device=dev, generator=gen)).float()
+        kn = (1 + 0.02 * torch.randn(d, device=dev, generator=gen)).float()
+    wsb = max(hip.qgemm_workspace(T, nqkv, H, n), hip.qgemm_workspace(T, H, nq * d, n),
+              hip.qgemm_workspace(T, F, H, n, True), hip.qgemm_workspace(T, H, F, n))
+    wsp = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    scale = 1.0 / float(np.sqrt(d))
+    ops = []
+
+    def op(label, fn):
+        ops.append((label, fn))
+    op("embed_rms", lambda: ctx.embed_gguf_rms(table_e.data_ptr(), W.GGML_ID[cfg["qtype"]], cfg["vocab"], H,
+                                               ids.data_ptr(), n, cfg["embd_scale"], wn[0].data_ptr(), eps,
+                                               x.data_ptr(), h.data_ptr(), f16))
+    op("qkv_matmul", lambda: ctx.qgemm(wqkv.data_ptr(), T, nqkv, H, h.data_ptr(), H, n, nqkv, wsp.data_ptr(), wsb,
+                                       qkv.data_ptr(), nqkv, f16))
+    op("rope_store_kv", lambda: ctx.rope_store_kv(
+        qkv.data_ptr(), nqkv, qkv.data_ptr() + 2 * nq * d, nqkv, qkv.data_ptr() + 2 * (nq + nk) * d, nqkv, n, nq,
+        nk, d, d, kind, dcos.data_ptr(), dsin.data_ptr(), n, pos.data_ptr(),
+        None if qn is None else qn.data_ptr(), None if kn is None else kn.data_ptr(), bool(cfg.get("qk_norm")),
+        eps, pk.data_ptr(), pv.data_ptr(), n_blocks, slots.data_ptr(), f16))
+    op("attention", lambda: ctx.attend_rows(qkv.data_ptr(), nqkv, pk.data_ptr(), pv.data_ptr(), n_blocks,
+                                            dtab.data_ptr(), len(table), ranges.data_ptr(), n, nq, nk, d, scale,
+                                            attn.data_ptr(), nq * d, f16))
+    op("o_matmul", lambda: ctx.qgemm(wo.data_ptr(), T, H, nq * d, attn.data_ptr(), nq * d, n, H, wsp.data_ptr(),
+                                     wsb, br.data_ptr(), H, f16))
+    op("add_rmsnorm_attn", lambda: ctx.add_rmsnorm(x.data_ptr(), br.data_ptr(), wn[1].data_ptr(), None, eps, eps,
+                                                   1.0, n, H, x.data_ptr(), h.data_ptr(), f16))
+    op("gate_up_glu_matmul", lambda: ctx.qgemm_glu(wg.data_ptr(), wu.data_ptr(), T, F, H, h.data_ptr(), H, n,
+                                                   hip.ACT_SILU, 0.0, wsp.data_ptr(), wsb, act.data_ptr(), F, f16))
+    op("down_matmul", lambda: ctx.qgemm(wd.data_ptr(), T, H, F, act.data_ptr(), F, n, H, wsp.data_ptr(), wsb,
+                                        br.data_ptr(), H, f16))
+    op("add_rmsnorm_ffn", lambda: ctx.add_rmsnorm(x.data_ptr(), br.data_ptr(), wn[2].data_ptr(), None, eps, eps,
+                                                  1.0, n, H, x.data_ptr(), h.data_ptr(), f16))
+    torch.cuda.synchronize()
+    # one layer, then check the attention of sampled rows against the oracle
+    for _, fn in ops[:4]:
+        fn()
+    torch.cuda.synchronize()
+    ctx.check_device()
+    rows = np.array([0, 1, 15, 16, 777, n // 2, n - 1])
+    q_rows = qkv[torch.from_numpy(rows).to(dev), : nq * d].cpu().numpy().reshape(len(rows), nq, d)
+    want = O.paged_attention(q_rows, np.repeat(table[None], len(rows), 0), ranges_np[rows], pk.cpu().numpy(),
+                             pv.cpu().numpy(), scale, threads=8)
+    got = attn[torch.from_numpy(rows).to(dev)].cpu().numpy().reshape(len(rows), nq, d)
+    vmax = np.abs(pv.cpu().numpy().astype(np.float64)).max()
+    ulp = np.spacing(np.abs(want).astype(np.float16)).astype(np.float64)
+    assert np.all(np.abs(got.astype(np.float64) - want) <= 2 * ulp + 1e-5 * vmax), "prefill layer attention"
+    # timed layers (the K/V store and attention rewrite the same pool rows)
+    counts = []
+    for _, fn in ops:
+        ctx.profile_start(64)
+        fn()
+        counts.append(len(ctx.profile_stop()))
+
+    def layer(i):
+        for _, fn in ops:
+            fn()
+    ms, parts = kernel_calls(ctx, layer, reps, 2, per_call=sum(counts))
+    assert len(parts) == sum(counts), (len(parts), counts)
+    assert torch.isfinite(h.float()).all(), "prefill layer: non-finite h"
+    per, j = {}, 0
+    for (label, _), c in zip(ops, counts):
+        per[label] = dict(kernels=[k for k, _ in parts[j:j + c]], us=round(sum(t for _, t in parts[j:j + c]) * 1000, 2))
+        j += c
+    att_flops = 4.0 * d * nq * (n * (n + 1) / 2)
+    per["attention"]["tflops"] = round(att_flops / (per["attention"]["us"] / 1e6) / 1e12, 1)
+    per["attention"]["mfma_frac"] = round(att_flops / (per["attention"]["us"] / 1e6) / 2.5e15, 4)
+    mm = sum(per[k]["us"] for k in ("qkv_matmul", "o_matmul", "gate_up_glu_matmul", "down_matmul"))
+    del wqkv, wo, wg, wu, wd, table_e
+    torch.cuda.empty_cache()
+    return dict(config=name, tokens=n, dtype="f16", weights="q4_0", us_per_layer=round(ms * 1000, 1),
+                tokens_per_s_per_layer=round(n / (ms / 1e3), 0), matmul_us=round(mm, 1),
+                attention_us=per["attention"]["us"], checked_attention_rows=int(rows.size), ops=per)
 
 
 def gemm_w16_bench(ctx, torch, reps=10):
@@ -1528,7 +1654,10 @@ def main():
             checked_rows += 2
         torch.cuda.empty_cache()
 
-    qmm = moe = head = qgemm = gemm16 = None
+    qmm = moe = head = qgemm = gemm16 = player = None
+    if not args.no_qmm and not args.no_attn:
+        log("a whole prefill layer (config C, 4096 tokens, f16): matmuls, RoPE + K/V store, attention")
+        player = prefill_layer_bench(ctx, torch, "C", 4096)
     if not args.no_qmm:
         log("quantized matmuls (8B decode shapes)")
         qmm = qmm_bench(ctx, torch)
@@ -1619,6 +1748,7 @@ def main():
         "moe_decode": moe,
         "end_of_step": head,
         "decode_us_per_layer": decode,
+        "prefill_layer": player,
         "prefill_bar": prefill_bar(ops, args.tokens, big, configs),
         "decode_bar": decode_bar(decode, attn),
         "roofline": {"kernel": glu["kernel"], "bound": "hbm",

@@ -49,20 +49,38 @@ typedef _Float16 attn_h4 __attribute__((ext_vector_type(4)));
 // [16 b, 16 b + 16).
 __device__ static inline bool rows_meets(int lo, int hi, int b) { return lo < 16 * b + 16 && hi > 16 * b; }
 
-template <typename T, int D, int G>
+template <typename T, int D, int G, int RT, int SBO = 0>
 __device__ static inline void attn_rows_body(const AttnRowsArgs &a) {
     constexpr bool F16 = sizeof(T) == 2;
-    constexpr int NT = 64 * G;                 // threads
+    constexpr int W = G * RT;                  // waves: (query head, row tile)
+    constexpr int NT = 64 * W;                 // threads
     constexpr int NS = D / 16;                 // output column slices
     constexpr int KST = F16 ? D + 16 : D + 4;  // K row stride in LDS (elements)
-    constexpr int VST = F16 ? 16 : D + 4;      // f16: V^T [D][16]; f32: V [16][D + 4]
-    __shared__ __align__(16) T ks[16 * KST];
-    __shared__ __align__(16) T vs[F16 ? D * 16 : 16 * (D + 4)];
+    constexpr int VT = 20;                     // f16: V^T [D][16 keys + 4 padding]
+    constexpr int VST = D + 4;                 // f32: V [16][D + 4]
+    constexpr int KSZ = 16 * KST, VSZ = F16 ? D * VT : 16 * VST;
+    // blocks of 16 positions per iteration: 2 where they fit 36 KB of LDS
+    // (the tiles are double-buffered: two workgroups of 8 waves per CU).
+    // Measured on MI355X, config C's causal attention of 4096 f16 rows: 1
+    // block 702 us, 2 blocks 675 us, 4 blocks (57 registers spilled at the
+    // 128-register cap) 974 us.
+    constexpr int PB = (KSZ + VSZ) * (int)sizeof(T);
+    constexpr int SB = SBO ? SBO : 2 * PB <= 36864 ? 2 : 1;
+    constexpr int CH = 16 * D * (int)sizeof(T) / 16; // 16-byte chunks of a block's K (and of its V)
+    constexpr int CPR = D * (int)sizeof(T) / 16;     // chunks per row
+    constexpr int LPT = (2 * CH + NT - 1) / NT;      // chunks a thread loads per block
+    __shared__ __align__(16) T ks[2][SB][KSZ];
+    __shared__ __align__(16) T vs[2][SB][VSZ];
+    __shared__ int span[2][RT];
+    // a launch of another shape would leave row tiles' spans unwritten (they
+    // bound the block loop and index the table): do nothing
+    if (blockDim.x != NT) return;
     const int wave = threadIdx.x / 64, lane = threadIdx.x & 63;
+    const int g = wave % G, rt = wave / G;
     const int r = lane & 15, grp = lane >> 4;
-    const int tile = blockIdx.x / a.n_kv, kvh = blockIdx.x - tile * a.n_kv;
-    const int row = tile * 16 + r;
-    const int head = kvh * G + wave;
+    const int wg_tile = blockIdx.x / a.n_kv, kvh = blockIdx.x - wg_tile * a.n_kv;
+    const int row = (wg_tile * RT + rt) * 16 + r;
+    const int head = kvh * G + g;
     const bool in_call = row < a.rows;
     int lo = 0, hi = 0;
     if (in_call) {
@@ -70,15 +88,24 @@ __device__ static inline void attn_rows_body(const AttnRowsArgs &a) {
         hi = a.ranges[2 * row + 1];
     }
     const bool valid = in_call && lo >= 0 && hi > lo && (int64_t)hi <= (int64_t)a.max_blocks * 16;
-    if (in_call && !valid && kvh == 0 && wave == 0 && grp == 0)
+    if (in_call && !valid && kvh == 0 && g == 0 && grp == 0)
         record_bad(a.status + CUCA_STATUS_KV_RANGE, (uint32_t)row, 0xffffffffu);
-    // the tile's blocks: the union of its valid rows' ranges (the same in
-    // every wave)
+    // the workgroup's blocks: the union of its valid rows' ranges
     int tlo = valid ? lo : 0x7fffffff, thi = valid ? hi : 0;
 #pragma unroll
     for (int off = 1; off < 16; off <<= 1) {
         tlo = min(tlo, __shfl_xor(tlo, off));
         thi = max(thi, __shfl_xor(thi, off));
+    }
+    if (g == 0 && lane == 0) {
+        span[0][rt] = tlo;
+        span[1][rt] = thi;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < RT; i++) {
+        tlo = min(tlo, span[0][i]);
+        thi = max(thi, span[1][i]);
     }
     T *orow = reinterpret_cast<T *>(a.out) + (int64_t)(in_call ? row : 0) * a.out_ld + (int64_t)head * D;
     // the query: lane (r, grp) holds row r's dims 16 j + 4 grp .. + 3 (f16)
@@ -100,69 +127,127 @@ __device__ static inline void attn_rows_body(const AttnRowsArgs &a) {
         acc[s] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
         if constexpr (F16) acl[s] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
+    // scores in the base-2 domain: x = q.k * scale * log2(e), weights
+    // 2^(x - max) (v_exp_f32); the exponent's extra rounding is a relative
+    // error of about |x| 2^-24 in a weight, far inside the bar
+    const float scale2 = a.scale * 1.4426950408889634f;
     float m = -__builtin_huge_valf(), l = 0.0f;
     bool bad = false;
+    const T *pk = reinterpret_cast<const T *>(a.pool_k);
     const T *pv = reinterpret_cast<const T *>(a.pool_v ? a.pool_v : a.pool_k);
-    if (thi > 0) {
+    if (thi > 0) { // uniform over the workgroup
         const int b0 = tlo >> 4, b1 = (thi - 1) >> 4;
-        for (int b = b0; b <= b1; b++) {
-            const uint32_t blk = a.table[b];
-            const bool ok = (int64_t)blk < a.n_blocks;
-            if (!ok && valid && rows_meets(lo, hi, b)) {
-                bad = true;
-                if (kvh == 0 && wave == 0 && grp == 0)
-                    record_bad(a.status + CUCA_STATUS_KV_RANGE, (uint32_t)row, (uint32_t)max(16 * b, lo));
-            }
-            const int64_t base = ((int64_t)(ok ? blk : 0u) * a.n_kv + kvh) * 16 * D; // the block's 16 rows
-            // stage K and V of the block (16 x D each) in LDS
-            constexpr int CH = 16 * D * (int)sizeof(T) / 16; // 16-byte chunks per block
-            constexpr int CPR = D * (int)sizeof(T) / 16;     // chunks per row
+        // the table entries of the blocks, 64 at a time: lane i holds block
+        // b0 + 64 c + i (entries past b1 repeat b1's: their keys are masked)
+        uint32_t tabv = 0;
+        auto load_tab = [&](int c) {
+            const int bi = b0 + 64 * c + lane;
+            tabv = a.table[bi <= b1 ? bi : b1];
+        };
+        auto blk_of = [&](int b) -> uint32_t { return (uint32_t)__builtin_amdgcn_readlane((int)tabv, (b - b0) & 63); };
+        // a thread's chunks of a block: c < CH of K (16 bytes along a row),
+        // the rest of V: f16, 4 keys x 2 columns (four dwords down the rows,
+        // written to the transposed tile as two 8-byte pieces); f32, 16
+        // bytes of a row, keys fastest
+        u32x4 pre[SB][LPT];
+        auto fetch = [&](int bs) {
 #pragma unroll
-            for (int c0 = 0; c0 < CH; c0 += NT) {
-                const int c = c0 + (int)threadIdx.x;
-                if (CH % NT == 0 || c < CH) {
-                    const int key = c / CPR, col = (c - key * CPR) * (16 / (int)sizeof(T));
-                    const u32x4 kc = *reinterpret_cast<const u32x4 *>(reinterpret_cast<const T *>(a.pool_k) + base +
-                                                                      key * D + col);
-                    const u32x4 vc = *reinterpret_cast<const u32x4 *>(pv + base + key * D + col);
-                    *reinterpret_cast<u32x4 *>(ks + key * KST + col) = kc;
-                    if constexpr (F16) {
-                        const f16x8 v8 = __builtin_bit_cast(f16x8, vc);
+            for (int i = 0; i < SB; i++) {
+                const uint32_t blk = blk_of(bs + i);
+                const int64_t base = ((int64_t)((int64_t)blk < a.n_blocks ? blk : 0u) * a.n_kv + kvh) * 16 * D;
 #pragma unroll
-                        for (int i = 0; i < 8; i++) vs[(col + i) * 16 + key] = v8[i];
-                    } else {
-                        *reinterpret_cast<u32x4 *>(vs + key * VST + col) = vc;
+                for (int t = 0; t < LPT; t++) {
+                    const int c = (int)threadIdx.x + t * NT;
+                    if (2 * CH % NT == 0 || c < 2 * CH) {
+                        if (c < CH) {
+                            const int key = c / CPR, col = (c - key * CPR) * (16 / (int)sizeof(T));
+                            pre[i][t] = *reinterpret_cast<const u32x4 *>(pk + base + key * D + col);
+                        } else if constexpr (F16) {
+                            // 4 keys x 2 columns: the dwords of columns 2 dp, 2 dp + 1 of rows 4 kq .. + 3
+                            const int u = c - CH, kq = u & 3, dp = u >> 2;
+                            const uint32_t *vr = reinterpret_cast<const uint32_t *>(pv + base + 4 * kq * D + 2 * dp);
+                            pre[i][t] = u32x4{vr[0], vr[D / 2], vr[D], vr[3 * D / 2]};
+                        } else {
+                            const int key = (c - CH) & 15, col = ((c - CH) >> 4) * 4;
+                            pre[i][t] = *reinterpret_cast<const u32x4 *>(pv + base + key * D + col);
+                        }
                     }
                 }
             }
-            __syncthreads();
-            // S^T: lane (r, grp) gets the scores of keys 4 grp + i with row r
-            f32x4 st = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-            if constexpr (F16) {
+        };
+        auto stage = [&](int buf) {
 #pragma unroll
-                for (int j = 0; j < NS; j++) {
-                    const attn_h4 kk = *reinterpret_cast<const attn_h4 *>(ks + r * KST + 16 * j + 4 * grp);
-                    st = __builtin_amdgcn_mfma_f32_16x16x16f16(kk, qh[j], st, 0, 0, 0);
+            for (int i = 0; i < SB; i++) {
+#pragma unroll
+                for (int t = 0; t < LPT; t++) {
+                    const int c = (int)threadIdx.x + t * NT;
+                    if (2 * CH % NT == 0 || c < 2 * CH) {
+                        if (c < CH) {
+                            const int key = c / CPR, col = (c - key * CPR) * (16 / (int)sizeof(T));
+                            *reinterpret_cast<u32x4 *>(&ks[buf][i][key * KST + col]) = pre[i][t];
+                        } else if constexpr (F16) {
+                            // the low halves are column 2 dp of the 4 keys, the high halves 2 dp + 1
+                            const int u = c - CH, kq = u & 3, dp = u >> 2;
+                            const u32x4 w = pre[i][t];
+                            const uint2 lo2 = {(w.x & 0xffffu) | (w.y << 16), (w.z & 0xffffu) | (w.w << 16)};
+                            const uint2 hi2 = {(w.x >> 16) | (w.y & 0xffff0000u), (w.z >> 16) | (w.w & 0xffff0000u)};
+                            *reinterpret_cast<uint2 *>(&vs[buf][i][(2 * dp) * VT + 4 * kq]) = lo2;
+                            *reinterpret_cast<uint2 *>(&vs[buf][i][(2 * dp + 1) * VT + 4 * kq]) = hi2;
+                        } else {
+                            const int key = (c - CH) & 15, col = ((c - CH) >> 4) * 4;
+                            *reinterpret_cast<u32x4 *>(&vs[buf][i][key * VST + col]) = pre[i][t];
+                        }
+                    }
                 }
-            } else {
-#pragma unroll
-                for (int j = 0; j < D / 4; j++)
-                    st = __builtin_amdgcn_mfma_f32_16x16x4f32((float)ks[r * KST + 4 * j + grp], qf[j], st, 0, 0, 0);
             }
-            float x[4];
-            bool in[4];
+        };
+        load_tab(0);
+        fetch(b0);
+        stage(0);
+        __syncthreads();
+        for (int bs = b0; bs <= b1; bs += SB) {
+            const int buf = ((bs - b0) / SB) & 1;
+            const bool more = bs + SB <= b1;
+            if (more && ((bs + SB - b0) & 63) == 0) load_tab((bs + SB - b0) >> 6);
+            if (more) fetch(bs + SB); // the next blocks' loads, in flight during these
+            // scores: lane (r, grp) gets keys 4 grp + i of each block with row r
+            float x[SB][4];
+            bool in[SB][4];
             float bmax = -__builtin_huge_valf();
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int p = 16 * b + 4 * grp + i;
-                in[i] = valid && p >= lo && p < hi;
-                x[i] = st[i] * a.scale;
-                if (in[i]) bmax = fmaxf(bmax, x[i]);
+            for (int sb = 0; sb < SB; sb++) {
+                const int b = bs + sb;
+                if (b <= b1 && (int64_t)blk_of(b) >= a.n_blocks && valid && rows_meets(lo, hi, b)) {
+                    bad = true;
+                    if (kvh == 0 && g == 0 && grp == 0)
+                        record_bad(a.status + CUCA_STATUS_KV_RANGE, (uint32_t)row, (uint32_t)max(16 * b, lo));
+                }
+                const T *kt = ks[buf][sb];
+                f32x4 st = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+                if constexpr (F16) {
+#pragma unroll
+                    for (int j = 0; j < NS; j++) {
+                        const attn_h4 kk = *reinterpret_cast<const attn_h4 *>(kt + r * KST + 16 * j + 4 * grp);
+                        st = __builtin_amdgcn_mfma_f32_16x16x16f16(kk, qh[j], st, 0, 0, 0);
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < D / 4; j++)
+                        st = __builtin_amdgcn_mfma_f32_16x16x4f32((float)kt[r * KST + 4 * j + grp], qf[j], st, 0, 0,
+                                                                  0);
+                }
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int p = 16 * b + 4 * grp + i;
+                    in[sb][i] = valid && p >= lo && p < hi;
+                    x[sb][i] = st[i] * scale2;
+                    if (in[sb][i]) bmax = fmaxf(bmax, x[sb][i]);
+                }
             }
             bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
             bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
             if (bmax > m) { // rescale what was accumulated under the old maximum
-                const float corr = expf(m - bmax);
+                const float corr = __builtin_amdgcn_exp2f(m - bmax);
                 l *= corr;
 #pragma unroll
                 for (int s = 0; s < NS; s++) {
@@ -171,38 +256,46 @@ __device__ static inline void attn_rows_body(const AttnRowsArgs &a) {
                 }
                 m = bmax;
             }
-            float e[4], es = 0.0f;
+            float es = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                e[i] = in[i] ? expf(x[i] - m) : 0.0f;
-                es += e[i];
+            for (int sb = 0; sb < SB; sb++) {
+                float e[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    e[i] = in[sb][i] ? __builtin_amdgcn_exp2f(x[sb][i] - m) : 0.0f;
+                    es += e[i];
+                }
+                // O^T += V^T P^T
+                const T *vt = vs[buf][sb];
+                if constexpr (F16) {
+                    attn_h4 ph, pl;
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        ph[i] = (_Float16)e[i];
+                        pl[i] = (_Float16)((e[i] - (float)ph[i]) * 2048.0f);
+                    }
+#pragma unroll
+                    for (int s = 0; s < NS; s++) {
+                        const attn_h4 vv = *reinterpret_cast<const attn_h4 *>(vt + (16 * s + r) * VT + 4 * grp);
+                        acc[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(vv, ph, acc[s], 0, 0, 0);
+                        acl[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(vv, pl, acl[s], 0, 0, 0);
+                    }
+                } else {
+#pragma unroll
+                    for (int s = 0; s < NS; s++)
+#pragma unroll
+                        for (int j = 0; j < 4; j++)
+                            acc[s] = __builtin_amdgcn_mfma_f32_16x16x4f32((float)vt[(4 * grp + j) * VST + 16 * s + r],
+                                                                          e[j], acc[s], 0, 0, 0);
+                }
             }
             es += __shfl_xor(es, 16);
             es += __shfl_xor(es, 32);
             l += es;
-            // O^T += V^T P^T
-            if constexpr (F16) {
-                attn_h4 ph, pl;
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    ph[i] = (_Float16)e[i];
-                    pl[i] = (_Float16)((e[i] - (float)ph[i]) * 2048.0f);
-                }
-#pragma unroll
-                for (int s = 0; s < NS; s++) {
-                    const attn_h4 vv = *reinterpret_cast<const attn_h4 *>(vs + (16 * s + r) * 16 + 4 * grp);
-                    acc[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(vv, ph, acc[s], 0, 0, 0);
-                    acl[s] = __builtin_amdgcn_mfma_f32_16x16x16f16(vv, pl, acl[s], 0, 0, 0);
-                }
-            } else {
-#pragma unroll
-                for (int s = 0; s < NS; s++)
-#pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        acc[s] = __builtin_amdgcn_mfma_f32_16x16x4f32((float)vs[(4 * grp + j) * VST + 16 * s + r], e[j],
-                                                                      acc[s], 0, 0, 0);
-            }
-            __syncthreads(); // before the next block overwrites the tiles
+            if (more) stage(buf ^ 1);
+            // the next blocks' tiles are in place, and every wave is done
+            // with these before the blocks after overwrite them
+            __syncthreads();
         }
     }
     if (!in_call) return;
@@ -297,9 +390,15 @@ __device__ static inline void attn_rows_generic_body(const AttnRowsArgs &a) {
     }
 }
 
+// Row tiles of 16 a workgroup: 4 at groups 1 and 2, 2 at 4, 1 at 8 (4 to 8
+// waves, every wave a query head and a row tile, all sharing the block's
+// K and V in LDS).
+// Up to head_dim 128, at most 128 registers (four waves per SIMD: two
+// workgroups of 8 waves per CU).
 #define CUCA_ATTN_ROWS(NAME, T, D, G)                                                      \
-    extern "C" __global__ __launch_bounds__(64 * G) void NAME(AttnRowsArgs a) {            \
-        attn_rows_body<T, D, G>(a);                                                        \
+    extern "C" __global__ __launch_bounds__(64 * G * (G <= 2 ? 4 : 8 / G), D <= 128 ? 4 : 1) \
+        void NAME(AttnRowsArgs a) {                                                        \
+        attn_rows_body<T, D, G, (G <= 2 ? 4 : 8 / G)>(a);                                  \
     }
 #define CUCA_ATTN_ROWS_SET(TN, T)                                                          \
     CUCA_ATTN_ROWS(cuca_attn_rows_##TN##_d64_g1, T, 64, 1)                                 \

@@ -1230,9 +1230,12 @@ static cuca_status attend_rows_run(cuca_hip_ctx *ctx, const void *q, int64_t q_l
               cuca_attn_rows_f16_d128_g8},
              {cuca_attn_rows_f16_d256_g1, cuca_attn_rows_f16_d256_g2, cuca_attn_rows_f16_d256_g4,
               cuca_attn_rows_f16_d256_g8}}};
-        const int64_t tiles = (rows + 15) / 16;
+        // a workgroup: RT tiles of 16 rows x the G query heads, one wave each
+        // (the kernels' launch shape: RT = 4 at groups 1 and 2, 8 / G beyond)
+        const int rt = G <= 2 ? 4 : 8 / G;
+        const int64_t tiles = (rows + 16 * rt - 1) / (16 * rt);
         if (tiles * n_kv > 0x7fffffffll) return fail(ctx, CUCA_UNSUPPORTED, "too many attention tiles");
-        return launch(ctx, table_k[f16][di][gi], (unsigned)(tiles * n_kv), (unsigned)(64 * G), 0u, a);
+        return launch(ctx, table_k[f16][di][gi], (unsigned)(tiles * n_kv), (unsigned)(64 * G * rt), 0u, a);
     }
     const int64_t jobs = rows * n_head;
     if ((jobs + 3) / 4 > 0x7fffffffll) return fail(ctx, CUCA_UNSUPPORTED, "too many attention rows");
