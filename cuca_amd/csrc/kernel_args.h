@@ -23,7 +23,8 @@ enum {
     CUCA_STATUS_KV_SLOT = 2,
     CUCA_STATUS_KV_RANGE = 3, /* attention: a key position without a block, or a bad range */
     CUCA_STATUS_MOE_PAIR = 4, /* MoE: a pair whose token is outside the activation rows */
-    CUCA_STATUS_WORDS = 5
+    CUCA_STATUS_HEAD_ROW = 5, /* indexed LM head: a vocabulary id past the head's rows */
+    CUCA_STATUS_WORDS = 6
 };
 
 typedef struct {
@@ -136,6 +137,20 @@ typedef struct {
     int32_t direct;         /* one part a row: the split writes out itself  */
     int32_t pad_;
 } AttnArgs;
+
+/* Packed weight rows gathered by index (the indexed LM head): dst row j =
+ * src row ids[j] (row_bytes each, a multiple of 16), zeros for an id past
+ * n_src (recorded). */
+typedef struct {
+    const uint8_t *src;
+    const uint32_t *ids;
+    uint8_t *dst;
+    unsigned long long *status;
+    int64_t n_src;
+    int64_t row_bytes;
+    int32_t n;
+    int32_t pad_;
+} RowGatherArgs;
 
 /* Paged attention of many query rows of one sequence (attn_rows.hip): row
  * r of q attends to the positions ranges[r] = [lo, hi) of the sequence's

@@ -59,13 +59,11 @@ __device__ static inline void attn_rows_body(const AttnRowsArgs &a) {
     constexpr int VT = 20;                     // f16: V^T [D][16 keys + 4 padding]
     constexpr int VST = D + 4;                 // f32: V [16][D + 4]
     constexpr int KSZ = 16 * KST, VSZ = F16 ? D * VT : 16 * VST;
-    // blocks of 16 positions per iteration: 2 where they fit 36 KB of LDS
-    // (the tiles are double-buffered: two workgroups of 8 waves per CU).
-    // Measured on MI355X, config C's causal attention of 4096 f16 rows: 1
-    // block 702 us, 2 blocks 675 us, 4 blocks (57 registers spilled at the
-    // 128-register cap) 974 us.
-    constexpr int PB = (KSZ + VSZ) * (int)sizeof(T);
-    constexpr int SB = SBO ? SBO : 2 * PB <= 36864 ? 2 : 1;
+    // blocks of 16 positions per iteration: one.  Measured on MI355X,
+    // config C's causal attention of 4096 f16 rows at the 128-register cap:
+    // 1 block 702 us, 2 blocks 675 us but 13 registers spilled to scratch,
+    // 4 blocks (57 spilled) 974 us; without the cap 2 blocks 850 us.
+    constexpr int SB = SBO ? SBO : 1;
     constexpr int CH = 16 * D * (int)sizeof(T) / 16; // 16-byte chunks of a block's K (and of its V)
     constexpr int CPR = D * (int)sizeof(T) / 16;     // chunks per row
     constexpr int LPT = (2 * CH + NT - 1) / NT;      // chunks a thread loads per block
@@ -393,10 +391,11 @@ __device__ static inline void attn_rows_generic_body(const AttnRowsArgs &a) {
 // Row tiles of 16 a workgroup: 4 at groups 1 and 2, 2 at 4, 1 at 8 (4 to 8
 // waves, every wave a query head and a row tile, all sharing the block's
 // K and V in LDS).
-// Up to head_dim 128, at most 128 registers (four waves per SIMD: two
-// workgroups of 8 waves per CU).
+// f16 up to head_dim 128: at most 128 registers (four waves per SIMD, two
+// workgroups of 8 waves per CU), which they fit without spilling.
 #define CUCA_ATTN_ROWS(NAME, T, D, G)                                                      \
-    extern "C" __global__ __launch_bounds__(64 * G * (G <= 2 ? 4 : 8 / G), D <= 128 ? 4 : 1) \
+    extern "C" __global__ __launch_bounds__(64 * G * (G <= 2 ? 4 : 8 / G),                 \
+                                            sizeof(T) == 2 && D <= 128 && G >= 2 ? 4 : 1)  \
         void NAME(AttnRowsArgs a) {                                                        \
         attn_rows_body<T, D, G, (G <= 2 ? 4 : 8 / G)>(a);                                  \
     }

@@ -292,3 +292,20 @@ extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void cuca_argmax_merge(PickA
 extern "C" __global__ __launch_bounds__(PICK_THREADS) void cuca_topk_f32(PickArgs a) { topk_body<float, 0>(a); }
 extern "C" __global__ __launch_bounds__(PICK_THREADS) void cuca_topk_f16(PickArgs a) { topk_body<_Float16, 0>(a); }
 extern "C" __global__ __launch_bounds__(PICK_THREADS) void cuca_topk_merge(PickArgs a) { topk_body<float, 1>(a); }
+
+// The indexed LM head's weight rows (head_indexed, cpu.rs:2603-2606;
+// QMatMul::forward_indexed, qmm.rs:1818-1843): workgroup j copies packed
+// row ids[j] of the head into row j of a contiguous matrix, which the
+// quantized matmul then runs as a row prefix -- the same kernel per row,
+// so the same bits as the full head's column ids[j].  An id past the head
+// is recorded and gives a zero row.
+extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void cuca_gather_rows(RowGatherArgs a) {
+    const int j = blockIdx.x;
+    const uint32_t id = a.ids[j];
+    const bool ok = (int64_t)id < a.n_src;
+    if (!ok && threadIdx.x == 0) record_bad(a.status + CUCA_STATUS_HEAD_ROW, (uint32_t)j, id);
+    const u32x4 *src = reinterpret_cast<const u32x4 *>(a.src + (int64_t)(ok ? id : 0u) * a.row_bytes);
+    u32x4 *dst = reinterpret_cast<u32x4 *>(a.dst + (int64_t)j * a.row_bytes);
+    for (int64_t c = threadIdx.x; c < a.row_bytes / 16; c += CUCA_BLOCK)
+        dst[c] = ok ? src[c] : u32x4{0u, 0u, 0u, 0u};
+}

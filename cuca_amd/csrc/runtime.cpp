@@ -84,6 +84,7 @@ struct cuca_hip_ctx {
     int64_t last_kv_blocks = 0;   // the pool size of the last K/V store (for messages)
     int64_t last_table_rows = 0;
     int64_t last_moe_tokens = 0;  // the activation rows of the last MoE up call
+    int64_t last_head_rows = 0;   // the vocabulary of the last indexed LM head
     // device scratch for the per-slice results of cuca_hip_argmax / _top_k
     // (allocated with the context: ops never allocate)
     void *pscratch = nullptr;
@@ -361,6 +362,11 @@ cuca_status cuca_hip_check_device(cuca_hip_ctx *ctx) {
         unsigned long long v = w[CUCA_STATUS_KV_SLOT];
         return fail(ctx, CUCA_OUT_OF_RANGE, "K/V slot %d outside the pool of %lld blocks (row %u)",
                     (int)(v & 0xffffffffu), (long long)ctx->last_kv_blocks, (unsigned)(v >> 32));
+    }
+    if (w[CUCA_STATUS_HEAD_ROW] != none) {
+        unsigned long long v = w[CUCA_STATUS_HEAD_ROW];
+        return fail(ctx, CUCA_OUT_OF_RANGE, "qmm: weight row %u out of range (%lld) (index %u)",
+                    (unsigned)(v & 0xffffffffu), (long long)ctx->last_head_rows, (unsigned)(v >> 32));
     }
     if (w[CUCA_STATUS_MOE_PAIR] != none) {
         unsigned long long v = w[CUCA_STATUS_MOE_PAIR];
@@ -1728,6 +1734,55 @@ cuca_status cuca_hip_lm_head(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_typ
     cap.logit_mult = logit_mult;
     cap.softcap = softcap;
     return qmm_common(ctx, w, nullptr, ggml_type, vocab, n_embd, x, ldx, m, rows, 0, 0.0f, logits, logits_ld,
+                      dtype, cap);
+}
+
+cuca_status cuca_hip_lm_head_indexed_workspace(uint32_t ggml_type, int64_t n_embd, int64_t n_ids, size_t *bytes) {
+    if (!bytes) return fail(nullptr, CUCA_INVALID_ARG, "null output pointer");
+    if (n_ids < 0) return fail(nullptr, CUCA_INVALID_ARG, "negative count");
+    if (n_ids == 0) {
+        *bytes = 0;
+        return CUCA_OK;
+    }
+    return cuca_hip_qweight_bytes(ggml_type, n_ids, n_embd, bytes);
+}
+
+cuca_status cuca_hip_lm_head_indexed(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type, int64_t vocab,
+                                     int64_t n_embd, const void *x, int64_t ldx, int64_t m, const uint32_t *ids,
+                                     int64_t n_ids, float logit_scale, float logit_mult, float softcap,
+                                     void *workspace, size_t workspace_bytes, void *logits, int64_t logits_ld,
+                                     cuca_dtype dtype) {
+    cuca_status st = use(ctx);
+    if (st != CUCA_OK) return st;
+    if (!(logit_scale > 0.0f) || !std::isfinite(logit_scale) || !std::isfinite(logit_mult) ||
+        !(softcap >= 0.0f) || !std::isfinite(softcap))
+        return fail(ctx, CUCA_INVALID_ARG, "lm head: bad logit scale, multiplier or soft-cap");
+    int g = 0, gb = 0;
+    if ((st = qweight_shape(ctx, ggml_type, vocab, n_embd, &g, &gb)) != CUCA_OK) return st;
+    if (n_ids < 0 || n_ids > 0x7fffffffll) return fail(ctx, CUCA_INVALID_ARG, "bad id count %lld", (long long)n_ids);
+    if (m < 0) return fail(ctx, CUCA_INVALID_ARG, "negative count");
+    if (n_ids == 0 || m == 0) return CUCA_OK;
+    size_t need = 0;
+    if ((st = cuca_hip_lm_head_indexed_workspace(ggml_type, n_embd, n_ids, &need)) != CUCA_OK) return st;
+    if (!w || !ids || !workspace || !logits) return fail(ctx, CUCA_INVALID_ARG, "null pointer");
+    if (workspace_bytes < need)
+        return fail(ctx, CUCA_INVALID_ARG, "lm head: workspace of %zu bytes, %zu needed", workspace_bytes, need);
+    if (!al16(w) || !al16(workspace)) return fail(ctx, CUCA_INVALID_ARG, "weights and workspace must be 16-byte aligned");
+    RowGatherArgs ga{};
+    ga.src = static_cast<const uint8_t *>(w);
+    ga.ids = ids;
+    ga.dst = static_cast<uint8_t *>(workspace);
+    ga.status = ctx->status;
+    ga.n_src = vocab;
+    ga.row_bytes = (int64_t)((n_embd / 32 + g - 1) / g) * gb;
+    ga.n = (int32_t)n_ids;
+    ctx->last_head_rows = vocab;
+    if ((st = launch(ctx, cuca_gather_rows, (unsigned)n_ids, 256u, 0u, ga)) != CUCA_OK) return st;
+    LogitCap cap;
+    cap.logit_scale = logit_scale;
+    cap.logit_mult = logit_mult;
+    cap.softcap = softcap;
+    return qmm_common(ctx, workspace, nullptr, ggml_type, n_ids, n_embd, x, ldx, m, n_ids, 0, 0.0f, logits, logits_ld,
                       dtype, cap);
 }
 

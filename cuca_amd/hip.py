@@ -124,6 +124,9 @@ SIGNATURES = {
     "cuca_hip_qmv_glu": (_st, [_p, _p, _p, _u32, _i64, _i64, _p, _p, _i64, _st, _f32, _p, _i64, _st]),
     "cuca_hip_lm_head": (_st, [_p, _p, _u32, _i64, _i64, _p, _i64, _i64, _i64, _f32, _f32, _f32, _p,
                                _i64, _st]),
+    "cuca_hip_lm_head_indexed_workspace": (_st, [_u32, _i64, _i64, ctypes.POINTER(_sz)]),
+    "cuca_hip_lm_head_indexed": (_st, [_p, _p, _u32, _i64, _i64, _p, _i64, _i64, _p, _i64, _f32, _f32,
+                                       _f32, _p, _sz, _p, _i64, _st]),
     "cuca_hip_argmax": (_st, [_p, _p, _i64, _i64, _i64, _st, _p]),
     "cuca_hip_top_k": (_st, [_p, _p, _i64, _i64, _i64, _st, _i32, _f32, _p, _p, _p]),
     "cuca_hip_sample_candidates": (_st, [_p, _p, _i32, _f32, _u32, ctypes.POINTER(ctypes.c_uint64),
@@ -526,6 +529,12 @@ class Context:
         self.check(self.L.cuca_hip_lm_head(self.ptr, w, ggml_type, vocab, n_embd, x, ldx, m, rows,
                                            logit_scale, logit_mult, softcap, logits, logits_ld, dtype))
 
+    def lm_head_indexed(self, w, ggml_type, vocab, n_embd, x, ldx, m, ids, n_ids, logit_scale, logit_mult,
+                        softcap, ws, ws_bytes, logits, logits_ld, dtype):
+        self.check(self.L.cuca_hip_lm_head_indexed(self.ptr, w, ggml_type, vocab, n_embd, x, ldx, m, ids,
+                                                   n_ids, logit_scale, logit_mult, softcap, ws, ws_bytes,
+                                                   logits, logits_ld, dtype))
+
     def argmax(self, logits, ld, rows, vocab, dtype, ids):
         self.check(self.L.cuca_hip_argmax(self.ptr, logits, ld, rows, vocab, dtype, ids))
 
@@ -588,6 +597,13 @@ def paged_decode_workspace(rows, n_head, head_dim, max_blocks):
     _check(lib().cuca_hip_paged_decode_workspace(rows, n_head, head_dim, max_blocks,
                                                  ctypes.byref(out)), None)
     return out.value
+
+
+def lm_head_indexed_workspace(ggml_type, n_embd, n_ids):
+    """Bytes of workspace cuca_hip_lm_head_indexed needs (host)."""
+    b = _sz(0)
+    _check(lib().cuca_hip_lm_head_indexed_workspace(ggml_type, n_embd, n_ids, ctypes.byref(b)))
+    return b.value
 
 
 def qweight_bytes(ggml_type, n, k):

@@ -52,6 +52,8 @@
  *   cuca_hip_moe_up/down_  the same as grouped GEMMs on   moe_kernel.rs:1163-1300
  *     qgemm                the matrix cores (prefill)
  *   cuca_hip_lm_head       head + cap_logits              cpu.rs:2588-2617
+ *   cuca_hip_lm_head_      head_indexed + cap_logits      cpu.rs:2603-2606,
+ *     indexed              (forward_indexed)              qmm.rs:1818-1843
  *   cuca_hip_argmax        greedy                         sampler.rs:44-56
  *   cuca_hip_top_k         select_top_k                   sampler.rs:254-286
  *
@@ -594,6 +596,23 @@ cuca_status cuca_hip_gemm_w16_glu(cuca_hip_ctx *ctx, const void *w16, int64_t ff
 cuca_status cuca_hip_lm_head(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type, int64_t vocab, int64_t n_embd,
                              const void *x, int64_t ldx, int64_t m, int64_t rows, float logit_scale,
                              float logit_mult, float softcap, void *logits, int64_t logits_ld, cuca_dtype dtype);
+
+/* The LM head over chosen vocabulary entries only (head_indexed,
+ * cpu.rs:2603-2606: QMatMul::forward_indexed, qmm.rs:1818-1843, then
+ * cap_logits): logits[t][j] is the full head's logit of entry ids[j] for
+ * row t -- the same bits as cuca_hip_lm_head's column ids[j] -- for
+ * j < n_ids (any order, repeats allowed).  ids: device u32 [n_ids].  The
+ * chosen packed rows are gathered into the workspace (device, 16-byte
+ * aligned, cuca_hip_lm_head_indexed_workspace bytes: n_ids packed rows)
+ * and run as a row prefix.  An id >= vocab is reported by
+ * cuca_hip_check_device ("weight row ... out of range", as the reference's
+ * error), its column then the logit of a zero row. */
+cuca_status cuca_hip_lm_head_indexed_workspace(uint32_t ggml_type, int64_t n_embd, int64_t n_ids, size_t *bytes);
+cuca_status cuca_hip_lm_head_indexed(cuca_hip_ctx *ctx, const void *w, uint32_t ggml_type, int64_t vocab,
+                                     int64_t n_embd, const void *x, int64_t ldx, int64_t m, const uint32_t *ids,
+                                     int64_t n_ids, float logit_scale, float logit_mult, float softcap,
+                                     void *workspace, size_t workspace_bytes, void *logits, int64_t logits_ld,
+                                     cuca_dtype dtype);
 
 /* Sampling's scans over the vocabulary on the device (sampler.rs), so a
  * step reads back an id or k candidates per row instead of the logits.

@@ -637,6 +637,32 @@ extern "C" {
         logits_ld: i64,
         dtype: cuca_dtype,
     ) -> cuca_status;
+    pub fn cuca_hip_lm_head_indexed_workspace(
+        ggml_type: u32,
+        n_embd: i64,
+        n_ids: i64,
+        bytes: *mut usize,
+    ) -> cuca_status;
+    pub fn cuca_hip_lm_head_indexed(
+        ctx: *mut cuca_hip_ctx,
+        w: *const c_void,
+        ggml_type: u32,
+        vocab: i64,
+        n_embd: i64,
+        x: *const c_void,
+        ldx: i64,
+        m: i64,
+        ids: *const u32,
+        n_ids: i64,
+        logit_scale: f32,
+        logit_mult: f32,
+        softcap: f32,
+        workspace: *mut c_void,
+        workspace_bytes: usize,
+        logits: *mut c_void,
+        logits_ld: i64,
+        dtype: cuca_dtype,
+    ) -> cuca_status;
     pub fn cuca_hip_sample_candidates(
         logits: *const f32,
         ids: *const u32,

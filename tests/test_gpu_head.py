@@ -171,3 +171,53 @@ def test_pick_errors(ctx):
         ctx.top_k(x.ptr, 10, 1, 10, hip.F32, 5, 0.0, o.ptr, i.ptr, c.ptr)
     with pytest.raises(hip.CucaError, match="logits shape"):
         ctx.argmax(x.ptr, 5, 1, 10, hip.F32, i.ptr)
+
+
+@pytest.mark.parametrize("qtype", ["q4_0", "q8_0"])
+@pytest.mark.parametrize("m,cap", [(1, 0.0), (3, 0.0), (2, 30.0)])
+def test_lm_head_indexed_is_the_full_heads_columns(ctx, qtype, m, cap):
+    """head_indexed (cpu.rs:2603-2606, QMatMul::forward_indexed qmm.rs:1818-1843):
+    the logits of chosen vocabulary ids, any order and repeats, bit for bit
+    the full head's columns (the same kernel per weight row)."""
+    rng = np.random.default_rng(m + int(cap))
+    vocab, k = 4100, 1024
+    T = W.GGML_ID[qtype]
+    raw = W.quant_table(rng, vocab, k, qtype, (0.01, 0.05))
+    w = ops.QmmWeight.from_raw(ctx, T, raw, vocab, k)
+    x = (rng.standard_normal((m, k)) * 4).astype(np.float32)
+    dx = ctx.array(x)
+    full = ctx.empty((m, vocab), np.float32)
+    ctx.lm_head(w.packed.ptr, T, vocab, k, dx.ptr, k, m, vocab, 1.0, 1.0, cap, full.ptr, vocab, hip.F32)
+    ids = np.concatenate([[vocab - 1, 0, 17, 17], rng.integers(0, vocab, 300)]).astype(np.uint32)
+    n = ids.size
+    wsb = hip.lm_head_indexed_workspace(T, k, n)
+    assert wsb == n * hip.qweight_bytes(T, 1, k)
+    ws = ctx.empty((wsb,), np.uint8)
+    out = ctx.empty((m, n + 3), np.float32)
+    ctx.lm_head_indexed(w.packed.ptr, T, vocab, k, dx.ptr, k, m, ctx.array(ids).ptr, n, 1.0, 1.0, cap, ws.ptr,
+                        wsb, out.ptr, n + 3, hip.F32)
+    ctx.check_device()
+    assert_bits_equal(out.numpy()[:, :n], full.numpy()[:, ids], "indexed head")
+    if cap == 0.0:
+        want = O.qmm(raw, T, vocab, k, x)[:, ids]
+        assert_bits_equal(out.numpy()[:, :n], want, "indexed head vs oracle")
+
+
+def test_lm_head_indexed_errors(ctx):
+    rng = np.random.default_rng(3)
+    vocab, k = 64, 256
+    raw = W.quant_table(rng, vocab, k, "q8_0", (0.01, 0.05))
+    w = ops.QmmWeight.from_raw(ctx, hip.GGML_Q8_0, raw, vocab, k)
+    dx = ctx.array(rng.standard_normal((1, k)).astype(np.float32))
+    ids = ctx.array(np.array([3, 64, 5], np.uint32))
+    wsb = hip.lm_head_indexed_workspace(hip.GGML_Q8_0, k, 3)
+    ws = ctx.empty((wsb,), np.uint8)
+    out = ctx.empty((1, 3), np.float32)
+    with pytest.raises(hip.CucaError, match="workspace of"):
+        ctx.lm_head_indexed(w.packed.ptr, hip.GGML_Q8_0, vocab, k, dx.ptr, k, 1, ids.ptr, 3, 1.0, 1.0, 0.0, ws.ptr,
+                            wsb - 16, out.ptr, 3, hip.F32)
+    ctx.lm_head_indexed(w.packed.ptr, hip.GGML_Q8_0, vocab, k, dx.ptr, k, 1, ids.ptr, 3, 1.0, 1.0, 0.0, ws.ptr,
+                        wsb, out.ptr, 3, hip.F32)
+    with pytest.raises(hip.CucaError, match="weight row 64 out of range"):
+        ctx.check_device()
+    assert out.numpy()[0, 1] == 0.0
