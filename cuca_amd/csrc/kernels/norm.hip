@@ -159,6 +159,43 @@ __device__ static inline void norm_body(const NormArgs &a) {
     }
 }
 
+// The prefill form of the plain residual step -- a branch, no sandwich,
+// rs = 1, weights, x' written, one chunk a thread covering the row -- with
+// nothing else in it: streaming loads of x and the branch issued
+// unconditionally (a row past the call reads row 0 and stores nothing),
+// the weights read after the sum.  The same arithmetic and order as
+// norm_body, so the same bits.  Measured on MI355X in the prefill steps
+// (median of three windows): config C at 4096 rows 0.703-0.704 -> 0.72-0.74
+// of the HBM peak, config E at 8192 rows 0.71-0.72 -> 0.725-0.73.
+template <typename T, int TPR, int RPB = 1>
+__device__ static inline void norm_plain_body(const NormArgs &a) {
+    constexpr int N = Chunk<T>::N;
+    constexpr int B = TPR > CUCA_WAVE ? TPR * RPB : CUCA_BLOCK;
+    __shared__ float red_main[TPR > CUCA_WAVE ? RPB * TPR / CUCA_WAVE : 1];
+    const int li = threadIdx.x & (TPR - 1);
+    const int64_t row = (int64_t)blockIdx.x * (B / TPR) + threadIdx.x / TPR;
+    const bool live = row < a.rows;
+    const int H = a.hidden; // = TPR * N (the host's choice)
+    const int64_t c = (live ? row * TPR : 0) + li;
+    float v[N], b[N];
+    load_chunk<T, true>(a.x, c, v);
+    load_chunk<T, true>(a.branch, c, b);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = Chunk<T>::as_stored(v[i] + b[i]);
+    if (live) Chunk<T>::store_nt(a.x_out, c, v);
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < N; i++) ss += v[i] * v[i];
+    ss = row_sum<TPR, RPB>(ss, red_main);
+    const float inv = 1.0f / sqrtf(ss / (float)H + a.eps);
+    if (!live) return;
+    float w[N], h[N];
+    load_w<N>(a.w, li, w);
+#pragma unroll
+    for (int i = 0; i < N; i++) h[i] = pin_f32(pin_f32(v[i] * inv) * w[i]);
+    Chunk<T>::store_nt(a.h_out, c, h);
+}
+
 template <typename T>
 __device__ static inline void norm_generic_body(const NormArgs &a) {
     __shared__ float red[16];
@@ -249,6 +286,16 @@ __device__ static inline void norm_generic_body(const NormArgs &a) {
 
 CUCA_NORM_SET(f32, float)
 CUCA_NORM_SET(f16, _Float16)
+#define CUCA_NORM_PLAIN(NAME, T, TPR, RPB)                                                 \
+    extern "C" __global__ __launch_bounds__(TPR * RPB) void NAME(NormArgs a) {             \
+        norm_plain_body<T, TPR, RPB>(a);                                                   \
+    }
+CUCA_NORM_PLAIN(cuca_norm_f32_t256_nts, float, 256, 2)
+CUCA_NORM_PLAIN(cuca_norm_f32_t512_nts, float, 512, 1)
+CUCA_NORM_PLAIN(cuca_norm_f32_t1024_nts, float, 1024, 1)
+CUCA_NORM_PLAIN(cuca_norm_f16_t256_nts, _Float16, 256, 2)
+CUCA_NORM_PLAIN(cuca_norm_f16_t512_nts, _Float16, 512, 1)
+CUCA_NORM_PLAIN(cuca_norm_f16_t1024_nts, _Float16, 1024, 1)
 // 8 chunks per thread: f32 rows of up to 32768 values fit in registers; f16
 // rows that wide would spill and take the generic kernel.
 CUCA_NORM(cuca_norm_f32_t1024_c8, float, 1024, 8, false)

@@ -669,7 +669,16 @@ cuca_status cuca_hip_add_rmsnorm(cuca_hip_ctx *ctx, const void *x, const void *b
     if (rows > 0x7fffffffll) return fail(ctx, CUCA_UNSUPPORTED, "too many rows (%lld)", (long long)rows);
     int tpr = 0, per = 0;
     const bool stream = (int64_t)(branch ? 2 : 1) * rows * hidden * (int64_t)es >= kStreamBytes;
-    const Kernel k = vec && norm_shape(nch, &tpr, &per) ? norm_kernel(f16, tpr, per, stream) : KERNEL_COUNT;
+    Kernel k = vec && norm_shape(nch, &tpr, &per) ? norm_kernel(f16, tpr, per, stream) : KERNEL_COUNT;
+    // the prefill form of the plain residual step (streamed, a branch and
+    // weights, no sandwich, rs 1, x' written, one chunk a thread over the
+    // whole row): the streamlined kernels, the same bits
+    if (k != KERNEL_COUNT && stream && per == 1 && nch == tpr && branch && w && !w_post && x_out &&
+        residual_scale == 1.0f && (tpr == 256 || tpr == 512 || tpr == 1024)) {
+        static const Kernel plain[2][3] = {{cuca_norm_f32_t256_nts, cuca_norm_f32_t512_nts, cuca_norm_f32_t1024_nts},
+                                           {cuca_norm_f16_t256_nts, cuca_norm_f16_t512_nts, cuca_norm_f16_t1024_nts}};
+        k = plain[f16][tpr == 256 ? 0 : tpr == 512 ? 1 : 2];
+    }
     if (k == KERNEL_COUNT)
         return launch(ctx, f16 ? cuca_norm_f16_generic : cuca_norm_f32_generic, (unsigned)rows, 256, 0, a);
     // (rows of 256 threads go two to a block: the _t256 kernels)

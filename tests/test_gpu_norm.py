@@ -8,7 +8,8 @@ A-E (1024, 4096, 3584, 2048), the QK-norm row width 128, short rows
 (several rows per wave), the Gemma sandwich, the residual scale, the
 weightless norm, in-place x' = x, empty and ragged row counts, the generic
 kernel (hidden not a multiple of the chunk, rows wider than the register
-kernel, misaligned buffers) and the full config C size on sampled rows.
+kernel, misaligned buffers), the full config C size on sampled rows and
+the streamlined prefill kernels (calls of 48 MiB or more in the plain form).
 """
 import numpy as np
 import pytest
@@ -166,3 +167,57 @@ def test_group_sum_matches_shfl_butterfly(ctx):
             assert_bits_equal(o[2 * gi], want, f"group_sum, groups of {g}")
     with pytest.raises(hip.CucaError, match="multiple of 256"):
         ctx.selftest_group_sum(dx.ptr, 100, out.ptr)
+
+
+def launched(ctx, call):
+    ctx.profile_start(16)
+    call()
+    return [k for k, _ in ctx.profile_stop()]
+
+
+@pytest.mark.parametrize("dtype,hidden,rows,kernel", [
+    ("f16", 2048, 6145, "cuca_norm_f16_t256_nts"), ("f32", 1024, 6145, "cuca_norm_f32_t256_nts"),
+    ("f16", 4096, 3073, "cuca_norm_f16_t512_nts"), ("f32", 2048, 3073, "cuca_norm_f32_t512_nts"),
+    ("f16", 8192, 1537, "cuca_norm_f16_t1024_nts"), ("f32", 4096, 1537, "cuca_norm_f32_t1024_nts")])
+def test_streamlined_prefill_kernels(ctx, dtype, hidden, rows, kernel):
+    """Calls of 48 MiB or more in the plain residual form (a branch, weights,
+    x' written, rs 1) take the streamlined kernels: the kernel named, x'
+    bit-exact, h against the oracle and bit-identical to the small-call
+    kernel's h on the same rows; an odd row count leaves the last block of
+    two 256-thread rows half empty.  Another residual scale stays on the
+    general streaming kernel."""
+    torch = pytest.importorskip("torch")
+    tdt = torch.float16 if dtype == "f16" else torch.float32
+    code = hip.F16 if dtype == "f16" else hip.F32
+    gen = torch.Generator(device="cuda").manual_seed(hidden + rows)
+    x = torch.randn((rows, hidden), device="cuda", generator=gen).to(tdt)
+    b = torch.randn((rows, hidden), device="cuda", generator=gen).to(tdt)
+    w = (1 + 0.02 * torch.randn(hidden, device="cuda", generator=gen)).float()
+    xo, h = torch.empty_like(x), torch.empty_like(x)
+    torch.cuda.synchronize()
+    names = launched(ctx, lambda: ctx.add_rmsnorm(x.data_ptr(), b.data_ptr(), w.data_ptr(), None, 1e-5,
+                                                  1e-5, 1.0, rows, hidden, xo.data_ptr(), h.data_ptr(), code))
+    assert names == [kernel], names
+    ctx.check_device()
+    # the small-call kernel on the first and last 33 rows
+    for lo in (0, rows - 33):
+        so, sh = torch.empty((33, hidden), dtype=tdt, device="cuda"), torch.empty((33, hidden), dtype=tdt,
+                                                                                  device="cuda")
+        ctx.add_rmsnorm(x[lo].data_ptr(), b[lo].data_ptr(), w.data_ptr(), None, 1e-5, 1e-5, 1.0, 33, hidden,
+                        so.data_ptr(), sh.data_ptr(), code)
+        ctx.sync()
+        assert_bits_equal(xo[lo:lo + 33].cpu().numpy(), so.cpu().numpy(), "x' vs small call")
+        assert_bits_equal(h[lo:lo + 33].cpu().numpy(), sh.cpu().numpy(), "h vs small call")
+    sample = torch.from_numpy(np.unique(np.concatenate(
+        [[0, 1, rows - 2, rows - 1], np.random.default_rng(rows).integers(0, rows, 60)]))).cuda()
+    wx, wh = O.add_rmsnorm(x[sample].cpu().numpy(), b[sample].cpu().numpy(), w.cpu().numpy(), 1e-5)
+    assert_bits_equal(xo[sample].cpu().numpy(), wx, "x'")
+    assert_close(h[sample].cpu().numpy(), wh, what="h")
+    names = launched(ctx, lambda: ctx.add_rmsnorm(x.data_ptr(), b.data_ptr(), w.data_ptr(), None, 1e-5,
+                                                  1e-5, 0.5, rows, hidden, xo.data_ptr(), h.data_ptr(), code))
+    assert names == [kernel[:-1]], names
+    ctx.check_device()
+    wx, wh = O.add_rmsnorm(x[sample].cpu().numpy(), b[sample].cpu().numpy(), w.cpu().numpy(), 1e-5,
+                           residual_scale=0.5)
+    assert_bits_equal(xo[sample].cpu().numpy(), wx, "scaled x'")
+    assert_close(h[sample].cpu().numpy(), wh, what="scaled h")

@@ -5,7 +5,8 @@ At this size the calls cross the streaming threshold (48 MiB of input), so
 they run the nontemporal kernels that the smaller tests never reach.  Each
 test names the kernel it means to cover and checks, from the C ABI's
 per-kernel profile, that the call launched exactly that kernel:
-  add_rmsnorm, H 2048: 2 x 8192 x 2048 f16 in = 64 MiB -> cuca_norm_f16_t256_nt
+  add_rmsnorm, H 2048: 2 x 8192 x 2048 f16 in = 64 MiB -> cuca_norm_f16_t256_nts
+    (the streamlined prefill form: a branch, weights, x' written, rs 1)
   QK-norm RoPE, Q 32 + K 4 heads x 128: 72 MiB  -> cuca_rope_f16_neox_qkn_nt_h2 (two heads per lane)
   the same + the paged K/V store (V 4 heads): 80 MiB -> cuca_rope_f16_neox_qkn_kv_nt_h2
   the SwiGLU over the 65536 expert-grouped rows of width 768 (Zipf(1.1)
@@ -56,7 +57,7 @@ def test_norm_streaming_kernel_at_8192_tokens(ctx, torch):
     torch.cuda.synchronize()
     names = launched(ctx, lambda: ctx.add_rmsnorm(x.data_ptr(), b.data_ptr(), w.data_ptr(), None, eps,
                                                   eps, 1.0, N, H, xo.data_ptr(), h.data_ptr(), hip.F16))
-    assert names == ["cuca_norm_f16_t256_nt"], names
+    assert names == ["cuca_norm_f16_t256_nts"], names
     ctx.check_device()
     st = torch.from_numpy(sample(N, 41)).cuda()
     wx, wh = O.add_rmsnorm(x[st].cpu().numpy(), b[st].cpu().numpy(), w.cpu().numpy(), eps)
