@@ -9,14 +9,19 @@
 // keys, the values a pool of their own.  The pools are [n_blocks, n_kv, 16,
 // d], read in place through the table (no gather copy).
 //
-// Matrix-core kernel: a workgroup per (16 query rows, KV head), one wave per
-// query head of the GQA group (G waves).  Per 16-position block of the
-// table (the paged block), the workgroup stages the block's K rows and V
-// rows in LDS, and every wave computes the block's scores transposed, S^T =
-// K Q^T (16 keys x 16 rows, MFMA), so that a lane holds four keys of ONE
-// query row: the row's softmax statistics are per lane, reduced over four
-// lanes, and S^T is already the P^T operand of O^T = V^T P^T (d x 16 rows,
-// MFMA), whose lane holds four consecutive output columns of its row.
+// Matrix-core kernel: a workgroup per (RT tiles of 16 query rows, KV head),
+// one wave per (query head of the GQA group, row tile): G RT waves, with RT
+// = 4 for groups of 1 and 2 and 8 / G above (8 waves a workgroup from
+// groups of 2 on).  Per 16-position block of the table (the paged block),
+// the workgroup stages the block's K rows and V rows in LDS once for all
+// its waves -- double-buffered: the next block's loads are in flight while
+// the current one computes -- and every wave computes the block's scores
+// transposed, S^T = K Q^T (16 keys x 16 rows, MFMA), so that a lane holds
+// four keys of ONE query row: the row's softmax statistics are per lane,
+// reduced over four lanes, and S^T is already the P^T operand of O^T =
+// V^T P^T (d x 16 rows, MFMA), whose lane holds four consecutive output
+// columns of its row.  The exponentials are base 2, the scale folded with
+// log2(e) into the scores.
 // - f16 pools: v_mfma_f32_16x16x16f16; the score products are exact, their
 //   sums f32.  The probabilities enter the value product as two f16 parts,
 //   p = hi + lo / 2048 (hi = f16(p), lo = f16((p - hi) 2048)), into two
