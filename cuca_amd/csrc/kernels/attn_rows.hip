@@ -60,7 +60,14 @@ __device__ static inline void attn_rows_body(const AttnRowsArgs &a) {
     constexpr int W = G * RT;                  // waves: (query head, row tile)
     constexpr int NT = 64 * W;                 // threads
     constexpr int NS = D / 16;                 // output column slices
-    constexpr int KST = F16 ? D + 16 : D + 4;  // K row stride in LDS (elements)
+    // K row stride in LDS (elements): rows 8 bytes (f16) or 16 bytes (f32)
+    // past a multiple of 128, so the 16 rows of a score fragment, read 8
+    // bytes a lane, start on 16 different bank pairs.  (At D + 16 the f16
+    // rows started 8 banks apart and four rows shared each bank pair: 53 % of
+    // the kernel's LDS cycles were bank conflicts, SQ_LDS_BANK_CONFLICT /
+    // SQ_LDS_IDX_ACTIVE.)  Staged with 8-byte writes (f16 rows are 8-byte
+    // aligned).
+    constexpr int KST = D + 4;
     constexpr int VT = 20;                     // f16: V^T [D][16 keys + 4 padding]
     constexpr int VST = D + 4;                 // f32: V [16][D + 4]
     constexpr int KSZ = 16 * KST, VSZ = F16 ? D * VT : 16 * VST;
@@ -187,7 +194,13 @@ __device__ static inline void attn_rows_body(const AttnRowsArgs &a) {
                     if (2 * CH % NT == 0 || c < 2 * CH) {
                         if (c < CH) {
                             const int key = c / CPR, col = (c - key * CPR) * (16 / (int)sizeof(T));
-                            *reinterpret_cast<u32x4 *>(&ks[buf][i][key * KST + col]) = pre[i][t];
+                            if constexpr (F16) {
+                                uint2 *kd = reinterpret_cast<uint2 *>(&ks[buf][i][key * KST + col]);
+                                kd[0] = uint2{pre[i][t].x, pre[i][t].y};
+                                kd[1] = uint2{pre[i][t].z, pre[i][t].w};
+                            } else {
+                                *reinterpret_cast<u32x4 *>(&ks[buf][i][key * KST + col]) = pre[i][t];
+                            }
                         } else if constexpr (F16) {
                             // the low halves are column 2 dp of the 4 keys, the high halves 2 dp + 1
                             const int u = c - CH, kq = u & 3, dp = u >> 2;
