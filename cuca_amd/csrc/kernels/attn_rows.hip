@@ -82,6 +82,12 @@ __device__ static inline void attn_rows_body(const AttnRowsArgs &a) {
     __shared__ __align__(16) T ks[2][SB][KSZ];
     __shared__ __align__(16) T vs[2][SB][VSZ];
     __shared__ int span[2][RT];
+    // The f16 kernels under the 128-register cap keep each wave's query rows
+    // in LDS (read back per block, rows padded as K's), which frees the
+    // registers of the loads two blocks ahead.
+    constexpr bool QL = F16 && D <= 128 && G >= 2;
+    constexpr int QST = D + 4;
+    __shared__ __align__(16) T qs[QL ? W : 1][QL ? 16 * QST : 1];
     // a launch of another shape would leave row tiles' spans unwritten (they
     // bound the block loop and index the table): do nothing
     if (blockDim.x != NT) return;
@@ -130,6 +136,10 @@ __device__ static inline void attn_rows_body(const AttnRowsArgs &a) {
             if constexpr (F16) qh[j] = *reinterpret_cast<const attn_h4 *>(qrow + 16 * j + 4 * grp);
             else qf[j] = (float)qrow[4 * j + grp];
         }
+        if constexpr (QL) { // (read after the barrier that follows the first blocks' staging)
+#pragma unroll
+            for (int j = 0; j < QN; j++) *reinterpret_cast<attn_h4 *>(&qs[wave][r * QST + 16 * j + 4 * grp]) = qh[j];
+        }
     }
     f32x4 acc[NS], acl[F16 ? NS : 1];
 #pragma unroll
@@ -158,12 +168,21 @@ __device__ static inline void attn_rows_body(const AttnRowsArgs &a) {
         // a thread's chunks of a block: c < CH of K (16 bytes along a row),
         // the rest of V: f16, 4 keys x 2 columns (four dwords down the rows,
         // written to the transposed tile as two 8-byte pieces); f32, 16
-        // bytes of a row, keys fastest
-        u32x4 pre[SB][LPT];
-        auto fetch = [&](int bs) {
+        // bytes of a row, keys fastest.  Two register slots: the blocks are
+        // loaded two iterations before they are computed (one before they
+        // are staged into LDS).  With the loads one iteration ahead, every
+        // iteration waited for a block's memory latency: config C's causal
+        // attention of 4096 f16 rows spent about 5000 cycles an iteration,
+        // its matrix cores and LDS each busy under a fifth of the time.
+        // okb: the slot's blocks exist in the pool (taken when the block is
+        // loaded, while the table window holds its entry).
+        u32x4 pre[2][SB][LPT];
+        bool okb[2][SB];
+        auto fetch = [&](int bs, int slot) {
 #pragma unroll
             for (int i = 0; i < SB; i++) {
                 const uint32_t blk = blk_of(bs + i);
+                okb[slot][i] = (int64_t)blk < a.n_blocks;
                 const int64_t base = ((int64_t)((int64_t)blk < a.n_blocks ? blk : 0u) * a.n_kv + kvh) * 16 * D;
 #pragma unroll
                 for (int t = 0; t < LPT; t++) {
@@ -171,21 +190,21 @@ __device__ static inline void attn_rows_body(const AttnRowsArgs &a) {
                     if (2 * CH % NT == 0 || c < 2 * CH) {
                         if (c < CH) {
                             const int key = c / CPR, col = (c - key * CPR) * (16 / (int)sizeof(T));
-                            pre[i][t] = *reinterpret_cast<const u32x4 *>(pk + base + key * D + col);
+                            pre[slot][i][t] = *reinterpret_cast<const u32x4 *>(pk + base + key * D + col);
                         } else if constexpr (F16) {
                             // 4 keys x 2 columns: the dwords of columns 2 dp, 2 dp + 1 of rows 4 kq .. + 3
                             const int u = c - CH, kq = u & 3, dp = u >> 2;
                             const uint32_t *vr = reinterpret_cast<const uint32_t *>(pv + base + 4 * kq * D + 2 * dp);
-                            pre[i][t] = u32x4{vr[0], vr[D / 2], vr[D], vr[3 * D / 2]};
+                            pre[slot][i][t] = u32x4{vr[0], vr[D / 2], vr[D], vr[3 * D / 2]};
                         } else {
                             const int key = (c - CH) & 15, col = ((c - CH) >> 4) * 4;
-                            pre[i][t] = *reinterpret_cast<const u32x4 *>(pv + base + key * D + col);
+                            pre[slot][i][t] = *reinterpret_cast<const u32x4 *>(pv + base + key * D + col);
                         }
                     }
                 }
             }
         };
-        auto stage = [&](int buf) {
+        auto stage = [&](int buf, int slot) {
 #pragma unroll
             for (int i = 0; i < SB; i++) {
 #pragma unroll
@@ -196,36 +215,38 @@ __device__ static inline void attn_rows_body(const AttnRowsArgs &a) {
                             const int key = c / CPR, col = (c - key * CPR) * (16 / (int)sizeof(T));
                             if constexpr (F16) {
                                 uint2 *kd = reinterpret_cast<uint2 *>(&ks[buf][i][key * KST + col]);
-                                kd[0] = uint2{pre[i][t].x, pre[i][t].y};
-                                kd[1] = uint2{pre[i][t].z, pre[i][t].w};
+                                kd[0] = uint2{pre[slot][i][t].x, pre[slot][i][t].y};
+                                kd[1] = uint2{pre[slot][i][t].z, pre[slot][i][t].w};
                             } else {
-                                *reinterpret_cast<u32x4 *>(&ks[buf][i][key * KST + col]) = pre[i][t];
+                                *reinterpret_cast<u32x4 *>(&ks[buf][i][key * KST + col]) = pre[slot][i][t];
                             }
                         } else if constexpr (F16) {
                             // the low halves are column 2 dp of the 4 keys, the high halves 2 dp + 1
                             const int u = c - CH, kq = u & 3, dp = u >> 2;
-                            const u32x4 w = pre[i][t];
+                            const u32x4 w = pre[slot][i][t];
                             const uint2 lo2 = {(w.x & 0xffffu) | (w.y << 16), (w.z & 0xffffu) | (w.w << 16)};
                             const uint2 hi2 = {(w.x >> 16) | (w.y & 0xffff0000u), (w.z >> 16) | (w.w & 0xffff0000u)};
                             *reinterpret_cast<uint2 *>(&vs[buf][i][(2 * dp) * VT + 4 * kq]) = lo2;
                             *reinterpret_cast<uint2 *>(&vs[buf][i][(2 * dp + 1) * VT + 4 * kq]) = hi2;
                         } else {
                             const int key = (c - CH) & 15, col = ((c - CH) >> 4) * 4;
-                            *reinterpret_cast<u32x4 *>(&vs[buf][i][key * VST + col]) = pre[i][t];
+                            *reinterpret_cast<u32x4 *>(&vs[buf][i][key * VST + col]) = pre[slot][i][t];
                         }
                     }
                 }
             }
         };
-        load_tab(0);
-        fetch(b0);
-        stage(0);
-        __syncthreads();
-        for (int bs = b0; bs <= b1; bs += SB) {
-            const int buf = ((bs - b0) / SB) & 1;
-            const bool more = bs + SB <= b1;
-            if (more && ((bs + SB - b0) & 63) == 0) load_tab((bs + SB - b0) >> 6);
-            if (more) fetch(bs + SB); // the next blocks' loads, in flight during these
+        // one iteration: blocks bs (register slot `slot`, LDS buffer `buf`)
+        // computed, bs + SB staged from the other slot into the other
+        // buffer, bs + 2 SB loaded into this slot (block k in slot k % 2,
+        // buffer k % 2; the slot is free once its blocks are staged)
+        auto iter = [&](int bs, int slot, int buf) {
+            const bool more = bs + SB <= b1, more2 = bs + 2 * SB <= b1;
+            bool okc[SB];
+#pragma unroll
+            for (int i = 0; i < SB; i++) okc[i] = okb[slot][i];
+            if (more2 && ((bs + 2 * SB - b0) & 63) == 0) load_tab((bs + 2 * SB - b0) >> 6);
+            if (more2) fetch(bs + 2 * SB, slot); // in flight during this and the next iteration
             // scores: lane (r, grp) gets keys 4 grp + i of each block with row r
             float x[SB][4];
             bool in[SB][4];
@@ -233,7 +254,7 @@ __device__ static inline void attn_rows_body(const AttnRowsArgs &a) {
 #pragma unroll
             for (int sb = 0; sb < SB; sb++) {
                 const int b = bs + sb;
-                if (b <= b1 && (int64_t)blk_of(b) >= a.n_blocks && valid && rows_meets(lo, hi, b)) {
+                if (b <= b1 && !okc[sb] && valid && rows_meets(lo, hi, b)) {
                     bad = true;
                     if (kvh == 0 && g == 0 && grp == 0)
                         record_bad(a.status + CUCA_STATUS_KV_RANGE, (uint32_t)row, (uint32_t)max(16 * b, lo));
@@ -244,7 +265,9 @@ __device__ static inline void attn_rows_body(const AttnRowsArgs &a) {
 #pragma unroll
                     for (int j = 0; j < NS; j++) {
                         const attn_h4 kk = *reinterpret_cast<const attn_h4 *>(kt + r * KST + 16 * j + 4 * grp);
-                        st = __builtin_amdgcn_mfma_f32_16x16x16f16(kk, qh[j], st, 0, 0, 0);
+                        const attn_h4 qq =
+                            QL ? *reinterpret_cast<const attn_h4 *>(&qs[wave][r * QST + 16 * j + 4 * grp]) : qh[j];
+                        st = __builtin_amdgcn_mfma_f32_16x16x16f16(kk, qq, st, 0, 0, 0);
                     }
                 } else {
 #pragma unroll
@@ -308,10 +331,19 @@ __device__ static inline void attn_rows_body(const AttnRowsArgs &a) {
             es += __shfl_xor(es, 16);
             es += __shfl_xor(es, 32);
             l += es;
-            if (more) stage(buf ^ 1);
+            if (more) stage(buf ^ 1, slot ^ 1);
             // the next blocks' tiles are in place, and every wave is done
             // with these before the blocks after overwrite them
             __syncthreads();
+        };
+        load_tab(0);
+        fetch(b0, 0);
+        if (b0 + SB <= b1) fetch(b0 + SB, 1); // (within the first table window: SB < 64)
+        stage(0, 0);
+        __syncthreads();
+        for (int bs = b0; bs <= b1; bs += 2 * SB) {
+            iter(bs, 0, 0);
+            if (bs + SB <= b1) iter(bs + SB, 1, 1);
         }
     }
     if (!in_call) return;
