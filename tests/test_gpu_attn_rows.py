@@ -15,7 +15,8 @@ blocks before it, partial tiles of 16 rows, the configs' head layouts
 (matrix-core kernels: head_dim 64/128/256, groups 1-8, f32 and f16), shapes
 that take the generic kernel (head_dim 48, group 3, a q row stride the
 matrix-core loads cannot take), a row's bits alone and in its chunk, bad
-ranges and blocks (zero rows, reported), the latent form (head_dim 576,
+ranges and blocks (zero rows, reported; a missing block at the end of
+the kernel's first 64-entry table window), the latent form (head_dim 576,
 v_width 512 of DeepSeek-style caches, and a small one), and host checks.
 """
 import numpy as np
@@ -158,6 +159,34 @@ def test_bad_ranges_and_blocks_give_zero_rows_and_are_reported(ctx, nq, nk, d):
     good = [r for r in range(20) if r != 17]
     want = want_rows(q[good], pk, pk, table, ranges[good], 0.1)
     assert_close(got[good], want, floor=floor_of(table, ranges[good], pk, nq), what="good rows")
+
+
+@pytest.mark.parametrize("dtype", ["f16", "f32"])
+def test_a_missing_block_past_the_first_table_window_is_reported(ctx, dtype):
+    """Rows over more than 64 blocks (the kernel holds the table 64 entries
+    at a time): block 63, the last of the first window, is outside the pool.
+    The rows whose range meets it are zero and reported; the rows of the same
+    workgroup whose range starts after it match the oracle."""
+    rng = np.random.default_rng(21)
+    nq, nk, d, n_blocks = 32, 8, 128, 150
+    table = rng.choice(n_blocks, 130, replace=False).astype(np.uint32)
+    table[63] = 200                                  # outside the pool of 150
+    pk = rng.standard_normal((n_blocks, nk, 16, d)).astype(NP[dtype])
+    pv = rng.standard_normal((n_blocks, nk, 16, d)).astype(NP[dtype])
+    q = rng.standard_normal((32, nq, d)).astype(NP[dtype])
+    pos = 1100 + np.arange(32)
+    ranges = np.stack([np.where(np.arange(32) < 16, 0, 1024), pos + 1], 1).astype(np.int32)
+    dq, dk, dv = ctx.array(q.reshape(32, -1)), ctx.array(pk), ctx.array(pv)
+    dt, dr = ctx.array(table), ctx.array(ranges)
+    out = ctx.empty((32, nq, d), NP[dtype])
+    ctx.attend_rows(dq.ptr, nq * d, dk.ptr, dv.ptr, n_blocks, dt.ptr, len(table), dr.ptr, 32, nq, nk, d, 0.1,
+                    out.ptr, nq * d, hip.dtype_code(NP[dtype]))
+    with pytest.raises(hip.CucaError, match=r"attention row \d+: position 1008 has no K/V block"):
+        ctx.check_device()
+    got = out.numpy()
+    assert not np.any(got[:16]), "rows over the missing block are not zero"
+    want = want_rows(q[16:], pk, pv, table, ranges[16:], 0.1)
+    assert_close(got[16:], want, floor=floor_of(table, ranges[16:], pv, nq), what="rows after the block")
 
 
 @pytest.mark.parametrize("dtype", ["f32", "f16"])
