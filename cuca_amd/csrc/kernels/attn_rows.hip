@@ -285,7 +285,14 @@ __device__ static inline void attn_rows_body(const AttnRowsArgs &a) {
             }
             bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
             bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
-            if (bmax > m) { // rescale what was accumulated under the old maximum
+            // Rescale what was accumulated under the old maximum only when the
+            // block's maximum exceeds it by more than 8 (base 2): the weights
+            // are then at most 2^8, which f16 holds with room (the hi part up
+            // to 256, the lo part (p - hi) 2048 up to 256), and the f32 sums
+            // too.  Rescaling at every new maximum ran most blocks' 64
+            // accumulator multiplies; config C's causal attention of 4096
+            // f16 rows 605 -> 551 us.
+            if (bmax > m + 8.0f) {
                 const float corr = __builtin_amdgcn_exp2f(m - bmax);
                 l *= corr;
 #pragma unroll
