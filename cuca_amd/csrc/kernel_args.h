@@ -80,6 +80,7 @@ typedef struct {
     int32_t n_experts;
     float clamp;            /* > 0: clamp gate from above, up to +-clamp   */
 } GluArgs;
+#define CUCA_GLU_NT_BLOCK 64 /* threads of a streaming (_nt) GLU workgroup */
 
 typedef struct {
     void *q;                /* [rows, nq, d] with row stride q_ld           */

@@ -7,8 +7,12 @@
 //
 // Elementwise and HBM-bound: each lane reads one 16-byte chunk of gate and
 // of up and writes one chunk of out, so each tensor crosses HBM once.  One
-// workgroup covers CUCA_BLOCK chunks of one row (row = blockIdx / blocks per
-// row), so strided rows -- the fused [gate | up] projection -- need no copy.
+// workgroup covers BT chunks of one row (row = blockIdx / blocks per row), so
+// strided rows -- the fused [gate | up] projection -- need no copy.  The
+// streaming kernels run one wave per workgroup (BT = 64): at 16384 x 14336
+// f16 that is 208 us against 218 us with four waves, the same bits -- a
+// one-wave group retires as soon as its own loads land, so the CU takes new
+// work without waiting for a group's slowest wave.
 //
 // The activation is evaluated with the hardware transcendental unit,
 // keeping the ALU work well under the memory time:
@@ -53,7 +57,7 @@ template <int ACT> __device__ static inline float act_fn(float g) {
     return ACT == 0 ? act_silu(g) : act_gelu_tanh(g);
 }
 
-template <typename T, int ACT, bool RAGGED, bool NTL>
+template <typename T, int ACT, bool RAGGED, bool NTL, int BT = CUCA_BLOCK>
 __device__ static inline void glu_body(const GluArgs &a) {
     constexpr int N = Chunk<T>::N;
     const uint32_t bpr = (uint32_t)a.blocks_per_row;
@@ -66,7 +70,7 @@ __device__ static inline void glu_body(const GluArgs &a) {
     }
     if ((int64_t)row >= nrows) return;
     const int cpr = a.ff / N;
-    const int c = (int)cblk * CUCA_BLOCK + (int)threadIdx.x;
+    const int c = (int)cblk * BT + (int)threadIdx.x;
     if (c >= cpr) return;
     float g[N], u[N], o[N];
     load_chunk<T, NTL>(reinterpret_cast<const T *>(a.gate) + (int64_t)row * a.gate_ld, c, g);
@@ -108,12 +112,16 @@ __device__ static inline void glu_generic_body(const GluArgs &a) {
     extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void NAME(GluArgs a) {             \
         BODY<__VA_ARGS__>(a);                                                              \
     }
+#define CUCA_GLU_W(NAME, BODY, ...)                                                        \
+    extern "C" __global__ __launch_bounds__(CUCA_GLU_NT_BLOCK) void NAME(GluArgs a) {      \
+        BODY<__VA_ARGS__, CUCA_GLU_NT_BLOCK>(a);                                           \
+    }
 // "nt" variants stream gate and up (inputs larger than the last-level cache).
 #define CUCA_GLU_SET(TN, T)                                                                \
     CUCA_GLU(cuca_glu_##TN##_silu, glu_body, T, 0, false, false)                           \
     CUCA_GLU(cuca_glu_##TN##_gelu, glu_body, T, 1, false, false)                           \
-    CUCA_GLU(cuca_glu_##TN##_silu_nt, glu_body, T, 0, false, true)                         \
-    CUCA_GLU(cuca_glu_##TN##_gelu_nt, glu_body, T, 1, false, true)                         \
+    CUCA_GLU_W(cuca_glu_##TN##_silu_nt, glu_body, T, 0, false, true)                       \
+    CUCA_GLU_W(cuca_glu_##TN##_gelu_nt, glu_body, T, 1, false, true)                       \
     CUCA_GLU(cuca_glu_##TN##_silu_ragged, glu_body, T, 0, true, false)                     \
     CUCA_GLU(cuca_glu_##TN##_gelu_ragged, glu_body, T, 1, true, false)                     \
     CUCA_GLU(cuca_glu_##TN##_silu_generic, glu_generic_body, T, 0, false)                  \

@@ -736,10 +736,11 @@ static cuca_status glu_common(cuca_hip_ctx *ctx, const void *gate, int64_t gate_
         if (ragged)
             k = f16 ? (gelu ? cuca_glu_f16_gelu_ragged : cuca_glu_f16_silu_ragged)
                     : (gelu ? cuca_glu_f32_gelu_ragged : cuca_glu_f32_silu_ragged);
-        else if (stream)
+        else if (stream) {
             k = f16 ? (gelu ? cuca_glu_f16_gelu_nt : cuca_glu_f16_silu_nt)
                     : (gelu ? cuca_glu_f32_gelu_nt : cuca_glu_f32_silu_nt);
-        else
+            bpr = (ff / N + CUCA_GLU_NT_BLOCK - 1) / CUCA_GLU_NT_BLOCK;
+        } else
             k = f16 ? (gelu ? cuca_glu_f16_gelu : cuca_glu_f16_silu)
                     : (gelu ? cuca_glu_f32_gelu : cuca_glu_f32_silu);
     } else {
@@ -763,7 +764,7 @@ static cuca_status glu_common(cuca_hip_ctx *ctx, const void *gate, int64_t gate_
     a.blocks_per_row = (int32_t)bpr;
     a.n_experts = n_experts;
     a.clamp = clamp > 0.0f ? clamp : 0.0f;
-    return launch(ctx, k, (unsigned)(rows * bpr), 256, 0, a);
+    return launch(ctx, k, (unsigned)(rows * bpr), vec && stream ? CUCA_GLU_NT_BLOCK : 256, 0, a);
 }
 
 cuca_status cuca_hip_glu(cuca_hip_ctx *ctx, const void *gate, int64_t gate_ld, const void *up,
