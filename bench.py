@@ -1121,10 +1121,11 @@ def prefill_layer_bench(ctx, torch, name="C", n=4096, reps=5):
 
 def gemm_w16_bench(ctx, torch, reps=10):
     """The dense f16 path for many rows (cuca_hip_qweight_dequant once, then
-    cuca_hip_gemm_w16 / _gemm_w16_glu per call: hipBLASLt's f16 GEMM, f32
-    accumulation) at the 8B layer shapes, 512 and 4096 rows of f32
-    activations: time of the whole call on the stream (the f16 rounding of
-    the activations, the GEMM, the GLU epilogue), its f16 TFLOP/s against
+    cuca_hip_gemm_w16 / _gemm_w16_glu per call: the library's f16 GEMM on
+    the matrix cores, f32 accumulation, the GLU in registers) at the 8B
+    layer shapes, 512 and 4096 rows of f32 activations and 4096 of f16: time
+    of the whole call on the stream (the f16 rounding of f32 activations
+    and the GEMM), its f16 TFLOP/s against
     the 2.5 PFLOP/s dense peak, and the one-time dequantisation.  Sampled
     outputs are checked against the f64 product within the qgemm bound."""
     import numpy as np

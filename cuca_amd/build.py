@@ -130,7 +130,7 @@ def build(verbose: bool = False) -> str:
           "-D__HIP_PLATFORM_AMD__", f"-DCUCA_CODE_OBJECT=\"{CODE_OBJECT}\"",
           f"-I{os.path.join(ROOT, 'include')}", f"-I{CSRC}", f"-I{ROCM}/include",
           os.path.join(CSRC, "runtime.cpp"), noalloc_obj, "-o", lib_tmp,
-          f"-L{ROCM}/lib", "-lamdhip64", "-lhipblaslt", f"-Wl,-rpath,{ROCM}/lib",
+          f"-L{ROCM}/lib", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib",
           "-Wl,--no-undefined"], verbose)
     os.replace(lib_tmp, LIB)
     return LIB

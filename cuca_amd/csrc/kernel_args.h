@@ -259,10 +259,9 @@ typedef struct {
     int32_t n_experts, max_pairs, tm, moe_up;
 } QGemmArgs;
 
-/* The dense f16 path (qgemm.hip): cuca_qdequant_* (packed w [n][ng][GB],
- * row_bytes each -> out f16 [n][out_ld]), cuca_cvt_f16_f32 (x [m][ldx] f32
- * -> out f16 [m][out_ld], k values a row) and cuca_gemm_glu_epi_* (x = the
- * GEMM's f32 rows [m][ldx] holding gate[n] then up[n] -> out [m][out_ld]). */
+/* The dense f16 path's conversions (qgemm.hip): cuca_qdequant_* (packed w
+ * [n][ng][GB], row_bytes each -> out f16 [n][out_ld]) and cuca_cvt_f16_f32
+ * (x [m][ldx] f32 -> out f16 [m][out_ld], k values a row). */
 typedef struct {
     const uint8_t *w;
     const void *x;
@@ -273,6 +272,29 @@ typedef struct {
     float clamp;
     int32_t pad_;
 } QDequantArgs;
+
+/* The dense f16 GEMM (gemm16.hip): out [m][out_ld] = x [m][ldx] . w^T over
+ * f16 weight rows [.][ldw]; the GLU form reads gate rows from 0 and up rows
+ * from up_row and writes act(gate) * up.  Tiles of 256 (GLU 128) output
+ * columns x 256 rows; k a multiple of 32; ldw, ldx < 2^22. */
+typedef struct {
+    const void *w;
+    const void *x;
+    void *out;
+    int64_t ldw, ldx, out_ld;
+    int64_t up_row;
+    int32_t n, m, k;        /* output columns, rows, k                      */
+    int32_t n_tn, n_tm, gn; /* column tiles, row tiles, tile-order group    */
+    int32_t vec;            /* out_ld % 4 == 0: four-column stores          */
+    float clamp;            /* GLU: > 0 clamps gate from above, up to +-    */
+    /* split k (grid y = splits): k is then the length of one split, and
+     * split s takes k values from s k on and writes its sums to output
+     * matrix s (out + s m out_ld).  cuca_gemm16_reduce_* adds the splits'
+     * part [splits][m][n or 2 n] in order and applies the output (n, out,
+     * out_ld, clamp as for the GEMM). */
+    float *part;
+    int32_t splits, pad_;
+} Gemm16Args;
 
 /* Activation quantisation for the decode GEMV (Acts::new, qmm.rs:1272-1343):
  * x [m][ldx] -> quants [m][q_ld] int8 (element order) and scales [m][nb]. */

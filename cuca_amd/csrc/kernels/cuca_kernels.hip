@@ -15,4 +15,5 @@
 #include "qmv.hip"
 #include "qmd.hip"
 #include "qgemm.hip"
+#include "gemm16.hip"
 #include "attn_rows.hip"

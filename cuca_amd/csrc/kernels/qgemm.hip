@@ -551,48 +551,3 @@ extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void cuca_cvt_f16_f32(QDequa
     for (int i = 0; i < 8; i++) h[i] = (_Float16)v[i];
     *reinterpret_cast<f16x8 *>(reinterpret_cast<_Float16 *>(a.out) + r * a.out_ld + c) = h;
 }
-
-// The GLU after the dense GEMM: y [m][2 ff] f32 (gate columns, then up),
-// out = act(gate) * up with Glu::apply's clamp -- qgemm's epilogue.  Four
-// columns per thread (16-byte loads of gate and up) when ff and out_ld are
-// multiples of 4; one otherwise.
-__device__ static inline float glu_epi_one(float g, float u, float clamp, int act) {
-    if (clamp > 0.0f) { // Glu::apply's clamp (cpu.rs:364-368)
-        g = fminf(g, clamp);
-        u = fminf(fmaxf(u, -clamp), clamp);
-    }
-    return pin_f32((act == 0 ? act_silu(g) : act_gelu_tanh(g)) * u);
-}
-template <typename T, int ACT, int V> __device__ static inline void gemm_glu_epi_body(const QDequantArgs &a) {
-    const int64_t e = ((int64_t)blockIdx.x * CUCA_BLOCK + threadIdx.x) * V;
-    if (e >= (int64_t)a.m * a.n) return;
-    const int64_t tok = e / a.n, c = e - tok * a.n;
-    const float *y = reinterpret_cast<const float *>(a.x) + tok * a.ldx;
-    T *o = reinterpret_cast<T *>(a.out) + tok * a.out_ld + c;
-    if constexpr (V == 4) {
-        const f32x4 g = *reinterpret_cast<const f32x4 *>(y + c);
-        const f32x4 u = *reinterpret_cast<const f32x4 *>(y + a.n + c);
-        float r[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) r[i] = glu_epi_one(g[i], u[i], a.clamp, ACT);
-        if constexpr (sizeof(T) == 4) {
-            *reinterpret_cast<f32x4 *>(o) = f32x4{r[0], r[1], r[2], r[3]};
-        } else {
-            typedef _Float16 h4 __attribute__((ext_vector_type(4)));
-            *reinterpret_cast<h4 *>(o) = h4{(_Float16)r[0], (_Float16)r[1], (_Float16)r[2], (_Float16)r[3]};
-        }
-    } else {
-        o[0] = (T)glu_epi_one(y[c], y[a.n + c], a.clamp, ACT);
-    }
-}
-#define CUCA_GLU_EPI(TN, T, AN, ACT)                                                       \
-    extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void cuca_gemm_glu_epi_##TN##_##AN(QDequantArgs a) { \
-        gemm_glu_epi_body<T, ACT, 1>(a);                                                   \
-    }                                                                                      \
-    extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void cuca_gemm_glu_epi_##TN##_##AN##_v4(QDequantArgs a) { \
-        gemm_glu_epi_body<T, ACT, 4>(a);                                                   \
-    }
-CUCA_GLU_EPI(f32, float, silu, 0)
-CUCA_GLU_EPI(f32, float, gelu, 1)
-CUCA_GLU_EPI(f16, _Float16, silu, 0)
-CUCA_GLU_EPI(f16, _Float16, gelu, 1)

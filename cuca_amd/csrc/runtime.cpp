@@ -13,8 +13,6 @@
 #include "noalloc.h"
 
 #include <hip/hip_runtime_api.h>
-#include <hipblaslt/hipblaslt.h>
-#include <hipblaslt/hipblaslt-ext.hpp>
 
 #include <cmath>
 #include <cstdarg>
@@ -93,15 +91,6 @@ struct cuca_hip_ctx {
     // by those entry points only
     void *noalloc = nullptr;
     std::string noalloc_error;
-    // hipBLASLt for the dense f16 GEMM of many rows (created on first use)
-    // and the algorithms its heuristic picked, per shape
-    hipblasLtHandle_t lt = nullptr;
-    struct LtPlan {
-        int64_t rows, k, m, ldx, ldd;
-        int dtype;
-        hipblasLtMatmulAlgo_t algo;
-    };
-    std::vector<LtPlan> lt_plans;
     int cu_count = 256;
     std::string error;
     // per-kernel timing (cuca_hip_profile_start/stop)
@@ -272,7 +261,6 @@ void cuca_hip_ctx_destroy(cuca_hip_ctx *ctx) {
     }
     if (ctx->status) (void)hipFree(ctx->status);
     if (ctx->pscratch) (void)hipFree(ctx->pscratch);
-    if (ctx->lt) (void)hipblasLtDestroy(ctx->lt);
     if (ctx->module) (void)hipModuleUnload(ctx->module);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
@@ -1971,7 +1959,7 @@ cuca_status cuca_hip_add_rmsnorm_qmm_glu(cuca_hip_ctx *ctx, const void *x, const
 
 // ---------------------------------------------------------------------
 // the dense f16 path for many rows: a resident f16 copy of the weight and
-// hipBLASLt's f16 GEMM (f32 accumulation)
+// the library's f16 GEMM on the matrix cores (gemm16.hip, f32 accumulation)
 // ---------------------------------------------------------------------
 
 cuca_status cuca_hip_qweight_dequant(cuca_hip_ctx *ctx, const void *packed, uint32_t ggml_type, int64_t n, int64_t k,
@@ -1997,14 +1985,29 @@ cuca_status cuca_hip_qweight_dequant(cuca_hip_ctx *ctx, const void *packed, uint
                   (unsigned)div_up(n * ng * 16, CUCA_BLOCK_THREADS), CUCA_BLOCK_THREADS, 0, a);
 }
 
-// hipBLASLt's own workspace within the caller's, and the parts before it
-constexpr size_t kLtWorkspace = 32ull << 20;
+// Tiles of 256 (GLU 128) output columns x 256 rows.  A call of fewer than
+// 128 tiles splits k (up to 8 ways into equal splits of at least 8 stages of
+// 32 values) so that about 256 workgroups run; the splits' f32 sums go to
+// the workspace and a reduce launch adds them in split order.  The split
+// count follows from the shape alone, so a call's bits do not depend on the
+// device.
+static int gemm16_splits(int64_t n, int64_t k, int64_t m, bool glu) {
+    const int64_t tiles = ((n + (glu ? 127 : 255)) / (glu ? 128 : 256)) * ((m + 255) / 256);
+    if (tiles >= 128) return 1;
+    const int64_t nst = k / 32;
+    int64_t s = std::min<int64_t>(std::min<int64_t>(8, (256 + tiles - 1) / tiles), std::max<int64_t>(1, nst / 8));
+    while (nst % s) s--; // equal splits
+    return (int)s;
+}
+// The workspace: the activations rounded to f16 when they come as f32, then
+// the split sums.
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+static size_t gemm_w16_ws_x(int64_t k, int64_t m, cuca_dtype dtype) {
+    return dtype == CUCA_F32 ? align256((size_t)m * (size_t)k * 2) : 0;
+}
 static size_t gemm_w16_ws_bytes(int64_t n, int64_t k, int64_t m, bool glu, cuca_dtype dtype) {
-    size_t b = kLtWorkspace;
-    if (dtype == CUCA_F32) b += align256((size_t)m * (size_t)k * 2); // activations as f16
-    if (glu) b += align256((size_t)m * (size_t)(2 * n) * 4);          // the f32 gate|up rows
-    return b;
+    const int sp = gemm16_splits(n, k, m, glu);
+    return gemm_w16_ws_x(k, m, dtype) + (sp > 1 ? (size_t)sp * (glu ? 2 : 1) * (size_t)m * (size_t)n * 4 : 0);
 }
 
 cuca_status cuca_hip_gemm_w16_workspace(int64_t n, int64_t k, int64_t m, int32_t glu, cuca_dtype dtype,
@@ -2017,93 +2020,9 @@ cuca_status cuca_hip_gemm_w16_workspace(int64_t n, int64_t k, int64_t m, int32_t
     return CUCA_OK;
 }
 
-static cuca_status lt_fail(cuca_hip_ctx *ctx, hipblasStatus_t s, const char *what) {
-    return fail(ctx, CUCA_HIP_ERROR, "hipBLASLt %s: status %d", what, (int)s);
-}
-
-// D [m][ldd] (row-major) = X [m][ldx] . W [rows][k]^T, f16 operands, f32
-// accumulation, D of type dt.  In hipBLASLt's column-major terms: D^T
-// (rows x m) = op_T(W^T) (rows x k) . X^T (k x m).
-static cuca_status lt_gemm(cuca_hip_ctx *ctx, const void *w16, int64_t rows, int64_t k, const void *xh, int64_t ldx,
-                           int64_t m, void *d, int64_t ldd, hipDataType dt, void *lt_ws) {
-    hipblasStatus_t e;
-    if (!ctx->lt && (e = hipblasLtCreate(&ctx->lt)) != HIPBLAS_STATUS_SUCCESS) {
-        ctx->lt = nullptr;
-        return lt_fail(ctx, e, "create");
-    }
-    hipblasLtMatmulDesc_t op = nullptr;
-    hipblasLtMatrixLayout_t la = nullptr, lb = nullptr, ld = nullptr;
-    cuca_status st = CUCA_OK;
-    do {
-        if ((e = hipblasLtMatmulDescCreate(&op, HIPBLAS_COMPUTE_32F, HIP_R_32F)) != HIPBLAS_STATUS_SUCCESS) {
-            st = lt_fail(ctx, e, "matmul descriptor"); break;
-        }
-        const hipblasOperation_t ta = HIPBLAS_OP_T, tb = HIPBLAS_OP_N;
-        hipblasLtMatmulDescSetAttribute(op, HIPBLASLT_MATMUL_DESC_TRANSA, &ta, sizeof ta);
-        hipblasLtMatmulDescSetAttribute(op, HIPBLASLT_MATMUL_DESC_TRANSB, &tb, sizeof tb);
-        if ((e = hipblasLtMatrixLayoutCreate(&la, HIP_R_16F, (uint64_t)k, (uint64_t)rows, k)) != HIPBLAS_STATUS_SUCCESS ||
-            (e = hipblasLtMatrixLayoutCreate(&lb, HIP_R_16F, (uint64_t)k, (uint64_t)m, ldx)) != HIPBLAS_STATUS_SUCCESS ||
-            (e = hipblasLtMatrixLayoutCreate(&ld, dt, (uint64_t)rows, (uint64_t)m, ldd)) != HIPBLAS_STATUS_SUCCESS) {
-            st = lt_fail(ctx, e, "matrix layout"); break;
-        }
-        const hipblasLtMatmulAlgo_t *algo = nullptr;
-        for (const auto &p : ctx->lt_plans)
-            if (p.rows == rows && p.k == k && p.m == m && p.ldx == ldx && p.ldd == ldd && p.dtype == (int)dt) {
-                algo = &p.algo;
-                break;
-            }
-        if (!algo) {
-            hipblasLtMatmulPreference_t pref = nullptr;
-            if ((e = hipblasLtMatmulPreferenceCreate(&pref)) != HIPBLAS_STATUS_SUCCESS) {
-                st = lt_fail(ctx, e, "preference"); break;
-            }
-            const uint64_t wsb = kLtWorkspace;
-            hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &wsb, sizeof wsb);
-            hipblasLtMatmulHeuristicResult_t res[1];
-            int count = 0;
-            e = hipblasLtMatmulAlgoGetHeuristic(ctx->lt, op, la, lb, ld, ld, pref, 1, res, &count);
-            hipblasLtMatmulPreferenceDestroy(pref);
-            if (e != HIPBLAS_STATUS_SUCCESS || count < 1) {
-                st = fail(ctx, CUCA_UNSUPPORTED, "hipBLASLt: no algorithm for %lld x %lld x %lld (status %d)",
-                          (long long)m, (long long)rows, (long long)k, (int)e);
-                break;
-            }
-            // Use an answer only when the library itself confirms it for this
-            // exact problem and it fits the workspace passed to every call: its
-            // heuristic state, its stated workspace, and AlgoCheck's verdict and
-            // workspace.  Otherwise refuse the shape rather than launch it.
-            const float one = 1.0f, zero = 0.0f;
-            size_t chk_ws = 0;
-            const hipblasStatus_t ce =
-                res[0].state == HIPBLAS_STATUS_SUCCESS
-                    ? hipblaslt_ext::matmulIsAlgoSupported(ctx->lt, op, &one, la, lb, &zero, ld, ld, res[0].algo,
-                                                           chk_ws)
-                    : res[0].state;
-            if (res[0].state != HIPBLAS_STATUS_SUCCESS || res[0].workspaceSize > kLtWorkspace ||
-                ce != HIPBLAS_STATUS_SUCCESS || chk_ws > kLtWorkspace) {
-                st = fail(ctx, CUCA_UNSUPPORTED,
-                          "hipBLASLt: the algorithm for %lld x %lld x %lld is not confirmed (state %d, check %d, "
-                          "workspace %zu/%zu of %zu bytes)",
-                          (long long)m, (long long)rows, (long long)k, (int)res[0].state, (int)ce,
-                          (size_t)res[0].workspaceSize, chk_ws, (size_t)kLtWorkspace);
-                break;
-            }
-            ctx->lt_plans.push_back({rows, k, m, ldx, ldd, (int)dt, res[0].algo});
-            algo = &ctx->lt_plans.back().algo;
-        }
-        const float one = 1.0f, zero = 0.0f;
-        if ((e = hipblasLtMatmul(ctx->lt, op, &one, w16, la, xh, lb, &zero, d, ld, d, ld, algo, lt_ws, kLtWorkspace,
-                                 ctx->stream)) != HIPBLAS_STATUS_SUCCESS) {
-            st = lt_fail(ctx, e, "matmul"); break;
-        }
-        if (hipGetLastError() != hipSuccess) { st = fail(ctx, CUCA_HIP_ERROR, "hipBLASLt matmul launch"); break; }
-    } while (0);
-    if (la) hipblasLtMatrixLayoutDestroy(la);
-    if (lb) hipblasLtMatrixLayoutDestroy(lb);
-    if (ld) hipblasLtMatrixLayoutDestroy(ld);
-    if (op) hipblasLtMatmulDescDestroy(op);
-    return st;
-}
+// Row strides the kernel addresses with 32-bit byte offsets within a tile
+// of 256 rows.
+constexpr int64_t kGemm16MaxLd = 1ll << 22;
 
 // glu: 0 plain, 1 SiLU, 2 GELU-tanh; w16 [n][k] (gate rows, then up rows
 // for the GLU: n = 2 ff).
@@ -2123,25 +2042,26 @@ static cuca_status gemm_w16_common(cuca_hip_ctx *ctx, const void *w16, int64_t n
                     (long long)k);
     if (out_ld < (glu ? n / 2 : rows))
         return fail(ctx, CUCA_INVALID_ARG, "gemm: output row stride %lld too short", (long long)out_ld);
+    if (k >= kGemm16MaxLd || ldx >= kGemm16MaxLd)
+        return fail(ctx, CUCA_UNSUPPORTED, "gemm: row strides from %lld values on are not supported",
+                    (long long)kGemm16MaxLd);
     if (!(clamp == clamp)) return fail(ctx, CUCA_INVALID_ARG, "clamp is NaN");
     if (m == 0) return CUCA_OK;
-    if (!w16 || !x || !out || !ws) return fail(ctx, CUCA_INVALID_ARG, "null pointer");
+    const int64_t ncols = glu ? n / 2 : rows; // output columns
+    const size_t need = gemm_w16_ws_bytes(ncols, k, m, glu != 0, dtype);
+    if (!w16 || !x || !out || (need && !ws)) return fail(ctx, CUCA_INVALID_ARG, "null pointer");
     const size_t es = esize(dtype);
-    if (!al16(w16) || !al16(x) || !al16(out) || !al16(ws) || ((size_t)ldx * es) % 16 != 0)
+    if (!al16(w16) || !al16(x) || !al16(out) || (ws && !al16(ws)) || ((size_t)ldx * es) % 16 != 0)
         return fail(ctx, CUCA_INVALID_ARG, "gemm: weights, rows, output and workspace must be 16-byte aligned");
-    const size_t need = gemm_w16_ws_bytes(glu ? n / 2 : n, k, m, glu != 0, dtype);
     if (ws_bytes < need)
         return fail(ctx, CUCA_INVALID_ARG, "gemm: workspace of %zu bytes, %zu needed (cuca_hip_gemm_w16_workspace)",
                     ws_bytes, need);
-    char *p = static_cast<char *>(ws);
-    void *lt_ws = p;
-    p += kLtWorkspace;
     const void *xh = x;
     int64_t ldxh = ldx;
     if (dtype == CUCA_F32) { // the activations rounded to f16 once
         QDequantArgs c{};
         c.x = x;
-        c.out = p;
+        c.out = ws;
         c.ldx = ldx;
         c.out_ld = k;
         c.m = (int32_t)m;
@@ -2149,29 +2069,65 @@ static cuca_status gemm_w16_common(cuca_hip_ctx *ctx, const void *w16, int64_t n
         if ((st = launch(ctx, cuca_cvt_f16_f32, (unsigned)div_up(m * (k / 8), CUCA_BLOCK_THREADS),
                          CUCA_BLOCK_THREADS, 0, c)) != CUCA_OK)
             return st;
-        xh = p;
+        xh = ws;
         ldxh = k;
-        p += align256((size_t)m * (size_t)k * 2);
     }
-    const hipDataType dt = dtype == CUCA_F16 ? HIP_R_16F : HIP_R_32F;
-    if (!glu) return lt_gemm(ctx, w16, rows, k, xh, ldxh, m, out, out_ld, dt, lt_ws);
-    const int64_t ff = n / 2;
-    if ((st = lt_gemm(ctx, w16, n, k, xh, ldxh, m, p, n, HIP_R_32F, lt_ws)) != CUCA_OK) return st;
-    QDequantArgs e{};
-    e.x = p;
-    e.out = out;
-    e.ldx = n;
-    e.out_ld = out_ld;
-    e.n = ff;
-    e.m = (int32_t)m;
-    e.clamp = clamp > 0.0f ? clamp : 0.0f;
-    static const Kernel epi[2][2][2] = {
-        {{cuca_gemm_glu_epi_f32_silu, cuca_gemm_glu_epi_f32_gelu}, {cuca_gemm_glu_epi_f16_silu, cuca_gemm_glu_epi_f16_gelu}},
-        {{cuca_gemm_glu_epi_f32_silu_v4, cuca_gemm_glu_epi_f32_gelu_v4},
-         {cuca_gemm_glu_epi_f16_silu_v4, cuca_gemm_glu_epi_f16_gelu_v4}}};
-    const bool v4 = ff % 4 == 0 && out_ld % 4 == 0;
-    return launch(ctx, epi[v4][dtype == CUCA_F16][glu == 2],
-                  (unsigned)div_up(m * ff / (v4 ? 4 : 1), CUCA_BLOCK_THREADS), CUCA_BLOCK_THREADS, 0, e);
+    const bool f16 = dtype == CUCA_F16;
+    const int splits = gemm16_splits(ncols, k, m, glu != 0);
+    Gemm16Args a{};
+    a.w = w16;
+    a.x = xh;
+    a.ldw = k;
+    a.ldx = ldxh;
+    a.m = (int32_t)m;
+    a.n_tm = (int32_t)div_up(m, 256);
+    a.gn = 8;
+    a.clamp = clamp > 0.0f ? clamp : 0.0f;
+    a.splits = splits;
+    Kernel kern;
+    if (splits == 1) {
+        a.out = out;
+        a.out_ld = out_ld;
+        a.up_row = glu ? n / 2 : 0;
+        a.n = (int32_t)ncols;
+        a.k = (int32_t)k;
+        a.n_tn = (int32_t)div_up(ncols, glu ? 128 : 256);
+        a.vec = out_ld % 4 == 0 ? 1 : 0;
+        kern = glu == 0 ? (f16 ? cuca_gemm16_f16 : cuca_gemm16_f32)
+               : glu == 1 ? (f16 ? cuca_gemm16_glu_f16_silu : cuca_gemm16_glu_f32_silu)
+                          : (f16 ? cuca_gemm16_glu_f16_gelu : cuca_gemm16_glu_f32_gelu);
+    } else {
+        // the plain form over every weight row the call reads (the GLU's gate
+        // rows, then its up rows), k / splits values per split, each split's
+        // f32 sums to its own [m][width] matrix of the workspace
+        const int64_t width = glu ? n : ncols;
+        a.part = reinterpret_cast<float *>(static_cast<char *>(ws) + gemm_w16_ws_x(k, m, dtype));
+        a.out = a.part;
+        a.out_ld = width;
+        a.n = (int32_t)width;
+        a.k = (int32_t)(k / splits);
+        a.n_tn = (int32_t)div_up(width, 256);
+        a.vec = width % 4 == 0 ? 1 : 0;
+        kern = cuca_gemm16_f32;
+    }
+    const int64_t tiles = (int64_t)a.n_tn * a.n_tm;
+    if (tiles > 0x7ffffff8ll) return fail(ctx, CUCA_UNSUPPORTED, "gemm: grid too large");
+    // every XCD (workgroups x, x + 8, ...) gets ceil(tiles / 8) workgroups
+    if ((st = launch2(ctx, kern, (unsigned)(8 * div_up(tiles, 8)), (unsigned)splits, 256, 0, a)) != CUCA_OK ||
+        splits == 1)
+        return st;
+    Gemm16Args r{};
+    r.part = a.part;
+    r.out = out;
+    r.out_ld = out_ld;
+    r.n = (int32_t)ncols;
+    r.m = (int32_t)m;
+    r.splits = splits;
+    r.clamp = a.clamp;
+    static const Kernel red_k[2][3] = {
+        {cuca_gemm16_reduce_f32, cuca_gemm16_reduce_glu_f32_silu, cuca_gemm16_reduce_glu_f32_gelu},
+        {cuca_gemm16_reduce_f16, cuca_gemm16_reduce_glu_f16_silu, cuca_gemm16_reduce_glu_f16_gelu}};
+    return launch(ctx, red_k[f16][glu], div_up(m * ncols, CUCA_BLOCK_THREADS), CUCA_BLOCK_THREADS, 0, r);
 }
 
 cuca_status cuca_hip_gemm_w16(cuca_hip_ctx *ctx, const void *w16, int64_t n, int64_t k, const void *x, int64_t ldx,

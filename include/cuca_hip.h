@@ -559,8 +559,8 @@ cuca_status cuca_hip_qgemm_glu(cuca_hip_ctx *ctx, const void *gate, const void *
  * for MI355X's 288 GB: the weight is dequantised once into a resident f16
  * copy (2 bytes a value: 16 GB for an 8B model, next to the Q4_0 weights
  * the decode kernels read), and each call is one f16 GEMM on the matrix
- * cores (hipBLASLt, f32 accumulation).  The arithmetic class of
- * cuca_hip_qgemm (weights f16(d * q), activations f16(x), one rounding
+ * cores (the library's own kernel, f32 accumulation).  The arithmetic class
+ * of cuca_hip_qgemm (weights f16(d * q), activations f16(x), one rounding
  * each), held to the same bound.
  *   cuca_hip_qweight_dequant: packed (cuca_hip_qweight_pack) [n, k] ->
  *     w16 f16 [n][k] row-major, f16(d * q) per value.
@@ -568,10 +568,12 @@ cuca_status cuca_hip_qgemm_glu(cuca_hip_ctx *ctx, const void *gate, const void *
  *     dtype (f32 rows are rounded to f16 into the workspace first).
  *   cuca_hip_gemm_w16_glu: w16 [2 ff][k] = the gate rows, then the up rows
  *     (one GEMM); out[m][ff] = act(gate) * up with Glu::apply's clamp, from
- *     f32 sums.
+ *     the f32 sums in registers.
  * workspace: device, 16-byte aligned, cuca_hip_gemm_w16_workspace bytes
- * (n = the output width: rows, or ff for the GLU).  Not for a few rows:
- * decode batches take cuca_hip_qmm / cuca_hip_qgemm on the packed weight. */
+ * (n = the output width: rows, or ff for the GLU): the f32 activations
+ * rounded to f16, so 0 bytes (and workspace may be NULL) for f16 calls.
+ * k and ldx below 2^22.  Not for a few rows: decode batches take
+ * cuca_hip_qmm / cuca_hip_qgemm on the packed weight. */
 cuca_status cuca_hip_qweight_dequant(cuca_hip_ctx *ctx, const void *packed, uint32_t ggml_type, int64_t n,
                                      int64_t k, void *w16);
 cuca_status cuca_hip_gemm_w16_workspace(int64_t n, int64_t k, int64_t m, int32_t glu, cuca_dtype dtype,

@@ -1,8 +1,7 @@
 //! Link libcuca_hip.so: built in-tree by `python -m cuca_amd.build` into
 //! `cuca_amd/` of this repository (CUCA_HIP_LIB_DIR overrides the search
-//! directory).  The library depends on libamdhip64 and, for the dense f16
-//! GEMM of cuca_hip_gemm_w16 / _glu, libhipblaslt (ROCm's own libraries,
-//! found through the rpath the build records).
+//! directory).  The library depends on libamdhip64 only (ROCm's HIP
+//! runtime, found through the rpath the build records).
 use std::env;
 use std::path::PathBuf;
 

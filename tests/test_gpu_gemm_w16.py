@@ -11,7 +11,11 @@ cuca_hip_gemm_w16, cuca_hip_gemm_w16_glu) through the C ABI.
   and for the GLU the same bounds carried through act(g) * u.
 Covers Q4_0 / Q8_0, f32 / f16 activations, 1 to 2048 rows (ragged tails of
 rows and columns), weight-row prefixes, a row stride wider than k, repeated
-calls, and the host's checks.
+calls, and the host's checks.  The GEMM is the library's own kernel
+(gemm16.hip, cuca_gemm16_*): calls of fewer than 128 tiles of 256 x 256
+(GLU: 128 columns) split k (the plain f32 form over every weight row, one
+output matrix a split) and add the splits in a reduce launch; both forms are
+covered, and a test pins which kernels a call launches.
 """
 import numpy as np
 import pytest
@@ -139,3 +143,45 @@ def test_row_prefix_and_host_checks(ctx):
         ctx.gemm_w16(w16.ptr, n, k, dx.ptr, k, m, n + 1, ws.ptr, wsb, full.ptr, n + 1, hip.F32)
     with pytest.raises(hip.CucaError, match="row stride"):
         ctx.gemm_w16(w16.ptr, n, k, dx.ptr, k - 32, m, n, ws.ptr, wsb, full.ptr, n, hip.F32)
+
+
+@pytest.mark.parametrize("m,n,k,glu,kernels", [
+    (512, 4096, 4096, False, ["cuca_gemm16_f32", "cuca_gemm16_reduce_f16"]),   # 32 tiles: k split 8 ways
+    (1024, 8192, 512, False, ["cuca_gemm16_f16"]),                          # 128 tiles: one pass
+    (512, 2048, 1024, True, ["cuca_gemm16_f32", "cuca_gemm16_reduce_glu_f16_silu"]),
+    (2048, 2048, 256, True, ["cuca_gemm16_glu_f16_silu"]),
+])
+def test_the_library_kernels_run(ctx, m, n, k, glu, kernels):
+    """The dense GEMM is this library's kernel (no library GEMM underneath):
+    the launched kernels by name, and the result within the bound on a few
+    sampled rows."""
+    rng = np.random.default_rng(m + n + k)
+    rows = 2 * n if glu else n
+    w = (rng.standard_normal((rows, k)) * 0.02).astype(np.float16)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    dw, dx = ctx.array(w), ctx.array(x)
+    out = ctx.empty((m, n), np.float16)
+    wsb = hip.gemm_w16_workspace(n, k, m, glu, hip.F16)
+    ws = ctx.empty((max(wsb, 16),), np.uint8)
+    ctx.sync()
+    ctx.profile_start(4)
+    if glu:
+        ctx.gemm_w16_glu(dw.ptr, n, k, dx.ptr, k, m, hip.ACT_SILU, 0.0, ws.ptr, wsb, out.ptr, n, hip.F16)
+    else:
+        ctx.gemm_w16(dw.ptr, n, k, dx.ptr, k, m, n, ws.ptr, wsb, out.ptr, n, hip.F16)
+    names = [kn for kn, _ in ctx.profile_stop()]
+    assert names == kernels, names
+    sel = np.array([0, m // 3, m - 1])
+    xf, wf = x[sel].astype(np.float64), w.astype(np.float64)
+    got = out.numpy()[sel].astype(np.float64)
+    if glu:
+        g, u = xf @ wf[:n].T, xf @ wf[n:].T
+        bg, bu = bound(xf, wf[:n], k), bound(xf, wf[n:], k)
+        a = g / (1.0 + np.exp(-g))
+        want = a * u
+        tol = 1.2 * bg * (np.abs(u) + bu) + np.abs(a) * bu + 1e-5 * np.abs(want)
+    else:
+        want = xf @ wf.T
+        tol = bound(xf, wf, k)
+    tol = tol + 2.0 ** -11 * np.abs(want) + 1e-30
+    assert np.all(np.abs(got - want) <= tol), float(np.max(np.abs(got - want) / tol))
