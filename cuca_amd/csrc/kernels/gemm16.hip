@@ -29,15 +29,17 @@
 // order and applies the output (and the GLU).
 //
 // LDS layout: row R's 16-byte unit u sits at unit u ^ f(R), f(R) =
-// ((R >> 1) ^ (R >> 3)) & 3, so the fragment reads of 16 consecutive rows at
-// one unit fall in distinct banks whether the LDS serves 8 or 16 lanes of a
-// 16-byte read at a time.
+// (R >> 1) & 3.  Measured on MI355X with a probe of 16-byte LDS reads whose
+// 16 lanes of a unit step through 64-byte rows: unswizzled, or swizzled by
+// R & 3, (R >> 2) & 3 or ((R >> 1) ^ (R >> 3)) & 3, such a read takes twice
+// the LDS cycles of a linear one (SQ_LDS_IDX_ACTIVE 8 against 4 a read);
+// swizzled by (R >> 1) & 3 it takes the same 4 cycles as a linear read.
 //
 // Measured on MI355X at 4096 f16 rows (Llama-3-8B shapes), in one process
-// against hipBLASLt's f16 GEMM: down 4096 x 14336 385-407 us (0.47-0.50 of
-// the 2.5 PFLOP/s dense peak) against 323-398; q/o 4096 x 4096 122-128 us
-// (0.43-0.45) against 98-100; gate+up with SwiGLU 817-847 us (0.46-0.47)
-// against 916-1065 for hipBLASLt's GEMM plus the separate GLU pass.
+// against torch's f16 matmul (hipBLASLt): down 4096 x 14336 384-424 us
+// (0.45-0.50 of the 2.5 PFLOP/s dense peak) against 326-402; q/o 4096 x
+// 4096 117-132 us (0.42-0.47) against 101-103; gate+up with SwiGLU 884-897
+// us (0.43), against 916-1065 for hipBLASLt's GEMM plus a separate GLU pass.
 #include "common.h"
 #include <type_traits>
 
@@ -68,7 +70,7 @@ __device__ static inline void gemm16_body(const Gemm16Args &a) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wn = wave & 1, wm = wave >> 1;
-    const int r = lane & 15, u4 = lane >> 4;
+    int r = lane & 15, u4 = lane >> 4;
     // The tile: XCD x (workgroups x, x + 8, ...) takes tiles [x per, (x + 1)
     // per) in launch order, grouped gn column tiles at a time and walked
     // token tile by token tile, so that the workgroups resident on an XCD at
@@ -118,7 +120,7 @@ __device__ static inline void gemm16_body(const Gemm16Args &a) {
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         const int R = 16 * (8 * wave + i) + (lane >> 2); // LDS row 0..511
-        const int pu = (lane & 3) ^ (((R >> 1) ^ (R >> 3)) & 3);
+        const int pu = (lane & 3) ^ ((R >> 1) & 3);
         int lr = wave < 2 ? R & 127 : R - 256; // the row within the wave's source
         if (lr >= lim) lr = 0;
         off[i] = 2u * ((uint32_t)lr * ld + 8u * (uint32_t)pu);
@@ -158,17 +160,16 @@ __device__ static inline void gemm16_body(const Gemm16Args &a) {
         brow[i] = 256 + 128 * wm + 16 * i;
     }
     // Fragment of a block at base 16 q: lane (r, u4) holds row 16 q + r,
-    // k unit u4, at unit u4 ^ f(16 q + r) = u4 ^ f(r) ^ 2 (q & 1); q & 1 is
-    // the parity of the block's index within arow / brow.
-    const int pos = 8 * (u4 ^ (((r >> 1) ^ (r >> 3)) & 3));
+    // k unit u4, at unit u4 ^ f(16 q + r) = u4 ^ f(r).
+    const int pos = 8 * (u4 ^ ((r >> 1) & 3));
     g16_h8 fa[2][8], fb[2][8];
     auto frags = [&](const _Float16 *S, g16_h8 (&av)[8], g16_h8 (&bv)[8]) {
 #pragma unroll
         for (int i = 0; i < 8; i++)
-            av[i] = *reinterpret_cast<const g16_h8 *>(&S[(arow[i] + r) * G16_BK + (pos ^ (16 * (i & 1)))]);
+            av[i] = *reinterpret_cast<const g16_h8 *>(&S[(arow[i] + r) * G16_BK + pos]);
 #pragma unroll
         for (int j = 0; j < 8; j++)
-            bv[j] = *reinterpret_cast<const g16_h8 *>(&S[(brow[j] + r) * G16_BK + (pos ^ (16 * (j & 1)))]);
+            bv[j] = *reinterpret_cast<const g16_h8 *>(&S[(brow[j] + r) * G16_BK + pos]);
     };
     // Stage st, its fragments in slot sl (read during the stage before); Sc
     // its buffer, Sn the next stage's.  FULL: the stages up to st + 4 exist.
@@ -225,6 +226,14 @@ __device__ static inline void gemm16_body(const Gemm16Args &a) {
 
     // Accumulator e of lane (r, u4) in tile (i, j): weight row 16 i + 4 u4 +
     // e of the wave's blocks, token 16 j + r: four consecutive columns.
+    // (The lane's r and u4 computed afresh from its lane number: otherwise
+    // values derived from them before the k loop are kept through it, and
+    // with every register in use there one of them spills.)
+    {
+        const int ln = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+        r = ln & 15;
+        u4 = ln >> 4;
+    }
     // (i outer: one block of columns at a time; with the tokens outer, the
     // compiler copied every tile out of the accumulators at once and spilled)
 #pragma unroll
