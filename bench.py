@@ -993,17 +993,20 @@ def qgemm_bench(ctx, torch, reps=10):
     return res
 
 
-def prefill_layer_bench(ctx, torch, name="C", n=4096, reps=5):
+def prefill_layer_bench(ctx, torch, name="C", n=4096, reps=5, dense=False):
     """A whole prefill layer of config `name` at n f16 tokens on this
     library, end to end: the fused gather + first-block norm, the Q|K|V
     projection (cuca_hip_qgemm, Q4_0), RoPE + paged K/V store, the causal
     attention of the n rows over the cache they were just stored in
     (cuca_hip_attend_rows), the output projection, residual + norm, the
     gate/up projection with the SwiGLU in its epilogue (cuca_hip_qgemm_glu),
-    down, residual + norm.  Per op: kernel time (per-kernel timestamps,
-    median of `reps` layers); the attention also as TFLOP/s of its causal
-    products (4 d heads per (row, key) pair).  Checked: sampled attention
-    rows against the oracle's attend_paged_rows, finite outputs."""
+    down, residual + norm.  dense: the four projections on the dense f16
+    path instead (the Q4_0 weights dequantised once, untimed, then
+    cuca_hip_gemm_w16 / _gemm_w16_glu: the reference GPU engine's prefill
+    form).  Per op: kernel time (per-kernel timestamps, median of `reps`
+    layers); the attention also as TFLOP/s of its causal products (4 d heads
+    per (row, key) pair).  Checked: sampled attention rows against the
+    oracle's attend_paged_rows, finite outputs."""
     import numpy as np
     from cuca_amd import hip
     from cuca_amd import workloads as W
@@ -1048,7 +1051,28 @@ def prefill_layer_bench(ctx, torch, name="C", n=4096, reps=5):
         kn = (1 + 0.02 * torch.randn(d, device=dev, generator=gen)).float()
     wsb = max(hip.qgemm_workspace(T, nqkv, H, n), hip.qgemm_workspace(T, H, nq * d, n),
               hip.qgemm_workspace(T, F, H, n, True), hip.qgemm_workspace(T, H, F, n))
+    dq_us = 0.0
+    if dense:  # resident f16 copies (gate rows, then up rows, for the GLU)
+        def w16_of(ps, rows, k):
+            w = torch.empty((len(ps) * rows, k), dtype=hf, device=dev)
+            for i, p in enumerate(ps):
+                ctx.qweight_dequant(p.data_ptr(), T, rows, k, w.data_ptr() + i * rows * k * 2)
+            return w
+        t0 = time.perf_counter()
+        wqkv, wo, wgu, wd = w16_of([wqkv], nqkv, H), w16_of([wo], H, nq * d), w16_of([wg, wu], F, H), w16_of([wd], H, F)
+        torch.cuda.synchronize()
+        dq_us = (time.perf_counter() - t0) * 1e6
+        wg = wu = None
+        wsb = max(hip.gemm_w16_workspace(nqkv, H, n, False, f16), hip.gemm_w16_workspace(H, nq * d, n, False, f16),
+                  hip.gemm_w16_workspace(F, H, n, True, f16), hip.gemm_w16_workspace(H, F, n, False, f16), 16)
     wsp = torch.empty(wsb, dtype=torch.uint8, device=dev)
+
+    def matmul(w, rows, k, xin, out):
+        if dense:
+            return ctx.gemm_w16(w.data_ptr(), rows, k, xin.data_ptr(), k, n, rows, wsp.data_ptr(), wsb,
+                                out.data_ptr(), rows, f16)
+        return ctx.qgemm(w.data_ptr(), T, rows, k, xin.data_ptr(), k, n, rows, wsp.data_ptr(), wsb, out.data_ptr(),
+                         rows, f16)
     scale = 1.0 / float(np.sqrt(d))
     ops = []
 
@@ -1057,8 +1081,7 @@ def prefill_layer_bench(ctx, torch, name="C", n=4096, reps=5):
     op("embed_rms", lambda: ctx.embed_gguf_rms(table_e.data_ptr(), W.GGML_ID[cfg["qtype"]], cfg["vocab"], H,
                                                ids.data_ptr(), n, cfg["embd_scale"], wn[0].data_ptr(), eps,
                                                x.data_ptr(), h.data_ptr(), f16))
-    op("qkv_matmul", lambda: ctx.qgemm(wqkv.data_ptr(), T, nqkv, H, h.data_ptr(), H, n, nqkv, wsp.data_ptr(), wsb,
-                                       qkv.data_ptr(), nqkv, f16))
+    op("qkv_matmul", lambda: matmul(wqkv, nqkv, H, h, qkv))
     op("rope_store_kv", lambda: ctx.rope_store_kv(
         qkv.data_ptr(), nqkv, qkv.data_ptr() + 2 * nq * d, nqkv, qkv.data_ptr() + 2 * (nq + nk) * d, nqkv, n, nq,
         nk, d, d, kind, dcos.data_ptr(), dsin.data_ptr(), n, pos.data_ptr(),
@@ -1067,14 +1090,17 @@ def prefill_layer_bench(ctx, torch, name="C", n=4096, reps=5):
     op("attention", lambda: ctx.attend_rows(qkv.data_ptr(), nqkv, pk.data_ptr(), pv.data_ptr(), n_blocks,
                                             dtab.data_ptr(), len(table), ranges.data_ptr(), n, nq, nk, d, scale,
                                             attn.data_ptr(), nq * d, f16))
-    op("o_matmul", lambda: ctx.qgemm(wo.data_ptr(), T, H, nq * d, attn.data_ptr(), nq * d, n, H, wsp.data_ptr(),
-                                     wsb, br.data_ptr(), H, f16))
+    op("o_matmul", lambda: matmul(wo, H, nq * d, attn, br))
     op("add_rmsnorm_attn", lambda: ctx.add_rmsnorm(x.data_ptr(), br.data_ptr(), wn[1].data_ptr(), None, eps, eps,
                                                    1.0, n, H, x.data_ptr(), h.data_ptr(), f16))
-    op("gate_up_glu_matmul", lambda: ctx.qgemm_glu(wg.data_ptr(), wu.data_ptr(), T, F, H, h.data_ptr(), H, n,
-                                                   hip.ACT_SILU, 0.0, wsp.data_ptr(), wsb, act.data_ptr(), F, f16))
-    op("down_matmul", lambda: ctx.qgemm(wd.data_ptr(), T, H, F, act.data_ptr(), F, n, H, wsp.data_ptr(), wsb,
-                                        br.data_ptr(), H, f16))
+    if dense:
+        op("gate_up_glu_matmul", lambda: ctx.gemm_w16_glu(wgu.data_ptr(), F, H, h.data_ptr(), H, n, hip.ACT_SILU, 0.0,
+                                                          wsp.data_ptr(), wsb, act.data_ptr(), F, f16))
+    else:
+        op("gate_up_glu_matmul", lambda: ctx.qgemm_glu(wg.data_ptr(), wu.data_ptr(), T, F, H, h.data_ptr(), H, n,
+                                                       hip.ACT_SILU, 0.0, wsp.data_ptr(), wsb, act.data_ptr(), F,
+                                                       f16))
+    op("down_matmul", lambda: matmul(wd, H, F, act, br))
     op("add_rmsnorm_ffn", lambda: ctx.add_rmsnorm(x.data_ptr(), br.data_ptr(), wn[2].data_ptr(), None, eps, eps,
                                                   1.0, n, H, x.data_ptr(), h.data_ptr(), f16))
     torch.cuda.synchronize()
@@ -1113,10 +1139,16 @@ def prefill_layer_bench(ctx, torch, name="C", n=4096, reps=5):
     per["attention"]["mfma_frac"] = round(att_flops / (per["attention"]["us"] / 1e6) / 2.5e15, 4)
     mm = sum(per[k]["us"] for k in ("qkv_matmul", "o_matmul", "gate_up_glu_matmul", "down_matmul"))
     del wqkv, wo, wg, wu, wd, table_e
+    if dense:
+        del wgu
     torch.cuda.empty_cache()
-    return dict(config=name, tokens=n, dtype="f16", weights="q4_0", us_per_layer=round(ms * 1000, 1),
-                tokens_per_s_per_layer=round(n / (ms / 1e3), 0), matmul_us=round(mm, 1),
-                attention_us=per["attention"]["us"], checked_attention_rows=int(rows.size), ops=per)
+    res = dict(config=name, tokens=n, dtype="f16", weights="q4_0 dequantised to f16 once" if dense else "q4_0",
+               us_per_layer=round(ms * 1000, 1), tokens_per_s_per_layer=round(n / (ms / 1e3), 0),
+               matmul_us=round(mm, 1), attention_us=per["attention"]["us"], checked_attention_rows=int(rows.size),
+               ops=per)
+    if dense:
+        res["dequant_once_us"] = round(dq_us, 1)
+    return res
 
 
 def gemm_w16_bench(ctx, torch, reps=10):
@@ -1655,10 +1687,12 @@ def main():
             checked_rows += 2
         torch.cuda.empty_cache()
 
-    qmm = moe = head = qgemm = gemm16 = player = None
+    qmm = moe = head = qgemm = gemm16 = player = player_dense = None
     if not args.no_qmm and not args.no_attn:
         log("a whole prefill layer (config C, 4096 tokens, f16): matmuls, RoPE + K/V store, attention")
         player = prefill_layer_bench(ctx, torch, "C", 4096)
+        log("the same layer with the projections on the dense f16 path")
+        player_dense = prefill_layer_bench(ctx, torch, "C", 4096, dense=True)
     if not args.no_qmm:
         log("quantized matmuls (8B decode shapes)")
         qmm = qmm_bench(ctx, torch)
@@ -1750,6 +1784,7 @@ def main():
         "end_of_step": head,
         "decode_us_per_layer": decode,
         "prefill_layer": player,
+        "prefill_layer_dense": player_dense,
         "prefill_bar": prefill_bar(ops, args.tokens, big, configs),
         "decode_bar": decode_bar(decode, attn),
         "roofline": {"kernel": glu["kernel"], "bound": "hbm",
