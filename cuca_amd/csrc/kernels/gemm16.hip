@@ -180,18 +180,41 @@ __device__ static inline void gemm16_body(const Gemm16Args &a) {
         // barrier, every wave's
         g16_wait(FULL ? 8 * (G16_NB - 2) : 8 * max(0, min(G16_NB - 2, nst - st - 2)));
         __syncthreads();
-        if (FULL || st + 1 < nst) frags(Sn, fa[sl ^ 1], fb[sl ^ 1]);
-        __builtin_amdgcn_sched_barrier(0);
+        const bool nx = FULL || st + 1 < nst;
         const bool cp = FULL || st + G16_NB < nst;
-#pragma unroll
-        for (int q = 0; q < 8; q++) {
-#pragma unroll
-            for (int j = 0; j < 8; j++)
-                acc[q][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[sl][q], fb[sl][j], acc[q][j], 0, 0, 0);
-            // (the scheduling barriers keep one copy after every 8 products)
+        // The products of this stage, 8 at a time, one copy after each group
+        // (the scheduling barriers keep that order).  The plain form issues
+        // two of the next stage's fragment reads before each group, so its
+        // products start right after the barrier; the GLU form reads them
+        // all first (interleaved, the compiler moves its accumulators between
+        // registers inside the loop).
+        if constexpr (GLU) {
+            if (nx) frags(Sn, fa[sl ^ 1], fb[sl ^ 1]);
             __builtin_amdgcn_sched_barrier(0);
-            if (cp) copy1(st + G16_NB, Sc, q);
-            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+                    acc[q][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[sl][q], fb[sl][j], acc[q][j], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (cp) copy1(st + G16_NB, Sc, q);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                if (nx) {
+                    fa[sl ^ 1][q] = *reinterpret_cast<const g16_h8 *>(&Sn[(arow[q] + r) * G16_BK + pos]);
+                    fb[sl ^ 1][q] = *reinterpret_cast<const g16_h8 *>(&Sn[(brow[q] + r) * G16_BK + pos]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+                    acc[q][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[sl][q], fb[sl][j], acc[q][j], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
+                if (cp) copy1(st + G16_NB, Sc, q);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     };
     using T1 = std::integral_constant<bool, true>;
