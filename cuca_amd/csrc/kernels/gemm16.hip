@@ -36,10 +36,10 @@
 // swizzled by (R >> 1) & 3 it takes the same 4 cycles as a linear read.
 //
 // Measured on MI355X at 4096 f16 rows (Llama-3-8B shapes), in one process
-// against torch's f16 matmul (hipBLASLt): down 4096 x 14336 384-424 us
-// (0.45-0.50 of the 2.5 PFLOP/s dense peak) against 326-402; q/o 4096 x
-// 4096 117-132 us (0.42-0.47) against 101-103; gate+up with SwiGLU 884-897
-// us (0.43), against 916-1065 for hipBLASLt's GEMM plus a separate GLU pass.
+// against torch's f16 matmul (hipBLASLt): down 4096 x 14336 370-402 us
+// (0.48-0.52 of the 2.5 PFLOP/s dense peak) against 326-383; q/o 4096 x
+// 4096 114-124 us (0.45-0.48) against 102-103; gate+up with SwiGLU 882-884
+// us (0.44), against 916-1065 for hipBLASLt's GEMM plus a separate GLU pass.
 #include "common.h"
 #include <type_traits>
 
