@@ -106,8 +106,20 @@ __device__ static inline void load_tab(const float *t, int64_t first, float (&v)
 // LP: the load policy of the head chunks (LP_DEV, LP_NT, LP_CACHED above).
 // LP_DEV addresses a row's chunks by 32-bit byte offsets from q, k and v:
 // the host checks that rows * row stride fits.
-template <typename T, int KIND, bool NORM, bool STORE, int LP, int HPL = 1>
+// WHOLE (the _h2w kernels; the host launches them for in-place RoPE whose
+// rotated dims cover the head, with QK-norm only when both projections have
+// norm weights, at a power-of-two head_dim, two heads a lane): every lane
+// rotates and every head is normalised with weights, so the per-value
+// selects of pass-through lanes and weightless heads drop out; the mean is
+// the sum times 1 / head_dim (exact for a power of two: the same bits as
+// the division); and the two heads' norm factors are computed once per lane
+// pair (below).  (In config E's prefill step, 8192 tokens of QK-norm NEOX
+// f16, the waves wait on memory 42 % of their resident time against 67 %
+// for config C's RoPE: instruction issue holds them.  The whole-head form
+// takes about 10 % of the per-lane instructions off and ran 2 % faster.)
+template <typename T, int KIND, bool NORM, bool STORE, int LP, int HPL = 1, bool WHOLE = false>
 __device__ static inline void rope_body(const RopeArgs &a) {
+    static_assert(!WHOLE || (HPL == 2 && !STORE), "whole-head kernels: two heads a lane, in place");
     constexpr int VP = Chunk<T>::N;
     constexpr int NC = KIND == 2 ? 2 : 1;       // chunks per lane
     constexpr int NT = KIND == 2 ? VP : VP / 2; // cos/sin entries per lane
@@ -145,7 +157,7 @@ __device__ static inline void rope_body(const RopeArgs &a) {
     } else {
         e[0] = u * VP; rot = e[0] < a.n_dims;
     }
-    rot = rot && hk != 2;
+    rot = WHOLE || (rot && hk != 2);
     // Every load is issued up front and unconditionally, from addresses that
     // are always valid (a lane past the last head reads row 0, a position
     // outside the table or a pass-through lane reads table entry 0, a head
@@ -204,6 +216,47 @@ __device__ static inline void rope_body(const RopeArgs &a) {
     for (int j = 0; j < HPL; j++)
 #pragma unroll
         for (int k = 0; k < NC; k++) pin(raw[j][k]);
+    // WHOLE with QK-norm: both heads' sums of squares first.  The butterfly's
+    // first step (xor tph/2) is taken transposed -- the lower half of a
+    // head's lanes keeps head 0's partial sums and the upper half head 1's,
+    // each lane adding its partner's partial of the head it keeps -- and the
+    // rest of the butterfly runs within each half, so every lane ends with
+    // exactly the sum the per-head butterfly gives (the same additions in
+    // the same order), of one head; each lane computes that head's factor,
+    // and takes the other head's from its partner.  (tph >= 2: a head_dim of
+    // at least 32 f16 or 16 f32 values; the host launches WHOLE only then.)
+    float winv[WHOLE && NORM ? HPL : 1];
+    if constexpr (WHOLE && NORM) {
+        float ssh[HPL];
+#pragma unroll
+        for (int j = 0; j < HPL; j++) {
+            float v[NC][VP];
+#pragma unroll
+            for (int k = 0; k < NC; k++) Chunk<T>::widen(raw[j][k], v[k]);
+            float ss = 0.0f;
+#pragma unroll
+            for (int k = 0; k < NC; k++)
+#pragma unroll
+                for (int i = 0; i < VP; i++) ss += v[k][i] * v[k][i];
+            ssh[j] = ss;
+        }
+        const int hb = tph >> 1;
+        const bool upper = (u & hb) != 0;
+        float t = (upper ? ssh[1] : ssh[0]) + xor_partner(upper ? ssh[0] : ssh[1], hb);
+        t = group_sum_rt(t, hb);
+        // (a power-of-two head_dim: the mean times 2^-log2(D) is the division's value)
+        const float rd = __builtin_amdgcn_ldexpf(1.0f, -(tl + (KIND == 2 ? 1 : 0) + (VP == 8 ? 3 : 2)));
+        const float mine = 1.0f / sqrtf(t * rd + a.eps);
+        const float other = xor_partner(mine, hb);
+        winv[0] = upper ? other : mine;
+        winv[1] = upper ? mine : other;
+        // widened again below, head by head: keeping both heads' widened
+        // values from the sums took 83 registers (5 waves per SIMD)
+#pragma unroll
+        for (int j = 0; j < HPL; j++)
+#pragma unroll
+            for (int k = 0; k < NC; k++) pin(raw[j][k]);
+    }
 #pragma unroll
     for (int j = 0; j < HPL; j++) {
     float v[NC][VP];
@@ -214,21 +267,30 @@ __device__ static inline void rope_body(const RopeArgs &a) {
 #pragma unroll
             for (int k = 0; k < NC; k++) pin(w[k]);
         }
-        float ss = 0.0f;
+        float inv;
+        if constexpr (WHOLE) {
+            inv = winv[j];
+        } else {
+            float ss = 0.0f;
 #pragma unroll
-        for (int k = 0; k < NC; k++)
+            for (int k = 0; k < NC; k++)
 #pragma unroll
-            for (int i = 0; i < VP; i++) ss += v[k][i] * v[k][i];
-        ss = group_sum_rt(ss, tph);
-        // the norm kernel's reciprocal form, x * (1 / sqrt(mean + eps)) * w;
-        // a weightless norm multiplies by 1 (exact)
-        const float inv = 1.0f / sqrtf(ss / (float)D + a.eps);
+                for (int i = 0; i < VP; i++) ss += v[k][i] * v[k][i];
+            ss = group_sum_rt(ss, tph);
+            // the norm kernel's reciprocal form, x * (1 / sqrt(mean + eps)) * w;
+            // a weightless norm multiplies by 1 (exact)
+            inv = 1.0f / sqrtf(ss / (float)D + a.eps);
+        }
 #pragma unroll
         for (int k = 0; k < NC; k++)
 #pragma unroll
             for (int i = 0; i < VP; i++) {
-                const float wi = nw ? w[k][i] : 1.0f;
-                v[k][i] = scale_h ? v[k][i] * inv * wi : v[k][i];
+                if constexpr (WHOLE) {
+                    v[k][i] = v[k][i] * inv * w[k][i];
+                } else {
+                    const float wi = nw ? w[k][i] : 1.0f;
+                    v[k][i] = scale_h ? v[k][i] * inv * wi : v[k][i];
+                }
             }
     }
     // The rotation is computed on every lane and selected.
@@ -238,8 +300,8 @@ __device__ static inline void rope_body(const RopeArgs &a) {
             const float x0 = v[0][i], x1 = v[NC - 1][i];
             const float r0 = x0 * c[i] - x1 * s[i];
             const float r1 = x0 * s[i] + x1 * c[i];
-            v[0][i] = rot ? r0 : x0;
-            v[NC - 1][i] = rot ? r1 : x1;
+            v[0][i] = WHOLE || rot ? r0 : x0;
+            v[NC - 1][i] = WHOLE || rot ? r1 : x1;
         }
     } else {
 #pragma unroll
@@ -247,8 +309,8 @@ __device__ static inline void rope_body(const RopeArgs &a) {
             const float x0 = v[0][2 * j], x1 = v[0][2 * j + 1];
             const float r0 = x0 * c[j] - x1 * s[j];
             const float r1 = x0 * s[j] + x1 * c[j];
-            v[0][2 * j] = rot ? r0 : x0;
-            v[0][2 * j + 1] = rot ? r1 : x1;
+            v[0][2 * j] = WHOLE || rot ? r0 : x0;
+            v[0][2 * j + 1] = WHOLE || rot ? r1 : x1;
         }
     }
     T *dst;
@@ -496,6 +558,11 @@ __device__ static inline void rope_generic_body(const RopeArgs &a) {
     extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void NAME##_g(RopeArgs a) {        \
         rope_body<T, KIND, NORM, STORE, LP_CACHED>(a);                                     \
     }
+// in-place RoPE of whole heads, two a lane (rope_body's WHOLE)
+#define CUCA_ROPE_W(NAME, T, KIND, NORM, LP)                                               \
+    extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void NAME##_h2w(RopeArgs a) {      \
+        rope_body<T, KIND, NORM, false, LP, 2, true>(a);                                   \
+    }
 // full-width QK-norm: a workgroup of up to 1024 threads per row
 #define CUCA_ROPE_FULL(NAME, T, KIND, STORE)                                               \
     extern "C" __global__ __launch_bounds__(1024) void NAME(RopeArgs a) {                  \
@@ -522,6 +589,12 @@ __device__ static inline void rope_generic_body(const RopeArgs &a) {
     CUCA_ROPE_NT(cuca_rope_##TN##_neox_qkn_nt, T, 2, false)                                \
     CUCA_ROPE_NT(cuca_rope_##TN##_norm_qkn_kv_nt, T, 0, true)                              \
     CUCA_ROPE_NT(cuca_rope_##TN##_neox_qkn_kv_nt, T, 2, true)                              \
+    CUCA_ROPE_W(cuca_rope_##TN##_norm, T, 0, false, LP_DEV)                                \
+    CUCA_ROPE_W(cuca_rope_##TN##_neox, T, 2, false, LP_DEV)                                \
+    CUCA_ROPE_W(cuca_rope_##TN##_norm_qkn, T, 0, true, LP_DEV)                             \
+    CUCA_ROPE_W(cuca_rope_##TN##_neox_qkn, T, 2, true, LP_DEV)                             \
+    CUCA_ROPE_W(cuca_rope_##TN##_norm_qkn_nt, T, 0, true, LP_NT)                           \
+    CUCA_ROPE_W(cuca_rope_##TN##_neox_qkn_nt, T, 2, true, LP_NT)                           \
     extern "C" __global__ __launch_bounds__(CUCA_BLOCK) void cuca_rope_##TN##_generic(     \
         RopeArgs a) {                                                                      \
         rope_generic_body<T>(a);                                                           \

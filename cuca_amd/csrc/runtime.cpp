@@ -925,8 +925,23 @@ static cuca_status rope_common(cuca_hip_ctx *ctx, void *q, int64_t q_ld, const v
     // K/V store 17.9 -> 16.7 and 65.1 -> 59.5 us, config E's QK-norm RoPE
     // 29.8 -> 27.9 us and its fused store 31.4 -> 30.4 us; four heads per
     // lane ran config E's QK-norm kernels slower (99 registers).
+    // In-place RoPE of whole heads (the rotated dims cover the head; with
+    // QK-norm, norm weights for both projections) takes the _h2w kernels:
+    // the same arithmetic without the per-value selects of pass-through
+    // lanes and weightless heads, and each QK-norm factor computed once per
+    // lane pair.  Measured on MI355X in the prefill steps, the two forms A/B in
+    // one process (same bits): config E's QK-norm RoPE 27.3-27.7 -> 26.8-27.1
+    // us at 8192 tokens, config C's RoPE 13.9-14.1 -> 13.6-13.8 us at 4096
+    // and 49.3-49.4 -> 49.0 us at 16384.
+    static const Kernel table_h2w[2][2][2] = {
+        {{cuca_rope_f32_norm_h2w, cuca_rope_f32_norm_qkn_h2w}, {cuca_rope_f32_neox_h2w, cuca_rope_f32_neox_qkn_h2w}},
+        {{cuca_rope_f16_norm_h2w, cuca_rope_f16_norm_qkn_h2w}, {cuca_rope_f16_neox_h2w, cuca_rope_f16_neox_qkn_h2w}}};
+    static const Kernel table_nt_h2w[2][2] = {{cuca_rope_f32_norm_qkn_nt_h2w, cuca_rope_f32_neox_qkn_nt_h2w},
+                                              {cuca_rope_f16_norm_qkn_nt_h2w, cuca_rope_f16_neox_qkn_nt_h2w}};
+    const bool whole = !store && n_dims == head_dim && tph >= 2 && (!norm || (q_norm_w && k_norm_w));
     if (dev && nq % 2 == 0 && nk % 2 == 0) {
-        const Kernel k2 = stream ? table_nt_h2[f16][neox][store] : table_h2[f16][neox][norm][store];
+        const Kernel k2 = whole ? (stream ? table_nt_h2w[f16][neox] : table_h2w[f16][neox][norm])
+                                : (stream ? table_nt_h2[f16][neox][store] : table_h2[f16][neox][norm][store]);
         return launch(ctx, k2, div_up(heads / 2, 256 / tph), 256, 0, a);
     }
     return launch(ctx, kk, div_up(heads, 256 / tph), 256, 0, a);

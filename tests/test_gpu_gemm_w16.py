@@ -185,3 +185,35 @@ def test_the_library_kernels_run(ctx, m, n, k, glu, kernels):
         tol = bound(xf, wf, k)
     tol = tol + 2.0 ** -11 * np.abs(want) + 1e-30
     assert np.all(np.abs(got - want) <= tol), float(np.max(np.abs(got - want) / tol))
+
+
+@pytest.mark.parametrize("m,n,k,glu", [(300, 257, 32, False), (5, 100, 64, False), (513, 300, 96, True),
+                                       (260, 70, 160, True), (1, 9, 32, True)])
+def test_short_k_and_ragged_tiles(ctx, m, n, k, glu):
+    """k of one to five stages of 32 (fewer stages than the kernel keeps in
+    flight), tiles cut by both m and n, odd output widths (element stores)."""
+    rng = np.random.default_rng(m * 3 + n + k)
+    rows = 2 * n if glu else n
+    w = (rng.standard_normal((rows, k)) * 0.05).astype(np.float16)
+    x = rng.standard_normal((m, k)).astype(np.float16)
+    dw, dx = ctx.array(w), ctx.array(x)
+    out = ctx.empty((m, n), np.float32)
+    wsb = hip.gemm_w16_workspace(n, k, m, glu, hip.F32)
+    ws = ctx.empty((max(wsb, 16),), np.uint8)
+    xf32 = ctx.array(x.astype(np.float32))
+    if glu:
+        ctx.gemm_w16_glu(dw.ptr, n, k, xf32.ptr, k, m, hip.ACT_SILU, 0.0, ws.ptr, wsb, out.ptr, n, hip.F32)
+    else:
+        ctx.gemm_w16(dw.ptr, n, k, xf32.ptr, k, m, n, ws.ptr, wsb, out.ptr, n, hip.F32)
+    xf, wf = x.astype(np.float64), w.astype(np.float64)
+    got = out.numpy().astype(np.float64)
+    if glu:
+        g, u = xf @ wf[:n].T, xf @ wf[n:].T
+        bg, bu = bound(xf, wf[:n], k), bound(xf, wf[n:], k)
+        a = g / (1.0 + np.exp(-g))
+        want = a * u
+        tol = 1.2 * bg * (np.abs(u) + bu) + np.abs(a) * bu + 1e-5 * np.abs(want) + 1e-30
+    else:
+        want = xf @ wf.T
+        tol = bound(xf, wf, k) + 1e-30
+    assert np.all(np.abs(got - want) <= tol), float(np.max(np.abs(got - want) / tol))

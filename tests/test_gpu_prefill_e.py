@@ -7,7 +7,8 @@ test names the kernel it means to cover and checks, from the C ABI's
 per-kernel profile, that the call launched exactly that kernel:
   add_rmsnorm, H 2048: 2 x 8192 x 2048 f16 in = 64 MiB -> cuca_norm_f16_t256_nts
     (the streamlined prefill form: a branch, weights, x' written, rs 1)
-  QK-norm RoPE, Q 32 + K 4 heads x 128: 72 MiB  -> cuca_rope_f16_neox_qkn_nt_h2 (two heads per lane)
+  QK-norm RoPE, Q 32 + K 4 heads x 128: 72 MiB  -> cuca_rope_f16_neox_qkn_nt_h2w (two whole heads
+    per lane)
   the same + the paged K/V store (V 4 heads): 80 MiB -> cuca_rope_f16_neox_qkn_kv_nt_h2
   the SwiGLU over the 65536 expert-grouped rows of width 768 (Zipf(1.1)
   routing, 8 of 128 experts per token) -> cuca_glu_f16_silu_ragged
@@ -81,7 +82,7 @@ def test_qk_norm_rope_streaming_kernel_at_8192_tokens(ctx, torch):
                                            hip.ROPE_NEOX, dcos.data_ptr(), dsin.data_ptr(), N,
                                            pos.data_ptr(), qw.data_ptr(), kw.data_ptr(), CFG["eps"],
                                            hip.F16))
-    assert names == ["cuca_rope_f16_neox_qkn_nt_h2"], names
+    assert names == ["cuca_rope_f16_neox_qkn_nt_h2w"], names
     ctx.check_device()
     s = sample(N, 43)
     st = torch.from_numpy(s).cuda()

@@ -7,7 +7,9 @@ With the QK-norm: within 1e-5 of the rotated pair's magnitude (f32) or
 NORM, head_dim 128 and 256, Q/K head counts, random and prefix positions),
 partial rotary dims, Q and K inside a fused QKV row, the generic kernel
 (head_dim 80, n_dims 6 of 8 = the cpu.rs:4336 case), bad positions and the
-full config C size on sampled rows.
+full config C size on sampled rows.  In-place RoPE of whole heads (two a
+lane) runs the _h2w kernels, which must give the bits of the per-head _h2
+kernels: pinned on calls that reach both.
 """
 import numpy as np
 import pytest
@@ -218,3 +220,40 @@ def test_full_width_qk_norm_inside_a_fused_qkv_row_and_bad_shapes(ctx):
         ops.rope_qk(q80, None, ctx.array(c80), ctx.array(s80), hip.ROPE_NEOX, 80,
                     ctx.array(np.zeros(2, np.int32)), q_norm_w=np.ones(160, np.float32),
                     qk_norm_full=True)
+
+
+@pytest.mark.parametrize("dtype,kind,d,rows", [("f16", hip.ROPE_NEOX, 128, 200), ("f32", hip.ROPE_NEOX, 128, 96),
+                                               ("f16", hip.ROPE_NORM, 128, 200), ("f32", hip.ROPE_NORM, 64, 96),
+                                               ("f16", hip.ROPE_NEOX, 32, 64), ("f16", hip.ROPE_NEOX, 128, 8192),
+                                               ("f32", hip.ROPE_NORM, 128, 4096)])
+def test_whole_head_kernels_give_the_per_head_bits(ctx, dtype, kind, d, rows):
+    """A Q-only QK-norm call (32 heads, nk 0) with a K norm weight given runs
+    the whole-head kernel (_h2w: no per-value selects, one norm factor per
+    lane pair); the same call without it runs the per-head kernel (_h2).
+    Both normalise Q with the same weights, so the bits must agree, and both
+    stay within the QK-norm bar of the oracle.  At 64 MiB of heads the calls
+    take the nontemporal-load kernels (_nt_h2w / _nt_h2); head_dim 32 f16
+    NEOX has two lanes a head, the smallest the whole-head form takes."""
+    nq = 32
+    rng = np.random.default_rng(rows + d)
+    q = rng.standard_normal((rows, nq, d)).astype(NP[dtype])
+    qw = (1 + 0.02 * rng.standard_normal(d)).astype(np.float32)
+    kw = (1 + 0.02 * rng.standard_normal(d)).astype(np.float32)
+    pos = rng.integers(0, 4 * rows, rows).astype(np.int32)
+    cos, sin = hip.rope_tables(kind, d, 10000.0, 4 * rows)
+    dcos, dsin, dpos, dqw, dkw = (ctx.array(a) for a in (cos, sin, pos, qw, kw))
+    big = rows * nq * d * q.itemsize >= 48 << 20
+    stem = f"cuca_rope_{dtype}_{'neox' if kind == hip.ROPE_NEOX else 'norm'}_qkn_{'nt_' if big else ''}h2"
+    got = {}
+    for kname, kptr in ((stem + "w", dkw.ptr), (stem, 0)):
+        dq = ctx.array(q)
+        ctx.profile_start(4)
+        ctx.rope(dq.ptr, nq * d, 0, 0, rows, nq, 0, d, d, kind, dcos.ptr, dsin.ptr, 4 * rows, dpos.ptr, dqw.ptr,
+                 kptr, 1e-6, hip.dtype_code(NP[dtype]))
+        names = [k for k, _ in ctx.profile_stop()]
+        assert names == [kname], names
+        got[kname] = dq.numpy()
+    assert_bits_equal(got[stem + "w"], got[stem], "whole-head q")
+    sel = np.arange(0, rows, max(1, rows // 64))
+    want = O.rope(q[sel], cos, sin, pos[sel], kind, norm_w=qw, eps=1e-6)
+    assert_close(got[stem + "w"][sel], want, floor=pair_floor(want, kind, d), what="q")
