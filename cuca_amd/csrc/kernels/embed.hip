@@ -412,17 +412,61 @@ __device__ static inline void embed_unit_load(const uint8_t *row, int u, uint32_
 }
 // The unit's 8 values from the packed words: the same arithmetic as
 // embed_dequant (d' = f32(d) * scale, then f32(q) * d').
+// (Q8_0: the 8 bytes as one vector of int8, so each conversion is one
+// byte-select convert; extracted by shifts, one of them compiled to a 64-bit
+// integer conversion of a dozen instructions)
 template <int QT>
 __device__ static inline void embed_unit_dequant(int u, uint32_t dq, u32x2_a2 q, float scale, float (&v)[8]) {
     const int p = (u * 8) & 31;
     const float d = (float)__builtin_bit_cast(_Float16, (uint16_t)dq) * scale;
+    if constexpr (QT == 2) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const uint32_t b = (q[i >> 2] >> (8 * (i & 3))) & 0xffu;
-        if (QT == 2) v[i] = (float)((int)((b >> (p >= 16 ? 4 : 0)) & 0xfu) - 8) * d;
-        else v[i] = (float)(int8_t)b * d;
+        for (int i = 0; i < 8; i++) {
+            const uint32_t b = (q[i >> 2] >> (8 * (i & 3))) & 0xffu;
+            v[i] = (float)((int)((b >> (p >= 16 ? 4 : 0)) & 0xfu) - 8) * d;
+        }
+    } else {
+        typedef int8_t i8x8 __attribute__((ext_vector_type(8)));
+        const i8x8 b = __builtin_bit_cast(i8x8, q);
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = (float)b[i] * d;
     }
 }
+
+// A unit's 8 output values as the row holds them (f16: 16 packed bytes; f32:
+// two 16-byte chunks), so that a bad id zeroes the packed words and the
+// norm reads the stored values back from them.
+template <typename OutT> struct EmbedOut;
+template <> struct EmbedOut<_Float16> {
+    u32x4 p;
+    __device__ inline void set(const float (&v)[8]) {
+        f16x8 h;
+#pragma unroll
+        for (int i = 0; i < 8; i++) h[i] = (_Float16)pin_f32(v[i]);
+        p = __builtin_bit_cast(u32x4, h);
+    }
+    __device__ inline void zero_if(bool z) { p = z ? u32x4{0u, 0u, 0u, 0u} : p; }
+    __device__ inline void store_nt(void *row, int u) const {
+        __builtin_nontemporal_store(p, reinterpret_cast<u32x4 *>(row) + u);
+    }
+    __device__ inline void values(float (&v)[8]) const { Chunk<_Float16>::widen(p, v); }
+};
+template <> struct EmbedOut<float> {
+    float x[8];
+    __device__ inline void set(const float (&v)[8]) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) x[i] = v[i];
+    }
+    __device__ inline void zero_if(bool z) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) x[i] = z ? 0.0f : x[i];
+    }
+    __device__ inline void store_nt(void *row, int u) const { embed_store<float>(reinterpret_cast<float *>(row), u, x); }
+    __device__ inline void values(float (&v)[8]) const {
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = x[i];
+    }
+};
 
 // The fused gather for many tokens, as persistent workgroups: TPR threads
 // per token (thread t owns unit t: hidden = 8 TPR), each workgroup taking
@@ -434,6 +478,15 @@ __device__ static inline void embed_unit_dequant(int u, uint32_t dq, u32x2_a2 q,
 // token's stores.  The sum of squares is the workgroup-per-token kernel's
 // order (per thread, a wave butterfly, an LDS sum in wave order), so h has
 // its bits; x is the plain gather's.  36 registers: 8 waves per SIMD.
+// Its instruction count matters (the VALU is busy about two thirds of the
+// kernel's time): the Q8_0 bytes convert as one int8 vector, a bad id zeroes
+// the packed words rather than each value, the norm reads the stored values
+// back from the packed words (one conversion a value), no weights is a
+// weight of 1 (x * 1 == x) rather than a second code path, and the mean is
+// the sum times 1 / hidden (exact: hidden is 8 TPR).  A quarter fewer
+// instructions a token, the same bits: 61.0-61.4 -> 59.8-60.0 us in the
+// config C step at 16384 tokens (0.69 -> 0.71 of the HBM peak), A/B in one
+// process.
 // Measured in the config C prefill step on MI355X (16384 Q8_0 tokens of 4096
 // -> f16): 61.3-61.6 us against 65.2-65.4 for the LDS-weights wave-per-token
 // kernel (0.69 against 0.65 of the HBM peak); 8 tokens per workgroup (two
@@ -445,13 +498,16 @@ __device__ static inline void embed_rms_persist_body(const EmbedArgs &a) {
     __shared__ float red[2][NW];
     const int t = threadIdx.x, lane = t & (CUCA_WAVE - 1), wave = t / CUCA_WAVE;
     const int G = gridDim.x;
-    const bool has_w = a.rms_w != nullptr;
+    // (no weights: 1, and x * 1 is x exactly, so one form serves both)
     float wv[8];
-    if (has_w) {
+    if (a.rms_w != nullptr) {
         const f32x4 *wp = reinterpret_cast<const f32x4 *>(a.rms_w) + 2 * t;
         const f32x4 w0 = wp[0], w1 = wp[1];
         wv[0] = w0.x; wv[1] = w0.y; wv[2] = w0.z; wv[3] = w0.w;
         wv[4] = w1.x; wv[5] = w1.y; wv[6] = w1.z; wv[7] = w1.w;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) wv[j] = 1.0f;
     }
     // lane i holds the id of the workgroup's token i (tokens past n read
     // the last token's id, so every load below stays inside the table)
@@ -482,17 +538,14 @@ __device__ static inline void embed_rms_persist_body(const EmbedArgs &a) {
             if (bad && t == 0) record_bad(a.status + CUCA_STATUS_EMBED_ID, (uint32_t)tok, id);
             float v[8];
             embed_unit_dequant<QT>(t, dq[it], q[it], a.scale, v);
-            if (bad) {
-#pragma unroll
-                for (int j = 0; j < 8; j++) v[j] = 0.0f;
-            }
-            embed_store<OutT>(orow, t, v);
+            EmbedOut<OutT> xo;
+            xo.set(v);
+            xo.zero_if(bad);
+            xo.store_nt(orow, t);
+            xo.values(v); // the stored values (zeros for a bad id)
             float ss = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                v[j] = Chunk<OutT>::as_stored(v[j]);
-                ss += v[j] * v[j];
-            }
+            for (int j = 0; j < 8; j++) ss += v[j] * v[j];
             ss = group_sum<CUCA_WAVE>(ss);
             // two slots, alternating: a wave that runs ahead writes the other
             // slot, and cannot come back to this one before every wave has
@@ -502,20 +555,16 @@ __device__ static inline void embed_rms_persist_body(const EmbedArgs &a) {
             ss = 0.0f;
 #pragma unroll
             for (int i = 0; i < NW; i++) ss += red[it & 1][i];
-            const float inv = 1.0f / sqrtf(ss / (float)a.hidden + a.rms_eps);
+            // (hidden = 8 TPR, a power of two: the sum times 1 / hidden is the
+            // division's value)
+            const float inv = 1.0f / sqrtf(ss * (1.0f / (8 * TPR)) + a.rms_eps);
             float y[8];
-            if (has_w) {
 #pragma unroll
-                for (int j = 0; j < 8; j++) y[j] = pin_f32(pin_f32(v[j] * inv) * wv[j]);
-            } else {
-#pragma unroll
-                for (int j = 0; j < 8; j++) y[j] = pin_f32(v[j] * inv);
-            }
-            if (bad) {
-#pragma unroll
-                for (int j = 0; j < 8; j++) y[j] = 0.0f;
-            }
-            embed_store<OutT>(hrow, t, y);
+            for (int j = 0; j < 8; j++) y[j] = pin_f32(pin_f32(v[j] * inv) * wv[j]);
+            EmbedOut<OutT> ho;
+            ho.set(y);
+            ho.zero_if(bad);
+            ho.store_nt(hrow, t);
         }
     }
 }
@@ -550,16 +599,20 @@ __device__ static inline void embed_rms_tpr_body(const EmbedArgs &a) {
     OutT *orow = reinterpret_cast<OutT *>(a.out) + (int64_t)tok * a.hidden;
     OutT *hrow = reinterpret_cast<OutT *>(a.h_out) + (int64_t)tok * a.hidden;
     const uint32_t id = a.ids[tok];
+    // (no weights: 1, and x * 1 is x exactly, so one form serves both)
     float wv[NU][8];
-    if (a.rms_w) {
 #pragma unroll
-        for (int k = 0; k < NU; k++) {
+    for (int k = 0; k < NU; k++) {
+        if (a.rms_w) {
             int u = t + TPR * k;
             u = u < nu ? u : 0;
             const f32x4 *wp = reinterpret_cast<const f32x4 *>(a.rms_w) + 2 * u;
             const f32x4 w0 = wp[0], w1 = wp[1];
             wv[k][0] = w0.x; wv[k][1] = w0.y; wv[k][2] = w0.z; wv[k][3] = w0.w;
             wv[k][4] = w1.x; wv[k][5] = w1.y; wv[k][6] = w1.z; wv[k][7] = w1.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; j++) wv[k][j] = 1.0f;
         }
     }
     constexpr int CPU = 8 / Chunk<OutT>::N;
@@ -591,12 +644,13 @@ __device__ static inline void embed_rms_tpr_body(const EmbedArgs &a) {
         const int u = t + TPR * k;
         embed_dequant<QT>(u, dq[k], w[k], a.scale, v[k]);
         if (u < nu) {
-            embed_store<OutT>(orow, u, v[k]);
+            // stored, and read back from the packed words (the stored values)
+            EmbedOut<OutT> xo;
+            xo.set(v[k]);
+            xo.store_nt(orow, u);
+            xo.values(v[k]);
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                v[k][j] = Chunk<OutT>::as_stored(v[k][j]);
-                ss += v[k][j] * v[k][j];
-            }
+            for (int j = 0; j < 8; j++) ss += v[k][j] * v[k][j];
         }
     }
     ss = group_sum<CUCA_WAVE>(ss);
@@ -607,18 +661,20 @@ __device__ static inline void embed_rms_tpr_body(const EmbedArgs &a) {
 #pragma unroll
         for (int i = 0; i < NW; i++) ss += red[i];
     }
-    const float inv = 1.0f / sqrtf(ss / (float)a.hidden + a.rms_eps);
+    // the mean: for a power-of-two hidden (uniform) the sum times 1 / hidden,
+    // the division's value without the division's instructions
+    float mean;
+    if ((a.hidden & (a.hidden - 1)) == 0)
+        mean = ss * __builtin_amdgcn_ldexpf(1.0f, -__builtin_ctz((unsigned)a.hidden));
+    else
+        mean = ss / (float)a.hidden;
+    const float inv = 1.0f / sqrtf(mean + a.rms_eps);
 #pragma unroll
     for (int k = 0; k < NU; k++) {
         const int u = t + TPR * k;
         float y[8];
-        if (a.rms_w) {
 #pragma unroll
-            for (int j = 0; j < 8; j++) y[j] = pin_f32(pin_f32(v[k][j] * inv) * wv[k][j]);
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; j++) y[j] = pin_f32(v[k][j] * inv);
-        }
+        for (int j = 0; j < 8; j++) y[j] = pin_f32(pin_f32(v[k][j] * inv) * wv[k][j]);
         if (u < nu) embed_store<OutT>(hrow, u, y);
     }
 }
