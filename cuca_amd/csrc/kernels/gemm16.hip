@@ -49,13 +49,18 @@ typedef float g16_acc __attribute__((ext_vector_type(4)));
 #define G16_BK 32 // k values a stage
 #define G16_NB 4  // stages resident in LDS
 
-// vmcnt(v) lgkmcnt(0) for the copy counts the pipeline waits on
+// vmcnt(v) lgkmcnt(0) for the copy counts the pipelines wait on (4 or 8
+// copies a stage, up to three stages in flight).  Any other count waits for
+// every copy (vmcnt(0)): a count missing here must cost time, never let a
+// stage be read before its copies have landed.
 __device__ static inline void g16_wait(int v) {
     switch (v) {
-    case 0: __builtin_amdgcn_s_waitcnt(0x0070); break;
+    case 4: __builtin_amdgcn_s_waitcnt(0x0074); break;
     case 8: __builtin_amdgcn_s_waitcnt(0x0078); break;
+    case 12: __builtin_amdgcn_s_waitcnt(0x007c); break;
     case 16: __builtin_amdgcn_s_waitcnt(0x4070); break;
-    default: __builtin_amdgcn_s_waitcnt(0x4078); break; // 24
+    case 24: __builtin_amdgcn_s_waitcnt(0x4078); break;
+    default: __builtin_amdgcn_s_waitcnt(0x0070); break; // 0
     }
 }
 
@@ -311,14 +316,217 @@ __device__ static inline void gemm16_body(const Gemm16Args &a) {
     }
 }
 
+// The GLU form with 8 waves a workgroup, two a SIMD: wave w computes the
+// weight half w & 1 (64 gate rows and the 64 up rows of the same columns) of
+// token quarter w >> 1 (64 tokens), 8 x 4 tiles, 128 accumulators, so a
+// SIMD holds two waves and one's products run while the other waits at the
+// barrier or on LDS.  The same tile, tile order, LDS layout, copies (four a
+// wave a stage) and stage pipeline; per stage a wave reads the next stage's
+// 4 token fragments first, then after each group of 4 products the next
+// stage's weight fragment of that group (in the register the group just
+// used), and issues its products at raised priority.  Each output sums its
+// k steps with the same instructions in the same order as the 4-wave
+// kernel.  Measured on MI355X at 4096 f16 rows with the launches of the two
+// forms interleaved (so that clock changes fall on both): gate+up with
+// SwiGLU 843-851 -> 784-793 us (0.45 -> 0.49 of the dense peak); the plain
+// form on 8 waves measured no faster (down 362-387 against 358-385 us, q/o
+// 116-127 against 113-118), so plain calls keep 4 waves.  (The body is
+// written for both forms; only the GLU kernels are built.)
+template <typename OutT, int ACT>
+__device__ static inline void gemm16_w8_body(const Gemm16Args &a) {
+    constexpr bool GLU = ACT >= 0;
+    __shared__ __attribute__((aligned(16))) _Float16 S0[512 * G16_BK], S1[512 * G16_BK], S2[512 * G16_BK],
+        S3[512 * G16_BK];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6); // 0..7
+    const int wn = wave & 1, wm = wave >> 1;                     // token quarter 0..3
+    int r = lane & 15, u4 = lane >> 4;
+    const int T = a.n_tn * a.n_tm, per = (T + 7) >> 3;
+    const int L = (int)(blockIdx.x & 7) * per + (int)(blockIdx.x >> 3);
+    if (L >= T) return; // uniform over the workgroup
+    const int grp = L / (a.gn * a.n_tm), within = L - grp * a.gn * a.n_tm;
+    const int gsz = min(a.gn, a.n_tn - grp * a.gn);
+    const int tn = grp * a.gn + within % gsz, tm = within / gsz;
+    const int n0 = tn * (GLU ? 128 : 256), t0 = tm * 256;
+    const int nst = a.k / G16_BK;
+    const int s0 = (int)blockIdx.y * nst;
+
+    // Copies: wave w fills LDS rows 64 w .. 64 w + 63 in pieces of 16 rows
+    // c = 4 w + i: waves 0-3 the weight tile (GLU: waves 0, 1 the gate rows,
+    // 2, 3 the up rows of the same columns), waves 4-7 the token tile.  Rows
+    // past the matrix read the first row of the wave's base; a base past the
+    // matrix falls back to the tile's first row.
+    const _Float16 *src;
+    int lim; // rows of the wave's source that exist
+    if (wave < 4) {
+        const int rb = GLU ? 64 * (wave & 1) : 64 * wave;
+        const int64_t first = GLU && wave >= 2 ? a.up_row + n0 : (int64_t)n0;
+        lim = a.n - n0 - rb;
+        src = reinterpret_cast<const _Float16 *>(a.w) + (first + (lim > 0 ? rb : 0)) * a.ldw;
+    } else {
+        const int rb = 64 * (wave - 4);
+        lim = a.m - t0 - rb;
+        src = reinterpret_cast<const _Float16 *>(a.x) + (int64_t)(t0 + (lim > 0 ? rb : 0)) * a.ldx;
+    }
+    const uint32_t ld = (uint32_t)(wave < 4 ? a.ldw : a.ldx);
+    uint32_t off[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int R = 16 * (4 * wave + i) + (lane >> 2); // LDS row 0..511
+        const int pu = (lane & 3) ^ ((R >> 1) & 3);
+        int lr = R - 64 * wave; // the row within the wave's source
+        if (lr >= lim) lr = 0;
+        off[i] = 2u * ((uint32_t)lr * ld + 8u * (uint32_t)pu);
+    }
+    const uint64_t sv = (uint64_t)(uintptr_t)(src + s0 * G16_BK);
+    const uint64_t bw = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(sv >> 32)) << 32) |
+                        (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)sv);
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+    auto copy1 = [&](int st, _Float16 *S, int i) {
+        const uint64_t base = bw + (uint64_t)st * (2 * G16_BK);
+        const uint32_t dst = (uint32_t)(uintptr_t)&S[16 * (4 * wave + i) * G16_BK];
+        asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1 sc0" ::"v"(off[i]), "s"(base), "s"(dst)
+                     : "memory", "m0");
+    };
+#pragma clang diagnostic pop
+
+    g16_acc acc[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = g16_acc{};
+    int arow[8], brow[4];
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+        arow[i] = GLU ? (i < 4 ? 64 * wn + 16 * i : 128 + 64 * wn + 16 * (i - 4)) : 128 * wn + 16 * i;
+#pragma unroll
+    for (int j = 0; j < 4; j++) brow[j] = 256 + 64 * wm + 16 * j;
+    const int pos = 8 * (u4 ^ ((r >> 1) & 3));
+    auto rd = [&](const _Float16 *S, int row) -> g16_h8 {
+        return *reinterpret_cast<const g16_h8 *>(&S[(row + r) * G16_BK + pos]);
+    };
+    g16_h8 fa[8], fb[2][4];
+    auto stage = [&](auto full, int st, int sl, _Float16 *Sc, _Float16 *Sn) {
+        constexpr bool FULL = decltype(full)::value;
+        // this wave's copies of stage st + 1 have landed and its reads of Sc
+        // are done; after the barrier, every wave's
+        g16_wait(FULL ? 4 * (G16_NB - 2) : 4 * max(0, min(G16_NB - 2, nst - st - 2)));
+        __syncthreads();
+        const bool nx = FULL || st + 1 < nst;
+        const bool cp = FULL || st + G16_NB < nst;
+        if (nx) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) fb[sl ^ 1][j] = rd(Sn, brow[j]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                acc[q][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[q], fb[sl][j], acc[q][j], 0, 0, 0);
+            __builtin_amdgcn_s_setprio(0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (nx) fa[q] = rd(Sn, arow[q]);
+            if (cp && (q & 1)) copy1(st + G16_NB, Sc, q >> 1);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    using T1 = std::integral_constant<bool, true>;
+    using T0 = std::integral_constant<bool, false>;
+    auto copy_stage = [&](int st, _Float16 *S) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) copy1(st, S, i);
+    };
+    copy_stage(0, S0);
+    if (nst > 1) copy_stage(1, S1);
+    if (nst > 2) copy_stage(2, S2);
+    if (nst > 3) copy_stage(3, S3);
+    g16_wait(4 * max(0, min(G16_NB, nst) - 1)); // stage 0 landed
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 8; i++) fa[i] = rd(S0, arow[i]);
+#pragma unroll
+    for (int j = 0; j < 4; j++) fb[0][j] = rd(S0, brow[j]);
+    int st = 0;
+    for (; st + 2 * G16_NB <= nst; st += G16_NB) {
+        stage(T1{}, st, 0, S0, S1);
+        stage(T1{}, st + 1, 1, S1, S2);
+        stage(T1{}, st + 2, 0, S2, S3);
+        stage(T1{}, st + 3, 1, S3, S0);
+    }
+    for (; st < nst; st += G16_NB) {
+        stage(T0{}, st, 0, S0, S1);
+        if (st + 1 < nst) stage(T0{}, st + 1, 1, S1, S2);
+        if (st + 2 < nst) stage(T0{}, st + 2, 0, S2, S3);
+        if (st + 3 < nst) stage(T0{}, st + 3, 1, S3, S0);
+    }
+    {
+        const int ln = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+        r = ln & 15;
+        u4 = ln >> 4;
+    }
+    // accumulator e of lane (r, u4) in tile (i, j): weight row 16 i + 4 u4 + e
+    // of the wave's blocks, token 64 wm + 16 j + r
+#pragma unroll
+    for (int i = 0; i < (GLU ? 4 : 8); i++) {
+        const int c = n0 + (GLU ? 64 * wn : 128 * wn) + 16 * i + 4 * u4;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            if (!GLU) asm volatile("" : "+a"(acc[i][j]));
+            const int t = t0 + 64 * wm + 16 * j + r;
+            if (t >= a.m) continue;
+            OutT *orow = reinterpret_cast<OutT *>(a.out) + ((int64_t)blockIdx.y * a.m + t) * a.out_ld;
+            float o[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                float g = acc[i][j][e];
+                if (GLU) {
+                    float u = acc[i + 4][j][e];
+                    if (a.clamp > 0.0f) { // Glu::apply's clamp (cpu.rs:364-368)
+                        g = fminf(g, a.clamp);
+                        u = fminf(fmaxf(u, -a.clamp), a.clamp);
+                    }
+                    g = (ACT == 0 ? act_silu(g) : act_gelu_tanh(g)) * u;
+                }
+                o[e] = g;
+            }
+            if (a.vec && c + 3 < a.n) {
+                if (!GLU && sizeof(OutT) == 4) {
+                    *reinterpret_cast<f32x4 *>(orow + c) = acc[i][j];
+                } else if (sizeof(OutT) == 4) {
+                    *reinterpret_cast<f32x4 *>(orow + c) = f32x4{o[0], o[1], o[2], o[3]};
+                } else {
+                    typedef _Float16 g16_h4 __attribute__((ext_vector_type(4)));
+                    *reinterpret_cast<g16_h4 *>(orow + c) =
+                        g16_h4{to_stored<_Float16>(o[0]), to_stored<_Float16>(o[1]), to_stored<_Float16>(o[2]),
+                               to_stored<_Float16>(o[3])};
+                }
+            } else if (!GLU && sizeof(OutT) == 4) {
+                const f32x4 v = acc[i][j];
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (c + e < a.n) orow[c + e] = v[e];
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    if (c + e < a.n) orow[c + e] = to_stored<OutT>(o[e]);
+            }
+        }
+    }
+}
+
 #define CUCA_GEMM16(NAME, T, ACT)                                                          \
     extern "C" __global__ __launch_bounds__(256) void NAME(Gemm16Args a) { gemm16_body<T, ACT>(a); }
 CUCA_GEMM16(cuca_gemm16_f32, float, -1)
 CUCA_GEMM16(cuca_gemm16_f16, _Float16, -1)
-CUCA_GEMM16(cuca_gemm16_glu_f32_silu, float, 0)
-CUCA_GEMM16(cuca_gemm16_glu_f32_gelu, float, 1)
-CUCA_GEMM16(cuca_gemm16_glu_f16_silu, _Float16, 0)
-CUCA_GEMM16(cuca_gemm16_glu_f16_gelu, _Float16, 1)
+#define CUCA_GEMM16_W8(NAME, T, ACT)                                                       \
+    extern "C" __global__ __launch_bounds__(512) void NAME(Gemm16Args a) { gemm16_w8_body<T, ACT>(a); }
+CUCA_GEMM16_W8(cuca_gemm16_w8_glu_f32_silu, float, 0)
+CUCA_GEMM16_W8(cuca_gemm16_w8_glu_f32_gelu, float, 1)
+CUCA_GEMM16_W8(cuca_gemm16_w8_glu_f16_silu, _Float16, 0)
+CUCA_GEMM16_W8(cuca_gemm16_w8_glu_f16_gelu, _Float16, 1)
 
 // The splits' f32 sums added in split order, then the output: one thread per
 // output.  part [splits][m][width]: width = n, or 2 n for the GLU (gate

@@ -14,8 +14,10 @@ rows and columns), weight-row prefixes, a row stride wider than k, repeated
 calls, and the host's checks.  The GEMM is the library's own kernel
 (gemm16.hip, cuca_gemm16_*): calls of fewer than 128 tiles of 256 x 256
 (GLU: 128 columns) split k (the plain f32 form over every weight row, one
-output matrix a split) and add the splits in a reduce launch; both forms are
-covered, and a test pins which kernels a call launches.
+output matrix a split) and add the splits in a reduce launch; the GLU form
+runs as 8 waves a workgroup, the plain form as 4.  Every form is covered, a
+test pins which kernels a call launches, and one pins the GLU form's bits to
+the plain form's sums put through the library's GLU op.
 """
 import numpy as np
 import pytest
@@ -149,7 +151,7 @@ def test_row_prefix_and_host_checks(ctx):
     (512, 4096, 4096, False, ["cuca_gemm16_f32", "cuca_gemm16_reduce_f16"]),   # 32 tiles: k split 8 ways
     (1024, 8192, 512, False, ["cuca_gemm16_f16"]),                          # 128 tiles: one pass
     (512, 2048, 1024, True, ["cuca_gemm16_f32", "cuca_gemm16_reduce_glu_f16_silu"]),
-    (2048, 2048, 256, True, ["cuca_gemm16_glu_f16_silu"]),
+    (2048, 2048, 256, True, ["cuca_gemm16_w8_glu_f16_silu"]),               # the GLU form: 8 waves
 ])
 def test_the_library_kernels_run(ctx, m, n, k, glu, kernels):
     """The dense GEMM is this library's kernel (no library GEMM underneath):
@@ -217,3 +219,32 @@ def test_short_k_and_ragged_tiles(ctx, m, n, k, glu):
         want = xf @ wf.T
         tol = bound(xf, wf, k) + 1e-30
     assert np.all(np.abs(got - want) <= tol), float(np.max(np.abs(got - want) / tol))
+
+
+def test_glu_form_bits_equal_plain_sums_through_the_glu_op(ctx):
+    """The GLU form (8 waves) with f32 activations and output against the
+    plain form (4 waves) over the same gate and up rows, whose f32 sums the
+    library's GLU op (cuca_hip_glu) turns into act(g) * u: each sum adds the
+    same products in the same order and act(g) * u is the same f32
+    arithmetic, so the bits must agree, with and without the clamp."""
+    rng = np.random.default_rng(6)
+    m, ff, k = 2048, 2048, 512
+    w = (rng.standard_normal((2 * ff, k)) * 0.05).astype(np.float16)
+    x = rng.standard_normal((m, k)).astype(np.float16).astype(np.float32)   # f16 values: rounded exactly
+    dw, dx = ctx.array(w), ctx.array(x)
+    wg = hip.gemm_w16_workspace(ff, k, m, True, hip.F32)
+    wp = hip.gemm_w16_workspace(2 * ff, k, m, False, hip.F32)
+    ws = ctx.empty((max(wg, wp),), np.uint8)
+    for act, clamp in ((hip.ACT_SILU, 0.0), (hip.ACT_GELU_TANH, 0.0), (hip.ACT_SILU, 2.0)):
+        glu_out = ctx.empty((m, ff), np.float32)
+        ctx.profile_start(4)
+        ctx.gemm_w16_glu(dw.ptr, ff, k, dx.ptr, k, m, act, clamp, ws.ptr, wg, glu_out.ptr, ff, hip.F32)
+        assert [kn for kn, _ in ctx.profile_stop()] == [
+            "cuca_cvt_f16_f32", "cuca_gemm16_w8_glu_f32_silu" if act == hip.ACT_SILU else "cuca_gemm16_w8_glu_f32_gelu"]
+        sums = ctx.empty((m, 2 * ff), np.float32)
+        ctx.profile_start(4)
+        ctx.gemm_w16(dw.ptr, 2 * ff, k, dx.ptr, k, m, 2 * ff, ws.ptr, wp, sums.ptr, 2 * ff, hip.F32)
+        assert [kn for kn, _ in ctx.profile_stop()] == ["cuca_cvt_f16_f32", "cuca_gemm16_f32"]
+        ref = ctx.empty((m, ff), np.float32)
+        ctx.glu(sums.ptr, 2 * ff, sums.ptr + ff * 4, 2 * ff, m, ff, act, clamp, ref.ptr, ff, hip.F32)
+        assert np.array_equal(glu_out.numpy().view(np.uint32), ref.numpy().view(np.uint32)), (act, clamp)
