@@ -312,14 +312,15 @@ def profiled_steps(torch, ctx, step, steps, warmup):
     return t0.elapsed_time(t1) / steps, {n: (k, t / steps) for n, (k, t) in per.items()}
 
 
-def profiled_windows(torch, ctx, step, steps, warmup, windows=3):
+def profiled_windows(torch, ctx, step, steps, warmup, windows=5):
     """profiled_steps over `windows` windows of `steps` steps each: the
     median per op of the windows' average kernel times (and of the step
     times).  The kernels of freshly allocated buffers run slower for the
     first tens of steps on MI355X (config E's steps of 8192 tokens: the
     gather 13.96 us in the first window of 20 steps after 25 unprofiled
-    ones, 12.8-13.1 in the next three); the median of three windows
-    reports the steady state."""
+    ones, 12.8-13.1 in the next three), and from window to window an op
+    varies by about 2 % with what the kernels before it left in the caches;
+    the median of five windows reports the steady state."""
     import numpy as np
     runs = [profiled_steps(torch, ctx, step, steps, warmup) for _ in range(windows)]
     ms = float(np.median([r[0] for r in runs]))
@@ -1613,7 +1614,7 @@ def main():
         torch.cuda.synchronize()
         log("timed steps (unprofiled)")
         ms_plain = time_steps(torch, st.step, steps, warmup)
-        log("timed steps (kernel timestamps, median of three windows)")
+        log("timed steps (kernel timestamps, median of five windows)")
         ms, per = profiled_windows(torch, ctx, st, steps, warmup)
         ctx.check_device()
         log(f"{ms * 1000:.1f} us per step ({ms_plain * 1000:.1f} unprofiled)")
